@@ -1,0 +1,274 @@
+"""Benchmark of the MoE-block decode hot path on one MI355X.
+
+Headline (BASELINE.json metric "MoE-block decode tokens/s; effective
+quant-weight GB/s vs HBM peak (1 GPU)"), measured on BASELINE config 5 at
+batch 1: one decode step = 40 chained MoE blocks (D=2048, FF=512, E=256,
+top-8, IQ4_XS gate/up + IQ3_XXS down, quantised shared expert, bf16 router),
+x_{l+1} = x_l + moe_l(rmsnorm(x_l)), captured once as a hipGraph and replayed;
+~15.5 GB of seeded random expert weights stay resident in HBM and each step
+feeds its output back as the next input, so routing changes step to step.
+A single block (config 3) would fit in the 256 MB Infinity Cache when
+replayed, so its per-block figures are reported from the chain.
+
+Timed region: `--steps` graph replays between a synchronize and two HIP
+events; inputs are resident in HBM before it starts.  One JSON line on stdout.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+HBM_PEAK_GBPS = 8000.0
+D, FF, E, K_TOP, N_LAYERS = 2048, 512, 256, 8, 40
+SEED = 20261201
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=N_LAYERS)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=6, help="blocks in the bounded CPU sample")
+    ap.add_argument("--no-extra", action="store_true", help="skip the batch-8 chain")
+    ap.add_argument("--calib-copy", action="store_true", help="only run a plain 256 MiB copy (counter calibration)")
+    return ap.parse_args()
+
+
+def build_layers(n_layers: int, device):
+    import torch
+    from npu_amd import synth
+    from npu_amd.gguf_types import GGMLQuantizationType as QT
+    from npu_amd.moe import GpuMoeBlock
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(SEED)
+    layers = []
+    for _ in range(n_layers):
+        gate = synth.device_quant_matrix(gen, QT.IQ4_XS, FF, D, E, device)
+        up = synth.device_quant_matrix(gen, QT.IQ4_XS, FF, D, E, device)
+        down = synth.device_quant_matrix(gen, QT.IQ3_XXS, D, FF, E, device)
+        router = synth.device_bf16_normal(gen, (E, D), synth.ROUTER_STD, device)
+        gate_sh = synth.device_quant_matrix(gen, QT.IQ4_XS, FF, D, None, device)
+        up_sh = synth.device_quant_matrix(gen, QT.IQ4_XS, FF, D, None, device)
+        down_sh = synth.device_quant_matrix(gen, QT.IQ3_XXS, D, FF, None, device)
+        sh_inp = synth.device_bf16_normal(gen, (D,), synth.ROUTER_STD, device)
+        norm_w = torch.ones(D, dtype=torch.float32, device=device)
+        layers.append(GpuMoeBlock(gate=gate, up=up, down=down, router=router, q_gate=QT.IQ4_XS,
+                                  q_down=QT.IQ3_XXS, D=D, FF=FF, E=E, k=K_TOP, gate_sh=gate_sh, up_sh=up_sh,
+                                  down_sh=down_sh, sh_gate_inp=sh_inp, norm_w=norm_w, norm_eps=1e-6,
+                                  device=device))
+    return layers
+
+
+def unique_experts(blk, T: int) -> int:
+    """Distinct experts the last call routed to (grouping table word 0)."""
+    import torch
+    from npu_amd import ops
+    ws = blk.workspace(T)
+    lay = ops.moe_workspace_offsets(blk.struct, T)
+    # the grouping table sits right after the weights array; its word 0 is n_unique
+    grp_off = lay["weights"] + ((T * blk.k * 4 + 255) // 256) * 256
+    return int(ws[grp_off:grp_off + 4].view(torch.int32).item())
+
+
+def run_chain(layers, T: int, steps: int, warmup: int, seed: int):
+    """Capture one decode step (all layers, ping-pong buffers) and time `steps` replays."""
+    import torch
+    from npu_amd import synth
+    dev = layers[0].gate.device
+    x0 = torch.from_numpy(synth.host_input(seed, T, D, rmsnorm=False)).to(dev)
+    bufs = [x0.clone(), torch.empty_like(x0)]
+    for i, blk in enumerate(layers):             # eager pass: workspaces, attributes
+        blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
+    torch.cuda.synchronize()
+    bufs[0].copy_(x0)
+    if len(layers) % 2:
+        raise ValueError("the ping-pong chain needs an even layer count")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i, blk in enumerate(layers):
+            blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    n_unique = [unique_experts(blk, T) for blk in layers]
+    finite = bool(torch.isfinite(bufs[0]).all())
+    return ms, n_unique, finite
+
+
+def time_stages(layers, T: int, reps: int = 3):
+    """Per-kernel durations (HIP events on torch's stream, which the kernels run on)."""
+    import torch
+    from npu_amd import synth
+    dev = layers[0].gate.device
+    x = torch.from_numpy(synth.host_input(SEED + 1, T, D, rmsnorm=False)).to(dev)
+    y = torch.empty_like(x)
+    n = len(layers) * reps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n)]
+    i = 0
+    for _ in range(reps):
+        for blk in layers:
+            e = ev[i]
+            e[0].record()
+            blk(x, residual=True, out=y, stage=1)
+            e[1].record()
+            blk(x, residual=True, out=y, stage=2)
+            e[2].record()
+            blk(x, residual=True, out=y, stage=3)
+            e[3].record()
+            i += 1
+    torch.cuda.synchronize()
+    st = [sum(e[j].elapsed_time(e[j + 1]) for e in ev) / n * 1e3 for j in range(3)]
+    return {"router_shared_us": st[0], "gateup_us": st[1], "down_us": st[2]}
+
+
+def cpu_baseline(layers, n_sample: int):
+    """Oracle (port of qwen/forward.py:moe_forward CPU branch, per-call dequant) on a sample."""
+    import numpy as np
+    import torch
+    from npu_amd import synth
+    from oracle import moe as OM
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    hosts = []
+    for blk in layers[:n_sample]:
+        h = synth.HostMoeLayer(
+            D=D, FF=FF, E=E, k=K_TOP, q_gate=blk.q_gate, q_down=blk.q_down,
+            gate=blk.gate.cpu().numpy(), up=blk.up.cpu().numpy(), down=blk.down.cpu().numpy(),
+            router=blk.router.cpu().numpy().view(np.uint16), gate_sh=blk.gate_sh.cpu().numpy(),
+            up_sh=blk.up_sh.cpu().numpy(), down_sh=blk.down_sh.cpu().numpy(),
+            sh_gate_inp=blk.sh_gate_inp.cpu().numpy().view(np.uint16), norm_w=blk.norm_w.cpu().numpy())
+        hosts.append(OM.OracleLayer(h))
+    x = torch.from_numpy(synth.host_input(SEED, 1, D, rmsnorm=False))
+    OM.block_forward(x, hosts[0], residual=True)          # warm-up (allocations)
+    t0 = time.perf_counter()
+    y = x
+    for L in hosts:
+        y = OM.block_forward(y, L, residual=True)
+    dt = time.perf_counter() - t0
+    per_block = dt / n_sample
+    step_s = per_block * N_LAYERS
+    return {
+        "value": 1.0 / step_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": (f"{n_sample} of {N_LAYERS} chained blocks of one B=1 decode step, per-call dequant "
+                   f"(numpy) + torch fp32 F.linear, scaled to 40 blocks; {dt:.1f} s measured"),
+        "block_ms": per_block * 1e3, "cpu": platform.processor() or platform.machine(),
+    }
+
+
+def calib_copy() -> None:
+    import torch
+    n = 256 << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calib_copy_bytes": n, "launches": 5}))
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); "
+              "multi-GPU expert parallelism is a design note, not built", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU available", file=sys.stderr)
+        return 1
+    if args.calib_copy:
+        calib_copy()
+        return 0
+    from npu_amd import _lib
+    _lib.lib()
+    dev = torch.device("cuda:0")
+
+    log(f"building {args.layers} layers of seeded synthetic weights on {torch.cuda.get_device_name(0)}")
+    t0 = time.time()
+    layers = build_layers(args.layers, dev)
+    torch.cuda.synchronize()
+    weight_gb = sum(sum(t.numel() * t.element_size() for t in (b.gate, b.up, b.down, b.router, b.gate_sh,
+                                                              b.up_sh, b.down_sh, b.sh_gate_inp))
+                    for b in layers) / 1e9
+    log(f"built {weight_gb:.2f} GB resident in {time.time() - t0:.1f} s")
+
+    per_expert = layers[0].gate[0].numel() + layers[0].up[0].numel() + layers[0].down[0].numel()
+    gu_bytes = layers[0].gate[0].numel() + layers[0].up[0].numel()
+    fixed = (sum(t.numel() for t in (layers[0].gate_sh, layers[0].up_sh, layers[0].down_sh))
+             + layers[0].router.numel() * 2 + layers[0].sh_gate_inp.numel() * 2)
+
+    log(f"B=1 chain: warmup {args.warmup}, steps {args.steps}")
+    ms1, nu1, ok1 = run_chain(layers, 1, args.steps, args.warmup, SEED)
+    bytes1 = sum(n * per_expert + fixed for n in nu1)
+    tok_s = 1e3 / ms1
+    eff_gbps = bytes1 / (ms1 * 1e-3) / 1e9
+    log(f"B=1: {ms1 * 1e3:.1f} us/step, {tok_s:.1f} tok/s, {eff_gbps:.1f} GB/s effective, finite={ok1}")
+
+    stages = time_stages(layers, 1)
+    gu_launch_bytes = K_TOP * gu_bytes + D * 4 + K_TOP * FF * 4
+    gu_gbps = gu_launch_bytes / (stages["gateup_us"] * 1e-6) / 1e9
+    log(f"stages (us): {stages}")
+
+    extra = {}
+    if not args.no_extra:
+        ms8, nu8, ok8 = run_chain(layers, 8, max(20, args.steps // 4), max(2, args.warmup // 4), SEED + 8)
+        bytes8 = sum(n * per_expert + fixed for n in nu8)
+        extra["batch8"] = {"ms_per_step": ms8, "tokens_per_s": 8e3 / ms8,
+                           "effective_weight_GBps": bytes8 / (ms8 * 1e-3) / 1e9,
+                           "mean_unique_experts_per_layer": sum(nu8) / len(nu8), "finite": ok8}
+        log(f"B=8: {extra['batch8']}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"CPU baseline: {args.cpu_layers} blocks of the oracle")
+        cpu = cpu_baseline(layers, args.cpu_layers)
+        log(f"CPU: {cpu}")
+
+    out = {
+        "metric": "MoE-block decode tokens/s; effective quant-weight GB/s vs HBM peak (1 GPU)",
+        "value": tok_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded, torch GPU generator; BASELINE config 5 distributions)",
+        "config": {"workload": "config5: 40 chained MoE blocks, decode T=1 batch 1, hipGraph replay",
+                   "D": D, "FF": FF, "experts": E, "top_k": K_TOP, "layers": args.layers,
+                   "gate_up": "IQ4_XS", "down": "IQ3_XXS", "shared_expert": "IQ4_XS/IQ3_XXS",
+                   "router": "bf16", "resident_weight_GB": round(weight_gb, 3)},
+        "effective_weight_GBps": eff_gbps,
+        "effective_weight_frac_of_peak": eff_gbps / HBM_PEAK_GBPS,
+        "block_us": ms1 * 1e3 / args.layers,
+        "weight_bytes_per_step": bytes1,
+        "roofline": {"bound": "hbm", "kernel": "k_moe_gateup (routed gate/up + SwiGLU, T=1)",
+                     "achieved": gu_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gu_gbps / HBM_PEAK_GBPS,
+                     "traffic": None, "bytes_per_launch": gu_launch_bytes, "avg_launch_us": stages["gateup_us"]},
+        "stage_us": stages,
+        "cpu_baseline": cpu,
+        "finite": ok1,
+    }
+    out.update(extra)
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

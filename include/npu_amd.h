@@ -1,0 +1,156 @@
+/*
+ * npu_amd.h -- C ABI of the gfx950 (MI355X) Qwen MoE-block hot path.
+ *
+ * Drop-in boundary for the path BojanFaletic/NPU runs through
+ * qwen/forward.py:moe_forward (563-665) and the npu.* operator wrappers it
+ * calls.  Every entry point:
+ *   - takes DEVICE pointers (owned by the caller, e.g. torch tensors) and plain
+ *     sizes; weights stay in raw GGUF layout (IQ4_XS 136-byte / IQ3_XXS 98-byte
+ *     superblocks, row-major [out][in/256 superblocks], experts outermost);
+ *   - enqueues on the caller's hipStream_t passed as `void* stream` and never
+ *     synchronises;
+ *   - allocates no device memory (scratch comes from the caller's workspace);
+ *   - returns 0 on success, a negative GM_E* code for a rejected argument, or
+ *     a positive hipError_t; gm_last_error() returns a thread-local message.
+ * No exceptions cross the ABI; the only global state is constant codebooks.
+ */
+#ifndef NPU_AMD_H
+#define NPU_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Weight formats: ggml type ids (gguf GGMLQuantizationType). */
+#define GM_QTYPE_F32 0
+#define GM_QTYPE_F16 1
+#define GM_QTYPE_IQ3_XXS 18
+#define GM_QTYPE_IQ4_XS 23
+#define GM_QTYPE_BF16 30
+
+/* Status codes (negative = argument errors). */
+#define GM_OK 0
+#define GM_EINVAL (-1)
+#define GM_EUNSUPPORTED (-2)
+#define GM_EWORKSPACE (-3)
+
+/* Flags for gm_moe_forward. */
+#define GM_MOE_RESIDUAL 1   /* y = x + moe(rmsnorm(x)) instead of y = moe(rmsnorm(x)) */
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* gm_last_error(void);
+
+/* ABI version (bumped on any signature change). */
+int gm_abi_version(void);
+
+/*
+ * Dequantise n_superblocks raw superblocks of `qtype` (IQ4_XS or IQ3_XXS) to
+ * fp32 (256 values per superblock).  Exact: every value is an fp32 product.
+ * Replaces gguf.quants.dequantize as called by TensorStore.get_expert
+ * (qwen/model.py:266) and npu/iq3_xxs.py:dequant_rows (97-119).
+ */
+int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out, void* stream);
+
+/*
+ * y[t][m] = sum_k W[m][k] * x[t][k] for t < n_tok, W given as M rows of raw
+ * `qtype` superblocks (IQ4_XS, IQ3_XXS) or bf16 (BF16), fp32 x/y, fp32
+ * accumulate.  K must be a multiple of 256.
+ * Replaces NpuQuantMatVec.__call__ (npu/quant_mv.py:419-463),
+ * NpuIQ4MatVec.__call__ (npu/quant_mv_iq4.py:317-361),
+ * NpuIQ4PackedMatVec.__call__ (npu/quant_mv_iq4_packed.py:320-364) and,
+ * with qtype BF16, NpuMatVec / NpuConcatMatVec.__call__ (npu/mv.py:222-347).
+ * The reference takes one vector (n_tok == 1); n_tok >= 1 is accepted.
+ */
+int gm_matvec(int qtype, const void* w, int M, int K, const float* x, int n_tok, float* y,
+              void* stream);
+
+/*
+ * SwiGLU MLP: y[t] = W_down (silu(W_gate x[t]) * (W_up x[t])), gate/up
+ * [FF][D] of qtype q_gu, down [D][FF] of qtype q_down; h is an fp32
+ * [n_tok][FF] scratch buffer.  Replaces NpuFusedMLP.__call__
+ * (npu/mlp.py:413-466) and the shared-expert F.linear chain
+ * (qwen/forward.py:592-598).
+ */
+int gm_swiglu_mlp(int q_gu, const void* w_gate, const void* w_up, int q_down, const void* w_down,
+                  int D, int FF, const float* x, int n_tok, float* h, float* y, void* stream);
+
+/*
+ * Router: logits[t][e] = W_router[e] . xn[t] (+ bias[e]), then softmax over E,
+ * top-k (ties -> lower expert id) and renormalisation of the k probabilities;
+ * also sh_gate[t] = sigmoid(w_sh_gate . xn[t]) when w_sh_gate != NULL.
+ * xn = rmsnorm(x, norm_w, eps) when norm_w != NULL, else x.
+ * W_router and w_sh_gate are bf16 bits.  `logits` may be NULL.
+ * Replaces qwen/forward.py:599-611 (router F.linear / NpuMatVec, softmax,
+ * topk, renormalise) and the shared scalar gate.
+ */
+int gm_router_topk(const uint16_t* w_router, const float* bias, const float* x, int T, int D, int E,
+                   int k, const uint16_t* w_sh_gate, const float* norm_w, float eps, int32_t* ids,
+                   float* weights, float* logits, float* sh_gate, void* stream);
+
+/*
+ * Token -> expert dispatch: counts[E] = pairs per expert, offsets[E+1] =
+ * exclusive prefix sum, sorted_pairs[T*k] = (token*k + slot) grouped by
+ * ascending expert, tokens ascending within an expert (stable).
+ * Replaces qwen/forward.py:612, 623-629 (torch.unique + nonzero per expert).
+ */
+int gm_moe_dispatch(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
+                    int32_t* sorted_pairs, void* stream);
+
+/* One MoE block's resident weights (device pointers) and shape. */
+typedef struct gm_moe_layer {
+  const void* gate_exps;        /* [E][FF][row_bytes(q_gate, D)]  raw GGUF bytes */
+  const void* up_exps;          /* [E][FF][row_bytes(q_up, D)] */
+  const void* down_exps;        /* [E][D][row_bytes(q_down, FF)] */
+  const void* gate_sh;          /* [FF_sh][row_bytes(q_gate_sh, D)] */
+  const void* up_sh;            /* [FF_sh][row_bytes(q_up_sh, D)] */
+  const void* down_sh;          /* [D][row_bytes(q_down_sh, FF_sh)] */
+  const uint16_t* router;       /* bf16 bits [E][D] */
+  const uint16_t* sh_gate_inp;  /* bf16 bits [D] (shared-expert scalar gate) */
+  const float* router_bias;     /* [E] added to logits, or NULL (not in the reference model) */
+  const float* norm_w;          /* [D] RMSNorm weight applied to x, or NULL */
+  float norm_eps;
+  int32_t q_gate, q_up, q_down;
+  int32_t q_gate_sh, q_up_sh, q_down_sh;
+  int32_t D, FF, FF_sh, E, k;
+} gm_moe_layer;
+
+/* Workspace bytes gm_moe_forward needs for T tokens (0 on bad arguments). */
+size_t gm_moe_workspace_bytes(const gm_moe_layer* L, int T);
+
+/*
+ * Byte offsets inside the workspace of the per-call intermediates, for
+ * stage-wise checks: router logits fp32 [T][E], top-k ids int32 [T][k],
+ * renormalised weights fp32 [T][k], shared gate fp32 [T].
+ */
+int gm_moe_workspace_offsets(const gm_moe_layer* L, int T, size_t* off_logits, size_t* off_ids,
+                             size_t* off_weights, size_t* off_sh_gate);
+
+/*
+ * The whole MoE block for T tokens: y = moe(xn) (+ x with GM_MOE_RESIDUAL),
+ * xn = rmsnorm(x) when L->norm_w != NULL.  Routing, dispatch, expert
+ * products, shared expert and the combine all run on the device from
+ * device-resident ids (no host synchronisation).  T <= 8 uses the decode
+ * kernels (fp32 accumulate); larger T uses the grouped bf16-MFMA prefill.
+ * x and y must not alias.  Replaces qwen/forward.py:moe_forward (563-665).
+ */
+int gm_moe_forward(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
+                   size_t ws_bytes, void* stream);
+
+/*
+ * One stage of gm_moe_forward, for stage-wise checks and per-kernel timing:
+ * stage 1 = router / top-k inputs (+ shared expert gate/up), 2 = routed
+ * gate/up + SwiGLU, 3 = down + combine (+ residual); stage 0 runs all three.
+ * Stages must run in order on the same workspace.  Decode path (T <= 8) only.
+ * Mirrors the stage boundaries of qwen/compare.py:compare_moe (191-297).
+ */
+int gm_moe_forward_stage(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
+                         size_t ws_bytes, int stage, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NPU_AMD_H */

@@ -1,0 +1,195 @@
+// extern "C" entry points: argument validation, error reporting, workspace
+// layout.  Kernels live in matvec.hip, moe_decode.hip, dispatch.hip and
+// prefill.hip.
+#include <cstdarg>
+#include <cstdio>
+
+#include "kernels.h"
+
+static thread_local char g_err[512] = "";
+
+int gm_fail_hip(hipError_t e, const char* what) {
+  snprintf(g_err, sizeof g_err, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+  return (int)e;
+}
+
+int gm_fail_arg(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return GM_EINVAL;
+}
+
+static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static bool is_quant(int q) { return q == GM_QTYPE_IQ4_XS || q == GM_QTYPE_IQ3_XXS; }
+static bool is_weight_fmt(int q) { return is_quant(q) || q == GM_QTYPE_BF16; }
+
+// K must be a multiple of 256 for superblock formats and of 32 for bf16.
+static int check_k(const char* fn, int qtype, int K) {
+  if (K <= 0) return gm_fail_arg("%s: K=%d must be positive", fn, K);
+  if (is_quant(qtype) && K % GM_QK) return gm_fail_arg("%s: K=%d must be a multiple of %d", fn, K, GM_QK);
+  if (qtype == GM_QTYPE_BF16 && K % GM_SUB) return gm_fail_arg("%s: K=%d must be a multiple of %d", fn, K, GM_SUB);
+  return GM_OK;
+}
+
+GmMoeWs gm_moe_ws_layout(const gm_moe_layer* L, int T) {
+  GmMoeWs w{};
+  size_t o = 0;
+  const size_t Tz = (size_t)T, E = (size_t)L->E, k = (size_t)L->k;
+  w.logits = o; o = align256(o + Tz * E * 4);
+  w.shg = o; o = align256(o + Tz * 4);
+  w.ids = o; o = align256(o + Tz * k * 4);
+  w.wts = o; o = align256(o + Tz * k * 4);
+  w.grp = o; o = align256(o + ((size_t)GM_GRP_WORDS + 2 * E + 1 + Tz * k) * 4);
+  w.h = o; o = align256(o + Tz * k * (size_t)L->FF * 4);
+  w.hsh = o; o = align256(o + Tz * (size_t)(L->FF_sh > 0 ? L->FF_sh : 0) * 4);
+  w.counters = o; o = align256(o + 256);
+  w.pre = o; o = align256(o + (T > GM_DECODE_MAX_T ? gm_prefill_scratch_bytes(L, T) : 0));
+  w.total = o;
+  return w;
+}
+
+static int check_layer(const gm_moe_layer* L) {
+  if (!L) return gm_fail_arg("gm_moe_forward: layer is NULL");
+  if (L->D <= 0 || L->FF <= 0 || L->E <= 0 || L->k <= 0)
+    return gm_fail_arg("gm_moe_forward: bad shape D=%d FF=%d E=%d k=%d", L->D, L->FF, L->E, L->k);
+  if (L->k > 8 || L->k > L->E) return gm_fail_arg("gm_moe_forward: k=%d must be <= min(8, E=%d)", L->k, L->E);
+  if (L->E > 512) return gm_fail_arg("gm_moe_forward: E=%d > 512 is not supported", L->E);
+  if (!L->gate_exps || !L->up_exps || !L->down_exps || !L->router)
+    return gm_fail_arg("gm_moe_forward: routed expert / router weights must be non-NULL");
+  if (!is_quant(L->q_gate) || L->q_up != L->q_gate || !is_quant(L->q_down))
+    return gm_fail_arg("gm_moe_forward: routed formats gate %d up %d down %d unsupported (gate == up, "
+                       "IQ4_XS or IQ3_XXS)", L->q_gate, L->q_up, L->q_down);
+  if (L->D % GM_QK || L->FF % GM_QK)
+    return gm_fail_arg("gm_moe_forward: D=%d and FF=%d must be multiples of %d", L->D, L->FF, GM_QK);
+  const bool has_sh = L->gate_sh || L->up_sh || L->down_sh;
+  if (has_sh) {
+    if (!L->gate_sh || !L->up_sh || !L->down_sh)
+      return gm_fail_arg("gm_moe_forward: shared expert needs gate, up and down");
+    if (L->FF_sh != L->FF) return gm_fail_arg("gm_moe_forward: FF_sh=%d must equal FF=%d", L->FF_sh, L->FF);
+    if (!is_weight_fmt(L->q_gate_sh) || L->q_up_sh != L->q_gate_sh || !is_weight_fmt(L->q_down_sh))
+      return gm_fail_arg("gm_moe_forward: shared formats gate %d up %d down %d unsupported", L->q_gate_sh,
+                         L->q_up_sh, L->q_down_sh);
+  }
+  if (L->norm_w && !(L->norm_eps >= 0.f)) return gm_fail_arg("gm_moe_forward: norm_eps must be >= 0");
+  return GM_OK;
+}
+
+extern "C" {
+
+const char* gm_last_error(void) { return g_err; }
+
+int gm_abi_version(void) { return 1; }
+
+int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out, void* stream) {
+  if (!is_quant(qtype)) return gm_fail_arg("gm_dequant_f32: qtype %d is not IQ4_XS(23)/IQ3_XXS(18)", qtype);
+  if (n_superblocks < 0) return gm_fail_arg("gm_dequant_f32: negative n_superblocks");
+  if (n_superblocks == 0) return GM_OK;
+  if (!raw || !out) return gm_fail_arg("gm_dequant_f32: NULL pointer");
+  if (reinterpret_cast<uintptr_t>(raw) % 8 || reinterpret_cast<uintptr_t>(out) % 16)
+    return gm_fail_arg("gm_dequant_f32: raw must be 8-byte and out 16-byte aligned");
+  return gm_launch_dequant(qtype, raw, n_superblocks, out, as_stream(stream));
+}
+
+int gm_matvec(int qtype, const void* w, int M, int K, const float* x, int n_tok, float* y, void* stream) {
+  if (!is_weight_fmt(qtype)) return gm_fail_arg("gm_matvec: unsupported qtype %d", qtype);
+  if (int rc = check_k("gm_matvec", qtype, K)) return rc;
+  if (M < 0 || n_tok < 0) return gm_fail_arg("gm_matvec: negative size");
+  if (M == 0 || n_tok == 0) return GM_OK;
+  if (!w || !x || !y) return gm_fail_arg("gm_matvec: NULL pointer");
+  if (K > 16384) return gm_fail_arg("gm_matvec: K=%d > 16384 not supported", K);
+  if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(x) % 16)
+    return gm_fail_arg("gm_matvec: w and x must be 16-byte aligned");
+  return gm_launch_matvec(qtype, w, M, K, x, n_tok, y, as_stream(stream));
+}
+
+int gm_swiglu_mlp(int q_gu, const void* w_gate, const void* w_up, int q_down, const void* w_down, int D, int FF,
+                  const float* x, int n_tok, float* h, float* y, void* stream) {
+  if (!is_weight_fmt(q_gu) || !is_weight_fmt(q_down))
+    return gm_fail_arg("gm_swiglu_mlp: unsupported qtypes %d / %d", q_gu, q_down);
+  if (int rc = check_k("gm_swiglu_mlp", q_gu, D)) return rc;
+  if (int rc = check_k("gm_swiglu_mlp", q_down, FF)) return rc;
+  if (D > 16384 || FF > 16384) return gm_fail_arg("gm_swiglu_mlp: D/FF > 16384 not supported");
+  if (n_tok < 0) return gm_fail_arg("gm_swiglu_mlp: negative n_tok");
+  if (n_tok == 0) return GM_OK;
+  if (!w_gate || !w_up || !w_down || !x || !h || !y) return gm_fail_arg("gm_swiglu_mlp: NULL pointer");
+  hipStream_t s = as_stream(stream);
+  if (int rc = gm_launch_gateup(q_gu, w_gate, w_up, FF, D, x, n_tok, h, s)) return rc;
+  return gm_launch_matvec(q_down, w_down, D, FF, h, n_tok, y, s);
+}
+
+int gm_router_topk(const uint16_t* w_router, const float* bias, const float* x, int T, int D, int E, int k,
+                   const uint16_t* w_sh_gate, const float* norm_w, float eps, int32_t* ids, float* weights,
+                   float* logits, float* sh_gate, void* stream) {
+  if (T < 0 || D <= 0 || E <= 0 || k <= 0) return gm_fail_arg("gm_router_topk: bad sizes");
+  if (E > 512 || k > 8 || k > E) return gm_fail_arg("gm_router_topk: need E <= 512 and k <= min(8, E)");
+  if (D % GM_SUB) return gm_fail_arg("gm_router_topk: D=%d must be a multiple of 32", D);
+  if (D > 16384) return gm_fail_arg("gm_router_topk: D > 16384 not supported");
+  if (T == 0) return GM_OK;
+  if (!w_router || !x || !ids || !weights || !logits) return gm_fail_arg("gm_router_topk: NULL pointer");
+  if (w_sh_gate && !sh_gate) return gm_fail_arg("gm_router_topk: sh_gate output missing");
+  hipStream_t s = as_stream(stream);
+  if (int rc = gm_launch_router(w_router, bias, x, T, D, E, w_sh_gate, norm_w, eps, logits, sh_gate, s)) return rc;
+  return gm_launch_topk(logits, T, E, k, ids, weights, s);
+}
+
+int gm_moe_dispatch(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
+                    int32_t* sorted_pairs, void* stream) {
+  if (T < 0 || k <= 0 || E <= 0) return gm_fail_arg("gm_moe_dispatch: bad sizes");
+  if (!ids || !counts || !offsets || !sorted_pairs) return gm_fail_arg("gm_moe_dispatch: NULL pointer");
+  return gm_launch_dispatch(ids, T, k, E, counts, offsets, sorted_pairs, as_stream(stream));
+}
+
+size_t gm_moe_workspace_bytes(const gm_moe_layer* L, int T) {
+  if (T < 0 || check_layer(L) != GM_OK) return 0;
+  return gm_moe_ws_layout(L, T).total;
+}
+
+int gm_moe_workspace_offsets(const gm_moe_layer* L, int T, size_t* off_logits, size_t* off_ids,
+                             size_t* off_weights, size_t* off_sh_gate) {
+  if (int rc = check_layer(L)) return rc;
+  const GmMoeWs w = gm_moe_ws_layout(L, T);
+  if (off_logits) *off_logits = w.logits;
+  if (off_ids) *off_ids = w.ids;
+  if (off_weights) *off_weights = w.wts;
+  if (off_sh_gate) *off_sh_gate = w.shg;
+  return GM_OK;
+}
+
+static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
+                            size_t ws_bytes, int stage, void* stream);
+
+int gm_moe_forward(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws, size_t ws_bytes,
+                   void* stream) {
+  return moe_forward_impl(L, x, y, T, flags, ws, ws_bytes, 0, stream);
+}
+
+int gm_moe_forward_stage(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
+                         size_t ws_bytes, int stage, void* stream) {
+  if (stage < 0 || stage > 3) return gm_fail_arg("gm_moe_forward_stage: stage %d not in 0..3", stage);
+  return moe_forward_impl(L, x, y, T, flags, ws, ws_bytes, stage, stream);
+}
+
+}  // extern "C"
+
+static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
+                            size_t ws_bytes, int stage, void* stream) {
+  if (int rc = check_layer(L)) return rc;
+  if (T < 0) return gm_fail_arg("gm_moe_forward: negative T");
+  if (T == 0) return GM_OK;
+  if (!x || !y || !ws) return gm_fail_arg("gm_moe_forward: NULL pointer");
+  if (x == y) return gm_fail_arg("gm_moe_forward: x and y must not alias");
+  const GmMoeWs lay = gm_moe_ws_layout(L, T);
+  if (ws_bytes < lay.total)
+    return gm_fail_arg("gm_moe_forward: workspace %zu bytes < %zu needed", ws_bytes, lay.total), GM_EWORKSPACE;
+  if (reinterpret_cast<uintptr_t>(ws) % 256) return gm_fail_arg("gm_moe_forward: workspace must be 256-byte aligned");
+  uint8_t* w = static_cast<uint8_t*>(ws);
+  hipStream_t s = as_stream(stream);
+  if (T <= GM_DECODE_MAX_T && T * L->k <= GM_GRP_MAXU) return gm_moe_decode(L, x, y, T, flags, w, lay, s, stage);
+  if (stage != 0) return gm_fail_arg("gm_moe_forward_stage: stages are only defined for the decode path (T <= 8)");
+  return gm_moe_prefill(L, x, y, T, flags, w, lay, s);
+}

@@ -1,0 +1,194 @@
+// Per-sub-block (32 weights) load and decode of raw GGUF superblocks.
+//
+// A row of an [M x K] weight is K/256 consecutive superblocks.  Sub-block
+// `sub` (0 .. K/32-1) of a row is sub-block (sub % 8) of superblock (sub / 8).
+// load_sub<QT>() fetches the raw bytes one lane needs for one sub-block;
+// decode_sub<QT>() turns them into 32 unscaled fp32 weights plus the
+// sub-block scale, so that  weight[i] == scale * wv[i]  exactly (every
+// product involved is exact in fp32; see the layout notes per format).
+#pragma once
+#include "common.h"
+#include "iq_tables.h"
+
+// kvalues_iq4nl as 16 int8 bytes, entry n in byte (n % 4) of word (n / 4).
+constexpr uint32_t kGmKv[4] = {GM_IQ4NL_PACKED_INIT};
+#define GM_KV0 kGmKv[0]
+#define GM_KV1 kGmKv[1]
+#define GM_KV2 kGmKv[2]
+#define GM_KV3 kGmKv[3]
+
+// Four IQ4 nibbles (one per byte, values 0..15) -> four int8 kvalues.
+// v_perm_b32 picks bytes from an 8-byte pool, so the 16-entry table is
+// looked up as two 8-entry halves and bit 3 of each nibble selects the half.
+__device__ __forceinline__ uint32_t gm_iq4nl_lut4(uint32_t nib) {
+  const uint32_t sel = nib & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(GM_KV1, GM_KV0, sel);
+  const uint32_t hi = __builtin_amdgcn_perm(GM_KV3, GM_KV2, sel);
+  const uint32_t pick = ((nib >> 1) & 0x04040404u) | 0x03020100u;
+  return __builtin_amdgcn_perm(hi, lo, pick);
+}
+
+__device__ __forceinline__ float gm_sbyte(uint32_t v, int i) {
+  return (float)(int)(int8_t)(uint8_t)(v >> (8 * i));
+}
+
+__device__ __forceinline__ float gm_ubyte(uint32_t v, int i) {
+  return (float)(uint32_t)((v >> (8 * i)) & 0xffu);
+}
+
+// ---------------------------------------------------------------- IQ4_XS
+// block_iq4_xs (136 B): fp16 d | u16 scales_h | u8 scales_l[4] | u8 qs[128].
+// ls_s = ((scales_l[s/2] >> 4*(s%2)) & 15) | (((scales_h >> 2s) & 3) << 4),
+// dl_s = d * (ls_s - 32); qs[16s + j]: low nibble -> weight 32s+j,
+// high nibble -> weight 32s+16+j.  (Reference: npu/quant_mv_iq4.py:180-202.)
+struct RawIq4 {
+  uint32_t h0, h1;      // d | scales_h, scales_l[0..3]
+  uint32_t q[4];        // 16 qs bytes of the sub-block
+};
+
+__device__ __forceinline__ RawIq4 gm_load_iq4(const uint8_t* __restrict__ row, int sub) {
+  const uint8_t* blk = row + (sub >> 3) * GM_IQ4XS_BYTES;     // 8-byte aligned
+  const uint2 h = *reinterpret_cast<const uint2*>(blk);
+  const uint2* qp = reinterpret_cast<const uint2*>(blk + 8 + 16 * (sub & 7));
+  const uint2 a = qp[0], b = qp[1];
+  RawIq4 r;
+  r.h0 = h.x; r.h1 = h.y;
+  r.q[0] = a.x; r.q[1] = a.y; r.q[2] = b.x; r.q[3] = b.y;
+  return r;
+}
+
+__device__ __forceinline__ float gm_decode_iq4(const RawIq4& r, int sub, float (&wv)[32]) {
+  const int s = sub & 7;
+  const float d = gm_h2f(r.h0 & 0xffffu);
+  const uint32_t sh = r.h0 >> 16;
+  const uint32_t sl = (r.h1 >> (8 * (s >> 1) + 4 * (s & 1))) & 15u;
+  const int ls = (int)(sl | (((sh >> (2 * s)) & 3u) << 4));
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t lo = gm_iq4nl_lut4(r.q[w] & 0x0f0f0f0fu);
+    const uint32_t hi = gm_iq4nl_lut4((r.q[w] >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      wv[4 * w + i] = gm_sbyte(lo, i);
+      wv[16 + 4 * w + i] = gm_sbyte(hi, i);
+    }
+  }
+  return d * (float)(ls - 32);
+}
+
+// --------------------------------------------------------------- IQ3_XXS
+// block_iq3_xxs (98 B): fp16 d | u8 qs[64] | u32 scale/sign words[8].
+// Fields are only 2-byte aligned (98 is not a multiple of 4), so they are
+// fetched as 16-bit words.  Sub-block s: qs[8s .. 8s+7], word w_s;
+// db = d * (0.5 + (w_s >> 28)) * 0.5; group g uses sign byte
+// ksigns[(w_s >> 7g) & 127] and grid points qs[8s+2g], qs[8s+2g+1].
+// (Reference: npu/iq3_xxs.py:4-15, 97-119.)
+struct RawIq3 {
+  uint32_t d;      // fp16 bits
+  uint32_t q0, q1; // 8 grid indices
+  uint32_t w;      // scale/sign word
+};
+
+__device__ __forceinline__ RawIq3 gm_load_iq3(const uint8_t* __restrict__ row, int sub) {
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(row + (sub >> 3) * GM_IQ3XXS_BYTES);
+  const int s = sub & 7;
+  RawIq3 r;
+  r.d = h[0];
+  r.q0 = (uint32_t)h[1 + 4 * s] | ((uint32_t)h[2 + 4 * s] << 16);
+  r.q1 = (uint32_t)h[3 + 4 * s] | ((uint32_t)h[4 + 4 * s] << 16);
+  r.w = (uint32_t)h[33 + 2 * s] | ((uint32_t)h[34 + 2 * s] << 16);
+  return r;
+}
+
+// ksigns byte for a 7-bit index: the 7 explicit sign bits plus a parity bit
+// that makes the byte's popcount even.
+__device__ __forceinline__ uint32_t gm_ksigns(uint32_t s7) {
+  return s7 | ((__builtin_popcount(s7) & 1u) << 7);
+}
+
+__device__ __forceinline__ float gm_decode_iq3(const RawIq3& r, const uint32_t* __restrict__ grid,
+                                               float (&wv)[32]) {
+  const float d = gm_h2f(r.d);
+  const float db = d * (0.5f + (float)(r.w >> 28)) * 0.5f;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t qw = g < 2 ? r.q0 : r.q1;
+    const uint32_t ga = grid[(qw >> (16 * (g & 1))) & 0xffu];
+    const uint32_t gb = grid[(qw >> (16 * (g & 1) + 8)) & 0xffu];
+    const uint32_t sg = gm_ksigns((r.w >> (7 * g)) & 127u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float m = gm_ubyte(i < 4 ? ga : gb, i & 3);
+      wv[8 * g + i] = ((sg >> i) & 1u) ? -m : m;
+    }
+  }
+  return db;
+}
+
+// ------------------------------------------------------------------ BF16
+struct RawBf16 {
+  uint4 v[4];   // 32 bf16 values
+};
+
+__device__ __forceinline__ RawBf16 gm_load_bf16(const uint8_t* __restrict__ row, int sub) {
+  const uint4* p = reinterpret_cast<const uint4*>(row + sub * 64);
+  RawBf16 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.v[i] = p[i];
+  return r;
+}
+
+__device__ __forceinline__ float gm_decode_bf16(const RawBf16& r, float (&wv)[32]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      wv[8 * i + 2 * j] = __uint_as_float(u[j] << 16);
+      wv[8 * i + 2 * j + 1] = __uint_as_float(u[j] & 0xffff0000u);
+    }
+  }
+  return 1.0f;
+}
+
+// ---------------------------------------------------------- generic front
+template <int QT> struct RawSub;
+template <> struct RawSub<GM_QTYPE_IQ4_XS> { using T = RawIq4; };
+template <> struct RawSub<GM_QTYPE_IQ3_XXS> { using T = RawIq3; };
+template <> struct RawSub<GM_QTYPE_BF16> { using T = RawBf16; };
+
+template <int QT>
+__device__ __forceinline__ typename RawSub<QT>::T gm_load_sub(const uint8_t* __restrict__ row, int sub) {
+  if constexpr (QT == GM_QTYPE_IQ4_XS) return gm_load_iq4(row, sub);
+  else if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_load_iq3(row, sub);
+  else return gm_load_bf16(row, sub);
+}
+
+template <int QT>
+__device__ __forceinline__ float gm_decode_sub(const typename RawSub<QT>::T& r, int sub,
+                                               const uint32_t* __restrict__ grid, float (&wv)[32]) {
+  if constexpr (QT == GM_QTYPE_IQ4_XS) return gm_decode_iq4(r, sub, wv);
+  else if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_decode_iq3(r, grid, wv);
+  else return gm_decode_bf16(r, wv);
+}
+
+// Stage the IQ3_XXS grid in LDS (1 KB); every thread of the block must call.
+__device__ __forceinline__ void gm_stage_grid(uint32_t* grid_lds) {
+  constexpr uint32_t kGrid[256] = {GM_IQ3XXS_GRID_INIT};
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) grid_lds[i] = kGrid[i];
+}
+
+// 32-wide dot of decoded weights with x (LDS or registers).
+__device__ __forceinline__ float gm_dot32(const float (&wv)[32], const float* __restrict__ x) {
+  float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; i += 8) {
+    const float4 a = *reinterpret_cast<const float4*>(x + i);
+    const float4 b = *reinterpret_cast<const float4*>(x + i + 4);
+    s0 = fmaf(wv[i + 0], a.x, s0); s1 = fmaf(wv[i + 4], b.x, s1);
+    s0 = fmaf(wv[i + 1], a.y, s0); s1 = fmaf(wv[i + 5], b.y, s1);
+    s0 = fmaf(wv[i + 2], a.z, s0); s1 = fmaf(wv[i + 6], b.z, s1);
+    s0 = fmaf(wv[i + 3], a.w, s0); s1 = fmaf(wv[i + 7], b.w, s1);
+  }
+  return s0 + s1;
+}

@@ -1,0 +1,47 @@
+// Internal launchers (host side).  All return GM_OK or an error status.
+#pragma once
+#include "common.h"
+
+int gm_launch_dequant(int qtype, const void* raw, int64_t n_sb, float* out, hipStream_t s);
+int gm_launch_matvec(int qtype, const void* w, int M, int K, const float* x, int n_tok, float* y,
+                     hipStream_t s);
+int gm_launch_gateup(int qtype, const void* wg, const void* wu, int FF, int D, const float* x, int n_tok,
+                     float* h, hipStream_t s);
+
+// MoE workspace layout for T tokens (offsets in bytes, 256-byte aligned).
+struct GmMoeWs {
+  size_t logits;   // f32 [T][E]
+  size_t shg;      // f32 [T]       sigmoid(shared scalar gate)
+  size_t ids;      // i32 [T][k]
+  size_t wts;      // f32 [T][k]
+  size_t grp;      // i32 grouping table (decode) / dispatch tables (prefill)
+  size_t h;        // f32 [T][k][FF]  routed SwiGLU activations (decode)
+  size_t hsh;      // f32 [T][FF_sh]  shared SwiGLU activations
+  size_t counters; // u32 [64]   self-resetting counters
+  size_t pre;      // prefill scratch (see prefill.hip)
+  size_t total;
+};
+
+GmMoeWs gm_moe_ws_layout(const gm_moe_layer* L, int T);
+size_t gm_prefill_scratch_bytes(const gm_moe_layer* L, int T);
+
+// Decode grouping table (int32 words) written to ws.grp by the gate/up kernel:
+//   [0]            n_unique
+//   [1 .. 64]      expert id of unique slot u (ascending)
+//   [65 .. 128]    member count of slot u
+//   [129 .. 640]   members: slot u, member m -> (token * k + topk_slot), tokens ascending
+#define GM_GRP_MAXU 64
+#define GM_GRP_MAXM 8
+#define GM_GRP_WORDS (1 + 2 * GM_GRP_MAXU + GM_GRP_MAXU * GM_GRP_MAXM)
+#define GM_DECODE_MAX_T 8
+
+int gm_launch_router(const uint16_t* w_router, const float* bias, const float* x, int T, int D, int E,
+                     const uint16_t* w_sh_gate, const float* norm_w, float eps, float* logits,
+                     float* sh_gate, hipStream_t s);
+int gm_launch_topk(const float* logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
+int gm_moe_decode(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
+                  const GmMoeWs& lay, hipStream_t s, int stage = 0);
+int gm_moe_prefill(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
+                   const GmMoeWs& lay, hipStream_t s);
+int gm_launch_dispatch(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
+                       int32_t* sorted_pairs, hipStream_t s);

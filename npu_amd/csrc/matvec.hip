@@ -1,0 +1,231 @@
+// Dequant (parity/debug) and dequant-matvec kernels for raw GGUF weights.
+//
+// Matvec lane mapping: one 64-lane wave works on RPS = 64/L rows at a time;
+// each row is covered by L lanes, lane l taking sub-blocks l, l+L, l+2L, ...
+// (L = min(64, K/32)).  Consecutive lanes read consecutive sub-blocks, so a
+// wave's loads cover whole rows contiguously.  x (fp32, up to NT tokens) is
+// staged in LDS; weights are decoded in registers and never written back.
+#include "iq_decode.h"
+#include "kernels.h"
+
+// ------------------------------------------------------------- dequant
+template <int QT>
+__global__ void __launch_bounds__(256) k_dequant(const uint8_t* __restrict__ raw, int64_t n_sub,
+                                                 float* __restrict__ out) {
+  __shared__ uint32_t grid[256];
+  if constexpr (QT == GM_QTYPE_IQ3_XXS) {
+    gm_stage_grid(grid);
+    __syncthreads();
+  }
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_sub) return;
+  // Treat the buffer as one row of n_sub/8 superblocks.
+  const int64_t sb = i >> 3;
+  const int sub = (int)(i & 7);
+  const uint8_t* blk = raw + sb * gm_block_bytes(QT);
+  float wv[32];
+  const auto r = gm_load_sub<QT>(blk, sub);
+  const float sc = gm_decode_sub<QT>(r, sub, grid, wv);
+  float4* o = reinterpret_cast<float4*>(out + i * 32);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    o[j] = make_float4(sc * wv[4 * j], sc * wv[4 * j + 1], sc * wv[4 * j + 2], sc * wv[4 * j + 3]);
+}
+
+int gm_launch_dequant(int qtype, const void* raw, int64_t n_sb, float* out, hipStream_t s) {
+  const int64_t n_sub = n_sb * 8;
+  const dim3 grid((unsigned)((n_sub + 255) / 256)), block(256);
+  const uint8_t* p = static_cast<const uint8_t*>(raw);
+  if (qtype == GM_QTYPE_IQ4_XS) hipLaunchKernelGGL(k_dequant<GM_QTYPE_IQ4_XS>, grid, block, 0, s, p, n_sub, out);
+  else if (qtype == GM_QTYPE_IQ3_XXS) hipLaunchKernelGGL(k_dequant<GM_QTYPE_IQ3_XXS>, grid, block, 0, s, p, n_sub, out);
+  else return gm_fail_arg("gm_dequant_f32: unsupported qtype %d", qtype);
+  GM_TRY(hipGetLastError());
+  return GM_OK;
+}
+
+// --------------------------------------------------------------- matvec
+// Partial dot products of one lane for one row over its sub-blocks.
+template <int QT, int L, int NT>
+__device__ __forceinline__ void gm_row_partial(const uint8_t* __restrict__ row, int nsub, int lane_in_row,
+                                               const float* __restrict__ xs, int xstride, int nt,
+                                               const uint32_t* __restrict__ grid, float (&acc)[NT]) {
+  for (int sub = lane_in_row; sub < nsub; sub += L) {
+    const auto r = gm_load_sub<QT>(row, sub);
+    float wv[32];
+    const float sc = gm_decode_sub<QT>(r, sub, grid, wv);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (t < nt) acc[t] = fmaf(sc, gm_dot32(wv, xs + t * xstride + sub * GM_SUB), acc[t]);
+    }
+  }
+}
+
+// y[t][row] for the rows of this block; x staged as [NT][K] in LDS.
+template <int QT, int L, int NT>
+__global__ void __launch_bounds__(256) k_matvec(const uint8_t* __restrict__ w, int M, int K,
+                                                int64_t row_bytes, const float* __restrict__ x,
+                                                int n_tok, float* __restrict__ y, int rows_per_wave) {
+  extern __shared__ float smem[];
+  uint32_t* grid = reinterpret_cast<uint32_t*>(smem);
+  float* xs = smem + 256;
+  const int t0 = blockIdx.y * NT;
+  const int nt = min(NT, n_tok - t0);
+  for (int i = threadIdx.x; i < NT * K; i += 256) {
+    const int t = i / K;
+    xs[i] = t < nt ? x[(int64_t)(t0 + t) * K + (i - t * K)] : 0.f;
+  }
+  if constexpr (QT == GM_QTYPE_IQ3_XXS) gm_stage_grid(grid);
+  __syncthreads();
+
+  constexpr int RPS = 64 / L;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nsub = K / GM_SUB;
+  const int rbase = (blockIdx.x * 4 + wave) * rows_per_wave;
+  for (int r0 = 0; r0 < rows_per_wave; r0 += RPS) {
+    const int row = rbase + r0 + lane / L;
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.f;
+    if (row < M) gm_row_partial<QT, L, NT>(w + row * row_bytes, nsub, lane % L, xs, K, nt, grid, acc);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = gm_group_sum<L>(acc[t]);
+    if (row < M && (lane % L) == 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        if (t < nt) y[(int64_t)(t0 + t) * M + row] = acc[t];
+    }
+  }
+}
+
+template <int QT, int L, int NT>
+static int launch_matvec_t(const uint8_t* w, int M, int K, const float* x, int n_tok, float* y,
+                           hipStream_t s) {
+  constexpr int RPS = 64 / L;
+  const int rows_per_wave = 2 * RPS;
+  const int rows_per_block = 4 * rows_per_wave;
+  const dim3 grid((unsigned)((M + rows_per_block - 1) / rows_per_block), (unsigned)((n_tok + NT - 1) / NT));
+  const size_t smem = (256 + (size_t)NT * K) * sizeof(float);
+  if (int rc = gm_set_smem(k_matvec<QT, L, NT>, smem)) return rc;
+  hipLaunchKernelGGL((k_matvec<QT, L, NT>), grid, dim3(256), smem, s, w, M, K, gm_row_bytes(QT, K), x,
+                     n_tok, y, rows_per_wave);
+  GM_TRY(hipGetLastError());
+  return GM_OK;
+}
+
+template <int QT, int L>
+static int launch_matvec_l(const uint8_t* w, int M, int K, const float* x, int n_tok, float* y,
+                           hipStream_t s) {
+  if (n_tok == 1) return launch_matvec_t<QT, L, 1>(w, M, K, x, n_tok, y, s);
+  if (n_tok <= 4 && 4 * K <= 16384) return launch_matvec_t<QT, L, 4>(w, M, K, x, n_tok, y, s);
+  if (8 * K <= 16384) return launch_matvec_t<QT, L, 8>(w, M, K, x, n_tok, y, s);
+  if (4 * K <= 16384) return launch_matvec_t<QT, L, 4>(w, M, K, x, n_tok, y, s);
+  return launch_matvec_t<QT, L, 1>(w, M, K, x, n_tok, y, s);
+}
+
+template <int QT>
+static int launch_matvec_q(const uint8_t* w, int M, int K, const float* x, int n_tok, float* y,
+                           hipStream_t s) {
+  const int nsub = K / GM_SUB;
+  if (nsub >= 64) return launch_matvec_l<QT, 64>(w, M, K, x, n_tok, y, s);
+  if (nsub >= 32) return launch_matvec_l<QT, 32>(w, M, K, x, n_tok, y, s);
+  if (nsub >= 16) return launch_matvec_l<QT, 16>(w, M, K, x, n_tok, y, s);
+  if (nsub >= 8) return launch_matvec_l<QT, 8>(w, M, K, x, n_tok, y, s);
+  if (nsub >= 4) return launch_matvec_l<QT, 4>(w, M, K, x, n_tok, y, s);
+  if (nsub >= 2) return launch_matvec_l<QT, 2>(w, M, K, x, n_tok, y, s);
+  return launch_matvec_l<QT, 1>(w, M, K, x, n_tok, y, s);
+}
+
+int gm_launch_matvec(int qtype, const void* w, int M, int K, const float* x, int n_tok, float* y,
+                     hipStream_t s) {
+  const uint8_t* p = static_cast<const uint8_t*>(w);
+  switch (qtype) {
+    case GM_QTYPE_IQ4_XS: return launch_matvec_q<GM_QTYPE_IQ4_XS>(p, M, K, x, n_tok, y, s);
+    case GM_QTYPE_IQ3_XXS: return launch_matvec_q<GM_QTYPE_IQ3_XXS>(p, M, K, x, n_tok, y, s);
+    case GM_QTYPE_BF16: return launch_matvec_q<GM_QTYPE_BF16>(p, M, K, x, n_tok, y, s);
+    default: return gm_fail_arg("gm_matvec: unsupported qtype %d", qtype);
+  }
+}
+
+// ------------------------------------------------------ SwiGLU gate/up
+// h[t][r] = silu(G[r] . x[t]) * (U[r] . x[t]); one wave per RPS rows.
+template <int QT, int L, int NT>
+__global__ void __launch_bounds__(256) k_gateup(const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu,
+                                                int FF, int D, int64_t row_bytes,
+                                                const float* __restrict__ x, int n_tok,
+                                                float* __restrict__ h, int rows_per_wave) {
+  extern __shared__ float smem[];
+  uint32_t* grid = reinterpret_cast<uint32_t*>(smem);
+  float* xs = smem + 256;
+  const int t0 = blockIdx.y * NT;
+  const int nt = min(NT, n_tok - t0);
+  for (int i = threadIdx.x; i < NT * D; i += 256) {
+    const int t = i / D;
+    xs[i] = t < nt ? x[(int64_t)(t0 + t) * D + (i - t * D)] : 0.f;
+  }
+  if constexpr (QT == GM_QTYPE_IQ3_XXS) gm_stage_grid(grid);
+  __syncthreads();
+  constexpr int RPS = 64 / L;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nsub = D / GM_SUB;
+  const int rbase = (blockIdx.x * 4 + wave) * rows_per_wave;
+  for (int r0 = 0; r0 < rows_per_wave; r0 += RPS) {
+    const int row = rbase + r0 + lane / L;
+    float ag[NT], au[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) { ag[t] = 0.f; au[t] = 0.f; }
+    if (row < FF) {
+      gm_row_partial<QT, L, NT>(wg + row * row_bytes, nsub, lane % L, xs, D, nt, grid, ag);
+      gm_row_partial<QT, L, NT>(wu + row * row_bytes, nsub, lane % L, xs, D, nt, grid, au);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) { ag[t] = gm_group_sum<L>(ag[t]); au[t] = gm_group_sum<L>(au[t]); }
+    if (row < FF && (lane % L) == 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        if (t < nt) h[(int64_t)(t0 + t) * FF + row] = gm_silu(ag[t]) * au[t];
+    }
+  }
+}
+
+template <int QT, int L, int NT>
+static int launch_gateup_t(const uint8_t* wg, const uint8_t* wu, int FF, int D, const float* x, int n_tok,
+                           float* h, hipStream_t s) {
+  constexpr int RPS = 64 / L;
+  const int rows_per_wave = 2 * RPS;
+  const int rows_per_block = 4 * rows_per_wave;
+  const dim3 grid((unsigned)((FF + rows_per_block - 1) / rows_per_block), (unsigned)((n_tok + NT - 1) / NT));
+  const size_t smem = (256 + (size_t)NT * D) * sizeof(float);
+  if (int rc = gm_set_smem(k_gateup<QT, L, NT>, smem)) return rc;
+  hipLaunchKernelGGL((k_gateup<QT, L, NT>), grid, dim3(256), smem, s, wg, wu, FF, D, gm_row_bytes(QT, D), x,
+                     n_tok, h, rows_per_wave);
+  GM_TRY(hipGetLastError());
+  return GM_OK;
+}
+
+template <int QT>
+static int launch_gateup_q(const uint8_t* wg, const uint8_t* wu, int FF, int D, const float* x, int n_tok,
+                           float* h, hipStream_t s) {
+  const int nsub = D / GM_SUB;
+  const bool one = n_tok == 1;
+#define GM_GU(LL)                                                                     \
+  return one ? launch_gateup_t<QT, LL, 1>(wg, wu, FF, D, x, n_tok, h, s)              \
+             : (8 * D <= 16384 ? launch_gateup_t<QT, LL, 8>(wg, wu, FF, D, x, n_tok, h, s) \
+                               : launch_gateup_t<QT, LL, 1>(wg, wu, FF, D, x, n_tok, h, s))
+  if (nsub >= 64) GM_GU(64);
+  if (nsub >= 32) GM_GU(32);
+  if (nsub >= 16) GM_GU(16);
+  GM_GU(8);
+#undef GM_GU
+}
+
+int gm_launch_gateup(int qtype, const void* wg, const void* wu, int FF, int D, const float* x, int n_tok,
+                     float* h, hipStream_t s) {
+  const uint8_t* g = static_cast<const uint8_t*>(wg);
+  const uint8_t* u = static_cast<const uint8_t*>(wu);
+  switch (qtype) {
+    case GM_QTYPE_IQ4_XS: return launch_gateup_q<GM_QTYPE_IQ4_XS>(g, u, FF, D, x, n_tok, h, s);
+    case GM_QTYPE_IQ3_XXS: return launch_gateup_q<GM_QTYPE_IQ3_XXS>(g, u, FF, D, x, n_tok, h, s);
+    case GM_QTYPE_BF16: return launch_gateup_q<GM_QTYPE_BF16>(g, u, FF, D, x, n_tok, h, s);
+    default: return gm_fail_arg("gm_swiglu_mlp: unsupported gate/up qtype %d", qtype);
+  }
+}

@@ -1,0 +1,71 @@
+"""GGUF tensor duck types for the drop-in operators.
+
+gguf-py (reference dependency, pinned 0.18.0 at ``uv.lock:132-134``) is not
+available here; these stand-ins carry the attributes the reference's
+``from_gguf_tensor`` paths read (``npu/quant_mv.py:245-295``,
+``qwen/model.py:230-277``): ``tensor_type`` (ggml id), ``shape`` in ggml order
+``(in, out[, n_expert])``, ``data`` as uint8 ``(n_expert, out, bytes_per_row)``
+(or ``(out, bytes_per_row)`` for 2-D tensors) and ``name``.
+"""
+from __future__ import annotations
+
+import enum
+from dataclasses import dataclass
+
+import numpy as np
+
+QK = 256
+
+
+class GGMLQuantizationType(enum.IntEnum):
+    F32 = 0
+    F16 = 1
+    IQ3_XXS = 18
+    IQ4_XS = 23
+    BF16 = 30
+
+
+_BLOCK_BYTES = {
+    GGMLQuantizationType.IQ4_XS: 136,
+    GGMLQuantizationType.IQ3_XXS: 98,
+    GGMLQuantizationType.BF16: 2 * QK,
+    GGMLQuantizationType.F32: 4 * QK,
+}
+
+
+def block_bytes(qtype: int) -> int:
+    try:
+        return _BLOCK_BYTES[GGMLQuantizationType(int(qtype))]
+    except (KeyError, ValueError):
+        raise ValueError(f"unsupported ggml type {qtype}") from None
+
+
+def row_bytes(qtype: int, K: int) -> int:
+    if K % QK:
+        raise ValueError(f"K={K} must be a multiple of {QK}")
+    return (K // QK) * block_bytes(qtype)
+
+
+@dataclass
+class QuantTensor:
+    """A GGUF tensor record: raw bytes plus ggml metadata."""
+
+    name: str
+    tensor_type: GGMLQuantizationType
+    shape: tuple[int, ...]          # ggml order: (in, out[, n_expert])
+    data: np.ndarray                # uint8 (n_expert, out, row_bytes) or (out, row_bytes)
+
+    def __post_init__(self) -> None:
+        self.tensor_type = GGMLQuantizationType(int(self.tensor_type))
+        self.shape = tuple(int(s) for s in self.shape)
+        if self.data.dtype != np.uint8:
+            raise TypeError("data must be uint8")
+        k, m = self.shape[0], self.shape[1]
+        rb = row_bytes(self.tensor_type, k)
+        want = ((self.shape[2],) if len(self.shape) == 3 else ()) + (m, rb)
+        if tuple(self.data.shape) != want:
+            raise ValueError(f"{self.name}: data shape {self.data.shape} != {want}")
+
+    @property
+    def n_expert(self) -> int:
+        return self.shape[2] if len(self.shape) == 3 else 1

@@ -1,0 +1,155 @@
+"""Device-resident MoE block: raw GGUF expert stacks in HBM + the fused forward.
+
+``GpuMoeBlock`` owns one block's weights on the GPU in the layout GGUF stores
+them (experts outermost, rows of raw superblocks), fills the C struct
+``gm_moe_layer`` and runs ``gm_moe_forward``: router -> top-k -> expert
+grouping -> gate/up SwiGLU -> down -> weighted combine + shared expert, all on
+the device from device-resident ids.  Reference semantics:
+``qwen/forward.py:563-665`` (moe_forward).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from npu_amd import _lib as L
+from npu_amd import ops
+from npu_amd.gguf_types import GGMLQuantizationType as QT, row_bytes
+
+
+def _dev(a, dtype=None, device="cuda") -> torch.Tensor | None:
+    if a is None:
+        return None
+    if isinstance(a, torch.Tensor):
+        t = a.to(device)
+    else:
+        arr = np.ascontiguousarray(a)
+        if arr.dtype == np.uint16:
+            arr = arr.view(np.int16)
+        t = torch.from_numpy(arr).to(device)
+    if dtype is not None and t.dtype != dtype:
+        t = t.to(dtype)
+    return t.contiguous()
+
+
+class GpuMoeBlock:
+    """One MoE block resident on the GPU."""
+
+    def __init__(self, *, gate, up, down, router, q_gate: int, q_down: int, D: int, FF: int, E: int, k: int,
+                 gate_sh=None, up_sh=None, down_sh=None, q_gate_sh: int | None = None,
+                 q_down_sh: int | None = None, sh_gate_inp=None, router_bias=None, norm_w=None,
+                 norm_eps: float = 1e-6, device="cuda"):
+        L.require_gpu()
+        self.D, self.FF, self.E, self.k = int(D), int(FF), int(E), int(k)
+        self.q_gate, self.q_down = int(q_gate), int(q_down)
+        self.q_gate_sh = int(q_gate_sh if q_gate_sh is not None else q_gate)
+        self.q_down_sh = int(q_down_sh if q_down_sh is not None else q_down)
+        self.gate = _dev(gate, device=device)
+        self.up = _dev(up, device=device)
+        self.down = _dev(down, device=device)
+        self.router = _dev(router, device=device)
+        if self.router.dtype == torch.bfloat16:
+            self.router = self.router.view(torch.int16)
+        self.gate_sh = _dev(gate_sh, device=device)
+        self.up_sh = _dev(up_sh, device=device)
+        self.down_sh = _dev(down_sh, device=device)
+        if self.q_gate_sh == QT.BF16 and self.gate_sh is not None and self.gate_sh.dtype == torch.bfloat16:
+            self.gate_sh, self.up_sh = self.gate_sh.view(torch.int16), self.up_sh.view(torch.int16)
+        if self.q_down_sh == QT.BF16 and self.down_sh is not None and self.down_sh.dtype == torch.bfloat16:
+            self.down_sh = self.down_sh.view(torch.int16)
+        self.sh_gate_inp = _dev(sh_gate_inp, device=device)
+        if self.sh_gate_inp is not None and self.sh_gate_inp.dtype == torch.bfloat16:
+            self.sh_gate_inp = self.sh_gate_inp.view(torch.int16)
+        self.router_bias = _dev(router_bias, torch.float32, device)
+        self.norm_w = _dev(norm_w, torch.float32, device)
+        self.norm_eps = float(norm_eps)
+        self._check_shapes()
+        s = L.GmMoeLayer()
+        s.gate_exps, s.up_exps, s.down_exps = L.ptr(self.gate), L.ptr(self.up), L.ptr(self.down)
+        s.gate_sh, s.up_sh, s.down_sh = L.ptr(self.gate_sh), L.ptr(self.up_sh), L.ptr(self.down_sh)
+        s.router, s.sh_gate_inp = L.ptr(self.router), L.ptr(self.sh_gate_inp)
+        s.router_bias, s.norm_w = L.ptr(self.router_bias), L.ptr(self.norm_w)
+        s.norm_eps = self.norm_eps
+        s.q_gate = s.q_up = self.q_gate
+        s.q_down = self.q_down
+        s.q_gate_sh = s.q_up_sh = self.q_gate_sh
+        s.q_down_sh = self.q_down_sh
+        s.D, s.FF, s.FF_sh, s.E, s.k = self.D, self.FF, self.FF if self.gate_sh is not None else 0, self.E, self.k
+        self.struct = s
+        self._ws: dict[int, torch.Tensor] = {}
+
+    def _check_shapes(self) -> None:
+        D, FF, E = self.D, self.FF, self.E
+        want = {
+            "gate": (E, FF, row_bytes(self.q_gate, D)), "up": (E, FF, row_bytes(self.q_gate, D)),
+            "down": (E, D, row_bytes(self.q_down, FF)),
+        }
+        for name, shp in want.items():
+            t = getattr(self, name)
+            if tuple(t.shape) != shp or t.dtype != torch.uint8:
+                raise ValueError(f"{name}: expected uint8 {shp}, got {t.dtype} {tuple(t.shape)}")
+        if tuple(self.router.shape) != (E, D):
+            raise ValueError(f"router: expected ({E}, {D}), got {tuple(self.router.shape)}")
+        if self.gate_sh is not None:
+            rb = (lambda q, K: row_bytes(q, K) if q != QT.BF16 else 2 * K)
+            g_elt = 1 if self.gate_sh.dtype == torch.uint8 else 2
+            if self.gate_sh.numel() * g_elt != FF * rb(self.q_gate_sh, D):
+                raise ValueError("gate_sh size does not match FF x D")
+            d_elt = 1 if self.down_sh.dtype == torch.uint8 else 2
+            if self.down_sh.numel() * d_elt != D * rb(self.q_down_sh, FF):
+                raise ValueError("down_sh size does not match D x FF")
+
+    @classmethod
+    def from_host(cls, h, device="cuda") -> "GpuMoeBlock":
+        """Upload a ``synth.HostMoeLayer`` (or anything with the same fields)."""
+        return cls(gate=h.gate, up=h.up, down=h.down, router=h.router, q_gate=h.q_gate, q_down=h.q_down,
+                   D=h.D, FF=h.FF, E=h.E, k=h.k, gate_sh=h.gate_sh, up_sh=h.up_sh, down_sh=h.down_sh,
+                   sh_gate_inp=h.sh_gate_inp, router_bias=h.router_bias, norm_w=h.norm_w, device=device)
+
+    # ------------------------------------------------------------------
+    def workspace(self, T: int) -> torch.Tensor:
+        ws = self._ws.get(T)
+        if ws is None:
+            n = ops.moe_workspace_bytes(self.struct, T)
+            ws = torch.zeros(n, dtype=torch.uint8, device=self.gate.device)
+            self._ws[T] = ws
+        return ws
+
+    def forward(self, x: torch.Tensor, *, residual: bool = False, out: torch.Tensor | None = None,
+                stage: int = 0) -> torch.Tensor:
+        """x fp32 [T, D] on the GPU -> y [T, D] = moe(rmsnorm(x)) (+ x).
+
+        ``stage`` 1..3 runs one decode stage only (router, gate/up, down)."""
+        if x.dim() != 2 or x.shape[1] != self.D:
+            raise ValueError(f"x must be [T, {self.D}], got {tuple(x.shape)}")
+        x = x.to(torch.float32).contiguous()
+        T = x.shape[0]
+        y = out if out is not None else torch.empty_like(x)
+        ops.moe_forward_raw(self.struct, x, y, self.workspace(T), residual=residual, stage=stage)
+        return y
+
+    __call__ = forward
+
+    def stages(self, T: int) -> dict[str, torch.Tensor]:
+        """Views of the last call's intermediates (router logits, ids, weights, shared gate)."""
+        ws = self.workspace(T)
+        off = ops.moe_workspace_offsets(self.struct, T)
+        E, k = self.E, self.k
+
+        def view(o, n, dt):
+            return ws[o:o + n * 4].view(dt)
+
+        return {
+            "ffn_moe_logits": view(off["logits"], T * E, torch.float32).view(T, E),
+            "topk_ids": view(off["ids"], T * k, torch.int32).view(T, k),
+            "ffn_moe_weights_norm": view(off["weights"], T * k, torch.float32).view(T, k),
+            "shared_expert_gate_sigmoid": view(off["sh_gate"], T, torch.float32),
+        }
+
+    def weight_bytes_per_token(self) -> int:
+        per_exp = (self.gate[0].numel() + self.up[0].numel() + self.down[0].numel())
+        sh = 0
+        if self.gate_sh is not None:
+            sh = sum(t.numel() * t.element_size() for t in (self.gate_sh, self.up_sh, self.down_sh))
+        g = 0 if self.sh_gate_inp is None else self.sh_gate_inp.numel() * 2
+        return self.k * per_exp + sh + self.router.numel() * 2 + g

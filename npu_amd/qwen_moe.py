@@ -1,0 +1,264 @@
+"""Drop-in for the MoE half of the reference's ``qwen/forward.py``.
+
+Same names and call signatures as the reference: ``MoELayer`` (438-491),
+``moe_forward(x, layer, cfg)`` (563-665), ``enable_npu(model, ops, *,
+expert_cache_limit)`` (723-831) with the same op names and ``layer.npu`` keys,
+and ``rms_norm`` (58-61).  The difference is where the block runs: the whole
+MoE block (router, top-k, dispatch, expert products, shared expert, combine)
+executes on the GPU from raw GGUF expert bytes resident in HBM, with routing
+kept on the device (no ``picked.tolist()`` host loop).  There is no CPU path:
+``moe_forward`` builds the device block on first use if ``enable_npu`` was not
+called.  Prefill (T > 8 tokens) uses the grouped bf16-MFMA kernels.
+
+``SyntheticTensorStore`` provides the ``TensorStore`` surface (``get``,
+``raw``, ``get_expert``, ``cfg``) over seeded synthetic layers, since the
+reference's 16 GB GGUF is not available.
+"""
+from __future__ import annotations
+
+from collections import OrderedDict
+from dataclasses import dataclass, field
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from npu_amd import ops
+from npu_amd._dropin import device
+from npu_amd.gguf_types import GGMLQuantizationType as QT, QuantTensor, row_bytes
+from npu_amd.moe import GpuMoeBlock
+from npu_amd.profiler import profile
+
+VALID_OPS = {"router", "shexp", "shexp_split", "attn_o", "attn_qkv", "ssm",
+             "experts", "experts_split", "experts_dense", "experts_packed_down"}
+
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    x_f = x.float()
+    rms = x_f.pow(2).mean(-1, keepdim=True).add(eps).rsqrt()
+    return ((x_f * rms) * w.float()).to(x.dtype)
+
+
+@dataclass
+class Config:
+    """The ``qwen/model.py:Config`` fields the MoE block reads."""
+
+    d_model: int = 2048
+    n_expert: int = 256
+    n_expert_used: int = 8
+    d_expert_ff: int = 512
+    rms_eps: float = 1e-6
+    n_layer: int = 1
+
+
+# ------------------------------------------------------------- tensor store
+class SyntheticTensorStore:
+    """GGUF-TensorStore stand-in over ``synth.HostMoeLayer`` blocks.
+
+    Names follow the GGUF file (``blk.{i}.ffn_gate_exps.weight`` ...); quantised
+    tensors come back from ``raw`` as ``QuantTensor`` records with ggml-order
+    shapes, dense ones from ``get`` as fp32 numpy arrays in (out, in) order.
+    """
+
+    def __init__(self, layers, cfg: Config | None = None):
+        self.layers = list(layers)
+        h = self.layers[0]
+        self.cfg = cfg or Config(d_model=h.D, n_expert=h.E, n_expert_used=h.k, d_expert_ff=h.FF,
+                                 n_layer=len(self.layers))
+        self._raw: dict[str, QuantTensor] = {}
+        self._dense: dict[str, np.ndarray] = {}
+        for i, L in enumerate(self.layers):
+            p = f"blk.{i}."
+            self._raw[p + "ffn_gate_exps.weight"] = QuantTensor(p + "ffn_gate_exps.weight", L.q_gate, (L.D, L.FF, L.E), L.gate)
+            self._raw[p + "ffn_up_exps.weight"] = QuantTensor(p + "ffn_up_exps.weight", L.q_gate, (L.D, L.FF, L.E), L.up)
+            self._raw[p + "ffn_down_exps.weight"] = QuantTensor(p + "ffn_down_exps.weight", L.q_down, (L.FF, L.D, L.E), L.down)
+            if L.gate_sh is not None:
+                self._raw[p + "ffn_gate_shexp.weight"] = QuantTensor(p + "ffn_gate_shexp.weight", L.q_gate, (L.D, L.FF), L.gate_sh)
+                self._raw[p + "ffn_up_shexp.weight"] = QuantTensor(p + "ffn_up_shexp.weight", L.q_gate, (L.D, L.FF), L.up_sh)
+                self._raw[p + "ffn_down_shexp.weight"] = QuantTensor(p + "ffn_down_shexp.weight", L.q_down, (L.FF, L.D), L.down_sh)
+            from npu_amd.synth import from_bf16
+            self._dense[p + "ffn_gate_inp.weight"] = from_bf16(L.router).reshape(L.E, L.D)
+            if L.sh_gate_inp is not None:
+                self._dense[p + "ffn_gate_inp_shexp.weight"] = from_bf16(L.sh_gate_inp)
+            if L.norm_w is not None:
+                self._dense[p + "post_attention_norm.weight"] = L.norm_w
+            if L.router_bias is not None:
+                self._dense[p + "ffn_gate_inp.bias"] = L.router_bias
+
+    def names(self) -> list[str]:
+        return list(self._raw) + list(self._dense)
+
+    def has(self, name: str) -> bool:
+        return name in self._raw or name in self._dense
+
+    def raw(self, name: str):
+        t = self._raw.get(name)
+        if t is None:
+            raise KeyError(name)
+        return t
+
+    def get(self, name: str, dtype: str = "fp32", keep: bool = True) -> np.ndarray:
+        if name in self._dense:
+            return self._dense[name]
+        t = self.raw(name)
+        full = ops.dequant(t.tensor_type, torch.from_numpy(np.ascontiguousarray(t.data).reshape(-1)).to(device()))
+        return full.cpu().numpy().reshape(tuple(reversed(t.shape)))
+
+    def get_expert(self, name: str, expert_idx: int, dtype: str = "fp32") -> np.ndarray:
+        t = self.raw(name)
+        if len(t.shape) != 3:
+            raise ValueError(f"{name} is not a stacked expert tensor (got shape {list(t.shape)})")
+        if not 0 <= expert_idx < t.shape[2]:
+            raise IndexError(expert_idx)
+        chunk = np.ascontiguousarray(t.data[expert_idx]).reshape(-1)
+        full = ops.dequant(t.tensor_type, torch.from_numpy(chunk).to(device()))
+        return full.cpu().numpy().reshape(t.shape[1], t.shape[0])
+
+
+# ------------------------------------------------------------------ layer
+def _w(ts, name: str, dtype=torch.float32) -> torch.Tensor | None:
+    if not ts.has(name):
+        return None
+    return torch.from_numpy(np.array(ts.get(name, dtype="fp32", keep=False), copy=True)).to(dtype)
+
+
+@dataclass
+class MoELayer:
+    """Same fields as the reference's ``MoELayer``; ``npu`` holds the device block."""
+
+    i: int
+    ts: object = field(repr=False)
+    dtype: torch.dtype = torch.float32
+    w_router: torch.Tensor | None = None          # [n_expert, D]
+    w_gate_sh: torch.Tensor | None = None          # [ff_sh, D] (dense models) or None
+    w_up_sh: torch.Tensor | None = None
+    w_down_sh: torch.Tensor | None = None          # [D, ff_sh]
+    w_gate_inp_sh: torch.Tensor | None = None      # [D]
+    npu: dict | None = None
+
+    @classmethod
+    def load(cls, ts, i: int, dtype=torch.float32) -> "MoELayer":
+        p = f"blk.{i}."
+
+        def dense_or_none(name):
+            if not ts.has(name):
+                return None
+            try:
+                raw = ts.raw(name)
+            except KeyError:
+                raw = None
+            if raw is not None and int(raw.tensor_type) in (QT.IQ4_XS, QT.IQ3_XXS):
+                return None          # quantised shared expert stays raw (see enable_npu)
+            return _w(ts, name, dtype)
+
+        return cls(i=i, ts=ts, dtype=dtype,
+                   w_router=_w(ts, p + "ffn_gate_inp.weight", dtype),
+                   w_gate_sh=dense_or_none(p + "ffn_gate_shexp.weight"),
+                   w_up_sh=dense_or_none(p + "ffn_up_shexp.weight"),
+                   w_down_sh=dense_or_none(p + "ffn_down_shexp.weight"),
+                   w_gate_inp_sh=_w(ts, p + "ffn_gate_inp_shexp.weight", dtype))
+
+    def dequant_one(self, expert_idx: int):
+        """(gate[ff,D], up[ff,D], down[D,ff]) of one expert, dequantised on the GPU."""
+        p = f"blk.{self.i}."
+        out = []
+        for n in ("ffn_gate_exps.weight", "ffn_up_exps.weight", "ffn_down_exps.weight"):
+            out.append(torch.from_numpy(self.ts.get_expert(p + n, expert_idx).copy()).to(self.dtype))
+        return tuple(out)
+
+
+def _build_block(layer: MoELayer) -> GpuMoeBlock:
+    ts = layer.ts
+    p = f"blk.{layer.i}."
+    g, u, d = (ts.raw(p + n) for n in ("ffn_gate_exps.weight", "ffn_up_exps.weight", "ffn_down_exps.weight"))
+    if int(g.tensor_type) != int(u.tensor_type):
+        raise NotImplementedError("gate and up experts must share a quant type")
+    D, FF, E = int(g.shape[0]), int(g.shape[1]), int(g.shape[2])
+    cfg = getattr(ts, "cfg", None)
+    k = int(getattr(cfg, "n_expert_used", 8))
+    router = torch.from_numpy(np.ascontiguousarray(layer.w_router.float().numpy())).to(torch.bfloat16)
+    kw = {}
+    if layer.w_gate_sh is not None:              # dense shared expert (the real model): bf16
+        kw.update(gate_sh=layer.w_gate_sh.to(torch.bfloat16), up_sh=layer.w_up_sh.to(torch.bfloat16),
+                  down_sh=layer.w_down_sh.to(torch.bfloat16), q_gate_sh=QT.BF16, q_down_sh=QT.BF16)
+    elif ts.has(p + "ffn_gate_shexp.weight"):     # quantised shared expert kept raw
+        gs, us, ds = (ts.raw(p + n) for n in ("ffn_gate_shexp.weight", "ffn_up_shexp.weight",
+                                               "ffn_down_shexp.weight"))
+        kw.update(gate_sh=gs.data, up_sh=us.data, down_sh=ds.data, q_gate_sh=int(gs.tensor_type),
+                  q_down_sh=int(ds.tensor_type))
+    sh_inp = None
+    if layer.w_gate_inp_sh is not None:
+        sh_inp = layer.w_gate_inp_sh.float().to(torch.bfloat16)
+    bias = torch.from_numpy(ts.get(p + "ffn_gate_inp.bias")) if ts.has(p + "ffn_gate_inp.bias") else None
+    return GpuMoeBlock(gate=g.data, up=u.data, down=d.data, router=router, q_gate=int(g.tensor_type),
+                       q_down=int(d.tensor_type), D=D, FF=FF, E=E, k=k, sh_gate_inp=sh_inp, router_bias=bias,
+                       device=device(), **kw)
+
+
+def _expert_cache_limit_from_env(default: int) -> int | None:
+    import os
+    raw = os.environ.get("QWEN_NPU_EXPERT_CACHE_LIMIT")
+    if raw is None or raw == "":
+        return default
+    val = raw.strip().lower()
+    if val in {"none", "unlimited", "inf", "-1"}:
+        return None
+    limit = int(val)
+    return None if limit < 0 else limit
+
+
+def enable_npu(model, ops: Sequence[str] = ("router",), *, expert_cache_limit: int | None = None) -> None:
+    """Attach device operators to every MoE layer of ``model`` (same op names as the reference).
+
+    Every expert-family op makes the layer run through the fused device block;
+    ``router`` / ``shexp`` / ``shexp_split`` additionally expose the stand-alone
+    operators under the reference's ``layer.npu`` keys.  The expert cache limit
+    is kept for compatibility: all experts are resident in HBM, so nothing is
+    evicted.  ``attn_*`` / ``ssm`` are outside this package's path and ignored.
+    """
+    from npu_amd.mlp import NpuFusedMLP
+    from npu_amd.mv import NpuMatVec
+
+    unknown = set(ops) - VALID_OPS
+    if unknown:
+        raise ValueError(f"unknown NPU ops: {sorted(unknown)} (valid: {sorted(VALID_OPS)})")
+    layers = [m for _, m in model.layers] if hasattr(model, "layers") else list(model)
+    for moe in layers:
+        if moe.npu is None:
+            moe.npu = {}
+        if "router" in ops:
+            moe.npu["router"] = NpuMatVec(moe.w_router)
+        if "shexp" in ops and moe.w_gate_sh is not None:
+            moe.npu["sh_mlp"] = NpuFusedMLP(moe.w_gate_sh, moe.w_down_sh, w_up=moe.w_up_sh)
+        if "shexp_split" in ops and moe.w_gate_sh is not None:
+            moe.npu["sh_gate"] = NpuMatVec(moe.w_gate_sh)
+            moe.npu["sh_up"] = NpuMatVec(moe.w_up_sh)
+            moe.npu["sh_down"] = NpuMatVec(moe.w_down_sh)
+        if {"experts", "experts_split", "experts_dense", "experts_packed_down"} & set(ops):
+            p = f"blk.{moe.i}."
+            moe.npu["expert_tensors"] = tuple(moe.ts.raw(p + n) for n in (
+                "ffn_gate_exps.weight", "ffn_up_exps.weight", "ffn_down_exps.weight"))
+            moe.npu["expert_cache"] = OrderedDict()
+            moe.npu["expert_dense"] = "experts_dense" in ops
+            moe.npu["expert_fused"] = "experts" in ops
+            moe.npu["expert_packed_down"] = "experts_packed_down" in ops
+            moe.npu["expert_cache_limit"] = (_expert_cache_limit_from_env(8) if expert_cache_limit is None
+                                             else (None if expert_cache_limit < 0 else expert_cache_limit))
+        moe.npu["moe_block"] = _build_block(moe)
+
+
+def moe_forward(x: torch.Tensor, layer: MoELayer, cfg) -> torch.Tensor:
+    """x [B, T, D] -> [B, T, D]: the whole MoE block on the GPU (reference :563-665)."""
+    B, T, D = x.shape
+    if layer.npu is None:
+        layer.npu = {}
+    blk = layer.npu.get("moe_block")
+    if blk is None:
+        blk = layer.npu["moe_block"] = _build_block(layer)
+    on_host = not x.is_cuda
+    with profile("moe.block"):
+        xf = x.reshape(B * T, D).to(device() if on_host else x.device, torch.float32).contiguous()
+        y = blk(xf)
+    if on_host:
+        y = y.cpu()
+    return y.to(x.dtype).view(B, T, D)

@@ -1,0 +1,156 @@
+"""Seeded synthetic inputs with the distributions BASELINE.json's configs state.
+
+* IQ4_XS superblock (136 B): fp16 d = |N(0,1)| * 2e-3, then uniform random
+  scales_h (u16), scales_l (4 x u8) and qs (128 x u8).
+* IQ3_XXS superblock (98 B): fp16 d = |N(0,1)| * 2e-3, then 64 uniform qs bytes
+  and 8 uniform u32 sign/scale words (four 7-bit ksigns indices + a 4-bit
+  scale each, uniform == a uniform u32).
+* Router: bf16(N(0, 0.02)) [E, D]; shared-expert scalar gate bf16(N(0, 0.02)) [D].
+* Activations: fp32 N(0, 1), RMSNorm'd (eps 1e-6, weight 1) where the config says so.
+* Prefill skew: per-expert router-logit bias ~ N(0, 1).
+
+Two generators produce these: ``host_*`` (numpy PCG64, used by the tests and
+small configs, bytes reproducible anywhere) and ``device_*`` (torch's seeded
+GPU generator, for the ~16 GB 40-layer decode config where host generation
+would take minutes).  Both follow the same distributions; their bytes differ.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from npu_amd.gguf_types import QK, GGMLQuantizationType as QT, block_bytes, row_bytes
+
+D_SCALE = 2e-3
+ROUTER_STD = 0.02
+
+
+def to_bf16(a: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits (uint16), round to nearest even (as qwen/model.py:280-289)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def from_bf16(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def _gen(seed: int, *stream: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(np.random.SeedSequence([int(seed), *map(int, stream)])))
+
+
+# ------------------------------------------------------------------ host
+def host_superblocks(g: np.random.Generator, qtype: int, n_sb: int) -> np.ndarray:
+    """uint8 [n_sb, block_bytes] raw superblocks."""
+    bb = block_bytes(qtype)
+    if qtype not in (QT.IQ4_XS, QT.IQ3_XXS):
+        raise ValueError(f"not a superblock format: {qtype}")
+    out = np.empty((n_sb, bb), dtype=np.uint8)
+    d = (np.abs(g.standard_normal(n_sb)) * D_SCALE).astype(np.float16)
+    out[:, 0:2] = d.view(np.uint8).reshape(n_sb, 2)
+    out[:, 2:] = g.integers(0, 256, size=(n_sb, bb - 2), dtype=np.uint8)
+    return out
+
+
+def host_quant_matrix(g: np.random.Generator, qtype: int, M: int, K: int, n_expert: int | None = None) -> np.ndarray:
+    """Raw weight bytes [n_expert?, M, row_bytes] for an [M x K] matrix (per expert)."""
+    E = 1 if n_expert is None else n_expert
+    sb = host_superblocks(g, qtype, E * M * (K // QK))
+    shape = (M, row_bytes(qtype, K)) if n_expert is None else (E, M, row_bytes(qtype, K))
+    return sb.reshape(shape)
+
+
+def host_bf16_normal(g: np.random.Generator, shape, std: float) -> np.ndarray:
+    return to_bf16((g.standard_normal(shape) * std).astype(np.float32))
+
+
+def rms_norm_np(x: np.ndarray, eps: float = 1e-6, w: np.ndarray | None = None) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float32)
+    rms = (1.0 / np.sqrt((x.astype(np.float32) ** 2).mean(-1, keepdims=True) + np.float32(eps))).astype(np.float32)
+    y = (x * rms).astype(np.float32)
+    return y if w is None else (y * w).astype(np.float32)
+
+
+def host_input(seed: int, T: int, D: int, rmsnorm: bool = True) -> np.ndarray:
+    x = _gen(seed, 99).standard_normal((T, D)).astype(np.float32)
+    return rms_norm_np(x) if rmsnorm else x
+
+
+@dataclass
+class HostMoeLayer:
+    """One MoE block's weights as raw host arrays (GGUF layout)."""
+
+    D: int
+    FF: int
+    E: int
+    k: int
+    q_gate: int
+    q_down: int
+    gate: np.ndarray          # uint8 [E, FF, row_bytes(q_gate, D)]
+    up: np.ndarray            # uint8 [E, FF, row_bytes(q_gate, D)]
+    down: np.ndarray          # uint8 [E, D, row_bytes(q_down, FF)]
+    router: np.ndarray        # uint16 bf16 bits [E, D]
+    gate_sh: np.ndarray | None = None   # uint8 [FF, row_bytes(q_gate, D)]
+    up_sh: np.ndarray | None = None
+    down_sh: np.ndarray | None = None   # uint8 [D, row_bytes(q_down, FF)]
+    sh_gate_inp: np.ndarray | None = None  # uint16 bf16 bits [D]
+    router_bias: np.ndarray | None = None  # float32 [E]
+    norm_w: np.ndarray | None = None       # float32 [D]
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def q_up(self) -> int:
+        return self.q_gate
+
+    def weight_bytes_per_token(self) -> int:
+        """Raw bytes one T=1 decode reads: k experts + shared + router + shared gate."""
+        per_exp = self.gate[0].nbytes + self.up[0].nbytes + self.down[0].nbytes
+        sh = 0 if self.gate_sh is None else self.gate_sh.nbytes + self.up_sh.nbytes + self.down_sh.nbytes
+        g = 0 if self.sh_gate_inp is None else self.sh_gate_inp.nbytes
+        return self.k * per_exp + sh + self.router.nbytes + g
+
+
+def host_moe_layer(seed: int, *, D: int = 2048, FF: int = 512, E: int = 256, k: int = 8,
+                   q_gate: int = QT.IQ4_XS, q_down: int = QT.IQ3_XXS, shared: bool = True,
+                   bias: bool = False, norm: bool = False) -> HostMoeLayer:
+    """Config-3/4 style MoE block (defaults: BASELINE's IQ4_XS gate/up, IQ3_XXS down)."""
+    L = HostMoeLayer(
+        D=D, FF=FF, E=E, k=k, q_gate=int(q_gate), q_down=int(q_down),
+        gate=host_quant_matrix(_gen(seed, 1), q_gate, FF, D, E),
+        up=host_quant_matrix(_gen(seed, 2), q_gate, FF, D, E),
+        down=host_quant_matrix(_gen(seed, 3), q_down, D, FF, E),
+        router=host_bf16_normal(_gen(seed, 4), (E, D), ROUTER_STD),
+    )
+    if shared:
+        L.gate_sh = host_quant_matrix(_gen(seed, 5), q_gate, FF, D)
+        L.up_sh = host_quant_matrix(_gen(seed, 6), q_gate, FF, D)
+        L.down_sh = host_quant_matrix(_gen(seed, 7), q_down, D, FF)
+        L.sh_gate_inp = host_bf16_normal(_gen(seed, 8), (D,), ROUTER_STD)
+    if bias:
+        L.router_bias = _gen(seed, 9).standard_normal(E).astype(np.float32)
+    if norm:
+        L.norm_w = (1.0 + 0.1 * _gen(seed, 10).standard_normal(D)).astype(np.float32)
+    return L
+
+
+# ---------------------------------------------------------------- device
+def _dev_superblocks(gen: torch.Generator, qtype: int, n_sb: int, device) -> torch.Tensor:
+    bb = block_bytes(qtype)
+    out = torch.randint(0, 256, (n_sb, bb), dtype=torch.uint8, device=device, generator=gen)
+    d = (torch.randn(n_sb, device=device, generator=gen).abs() * D_SCALE).to(torch.float16)
+    out[:, 0:2] = d.view(torch.uint8).reshape(n_sb, 2)
+    return out
+
+
+def device_quant_matrix(gen: torch.Generator, qtype: int, M: int, K: int, n_expert: int | None = None,
+                        device="cuda") -> torch.Tensor:
+    E = 1 if n_expert is None else n_expert
+    sb = _dev_superblocks(gen, qtype, E * M * (K // QK), device)
+    shape = (M, row_bytes(qtype, K)) if n_expert is None else (E, M, row_bytes(qtype, K))
+    return sb.reshape(shape)
+
+
+def device_bf16_normal(gen: torch.Generator, shape, std: float, device="cuda") -> torch.Tensor:
+    return (torch.randn(shape, device=device, generator=gen) * std).to(torch.bfloat16)

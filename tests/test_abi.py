@@ -1,0 +1,78 @@
+"""The C-ABI library loads and exports every entry point include/npu_amd.h declares.
+
+Runs without a GPU: only host-side paths (argument validation, workspace
+sizing) are exercised, never a kernel launch.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from npu_amd import _lib as L
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = (ROOT / "include" / "npu_amd.h").read_text()
+
+
+def declared_functions():
+    body = re.sub(r"/\*.*?\*/", "", HEADER, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\*?\s+\*?(gm_\w+)\s*\(", body, flags=re.M)))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    assert {"gm_dequant_f32", "gm_matvec", "gm_moe_forward", "gm_router_topk", "gm_moe_dispatch"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in include/npu_amd.h but not exported"
+        assert name in L.SIGNATURES, f"{name} has no ctypes signature in npu_amd._lib"
+
+
+def test_struct_layout_matches_header():
+    fields = re.search(r"typedef struct gm_moe_layer \{(.*?)\} gm_moe_layer;", HEADER, re.S).group(1)
+    names = re.findall(r"(\w+)(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?;", fields)
+    flat = [n for grp in names for n in grp if n]
+    assert flat == [f for f, _ in L.GmMoeLayer._fields_]
+
+
+def test_argument_errors_without_gpu():
+    lib = L.lib()
+    rc = lib.gm_matvec(L.GM_QTYPE_IQ4_XS, None, 512, 500, None, 1, None, None)
+    assert rc == L.GM_EINVAL and "multiple of 256" in L.last_error()
+    rc = lib.gm_dequant_f32(7, None, 1, None, None)
+    assert rc == L.GM_EINVAL and "qtype" in L.last_error()
+    assert lib.gm_dequant_f32(L.GM_QTYPE_IQ3_XXS, None, 0, None, None) == L.GM_OK
+    with pytest.raises(ValueError):
+        L.check(L.GM_EINVAL, "x")
+
+
+def _layer(**kw):
+    s = L.GmMoeLayer()
+    s.gate_exps = s.up_exps = s.down_exps = s.router = 256
+    s.q_gate = s.q_up = L.GM_QTYPE_IQ4_XS
+    s.q_down = L.GM_QTYPE_IQ3_XXS
+    s.D, s.FF, s.FF_sh, s.E, s.k = 2048, 512, 0, 256, 8
+    for k, v in kw.items():
+        setattr(s, k, v)
+    return s
+
+
+def test_workspace_sizing_and_layer_validation():
+    lib = L.lib()
+    s = _layer()
+    n1 = lib.gm_moe_workspace_bytes(ctypes.byref(s), 1)
+    n8 = lib.gm_moe_workspace_bytes(ctypes.byref(s), 8)
+    assert 0 < n1 < n8
+    assert n1 % 256 == 0
+    bad = _layer(k=9)
+    assert lib.gm_moe_workspace_bytes(ctypes.byref(bad), 1) == 0
+    bad = _layer(q_up=L.GM_QTYPE_IQ3_XXS)
+    assert lib.gm_moe_workspace_bytes(ctypes.byref(bad), 1) == 0
+    rc = lib.gm_moe_forward(ctypes.byref(s), 1024, 1024, 1, 0, 4096, 16, None)
+    assert rc == L.GM_EINVAL and "alias" in L.last_error()
+    rc = lib.gm_moe_forward(ctypes.byref(s), 1024, 2048, 1, 0, 4096, 16, None)
+    assert rc == L.GM_EWORKSPACE and "workspace" in L.last_error()

@@ -1,0 +1,91 @@
+"""GPU parity of the drop-in operators (reference npu/*.py and qwen/forward.py names)."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from npu_amd import iq3_xxs, mlp, mv, quant_mv, quant_mv_iq4, quant_mv_iq4_packed, qwen_moe, synth
+from npu_amd.gguf_types import GGMLQuantizationType as QT, QuantTensor
+from oracle import moe as OM
+from oracle import quants as Q
+
+pytestmark = pytest.mark.gpu
+
+
+def _stack(qtype, E, M, K, seed):
+    g = np.random.Generator(np.random.PCG64(seed))
+    return QuantTensor("t", qtype, (K, M, E), synth.host_quant_matrix(g, qtype, M, K, E))
+
+
+@pytest.mark.parametrize("cls,qtype,M,K", [
+    (quant_mv.NpuQuantMatVec, QT.IQ3_XXS, 512, 2048),
+    (quant_mv_iq4.NpuIQ4MatVec, QT.IQ4_XS, 2048, 512),
+    (quant_mv_iq4_packed.NpuIQ4PackedMatVec, QT.IQ4_XS, 2048, 512),
+])
+def test_quant_operators_from_gguf_tensor(gpu, cls, qtype, M, K):
+    t = _stack(qtype, 4, M, K, 3)
+    op = cls.from_gguf_tensor(t, expert_idx=2)
+    x = torch.randn(K, generator=torch.Generator().manual_seed(0)) * 0.05   # qwen/test_npu_experts.py:68
+    y = op(x)                                  # CPU in, CPU out (reference behaviour)
+    assert y.shape == (M,) and y.device.type == "cpu"
+    ref = F.linear(x, torch.from_numpy(Q.dequant_matrix(t.data[2], qtype, M, K)))
+    assert OM.cos(y, ref) >= 0.999999 and OM.rel_err(y, ref) <= 1e-3
+    y2 = op(x.reshape(1, 1, K).to(gpu))       # GPU in, GPU out; batched shape kept
+    assert y2.is_cuda and y2.shape == (1, 1, M)
+    assert torch.equal(y2.cpu().reshape(-1), y)
+    with pytest.raises(AssertionError):
+        op(torch.zeros(K + 1))
+
+
+def test_npu_matvec_and_concat(gpu):
+    g = torch.Generator().manual_seed(1)
+    Ws = [torch.randn(r, 2048, generator=g) * 0.02 for r in (256, 64, 32)]
+    x = torch.randn(2048, generator=g)
+    y = mv.NpuMatVec(Ws[0])(x)
+    ref = F.linear(x, Ws[0].to(torch.bfloat16).float())
+    assert OM.rel_err(y, ref) <= 1e-5
+    op = mv.NpuConcatMatVec(tuple(Ws))
+    yc = op(x)
+    refc = F.linear(x, torch.cat(Ws).to(torch.bfloat16).float())
+    assert op.out_splits == (256, 64, 32) and OM.rel_err(yc, refc) <= 1e-5
+
+
+@pytest.mark.parametrize("stacked", [False, True])
+def test_npu_fused_mlp(gpu, stacked):
+    g = torch.Generator().manual_seed(2)
+    hidden, ffn = 2048, 512
+    wg, wu, wd = (torch.randn(ffn, hidden, generator=g) * 0.02, torch.randn(ffn, hidden, generator=g) * 0.02,
+                  torch.randn(hidden, ffn, generator=g) * 0.02)
+    x = torch.randn(hidden, generator=g)
+    op = mlp.NpuFusedMLP(torch.cat([wg, wu]), wd) if stacked else mlp.NpuFusedMLP(wg, wd, w_up=wu)
+    y = op(x)
+    b = lambda w: w.to(torch.bfloat16).float()
+    ref = F.linear(F.silu(F.linear(x, b(wg))) * F.linear(x, b(wu)), b(wd))
+    assert OM.rel_err(y, ref) <= 1e-4
+    assert torch.equal(op(x), y), "repeat determinism (qwen/test_npu_shexp_fused.py:73-74)"
+
+
+def test_iq3_xxs_module(gpu):
+    g = np.random.Generator(np.random.PCG64(4))
+    blocks = synth.host_superblocks(g, QT.IQ3_XXS, 16)
+    assert np.array_equal(iq3_xxs.dequant_rows(blocks), Q.dequant_iq3_xxs(blocks))
+    assert np.array_equal(iq3_xxs.dequant_block(blocks[3].tobytes()), Q.dequant_iq3_xxs(blocks[3]))
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_qwen_moe_forward_dropin(gpu, T):
+    hs = [synth.host_moe_layer(40 + i, D=2048, FF=512, E=64, k=8) for i in range(2)]
+    ts = qwen_moe.SyntheticTensorStore(hs)
+    layers = [qwen_moe.MoELayer.load(ts, i) for i in range(2)]
+    qwen_moe.enable_npu(layers, ops=("router", "experts", "experts_packed_down"))
+    assert "router" in layers[0].npu and "expert_tensors" in layers[0].npu
+    x = torch.from_numpy(synth.host_input(9, T, 2048)).reshape(1, T, 2048)
+    for i, L in enumerate(layers):
+        y = qwen_moe.moe_forward(x, L, ts.cfg)
+        assert y.shape == x.shape and y.device.type == "cpu"
+        ref = OM.moe_forward(x, OM.OracleLayer(hs[i]))
+        assert OM.rel_err(y, ref) <= 1e-3
+    # dequant_one mirrors MoELayer.dequant_one (qwen/forward.py:480-491)
+    g, u, d = layers[0].dequant_one(5)
+    assert torch.equal(g, torch.from_numpy(Q.dequant_matrix(hs[0].gate[5], hs[0].q_gate, 512, 2048)))
+    assert d.shape == (2048, 512)

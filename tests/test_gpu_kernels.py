@@ -1,0 +1,126 @@
+"""GPU parity: dequant, matvec, SwiGLU MLP, router top-k and dispatch vs the CPU oracle.
+
+Tolerances: dequant is float-equal (exact products); fp32-accumulate
+products use rel = max|y - ref| / max|ref| <= 1e-3 (
+qwen/test_npu_experts.py:93 defines rel); top-k ids must be identical except
+for tokens whose fp64 8th/9th logit gap is below 1e-5 (reported as ambiguous,
+the near-tie rule of qwen/test_npu_generate5.py:107-124).
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from npu_amd import ops, synth
+from npu_amd.gguf_types import GGMLQuantizationType as QT
+from oracle import moe as OM
+from oracle import quants as Q
+
+pytestmark = pytest.mark.gpu
+KAT = np.load(__import__("pathlib").Path(__file__).resolve().parent / "golden" / "iq_kat.npz")
+REL_TOL = 1e-3
+
+
+def _g(seed):
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+@pytest.mark.parametrize("qtype", [QT.IQ4_XS, QT.IQ3_XXS])
+def test_dequant_kat_exact(gpu, qtype):
+    blocks = KAT["iq4_blocks" if qtype == QT.IQ4_XS else "iq3_blocks"]
+    want = KAT["iq4_expected" if qtype == QT.IQ4_XS else "iq3_expected"].reshape(-1)
+    got = ops.dequant(qtype, torch.from_numpy(blocks.copy()).to(gpu)).cpu().numpy()
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("qtype", [QT.IQ4_XS, QT.IQ3_XXS])
+def test_dequant_random_exact(gpu, qtype):
+    blocks = synth.host_superblocks(_g(11), qtype, 4096)
+    got = ops.dequant(qtype, torch.from_numpy(blocks).to(gpu)).cpu().numpy()
+    want = Q.dequant(blocks, qtype)
+    assert np.array_equal(got, want)
+
+
+def _ref_matvec(w_raw, qtype, M, K, x):
+    W = torch.from_numpy(Q.dequant_matrix(w_raw, qtype, M, K))
+    return F.linear(x, W), (x.double() @ W.double().T)
+
+
+@pytest.mark.parametrize("qtype,M,K", [
+    (QT.IQ4_XS, 512, 2048),    # config 1
+    (QT.IQ3_XXS, 2048, 512),   # config 2
+    (QT.IQ3_XXS, 512, 2048),   # config 2, transposed shape
+    (QT.IQ4_XS, 2048, 512),    # model's down shape
+    (QT.IQ4_XS, 40, 256),
+    (QT.IQ3_XXS, 33, 4096),
+])
+@pytest.mark.parametrize("n_tok", [1, 3, 8, 13])
+def test_matvec(gpu, qtype, M, K, n_tok):
+    w = synth.host_quant_matrix(_g(M * 7 + K), qtype, M, K)
+    x = torch.from_numpy(_g(5).standard_normal((n_tok, K)).astype(np.float32))
+    y = ops.matvec(qtype, torch.from_numpy(w).to(gpu), M, K, x.to(gpu)).cpu()
+    ref32, ref64 = _ref_matvec(w, qtype, M, K, x)
+    assert y.shape == (n_tok, M)
+    assert OM.rel_err(y, ref32) <= REL_TOL
+    assert OM.rel_err(y, ref64) <= 1e-5
+
+
+def test_matvec_bf16(gpu):
+    M, K = 256, 2048
+    W = synth.host_bf16_normal(_g(1), (M, K), 0.02)
+    x = torch.from_numpy(_g(2).standard_normal((2, K)).astype(np.float32))
+    y = ops.matvec(QT.BF16, torch.from_numpy(W.view(np.int16)).to(gpu), M, K, x.to(gpu)).cpu()
+    ref = x.double() @ torch.from_numpy(synth.from_bf16(W)).double().T
+    assert OM.rel_err(y, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("q_gu,q_d", [(QT.IQ4_XS, QT.IQ3_XXS), (QT.IQ3_XXS, QT.IQ4_XS)])
+@pytest.mark.parametrize("n_tok", [1, 5])
+def test_swiglu_mlp(gpu, q_gu, q_d, n_tok):
+    D, FF = 2048, 512
+    wg = synth.host_quant_matrix(_g(21), q_gu, FF, D)
+    wu = synth.host_quant_matrix(_g(22), q_gu, FF, D)
+    wd = synth.host_quant_matrix(_g(23), q_d, D, FF)
+    x = torch.from_numpy(synth.host_input(3, n_tok, D))
+    dev = [torch.from_numpy(a).to(gpu) for a in (wg, wu, wd)]
+    y = ops.swiglu_mlp(q_gu, dev[0], dev[1], q_d, dev[2], D, FF, x.to(gpu)).cpu()
+    G = torch.from_numpy(Q.dequant_matrix(wg, q_gu, FF, D))
+    U = torch.from_numpy(Q.dequant_matrix(wu, q_gu, FF, D))
+    Dn = torch.from_numpy(Q.dequant_matrix(wd, q_d, D, FF))
+    ref = F.linear(F.silu(F.linear(x, G)) * F.linear(x, U), Dn)
+    assert OM.rel_err(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("T,E,k,bias", [(1, 256, 8, False), (8, 256, 8, False), (64, 256, 8, True),
+                                        (5, 16, 4, False), (3, 512, 8, True)])
+def test_router_topk(gpu, T, E, k, bias):
+    D = 2048
+    h = synth.host_moe_layer(31 + E, D=D, FF=256, E=E, k=k, shared=True, bias=bias, norm=True)
+    ol = OM.OracleLayer(h)
+    x = torch.from_numpy(synth.host_input(4, T, D, rmsnorm=False))
+    dev = lambda a: torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).to(gpu)
+    ids, wts, logits, shg = ops.router_topk(dev(h.router), x.to(gpu), k,
+                                            bias=dev(h.router_bias) if bias else None,
+                                            w_sh_gate=dev(h.sh_gate_inp), norm_w=dev(h.norm_w), eps=1e-6)
+    st = {}
+    xn = OM.rms_norm(x, ol.norm_w, 1e-6)
+    OM.moe_forward(xn.unsqueeze(0), ol, stages=st)
+    margin = OM.topk_margin(OM.router_logits64(x, ol), k)
+    clear = margin > 1e-5
+    assert bool(clear.any())
+    assert torch.equal(ids.cpu().long()[clear], st["topk_ids"][clear])
+    assert torch.allclose(logits.cpu(), st["ffn_moe_logits"], rtol=0, atol=2e-5)
+    assert torch.allclose(wts.cpu()[clear], st["ffn_moe_weights_norm"][clear], rtol=1e-5, atol=1e-6)
+    assert torch.allclose(shg.cpu(), st["shared_expert_gate_sigmoid"], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("T,k,E", [(512, 8, 256), (1, 8, 256), (37, 4, 16), (2000, 8, 512)])
+def test_dispatch_stable_sort(gpu, T, k, E):
+    g = _g(T + E)
+    ids = np.stack([g.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    counts, offsets, pairs = ops.moe_dispatch(torch.from_numpy(ids).to(gpu), E)
+    counts, offsets, pairs = counts.cpu().numpy(), offsets.cpu().numpy(), pairs.cpu().numpy()
+    flat = ids.reshape(-1)
+    assert np.array_equal(counts, np.bincount(flat, minlength=E))
+    assert np.array_equal(offsets, np.concatenate([[0], np.cumsum(counts)]))
+    assert np.array_equal(pairs, np.argsort(flat, kind="stable"))
