@@ -9,12 +9,13 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libnpu_amd.so"
-SOURCES = ["capi.hip", "matvec.hip", "moe_decode.hip", "dispatch.hip", "prefill.hip"]
+SOURCES = ["capi.hip", "matvec.hip", "router.hip", "moe_decode.hip", "dispatch.hip", "prefill.hip"]
 ARCH = os.environ.get("NPU_AMD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -37,18 +38,32 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> Path:
-    srcs = [str(CSRC / s) for s in SOURCES]
+    """Compile every source to an object in parallel, then link the library."""
+    objdir = HERE / "_build"
+    objdir.mkdir(exist_ok=True)
+    inc = ["-I", str(HERE.parent / "include")]
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+
+    def compile_one(src: str):
+        obj = objdir / (Path(src).stem + ".o")
+        cmd = [hipcc(), *compile_flags, *inc, "-c", str(CSRC / src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        return obj, subprocess.run(cmd, capture_output=True, text=True)
+
+    jobs = max(1, min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8"))))
+    with ThreadPoolExecutor(jobs) as ex:
+        results = list(ex.map(compile_one, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(HERE.parent / "include"), *srcs, "-o", str(tmp)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
-                    if "packed-fp32-ops" not in l and l.strip())
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{out}")
-    if verbose and out:
-        print(out)
+    link = [hipcc(), *HIPCC_FLAGS, *[str(o) for o, _ in results], "-o", str(tmp)]
+    results.append((None, subprocess.run(link, capture_output=True, text=True)))
+    for _, res in results:
+        out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
+                        if "packed-fp32-ops" not in l and l.strip())
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{out}")
+        if verbose and out:
+            print(out)
     os.replace(tmp, LIB)
     return LIB
 

@@ -68,6 +68,42 @@ __device__ __forceinline__ float gm_group_sum(float v) {
   return v;
 }
 
+// ---- DPP reductions (VALU-rate; no LDS round trips) ----------------------
+#define GM_DPP_F(v, ctrl) __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, false))
+#define GM_DPP_I(v, ctrl) __builtin_amdgcn_update_dpp(0, (v), (ctrl), 0xF, 0xF, false)
+#define GM_ROW_ROR8 0x128
+#define GM_ROW_ROR4 0x124
+#define GM_QPERM_2301 0x4E
+#define GM_QPERM_1032 0xB1
+
+// Sum over each 16-lane row; every lane of the row receives the row total.
+__device__ __forceinline__ float gm_row_sum16(float v) {
+  v += GM_DPP_F(v, GM_ROW_ROR8);
+  v += GM_DPP_F(v, GM_ROW_ROR4);
+  v += GM_DPP_F(v, GM_QPERM_2301);
+  v += GM_DPP_F(v, GM_QPERM_1032);
+  return v;
+}
+
+// Sum over all 64 lanes (wave-uniform result).
+__device__ __forceinline__ float gm_wave_sum64(float v) {
+  v = gm_row_sum16(v);
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Sum over aligned groups of L lanes, L in {16, 64} via DPP, else shuffles.
+template <int L>
+__device__ __forceinline__ float gm_lane_group_sum(float v) {
+  if constexpr (L == 16) return gm_row_sum16(v);
+  else if constexpr (L == 64) return gm_wave_sum64(v);
+  else return gm_group_sum<L>(v);
+}
+
 // Dynamic LDS above 64 KB needs an explicit opt-in per kernel (gfx950 has 160 KB).
 template <typename K>
 inline int gm_set_smem(K kern, size_t bytes) {

@@ -15,7 +15,7 @@ constexpr int kMaxE = 512;
 
 __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ ids, int P, int E,
                                                    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                                                   int32_t* __restrict__ sorted) {
+                                                   int32_t* __restrict__ sorted, int32_t* __restrict__ inv) {
   extern __shared__ int32_t cnt[];          // [kWaves][E] per-wave counts, then bases
   __shared__ int32_t tot_scan[kMaxE + 1];
   __shared__ int32_t wsum[kWaves];
@@ -81,6 +81,7 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ i
     __builtin_amdgcn_wave_barrier();
     if (e >= 0 && e < E) {
       sorted[pos] = p;
+      if (inv) inv[p] = pos;
       if (last) cnt[wave * E + e] = pos + 1;
     }
     __builtin_amdgcn_wave_barrier();
@@ -89,12 +90,17 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ i
 
 }  // namespace
 
-int gm_launch_dispatch(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
-                       int32_t* sorted_pairs, hipStream_t s) {
+int gm_launch_dispatch_inv(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
+                           int32_t* sorted_pairs, int32_t* inv, hipStream_t s) {
   if (E <= 0 || E > kMaxE) return gm_fail_arg("gm_moe_dispatch: E=%d out of range (1..%d)", E, kMaxE);
   const int P = T * k;
   const size_t smem = (size_t)kWaves * E * sizeof(int32_t);
-  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), smem, s, ids, P, E, counts, offsets, sorted_pairs);
+  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), smem, s, ids, P, E, counts, offsets, sorted_pairs, inv);
   GM_TRY(hipGetLastError());
   return GM_OK;
+}
+
+int gm_launch_dispatch(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
+                       int32_t* sorted_pairs, hipStream_t s) {
+  return gm_launch_dispatch_inv(ids, T, k, E, counts, offsets, sorted_pairs, nullptr, s);
 }

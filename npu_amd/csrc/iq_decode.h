@@ -89,14 +89,27 @@ struct RawIq3 {
   uint32_t w;      // scale/sign word
 };
 
+// Superblocks start at 98*sb, so every field offset is 0 or 2 mod 4 (rows and
+// expert slices are 4-byte multiples).  Fields are fetched with aligned dword
+// loads and re-aligned with v_alignbyte_b32; every dword read contains at
+// least one byte of this superblock, so no load crosses into an unmapped page.
 __device__ __forceinline__ RawIq3 gm_load_iq3(const uint8_t* __restrict__ row, int sub) {
-  const uint16_t* h = reinterpret_cast<const uint16_t*>(row + (sub >> 3) * GM_IQ3XXS_BYTES);
-  const int s = sub & 7;
+  const int sb = sub >> 3, s = sub & 7;
+  const uint8_t* base = row + sb * GM_IQ3XXS_BYTES;
+  const int odd = sb & 1;                       // base % 4 == 2 * odd
+  const uint32_t* dp = reinterpret_cast<const uint32_t*>(base - 2 * odd);
   RawIq3 r;
-  r.d = h[0];
-  r.q0 = (uint32_t)h[1 + 4 * s] | ((uint32_t)h[2 + 4 * s] << 16);
-  r.q1 = (uint32_t)h[3 + 4 * s] | ((uint32_t)h[4 + 4 * s] << 16);
-  r.w = (uint32_t)h[33 + 2 * s] | ((uint32_t)h[34 + 2 * s] << 16);
+  r.d = odd ? (dp[0] >> 16) : (dp[0] & 0xffffu);
+  // qs at base + 2 + 8s: offset % 4 == 2 when sb is even, 0 when odd
+  const int rq = odd ? 0 : 2;
+  const uint32_t* qp = reinterpret_cast<const uint32_t*>(base + 2 + 8 * s - rq);
+  const uint32_t q0 = qp[0], q1 = qp[1], q2 = qp[rq ? 2 : 1];
+  r.q0 = __builtin_amdgcn_alignbyte(q1, q0, rq);
+  r.q1 = __builtin_amdgcn_alignbyte(q2, q1, rq);
+  // word at base + 66 + 4s: same parity rule
+  const uint32_t* wp = reinterpret_cast<const uint32_t*>(base + 66 + 4 * s - rq);
+  const uint32_t w0 = wp[0], w1 = wp[rq ? 1 : 0];
+  r.w = __builtin_amdgcn_alignbyte(w1, w0, rq);
   return r;
 }
 

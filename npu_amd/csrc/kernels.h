@@ -45,3 +45,5 @@ int gm_moe_prefill(const gm_moe_layer* L, const float* x, float* y, int T, int f
                    const GmMoeWs& lay, hipStream_t s);
 int gm_launch_dispatch(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
                        int32_t* sorted_pairs, hipStream_t s);
+int gm_launch_dispatch_inv(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
+                           int32_t* sorted_pairs, int32_t* inv, hipStream_t s);
