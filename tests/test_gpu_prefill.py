@@ -1,0 +1,88 @@
+"""GPU parity of the MoE block prefill path (T > 8: grouped bf16-MFMA GEMMs).
+
+Oracle: oracle.moe.block_forward, the restatement of qwen/forward.py:563-665
+(the reference runs prefill through the same CPU loop).  Bar: top-k ids
+identical for every token whose k-th/(k+1)-th logit margin is clear of fp32
+rounding, rel <= 1e-2 over those tokens (activations and h are rounded to bf16
+before the MFMA products), bit-identical repeats (fixed-order combine).
+"""
+import numpy as np
+import pytest
+import torch
+
+from npu_amd import synth
+from npu_amd.gguf_types import GGMLQuantizationType as QT
+from npu_amd.moe import GpuMoeBlock
+from oracle import moe as OM
+
+pytestmark = pytest.mark.gpu
+REL_TOL = 1e-2
+
+
+def _check(gpu, h, T, residual=False, seed=5, rmsnorm_input=True):
+    print(f"prefill case D={h.D} FF={h.FF} E={h.E} k={h.k} T={T} q=({h.q_gate},{h.q_down}) "
+          f"shared={h.gate_sh is not None} residual={residual}", flush=True)
+    ol = OM.OracleLayer(h)
+    x = torch.from_numpy(synth.host_input(seed, T, h.D, rmsnorm=rmsnorm_input))
+    blk = GpuMoeBlock.from_host(h, device=gpu)
+    y = blk(x.to(gpu), residual=residual)
+    y2 = blk(x.to(gpu), residual=residual)
+    st_gpu = {k: v.clone().cpu() for k, v in blk.stages(T).items()}
+    y, y2 = y.cpu(), y2.cpu()
+    st = {}
+    ref = OM.block_forward(x, ol, residual=residual, stages=st)
+    margin = OM.topk_margin(OM.router_logits64(x, ol), h.k)
+    clear = margin > 1e-5
+    assert int(clear.sum()) >= T - 2, "too many near-ties for a meaningful check"
+    assert torch.equal(st_gpu["topk_ids"].long()[clear], st["topk_ids"][clear]), "top-k ids differ"
+    assert torch.allclose(st_gpu["ffn_moe_weights_norm"][clear], st["ffn_moe_weights_norm"][clear], rtol=1e-5,
+                          atol=1e-7)
+    assert torch.isfinite(y).all()
+    rel = float((y[clear] - ref[clear]).abs().max() / ref[clear].abs().max())
+    assert rel <= REL_TOL, rel
+    assert torch.equal(y, y2), "repeat calls must be bit-identical"
+    return rel, st
+
+
+def test_config4_prefill(gpu):
+    """T=512, D=2048, FF=512, E=256, top-8, per-expert router bias ~ N(0,1)."""
+    h = synth.host_moe_layer(40, q_gate=QT.IQ4_XS, q_down=QT.IQ3_XXS, bias=True)
+    rel, st = _check(gpu, h, 512, seed=7, rmsnorm_input=False)
+    counts = torch.bincount(st["topk_ids"].flatten(), minlength=h.E)
+    assert int(counts.max()) > 64, "the skew must give experts more than one 64-token segment"
+
+
+@pytest.mark.parametrize("q_gate,q_down", [(QT.IQ4_XS, QT.IQ3_XXS), (QT.IQ3_XXS, QT.IQ4_XS),
+                                           (QT.IQ4_XS, QT.IQ4_XS), (QT.IQ3_XXS, QT.IQ3_XXS)])
+@pytest.mark.parametrize("T", [9, 64, 130])
+@pytest.mark.parametrize("shared", [True, False])
+def test_small_prefill(gpu, q_gate, q_down, T, shared):
+    h = synth.host_moe_layer(60 + T, D=512, FF=256, E=16, k=4, q_gate=q_gate, q_down=q_down, shared=shared,
+                             bias=True)
+    _check(gpu, h, T, seed=T)
+
+
+@pytest.mark.parametrize("T", [16, 200])
+def test_prefill_norm_and_residual(gpu, T):
+    h = synth.host_moe_layer(70 + T, D=1024, FF=512, E=64, k=8, norm=True, bias=True)
+    _check(gpu, h, T, residual=True, rmsnorm_input=False)
+
+
+def test_prefill_model_assignment(gpu):
+    """The reference model's assignment (IQ3_XXS gate/up, IQ4_XS down), E=128, T=96."""
+    h = synth.host_moe_layer(80, D=2048, FF=512, E=128, k=8, q_gate=QT.IQ3_XXS, q_down=QT.IQ4_XS)
+    _check(gpu, h, 96, seed=3)
+
+
+def test_prefill_stage_outputs(gpu):
+    h = synth.host_moe_layer(81, D=512, FF=256, E=32, k=4, bias=True)
+    T = 40
+    x = torch.from_numpy(synth.host_input(4, T, h.D))
+    blk = GpuMoeBlock.from_host(h, device=gpu)
+    blk(x.to(gpu))
+    got = {k: v.cpu() for k, v in blk.stages(T).items()}
+    st = {}
+    OM.block_forward(x, OM.OracleLayer(h), stages=st)
+    assert torch.allclose(got["ffn_moe_logits"], st["ffn_moe_logits"], rtol=0, atol=2e-5)
+    assert torch.equal(got["topk_ids"].long(), st["topk_ids"])
+    assert torch.allclose(got["shared_expert_gate_sigmoid"], st["shared_expert_gate_sigmoid"], rtol=1e-5)
