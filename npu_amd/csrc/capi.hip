@@ -44,9 +44,10 @@ GmMoeWs gm_moe_ws_layout(const gm_moe_layer* L, int T) {
   w.shg = o; o = align256(o + Tz * 4);
   w.ids = o; o = align256(o + Tz * k * 4);
   w.wts = o; o = align256(o + Tz * k * 4);
-  w.grp = o; o = align256(o + ((size_t)GM_GRP_WORDS + 2 * E + 1 + Tz * k) * 4);
-  w.h = o; o = align256(o + Tz * k * (size_t)L->FF * 4);
+  w.grp = o; o = align256(o + ((size_t)GM_GRP_WORDS + 8 + 2 * E + 1 + Tz * k) * 4);
+  w.h = o; o = o + Tz * k * (size_t)L->FF * 4;     // FF % 256 == 0: h_sh starts 256-byte aligned
   w.hsh = o; o = align256(o + Tz * (size_t)(L->FF_sh > 0 ? L->FF_sh : 0) * 4);
+  w.yp = o; o = align256(o + (T <= GM_DECODE_MAX_T ? (Tz * k + Tz) * (size_t)L->D * 4 : 0));
   w.counters = o; o = align256(o + 256);
   w.pre = o; o = align256(o + (T > GM_DECODE_MAX_T ? gm_prefill_scratch_bytes(L, T) : 0));
   w.total = o;
@@ -76,6 +77,10 @@ static int check_layer(const gm_moe_layer* L) {
                          L->q_up_sh, L->q_down_sh);
   }
   if (L->norm_w && !(L->norm_eps >= 0.f)) return gm_fail_arg("gm_moe_forward: norm_eps must be >= 0");
+  const void* wptrs[] = {L->gate_exps, L->up_exps, L->down_exps, L->gate_sh, L->up_sh, L->down_sh, L->router};
+  for (const void* p : wptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16)
+      return gm_fail_arg("gm_moe_forward: weight pointers must be 16-byte aligned");
   return GM_OK;
 }
 

@@ -11,6 +11,12 @@
 #define GM_IQ3XXS_BYTES 98   // GGUF block_iq3_xxs
 #define GM_WAVE 64
 
+// Native 4 x f32 vector.  Staging copies use it instead of HIP's float4
+// struct: a struct load + store pair is turned into a memcpy by the optimiser,
+// which then issues every load right before its store.
+typedef float gm_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gm_u32x4 __attribute__((ext_vector_type(4)));
+
 // Host-side launch-check helper: every entry point returns an int status.
 #define GM_TRY(expr)                                   \
   do {                                                 \

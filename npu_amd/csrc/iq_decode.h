@@ -89,14 +89,14 @@ struct RawIq3 {
   uint32_t w;      // scale/sign word
 };
 
-// Superblocks start at 98*sb, so every field offset is 0 or 2 mod 4 (rows and
-// expert slices are 4-byte multiples).  Fields are fetched with aligned dword
-// loads and re-aligned with v_alignbyte_b32; every dword read contains at
+// Superblocks are 2-byte aligned (98 B each), so every field offset is 0 or
+// 2 mod 4.  Fields are fetched with aligned dword loads (global memory or
+// LDS) and re-aligned with v_alignbyte_b32; every dword read contains at
 // least one byte of this superblock, so no load crosses into an unmapped page.
 __device__ __forceinline__ RawIq3 gm_load_iq3(const uint8_t* __restrict__ row, int sub) {
   const int sb = sub >> 3, s = sub & 7;
   const uint8_t* base = row + sb * GM_IQ3XXS_BYTES;
-  const int odd = sb & 1;                       // base % 4 == 2 * odd
+  const int odd = (int)((reinterpret_cast<uintptr_t>(base) >> 1) & 1);   // base % 4 == 2 * odd
   const uint32_t* dp = reinterpret_cast<const uint32_t*>(base - 2 * odd);
   RawIq3 r;
   r.d = odd ? (dp[0] >> 16) : (dp[0] & 0xffffu);
@@ -185,10 +185,69 @@ __device__ __forceinline__ float gm_decode_sub(const typename RawSub<QT>::T& r, 
   else return gm_decode_bf16(r, wv);
 }
 
+// The IQ3_XXS grid (256 x 4 magnitudes) in global constant memory.
+static __device__ const uint32_t gm_iq3xxs_grid[256] = {GM_IQ3XXS_GRID_INIT};
+
 // Stage the IQ3_XXS grid in LDS (1 KB); every thread of the block must call.
 __device__ __forceinline__ void gm_stage_grid(uint32_t* grid_lds) {
-  constexpr uint32_t kGrid[256] = {GM_IQ3XXS_GRID_INIT};
-  for (int i = threadIdx.x; i < 256; i += blockDim.x) grid_lds[i] = kGrid[i];
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) grid_lds[i] = gm_iq3xxs_grid[i];
+}
+
+// IQ3_XXS decode table in LDS (4 KB): the grid as float magnitudes,
+// gridf[i] = the 4 magnitudes of grid entry i.  Signs are applied with one
+// bit operation per weight (the magnitudes are positive).
+struct Iq3Tab {
+  gm_f32x4 gridf[256];
+};
+
+// Threads 0..255 each load one grid word (step 1) and write one gridf entry
+// (step 2); the block size must be >= 256.
+__device__ __forceinline__ uint32_t gm_iq3_tab_load() {
+  return threadIdx.x < 256 ? gm_iq3xxs_grid[threadIdx.x] : 0u;
+}
+
+__device__ __forceinline__ void gm_iq3_tab_store(uint32_t g, Iq3Tab* __restrict__ tab) {
+  if (threadIdx.x < 256) {
+    gm_f32x4 m;
+    m.x = (float)(g & 0xffu); m.y = (float)((g >> 8) & 0xffu);
+    m.z = (float)((g >> 16) & 0xffu); m.w = (float)(g >> 24);
+    tab->gridf[threadIdx.x] = m;
+  }
+}
+
+// magnitude m >= 0 with the sign of bit i of sb
+__device__ __forceinline__ float gm_signed(float m, uint32_t sb, int i) {
+  return __int_as_float(__float_as_int(m) | (int)((sb << (31 - i)) & 0x80000000u));
+}
+
+__device__ __forceinline__ float gm_decode_iq3_tab(const RawIq3& r, const Iq3Tab* __restrict__ tab,
+                                                   float (&wv)[32]) {
+  const float d = gm_h2f(r.d);
+  const float db = d * (0.5f + (float)(r.w >> 28)) * 0.5f;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint32_t qw = g < 2 ? r.q0 : r.q1;
+    const gm_f32x4 ma = tab->gridf[(qw >> (16 * (g & 1))) & 0xffu];
+    const gm_f32x4 mb = tab->gridf[(qw >> (16 * (g & 1) + 8)) & 0xffu];
+    const uint32_t sb = gm_ksigns((r.w >> (7 * g)) & 127u);
+    wv[8 * g + 0] = gm_signed(ma.x, sb, 0);
+    wv[8 * g + 1] = gm_signed(ma.y, sb, 1);
+    wv[8 * g + 2] = gm_signed(ma.z, sb, 2);
+    wv[8 * g + 3] = gm_signed(ma.w, sb, 3);
+    wv[8 * g + 4] = gm_signed(mb.x, sb, 4);
+    wv[8 * g + 5] = gm_signed(mb.y, sb, 5);
+    wv[8 * g + 6] = gm_signed(mb.z, sb, 6);
+    wv[8 * g + 7] = gm_signed(mb.w, sb, 7);
+  }
+  return db;
+}
+
+// Decode with the LDS tables (IQ3_XXS); other formats need none.
+template <int QT>
+__device__ __forceinline__ float gm_decode_sub_t(const typename RawSub<QT>::T& r, int sub,
+                                                 const Iq3Tab* __restrict__ tab, float (&wv)[32]) {
+  if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_decode_iq3_tab(r, tab, wv);
+  else return gm_decode_sub<QT>(r, sub, nullptr, wv);
 }
 
 // 32-wide dot of decoded weights with x (LDS or registers).

@@ -16,7 +16,8 @@ struct GmMoeWs {
   size_t wts;      // f32 [T][k]
   size_t grp;      // i32 grouping table (decode) / dispatch tables (prefill)
   size_t h;        // f32 [T][k][FF]  routed SwiGLU activations (decode)
-  size_t hsh;      // f32 [T][FF_sh]  shared SwiGLU activations
+  size_t hsh;      // f32 [T][FF_sh]  shared SwiGLU activations (directly after h)
+  size_t yp;       // f32 [T * k + T][D]  per-pair / shared partial outputs (decode, T > 1)
   size_t counters; // u32 [64]   self-resetting counters
   size_t pre;      // prefill scratch (see prefill.hip)
   size_t total;
@@ -30,6 +31,7 @@ size_t gm_prefill_scratch_bytes(const gm_moe_layer* L, int T);
 //   [1 .. 64]      expert id of unique slot u (ascending)
 //   [65 .. 128]    member count of slot u
 //   [129 .. 640]   members: slot u, member m -> (token * k + topk_slot), tokens ascending
+//   [641 .. 648]   T = 1 only: routing weight of slot u (float bits)
 #define GM_GRP_MAXU 64
 #define GM_GRP_MAXM 8
 #define GM_GRP_WORDS (1 + 2 * GM_GRP_MAXU + GM_GRP_MAXU * GM_GRP_MAXM)

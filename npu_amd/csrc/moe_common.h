@@ -98,85 +98,112 @@ __device__ __forceinline__ void stage_rows_il(const float* __restrict__ src, int
 // E, renormalised top-k probabilities (qwen/forward.py:609-611).  Each lane
 // sorts its MAXV values once; every round takes the wave-wide best lane head
 // (DPP inside 16-lane rows, readlane across rows) and pops it.
-template <int CTRL>
-__device__ __forceinline__ void dpp_argmax_step(float& bv, int& bi) {
-  const float ov = GM_DPP_F(bv, CTRL);
-  const int oi = GM_DPP_I(bi, CTRL);
-  if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-}
-
-__device__ __forceinline__ bool better(float av, int ai, float bv, int bi) { return av > bv || (av == bv && ai < bi); }
-
+// Lane values of one wave's top-k input: logits lane + 64 i (clamped loads,
+// so every lane issues the same MAXV loads; out-of-range entries are masked
+// in topk_finish).
 template <int MAXV>
-__device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int E, int k, int32_t* __restrict__ ids,
-                                          float* __restrict__ wts) {
+__device__ __forceinline__ void topk_load(const float* __restrict__ lg, int E, float (&v)[MAXV], int (&ix)[MAXV]) {
   const int lane = threadIdx.x & 63;
-  float v[MAXV];
-  int ix[MAXV];
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     ix[i] = lane + 64 * i;
-    v[i] = ix[i] < E ? lg[ix[i]] : -INFINITY;
+    v[i] = lg[ix[i] < E ? ix[i] : E - 1];
   }
+}
+
+// Float <-> int32 key with the same order (an involution): the top-k runs on
+// integer keys so that every max/min step is one fused DPP instruction.
+__device__ __forceinline__ int fkey(float f) {
+  const int b = __float_as_int(f);
+  return b >= 0 ? b : b ^ 0x7fffffff;
+}
+__device__ __forceinline__ float fkey_inv(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7fffffff); }
+
+__device__ __forceinline__ int wave_max_int_uniform(int v) {
+  v = max(v, GM_DPP_I(v, GM_ROW_ROR8));
+  v = max(v, GM_DPP_I(v, GM_ROW_ROR4));
+  v = max(v, GM_DPP_I(v, GM_QPERM_2301));
+  v = max(v, GM_DPP_I(v, GM_QPERM_1032));
+  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+__device__ __forceinline__ int wave_min_int_uniform(int v) {
+  v = min(v, GM_DPP_I(v, GM_ROW_ROR8));
+  v = min(v, GM_DPP_I(v, GM_ROW_ROR4));
+  v = min(v, GM_DPP_I(v, GM_QPERM_2301));
+  v = min(v, GM_DPP_I(v, GM_QPERM_1032));
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// Every round takes the wave-wide largest lane head (a max reduction, then a
+// ballot of the lanes holding it; an exact tie goes to the lowest expert id)
+// and pops it.  The softmax weights of the k winners are computed afterwards,
+// one per lane, in parallel.
+// Lane r < k ends with pick r: its expert id (out_id) and renormalised weight
+// (out_w); other lanes get INT_MAX / 0.
+template <int MAXV>
+__device__ __forceinline__ void topk_finish(float (&v)[MAXV], int (&ix)[MAXV], int E, int k, int& out_id,
+                                            float& out_w) {
+  const int lane = threadIdx.x & 63;
+  int key[MAXV];
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) key[i] = ix[i] < E ? fkey(v[i]) : INT_MIN;
   // per-lane sort, descending (ties: lower index first)
 #pragma unroll
   for (int a = 0; a < MAXV; ++a)
 #pragma unroll
     for (int b = MAXV - 1; b > a; --b)
-      if (better(v[b], ix[b], v[b - 1], ix[b - 1])) {
-        const float tv = v[b]; v[b] = v[b - 1]; v[b - 1] = tv;
+      if (key[b] > key[b - 1] || (key[b] == key[b - 1] && ix[b] < ix[b - 1])) {
+        const int tk = key[b]; key[b] = key[b - 1]; key[b - 1] = tk;
         const int ti = ix[b]; ix[b] = ix[b - 1]; ix[b - 1] = ti;
       }
-  // softmax normaliser over all E (max = best head)
-  float m = v[0];
-  m = fmaxf(m, GM_DPP_F(m, GM_ROW_ROR8));
-  m = fmaxf(m, GM_DPP_F(m, GM_ROW_ROR4));
-  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_2301));
-  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_1032));
-  {
-    const int b = __builtin_bit_cast(int, m);
-    m = fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
-                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
-              fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
-                    __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
-  }
+  // softmax normaliser over all E
+  const float m = fkey_inv(wave_max_int_uniform(key[0]));
   float z = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXV; ++i)
-    if (ix[i] < E) z += expf(v[i] - m);
+    if (key[i] != INT_MIN) z += expf(fkey_inv(key[i]) - m);
   z = gm_wave_sum64(z);
-  float psum = 0.f, myp = 0.f;
-  int myid = 0;
+  int mykey = INT_MIN, myid = 0;
   for (int r = 0; r < k; ++r) {
-    float bv = v[0];
-    int bi = ix[0];
-    dpp_argmax_step<GM_ROW_ROR8>(bv, bi);
-    dpp_argmax_step<GM_ROW_ROR4>(bv, bi);
-    dpp_argmax_step<GM_QPERM_2301>(bv, bi);
-    dpp_argmax_step<GM_QPERM_1032>(bv, bi);
-    const int bb = __builtin_bit_cast(int, bv);
-    float wv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bb, 0));
-    int wi = __builtin_amdgcn_readlane(bi, 0);
-#pragma unroll
-    for (int row = 16; row < 64; row += 16) {
-      const float rv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(bb, row));
-      const int ri = __builtin_amdgcn_readlane(bi, row);
-      if (better(rv, ri, wv, wi)) { wv = rv; wi = ri; }
+    const int hm = wave_max_int_uniform(key[0]);
+    const uint64_t bal = __ballot(key[0] == hm);
+    int wl;
+    if (__popcll(bal) == 1) {
+      wl = __ffsll((unsigned long long)bal) - 1;
+    } else {                        // exact tie: lowest expert id among the tied heads
+      wl = wave_min_int_uniform(key[0] == hm ? ix[0] : 0x7fffffff) & 63;
     }
-    if ((wi & 63) == lane) {         // pop the winner's head
+    const int wi = __builtin_amdgcn_readlane(ix[0], wl);
+    if (lane == r) { mykey = hm; myid = wi; }
+    if (lane == wl) {               // pop the winner's head
 #pragma unroll
-      for (int i = 0; i + 1 < MAXV; ++i) { v[i] = v[i + 1]; ix[i] = ix[i + 1]; }
-      v[MAXV - 1] = -INFINITY;
+      for (int i = 0; i + 1 < MAXV; ++i) { key[i] = key[i + 1]; ix[i] = ix[i + 1]; }
+      key[MAXV - 1] = INT_MIN;
       ix[MAXV - 1] = 0x7fffffff;
     }
-    const float p = expf(wv - m) / z;
-    psum += p;
-    if (lane == r) { myp = p; myid = wi; }
   }
-  const float den = fmaxf(psum, 1e-20f);
+  const float p = lane < k ? expf(fkey_inv(mykey) - m) / z : 0.f;
+  const float den = fmaxf(gm_wave_sum64(p), 1e-20f);
+  out_id = lane < k ? myid : 0x7fffffff;
+  out_w = p / den;
+}
+
+template <int MAXV>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int E, int k, int32_t* __restrict__ ids,
+                                          float* __restrict__ wts) {
+  float v[MAXV];
+  int ix[MAXV];
+  topk_load<MAXV>(lg, E, v, ix);
+  int id;
+  float w;
+  topk_finish<MAXV>(v, ix, E, k, id, w);
+  const int lane = threadIdx.x & 63;
   if (lane < k) {
-    ids[lane] = myid;
-    wts[lane] = myp / den;
+    ids[lane] = id;
+    wts[lane] = w;
   }
 }
 
@@ -221,6 +248,197 @@ __device__ __forceinline__ void block_group(const int32_t* __restrict__ ids, int
     }
   }
   __syncthreads();
+}
+
+// Keeps the compiler's scheduler from moving instructions across this point:
+// placed after a kernel has issued all of its loads, so that none is sunk
+// next to its first use (where, behind the weight loads in the in-order
+// vmcnt queue, each would wait for everything issued before it).
+__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// --------------------------------------------------------- row streaming
+// The decode kernels issue every weight load a lane needs before they wait on
+// anything: SPL sub-blocks per lane and row, at sub = lir + LR * i.  Indices
+// past the row are clamped to its last sub-block (a harmless duplicate load
+// whose result is skipped), so the loads are unconditional and straight-line
+// and the compiler can count them instead of draining the queue before each.
+template <int QT, int SPL>
+struct RowFetch {
+  typename RawSub<QT>::T r[SPL];
+};
+
+template <int QT, int LR, int SPL>
+__device__ __forceinline__ void fetch_subs(RowFetch<QT, SPL>& f, const uint8_t* __restrict__ row, int lir, int nsub) {
+#pragma unroll
+  for (int i = 0; i < SPL; ++i) {
+    const int sub = lir + LR * i;
+    f.r[i] = gm_load_sub<QT>(row, sub < nsub ? sub : nsub - 1);
+  }
+}
+
+// acc[m] += W_row . act[idx[m]] over the fetched sub-blocks, m < nt; act rows
+// are interleaved LDS rows of K floats.
+template <int QT, int LR, int SPL, int NT>
+__device__ __forceinline__ void dot_subs(const RowFetch<QT, SPL>& f, int lir, int nsub, const float* __restrict__ act,
+                                         int K, const int (&idx)[NT], int nt, const Iq3Tab* __restrict__ tab,
+                                         float (&acc)[NT]) {
+#pragma unroll
+  for (int i = 0; i < SPL; ++i) {
+    const int sub = lir + LR * i;
+    if (sub < nsub) {
+      float wv[32];
+      const float sc = gm_decode_sub_t<QT>(f.r[i], sub, tab, wv);
+#pragma unroll
+      for (int m = 0; m < NT; ++m)
+        if (m < nt) acc[m] = fmaf(sc, gm_dot32_il(wv, act + idx[m] * K, sub, nsub), acc[m]);
+    }
+  }
+}
+
+// Sum over the LR lanes of a row (LR = 16, 32 or 64), result in every lane.
+template <int LR>
+__device__ __forceinline__ float row_sum(float v) {
+  if constexpr (LR == 64) return gm_wave_sum64(v);
+  v = gm_row_sum16(v);
+  if constexpr (LR == 32) v += __shfl_xor(v, 16, 64);
+  return v;
+}
+
+// ------------------------------------------------------ activation rows
+// Up to NT activation rows of D floats (plus the RMSNorm weight) held in
+// registers: XPT float4 per thread per row, thread-strided (blockDim 256).
+template <int NT, int XPT>
+struct XRegs {
+  gm_f32x4 v[NT][XPT];
+  gm_f32x4 w[XPT];
+};
+
+// Rows tok[m], m < nt (uniform), of x [.][D]; loads of rows past nt are skipped.
+template <int NT, int XPT>
+__device__ __forceinline__ void load_x(XRegs<NT, XPT>& r, const float* __restrict__ x, const int (&tok)[NT], int nt,
+                                       int D, const float* __restrict__ norm_w) {
+  const int nq = D >> 2;
+  const gm_f32x4* x4 = reinterpret_cast<const gm_f32x4*>(x);
+#pragma unroll
+  for (int m = 0; m < NT; ++m) {
+    if (m < nt) {
+#pragma unroll
+      for (int i = 0; i < XPT; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        r.v[m][i] = x4[(int64_t)tok[m] * nq + (c < nq ? c : nq - 1)];
+      }
+    }
+  }
+  if (norm_w != nullptr) {
+    const gm_f32x4* w4 = reinterpret_cast<const gm_f32x4*>(norm_w);
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      r.w[i] = w4[c < nq ? c : nq - 1];
+    }
+  }
+}
+
+// Write the rows to interleaved LDS rows xs[m][D], applying
+// xn = (x * rms) * w with rms = 1/sqrt(mean(x^2) + eps) when norm_w != NULL
+// (qwen/forward.py:58-61).  One barrier for all rows.  red: 4 * NT floats.
+// xs holds NT * D + 4 floats: lanes past the row store into the last float4,
+// so the stores are unconditional and the loads feeding them are not sunk
+// into branches (where each would end in a full wait).  All 256 threads
+// call; ends with a barrier.
+template <int NT, int XPT>
+__device__ __forceinline__ void stage_x_regs(XRegs<NT, XPT>& r, int nt, int D, const float* __restrict__ norm_w,
+                                             float eps, float* __restrict__ xs, float* __restrict__ red) {
+  const int nq = D >> 2, nsub = D >> 5;
+  gm_f32x4* xs4 = reinterpret_cast<gm_f32x4*>(xs);
+  if (norm_w != nullptr) {
+    float ss[NT];
+#pragma unroll
+    for (int m = 0; m < NT; ++m) {
+      ss[m] = 0.f;
+      if (m < nt) {
+#pragma unroll
+        for (int i = 0; i < XPT; ++i) {
+          const int c = threadIdx.x + 256 * i;
+          const gm_f32x4 v = r.v[m][i];
+          if (c < nq) ss[m] = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss[m]))));
+        }
+      }
+      ss[m] = gm_wave_sum64(ss[m]);
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+      for (int m = 0; m < NT; ++m) red[wave * NT + m] = ss[m];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < NT; ++m) {
+      if (m < nt) {
+        const float tot = (red[m] + red[NT + m]) + (red[2 * NT + m] + red[3 * NT + m]);
+        const float rms = 1.0f / sqrtf(tot / (float)D + eps);
+#pragma unroll
+        for (int i = 0; i < XPT; ++i) {
+          const int c = threadIdx.x + 256 * i;
+          gm_f32x4 v = r.v[m][i];
+          const gm_f32x4 w = r.w[i];
+          v.x = (v.x * rms) * w.x; v.y = (v.y * rms) * w.y; v.z = (v.z * rms) * w.z; v.w = (v.w * rms) * w.w;
+          xs4[c < nq ? m * nq + il_index4(c & 7, c >> 3, nsub) : NT * nq] = v;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < NT; ++m) {
+      if (m < nt) {
+#pragma unroll
+        for (int i = 0; i < XPT; ++i) {
+          const int c = threadIdx.x + 256 * i;
+          xs4[c < nq ? m * nq + il_index4(c & 7, c >> 3, nsub) : NT * nq] = r.v[m][i];
+        }
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// One wave stages x [D] (XW float4 per lane, RMSNorm'd when norm_w != NULL)
+// into the interleaved LDS row xs [D + 4]; no block barrier involved.
+template <int XW>
+__device__ __forceinline__ void stage_x_wave(const float* __restrict__ x, int D, const float* __restrict__ norm_w,
+                                             float eps, float* __restrict__ xs) {
+  const int lane = threadIdx.x & 63, nq = D >> 2, nsub = D >> 5;
+  const gm_f32x4* x4 = reinterpret_cast<const gm_f32x4*>(x);
+  const gm_f32x4* w4 = reinterpret_cast<const gm_f32x4*>(norm_w);
+  gm_f32x4 v[XW], w[XW];
+#pragma unroll
+  for (int i = 0; i < XW; ++i) {
+    const int c = lane + 64 * i;
+    v[i] = x4[c < nq ? c : nq - 1];
+  }
+  if (norm_w != nullptr) {
+#pragma unroll
+    for (int i = 0; i < XW; ++i) {
+      const int c = lane + 64 * i;
+      w[i] = w4[c < nq ? c : nq - 1];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < XW; ++i)
+      if (lane + 64 * i < nq) ss = fmaf(v[i].x, v[i].x, fmaf(v[i].y, v[i].y, fmaf(v[i].z, v[i].z, fmaf(v[i].w, v[i].w, ss))));
+    const float rms = 1.0f / sqrtf(gm_wave_sum64(ss) / (float)D + eps);
+#pragma unroll
+    for (int i = 0; i < XW; ++i) {
+      v[i].x = (v[i].x * rms) * w[i].x; v[i].y = (v[i].y * rms) * w[i].y;
+      v[i].z = (v[i].z * rms) * w[i].z; v[i].w = (v[i].w * rms) * w[i].w;
+    }
+  }
+  gm_f32x4* xs4 = reinterpret_cast<gm_f32x4*>(xs);
+#pragma unroll
+  for (int i = 0; i < XW; ++i) {
+    const int c = lane + 64 * i;
+    xs4[c < nq ? il_index4(c & 7, c >> 3, nsub) : nq] = v[i];
+  }
 }
 
 }  // namespace gm_moe

@@ -1,0 +1,28 @@
+// Decode-path (T <= 8) launchers shared by moe_decode*.hip.
+#pragma once
+#include "kernels.h"
+
+// Device pointers into the MoE workspace for one call.
+struct GmDecArgs {
+  float* logits;    // [T][E]
+  float* shg;       // [T]
+  int32_t* ids;     // [T][k]
+  float* wts;       // [T][k]
+  int32_t* grp;     // grouping table, see kernels.h; words GM_GRP_WORDS.. hold the T = 1
+                    // routing weights in ascending-expert order
+  float* h;         // [T * k][FF], directly followed by hsh
+  float* hsh;       // [T][FF]
+  float* yp;        // [T * k + T][D] per-pair / shared partial outputs (general path)
+};
+
+// Weight-row chunk sizes: D and FF in units of 1024 and 512 elements.
+inline int gm_dec_dc(int D) { return D <= 1024 ? 1 : D <= 2048 ? 2 : 4; }
+inline int gm_dec_fc(int FF) { return FF <= 512 ? 1 : FF <= 1024 ? 2 : 4; }
+
+// Stage 2: top-k + grouping + routed gate/up.  fast1: the T = 1 kernel that
+// recomputes the top-k in every block; otherwise one routing block, then the
+// grouped gate/up kernel.
+int gm_dec_gateup(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s);
+// Stage 3: down projections and the weighted combine (+ shared expert, + x).
+int gm_dec_down(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
+                hipStream_t s);

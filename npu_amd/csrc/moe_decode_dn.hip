@@ -1,0 +1,374 @@
+// MoE decode, stage 3: down projections and the weighted combine
+// (qwen/forward.py:659-665: routed experts accumulated in ascending expert id,
+// then + sigmoid(gate) * shared expert; the residual add of :880-884 fused).
+//
+// T = 1 (k_dec_down1): block = 8 output rows; every lane loads its sub-block
+// of all k routed down rows and the shared down row up front, the k + 1 SwiGLU
+// rows are staged in LDS meanwhile, and the rows are reduced in a fixed order.
+//
+// T > 1: k_dec_down8 (unique expert or shared expert, 64-row tile) writes one
+// partial output row per member token, k_dec_combine sums each token's
+// partials in ascending expert order.  Fixed order, no atomics.
+#include "moe_common.h"
+#include "moe_decode.h"
+
+using namespace gm_moe;
+
+namespace {
+
+// Sum over aligned groups of n lanes (n = 8, 16 or 32), result in every lane.
+__device__ __forceinline__ float group_sum(float v, int n) {
+  if (n == 8) {
+    v += GM_DPP_F(v, 0x141);               // row_half_mirror: lane i <-> 7 - i
+    v += GM_DPP_F(v, GM_QPERM_2301);
+    v += GM_DPP_F(v, GM_QPERM_1032);
+    return v;
+  }
+  v = gm_row_sum16(v);
+  if (n == 32) v += __shfl_xor(v, 16, 64);
+  return v;
+}
+
+// Block = 8 output rows, 9 waves: wave w reduces routed down matrix w (w < k,
+// in ascending expert order) or, for w == k, the shared one.  Lane (rg, sub)
+// takes sub-block sub of rows rg R .. rg R + R - 1 (R = nsub / 8), so every
+// lane decodes 32 R weights and reads its 32 SwiGLU values once for them.
+// The 8-row slices of the k + 1 down matrices are contiguous, 16-byte aligned
+// runs of raw superblocks: they are copied to LDS with 16-byte loads and
+// decoded from there.  The 9 x 8 partial sums are added in a fixed order.
+template <int QTD, int QTS, int FC>
+__global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* __restrict__ x, int flags,
+                                                   const int32_t* __restrict__ g_grp, const float* __restrict__ h,
+                                                   const float* __restrict__ shg, float* __restrict__ y) {
+  constexpr int NTH = 576;
+  constexpr bool IQ3 = QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS;
+  constexpr int RMAX = 2 * FC;                                 // rows per lane, FF <= 512 FC
+  constexpr int HPT = (9 * 128 * FC + NTH - 1) / NTH;          // float4 of the k + 1 SwiGLU rows per thread
+  constexpr int RB_MAX = 2 * FC * GM_IQ4XS_BYTES;              // widest routed row
+  constexpr int CR = (8 * 8 * RB_MAX / 16 + NTH - 1) / NTH;    // routed 16-byte chunks per thread
+  constexpr int RBS_MAX = QTS == GM_QTYPE_BF16 ? 1024 * FC : RB_MAX;
+  constexpr int CS = (8 * RBS_MAX / 16 + NTH - 1) / NTH;       // shared 16-byte chunks per thread
+  extern __shared__ float smem[];
+  __shared__ float s_wj[8];        // routing weight and h row of routed matrix m
+  __shared__ int32_t s_pr[8];
+  __shared__ float s_part[9][8];
+  const int D = P.D, FF = P.FF, k = P.k, nsub = FF / GM_SUB;
+  const int rbd = (int)gm_row_bytes(QTD, FF), rbs = (int)gm_row_bytes(QTS, FF);
+  const int nqr = FF >> 2;
+  const int wbytes = k * 8 * rbd + 8 * rbs;
+  float* hs = smem;                                                    // (k + 1) rows of FF (+ 4)
+  uint8_t* wr = reinterpret_cast<uint8_t*>(smem + (k + 1) * FF + 4);   // [k][8][rbd], [8][rbs], 16 spare
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(wr + ((wbytes + 16 + 15) & ~15));
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r0 = blockIdx.x * 8;
+  const bool has_sh = P.down_sh != nullptr;
+  const int trash = wbytes;                                            // spare 16 bytes
+  // --- A: loads that do not depend on the routing
+  int ex[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ex[j] = g_grp[1 + (j < k ? j : k - 1)];
+  const int jj = (tid & 7) < k ? (tid & 7) : k - 1;               // every thread loads, threads < 8 store
+  const int my_pr = g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * jj];
+  const float my_wj = __int_as_float(g_grp[GM_GRP_WORDS + jj]);
+  const float sg = has_sh ? shg[0] : 0.f;
+  const float xres = (flags & GM_MOE_RESIDUAL) ? x[r0 + (tid & 7)] : 0.f;
+  uint32_t gw = 0;
+  if constexpr (IQ3) gw = gm_iq3_tab_load();
+  const int nq_rows = (k + (has_sh ? 1 : 0)) * nqr;             // h [k][FF] directly followed by h_sh [FF]
+  const gm_f32x4* h4 = reinterpret_cast<const gm_f32x4*>(h);
+  gm_f32x4 hr[HPT];
+#pragma unroll
+  for (int i = 0; i < HPT; ++i) {
+    const int c = tid + NTH * i;
+    hr[i] = h4[c < nq_rows ? c : nq_rows - 1];
+  }
+  const int n16s = has_sh ? 8 * rbs / 16 : 1;
+  const uint8_t* sbase = has_sh ? static_cast<const uint8_t*>(P.down_sh) + (int64_t)r0 * rbs
+                                : static_cast<const uint8_t*>(P.down_exps);
+  gm_u32x4 sr[CS];
+#pragma unroll
+  for (int i = 0; i < CS; ++i) {
+    const int c = tid + NTH * i;
+    sr[i] = *reinterpret_cast<const gm_u32x4*>(sbase + 16 * (c < n16s ? c : n16s - 1));
+  }
+  issue_fence();
+  // --- B: stage them
+  if (tid < 8) { s_pr[tid] = my_pr; s_wj[tid] = my_wj; }
+  if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
+  {
+    const uint32_t magic = 0xffffffffu / (uint32_t)nqr + 1u;     // c / nqr == umulhi(c, magic) for c < 2^16
+    gm_f32x4* hs4 = reinterpret_cast<gm_f32x4*>(hs);
+#pragma unroll
+    for (int i = 0; i < HPT; ++i) {
+      const int c = tid + NTH * i;
+      const int rr = (int)__umulhi((uint32_t)c, magic), cc = c - rr * nqr;
+      hs4[c < nq_rows ? rr * nqr + il_index4(cc & 7, cc >> 3, nsub) : (k + 1) * nqr] = hr[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < CS; ++i) {
+    const int c = tid + NTH * i;
+    *reinterpret_cast<gm_u32x4*>(wr + (c < n16s && has_sh ? k * 8 * rbd + 16 * c : trash)) = sr[i];
+  }
+  // --- C: routed rows (addresses from the routing)
+  {
+    const int n16 = 8 * rbd / 16, total = k * n16;
+    const uint32_t magic = 0xffffffffu / (uint32_t)n16 + 1u;
+    gm_u32x4 rr[CR];
+    int dst[CR];
+#pragma unroll
+    for (int i = 0; i < CR; ++i) {
+      const int c = tid + NTH * i;
+      const int cc = c < total ? c : total - 1;
+      const int m = (int)__umulhi((uint32_t)cc, magic), j = cc - m * n16;
+      int e = ex[0];
+#pragma unroll
+      for (int q = 1; q < 8; ++q) e = m == q ? ex[q] : e;
+      rr[i] = *reinterpret_cast<const gm_u32x4*>(static_cast<const uint8_t*>(P.down_exps) +
+                                                  ((int64_t)e * D + r0) * rbd + 16 * j);
+      dst[i] = c < total ? m * 8 * rbd + 16 * j : trash;
+    }
+    issue_fence();
+#pragma unroll
+    for (int i = 0; i < CR; ++i) *reinterpret_cast<gm_u32x4*>(wr + dst[i]) = rr[i];
+  }
+  __syncthreads();
+  // --- D: decode from LDS; wave w -> matrix w
+  const bool routed = wave < k, shared = has_sh && wave == k;
+  if (routed || shared) {
+    const int lg = nsub == 8 ? 3 : nsub == 16 ? 4 : 5;
+    const int R = nsub >> 3, rg = lane >> lg, sub = lane & (nsub - 1);
+    const int hrow = routed ? s_pr[wave] : k;
+    float hv[32];                                              // SwiGLU values of this sub-block
+    {
+      const gm_f32x4* hrow4 = reinterpret_cast<const gm_f32x4*>(hs + hrow * FF);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const gm_f32x4 a = hrow4[il_index4(q, sub, nsub)];
+        hv[4 * q] = a.x; hv[4 * q + 1] = a.y; hv[4 * q + 2] = a.z; hv[4 * q + 3] = a.w;
+      }
+    }
+    float part[RMAX];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+      part[r] = 0.f;
+      if (r < R) {
+        float wv[32], sc;
+        if (routed) {
+          const typename RawSub<QTD>::T raw = gm_load_sub<QTD>(wr + (wave * 8 + rg * R + r) * rbd, sub);
+          sc = gm_decode_sub_t<QTD>(raw, sub, tab, wv);
+        } else {
+          const typename RawSub<QTS>::T raw = gm_load_sub<QTS>(wr + k * 8 * rbd + (rg * R + r) * rbs, sub);
+          sc = gm_decode_sub_t<QTS>(raw, sub, tab, wv);
+        }
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 32; j += 2) { s0 = fmaf(wv[j], hv[j], s0); s1 = fmaf(wv[j + 1], hv[j + 1], s1); }
+        part[r] = sc * (s0 + s1);
+      }
+    }
+    const float wgt = routed ? s_wj[wave] : sg;
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+      if (r < R) {
+        const float v = group_sum(part[r], nsub);
+        if (sub == 0) s_part[wave][rg * R + r] = wgt * v;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < 8) {
+    float acc = 0.f;
+    for (int w = 0; w < k; ++w) acc += s_part[w][tid];
+    if (has_sh) acc += s_part[k][tid];
+    if (r0 + tid < D) y[r0 + tid] = (flags & GM_MOE_RESIDUAL) ? xres + acc : acc;
+  }
+}
+
+// 64 rows of one down matrix for nm <= 8 member rows of hsrc (global rows
+// src[m] of h, where h_sh follows h), written to yp rows dst[m].
+template <int QTW, int FC>
+__device__ __forceinline__ void down_tile(const uint8_t* __restrict__ wbase, int D, int FF, int tile, int nm,
+                                          const int (&src)[8], const int (&dst)[8], const float* __restrict__ h,
+                                          float* __restrict__ hs, uint32_t gw, Iq3Tab* __restrict__ tab,
+                                          float* __restrict__ yp) {
+  constexpr int HPT = 4 * FC;     // float4 per thread: 8 * FF <= 8 * 512 * FC floats over 256 threads
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane & 15, nsub = FF >> 5;
+  const int64_t rb = gm_row_bytes(QTW, FF);
+  RowFetch<QTW, FC> f[4];
+  int rows[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    rows[q] = tile * 64 + wave * 16 + q * 4 + (lane >> 4);
+    fetch_subs<QTW, 16, FC>(f[q], wbase + (int64_t)(rows[q] < D ? rows[q] : 0) * rb, lir, nsub);
+  }
+  const int nqr = FF >> 2, nq = nm * nqr;
+  const gm_f32x4* h4 = reinterpret_cast<const gm_f32x4*>(h);
+  gm_f32x4 hr[HPT];
+#pragma unroll
+  for (int i = 0; i < HPT; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    const int m = c < nq ? c / nqr : 0;
+    int s = src[0];
+#pragma unroll
+    for (int mm = 1; mm < 8; ++mm) s = m == mm ? src[mm] : s;
+    hr[i] = h4[(int64_t)s * nqr + (c < nq ? c - m * nqr : 0)];
+  }
+  issue_fence();
+  if constexpr (QTW == GM_QTYPE_IQ3_XXS) gm_iq3_tab_store(gw, tab);
+  gm_f32x4* hs4 = reinterpret_cast<gm_f32x4*>(hs);
+#pragma unroll
+  for (int i = 0; i < HPT; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    const int m = c / nqr, cc = c - m * nqr;
+    hs4[c < nq ? m * nqr + il_index4(cc & 7, cc >> 3, nsub) : 8 * nqr] = hr[i];   // unconditional
+  }
+  __syncthreads();
+  int idx[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) idx[m] = m;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float part[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) part[m] = 0.f;
+    dot_subs<QTW, 16, FC, 8>(f[q], lir, nsub, hs, FF, idx, nm, tab, part);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      if (m < nm) {
+        const float sm = row_sum<16>(part[m]);
+        if (lir == 0 && rows[q] < D) yp[(int64_t)dst[m] * D + rows[q]] = sm;
+      }
+    }
+  }
+}
+
+// Block = (unit u, 64-row tile); units 0 .. nu-1 are the unique routed experts,
+// unit nu the shared expert (all T tokens).
+template <int QTD, int QTS, int FC>
+__global__ void __launch_bounds__(256) k_dec_down8(gm_moe_layer P, int T, const int32_t* __restrict__ g_grp,
+                                                   const float* __restrict__ h, float* __restrict__ yp,
+                                                   int n_tiles) {
+  extern __shared__ float hs[];                 // [8][FF] interleaved (+ 4), then the IQ3 tables
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(hs + 8 * P.FF + 4);
+  const int D = P.D, FF = P.FF, k = P.k, Ptot = T * k;
+  const int u = blockIdx.x / n_tiles, tile = blockIdx.x - u * n_tiles;
+  const int nu = g_grp[0];
+  const bool has_sh = P.down_sh != nullptr;
+  if (u > nu || (u == nu && !has_sh)) return;   // uniform per block
+  uint32_t gw = 0;
+  if constexpr (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS) gw = gm_iq3_tab_load();
+  int src[8], dst[8];
+  if (u == nu) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) { src[m] = Ptot + (m < T ? m : 0); dst[m] = src[m]; }
+    down_tile<QTS, FC>(static_cast<const uint8_t*>(P.down_sh), D, FF, tile, T, src, dst, h, hs, gw, tab, yp);
+  } else {
+    const int e = g_grp[1 + u];
+    const int nm = g_grp[1 + GM_GRP_MAXU + u];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      src[m] = g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * u + (m < nm ? m : 0)];
+      dst[m] = src[m];
+    }
+    down_tile<QTD, FC>(static_cast<const uint8_t*>(P.down_exps) + (int64_t)e * D * gm_row_bytes(QTD, FF), D, FF,
+                       tile, nm, src, dst, h, hs, gw, tab, yp);
+  }
+}
+
+// y[t] = sum over t's top-k slots in ascending expert id of w * yp[t*k + j]
+//        + sigmoid gate * yp[T*k + t]  (+ x[t]).
+__global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ x, int T, int k, int D, int flags,
+                                                     const int32_t* __restrict__ g_ids,
+                                                     const float* __restrict__ g_wts, const float* __restrict__ shg,
+                                                     int has_sh, const float* __restrict__ yp, float* __restrict__ y) {
+  const int t = blockIdx.y;
+  const int d = blockIdx.x * 256 + threadIdx.x;
+  int id[8], sl[8];
+  float w[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    id[j] = j < k ? g_ids[t * k + j] : 0x7fffffff;
+    w[j] = j < k ? g_wts[t * k + j] : 0.f;
+    sl[j] = j;
+  }
+#pragma unroll
+  for (int i = 1; i < 8; ++i)
+#pragma unroll
+    for (int j = i; j > 0; --j)
+      if (id[j] < id[j - 1]) {
+        const int ti = id[j]; id[j] = id[j - 1]; id[j - 1] = ti;
+        const float tw = w[j]; w[j] = w[j - 1]; w[j - 1] = tw;
+        const int ts = sl[j]; sl[j] = sl[j - 1]; sl[j - 1] = ts;
+      }
+  if (d >= D) return;
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j < k) acc = fmaf(w[j], yp[(int64_t)(t * k + sl[j]) * D + d], acc);
+  if (has_sh) acc = fmaf(shg[t], yp[(int64_t)(T * k + t) * D + d], acc);
+  if (flags & GM_MOE_RESIDUAL) acc = x[(int64_t)t * D + d] + acc;
+  y[(int64_t)t * D + d] = acc;
+}
+
+template <int QTD, int QTS, int FC>
+int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
+              hipStream_t s) {
+  const int D = P->D, FF = P->FF, k = P->k;
+  if (fast1) {
+    if constexpr (FC <= 2) {
+      const size_t wbytes = (size_t)k * 8 * gm_row_bytes(QTD, FF) + 8 * (size_t)gm_row_bytes(QTS, FF);
+      const size_t smem = ((size_t)(k + 1) * FF + 4) * 4 + ((wbytes + 16 + 15) & ~(size_t)15) +
+                          (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+      if (int rc = gm_set_smem(k_dec_down1<QTD, QTS, FC>, smem)) return rc;
+      hipLaunchKernelGGL((k_dec_down1<QTD, QTS, FC>), dim3((D + 7) / 8), dim3(576), smem, s, *P, x, flags, a.grp,
+                         a.h, a.shg, y);
+      GM_TRY(hipGetLastError());
+      return GM_OK;
+    }
+  }
+  const int n_tiles = (D + 63) / 64;
+  const int max_u = T * k < P->E ? T * k : P->E;
+  const size_t smem = ((size_t)8 * FF + 4) * 4 + (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+  if (int rc = gm_set_smem(k_dec_down8<QTD, QTS, FC>, smem)) return rc;
+  hipLaunchKernelGGL((k_dec_down8<QTD, QTS, FC>), dim3((max_u + 1) * n_tiles), dim3(256), smem, s, *P, T, a.grp, a.h,
+                     a.yp, n_tiles);
+  GM_TRY(hipGetLastError());
+  hipLaunchKernelGGL(k_dec_combine, dim3((D + 255) / 256, T), dim3(256), 0, s, x, T, k, D, flags, a.ids, a.wts,
+                     a.shg, P->down_sh ? 1 : 0, a.yp, y);
+  GM_TRY(hipGetLastError());
+  return GM_OK;
+}
+
+template <int QTD, int QTS>
+int launch_dn_f(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
+                hipStream_t s) {
+  switch (gm_dec_fc(P->FF)) {
+    case 1: return launch_dn<QTD, QTS, 1>(P, x, y, T, flags, fast1, a, s);
+    case 2: return launch_dn<QTD, QTS, 2>(P, x, y, T, flags, fast1, a, s);
+    default: return launch_dn<QTD, QTS, 4>(P, x, y, T, flags, fast1, a, s);
+  }
+}
+
+template <int QTD>
+int launch_dn_s(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
+                hipStream_t s) {
+  if (!P->down_sh) return launch_dn_f<QTD, QTD>(P, x, y, T, flags, fast1, a, s);
+  switch (P->q_down_sh) {
+    case GM_QTYPE_IQ4_XS: return launch_dn_f<QTD, GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s);
+    case GM_QTYPE_IQ3_XXS: return launch_dn_f<QTD, GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s);
+    case GM_QTYPE_BF16: return launch_dn_f<QTD, GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s);
+    default: return gm_fail_arg("gm_moe_forward: shared down format %d unsupported", P->q_down_sh);
+  }
+}
+
+}  // namespace
+
+int gm_dec_down(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
+                hipStream_t s) {
+  switch (P->q_down) {
+    case GM_QTYPE_IQ4_XS: return launch_dn_s<GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s);
+    case GM_QTYPE_IQ3_XXS: return launch_dn_s<GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s);
+    default: return gm_fail_arg("gm_moe_forward: routed down format %d unsupported", P->q_down);
+  }
+}

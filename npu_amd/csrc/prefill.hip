@@ -21,7 +21,6 @@
 using namespace gm_moe;
 
 typedef __bf16 gm_bf16x8 __attribute__((ext_vector_type(8)));
-typedef float gm_f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
