@@ -115,30 +115,36 @@ def run_chain(layers, T: int, steps: int, warmup: int, seed: int):
     return ms, n_unique, finite
 
 
-def time_stages(layers, T: int, reps: int = 3):
-    """Per-kernel durations (HIP events on torch's stream, which the kernels run on)."""
+def time_stages(layers, T: int, reps: int = 20):
+    """Average launch period of each decode stage kernel: one hipGraph per stage holding
+    that stage's launch for every layer (distinct weights), replayed `reps` times between
+    two HIP events on the replay stream.  Back-to-back dependent launches of one kernel,
+    so the period is the kernel's duration plus the ~1 us dependent-dispatch gap (the
+    rocprof duration of the same kernel is the lower bound)."""
     import torch
     from npu_amd import synth
     dev = layers[0].gate.device
     x = torch.from_numpy(synth.host_input(SEED + 1, T, D, rmsnorm=False)).to(dev)
     y = torch.empty_like(x)
-    n = len(layers) * reps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n)]
-    i = 0
-    for _ in range(reps):
-        for blk in layers:
-            e = ev[i]
-            e[0].record()
-            blk(x, residual=True, out=y, stage=1)
-            e[1].record()
-            blk(x, residual=True, out=y, stage=2)
-            e[2].record()
-            blk(x, residual=True, out=y, stage=3)
-            e[3].record()
-            i += 1
+    for blk in layers:                       # routing state in every workspace
+        blk(x, residual=True, out=y)
     torch.cuda.synchronize()
-    st = [sum(e[j].elapsed_time(e[j + 1]) for e in ev) / n * 1e3 for j in range(3)]
-    return {"router_shared_us": st[0], "gateup_us": st[1], "down_us": st[2]}
+    out = {}
+    for stage, name in ((1, "router_shared_us"), (2, "gateup_us"), (3, "down_us")):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for blk in layers:
+                blk(x, residual=True, out=y, stage=stage)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
+    return out
 
 
 def run_prefill(layers, T: int = 512, n_blocks: int = 8, reps: int = 5):
@@ -232,6 +238,18 @@ def cpu_baseline(layers, n_sample: int):
     }
 
 
+def traffic_bytes(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (profiles/hbm_traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the
+    same counters read on a plain copy kernel of known size); None if absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["kernels"][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def calib_copy() -> None:
     import torch
     n = 256 << 20
@@ -282,7 +300,9 @@ def main() -> int:
     log(f"B=1: {ms1 * 1e3:.1f} us/step, {tok_s:.1f} tok/s, {eff_gbps:.1f} GB/s effective, finite={ok1}")
 
     stages = time_stages(layers, 1)
-    gu_launch_bytes = K_TOP * gu_bytes + D * 4 + K_TOP * FF * 4
+    # k_dec_gateup1 algorithmic bytes: the k routed experts' raw gate+up rows, x, the
+    # router logits and the SwiGLU rows it writes
+    gu_launch_bytes = K_TOP * gu_bytes + D * 4 + E * 4 + K_TOP * FF * 4
     gu_gbps = gu_launch_bytes / (stages["gateup_us"] * 1e-6) / 1e9
     log(f"stages (us): {stages}")
 
@@ -316,9 +336,10 @@ def main() -> int:
         "effective_weight_frac_of_peak": eff_gbps / HBM_PEAK_GBPS,
         "block_us": ms1 * 1e3 / args.layers,
         "weight_bytes_per_step": bytes1,
-        "roofline": {"bound": "hbm", "kernel": "k_moe_gateup (routed gate/up + SwiGLU, T=1)",
+        "roofline": {"bound": "hbm", "kernel": "k_dec_gateup1 (top-k + routed gate/up + SwiGLU, T=1)",
                      "achieved": gu_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gu_gbps / HBM_PEAK_GBPS,
-                     "traffic": None, "bytes_per_launch": gu_launch_bytes, "avg_launch_us": stages["gateup_us"]},
+                     "traffic": traffic_bytes("k_dec_gateup1"), "bytes_per_launch": gu_launch_bytes,
+                     "avg_launch_us": stages["gateup_us"]},
         "stage_us": stages,
         "cpu_baseline": cpu,
         "finite": ok1,

@@ -1,0 +1,128 @@
+"""Summaries of rocprofv3 output for the MoE-block kernels (the files under profiles/).
+
+Reads a ``--kernel-trace --stats`` kernel-stats CSV and four ``--pmc`` counter CSVs
+(FETCH_SIZE and WRITE_SIZE, KiB per dispatch, each for the workload and for a plain
+copy kernel of known size) and writes
+
+* ``hbm_traffic.json`` -- per kernel: rocprof average duration, counter means, the
+  copy-calibrated HBM bytes per launch and the algorithmic bytes per launch;
+* ``<name>.md`` -- the same as a table, with the commands that produced the inputs.
+
+Calibration: the copy kernel moves ``calib_bytes`` each way per launch, so
+``scale = calib_bytes / (counter KiB * 1024)`` for each counter; a kernel's HBM bytes
+per launch are ``FETCH * 1024 * scale_fetch + WRITE * 1024 * scale_write``.
+
+    python -m npu_amd.rocprof_summary --stats S.csv --fetch F.csv --write W.csv \\
+        --calib-fetch CF.csv --calib-write CW.csv --calib-bytes 268435456 --out profiles
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import statistics
+from collections import defaultdict
+from pathlib import Path
+
+# Config-5 block shape (BASELINE configs 3 and 5).
+D, FF, E, K = 2048, 512, 256, 8
+IQ4_ROW = D // 256 * 136          # gate/up row, IQ4_XS
+IQ3_ROW = FF // 256 * 98          # down row, IQ3_XXS
+
+
+def algorithmic_bytes() -> dict[str, int]:
+    """Bytes each T = 1 decode kernel must move at least once (weights read, activations
+    read once, outputs written once)."""
+    return {
+        "k_dec_router": E * D * 2 + D * 2 + 2 * FF * IQ4_ROW + D * 4 + E * 4 + 4 + FF * 4,
+        "k_dec_gateup1": K * 2 * FF * IQ4_ROW + D * 4 + E * 4 + K * FF * 4,
+        "k_dec_down1": K * D * IQ3_ROW + D * IQ3_ROW + (K + 1) * FF * 4 + D * 4 + D * 4,
+    }
+
+
+def short(name: str) -> str:
+    """Kernel name without return type, namespaces in parentheses and arguments."""
+    base = name.replace("(anonymous namespace)::", "")
+    if base.startswith("void "):
+        base = base[5:]
+    return base.split("(")[0].strip()
+
+
+def family(name: str) -> str:
+    return short(name).split("<")[0]
+
+
+def counter_means(path: str) -> dict[str, float]:
+    vals: dict[str, list[float]] = defaultdict(list)
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            vals[short(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+    return {k: statistics.fmean(v) for k, v in vals.items()}
+
+
+def kernel_stats(path: str) -> dict[str, dict]:
+    out = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            out[short(r["Name"])] = {"calls": int(r["Calls"]), "avg_us": float(r["AverageNs"]) / 1e3,
+                                     "min_us": float(r["MinNs"]) / 1e3, "max_us": float(r["MaxNs"]) / 1e3}
+    return out
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--stats", required=True)
+    ap.add_argument("--fetch", required=True)
+    ap.add_argument("--write", required=True)
+    ap.add_argument("--calib-fetch", required=True)
+    ap.add_argument("--calib-write", required=True)
+    ap.add_argument("--calib-bytes", type=int, default=256 << 20)
+    ap.add_argument("--calib-kernel", default="__amd_rocclr_copyBuffer")
+    ap.add_argument("--out", default="profiles")
+    ap.add_argument("--name", default="moe_decode_config5")
+    ap.add_argument("--commands", default="", help="text describing the commands (markdown)")
+    a = ap.parse_args()
+
+    stats = kernel_stats(a.stats)
+    fetch, write = counter_means(a.fetch), counter_means(a.write)
+    cf, cw = counter_means(a.calib_fetch)[a.calib_kernel], counter_means(a.calib_write)[a.calib_kernel]
+    s_fetch, s_write = a.calib_bytes / (cf * 1024), a.calib_bytes / (cw * 1024)
+    algo = algorithmic_bytes()
+    kernels = {}
+    for name, st in stats.items():
+        fam = family(name)
+        if fam not in algo or name not in fetch:
+            continue
+        hbm = fetch[name] * 1024 * s_fetch + write.get(name, 0.0) * 1024 * s_write
+        kernels[fam] = {
+            "instance": name, "calls": st["calls"], "rocprof_avg_us": st["avg_us"],
+            "fetch_kib": fetch[name], "write_kib": write.get(name, 0.0),
+            "hbm_bytes_per_launch": round(hbm), "algorithmic_bytes_per_launch": algo[fam],
+            "traffic_over_algorithmic": hbm / algo[fam],
+            "algorithmic_GBps_at_rocprof_avg": algo[fam] / (st["avg_us"] * 1e-6) / 1e9,
+        }
+    out = Path(a.out)
+    out.mkdir(parents=True, exist_ok=True)
+    doc = {"calibration": {"kernel": a.calib_kernel, "bytes_each_way": a.calib_bytes, "fetch_kib": cf,
+                           "write_kib": cw, "fetch_scale": s_fetch, "write_scale": s_write},
+           "kernels": kernels}
+    (out / "hbm_traffic.json").write_text(json.dumps(doc, indent=1) + "\n")
+    lines = [f"# {a.name}: kernel durations and HBM traffic", "", a.commands, "",
+             f"Copy calibration ({a.calib_kernel}, {a.calib_bytes} B each way): FETCH_SIZE reads "
+             f"{cf:.1f} KiB (scale {s_fetch:.4f}), WRITE_SIZE {cw:.1f} KiB (scale {s_write:.4f}).", "",
+             "| kernel | calls | rocprof avg us | FETCH KiB | WRITE KiB | HBM bytes/launch | algorithmic bytes | "
+             "traffic/algorithmic | algorithmic GB/s |", "|---|---|---|---|---|---|---|---|---|"]
+    for fam, k in kernels.items():
+        lines.append(f"| {k['instance']} | {k['calls']} | {k['rocprof_avg_us']:.2f} | {k['fetch_kib']:.1f} | "
+                     f"{k['write_kib']:.1f} | {k['hbm_bytes_per_launch']} | {k['algorithmic_bytes_per_launch']} | "
+                     f"{k['traffic_over_algorithmic']:.3f} | {k['algorithmic_GBps_at_rocprof_avg']:.1f} |")
+    lines += ["", "All kernels (rocprof --stats):", "", "| kernel | calls | avg us | min us | max us |",
+              "|---|---|---|---|---|"]
+    for name, st in sorted(stats.items(), key=lambda kv: -kv[1]["calls"] * kv[1]["avg_us"])[:16]:
+        lines.append(f"| {name[:90]} | {st['calls']} | {st['avg_us']:.2f} | {st['min_us']:.2f} | {st['max_us']:.2f} |")
+    (out / f"{a.name}.md").write_text("\n".join(lines) + "\n")
+    print(json.dumps(kernels, indent=1))
+
+
+if __name__ == "__main__":
+    main()
