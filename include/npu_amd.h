@@ -140,9 +140,22 @@ int gm_moe_forward(const gm_moe_layer* L, const float* x, float* y, int T, int f
                    size_t ws_bytes, void* stream);
 
 /*
+ * gm_moe_forward forced onto one path.  gm_moe_decode: the fp32-accumulate
+ * decode kernels, 1 <= T <= 8 (the reference's NPU expert path is T = 1:
+ * qwen/forward.py:494-560 via _npu_routed_expert).  gm_moe_prefill: the
+ * grouped bf16-MFMA GEMMs for any T >= 1 (the reference runs prefill through
+ * the CPU loop of qwen/forward.py:622-663).  Same workspace as gm_moe_forward.
+ */
+int gm_moe_decode(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
+                  size_t ws_bytes, void* stream);
+int gm_moe_prefill(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
+                   size_t ws_bytes, void* stream);
+
+/*
  * One stage of gm_moe_forward, for stage-wise checks and per-kernel timing:
- * stage 1 = router / top-k inputs (+ shared expert gate/up), 2 = routed
- * gate/up + SwiGLU, 3 = down + combine (+ residual); stage 0 runs all three.
+ * stage 1 = router logits and shared scalar gate (+ shared expert gate/up),
+ * 2 = top-k, grouping and routed gate/up + SwiGLU, 3 = down + combine
+ * (+ residual); stage 0 runs all three.
  * Stages must run in order on the same workspace.  Decode path (T <= 8) only.
  * Mirrors the stage boundaries of qwen/compare.py:compare_moe (191-297).
  */

@@ -62,6 +62,8 @@ SIGNATURES = {
                                         ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "gm_moe_forward": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _vp]),
     "gm_moe_forward_stage": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _i32, _vp]),
+    "gm_moe_decode": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _vp]),
+    "gm_moe_prefill": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _vp]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -49,7 +49,7 @@ GmMoeWs gm_moe_ws_layout(const gm_moe_layer* L, int T) {
   w.hsh = o; o = align256(o + Tz * (size_t)(L->FF_sh > 0 ? L->FF_sh : 0) * 4);
   w.yp = o; o = align256(o + (T <= GM_DECODE_MAX_T ? (Tz * k + Tz) * (size_t)L->D * 4 : 0));
   w.counters = o; o = align256(o + 256);
-  w.pre = o; o = align256(o + (T > GM_DECODE_MAX_T ? gm_prefill_scratch_bytes(L, T) : 0));
+  w.pre = o; o = align256(o + gm_prefill_scratch_bytes(L, T));     // every T: gm_moe_prefill takes any T
   w.total = o;
   return w;
 }
@@ -165,24 +165,37 @@ int gm_moe_workspace_offsets(const gm_moe_layer* L, int T, size_t* off_logits, s
   return GM_OK;
 }
 
+enum { kPathAuto = 0, kPathDecode = 1, kPathPrefill = 2 };
+
 static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
-                            size_t ws_bytes, int stage, void* stream);
+                            size_t ws_bytes, int stage, int path, void* stream);
 
 int gm_moe_forward(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws, size_t ws_bytes,
                    void* stream) {
-  return moe_forward_impl(L, x, y, T, flags, ws, ws_bytes, 0, stream);
+  return moe_forward_impl(L, x, y, T, flags, ws, ws_bytes, 0, kPathAuto, stream);
+}
+
+int gm_moe_decode(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws, size_t ws_bytes,
+                  void* stream) {
+  if (T > GM_DECODE_MAX_T) return gm_fail_arg("gm_moe_decode: T=%d > %d (use gm_moe_prefill)", T, GM_DECODE_MAX_T);
+  return moe_forward_impl(L, x, y, T, flags, ws, ws_bytes, 0, kPathDecode, stream);
+}
+
+int gm_moe_prefill(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws, size_t ws_bytes,
+                   void* stream) {
+  return moe_forward_impl(L, x, y, T, flags, ws, ws_bytes, 0, kPathPrefill, stream);
 }
 
 int gm_moe_forward_stage(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
                          size_t ws_bytes, int stage, void* stream) {
   if (stage < 0 || stage > 3) return gm_fail_arg("gm_moe_forward_stage: stage %d not in 0..3", stage);
-  return moe_forward_impl(L, x, y, T, flags, ws, ws_bytes, stage, stream);
+  return moe_forward_impl(L, x, y, T, flags, ws, ws_bytes, stage, kPathAuto, stream);
 }
 
 }  // extern "C"
 
 static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
-                            size_t ws_bytes, int stage, void* stream) {
+                            size_t ws_bytes, int stage, int path, void* stream) {
   if (int rc = check_layer(L)) return rc;
   if (T < 0) return gm_fail_arg("gm_moe_forward: negative T");
   if (T == 0) return GM_OK;
@@ -194,7 +207,8 @@ static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int
   if (reinterpret_cast<uintptr_t>(ws) % 256) return gm_fail_arg("gm_moe_forward: workspace must be 256-byte aligned");
   uint8_t* w = static_cast<uint8_t*>(ws);
   hipStream_t s = as_stream(stream);
-  if (T <= GM_DECODE_MAX_T && T * L->k <= GM_GRP_MAXU) return gm_moe_decode(L, x, y, T, flags, w, lay, s, stage);
+  const bool decode = path == kPathDecode || (path == kPathAuto && T <= GM_DECODE_MAX_T && T * L->k <= GM_GRP_MAXU);
+  if (decode) return gm_dec_run(L, x, y, T, flags, w, lay, s, stage);
   if (stage != 0) return gm_fail_arg("gm_moe_forward_stage: stages are only defined for the decode path (T <= 8)");
-  return gm_moe_prefill(L, x, y, T, flags, w, lay, s);
+  return gm_pf_run(L, x, y, T, flags, w, lay, s);
 }

@@ -41,9 +41,9 @@ int gm_launch_router(const uint16_t* w_router, const float* bias, const float* x
                      const uint16_t* w_sh_gate, const float* norm_w, float eps, float* logits,
                      float* sh_gate, hipStream_t s);
 int gm_launch_topk(const float* logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
-int gm_moe_decode(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
+int gm_dec_run(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
                   const GmMoeWs& lay, hipStream_t s, int stage = 0);
-int gm_moe_prefill(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
+int gm_pf_run(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
                    const GmMoeWs& lay, hipStream_t s);
 int gm_launch_dispatch(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
                        int32_t* sorted_pairs, hipStream_t s);

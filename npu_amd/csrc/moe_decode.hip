@@ -128,7 +128,7 @@ int launch_router(const gm_moe_layer* P, const float* x, int T, const GmDecArgs&
 
 }  // namespace
 
-int gm_moe_decode(const gm_moe_layer* P, const float* x, float* y, int T, int flags, uint8_t* ws,
+int gm_dec_run(const gm_moe_layer* P, const float* x, float* y, int T, int flags, uint8_t* ws,
                   const GmMoeWs& lay, hipStream_t s, int stage) {
   if (T < 1 || T > GM_DECODE_MAX_T) return gm_fail_arg("gm_moe_forward: decode path needs 1 <= T <= 8 (T=%d)", T);
   if (P->D % 256 || P->FF % 256) return gm_fail_arg("gm_moe_forward: D and FF must be multiples of 256");

@@ -397,7 +397,7 @@ size_t gm_prefill_scratch_bytes(const gm_moe_layer* L, int T) {
   return total;
 }
 
-int gm_moe_prefill(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
+int gm_pf_run(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
                    const GmMoeWs& lay, hipStream_t s) {
   if (L->gate_sh && (L->q_gate_sh != L->q_gate || L->q_down_sh != L->q_down))
     return gm_fail_arg("gm_moe_forward: the prefill path needs the shared expert in the routed formats"),

@@ -116,16 +116,17 @@ class GpuMoeBlock:
         return ws
 
     def forward(self, x: torch.Tensor, *, residual: bool = False, out: torch.Tensor | None = None,
-                stage: int = 0) -> torch.Tensor:
+                stage: int = 0, path: str = "auto") -> torch.Tensor:
         """x fp32 [T, D] on the GPU -> y [T, D] = moe(rmsnorm(x)) (+ x).
 
-        ``stage`` 1..3 runs one decode stage only (router, gate/up, down)."""
+        ``stage`` 1..3 runs one decode stage only (router, gate/up, down);
+        ``path`` forces the decode kernels or the prefill GEMMs ("auto" picks by T)."""
         if x.dim() != 2 or x.shape[1] != self.D:
             raise ValueError(f"x must be [T, {self.D}], got {tuple(x.shape)}")
         x = x.to(torch.float32).contiguous()
         T = x.shape[0]
         y = out if out is not None else torch.empty_like(x)
-        ops.moe_forward_raw(self.struct, x, y, self.workspace(T), residual=residual, stage=stage)
+        ops.moe_forward_raw(self.struct, x, y, self.workspace(T), residual=residual, stage=stage, path=path)
         return y
 
     __call__ = forward

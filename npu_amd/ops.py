@@ -122,13 +122,16 @@ def moe_workspace_offsets(layer: L.GmMoeLayer, T: int) -> dict[str, int]:
 
 
 def moe_forward_raw(layer: L.GmMoeLayer, x: torch.Tensor, y: torch.Tensor, ws: torch.Tensor,
-                    residual: bool = False, stage: int = 0) -> None:
-    """Enqueue the fused MoE block (stage 0) or one of its stages 1..3: y = moe(rmsnorm(x)) (+ x)."""
+                    residual: bool = False, stage: int = 0, path: str = "auto") -> None:
+    """Enqueue the fused MoE block (stage 0) or one of its stages 1..3: y = moe(rmsnorm(x)) (+ x).
+
+    path: "auto" (decode kernels for T <= 8, prefill GEMMs above), "decode" or "prefill"."""
     T = x.shape[0]
     flags = L.GM_MOE_RESIDUAL if residual else 0
     if stage == 0:
-        rc = L.lib().gm_moe_forward(ctypes.byref(layer), L.ptr(x), L.ptr(y), T, flags, L.ptr(ws), ws.numel(),
-                                    L.stream_ptr())
+        fn = {"auto": "gm_moe_forward", "decode": "gm_moe_decode", "prefill": "gm_moe_prefill"}[path]
+        rc = getattr(L.lib(), fn)(ctypes.byref(layer), L.ptr(x), L.ptr(y), T, flags, L.ptr(ws), ws.numel(),
+                                  L.stream_ptr())
     else:
         rc = L.lib().gm_moe_forward_stage(ctypes.byref(layer), L.ptr(x), L.ptr(y), T, flags, L.ptr(ws),
                                           ws.numel(), stage, L.stream_ptr())

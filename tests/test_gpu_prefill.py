@@ -86,3 +86,20 @@ def test_prefill_stage_outputs(gpu):
     assert torch.allclose(got["ffn_moe_logits"], st["ffn_moe_logits"], rtol=0, atol=2e-5)
     assert torch.equal(got["topk_ids"].long(), st["topk_ids"])
     assert torch.allclose(got["shared_expert_gate_sigmoid"], st["shared_expert_gate_sigmoid"], rtol=1e-5)
+
+
+@pytest.mark.parametrize("T", [1, 3, 8])
+def test_prefill_path_at_decode_sizes(gpu, T):
+    """gm_moe_prefill at T <= 8 against the oracle, and against the decode kernels."""
+    h = synth.host_moe_layer(90 + T, q_gate=QT.IQ4_XS, q_down=QT.IQ3_XXS)
+    ol = OM.OracleLayer(h)
+    x = torch.from_numpy(synth.host_input(T, T, h.D))
+    blk = GpuMoeBlock.from_host(h, device=gpu)
+    yp = blk(x.to(gpu), path="prefill").cpu()
+    yd = blk(x.to(gpu), path="decode").cpu()
+    ref = OM.block_forward(x, ol)
+    margin = OM.topk_margin(OM.router_logits64(x, ol), h.k)
+    if bool((margin > 1e-5).all()):
+        assert OM.rel_err(yp, ref) <= REL_TOL
+        assert OM.rel_err(yd, ref) <= 1e-3
+        assert OM.rel_err(yp, yd) <= REL_TOL
