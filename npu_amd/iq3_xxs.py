@@ -43,7 +43,7 @@ assert KSIGNS.shape == (128, 8) and KSIGNS.dtype == np.int8
 
 def dequant_rows(blocks_u8: np.ndarray) -> np.ndarray:
     """(..., n_blocks, 98) uint8 -> fp32 (..., n_blocks*256), on the GPU."""
-    blocks_u8 = np.ascontiguousarray(blocks_u8)
+    blocks_u8 = np.array(blocks_u8, copy=True, order="C")      # writable: torch.from_numpy shares it
     if blocks_u8.dtype != np.uint8 or blocks_u8.shape[-1] != 98:
         raise ValueError(f"need (..., n, 98) uint8, got {blocks_u8.shape}/{blocks_u8.dtype}")
     n = blocks_u8.size // 98
