@@ -208,38 +208,35 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int E, i
 }
 
 // --------------------------------------------------------------- grouping
-// Grouping of (token, slot) pairs by expert into LDS (all threads call; pairs
-// are handled by wave 0): g[0] = n_unique, g[1+u] = expert of slot u
-// (ascending), g[65+u] = member count, g[129 + 8u + m] = pair index t*k + j
-// of member m (tokens ascending).
+// Grouping of (token, slot) pairs by expert into LDS: g[0] = n_unique,
+// g[1+u] = expert of unique slot u (ascending), g[65+u] = member count,
+// g[129 + 8u + m] = pair index t*k + j of member m (pairs ascending).  Wave 0
+// does the work (P <= 64 pairs, one per lane): the lanes sharing a lane's
+// expert are found with one ballot per bit of the id, the rank of the expert
+// among the unique ones from an LDS bitmap.  All threads call; ends with a
+// barrier.
 __device__ __forceinline__ void block_group(const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ g,
                                             uint32_t* __restrict__ bits) {
-  const int nwords = (E + 31) / 32;
-  for (int i = threadIdx.x; i < nwords; i += blockDim.x) bits[i] = 0u;
-  __syncthreads();
-  const int lane = threadIdx.x & 63;
-  const bool w0 = threadIdx.x < 64;
-  const int e = (w0 && lane < P) ? ids[lane] : -1;
-  if (e >= 0) atomicOr(&bits[e >> 5], 1u << (e & 31));
-  __syncthreads();
-  if (w0) {
-    int nu = 0, rank = 0;
-    for (int w = 0; w < nwords; ++w) {
-      const uint32_t b = bits[w];
-      nu += __builtin_popcount(b);
-      if (e >= 0 && (w << 5) < e) {
-        const int hi = e - (w << 5);
-        rank += hi >= 32 ? __builtin_popcount(b) : __builtin_popcount(b & ((1u << hi) - 1u));
-      }
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int nwords = (E + 31) / 32;
+    if (lane < nwords) bits[lane] = 0u;
+    const int e = lane < P ? ids[lane] : -1;
+    const uint64_t valid = __ballot(e >= 0);
+    uint64_t same = valid;
+    for (int b = 0; (1 << b) < E; ++b) {
+      const uint64_t bm = __ballot((e >> b) & 1);
+      same &= ((e >> b) & 1) ? bm : ~bm;
     }
-    int m = 0, cnt = 0;
-    for (int q = 0; q < P; ++q) {
-      const int eq = __builtin_amdgcn_readlane(e, q);
-      if (eq == e) {
-        cnt += 1;
-        if (q < lane) m += 1;
-      }
+    const int m = __popcll(same & ((1ull << lane) - 1ull));   // members of my expert before me
+    const int cnt = __popcll(same);
+    if (e >= 0 && m == 0) atomicOr(&bits[e >> 5], 1u << (e & 31));   // same wave: LDS ops stay in order
+    int rank = 0;
+    if (e >= 0) {
+      for (int w = 0; w < (e >> 5); ++w) rank += __builtin_popcount(bits[w]);
+      rank += __builtin_popcount(bits[e >> 5] & ((1u << (e & 31)) - 1u));
     }
+    const int nu = __popcll(__ballot(e >= 0 && m == 0));       // ballot with every lane active
     if (lane == 0) g[0] = nu;
     if (e >= 0) {
       g[1 + rank] = e;
@@ -253,7 +250,8 @@ __device__ __forceinline__ void block_group(const int32_t* __restrict__ ids, int
 // Keeps the compiler's scheduler from moving instructions across this point:
 // placed after a kernel has issued all of its loads, so that none is sunk
 // next to its first use (where, behind the weight loads in the in-order
-// vmcnt queue, each would wait for everything issued before it).
+// vmcnt queue, each would wait for everything issued before it), and between
+// independent passes to bound register pressure.
 __device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // --------------------------------------------------------- row streaming
@@ -274,6 +272,17 @@ __device__ __forceinline__ void fetch_subs(RowFetch<QT, SPL>& f, const uint8_t* 
     const int sub = lir + LR * i;
     f.r[i] = gm_load_sub<QT>(row, sub < nsub ? sub : nsub - 1);
   }
+}
+
+// Makes fetched raw weights opaque to the optimiser at this point, so that
+// their decode stays inside a loop instead of being hoisted out of it with
+// every decoded value kept live across iterations.
+template <int QT, int SPL>
+__device__ __forceinline__ void opaque(RowFetch<QT, SPL>& f) {
+  static_assert(sizeof(typename RawSub<QT>::T) % 4 == 0, "raw sub-block is whole dwords");
+  uint32_t* w = reinterpret_cast<uint32_t*>(&f.r[0]);
+#pragma unroll
+  for (int i = 0; i < SPL * (int)sizeof(typename RawSub<QT>::T) / 4; ++i) asm volatile("" : "+v"(w[i]));
 }
 
 // acc[m] += W_row . act[idx[m]] over the fetched sub-blocks, m < nt; act rows

@@ -13,6 +13,7 @@ struct GmDecArgs {
   float* h;         // [T * k][FF], directly followed by hsh
   float* hsh;       // [T][FF]
   float* yp;        // [T * k + T][D] per-pair / shared partial outputs (general path)
+  float* xn;        // [T][D] RMSNorm'd input (general path)
 };
 
 // Weight-row chunk sizes: D and FF in units of 1024 and 512 elements.

@@ -2,8 +2,10 @@
 // qwen/forward.py:563-665 (moe_forward).
 //
 // Stage 1  k_dec_router   router logits (bf16 W, fp32 RMSNorm'd x), the shared
-//                         scalar gate, and the shared expert's gate/up + SwiGLU;
-//                         none of it depends on the routing.
+//                         scalar gate, and (T = 1 kernels) the shared expert's
+//                         gate/up + SwiGLU; none of it depends on the routing.
+//                         For the grouped T > 1 kernels it publishes xn instead
+//                         and the shared expert runs with the routed ones.
 // Stage 2  (moe_decode_gu.hip) top-k, expert grouping, routed gate/up + SwiGLU.
 // Stage 3  (moe_decode_dn.hip) down projections, weighted combine in ascending
 //                         expert order, + sigmoid-gated shared expert (+ x).
@@ -24,7 +26,7 @@ namespace {
 template <int QTS, int NT, int DC>
 __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float* __restrict__ x, int T,
                                                     float* __restrict__ logits, float* __restrict__ shg,
-                                                    float* __restrict__ hsh, int n_rb) {
+                                                    float* __restrict__ hsh, float* __restrict__ xn, int n_rb) {
   constexpr int SPLR = DC > 1 ? DC / 2 : 1;
   constexpr bool IQ3 = QTS == GM_QTYPE_IQ3_XXS;
   extern __shared__ float smem[];
@@ -49,6 +51,15 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
     fetch_subs<GM_QTYPE_BF16, 64, SPLR>(f, wr, lane, nsub);
     issue_fence();
     stage_x_regs<NT, DC>(xr, T, D, P.norm_w, P.norm_eps, xs, red);
+    if (xn != nullptr && blockIdx.x == 0) {                    // publish xn [T][D] for the grouped kernels
+      const int nq = D >> 2;
+      const gm_f32x4* xs4 = reinterpret_cast<const gm_f32x4*>(xs);
+      gm_f32x4* xn4 = reinterpret_cast<gm_f32x4*>(xn);
+      for (int i = threadIdx.x; i < T * nq; i += 256) {
+        const int t = i / nq, c = i - t * nq;
+        xn4[i] = xs4[t * nq + il_index4(c & 7, c >> 3, nsub)];
+      }
+    }
     float acc[NT];
 #pragma unroll
     for (int m = 0; m < NT; ++m) acc[m] = 0.f;
@@ -89,39 +100,38 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
   }
 }
 
+// with_shared: the shared expert's gate/up run here (T = 1 kernels); otherwise
+// they run with the routed experts in k_dec_gateup8 and this kernel publishes xn.
 template <int QTS, int NT, int DC>
-int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s) {
+int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s,
+                    bool with_shared) {
   const int nrows = P->E + (P->sh_gate_inp ? 1 : 0);
   const int n_rb = (nrows + 3) / 4;
-  const int n_sb = P->gate_sh ? (P->FF_sh + 7) / 8 : 0;
+  const int n_sb = P->gate_sh && with_shared ? (P->FF_sh + 7) / 8 : 0;
   const size_t smem = ((size_t)NT * P->D + 4 + 4 * NT) * 4 + (QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
   if (int rc = gm_set_smem(k_dec_router<QTS, NT, DC>, smem)) return rc;
   hipLaunchKernelGGL((k_dec_router<QTS, NT, DC>), dim3(n_rb + n_sb), dim3(256), smem, s, *P, x, T, a.logits, a.shg,
-                     a.hsh, n_rb);
+                     a.hsh, with_shared ? nullptr : a.xn, n_rb);
   GM_TRY(hipGetLastError());
   return GM_OK;
 }
 
 template <int QTS, int NT>
-int launch_router_n(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s) {
+int launch_router_n(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s, bool ws) {
   switch (gm_dec_dc(P->D)) {
-    case 1: return launch_router_t<QTS, NT, 1>(P, x, T, a, s);
-    case 2: return launch_router_t<QTS, NT, 2>(P, x, T, a, s);
-    default: return launch_router_t<QTS, NT, 4>(P, x, T, a, s);
+    case 1: return launch_router_t<QTS, NT, 1>(P, x, T, a, s, ws);
+    case 2: return launch_router_t<QTS, NT, 2>(P, x, T, a, s, ws);
+    default: return launch_router_t<QTS, NT, 4>(P, x, T, a, s, ws);
   }
 }
 
-template <int QTS>
-int launch_router_q(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s) {
-  return T == 1 ? launch_router_n<QTS, 1>(P, x, T, a, s) : launch_router_n<QTS, 8>(P, x, T, a, s);
-}
-
-int launch_router(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s) {
-  if (!P->gate_sh) return launch_router_q<GM_QTYPE_IQ4_XS>(P, x, T, a, s);     // no shared blocks launched
+int launch_router(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s, bool fast1) {
+  if (!fast1) return launch_router_n<GM_QTYPE_IQ4_XS, 8>(P, x, T, a, s, false);   // router rows only
+  if (!P->gate_sh) return launch_router_n<GM_QTYPE_IQ4_XS, 1>(P, x, T, a, s, true);
   switch (P->q_gate_sh) {
-    case GM_QTYPE_IQ4_XS: return launch_router_q<GM_QTYPE_IQ4_XS>(P, x, T, a, s);
-    case GM_QTYPE_IQ3_XXS: return launch_router_q<GM_QTYPE_IQ3_XXS>(P, x, T, a, s);
-    case GM_QTYPE_BF16: return launch_router_q<GM_QTYPE_BF16>(P, x, T, a, s);
+    case GM_QTYPE_IQ4_XS: return launch_router_n<GM_QTYPE_IQ4_XS, 1>(P, x, T, a, s, true);
+    case GM_QTYPE_IQ3_XXS: return launch_router_n<GM_QTYPE_IQ3_XXS, 1>(P, x, T, a, s, true);
+    case GM_QTYPE_BF16: return launch_router_n<GM_QTYPE_BF16, 1>(P, x, T, a, s, true);
     default: return gm_fail_arg("gm_moe_forward: shared gate/up format %d unsupported", P->q_gate_sh);
   }
 }
@@ -144,12 +154,13 @@ int gm_dec_run(const gm_moe_layer* P, const float* x, float* y, int T, int flags
   a.h = reinterpret_cast<float*>(ws + lay.h);
   a.hsh = reinterpret_cast<float*>(ws + lay.hsh);
   a.yp = reinterpret_cast<float*>(ws + lay.yp);
+  a.xn = reinterpret_cast<float*>(ws + lay.xn);
   if (a.hsh != a.h + (size_t)T * P->k * P->FF) return gm_fail_arg("gm_moe_forward: internal workspace layout error");
   // The T = 1 down kernel stages (k + 1) rows of FF activations per block and
   // maps a wave's lanes onto 8 rows x FF/32 sub-blocks (FF/32 in {8, 16, 32}).
   const bool fast1 = T == 1 && (P->FF == 256 || P->FF == 512 || P->FF == 1024);
   if (stage == 0 || stage == 1)
-    if (int rc = launch_router(P, x, T, a, s)) return rc;
+    if (int rc = launch_router(P, x, T, a, s, fast1)) return rc;
   if (stage == 0 || stage == 2)
     if (int rc = gm_dec_gateup(P, x, T, fast1, a, s)) return rc;
   if (stage == 0 || stage == 3)

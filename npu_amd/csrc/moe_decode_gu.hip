@@ -8,8 +8,9 @@
 // for stage 3.
 //
 // T > 1: k_dec_route (one block) runs the per-token top-k and groups the
-// (token, slot) pairs by expert; k_dec_gateup8 then runs (unique expert, 8-row
-// chunk) blocks over the expert's member tokens only.
+// (token, slot) pairs by expert; k_dec_gateup8 then runs (unit, 16-row chunk)
+// blocks, a unit being a unique routed expert over its member tokens only or
+// the shared expert over all T tokens, reading the RMSNorm'd xn of stage 1.
 #include "moe_common.h"
 #include "moe_decode.h"
 
@@ -93,61 +94,116 @@ __global__ void __launch_bounds__(512) k_dec_route(const float* __restrict__ log
   for (int i = threadIdx.x; i < GM_GRP_WORDS; i += blockDim.x) g_grp[i] = grp[i];
 }
 
-// Block = (unique expert u, 8 rows); x rows of the expert's member tokens only.
-template <int QT, int DC>
-__global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const float* __restrict__ x,
-                                                     const int32_t* __restrict__ g_grp, float* __restrict__ h,
-                                                     int n_chunks) {
-  constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
-  extern __shared__ float smem[];
-  float* xs = smem;                                            // [8][D] interleaved (+ 4)
-  float* red = smem + 8 * P.D + 4;                             // [32]
-  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(red + 32);           // IQ3 only
-  const int D = P.D, k = P.k, FF = P.FF, nsub = D / GM_SUB;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int u = blockIdx.x / n_chunks, chunk = blockIdx.x - u * n_chunks;
-  const int nu = g_grp[0];
-  if (u >= nu) return;                                         // uniform per block
-  const int e = g_grp[1 + u];
-  const int nm = g_grp[1 + GM_GRP_MAXU + u];
-  int pair[8], tok[8], idx[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    pair[m] = g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * u + (m < nm ? m : 0)];
-    tok[m] = pair[m] / k;
-    idx[m] = m;
-  }
-  uint32_t gw = 0;
-  if constexpr (IQ3) gw = gm_iq3_tab_load();
+// Rows r0 .. r0 + 8 NP - 1 of one gate/up pair for nm member tokens (xn rows tok[m],
+// h rows dst[m]), members staged MG = 2 at a time in LDS (most routed units
+// have one member; the shared unit takes T / 2 passes).  Block of 256 threads:
+// wave w, pass p -> rows r0 + 8p + 2w + (lane >> 5), 32 lanes per row.
+template <int QT, int DC, int NP>
+__device__ __forceinline__ void gateup_group(const uint8_t* __restrict__ gbase, const uint8_t* __restrict__ ubase,
+                                             int FF, int D, int r0, int nm, const int (&tok)[8], const int (&dst)[8],
+                                             const float* __restrict__ xn, float* __restrict__ xs, uint32_t gw,
+                                             Iq3Tab* __restrict__ tab, float* __restrict__ h) {
+  constexpr int MG = 2;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane & 31, nsub = D / GM_SUB;
   const int64_t rb = gm_row_bytes(QT, D);
-  const int row = chunk * 8 + wave * 2 + (lane >> 5);
-  const bool live = row < FF;
-  const int r = live ? row : 0;
-  RowFetch<QT, DC> fg, fu;
-  fetch_subs<QT, 32, DC>(fg, static_cast<const uint8_t*>(P.gate_exps) + ((int64_t)e * FF + r) * rb, lane & 31, nsub);
-  fetch_subs<QT, 32, DC>(fu, static_cast<const uint8_t*>(P.up_exps) + ((int64_t)e * FF + r) * rb, lane & 31, nsub);
-  XRegs<8, DC> xr;
-  load_x<8, DC>(xr, x, tok, nm, D, P.norm_w);
-  if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
-  stage_x_regs<8, DC>(xr, nm, D, P.norm_w, P.norm_eps, xs, red);
-  float ag[8], au[8];
+  RowFetch<QT, DC> fg[NP], fu[NP];
+  int rows[NP];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) { ag[m] = 0.f; au[m] = 0.f; }
-  dot_subs<QT, 32, DC, 8>(fg, lane & 31, nsub, xs, D, idx, nm, tab, ag);
-  dot_subs<QT, 32, DC, 8>(fu, lane & 31, nsub, xs, D, idx, nm, tab, au);
+  for (int p = 0; p < NP; ++p) {
+    rows[p] = r0 + 8 * p + 2 * wave + (lane >> 5);
+    const int r = rows[p] < FF ? rows[p] : 0;
+    fetch_subs<QT, 32, DC>(fg[p], gbase + r * rb, lir, nsub);
+    fetch_subs<QT, 32, DC>(fu[p], ubase + r * rb, lir, nsub);
+  }
+  for (int g0 = 0; g0 < nm; g0 += MG) {                      // usually one group
+    int gt[MG], idx[MG];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    if (m < nm) {
-      const float hv = gm_silu(row_sum<32>(ag[m])) * row_sum<32>(au[m]);
-      if (live && (lane & 31) == 0) h[(int64_t)pair[m] * FF + row] = hv;
+    for (int m = 0; m < MG; ++m) {
+      int t = tok[0];
+#pragma unroll
+      for (int q = 1; q < 8; ++q) t = g0 + m == q ? tok[q] : t;
+      gt[m] = t;
+      idx[m] = m;
+    }
+    const int ng = nm - g0 < MG ? nm - g0 : MG;
+    XRegs<MG, DC> xr;
+    load_x<MG, DC>(xr, xn, gt, ng, D, nullptr);
+    if (g0 > 0) __syncthreads();                             // previous group's reads are done
+    else if constexpr (QT == GM_QTYPE_IQ3_XXS) gm_iq3_tab_store(gw, tab);
+    stage_x_regs<MG, DC>(xr, ng, D, nullptr, 0.f, xs, nullptr);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      opaque(fg[p]);
+      opaque(fu[p]);
+      float ag[MG], au[MG];
+#pragma unroll
+      for (int m = 0; m < MG; ++m) { ag[m] = 0.f; au[m] = 0.f; }
+      dot_subs<QT, 32, DC, MG>(fg[p], lir, nsub, xs, D, idx, ng, tab, ag);
+      dot_subs<QT, 32, DC, MG>(fu[p], lir, nsub, xs, D, idx, ng, tab, au);
+#pragma unroll
+      for (int m = 0; m < MG; ++m) {
+        if (m < ng) {
+          const float hv = gm_silu(row_sum<32>(ag[m])) * row_sum<32>(au[m]);
+          int d = dst[0];
+#pragma unroll
+          for (int q = 1; q < 8; ++q) d = g0 + m == q ? dst[q] : d;
+          if (rows[p] < FF && lir == 0) h[(int64_t)d * FF + rows[p]] = hv;
+        }
+      }
+      issue_fence();                                           // one pass's decoded rows live at a time
     }
   }
 }
 
+// Block = (unit u, 8 rows).  Units 0 .. nu-1 are the unique routed experts
+// (members from the grouping table), unit nu the shared expert (all T tokens,
+// h rows after the routed ones).  sh_mode 0: routed units, plus the shared
+// unit when its format is QT; sh_mode 1: the shared unit only (its own format).
 template <int QT, int DC>
+__global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const float* __restrict__ xn, int T,
+                                                     const int32_t* __restrict__ g_grp, float* __restrict__ h,
+                                                     int n_chunks, int sh_mode) {
+  constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
+  extern __shared__ float smem[];
+  float* xs = smem;                                            // [2][D] interleaved (+ 4)
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(smem + 2 * P.D + 4); // IQ3 only
+  const int D = P.D, k = P.k, FF = P.FF, Ptot = T * k;
+  const int nu = g_grp[0];
+  const int u = sh_mode ? nu : (int)blockIdx.x / n_chunks;
+  const int chunk = (int)blockIdx.x - (sh_mode ? 0 : u * n_chunks);
+  const bool shared = u == nu;
+  const bool sh_here = P.gate_sh != nullptr && (sh_mode || P.q_gate_sh == QT);
+  if (u > nu || (shared && !sh_here)) return;                  // uniform per block
+  uint32_t gw = 0;
+  if constexpr (IQ3) gw = gm_iq3_tab_load();
+  const int64_t rb = gm_row_bytes(QT, D);
+  const uint8_t* gbase;
+  const uint8_t* ubase;
+  int nm, tok[8], dst[8];
+  if (shared) {
+    gbase = static_cast<const uint8_t*>(P.gate_sh);
+    ubase = static_cast<const uint8_t*>(P.up_sh);
+    nm = T;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) { tok[m] = m < T ? m : 0; dst[m] = Ptot + tok[m]; }
+  } else {
+    const int e = g_grp[1 + u];
+    gbase = static_cast<const uint8_t*>(P.gate_exps) + (int64_t)e * FF * rb;
+    ubase = static_cast<const uint8_t*>(P.up_exps) + (int64_t)e * FF * rb;
+    nm = g_grp[1 + GM_GRP_MAXU + u];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      dst[m] = g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * u + (m < nm ? m : 0)];
+      tok[m] = dst[m] / k;
+    }
+  }
+  gateup_group<QT, DC, 1>(gbase, ubase, FF, D, chunk * 8, nm, tok, dst, xn, xs, gw, tab, h);
+}
+
+template <int QT, int QTS, int DC>
 int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s) {
-  const int n_chunks = (P->FF + 7) / 8;
   if (fast1) {
+    const int n_chunks = (P->FF + 7) / 8;
     const size_t smem = ((size_t)P->D + 4) * 4 + (QT == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
     if (int rc = gm_set_smem(k_dec_gateup1<QT, DC, 4>, smem)) return rc;
     if (int rc = gm_set_smem(k_dec_gateup1<QT, DC, 8>, smem)) return rc;
@@ -165,21 +221,42 @@ int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const Gm
   else
     hipLaunchKernelGGL(k_dec_route<8>, dim3(1), dim3(512), 0, s, a.logits, T, P->E, P->k, a.ids, a.wts, a.grp);
   GM_TRY(hipGetLastError());
-  const int max_u = T * P->k < P->E ? T * P->k : P->E;
-  const size_t smem = (8 * (size_t)P->D + 4 + 32) * 4 + (QT == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
-  if (int rc = gm_set_smem(k_dec_gateup8<QT, DC>, smem)) return rc;
-  hipLaunchKernelGGL((k_dec_gateup8<QT, DC>), dim3(max_u * n_chunks), dim3(256), smem, s, *P, x, a.grp, a.h,
-                     n_chunks);
+  const int n_chunks = (P->FF + 7) / 8;
+  const int max_u = (T * P->k < P->E ? T * P->k : P->E) + 1;      // + the shared expert
+  {
+    const size_t smem = (2 * (size_t)P->D + 4) * 4 + (QT == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+    if (int rc = gm_set_smem(k_dec_gateup8<QT, DC>, smem)) return rc;
+    hipLaunchKernelGGL((k_dec_gateup8<QT, DC>), dim3(max_u * n_chunks), dim3(256), smem, s, *P, a.xn, T, a.grp,
+                       a.h, n_chunks, 0);
+    GM_TRY(hipGetLastError());
+  }
+  if (P->gate_sh && P->q_gate_sh != QT) {                         // shared expert in its own format
+    const size_t smem = (2 * (size_t)P->D + 4) * 4 + (QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+    if (int rc = gm_set_smem(k_dec_gateup8<QTS, DC>, smem)) return rc;
+    hipLaunchKernelGGL((k_dec_gateup8<QTS, DC>), dim3(n_chunks), dim3(256), smem, s, *P, a.xn, T, a.grp, a.h,
+                       n_chunks, 1);
+  }
   GM_TRY(hipGetLastError());
   return GM_OK;
 }
 
-template <int QT>
+template <int QT, int QTS>
 int launch_gu_q(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s) {
   switch (gm_dec_dc(P->D)) {
-    case 1: return launch_gu<QT, 1>(P, x, T, fast1, a, s);
-    case 2: return launch_gu<QT, 2>(P, x, T, fast1, a, s);
-    default: return launch_gu<QT, 4>(P, x, T, fast1, a, s);
+    case 1: return launch_gu<QT, QTS, 1>(P, x, T, fast1, a, s);
+    case 2: return launch_gu<QT, QTS, 2>(P, x, T, fast1, a, s);
+    default: return launch_gu<QT, QTS, 4>(P, x, T, fast1, a, s);
+  }
+}
+
+template <int QT>
+int launch_gu_s(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s) {
+  if (fast1 || !P->gate_sh) return launch_gu_q<QT, QT>(P, x, T, fast1, a, s);   // shared gate/up run in stage 1
+  switch (P->q_gate_sh) {
+    case GM_QTYPE_IQ4_XS: return launch_gu_q<QT, GM_QTYPE_IQ4_XS>(P, x, T, fast1, a, s);
+    case GM_QTYPE_IQ3_XXS: return launch_gu_q<QT, GM_QTYPE_IQ3_XXS>(P, x, T, fast1, a, s);
+    case GM_QTYPE_BF16: return launch_gu_q<QT, GM_QTYPE_BF16>(P, x, T, fast1, a, s);
+    default: return gm_fail_arg("gm_moe_forward: shared gate/up format %d unsupported", P->q_gate_sh);
   }
 }
 
@@ -187,8 +264,8 @@ int launch_gu_q(const gm_moe_layer* P, const float* x, int T, bool fast1, const 
 
 int gm_dec_gateup(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s) {
   switch (P->q_gate) {
-    case GM_QTYPE_IQ4_XS: return launch_gu_q<GM_QTYPE_IQ4_XS>(P, x, T, fast1, a, s);
-    case GM_QTYPE_IQ3_XXS: return launch_gu_q<GM_QTYPE_IQ3_XXS>(P, x, T, fast1, a, s);
+    case GM_QTYPE_IQ4_XS: return launch_gu_s<GM_QTYPE_IQ4_XS>(P, x, T, fast1, a, s);
+    case GM_QTYPE_IQ3_XXS: return launch_gu_s<GM_QTYPE_IQ3_XXS>(P, x, T, fast1, a, s);
     default: return gm_fail_arg("gm_moe_forward: routed gate/up format %d unsupported", P->q_gate);
   }
 }
