@@ -1,33 +1,45 @@
-// MoE block, prefill path (T > 8 tokens): grouped dequant-to-bf16 MFMA GEMMs.
+// MoE block, prefill path (T > 8 tokens): grouped dequant-GEMMs on MFMA.
 //
-//   1. router logits + top-k (router.hip), dispatch: histogram -> exclusive scan
-//      -> stable scatter of (token, slot) pairs by expert (dispatch.hip), plus the
-//      inverse permutation
-//   2. k_pf_segments: split every expert's token list (and the shared expert's,
-//      which takes all T tokens) into segments of <= 64 tokens
-//   3. k_pf_prep_x:   xn = rmsnorm(x) (or x), rounded to bf16
-//   4. k_pf_gateup:   per (segment, 64-row tile): h = silu(G x) * (U x) with the
-//                     weights dequantised to bf16 in registers straight into
-//                     v_mfma_f32_16x16x32_bf16 operands, token tiles staged in LDS;
-//                     h stored as bf16 in expert-sorted row order
-//   5. k_pf_down:     per (segment, 64-row tile): y_pair = Down_e h, fp32
+//   1. k_pf_prep:     xn = rmsnorm(x) (or x) -> three bf16 planes whose sum is
+//                     xn to ~2^-27 (router operand) and an f16 copy (gate/up operand)
+//   2. k_pf_router:   logits = xn W^T (+ bias) and the shared scalar gate on
+//                     v_mfma_f32_16x16x32_bf16, one MFMA per plane: every
+//                     product of a bf16 weight and a bf16 plane is exact in fp32
+//   3. top-k (router.hip), dispatch: histogram -> exclusive scan -> stable
+//      scatter of (token, slot) pairs by expert, plus the inverse permutation
+//      (dispatch.hip); k_pf_segments splits every expert's token list (and the
+//      shared expert's, which takes all T tokens) into segments of <= 64 tokens
+//   4. k_pf_gateup:   per (segment, 64 weight rows): h = silu(G x) * (U x).  The raw
+//                     superblocks are fetched one superblock ahead into registers
+//                     and decoded to f16 integers (kvalue or grid magnitude times
+//                     the integer part of the sub-block scale) straight into
+//                     v_mfma_f32_16x16x32_f16 operands; the superblock's fp16 d
+//                     multiplies the fp32 partial sum of each superblock.  The
+//                     segment's activation tile is double-buffered in LDS.  h is
+//                     stored as bf16 in expert-sorted row order.
+//   5. k_pf_down:     per (segment, 128 weight rows): y_pair = Down_e h on
+//                     v_mfma_f32_16x16x32_bf16 (h keeps bf16's range), fp32 out
 //   6. k_pf_combine:  y[t] = sum over t's experts in ascending id of w * y_pair
 //                     + sigmoid gate * y_shared (+ x); fixed order, no atomics
 //
-// Reference semantics: the CPU loop of qwen/forward.py:622-663 (prefill takes
+// Reference semantics: the CPU loop of qwen/forward.py:563-665 (prefill takes
 // that path in the reference; its NPU kernels are T = 1 only).
 #include "moe_common.h"
 
 using namespace gm_moe;
 
 typedef __bf16 gm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 gm_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 gm_f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 gm_f16x2 __attribute__((ext_vector_type(2)));
+typedef float gm_f32x2 __attribute__((ext_vector_type(2)));
 
 namespace {
 
-constexpr int kSegTok = 64;      // tokens per segment (4 MFMA column tiles)
-constexpr int kRowTile = 64;     // weight rows per block (4 waves x 16)
-constexpr int kChunk = 256;      // K elements staged per step (one superblock column)
-constexpr int kPitch = kChunk + 8;  // bf16 row pitch in LDS (pad against bank conflicts)
+constexpr int kSegTok = 64;         // tokens per segment (4 MFMA column tiles)
+constexpr int kChunk = 256;         // K elements per pipeline step (one superblock column)
+constexpr int kPitchB = 2 * kChunk + 16;   // bytes per LDS activation row (16 B of padding)
+constexpr int kTileB = kSegTok * kPitchB;  // one activation buffer
 
 struct PfWs {
   int32_t* counts;    // [E]
@@ -35,12 +47,22 @@ struct PfWs {
   int32_t* sorted;    // [P]
   int32_t* inv;       // [P]   position of pair p in sorted order
   int32_t* segs;      // [1 + 4 * max_seg]  n_seg, then (expert, start, n, unused)
-  uint16_t* xb;       // [T][D]   bf16 xn
+  uint16_t* xr;       // [3][T][D]  bf16 planes of xn (router operand)
+  uint16_t* xh;       // [T][D]     f16 xn (gate/up operand)
+  float* part;        // [kRouterSplit][T][ldp]  partial router dot products
   uint16_t* hb;       // [P + T][FF]  bf16 SwiGLU rows (sorted pairs, then shared per token)
   float* yp;          // [P + T][D]   fp32 per-pair / shared outputs
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+constexpr int kRouterSplit = 8;   // most K ranges of the router GEMM (partials summed in k_pf_topk)
+
+// K ranges actually used: each must hold an even number of 32-wide k-steps.
+int router_split(int D) { return D % (64 * kRouterSplit) == 0 ? kRouterSplit : 4; }
+
+// Row stride of the router partials: E rows + the shared gate row, padded to 4.
+int router_ld(const gm_moe_layer* L) { return (L->E + 1 + 3) & ~3; }
 
 int max_segments(int T, int k, int E) { return (T * k) / kSegTok + E + (T + kSegTok - 1) / kSegTok + 1; }
 
@@ -54,11 +76,24 @@ PfWs pf_layout(const gm_moe_layer* L, int T, uint8_t* base, size_t* total) {
   w.sorted = reinterpret_cast<int32_t*>(take(P * 4));
   w.inv = reinterpret_cast<int32_t*>(take(P * 4));
   w.segs = reinterpret_cast<int32_t*>(take((1 + 4 * (size_t)max_segments(T, L->k, L->E)) * 4));
-  w.xb = reinterpret_cast<uint16_t*>(take((size_t)T * L->D * 2));
+  w.xr = reinterpret_cast<uint16_t*>(take(3 * (size_t)T * L->D * 2));
+  w.xh = reinterpret_cast<uint16_t*>(take((size_t)T * L->D * 2));
+  w.part = reinterpret_cast<float*>(take((size_t)kRouterSplit * T * router_ld(L) * 4));
   w.hb = reinterpret_cast<uint16_t*>(take((P + T) * (size_t)L->FF * 2));
   w.yp = reinterpret_cast<float*>(take((P + T) * (size_t)L->D * 4));
   if (total) *total = o;
   return w;
+}
+
+// Blocks run on the 8 XCDs round-robin (block b on XCD b % 8).  Segment
+// seg goes to XCD seg % 8 and its nrt row tiles to consecutive slots there,
+// so they share the segment's activation tile in one L2, and the grid's
+// unused tail (it is sized for the most segments the routing can produce)
+// is spread over all XCDs.  Grid size: a multiple of 8 * nrt.
+__device__ __forceinline__ void xcd_tile(int b, int nrt, int& seg, int& rt) {
+  const int slot = b >> 3;
+  seg = (slot / nrt) * 8 + (b & 7);
+  rt = slot - (slot / nrt) * nrt;
 }
 
 // ---------------------------------------------------------------- segments
@@ -91,226 +126,617 @@ __global__ void __launch_bounds__(1024) k_pf_segments(const int32_t* __restrict_
 }
 
 // ---------------------------------------------------------------- prep x
-__global__ void __launch_bounds__(256) k_pf_prep_x(const float* __restrict__ x, int D, const float* __restrict__ norm_w,
-                                                   float eps, uint16_t* __restrict__ xb) {
+// xn = (x * rms) * w (qwen/forward.py:58-61) or x; planes p0 = bf16(xn),
+// p1 = bf16(xn - p0), p2 = bf16(xn - p0 - p1) (each difference exact in fp32);
+// xh = f16(xn).  One block per token.
+__global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, int T, int D,
+                                                 const float* __restrict__ norm_w, float eps,
+                                                 uint16_t* __restrict__ xr, uint16_t* __restrict__ xh) {
   __shared__ float red[4];
   const int t = blockIdx.x;
-  const float* xr = x + (int64_t)t * D;
+  const gm_f32x2* x2 = reinterpret_cast<const gm_f32x2*>(x + (int64_t)t * D);
+  const int n2 = D >> 1;
   float rms = 1.f;
   if (norm_w) {
     float ss = 0.f;
-    for (int i = threadIdx.x; i < D; i += 256) ss = fmaf(xr[i], xr[i], ss);
+    for (int i = threadIdx.x; i < n2; i += 256) { const gm_f32x2 v = x2[i]; ss = fmaf(v.x, v.x, fmaf(v.y, v.y, ss)); }
     ss = gm_wave_sum64(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
-    rms = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)D + eps);
+    rms = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)D + eps);
   }
-  for (int i = threadIdx.x; i < D; i += 256) {
-    const float v = norm_w ? (xr[i] * rms) * norm_w[i] : xr[i];
-    xb[(int64_t)t * D + i] = (uint16_t)gm_f2bf(v);
+  const gm_f32x2* w2 = reinterpret_cast<const gm_f32x2*>(norm_w);
+  uint32_t* p0 = reinterpret_cast<uint32_t*>(xr) + (int64_t)t * n2;
+  uint32_t* p1 = p0 + (int64_t)T * n2;
+  uint32_t* p2 = p1 + (int64_t)T * n2;
+  uint32_t* ph = reinterpret_cast<uint32_t*>(xh) + (int64_t)t * n2;
+  for (int i = threadIdx.x; i < n2; i += 256) {
+    gm_f32x2 v = x2[i];
+    if (norm_w) { const gm_f32x2 w = w2[i]; v.x = (v.x * rms) * w.x; v.y = (v.y * rms) * w.y; }
+    const gm_bf16x2 b0 = __builtin_convertvector(v, gm_bf16x2);
+    const gm_f32x2 r0 = v - __builtin_convertvector(b0, gm_f32x2);
+    const gm_bf16x2 b1 = __builtin_convertvector(r0, gm_bf16x2);
+    const gm_f32x2 r1 = r0 - __builtin_convertvector(b1, gm_f32x2);
+    const gm_bf16x2 b2 = __builtin_convertvector(r1, gm_bf16x2);
+    p0[i] = __builtin_bit_cast(uint32_t, b0);
+    p1[i] = __builtin_bit_cast(uint32_t, b1);
+    p2[i] = __builtin_bit_cast(uint32_t, b2);
+    ph[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, gm_f16x2));
   }
 }
 
-// ------------------------------------------------------- A operand decode
-// MFMA 16x16x32 operand layout: lane l holds 8 values of row (l % 16) at
-// k-slots 8*(l/16) .. 8*(l/16)+7 of the 32-wide step.  Weights and
-// activations must use the same slot -> k map within a sub-block:
-//   IQ3_XXS: slot 8q+i -> k = 8q+i (sign group q, grid points qs[2q], qs[2q+1])
-//   IQ4_XS:  slot 8q+i -> k = 4q+i (i < 4, low nibbles of qs bytes 4q..4q+3)
-//                         k = 16+4q+(i-4) (i >= 4, high nibbles of the same bytes)
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b) { return gm_f2bf(a) | (gm_f2bf(b) << 16); }
+// ---------------------------------------------------------------- router
+// Partial router dot products part[z][t][r] = xn[t] . W[r] over the z-th of
+// gridDim.z equal K ranges (each an even number of k-steps), rows r < E of W and row E = the shared gate vector
+// (qwen/forward.py:599-600, 608).  Block: 64 rows x 64 tokens x one K range;
+// wave w takes tokens 16w .. 16w+15 against the 4 row tiles.  MFMA operand
+// layout (16x16x32): lane l holds row / column l % 16 at k = 8 (l / 16) .. +7.
+// Operands are fetched two k-steps ahead.
+
+__device__ __forceinline__ void router_step(const gm_u32x4 (&a)[4], const gm_u32x4 (&b)[3], gm_f32x4 (&acc)[4]) {
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+      acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gm_bf16x8, a[rt]),
+                                                        __builtin_bit_cast(gm_bf16x8, b[p]), acc[rt], 0, 0, 0);
+}
+
+__global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ w, const uint16_t* __restrict__ wsh,
+                                                   const uint16_t* __restrict__ xr, int T, int D, int E, int ldp,
+                                                   float* __restrict__ part) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
+  const int nrows = E + (wsh ? 1 : 0);
+  const int r0 = blockIdx.x * 64;
+  const int tok = blockIdx.y * 64 + wave * 16 + l16;
+  const int tokc = tok < T ? tok : T - 1;
+  const int kr = D / (int)gridDim.z, k0 = blockIdx.z * kr, nk = kr / 32;
+  const gm_u32x4* arow[4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) {
+    const int row = r0 + rt * 16 + l16;
+    const uint16_t* p = row < E ? w + (int64_t)row * D : (row == E && wsh ? wsh : w);
+    arow[rt] = reinterpret_cast<const gm_u32x4*>(p + k0 + 8 * q);
+  }
+  const int64_t plane = (int64_t)T * D / 8;                     // in 16-byte units
+  const gm_u32x4* brow = reinterpret_cast<const gm_u32x4*>(xr + (int64_t)tokc * D + k0 + 8 * q);
+  gm_f32x4 acc[4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) acc[rt] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+  gm_u32x4 a0[4], b0[3], a1[4], b1[3];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) { a0[rt] = arow[rt][0]; a1[rt] = arow[rt][4]; }
+#pragma unroll
+  for (int p = 0; p < 3; ++p) { b0[p] = brow[p * plane]; b1[p] = brow[p * plane + 4]; }
+  for (int ks = 0; ks < nk; ks += 2) {                          // nk is even
+    const int n0 = (ks + 2 < nk ? ks + 2 : ks) * 4, n1 = (ks + 3 < nk ? ks + 3 : ks + 1) * 4;
+    router_step(a0, b0, acc);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) a0[rt] = arow[rt][n0];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) b0[p] = brow[p * plane + n0];
+    router_step(a1, b1, acc);
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) a1[rt] = arow[rt][n1];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) b1[p] = brow[p * plane + n1];
+  }
+  if (tok >= T) return;
+  float* out = part + ((int64_t)blockIdx.z * T + tok) * ldp;
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) {
+    const int row = r0 + rt * 16 + 4 * q;
+    if (row + 3 < nrows) *reinterpret_cast<gm_f32x4*>(out + row) = acc[rt];
+    else
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (row + i < nrows) out[row + i] = acc[rt][i];
+  }
+}
+
+// One wave per token: logits = sum of the nsplit partials (fixed order)
+// + bias, the shared gate sigmoid, and the top-k (ties -> lower id) with
+// renormalised softmax weights (qwen/forward.py:609-611).
+template <int MAXV>
+__global__ void __launch_bounds__(256) k_pf_topk(const float* __restrict__ part, int ldp, int nsplit, int T, int E, int k,
+                                                 int has_gate, const float* __restrict__ bias,
+                                                 float* __restrict__ logits, float* __restrict__ shg,
+                                                 int32_t* __restrict__ ids, float* __restrict__ wts) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const int64_t zs = (int64_t)T * ldp;
+  const float* pt = part + (int64_t)t * ldp;
+  float v[MAXV];
+  int ix[MAXV];
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    ix[i] = lane + 64 * i;
+    const int r = ix[i] < E ? ix[i] : E - 1;
+    float acc = 0.f;
+#pragma unroll
+    for (int z = 0; z < nsplit; ++z) acc += pt[z * zs + r];
+    v[i] = acc + (bias ? bias[r] : 0.f);
+    if (ix[i] < E) logits[(int64_t)t * E + ix[i]] = v[i];
+  }
+  if (has_gate && lane == 0) {
+    float g = 0.f;
+#pragma unroll
+    for (int z = 0; z < nsplit; ++z) g += pt[z * zs + E];
+    shg[t] = gm_sigmoid(g);
+  }
+  int id;
+  float wt;
+  topk_finish<MAXV>(v, ix, E, k, id, wt);
+  if (lane < k) {
+    ids[(int64_t)t * k + lane] = id;
+    wts[(int64_t)t * k + lane] = wt;
+  }
+}
+
+// ------------------------------------------------------- raw superblocks
+// The bytes of one superblock of one weight row that lane quarter q needs.
+// Lane quarter q covers sub-blocks 2q and 2q+1 of every superblock; k-step j
+// (0..7) of the superblock uses sub-block 2q + (j >> 2).
+template <int QT> struct PfRaw;
+template <> struct PfRaw<GM_QTYPE_IQ4_XS> {
+  uint32_t h0, h1;      // d | scales_h, scales_l[0..3]
+  uint32_t q[8];        // qs bytes 32q .. 32q+31 (sub-blocks 2q, 2q+1)
+};
+template <> struct PfRaw<GM_QTYPE_IQ3_XXS> {
+  uint32_t d;           // fp16 bits
+  uint32_t q[4];        // qs bytes 16q .. 16q+15 (sub-blocks 2q, 2q+1)
+  uint32_t w0, w1;      // scale/sign words 2q, 2q+1
+};
+
+// IQ4_XS superblocks are 8-byte aligned (136 = 8 * 17, rows of whole superblocks).
+__device__ __forceinline__ PfRaw<GM_QTYPE_IQ4_XS> pf_load_iq4(const uint8_t* __restrict__ sb, int q) {
+  PfRaw<GM_QTYPE_IQ4_XS> r;
+  const uint2 h = *reinterpret_cast<const uint2*>(sb);
+  const uint2* p = reinterpret_cast<const uint2*>(sb + 8 + 32 * q);
+  r.h0 = h.x; r.h1 = h.y;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { const uint2 v = p[i]; r.q[2 * i] = v.x; r.q[2 * i + 1] = v.y; }
+  return r;
+}
+
+// IQ3_XXS superblocks are 2-byte aligned (98 B): dword loads re-aligned with
+// v_alignbyte_b32.  Every dword read holds at least one byte of this
+// superblock, so no read leaves the superblock's 4 KB page.
+__device__ __forceinline__ PfRaw<GM_QTYPE_IQ3_XXS> pf_load_iq3(const uint8_t* __restrict__ sb, int q) {
+  PfRaw<GM_QTYPE_IQ3_XXS> r;
+  const int odd = (int)((reinterpret_cast<uintptr_t>(sb) >> 1) & 1);     // sb % 4 == 2 * odd
+  const int rq = odd ? 0 : 2;                                           // (sb + 2) % 4
+  const uint32_t* dp = reinterpret_cast<const uint32_t*>(sb - 2 * odd);
+  const uint32_t dw = dp[0];
+  r.d = odd ? (dw >> 16) : (dw & 0xffffu);
+  const uint32_t* qp = reinterpret_cast<const uint32_t*>(sb + 2 + 16 * q - rq);
+  uint32_t v[5];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = qp[i];
+  v[4] = qp[rq ? 4 : 3];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.q[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], rq);
+  const uint32_t* wp = reinterpret_cast<const uint32_t*>(sb + 66 + 8 * q - rq);
+  const uint32_t w0 = wp[0], w1 = wp[1], w2 = wp[rq ? 2 : 1];
+  r.w0 = __builtin_amdgcn_alignbyte(w1, w0, rq);
+  r.w1 = __builtin_amdgcn_alignbyte(w2, w1, rq);
+  return r;
+}
 
 template <int QT>
-__device__ __forceinline__ gm_bf16x8 decode_a(const uint8_t* __restrict__ sbp, int s, int q,
-                                              const uint32_t* __restrict__ grid) {
-  uint32_t w4[4];
+__device__ __forceinline__ PfRaw<QT> pf_load(const uint8_t* __restrict__ sb, int q) {
+  if constexpr (QT == GM_QTYPE_IQ4_XS) return pf_load_iq4(sb, q);
+  else return pf_load_iq3(sb, q);
+}
+
+// Sub-block scales of the lane's two sub-blocks (2q, 2q+1): the full scale
+// (bf16 path) or, for the f16 path, only its integer factor, with the
+// superblock factor pf_dscale applied to the fp32 accumulator instead:
+//   IQ4_XS: d * (ls - 32)            -> integer ls - 32 in [-32, 31], factor d
+//   IQ3_XXS: d * (0.5 + s4) * 0.5    -> integer 2 s4 + 1 in [1, 31], factor d / 4
+// so every f16 weight is an exact integer (|kv (ls - 32)| <= 4064 rounds at
+// most once, |(2 s4 + 1) g| <= 1922 is exact) and f16's small exponent range
+// never meets a tiny d.
+template <int QT>
+__device__ __forceinline__ gm_f32x2 pf_scales(const PfRaw<QT>& r, int q) {
   if constexpr (QT == GM_QTYPE_IQ4_XS) {
-    const uint2 hdr = *reinterpret_cast<const uint2*>(sbp);
-    const uint32_t qw = *reinterpret_cast<const uint32_t*>(sbp + 8 + 16 * s + 4 * q);
-    const float d = gm_h2f(hdr.x & 0xffffu);
-    const uint32_t sl = (hdr.y >> (8 * (s >> 1) + 4 * (s & 1))) & 15u;
-    const int ls = (int)(sl | (((hdr.x >> 16 >> (2 * s)) & 3u) << 4));
-    const float dl = d * (float)(ls - 32);
-    const uint32_t lo = gm_iq4nl_lut4(qw & 0x0f0f0f0fu);
-    const uint32_t hi = gm_iq4nl_lut4((qw >> 4) & 0x0f0f0f0fu);
-    w4[0] = pk_bf16(dl * gm_sbyte(lo, 0), dl * gm_sbyte(lo, 1));
-    w4[1] = pk_bf16(dl * gm_sbyte(lo, 2), dl * gm_sbyte(lo, 3));
-    w4[2] = pk_bf16(dl * gm_sbyte(hi, 0), dl * gm_sbyte(hi, 1));
-    w4[3] = pk_bf16(dl * gm_sbyte(hi, 2), dl * gm_sbyte(hi, 3));
+    const float d = gm_h2f(r.h0 & 0xffffu);
+    const uint32_t sh = r.h0 >> 16, sl = (r.h1 >> (8 * q)) & 0xffu;
+    const int ls0 = (int)((sl & 15u) | (((sh >> (4 * q)) & 3u) << 4));
+    const int ls1 = (int)((sl >> 4) | (((sh >> (4 * q + 2)) & 3u) << 4));
+    return gm_f32x2{d * (float)(ls0 - 32), d * (float)(ls1 - 32)};
   } else {
-    const uint16_t* h16 = reinterpret_cast<const uint16_t*>(sbp);
-    const float d = gm_h2f(h16[0]);
-    const uint32_t qq = h16[1 + 4 * s + q];                       // qs[8s+2q], qs[8s+2q+1]
-    const uint32_t w = (uint32_t)h16[33 + 2 * s] | ((uint32_t)h16[34 + 2 * s] << 16);
-    const float db = d * (0.5f + (float)(w >> 28)) * 0.5f;
-    const uint32_t ga = grid[qq & 0xffu], gb = grid[qq >> 8];
-    const uint32_t sg = gm_ksigns((w >> (7 * q)) & 127u);
-    float v[8];
+    const float d = gm_h2f(r.d);
+    return gm_f32x2{d * (0.5f + (float)(r.w0 >> 28)) * 0.5f, d * (0.5f + (float)(r.w1 >> 28)) * 0.5f};
+  }
+}
+
+template <int QT>
+__device__ __forceinline__ gm_f32x2 pf_int_scales(const PfRaw<QT>& r, int q) {
+  if constexpr (QT == GM_QTYPE_IQ4_XS) {
+    const uint32_t sh = r.h0 >> 16, sl = (r.h1 >> (8 * q)) & 0xffu;
+    const int ls0 = (int)((sl & 15u) | (((sh >> (4 * q)) & 3u) << 4));
+    const int ls1 = (int)((sl >> 4) | (((sh >> (4 * q + 2)) & 3u) << 4));
+    return gm_f32x2{(float)(ls0 - 32), (float)(ls1 - 32)};
+  } else {
+    return gm_f32x2{(float)(2 * (r.w0 >> 28) + 1), (float)(2 * (r.w1 >> 28) + 1)};
+  }
+}
+
+template <int QT>
+__device__ __forceinline__ float pf_dscale(const PfRaw<QT>& r) {
+  if constexpr (QT == GM_QTYPE_IQ4_XS) return gm_h2f(r.h0 & 0xffffu);
+  else return gm_h2f(r.d) * 0.25f;
+}
+
+// kvalues_iq4nl + 128 as unsigned bytes (entry n in byte n % 4 of word n / 4).
+constexpr uint32_t kKvU[4] = {kGmKv[0] ^ 0x80808080u, kGmKv[1] ^ 0x80808080u, kGmKv[2] ^ 0x80808080u,
+                              kGmKv[3] ^ 0x80808080u};
+
+__device__ __forceinline__ uint32_t lut_kvu(uint32_t nib) {
+  const uint32_t sel = nib & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(kKvU[1], kKvU[0], sel);
+  const uint32_t hi = __builtin_amdgcn_perm(kKvU[3], kKvU[2], sel);
+  return __builtin_amdgcn_perm(hi, lo, ((nib >> 1) & 0x04040404u) | 0x03020100u);
+}
+
+// Four unsigned bytes u -> two f16x2 holding (u - 128) * s exactly-then-once-rounded:
+// 0x6400 | u is the f16 1024 + u, and 1024 + u - 1152 is exact.
+__device__ __forceinline__ void u8x4_to_f16(uint32_t u, gm_f16x2 s, uint32_t& o0, uint32_t& o1) {
+  const gm_f16x2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+  const gm_f16x2 a = __builtin_bit_cast(gm_f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
+  const gm_f16x2 b = __builtin_bit_cast(gm_f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
+  o0 = __builtin_bit_cast(uint32_t, (a - off) * s);
+  o1 = __builtin_bit_cast(uint32_t, (b - off) * s);
+}
+
+// IQ3_XXS sign table for k-step decode: entry i (7-bit ksigns index) holds
+// byte masks (0x00 / 0xff) for the 8 signs of ksigns(i) and the same masks
+// & 0x01 per byte: {signs 0-3, signs 4-7, low bits 0-3, low bits 4-7}.
+__device__ __forceinline__ void pf_stage_signs_u8(gm_u32x4* tab) {
+  for (int i = threadIdx.x; i < 128; i += blockDim.x) {
+    const uint32_t s = gm_ksigns((uint32_t)i);
+    uint32_t m0 = 0, m1 = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float m = gm_ubyte(i < 4 ? ga : gb, i & 3);
-      v[i] = db * (((sg >> i) & 1u) ? -m : m);
+    for (int b = 0; b < 4; ++b) {
+      m0 |= ((s >> b) & 1u) ? 0xffu << (8 * b) : 0u;
+      m1 |= ((s >> (b + 4)) & 1u) ? 0xffu << (8 * b) : 0u;
     }
+    tab[i] = gm_u32x4{m0, m1, m0 & 0x01010101u, m1 & 0x01010101u};
+  }
+}
+
+// Same signs as bf16-pair sign bits: dword p has bit 15 = sign 2p, bit 31 = sign 2p+1.
+__device__ __forceinline__ void pf_stage_signs_bf16(gm_u32x4* tab) {
+  for (int i = threadIdx.x; i < 128; i += blockDim.x) {
+    const uint32_t s = gm_ksigns((uint32_t)i);
+    uint32_t m[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w4[j] = pk_bf16(v[2 * j], v[2 * j + 1]);
+    for (int p = 0; p < 4; ++p) m[p] = (((s >> (2 * p)) & 1u) << 15) | (((s >> (2 * p + 1)) & 1u) << 31);
+    tab[i] = gm_u32x4{m[0], m[1], m[2], m[3]};
   }
-  gm_bf16x8 r;
-  __builtin_memcpy(&r, w4, 16);
-  return r;
 }
 
-// B operand: 8 activations of LDS row `col` at the same slot -> k map.
+// f16 A operand of k-step j: 8 weights (scale folded in) at the lane's k-slots.
+//   IQ4_XS: slot i < 4 -> k = 32s + 4c + i (low nibbles of qs bytes 16s+4c ..+3),
+//           slot i >= 4 -> k = 32s + 16 + 4c + (i - 4) (high nibbles), c = j & 3
+//   IQ3_XXS: slot i -> k = 32s + 8g + i, g = j & 3
+// with s = 2q + (j >> 2).
 template <int QT>
-__device__ __forceinline__ gm_bf16x8 load_b(const uint16_t* __restrict__ xrow, int s, int q) {
-  uint32_t w4[4];
+__device__ __forceinline__ gm_f16x8 a_f16(const PfRaw<QT>& r, int j, gm_f16x2 sc, const uint32_t* __restrict__ grid,
+                                          const gm_u32x4* __restrict__ sgn) {
+  uint32_t o[4];
   if constexpr (QT == GM_QTYPE_IQ4_XS) {
-    const uint2 a = *reinterpret_cast<const uint2*>(xrow + 32 * s + 4 * q);
-    const uint2 b = *reinterpret_cast<const uint2*>(xrow + 32 * s + 16 + 4 * q);
-    w4[0] = a.x; w4[1] = a.y; w4[2] = b.x; w4[3] = b.y;
+    const uint32_t nib = r.q[4 * (j >> 2) + (j & 3)];
+    u8x4_to_f16(lut_kvu(nib & 0x0f0f0f0fu), sc, o[0], o[1]);
+    u8x4_to_f16(lut_kvu((nib >> 4) & 0x0f0f0f0fu), sc, o[2], o[3]);
   } else {
-    const uint4 a = *reinterpret_cast<const uint4*>(xrow + 32 * s + 8 * q);
-    w4[0] = a.x; w4[1] = a.y; w4[2] = a.z; w4[3] = a.w;
+    const int sl = j >> 2, g = j & 3;
+    const uint32_t qw = r.q[2 * sl + (g >> 1)] >> (16 * (g & 1));
+    const uint32_t ga = grid[qw & 0xffu], gb = grid[(qw >> 8) & 0xffu];
+    const uint32_t w = sl ? r.w1 : r.w0;
+    const gm_u32x4 m = sgn[(w >> (7 * g)) & 127u];
+    // signed magnitude + 128 per byte: |v| <= 62, so no byte carries into the next
+    const uint32_t ua = ((ga ^ m.x) + m.z) ^ 0x80808080u;
+    const uint32_t ub = ((gb ^ m.y) + m.w) ^ 0x80808080u;
+    u8x4_to_f16(ua, sc, o[0], o[1]);
+    u8x4_to_f16(ub, sc, o[2], o[3]);
   }
-  gm_bf16x8 r;
-  __builtin_memcpy(&r, w4, 16);
-  return r;
+  return __builtin_bit_cast(gm_f16x8, gm_u32x4{o[0], o[1], o[2], o[3]});
 }
 
-// Stage the segment's activation rows [c0, c0+256) into LDS (zero past n).
-__device__ __forceinline__ void stage_b(uint16_t* __restrict__ lds, const uint16_t* __restrict__ src, int K,
-                                        const int32_t* __restrict__ rows, int n, int c0) {
-  // 64 rows x 256 bf16 = 64 x 32 uint4
-  for (int i = threadIdx.x; i < kSegTok * (kChunk / 8); i += blockDim.x) {
-    const int r = i / (kChunk / 8), c = i % (kChunk / 8);
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (r < n) v = *reinterpret_cast<const uint4*>(src + (int64_t)rows[r] * K + c0 + 8 * c);
-    *reinterpret_cast<uint4*>(lds + r * kPitch + 8 * c) = v;
+// bf16 A operand of k-step j (same k-slot map as a_f16).
+template <int QT>
+__device__ __forceinline__ gm_bf16x8 a_bf16(const PfRaw<QT>& r, int j, float sc, const uint32_t* __restrict__ grid,
+                                            const gm_u32x4* __restrict__ sgn) {
+  gm_f32x2 v[4];
+  uint32_t flip[4] = {0u, 0u, 0u, 0u};
+  if constexpr (QT == GM_QTYPE_IQ4_XS) {
+    const uint32_t nib = r.q[4 * (j >> 2) + (j & 3)];
+    const uint32_t lo = gm_iq4nl_lut4(nib & 0x0f0f0f0fu), hi = gm_iq4nl_lut4((nib >> 4) & 0x0f0f0f0fu);
+    v[0] = gm_f32x2{sc * gm_sbyte(lo, 0), sc * gm_sbyte(lo, 1)};
+    v[1] = gm_f32x2{sc * gm_sbyte(lo, 2), sc * gm_sbyte(lo, 3)};
+    v[2] = gm_f32x2{sc * gm_sbyte(hi, 0), sc * gm_sbyte(hi, 1)};
+    v[3] = gm_f32x2{sc * gm_sbyte(hi, 2), sc * gm_sbyte(hi, 3)};
+  } else {
+    const int sl = j >> 2, g = j & 3;
+    const uint32_t qw = r.q[2 * sl + (g >> 1)] >> (16 * (g & 1));
+    const uint32_t ga = grid[qw & 0xffu], gb = grid[(qw >> 8) & 0xffu];
+    const uint32_t w = sl ? r.w1 : r.w0;
+    const gm_u32x4 m = sgn[(w >> (7 * g)) & 127u];
+    flip[0] = m.x; flip[1] = m.y; flip[2] = m.z; flip[3] = m.w;
+    v[0] = gm_f32x2{sc * gm_ubyte(ga, 0), sc * gm_ubyte(ga, 1)};
+    v[1] = gm_f32x2{sc * gm_ubyte(ga, 2), sc * gm_ubyte(ga, 3)};
+    v[2] = gm_f32x2{sc * gm_ubyte(gb, 0), sc * gm_ubyte(gb, 1)};
+    v[3] = gm_f32x2{sc * gm_ubyte(gb, 2), sc * gm_ubyte(gb, 3)};
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) o[p] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v[p], gm_bf16x2)) ^ flip[p];
+  return __builtin_bit_cast(gm_bf16x8, gm_u32x4{o[0], o[1], o[2], o[3]});
+}
+
+// B operand of k-step j from an LDS activation row: the 8 activations of the
+// lane's k-slots are contiguous (for IQ4_XS the chunk is stored permuted
+// within every 32-element sub-block, see act_store), so one 16-byte read.
+__device__ __forceinline__ gm_u32x4 b_lds(const uint8_t* __restrict__ row, int q, int j) {
+  return *reinterpret_cast<const gm_u32x4*>(row + 2 * (32 * (2 * q + (j >> 2)) + 8 * (j & 3)));
+}
+
+// One superblock column of the gate and up rows against NT token tiles:
+// f16 integer operands into per-superblock partial sums, then the partial
+// sums times the superblock factor of each accumulator row into ag / au.
+template <int QT, int NT>
+__device__ __forceinline__ void gu_superblock(const PfRaw<QT>& wg, const PfRaw<QT>& wu, int q, int l16,
+                                              const uint8_t* __restrict__ xb, const uint32_t* __restrict__ grid,
+                                              const gm_u32x4* __restrict__ sgn, gm_f32x4 (&ag)[4],
+                                              gm_f32x4 (&au)[4]) {
+  const gm_f32x2 sg2 = pf_int_scales<QT>(wg, q), su2 = pf_int_scales<QT>(wu, q);
+  gm_f32x4 pg[NT], pu[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) { pg[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; pu[t] = pg[t]; }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float sgf = j < 4 ? sg2.x : sg2.y, suf = j < 4 ? su2.x : su2.y;
+    const gm_f16x2 sgh = {(_Float16)sgf, (_Float16)sgf}, suh = {(_Float16)suf, (_Float16)suf};
+    const gm_f16x8 A = a_f16<QT>(wg, j, sgh, grid, sgn);
+    const gm_f16x8 U = a_f16<QT>(wu, j, suh, grid, sgn);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const gm_f16x8 B = __builtin_bit_cast(gm_f16x8, b_lds(xb + (t * 16 + l16) * kPitchB, q, j));
+      pg[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, pg[t], 0, 0, 0);
+      pu[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(U, B, pu[t], 0, 0, 0);
+    }
+    issue_fence();                                     // one k-step's operands live at a time
+  }
+  // superblock factors of the 4 accumulator rows 4q + i (held by lanes 4q + i)
+  const float dgl = pf_dscale<QT>(wg), dul = pf_dscale<QT>(wu);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float dg = __shfl(dgl, 4 * q + i, 64), du = __shfl(dul, 4 * q + i, 64);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      ag[t][i] = fmaf(dg, pg[t][i], ag[t][i]);
+      au[t][i] = fmaf(du, pu[t][i], au[t][i]);
+    }
+  }
+}
+
+// One superblock column of two down row tiles against NT token tiles (bf16).
+template <int QT, int NT>
+__device__ __forceinline__ void dn_superblock(const PfRaw<QT>& w0, const PfRaw<QT>& w1, int q, int l16,
+                                              const uint8_t* __restrict__ hbuf, const uint32_t* __restrict__ grid,
+                                              const gm_u32x4* __restrict__ sgn, gm_f32x4 (&acc)[2][4]) {
+  const gm_f32x2 s0 = pf_scales<QT>(w0, q), s1 = pf_scales<QT>(w1, q);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const gm_bf16x8 A0 = a_bf16<QT>(w0, j, j < 4 ? s0.x : s0.y, grid, sgn);
+    const gm_bf16x8 A1 = a_bf16<QT>(w1, j, j < 4 ? s1.x : s1.y, grid, sgn);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const gm_bf16x8 B = __builtin_bit_cast(gm_bf16x8, b_lds(hbuf + (t * 16 + l16) * kPitchB, q, j));
+      acc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B, acc[0][t], 0, 0, 0);
+      acc[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B, acc[1][t], 0, 0, 0);
+    }
+    issue_fence();
+  }
+}
+
+// Activation chunk [c0, c0 + 256) of the segment's rows -> registers: 64 rows x
+// 32 granules of 16 B, 8 per thread (rows past n repeat a valid row; their
+// output columns are never stored).
+struct ActRegs { gm_u32x4 v[8]; };
+
+__device__ __forceinline__ void act_load(ActRegs& a, const uint16_t* __restrict__ src, int K,
+                                         const int32_t* __restrict__ rows, int c0) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int g = threadIdx.x + 256 * i, r = g >> 5, c = g & 31;
+    a.v[i] = *reinterpret_cast<const gm_u32x4*>(src + (int64_t)rows[r] * K + c0 + 8 * c);
+  }
+}
+
+// IQ4 (PERM): within each sub-block, element 4c + i (c < 4, i < 4) goes to
+// slot 8c + i and element 16 + 4c + i to slot 8c + 4 + i, so that the low- and
+// high-nibble halves of a k-step sit side by side.  Granule c (8 elements) of a
+// sub-block: elements 0-3 -> slot 16 (c & 1) + 4 (c >> 1), 4-7 -> that + 8.
+template <bool PERM>
+__device__ __forceinline__ void act_store(const ActRegs& a, uint8_t* __restrict__ buf) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int g = threadIdx.x + 256 * i, r = g >> 5, c = g & 31;
+    uint8_t* row = buf + r * kPitchB;
+    if constexpr (PERM) {
+      const int sub = c >> 2, gc = c & 3;
+      const int slot = 32 * sub + 16 * (gc & 1) + 4 * (gc >> 1);
+      *reinterpret_cast<uint2*>(row + 2 * slot) = make_uint2(a.v[i].x, a.v[i].y);
+      *reinterpret_cast<uint2*>(row + 2 * (slot + 8)) = make_uint2(a.v[i].z, a.v[i].w);
+    } else {
+      *reinterpret_cast<gm_u32x4*>(row + 16 * c) = a.v[i];
+    }
   }
 }
 
 // -------------------------------------------------------------- gate/up
+// Block = (segment, 64 rows of FF); wave w -> rows 16w .. 16w+15 of both the
+// gate and the up matrix, all of the segment's token tiles.
 template <int QT>
-__global__ void __launch_bounds__(256) k_pf_gateup(gm_moe_layer P, const int32_t* __restrict__ segs,
-                                                   const int32_t* __restrict__ offsets,
-                                                   const int32_t* __restrict__ sorted, const uint16_t* __restrict__ xb,
-                                                   uint16_t* __restrict__ hb, int T, int n_row_tiles) {
-  __shared__ uint32_t grid[256];
-  __shared__ int32_t tok_row[kSegTok];
-  __shared__ int32_t out_row[kSegTok];
-  __shared__ __attribute__((aligned(16))) uint16_t xl[kSegTok * kPitch];
-  const int seg = blockIdx.x / n_row_tiles, rt = blockIdx.x - seg * n_row_tiles;
+__global__ void __launch_bounds__(256, 2) k_pf_gateup(gm_moe_layer P, const int32_t* __restrict__ segs,
+                                                      const int32_t* __restrict__ offsets,
+                                                      const int32_t* __restrict__ sorted,
+                                                      const uint16_t* __restrict__ xh, uint16_t* __restrict__ hb,
+                                                      int T, int n_row_tiles) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* xl = smem;                                                   // [2][64][kPitchB]
+  uint32_t* grid = reinterpret_cast<uint32_t*>(smem + 2 * kTileB);      // [256] (IQ3)
+  gm_u32x4* sgn = reinterpret_cast<gm_u32x4*>(grid + 256);              // [128] (IQ3)
+  int32_t* tok_row = reinterpret_cast<int32_t*>(sgn + 128);             // [64]
+  int32_t* out_row = tok_row + kSegTok;                                 // [64]
+  int seg, rt;
+  xcd_tile(blockIdx.x, n_row_tiles, seg, rt);
   if (seg >= segs[0]) return;
   const int e = segs[1 + 4 * seg], start = segs[2 + 4 * seg], n = segs[3 + 4 * seg];
   const int D = P.D, FF = P.FF, k = P.k, E = P.E;
-  const int Ptot = T * k;
   const bool shared = e == E;
-  if constexpr (QT == GM_QTYPE_IQ3_XXS) gm_stage_grid(grid);
+  if constexpr (QT == GM_QTYPE_IQ3_XXS) {
+    gm_stage_grid(grid);
+    pf_stage_signs_u8(sgn);
+  }
   if (threadIdx.x < kSegTok) {
     const int c = threadIdx.x;
     int tr = 0, orow = 0;
     if (c < n) {
-      if (shared) { tr = start + c; orow = Ptot + start + c; }
+      if (shared) { tr = start + c; orow = T * k + start + c; }
       else { const int pos = offsets[e] + start + c; tr = sorted[pos] / k; orow = pos; }
+    } else {
+      tr = shared ? start : sorted[offsets[e] + start] / k;     // a valid row of the segment
     }
     tok_row[c] = tr;
     out_row[c] = orow;
   }
+  __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4, l16 = lane & 15;
-  const int row = rt * kRowTile + wave * 16 + l16;
-  const bool live_row = row < FF;
+  const int row = rt * 64 + wave * 16 + l16;
   const int64_t rb = gm_row_bytes(QT, D);
-  const uint8_t* gbase = shared ? static_cast<const uint8_t*>(P.gate_sh) : static_cast<const uint8_t*>(P.gate_exps) + (int64_t)e * FF * rb;
-  const uint8_t* ubase = shared ? static_cast<const uint8_t*>(P.up_sh) : static_cast<const uint8_t*>(P.up_exps) + (int64_t)e * FF * rb;
-  const uint8_t* grow = gbase + (int64_t)(live_row ? row : 0) * rb;
-  const uint8_t* urow = ubase + (int64_t)(live_row ? row : 0) * rb;
-  const int ntiles = (n + 15) / 16;
+  const uint8_t* gbase = shared ? static_cast<const uint8_t*>(P.gate_sh)
+                                : static_cast<const uint8_t*>(P.gate_exps) + (int64_t)e * FF * rb;
+  const uint8_t* ubase = shared ? static_cast<const uint8_t*>(P.up_sh)
+                                : static_cast<const uint8_t*>(P.up_exps) + (int64_t)e * FF * rb;
+  const uint8_t* grow = gbase + (int64_t)(row < FF ? row : 0) * rb;
+  const uint8_t* urow = ubase + (int64_t)(row < FF ? row : 0) * rb;
+  constexpr int SBB = QT == GM_QTYPE_IQ4_XS ? GM_IQ4XS_BYTES : GM_IQ3XXS_BYTES;
+  const int nsb = D / kChunk, ntiles = (n + 15) >> 4;
   gm_f32x4 ag[4], au[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) { ag[j] = gm_f32x4{0, 0, 0, 0}; au[j] = gm_f32x4{0, 0, 0, 0}; }
-  for (int c0 = 0; c0 < D; c0 += kChunk) {
-    __syncthreads();
-    stage_b(xl, xb, D, tok_row, n, c0);
-    __syncthreads();
-    const int sb = c0 / GM_QK;
-    const uint8_t* gsb = grow + sb * gm_block_bytes(QT);
-    const uint8_t* usb = urow + sb * gm_block_bytes(QT);
-#pragma unroll 2
-    for (int s = 0; s < 8; ++s) {
-      const gm_bf16x8 wg = decode_a<QT>(gsb, s, q, grid);
-      const gm_bf16x8 wu = decode_a<QT>(usb, s, q, grid);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j < ntiles) {
-          const gm_bf16x8 b = load_b<QT>(xl + (j * 16 + l16) * kPitch, s, q);
-          ag[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wg, b, ag[j], 0, 0, 0);
-          au[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wu, b, au[j], 0, 0, 0);
-        }
-      }
+  for (int t = 0; t < 4; ++t) { ag[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; au[t] = ag[t]; }
+  ActRegs xa;
+  act_load(xa, xh, D, tok_row, 0);
+  PfRaw<QT> wg = pf_load<QT>(grow, q), wu = pf_load<QT>(urow, q);
+  act_store<QT == GM_QTYPE_IQ4_XS>(xa, xl);
+  __syncthreads();
+  for (int sb = 0; sb < nsb; ++sb) {
+    const int sn = sb + 1 < nsb ? sb + 1 : sb;                   // next superblock (clamped)
+    act_load(xa, xh, D, tok_row, sn * kChunk);
+    const PfRaw<QT> wgn = pf_load<QT>(grow + sn * SBB, q), wun = pf_load<QT>(urow + sn * SBB, q);
+    const uint8_t* xb = xl + (sb & 1) * kTileB;
+    switch (ntiles) {
+      case 1: gu_superblock<QT, 1>(wg, wu, q, l16, xb, grid, sgn, ag, au); break;
+      case 2: gu_superblock<QT, 2>(wg, wu, q, l16, xb, grid, sgn, ag, au); break;
+      case 3: gu_superblock<QT, 3>(wg, wu, q, l16, xb, grid, sgn, ag, au); break;
+      default: gu_superblock<QT, 4>(wg, wu, q, l16, xb, grid, sgn, ag, au); break;
     }
+    if (sb + 1 < nsb) act_store<QT == GM_QTYPE_IQ4_XS>(xa, xl + ((sb + 1) & 1) * kTileB);
+    wg = wgn;
+    wu = wun;
+    __syncthreads();
   }
-  // C layout: lane l holds rows 4*(l/16)+i (i = 0..3) of the 16-row tile, column l % 16
-  const int r0 = rt * kRowTile + wave * 16 + 4 * q;
+  // C layout: lane l holds rows 4 (l / 16) + i of the 16-row tile, column l % 16
+  const int r0 = rt * 64 + wave * 16 + 4 * q;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = j * 16 + l16;
-    if (j < ntiles && col < n && r0 < FF) {
-      uint32_t h01 = pk_bf16(gm_silu(ag[j][0]) * au[j][0], gm_silu(ag[j][1]) * au[j][1]);
-      uint32_t h23 = pk_bf16(gm_silu(ag[j][2]) * au[j][2], gm_silu(ag[j][3]) * au[j][3]);
-      *reinterpret_cast<uint2*>(hb + (int64_t)out_row[col] * FF + r0) = make_uint2(h01, h23);
+  for (int t = 0; t < 4; ++t) {
+    const int col = t * 16 + l16;
+    if (t < ntiles && col < n && r0 < FF) {
+      gm_f32x2 h01 = {gm_silu(ag[t][0]) * au[t][0], gm_silu(ag[t][1]) * au[t][1]};
+      gm_f32x2 h23 = {gm_silu(ag[t][2]) * au[t][2], gm_silu(ag[t][3]) * au[t][3]};
+      *reinterpret_cast<uint2*>(hb + (int64_t)out_row[col] * FF + r0) =
+          make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(h01, gm_bf16x2)),
+                     __builtin_bit_cast(uint32_t, __builtin_convertvector(h23, gm_bf16x2)));
     }
   }
 }
 
 // ------------------------------------------------------------------ down
+// Block = (segment, 128 rows of D); wave w -> row tiles 2w, 2w+1 (16 rows each).
 template <int QT>
-__global__ void __launch_bounds__(256) k_pf_down(gm_moe_layer P, const int32_t* __restrict__ segs,
-                                                 const int32_t* __restrict__ offsets, const uint16_t* __restrict__ hb,
-                                                 float* __restrict__ yp, int T, int n_row_tiles) {
-  __shared__ uint32_t grid[256];
-  __shared__ int32_t in_row[kSegTok];
-  __shared__ __attribute__((aligned(16))) uint16_t hl[kSegTok * kPitch];
-  const int seg = blockIdx.x / n_row_tiles, rt = blockIdx.x - seg * n_row_tiles;
+__global__ void __launch_bounds__(256, 2) k_pf_down(gm_moe_layer P, const int32_t* __restrict__ segs,
+                                                    const int32_t* __restrict__ offsets,
+                                                    const uint16_t* __restrict__ hb, float* __restrict__ yp, int T,
+                                                    int n_row_tiles) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* hl = smem;                                                   // [2][64][kPitchB]
+  uint32_t* grid = reinterpret_cast<uint32_t*>(smem + 2 * kTileB);
+  gm_u32x4* sgn = reinterpret_cast<gm_u32x4*>(grid + 256);
+  int32_t* in_row = reinterpret_cast<int32_t*>(sgn + 128);
+  int seg, rt;
+  xcd_tile(blockIdx.x, n_row_tiles, seg, rt);
   if (seg >= segs[0]) return;
   const int e = segs[1 + 4 * seg], start = segs[2 + 4 * seg], n = segs[3 + 4 * seg];
   const int D = P.D, FF = P.FF, k = P.k, E = P.E;
   const bool shared = e == E;
-  const int row0 = shared ? T * k + start : offsets[e] + start;    // rows of hb / yp
-  if constexpr (QT == GM_QTYPE_IQ3_XXS) gm_stage_grid(grid);
-  if (threadIdx.x < kSegTok) in_row[threadIdx.x] = row0 + (threadIdx.x < n ? threadIdx.x : 0);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4, l16 = lane & 15;
-  const int row = rt * kRowTile + wave * 16 + l16;
-  const bool live_row = row < D;
-  const int64_t rb = gm_row_bytes(QT, FF);
-  const uint8_t* base = shared ? static_cast<const uint8_t*>(P.down_sh) : static_cast<const uint8_t*>(P.down_exps) + (int64_t)e * D * rb;
-  const uint8_t* wrow = base + (int64_t)(live_row ? row : 0) * rb;
-  const int ntiles = (n + 15) / 16;
-  gm_f32x4 acc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = gm_f32x4{0, 0, 0, 0};
-  for (int c0 = 0; c0 < FF; c0 += kChunk) {
-    __syncthreads();
-    stage_b(hl, hb, FF, in_row, n, c0);
-    __syncthreads();
-    const uint8_t* sbp = wrow + (c0 / GM_QK) * gm_block_bytes(QT);
-#pragma unroll 2
-    for (int s = 0; s < 8; ++s) {
-      const gm_bf16x8 w = decode_a<QT>(sbp, s, q, grid);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j < ntiles) {
-          const gm_bf16x8 b = load_b<QT>(hl + (j * 16 + l16) * kPitch, s, q);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, b, acc[j], 0, 0, 0);
-        }
-      }
-    }
+  const int row0 = shared ? T * k + start : offsets[e] + start;        // rows of hb / yp
+  if constexpr (QT == GM_QTYPE_IQ3_XXS) {
+    gm_stage_grid(grid);
+    pf_stage_signs_bf16(sgn);
   }
-  const int r0 = rt * kRowTile + wave * 16 + 4 * q;
+  if (threadIdx.x < kSegTok) in_row[threadIdx.x] = row0 + (threadIdx.x < n ? threadIdx.x : 0);
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, q = lane >> 4, l16 = lane & 15;
+  const int64_t rb = gm_row_bytes(QT, FF);
+  const uint8_t* base = shared ? static_cast<const uint8_t*>(P.down_sh)
+                               : static_cast<const uint8_t*>(P.down_exps) + (int64_t)e * D * rb;
+  const uint8_t* wrow[2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = j * 16 + l16;
-    if (j < ntiles && col < n && r0 < D)
-      *reinterpret_cast<float4*>(yp + (int64_t)(row0 + col) * D + r0) =
-          make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+  for (int m = 0; m < 2; ++m) {
+    const int row = rt * 128 + wave * 32 + m * 16 + l16;
+    wrow[m] = base + (int64_t)(row < D ? row : 0) * rb;
+  }
+  constexpr int SBB = QT == GM_QTYPE_IQ4_XS ? GM_IQ4XS_BYTES : GM_IQ3XXS_BYTES;
+  const int nsb = FF / kChunk, ntiles = (n + 15) >> 4;
+  gm_f32x4 acc[2][4];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[m][t] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+  ActRegs ha;
+  act_load(ha, hb, FF, in_row, 0);
+  PfRaw<QT> w0 = pf_load<QT>(wrow[0], q), w1 = pf_load<QT>(wrow[1], q);
+  act_store<QT == GM_QTYPE_IQ4_XS>(ha, hl);
+  __syncthreads();
+  for (int sb = 0; sb < nsb; ++sb) {
+    const int sn = sb + 1 < nsb ? sb + 1 : sb;
+    act_load(ha, hb, FF, in_row, sn * kChunk);
+    const PfRaw<QT> w0n = pf_load<QT>(wrow[0] + sn * SBB, q), w1n = pf_load<QT>(wrow[1] + sn * SBB, q);
+    const uint8_t* hbuf = hl + (sb & 1) * kTileB;
+    switch (ntiles) {
+      case 1: dn_superblock<QT, 1>(w0, w1, q, l16, hbuf, grid, sgn, acc); break;
+      case 2: dn_superblock<QT, 2>(w0, w1, q, l16, hbuf, grid, sgn, acc); break;
+      case 3: dn_superblock<QT, 3>(w0, w1, q, l16, hbuf, grid, sgn, acc); break;
+      default: dn_superblock<QT, 4>(w0, w1, q, l16, hbuf, grid, sgn, acc); break;
+    }
+    if (sb + 1 < nsb) act_store<QT == GM_QTYPE_IQ4_XS>(ha, hl + ((sb + 1) & 1) * kTileB);
+    w0 = w0n;
+    w1 = w1n;
+    __syncthreads();
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int r0 = rt * 128 + wave * 32 + m * 16 + 4 * q;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int col = t * 16 + l16;
+      if (t < ntiles && col < n && r0 < D)
+        *reinterpret_cast<gm_f32x4*>(yp + (int64_t)(row0 + col) * D + r0) = acc[m][t];
+    }
   }
 }
 
@@ -341,19 +767,32 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ x,
     }
   }
   const float sg = has_sh ? shg[t] : 0.f;
-  const int Ptot = T * k;
-  for (int d = threadIdx.x; d < D; d += 256) {
-    float acc = 0.f;
+  const int Ptot = T * k, nq = D >> 2;
+  const gm_f32x4* yp4 = reinterpret_cast<const gm_f32x4*>(yp);
+  for (int c = threadIdx.x; c < nq; c += 256) {
+    gm_f32x4 v[9];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = yp4[(int64_t)(j < k ? pos[j] : pos[0]) * nq + c];
+    v[8] = yp4[(int64_t)(has_sh ? Ptot + t : pos[0]) * nq + c];
+    gm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (j < k) acc = fmaf(w[j], yp[(int64_t)pos[j] * D + d], acc);
-    if (has_sh) acc += sg * yp[(int64_t)(Ptot + t) * D + d];
-    if (flags & GM_MOE_RESIDUAL) acc = x[(int64_t)t * D + d] + acc;
-    y[(int64_t)t * D + d] = acc;
+      if (j < k) {
+        acc.x = fmaf(w[j], v[j].x, acc.x); acc.y = fmaf(w[j], v[j].y, acc.y);
+        acc.z = fmaf(w[j], v[j].z, acc.z); acc.w = fmaf(w[j], v[j].w, acc.w);
+      }
+    if (has_sh) { acc.x += sg * v[8].x; acc.y += sg * v[8].y; acc.z += sg * v[8].z; acc.w += sg * v[8].w; }
+    if (flags & GM_MOE_RESIDUAL) {
+      const gm_f32x4 xv = reinterpret_cast<const gm_f32x4*>(x + (int64_t)t * D)[c];
+      acc.x = xv.x + acc.x; acc.y = xv.y + acc.y; acc.z = xv.z + acc.z; acc.w = xv.w + acc.w;
+    }
+    reinterpret_cast<gm_f32x4*>(y + (int64_t)t * D)[c] = acc;
   }
 }
 
-template <int QTG, int QTD, int QTSG, int QTSD>
+constexpr size_t kGemmSmem = 2 * (size_t)kTileB + 256 * 4 + 128 * 16 + 2 * kSegTok * 4;
+
+template <int QTG, int QTD>
 int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws, const GmMoeWs& lay,
               hipStream_t s) {
   const int D = L->D, FF = L->FF, E = L->E, k = L->k;
@@ -363,24 +802,38 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
   float* wts = reinterpret_cast<float*>(ws + lay.wts);
   PfWs w = pf_layout(L, T, ws + lay.pre, nullptr);
   const bool has_sh = L->gate_sh != nullptr;
-  if (int rc = gm_launch_router(L->router, L->router_bias, x, T, D, E, L->sh_gate_inp, L->norm_w, L->norm_eps,
-                                logits, shg, s)) return rc;
-  if (int rc = gm_launch_topk(logits, T, E, k, ids, wts, s)) return rc;
+  const int nrows = E + (L->sh_gate_inp ? 1 : 0);
+  hipLaunchKernelGGL(k_pf_prep, dim3(T), dim3(256), 0, s, x, T, D, L->norm_w, L->norm_eps, w.xr, w.xh);
+  GM_TRY(hipGetLastError());
+  const int ldp = router_ld(L);
+  const int nsplit = router_split(D);
+  hipLaunchKernelGGL(k_pf_router, dim3((nrows + 63) / 64, (T + 63) / 64, nsplit), dim3(256), 0, s, L->router,
+                     L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
+  GM_TRY(hipGetLastError());
+  if (E <= 256)
+    hipLaunchKernelGGL(k_pf_topk<4>, dim3((T + 3) / 4), dim3(256), 0, s, w.part, ldp, nsplit, T, E, k,
+                       L->sh_gate_inp ? 1 : 0, L->router_bias, logits, shg, ids, wts);
+  else
+    hipLaunchKernelGGL(k_pf_topk<8>, dim3((T + 3) / 4), dim3(256), 0, s, w.part, ldp, nsplit, T, E, k,
+                       L->sh_gate_inp ? 1 : 0, L->router_bias, logits, shg, ids, wts);
+  GM_TRY(hipGetLastError());
   if (int rc = gm_launch_dispatch_inv(ids, T, k, E, w.counts, w.offsets, w.sorted, w.inv, s)) return rc;
   hipLaunchKernelGGL(k_pf_segments, dim3(1), dim3(1024), 0, s, w.counts, E, T, has_sh ? 1 : 0, w.segs);
   GM_TRY(hipGetLastError());
-  hipLaunchKernelGGL(k_pf_prep_x, dim3(T), dim3(256), 0, s, x, D, L->norm_w, L->norm_eps, w.xb);
-  GM_TRY(hipGetLastError());
   const int nseg = max_segments(T, k, E);
   {
-    const int nrt = (FF + kRowTile - 1) / kRowTile;
-    hipLaunchKernelGGL(k_pf_gateup<QTG>, dim3(nseg * nrt), dim3(256), 0, s, *L, w.segs, w.offsets, w.sorted, w.xb,
+    const int nrt = FF / 64;
+    const int nb = (nseg + 7) / 8 * 8 * nrt;
+    if (int rc = gm_set_smem(k_pf_gateup<QTG>, kGemmSmem)) return rc;
+    hipLaunchKernelGGL(k_pf_gateup<QTG>, dim3(nb), dim3(256), kGemmSmem, s, *L, w.segs, w.offsets, w.sorted, w.xh,
                        w.hb, T, nrt);
     GM_TRY(hipGetLastError());
   }
   {
-    const int nrt = (D + kRowTile - 1) / kRowTile;
-    hipLaunchKernelGGL(k_pf_down<QTD>, dim3(nseg * nrt), dim3(256), 0, s, *L, w.segs, w.offsets, w.hb, w.yp, T, nrt);
+    const int nrt = (D + 127) / 128;
+    const int nb = (nseg + 7) / 8 * 8 * nrt;
+    if (int rc = gm_set_smem(k_pf_down<QTD>, kGemmSmem)) return rc;
+    hipLaunchKernelGGL(k_pf_down<QTD>, dim3(nb), dim3(256), kGemmSmem, s, *L, w.segs, w.offsets, w.hb, w.yp, T, nrt);
     GM_TRY(hipGetLastError());
   }
   hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(256), 0, s, x, w.yp, w.inv, wts, shg, T, k, D, has_sh ? 1 : 0,
@@ -397,21 +850,17 @@ size_t gm_prefill_scratch_bytes(const gm_moe_layer* L, int T) {
   return total;
 }
 
-int gm_pf_run(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
-                   const GmMoeWs& lay, hipStream_t s) {
+int gm_pf_run(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws, const GmMoeWs& lay,
+              hipStream_t s) {
   if (L->gate_sh && (L->q_gate_sh != L->q_gate || L->q_down_sh != L->q_down))
     return gm_fail_arg("gm_moe_forward: the prefill path needs the shared expert in the routed formats"),
            GM_EUNSUPPORTED;
   if (L->D % kChunk || L->FF % kChunk)
     return gm_fail_arg("gm_moe_forward: prefill needs D and FF multiples of %d", kChunk);
   const int qg = L->q_gate, qd = L->q_down;
-  if (qg == GM_QTYPE_IQ4_XS && qd == GM_QTYPE_IQ3_XXS)
-    return prefill_t<GM_QTYPE_IQ4_XS, GM_QTYPE_IQ3_XXS, 0, 0>(L, x, y, T, flags, ws, lay, s);
-  if (qg == GM_QTYPE_IQ3_XXS && qd == GM_QTYPE_IQ4_XS)
-    return prefill_t<GM_QTYPE_IQ3_XXS, GM_QTYPE_IQ4_XS, 0, 0>(L, x, y, T, flags, ws, lay, s);
-  if (qg == GM_QTYPE_IQ4_XS && qd == GM_QTYPE_IQ4_XS)
-    return prefill_t<GM_QTYPE_IQ4_XS, GM_QTYPE_IQ4_XS, 0, 0>(L, x, y, T, flags, ws, lay, s);
-  if (qg == GM_QTYPE_IQ3_XXS && qd == GM_QTYPE_IQ3_XXS)
-    return prefill_t<GM_QTYPE_IQ3_XXS, GM_QTYPE_IQ3_XXS, 0, 0>(L, x, y, T, flags, ws, lay, s);
+  if (qg == GM_QTYPE_IQ4_XS && qd == GM_QTYPE_IQ3_XXS) return prefill_t<GM_QTYPE_IQ4_XS, GM_QTYPE_IQ3_XXS>(L, x, y, T, flags, ws, lay, s);
+  if (qg == GM_QTYPE_IQ3_XXS && qd == GM_QTYPE_IQ4_XS) return prefill_t<GM_QTYPE_IQ3_XXS, GM_QTYPE_IQ4_XS>(L, x, y, T, flags, ws, lay, s);
+  if (qg == GM_QTYPE_IQ4_XS && qd == GM_QTYPE_IQ4_XS) return prefill_t<GM_QTYPE_IQ4_XS, GM_QTYPE_IQ4_XS>(L, x, y, T, flags, ws, lay, s);
+  if (qg == GM_QTYPE_IQ3_XXS && qd == GM_QTYPE_IQ3_XXS) return prefill_t<GM_QTYPE_IQ3_XXS, GM_QTYPE_IQ3_XXS>(L, x, y, T, flags, ws, lay, s);
   return gm_fail_arg("gm_moe_forward: unsupported routed formats gate/up %d down %d", qg, qd);
 }
