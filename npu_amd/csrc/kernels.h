@@ -48,5 +48,9 @@ int gm_pf_run(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
                    const GmMoeWs& lay, hipStream_t s);
 int gm_launch_dispatch(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
                        int32_t* sorted_pairs, hipStream_t s);
-int gm_launch_dispatch_inv(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
-                           int32_t* sorted_pairs, int32_t* inv, hipStream_t s);
+// Dispatch plus (inv != NULL) the inverse permutation and (segs != NULL) the
+// segment list: segs[0] = count, then (unit, start, n, 0) per segment of at
+// most seg_tok pairs; unit E is a shared unit of shared_T tokens (0: none).
+int gm_launch_dispatch_seg(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
+                           int32_t* sorted_pairs, int32_t* inv, int32_t* segs, int seg_tok, int shared_T,
+                           hipStream_t s);

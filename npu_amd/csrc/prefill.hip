@@ -5,10 +5,10 @@
 //   2. k_pf_router:   logits = xn W^T (+ bias) and the shared scalar gate on
 //                     v_mfma_f32_16x16x32_bf16, one MFMA per plane: every
 //                     product of a bf16 weight and a bf16 plane is exact in fp32
-//   3. top-k (router.hip), dispatch: histogram -> exclusive scan -> stable
-//      scatter of (token, slot) pairs by expert, plus the inverse permutation
-//      (dispatch.hip); k_pf_segments splits every expert's token list (and the
-//      shared expert's, which takes all T tokens) into segments of <= 64 tokens
+//   3. k_pf_topk sums the router partials, then dispatch (dispatch.hip):
+//      histogram -> exclusive scan -> stable scatter of (token, slot) pairs by
+//      expert, the inverse permutation, and every expert's token list (and the
+//      shared expert's, which takes all T tokens) cut into segments of <= 64
 //   4. k_pf_gateup:   per (segment, 64 weight rows): h = silu(G x) * (U x).  The raw
 //                     superblocks are fetched one superblock ahead into registers
 //                     and decoded to f16 integers (kvalue or grid magnitude times
@@ -17,8 +17,9 @@
 //                     multiplies the fp32 partial sum of each superblock.  The
 //                     segment's activation tile is double-buffered in LDS.  h is
 //                     stored as bf16 in expert-sorted row order.
-//   5. k_pf_down:     per (segment, 128 weight rows): y_pair = Down_e h on
-//                     v_mfma_f32_16x16x32_bf16 (h keeps bf16's range), fp32 out
+//   5. k_pf_down:     per (segment, 256 weight rows): y_pair = Down_e h on
+//                     v_mfma_f32_16x16x32_bf16 (h keeps bf16's range), fp32 out;
+//                     the segment's h tile is staged in LDS once per block
 //   6. k_pf_combine:  y[t] = sum over t's experts in ascending id of w * y_pair
 //                     + sigmoid gate * y_shared (+ x); fixed order, no atomics
 //
@@ -94,35 +95,6 @@ __device__ __forceinline__ void xcd_tile(int b, int nrt, int& seg, int& rt) {
   const int slot = b >> 3;
   seg = (slot / nrt) * 8 + (b & 7);
   rt = slot - (slot / nrt) * nrt;
-}
-
-// ---------------------------------------------------------------- segments
-__global__ void __launch_bounds__(1024) k_pf_segments(const int32_t* __restrict__ counts, int E, int T, int shared,
-                                                      int32_t* __restrict__ segs) {
-  __shared__ int32_t nseg[1024 + 1];
-  __shared__ int32_t base[1024 + 1];
-  const int n_units = E + (shared ? 1 : 0);
-  for (int u = threadIdx.x; u < n_units; u += blockDim.x) {
-    const int n = u < E ? counts[u] : T;
-    nseg[u] = (n + kSegTok - 1) / kSegTok;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {            // n_units <= 513: a serial scan is cheap
-    int run = 0;
-    for (int u = 0; u < n_units; ++u) { base[u] = run; run += nseg[u]; }
-    segs[0] = run;
-  }
-  __syncthreads();
-  for (int u = threadIdx.x; u < n_units; u += blockDim.x) {
-    const int n = u < E ? counts[u] : T;
-    for (int j = 0; j < nseg[u]; ++j) {
-      int32_t* s = segs + 1 + 4 * (base[u] + j);
-      s[0] = u;
-      s[1] = j * kSegTok;
-      s[2] = min(kSegTok, n - j * kSegTok);
-      s[3] = 0;
-    }
-  }
 }
 
 // ---------------------------------------------------------------- prep x
@@ -507,7 +479,7 @@ __device__ __forceinline__ void gu_superblock(const PfRaw<QT>& wg, const PfRaw<Q
       pg[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, pg[t], 0, 0, 0);
       pu[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(U, B, pu[t], 0, 0, 0);
     }
-    issue_fence();                                     // one k-step's operands live at a time
+    if (j & 1) issue_fence();                          // two k-steps' operands live at a time
   }
   // superblock factors of the 4 accumulator rows 4q + i (held by lanes 4q + i)
   const float dgl = pf_dscale<QT>(wg), dul = pf_dscale<QT>(wu);
@@ -525,8 +497,9 @@ __device__ __forceinline__ void gu_superblock(const PfRaw<QT>& wg, const PfRaw<Q
 // One superblock column of two down row tiles against NT token tiles (bf16).
 template <int QT, int NT>
 __device__ __forceinline__ void dn_superblock(const PfRaw<QT>& w0, const PfRaw<QT>& w1, int q, int l16,
-                                              const uint8_t* __restrict__ hbuf, const uint32_t* __restrict__ grid,
-                                              const gm_u32x4* __restrict__ sgn, gm_f32x4 (&acc)[2][4]) {
+                                              const uint8_t* __restrict__ hbuf, int pitch,
+                                              const uint32_t* __restrict__ grid, const gm_u32x4* __restrict__ sgn,
+                                              gm_f32x4 (&acc)[2][4]) {
   const gm_f32x2 s0 = pf_scales<QT>(w0, q), s1 = pf_scales<QT>(w1, q);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -534,11 +507,11 @@ __device__ __forceinline__ void dn_superblock(const PfRaw<QT>& w0, const PfRaw<Q
     const gm_bf16x8 A1 = a_bf16<QT>(w1, j, j < 4 ? s1.x : s1.y, grid, sgn);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const gm_bf16x8 B = __builtin_bit_cast(gm_bf16x8, b_lds(hbuf + (t * 16 + l16) * kPitchB, q, j));
+      const gm_bf16x8 B = __builtin_bit_cast(gm_bf16x8, b_lds(hbuf + (t * 16 + l16) * pitch, q, j));
       acc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B, acc[0][t], 0, 0, 0);
       acc[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B, acc[1][t], 0, 0, 0);
     }
-    issue_fence();
+    if (j & 1) issue_fence();
   }
 }
 
@@ -561,11 +534,11 @@ __device__ __forceinline__ void act_load(ActRegs& a, const uint16_t* __restrict_
 // high-nibble halves of a k-step sit side by side.  Granule c (8 elements) of a
 // sub-block: elements 0-3 -> slot 16 (c & 1) + 4 (c >> 1), 4-7 -> that + 8.
 template <bool PERM>
-__device__ __forceinline__ void act_store(const ActRegs& a, uint8_t* __restrict__ buf) {
+__device__ __forceinline__ void act_store(const ActRegs& a, uint8_t* __restrict__ buf, int pitch = kPitchB) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int g = threadIdx.x + 256 * i, r = g >> 5, c = g & 31;
-    uint8_t* row = buf + r * kPitchB;
+    uint8_t* row = buf + r * pitch;
     if constexpr (PERM) {
       const int sub = c >> 2, gc = c & 3;
       const int slot = 32 * sub + 16 * (gc & 1) + 4 * (gc >> 1);
@@ -666,19 +639,23 @@ __global__ void __launch_bounds__(256, 2) k_pf_gateup(gm_moe_layer P, const int3
 }
 
 // ------------------------------------------------------------------ down
-// Block = (segment, 128 rows of D); wave w -> row tiles 2w, 2w+1 (16 rows each).
-template <int QT>
-__global__ void __launch_bounds__(256, 2) k_pf_down(gm_moe_layer P, const int32_t* __restrict__ segs,
+// Block = (segment, rg_per_blk groups of 128 rows of D).  The segment's whole
+// h tile (64 rows x FF, FF = 256 NSB) is staged in LDS once; the block then
+// walks its row groups with the next group's raw superblocks in flight.
+// Wave w -> row tiles 2w, 2w+1 (16 rows each) of a group.
+template <int QT, int NSB>
+__global__ void __launch_bounds__(256, NSB == 4 ? 1 : 2) k_pf_down(gm_moe_layer P, const int32_t* __restrict__ segs,
                                                     const int32_t* __restrict__ offsets,
                                                     const uint16_t* __restrict__ hb, float* __restrict__ yp, int T,
-                                                    int n_row_tiles) {
+                                                    int n_blk, int rg_per_blk) {
+  constexpr int PITCH = NSB * 2 * kChunk + 16;                          // bytes per LDS h row
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* hl = smem;                                                   // [2][64][kPitchB]
-  uint32_t* grid = reinterpret_cast<uint32_t*>(smem + 2 * kTileB);
+  uint8_t* hl = smem;                                                   // [64][PITCH]
+  uint32_t* grid = reinterpret_cast<uint32_t*>(smem + kSegTok * PITCH);
   gm_u32x4* sgn = reinterpret_cast<gm_u32x4*>(grid + 256);
   int32_t* in_row = reinterpret_cast<int32_t*>(sgn + 128);
-  int seg, rt;
-  xcd_tile(blockIdx.x, n_row_tiles, seg, rt);
+  int seg, bi;
+  xcd_tile(blockIdx.x, n_blk, seg, bi);
   if (seg >= segs[0]) return;
   const int e = segs[1 + 4 * seg], start = segs[2 + 4 * seg], n = segs[3 + 4 * seg];
   const int D = P.D, FF = P.FF, k = P.k, E = P.E;
@@ -694,49 +671,62 @@ __global__ void __launch_bounds__(256, 2) k_pf_down(gm_moe_layer P, const int32_
   const int64_t rb = gm_row_bytes(QT, FF);
   const uint8_t* base = shared ? static_cast<const uint8_t*>(P.down_sh)
                                : static_cast<const uint8_t*>(P.down_exps) + (int64_t)e * D * rb;
-  const uint8_t* wrow[2];
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int row = rt * 128 + wave * 32 + m * 16 + l16;
-    wrow[m] = base + (int64_t)(row < D ? row : 0) * rb;
-  }
   constexpr int SBB = QT == GM_QTYPE_IQ4_XS ? GM_IQ4XS_BYTES : GM_IQ3XXS_BYTES;
-  const int nsb = FF / kChunk, ntiles = (n + 15) >> 4;
-  gm_f32x4 acc[2][4];
+  const int n_groups = (D + 127) / 128, g0 = bi * rg_per_blk;
+  const int g1 = g0 + rg_per_blk < n_groups ? g0 + rg_per_blk : n_groups;
+  auto row_ptr = [&](int g, int m) {
+    const int row = g * 128 + wave * 32 + m * 16 + l16;
+    return base + (int64_t)(row < D ? row : 0) * rb;
+  };
+  PfRaw<QT> wc[2][NSB];
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[m][t] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
-  ActRegs ha;
-  act_load(ha, hb, FF, in_row, 0);
-  PfRaw<QT> w0 = pf_load<QT>(wrow[0], q), w1 = pf_load<QT>(wrow[1], q);
-  act_store<QT == GM_QTYPE_IQ4_XS>(ha, hl);
-  __syncthreads();
-  for (int sb = 0; sb < nsb; ++sb) {
-    const int sn = sb + 1 < nsb ? sb + 1 : sb;
-    act_load(ha, hb, FF, in_row, sn * kChunk);
-    const PfRaw<QT> w0n = pf_load<QT>(wrow[0] + sn * SBB, q), w1n = pf_load<QT>(wrow[1] + sn * SBB, q);
-    const uint8_t* hbuf = hl + (sb & 1) * kTileB;
-    switch (ntiles) {
-      case 1: dn_superblock<QT, 1>(w0, w1, q, l16, hbuf, grid, sgn, acc); break;
-      case 2: dn_superblock<QT, 2>(w0, w1, q, l16, hbuf, grid, sgn, acc); break;
-      case 3: dn_superblock<QT, 3>(w0, w1, q, l16, hbuf, grid, sgn, acc); break;
-      default: dn_superblock<QT, 4>(w0, w1, q, l16, hbuf, grid, sgn, acc); break;
-    }
-    if (sb + 1 < nsb) act_store<QT == GM_QTYPE_IQ4_XS>(ha, hl + ((sb + 1) & 1) * kTileB);
-    w0 = w0n;
-    w1 = w1n;
-    __syncthreads();
+    for (int sb = 0; sb < NSB; ++sb) wc[m][sb] = pf_load<QT>(row_ptr(g0, m) + sb * SBB, q);
+#pragma unroll
+  for (int sb = 0; sb < NSB; ++sb) {
+    ActRegs ha;
+    act_load(ha, hb, FF, in_row, sb * kChunk);
+    act_store<QT == GM_QTYPE_IQ4_XS>(ha, hl + sb * 2 * kChunk, PITCH);
   }
+  __syncthreads();
+  const int ntiles = (n + 15) >> 4;
+  for (int g = g0; g < g1; ++g) {
+    const int gn = g + 1 < g1 ? g + 1 : g;
+    PfRaw<QT> wn[2][NSB];
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int r0 = rt * 128 + wave * 32 + m * 16 + 4 * q;
+    for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int col = t * 16 + l16;
-      if (t < ntiles && col < n && r0 < D)
-        *reinterpret_cast<gm_f32x4*>(yp + (int64_t)(row0 + col) * D + r0) = acc[m][t];
+      for (int sb = 0; sb < NSB; ++sb) wn[m][sb] = pf_load<QT>(row_ptr(gn, m) + sb * SBB, q);
+    gm_f32x4 acc[2][4];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[m][t] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sb = 0; sb < NSB; ++sb) {
+      const uint8_t* hbuf = hl + sb * 2 * kChunk;
+      switch (ntiles) {
+        case 1: dn_superblock<QT, 1>(wc[0][sb], wc[1][sb], q, l16, hbuf, PITCH, grid, sgn, acc); break;
+        case 2: dn_superblock<QT, 2>(wc[0][sb], wc[1][sb], q, l16, hbuf, PITCH, grid, sgn, acc); break;
+        case 3: dn_superblock<QT, 3>(wc[0][sb], wc[1][sb], q, l16, hbuf, PITCH, grid, sgn, acc); break;
+        default: dn_superblock<QT, 4>(wc[0][sb], wc[1][sb], q, l16, hbuf, PITCH, grid, sgn, acc); break;
+      }
     }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int r0 = g * 128 + wave * 32 + m * 16 + 4 * q;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int col = t * 16 + l16;
+        if (t < ntiles && col < n && r0 < D)
+          *reinterpret_cast<gm_f32x4*>(yp + (int64_t)(row0 + col) * D + r0) = acc[m][t];
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int sb = 0; sb < NSB; ++sb) wc[m][sb] = wn[m][sb];
   }
 }
 
@@ -817,9 +807,9 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
     hipLaunchKernelGGL(k_pf_topk<8>, dim3((T + 3) / 4), dim3(256), 0, s, w.part, ldp, nsplit, T, E, k,
                        L->sh_gate_inp ? 1 : 0, L->router_bias, logits, shg, ids, wts);
   GM_TRY(hipGetLastError());
-  if (int rc = gm_launch_dispatch_inv(ids, T, k, E, w.counts, w.offsets, w.sorted, w.inv, s)) return rc;
-  hipLaunchKernelGGL(k_pf_segments, dim3(1), dim3(1024), 0, s, w.counts, E, T, has_sh ? 1 : 0, w.segs);
-  GM_TRY(hipGetLastError());
+  if (int rc = gm_launch_dispatch_seg(ids, T, k, E, w.counts, w.offsets, w.sorted, w.inv, w.segs, kSegTok,
+                                     has_sh ? T : 0, s))
+    return rc;
   const int nseg = max_segments(T, k, E);
   {
     const int nrt = FF / 64;
@@ -830,10 +820,27 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
     GM_TRY(hipGetLastError());
   }
   {
-    const int nrt = (D + 127) / 128;
-    const int nb = (nseg + 7) / 8 * 8 * nrt;
-    if (int rc = gm_set_smem(k_pf_down<QTD>, kGemmSmem)) return rc;
-    hipLaunchKernelGGL(k_pf_down<QTD>, dim3(nb), dim3(256), kGemmSmem, s, *L, w.segs, w.offsets, w.hb, w.yp, T, nrt);
+    constexpr int kGroupsPerBlock = 2;
+    const int n_blk = ((D + 127) / 128 + kGroupsPerBlock - 1) / kGroupsPerBlock;
+    const int nb = (nseg + 7) / 8 * 8 * n_blk;
+    const size_t smem = kSegTok * (2 * (size_t)FF + 16) + 256 * 4 + 128 * 16 + kSegTok * 4;
+    switch (FF / kChunk) {
+      case 1:
+        if (int rc = gm_set_smem(k_pf_down<QTD, 1>, smem)) return rc;
+        hipLaunchKernelGGL((k_pf_down<QTD, 1>), dim3(nb), dim3(256), smem, s, *L, w.segs, w.offsets, w.hb, w.yp, T,
+                           n_blk, kGroupsPerBlock);
+        break;
+      case 2:
+        if (int rc = gm_set_smem(k_pf_down<QTD, 2>, smem)) return rc;
+        hipLaunchKernelGGL((k_pf_down<QTD, 2>), dim3(nb), dim3(256), smem, s, *L, w.segs, w.offsets, w.hb, w.yp, T,
+                           n_blk, kGroupsPerBlock);
+        break;
+      default:
+        if (int rc = gm_set_smem(k_pf_down<QTD, 4>, smem)) return rc;
+        hipLaunchKernelGGL((k_pf_down<QTD, 4>), dim3(nb), dim3(256), smem, s, *L, w.segs, w.offsets, w.hb, w.yp, T,
+                           n_blk, kGroupsPerBlock);
+        break;
+    }
     GM_TRY(hipGetLastError());
   }
   hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(256), 0, s, x, w.yp, w.inv, wts, shg, T, k, D, has_sh ? 1 : 0,
@@ -855,8 +862,8 @@ int gm_pf_run(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
   if (L->gate_sh && (L->q_gate_sh != L->q_gate || L->q_down_sh != L->q_down))
     return gm_fail_arg("gm_moe_forward: the prefill path needs the shared expert in the routed formats"),
            GM_EUNSUPPORTED;
-  if (L->D % kChunk || L->FF % kChunk)
-    return gm_fail_arg("gm_moe_forward: prefill needs D and FF multiples of %d", kChunk);
+  if (L->D % kChunk || L->FF % kChunk || L->FF > 4 * kChunk)
+    return gm_fail_arg("gm_moe_forward: prefill needs D and FF multiples of %d and FF <= %d", kChunk, 4 * kChunk);
   const int qg = L->q_gate, qd = L->q_down;
   if (qg == GM_QTYPE_IQ4_XS && qd == GM_QTYPE_IQ3_XXS) return prefill_t<GM_QTYPE_IQ4_XS, GM_QTYPE_IQ3_XXS>(L, x, y, T, flags, ws, lay, s);
   if (qg == GM_QTYPE_IQ3_XXS && qd == GM_QTYPE_IQ4_XS) return prefill_t<GM_QTYPE_IQ3_XXS, GM_QTYPE_IQ4_XS>(L, x, y, T, flags, ws, lay, s);
