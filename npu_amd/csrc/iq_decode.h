@@ -193,61 +193,83 @@ __device__ __forceinline__ void gm_stage_grid(uint32_t* grid_lds) {
   for (int i = threadIdx.x; i < 256; i += blockDim.x) grid_lds[i] = gm_iq3xxs_grid[i];
 }
 
-// IQ3_XXS decode table in LDS (4 KB): the grid as float magnitudes,
-// gridf[i] = the 4 magnitudes of grid entry i.  Signs are applied with one
-// bit operation per weight (the magnitudes are positive).
+// IQ3_XXS decode tables in LDS (3 KB): the grid as packed byte magnitudes,
+// and per 7-bit ksigns index the byte masks of its 8 signs (0x00 / 0xff) with
+// the same masks & 0x01 per byte: {signs 0-3, signs 4-7, low 0-3, low 4-7}.
 struct Iq3Tab {
-  gm_f32x4 gridf[256];
+  uint32_t grid[256];
+  gm_u32x4 sgn[128];
 };
 
-// Threads 0..255 each load one grid word (step 1) and write one gridf entry
-// (step 2); the block size must be >= 256.
+// Threads 0..255 each load one grid word (step 1) and store it with the sign
+// masks (step 2); the block size must be >= 256.
 __device__ __forceinline__ uint32_t gm_iq3_tab_load() {
   return threadIdx.x < 256 ? gm_iq3xxs_grid[threadIdx.x] : 0u;
 }
 
 __device__ __forceinline__ void gm_iq3_tab_store(uint32_t g, Iq3Tab* __restrict__ tab) {
-  if (threadIdx.x < 256) {
-    gm_f32x4 m;
-    m.x = (float)(g & 0xffu); m.y = (float)((g >> 8) & 0xffu);
-    m.z = (float)((g >> 16) & 0xffu); m.w = (float)(g >> 24);
-    tab->gridf[threadIdx.x] = m;
-  }
-}
-
-// magnitude m >= 0 with the sign of bit i of sb
-__device__ __forceinline__ float gm_signed(float m, uint32_t sb, int i) {
-  return __int_as_float(__float_as_int(m) | (int)((sb << (31 - i)) & 0x80000000u));
-}
-
-__device__ __forceinline__ float gm_decode_iq3_tab(const RawIq3& r, const Iq3Tab* __restrict__ tab,
-                                                   float (&wv)[32]) {
-  const float d = gm_h2f(r.d);
-  const float db = d * (0.5f + (float)(r.w >> 28)) * 0.5f;
+  if (threadIdx.x < 256) tab->grid[threadIdx.x] = g;
+  if (threadIdx.x < 128) {
+    const uint32_t s = gm_ksigns(threadIdx.x);
+    uint32_t m0 = 0, m1 = 0;
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const uint32_t qw = g < 2 ? r.q0 : r.q1;
-    const gm_f32x4 ma = tab->gridf[(qw >> (16 * (g & 1))) & 0xffu];
-    const gm_f32x4 mb = tab->gridf[(qw >> (16 * (g & 1) + 8)) & 0xffu];
-    const uint32_t sb = gm_ksigns((r.w >> (7 * g)) & 127u);
-    wv[8 * g + 0] = gm_signed(ma.x, sb, 0);
-    wv[8 * g + 1] = gm_signed(ma.y, sb, 1);
-    wv[8 * g + 2] = gm_signed(ma.z, sb, 2);
-    wv[8 * g + 3] = gm_signed(ma.w, sb, 3);
-    wv[8 * g + 4] = gm_signed(mb.x, sb, 4);
-    wv[8 * g + 5] = gm_signed(mb.y, sb, 5);
-    wv[8 * g + 6] = gm_signed(mb.z, sb, 6);
-    wv[8 * g + 7] = gm_signed(mb.w, sb, 7);
+    for (int b = 0; b < 4; ++b) {
+      m0 |= ((s >> b) & 1u) ? 0xffu << (8 * b) : 0u;
+      m1 |= ((s >> (b + 4)) & 1u) ? 0xffu << (8 * b) : 0u;
+    }
+    tab->sgn[threadIdx.x] = gm_u32x4{m0, m1, m0 & 0x01010101u, m1 & 0x01010101u};
   }
-  return db;
 }
 
-// Decode with the LDS tables (IQ3_XXS); other formats need none.
+// Signed int8 weights of one sub-block in k order (byte i of w[c] is weight
+// 4c + i) and the sub-block scale: weight[k] == scale * int8 exactly.
+//   IQ4_XS: kvalues (npu/quant_mv_iq4.py:194-197), scale d (ls - 32);
+//   IQ3_XXS: +-grid magnitude (<= 62, never 0, so the byte negation
+//            (g ^ 0xff) + 1 cannot carry), scale d (0.5 + s4) / 2.
+template <int QT>
+__device__ __forceinline__ float gm_decode_i8(const typename RawSub<QT>::T& r, int sub, const Iq3Tab* __restrict__ tab,
+                                              uint32_t (&w)[8]) {
+  if constexpr (QT == GM_QTYPE_IQ4_XS) {
+    const int s = sub & 7;
+    const float d = gm_h2f(r.h0 & 0xffffu);
+    const uint32_t sh = r.h0 >> 16;
+    const uint32_t sl = (r.h1 >> (8 * (s >> 1) + 4 * (s & 1))) & 15u;
+    const int ls = (int)(sl | (((sh >> (2 * s)) & 3u) << 4));
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      w[c] = gm_iq4nl_lut4(r.q[c] & 0x0f0f0f0fu);
+      w[4 + c] = gm_iq4nl_lut4((r.q[c] >> 4) & 0x0f0f0f0fu);
+    }
+    return d * (float)(ls - 32);
+  } else {
+    const float d = gm_h2f(r.d);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t qw = (g < 2 ? r.q0 : r.q1) >> (16 * (g & 1));
+      const uint32_t ga = tab->grid[qw & 0xffu], gb = tab->grid[(qw >> 8) & 0xffu];
+      const gm_u32x4 m = tab->sgn[(r.w >> (7 * g)) & 127u];
+      w[2 * g] = (ga ^ m.x) + m.z;
+      w[2 * g + 1] = (gb ^ m.y) + m.w;
+    }
+    return d * (0.5f + (float)(r.w >> 28)) * 0.5f;
+  }
+}
+
+// Float weights (scale excluded) with the LDS tables where a format needs them.
 template <int QT>
 __device__ __forceinline__ float gm_decode_sub_t(const typename RawSub<QT>::T& r, int sub,
                                                  const Iq3Tab* __restrict__ tab, float (&wv)[32]) {
-  if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_decode_iq3_tab(r, tab, wv);
-  else return gm_decode_sub<QT>(r, sub, nullptr, wv);
+  if constexpr (QT == GM_QTYPE_IQ3_XXS || QT == GM_QTYPE_IQ4_XS) {
+    uint32_t w[8];
+    const float sc = gm_decode_i8<QT>(r, sub, tab, w);
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wv[4 * c + i] = gm_sbyte(w[c], i);
+    return sc;
+  } else {
+    return gm_decode_sub<QT>(r, sub, nullptr, wv);
+  }
 }
 
 // 32-wide dot of decoded weights with x (LDS or registers).

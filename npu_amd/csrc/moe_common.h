@@ -304,6 +304,161 @@ __device__ __forceinline__ void dot_subs(const RowFetch<QT, SPL>& f, int lir, in
   }
 }
 
+// ------------------------------------------------- int8-limb activations
+// The decode kernels multiply the int8 weights of gm_decode_i8 with
+// activations split into three int8 limbs on v_dot4_i32_i8.  A sub-block of
+// 32 activations a_k with |a_k| < 2^E is held as q_k = rne(a_k 2^(22-E)),
+// q_k = L2 2^16 + L1 2^8 + L0 (L0, L1 in [-128, 127], |L2| <= 65), so that
+// a_k = 2^(E-22) q_k to within 2^(E-23) and every partial dot product
+// sum_k w_k L_k (|w| <= 127, 32 terms) is an exact int32 below 2^24.
+// LDS layout per sub-block, GM_LSUB = 112 bytes (a 28-dword stride spreads 16
+// consecutive sub-blocks over all 64 banks): plane L0 (32 bytes, byte i of
+// dword c = k 4c + i), plane L1, plane L2, float 2^(E-22), 12 spare bytes.
+constexpr int GM_LSUB = 112;
+
+__host__ __device__ inline int gm_limb_row_bytes(int K) { return (K / GM_SUB) * GM_LSUB; }
+
+// Max over lanes 8j .. 8j+7: the two quad swaps, then the half-row mirror.
+__device__ __forceinline__ float gm_max8(float m) {
+  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_1032));
+  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_2301));
+  return fmaxf(m, GM_DPP_F(m, 0x141));                       // row_half_mirror
+}
+
+// Low bytes of four int32 -> one dword.
+__device__ __forceinline__ uint32_t gm_pack_lo4(int a, int b, int c, int d) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000c0cu);
+  return lo | hi;
+}
+
+// Limbs of activations 4c .. 4c+3 of a row into `row` (limb layout).  The 8
+// lanes holding the float4s of one sub-block must be lanes 8j .. 8j+7 of one
+// wave (c % 8 == lane % 8), all executing this call (store to a spare
+// sub-block when c is past the row).  A non-finite activation makes the
+// sub-block's scale NaN.
+__device__ __forceinline__ void gm_put_limbs4(gm_f32x4 v, int c, uint8_t* __restrict__ row) {
+  const float ax = fabsf(v.x), ay = fabsf(v.y), az = fabsf(v.z), aw = fabsf(v.w);
+  const bool fin = ax <= 3.4e38f && ay <= 3.4e38f && az <= 3.4e38f && aw <= 3.4e38f;
+  const float m = gm_max8(fin ? fmaxf(fmaxf(ax, ay), fmaxf(az, aw)) : __builtin_inff());
+  // m in [2^(E-1), 2^E); below 2^-100 the sub-block is quantised against 2^-100
+  const int E = m > 0.f && m <= 3.4e38f ? max(__builtin_amdgcn_frexp_expf(m), -100) : 0;
+  const float up = __builtin_ldexpf(1.0f, 22 - E);
+  const float scale = m <= 3.4e38f ? __builtin_ldexpf(1.0f, E - 22) : __builtin_nanf("");
+  int q[4];
+  const float f[4] = {v.x * up, v.y * up, v.z * up, v.w * up};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q[i] = __float_as_int(f[i] + 12582912.0f) - 0x4B400000;   // rne, |f| < 2^22
+  int t1[4], t2[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { t1[i] = (q[i] + 128) >> 8; t2[i] = (t1[i] + 128) >> 8; }
+  uint8_t* sb = row + (c >> 3) * GM_LSUB + 4 * (c & 7);
+  *reinterpret_cast<uint32_t*>(sb) = gm_pack_lo4(q[0], q[1], q[2], q[3]);
+  *reinterpret_cast<uint32_t*>(sb + 32) = gm_pack_lo4(t1[0], t1[1], t1[2], t1[3]);
+  *reinterpret_cast<uint32_t*>(sb + 64) = gm_pack_lo4(t2[0], t2[1], t2[2], t2[3]);
+  *reinterpret_cast<float*>(row + (c >> 3) * GM_LSUB + 96) = scale;     // same value from all 8 lanes
+}
+
+// One wave stages x [D] (XW float4 per lane, RMSNorm'd when norm_w != NULL)
+// as a limb row `row` (gm_limb_row_bytes(D) + GM_LSUB bytes); no block barrier.
+template <int XW>
+__device__ __forceinline__ void stage_limbs_wave(const float* __restrict__ x, int D, const float* __restrict__ norm_w,
+                                                 float eps, uint8_t* __restrict__ row) {
+  const int lane = threadIdx.x & 63, nq = D >> 2;
+  const gm_f32x4* x4 = reinterpret_cast<const gm_f32x4*>(x);
+  const gm_f32x4* w4 = reinterpret_cast<const gm_f32x4*>(norm_w);
+  gm_f32x4 v[XW], w[XW];
+#pragma unroll
+  for (int i = 0; i < XW; ++i) {
+    const int c = lane + 64 * i;
+    v[i] = x4[c < nq ? c : nq - 1];
+  }
+  if (norm_w != nullptr) {
+#pragma unroll
+    for (int i = 0; i < XW; ++i) {
+      const int c = lane + 64 * i;
+      w[i] = w4[c < nq ? c : nq - 1];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < XW; ++i)
+      if (lane + 64 * i < nq) ss = fmaf(v[i].x, v[i].x, fmaf(v[i].y, v[i].y, fmaf(v[i].z, v[i].z, fmaf(v[i].w, v[i].w, ss))));
+    const float rms = 1.0f / sqrtf(gm_wave_sum64(ss) / (float)D + eps);
+#pragma unroll
+    for (int i = 0; i < XW; ++i) {
+      v[i].x = (v[i].x * rms) * w[i].x; v[i].y = (v[i].y * rms) * w[i].y;
+      v[i].z = (v[i].z * rms) * w[i].z; v[i].w = (v[i].w * rms) * w[i].w;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < XW; ++i) {
+    const int c = lane + 64 * i;
+    gm_put_limbs4(v[i], c < nq ? c : nq + (c & 7), row);
+  }
+}
+
+// acc[m] += W_row . act[idx[m]] over the fetched sub-blocks, m < nt; act rows
+// are limb rows of row_bytes bytes.  BF16 weights (a shared expert kept in
+// bf16) take the activations back to fp32 from their limbs.
+template <int QT, int LR, int SPL, int NT>
+__device__ __forceinline__ void dot_subs_i8(const RowFetch<QT, SPL>& f, int lir, int nsub,
+                                            const uint8_t* __restrict__ act, int row_bytes, const int (&idx)[NT],
+                                            int nt, const Iq3Tab* __restrict__ tab, float (&acc)[NT]) {
+#pragma unroll
+  for (int i = 0; i < SPL; ++i) {
+    const int sub = lir + LR * i;
+    if (sub < nsub) {
+      if constexpr (QT == GM_QTYPE_BF16) {
+        float wv[32];
+        gm_decode_bf16(f.r[i], wv);
+#pragma unroll
+        for (int m = 0; m < NT; ++m) {
+          if (m < nt) {
+            const uint8_t* s = act + idx[m] * row_bytes + sub * GM_LSUB;
+            const gm_u32x4* p = reinterpret_cast<const gm_u32x4*>(s);
+            const gm_u32x4 l0a = p[0], l0b = p[1], l1a = p[2], l1b = p[3], l2a = p[4], l2b = p[5];
+            const uint32_t l0[8] = {l0a.x, l0a.y, l0a.z, l0a.w, l0b.x, l0b.y, l0b.z, l0b.w};
+            const uint32_t l1[8] = {l1a.x, l1a.y, l1a.z, l1a.w, l1b.x, l1b.y, l1b.z, l1b.w};
+            const uint32_t l2[8] = {l2a.x, l2a.y, l2a.z, l2a.w, l2b.x, l2b.y, l2b.z, l2b.w};
+            float sacc = 0.f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+#pragma unroll
+              for (int b = 0; b < 4; ++b) {
+                const float a = fmaf(gm_sbyte(l2[c], b), 65536.f, fmaf(gm_sbyte(l1[c], b), 256.f, gm_sbyte(l0[c], b)));
+                sacc = fmaf(wv[4 * c + b], a, sacc);
+              }
+            acc[m] = fmaf(*reinterpret_cast<const float*>(s + 96), sacc, acc[m]);
+          }
+        }
+      } else {
+        uint32_t w[8];
+        const float ws = gm_decode_i8<QT>(f.r[i], sub, tab, w);
+#pragma unroll
+        for (int m = 0; m < NT; ++m) {
+          if (m < nt) {
+            const uint8_t* s = act + idx[m] * row_bytes + sub * GM_LSUB;
+            const gm_u32x4* p = reinterpret_cast<const gm_u32x4*>(s);
+            const gm_u32x4 l0a = p[0], l0b = p[1], l1a = p[2], l1b = p[3], l2a = p[4], l2b = p[5];
+            const uint32_t l0[8] = {l0a.x, l0a.y, l0a.z, l0a.w, l0b.x, l0b.y, l0b.z, l0b.w};
+            const uint32_t l1[8] = {l1a.x, l1a.y, l1a.z, l1a.w, l1b.x, l1b.y, l1b.z, l1b.w};
+            const uint32_t l2[8] = {l2a.x, l2a.y, l2a.z, l2a.w, l2b.x, l2b.y, l2b.z, l2b.w};
+            int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              s0 = __builtin_amdgcn_sdot4((int)w[c], (int)l0[c], s0, false);
+              s1 = __builtin_amdgcn_sdot4((int)w[c], (int)l1[c], s1, false);
+              s2 = __builtin_amdgcn_sdot4((int)w[c], (int)l2[c], s2, false);
+            }
+            const float r = fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0));
+            acc[m] = fmaf(ws * *reinterpret_cast<const float*>(s + 96), r, acc[m]);
+          }
+        }
+      }
+    }
+  }
+}
+
 // Sum over the LR lanes of a row (LR = 16, 32 or 64), result in every lane.
 template <int LR>
 __device__ __forceinline__ float row_sum(float v) {
@@ -405,6 +560,60 @@ __device__ __forceinline__ void stage_x_regs(XRegs<NT, XPT>& r, int nt, int D, c
           const int c = threadIdx.x + 256 * i;
           xs4[c < nq ? m * nq + il_index4(c & 7, c >> 3, nsub) : NT * nq] = r.v[m][i];
         }
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// As stage_x_regs, into limb rows: row m of xs at m * gm_limb_row_bytes(D);
+// lanes past the row store into the spare sub-block after row NT - 1.
+template <int NT, int XPT>
+__device__ __forceinline__ void stage_limbs_regs(XRegs<NT, XPT>& r, int nt, int D, const float* __restrict__ norm_w,
+                                                 float eps, uint8_t* __restrict__ xs, float* __restrict__ red) {
+  const int nq = D >> 2, rbytes = gm_limb_row_bytes(D);
+  float rms[NT];
+#pragma unroll
+  for (int m = 0; m < NT; ++m) rms[m] = 1.f;
+  if (norm_w != nullptr) {
+    float ss[NT];
+#pragma unroll
+    for (int m = 0; m < NT; ++m) {
+      ss[m] = 0.f;
+      if (m < nt) {
+#pragma unroll
+        for (int i = 0; i < XPT; ++i) {
+          const int c = threadIdx.x + 256 * i;
+          const gm_f32x4 v = r.v[m][i];
+          if (c < nq) ss[m] = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss[m]))));
+        }
+      }
+      ss[m] = gm_wave_sum64(ss[m]);
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+      for (int m = 0; m < NT; ++m) red[wave * NT + m] = ss[m];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < NT; ++m) {
+      const float tot = (red[m] + red[NT + m]) + (red[2 * NT + m] + red[3 * NT + m]);
+      rms[m] = 1.0f / sqrtf(tot / (float)D + eps);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < NT; ++m) {
+    if (m < nt) {
+#pragma unroll
+      for (int i = 0; i < XPT; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        gm_f32x4 v = r.v[m][i];
+        if (norm_w != nullptr) {
+          const gm_f32x4 w = r.w[i];
+          v.x = (v.x * rms[m]) * w.x; v.y = (v.y * rms[m]) * w.y; v.z = (v.z * rms[m]) * w.z; v.w = (v.w * rms[m]) * w.w;
+        }
+        gm_put_limbs4(v, c < nq ? c : (c & 7), xs + (c < nq ? m : NT) * rbytes);   // unconditional (DPP inside)
       }
     }
   }

@@ -87,12 +87,14 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
   fetch_subs<QTS, 32, DC>(fg, static_cast<const uint8_t*>(P.gate_sh) + r * rb, lane & 31, nsub);
   fetch_subs<QTS, 32, DC>(fu, static_cast<const uint8_t*>(P.up_sh) + r * rb, lane & 31, nsub);
   issue_fence();
-  stage_x_regs<NT, DC>(xr, T, D, P.norm_w, P.norm_eps, xs, red);
+  uint8_t* xl = reinterpret_cast<uint8_t*>(xs);                // limb rows (fit in the fp32 rows' space)
+  stage_limbs_regs<NT, DC>(xr, T, D, P.norm_w, P.norm_eps, xl, red);
   float ag[NT], au[NT];
 #pragma unroll
   for (int m = 0; m < NT; ++m) { ag[m] = 0.f; au[m] = 0.f; }
-  dot_subs<QTS, 32, DC, NT>(fg, lane & 31, nsub, xs, D, tok, T, tab, ag);
-  dot_subs<QTS, 32, DC, NT>(fu, lane & 31, nsub, xs, D, tok, T, tab, au);
+  const int rbytes = gm_limb_row_bytes(D);
+  dot_subs_i8<QTS, 32, DC, NT>(fg, lane & 31, nsub, xl, rbytes, tok, T, tab, ag);
+  dot_subs_i8<QTS, 32, DC, NT>(fu, lane & 31, nsub, xl, rbytes, tok, T, tab, au);
 #pragma unroll
   for (int m = 0; m < NT; ++m) {
     const float hv = gm_silu(row_sum<32>(ag[m])) * row_sum<32>(au[m]);

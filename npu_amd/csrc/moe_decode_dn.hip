@@ -48,7 +48,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   constexpr int CR = (8 * 8 * RB_MAX / 16 + NTH - 1) / NTH;    // routed 16-byte chunks per thread
   constexpr int RBS_MAX = QTS == GM_QTYPE_BF16 ? 1024 * FC : RB_MAX;
   constexpr int CS = (8 * RBS_MAX / 16 + NTH - 1) / NTH;       // shared 16-byte chunks per thread
-  extern __shared__ float smem[];
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ float s_wj[8];        // routing weight and h row of routed matrix m
   __shared__ int32_t s_pr[8];
   __shared__ float s_part[9][8];
@@ -56,8 +56,9 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   const int rbd = (int)gm_row_bytes(QTD, FF), rbs = (int)gm_row_bytes(QTS, FF);
   const int nqr = FF >> 2;
   const int wbytes = k * 8 * rbd + 8 * rbs;
-  float* hs = smem;                                                    // (k + 1) rows of FF (+ 4)
-  uint8_t* wr = reinterpret_cast<uint8_t*>(smem + (k + 1) * FF + 4);   // [k][8][rbd], [8][rbs], 16 spare
+  const int hbytes = gm_limb_row_bytes(FF);
+  uint8_t* hs = smem;                                                  // (k + 1) limb rows of FF (+ spare)
+  uint8_t* wr = smem + (k + 2) * hbytes;                               // [k][8][rbd], [8][rbs], 16 spare
   Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(wr + ((wbytes + 16 + 15) & ~15));
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r0 = blockIdx.x * 8;
@@ -97,12 +98,11 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
   {
     const uint32_t magic = 0xffffffffu / (uint32_t)nqr + 1u;     // c / nqr == umulhi(c, magic) for c < 2^16
-    gm_f32x4* hs4 = reinterpret_cast<gm_f32x4*>(hs);
 #pragma unroll
     for (int i = 0; i < HPT; ++i) {
-      const int c = tid + NTH * i;
+      const int c = tid + NTH * i;                               // 8-lane groups never straddle a row
       const int rr = (int)__umulhi((uint32_t)c, magic), cc = c - rr * nqr;
-      hs4[c < nq_rows ? rr * nqr + il_index4(cc & 7, cc >> 3, nsub) : (k + 1) * nqr] = hr[i];
+      gm_put_limbs4(hr[i], c < nq_rows ? cc : (c & 7), hs + (c < nq_rows ? rr : k + 1) * hbytes);
     }
   }
 #pragma unroll
@@ -139,32 +139,54 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
     const int lg = nsub == 8 ? 3 : nsub == 16 ? 4 : 5;
     const int R = nsub >> 3, rg = lane >> lg, sub = lane & (nsub - 1);
     const int hrow = routed ? s_pr[wave] : k;
-    float hv[32];                                              // SwiGLU values of this sub-block
-    {
-      const gm_f32x4* hrow4 = reinterpret_cast<const gm_f32x4*>(hs + hrow * FF);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const gm_f32x4 a = hrow4[il_index4(q, sub, nsub)];
-        hv[4 * q] = a.x; hv[4 * q + 1] = a.y; hv[4 * q + 2] = a.z; hv[4 * q + 3] = a.w;
-      }
-    }
+    // limbs and scale of this sub-block of the SwiGLU row
+    const uint8_t* hsub = hs + hrow * hbytes + sub * GM_LSUB;
+    const gm_u32x4* hp = reinterpret_cast<const gm_u32x4*>(hsub);
+    const gm_u32x4 l0a = hp[0], l0b = hp[1], l1a = hp[2], l1b = hp[3], l2a = hp[4], l2b = hp[5];
+    const uint32_t l0[8] = {l0a.x, l0a.y, l0a.z, l0a.w, l0b.x, l0b.y, l0b.z, l0b.w};
+    const uint32_t l1[8] = {l1a.x, l1a.y, l1a.z, l1a.w, l1b.x, l1b.y, l1b.z, l1b.w};
+    const uint32_t l2[8] = {l2a.x, l2a.y, l2a.z, l2a.w, l2b.x, l2b.y, l2b.z, l2b.w};
+    const float hscale = *reinterpret_cast<const float*>(hsub + 96);
     float part[RMAX];
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {
       part[r] = 0.f;
       if (r < R) {
-        float wv[32], sc;
-        if (routed) {
-          const typename RawSub<QTD>::T raw = gm_load_sub<QTD>(wr + (wave * 8 + rg * R + r) * rbd, sub);
-          sc = gm_decode_sub_t<QTD>(raw, sub, tab, wv);
-        } else {
-          const typename RawSub<QTS>::T raw = gm_load_sub<QTS>(wr + k * 8 * rbd + (rg * R + r) * rbs, sub);
-          sc = gm_decode_sub_t<QTS>(raw, sub, tab, wv);
-        }
-        float s0 = 0.f, s1 = 0.f;
+        if constexpr (QTD == GM_QTYPE_BF16 || QTS == GM_QTYPE_BF16) {
+          float wv[32], sc;                                    // bf16 matrices: fp32 activations from the limbs
+          if (routed) {
+            const typename RawSub<QTD>::T raw = gm_load_sub<QTD>(wr + (wave * 8 + rg * R + r) * rbd, sub);
+            sc = gm_decode_sub_t<QTD>(raw, sub, tab, wv);
+          } else {
+            const typename RawSub<QTS>::T raw = gm_load_sub<QTS>(wr + k * 8 * rbd + (rg * R + r) * rbs, sub);
+            sc = gm_decode_sub_t<QTS>(raw, sub, tab, wv);
+          }
+          float a = 0.f;
 #pragma unroll
-        for (int j = 0; j < 32; j += 2) { s0 = fmaf(wv[j], hv[j], s0); s1 = fmaf(wv[j + 1], hv[j + 1], s1); }
-        part[r] = sc * (s0 + s1);
+          for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+              a = fmaf(wv[4 * c + b], fmaf(gm_sbyte(l2[c], b), 65536.f, fmaf(gm_sbyte(l1[c], b), 256.f, gm_sbyte(l0[c], b))), a);
+          part[r] = sc * hscale * a;
+        } else {
+          uint32_t w[8];
+          float sc;
+          if (routed) {
+            const typename RawSub<QTD>::T raw = gm_load_sub<QTD>(wr + (wave * 8 + rg * R + r) * rbd, sub);
+            sc = gm_decode_i8<QTD>(raw, sub, tab, w);
+          } else {
+            const typename RawSub<QTS>::T raw = gm_load_sub<QTS>(wr + k * 8 * rbd + (rg * R + r) * rbs, sub);
+            sc = gm_decode_i8<QTS>(raw, sub, tab, w);
+          }
+          int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            s0 = __builtin_amdgcn_sdot4((int)w[c], (int)l0[c], s0, false);
+            s1 = __builtin_amdgcn_sdot4((int)w[c], (int)l1[c], s1, false);
+            s2 = __builtin_amdgcn_sdot4((int)w[c], (int)l2[c], s2, false);
+          }
+          part[r] = sc * hscale * fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0));
+        }
       }
     }
     const float wgt = routed ? s_wj[wave] : sg;
@@ -187,21 +209,26 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
 
 // 64 rows of one down matrix for nm <= 8 member rows of hsrc (global rows
 // src[m] of h, where h_sh follows h), written to yp rows dst[m].
-template <int QTW, int FC>
-__device__ __forceinline__ void down_tile(const uint8_t* __restrict__ wbase, int D, int FF, int tile, int nm,
+// Rows [row0, row0 + 64 NTILE) of one down matrix for nm member rows of h
+// (h rows src[m] -> yp rows dst[m]): every tile's raw rows are fetched first
+// (wave w, pass q of tile t -> row row0 + 64t + 16w + 4q + (lane >> 4), 16 lanes
+// per row), the members are staged in LDS meanwhile, then the tiles are decoded.
+template <int QTW, int FC, int NTILE>
+__device__ __forceinline__ void down_rows(const uint8_t* __restrict__ wbase, int D, int FF, int row0, int nm,
                                           const int (&src)[8], const int (&dst)[8], const float* __restrict__ h,
-                                          float* __restrict__ hs, uint32_t gw, Iq3Tab* __restrict__ tab,
+                                          uint8_t* __restrict__ hs, uint32_t gw, Iq3Tab* __restrict__ tab,
                                           float* __restrict__ yp) {
   constexpr int HPT = 4 * FC;     // float4 per thread: 8 * FF <= 8 * 512 * FC floats over 256 threads
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane & 15, nsub = FF >> 5;
   const int64_t rb = gm_row_bytes(QTW, FF);
-  RowFetch<QTW, FC> f[4];
-  int rows[4];
+  RowFetch<QTW, FC> f[NTILE][4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    rows[q] = tile * 64 + wave * 16 + q * 4 + (lane >> 4);
-    fetch_subs<QTW, 16, FC>(f[q], wbase + (int64_t)(rows[q] < D ? rows[q] : 0) * rb, lir, nsub);
-  }
+  for (int t = 0; t < NTILE; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = row0 + 64 * t + wave * 16 + q * 4 + (lane >> 4);
+      fetch_subs<QTW, 16, FC>(f[t][q], wbase + (int64_t)(row < D ? row : 0) * rb, lir, nsub);
+    }
   const int nqr = FF >> 2, nq = nm * nqr;
   const gm_f32x4* h4 = reinterpret_cast<const gm_f32x4*>(h);
   gm_f32x4 hr[HPT];
@@ -216,53 +243,65 @@ __device__ __forceinline__ void down_tile(const uint8_t* __restrict__ wbase, int
   }
   issue_fence();
   if constexpr (QTW == GM_QTYPE_IQ3_XXS) gm_iq3_tab_store(gw, tab);
-  gm_f32x4* hs4 = reinterpret_cast<gm_f32x4*>(hs);
+  const int rbytes = gm_limb_row_bytes(FF);
 #pragma unroll
   for (int i = 0; i < HPT; ++i) {
     const int c = threadIdx.x + 256 * i;
     const int m = c / nqr, cc = c - m * nqr;
-    hs4[c < nq ? m * nqr + il_index4(cc & 7, cc >> 3, nsub) : 8 * nqr] = hr[i];   // unconditional
+    gm_put_limbs4(hr[i], c < nq ? cc : (c & 7), hs + (c < nq ? m : 8) * rbytes);   // unconditional (DPP inside)
   }
   __syncthreads();
   int idx[8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) idx[m] = m;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    float part[8];
+  for (int t = 0; t < NTILE; ++t) {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) part[m] = 0.f;
-    dot_subs<QTW, 16, FC, 8>(f[q], lir, nsub, hs, FF, idx, nm, tab, part);
+    for (int q = 0; q < 4; ++q) {
+      opaque(f[t][q]);
+      float part[8];
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      if (m < nm) {
-        const float sm = row_sum<16>(part[m]);
-        if (lir == 0 && rows[q] < D) yp[(int64_t)dst[m] * D + rows[q]] = sm;
+      for (int m = 0; m < 8; ++m) part[m] = 0.f;
+      dot_subs_i8<QTW, 16, FC, 8>(f[t][q], lir, nsub, hs, rbytes, idx, nm, tab, part);
+      const int row = row0 + 64 * t + wave * 16 + q * 4 + (lane >> 4);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        if (m < nm) {
+          const float sm = row_sum<16>(part[m]);
+          if (lir == 0 && row < D) yp[(int64_t)dst[m] * D + row] = sm;
+        }
       }
+      issue_fence();                                          // one pass's decoded row live at a time
     }
   }
 }
 
-// Block = (unit u, 64-row tile); units 0 .. nu-1 are the unique routed experts,
-// unit nu the shared expert (all T tokens).
+// Blocks [0, n_sh): the shared expert (all T tokens), dn_tiles(FC) 64-row
+// tiles each; blocks [n_sh, ...): unit (b - n_sh) / n_tg of the unique routed
+// experts.  Tiles per block: 4 / FC, so the raw rows of a block stay 64 VGPRs.
+constexpr int dn_tiles(int fc) { return 1; }
+
 template <int QTD, int QTS, int FC>
 __global__ void __launch_bounds__(256) k_dec_down8(gm_moe_layer P, int T, const int32_t* __restrict__ g_grp,
                                                    const float* __restrict__ h, float* __restrict__ yp,
-                                                   int n_tiles) {
-  extern __shared__ float hs[];                 // [8][FF] interleaved (+ 4), then the IQ3 tables
-  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(hs + 8 * P.FF + 4);
+                                                   int n_sh, int n_tg) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t hs[];   // 8 limb rows of FF (+ a spare sub-block)
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(hs + 8 * gm_limb_row_bytes(P.FF) + GM_LSUB);
   const int D = P.D, FF = P.FF, k = P.k, Ptot = T * k;
-  const int u = blockIdx.x / n_tiles, tile = blockIdx.x - u * n_tiles;
   const int nu = g_grp[0];
-  const bool has_sh = P.down_sh != nullptr;
-  if (u > nu || (u == nu && !has_sh)) return;   // uniform per block
+  const bool shared = (int)blockIdx.x < n_sh;
+  const int u = shared ? nu : ((int)blockIdx.x - n_sh) / n_tg;
+  const int tg = shared ? (int)blockIdx.x : (int)blockIdx.x - n_sh - u * n_tg;
+  if (u > nu || (!shared && u == nu)) return;   // uniform per block
+  constexpr int NT = dn_tiles(FC);
+  const int row0 = tg * 64 * NT;
   uint32_t gw = 0;
   if constexpr (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS) gw = gm_iq3_tab_load();
   int src[8], dst[8];
-  if (u == nu) {
+  if (shared) {
 #pragma unroll
     for (int m = 0; m < 8; ++m) { src[m] = Ptot + (m < T ? m : 0); dst[m] = src[m]; }
-    down_tile<QTS, FC>(static_cast<const uint8_t*>(P.down_sh), D, FF, tile, T, src, dst, h, hs, gw, tab, yp);
+    down_rows<QTS, FC, NT>(static_cast<const uint8_t*>(P.down_sh), D, FF, row0, T, src, dst, h, hs, gw, tab, yp);
   } else {
     const int e = g_grp[1 + u];
     const int nm = g_grp[1 + GM_GRP_MAXU + u];
@@ -271,8 +310,8 @@ __global__ void __launch_bounds__(256) k_dec_down8(gm_moe_layer P, int T, const 
       src[m] = g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * u + (m < nm ? m : 0)];
       dst[m] = src[m];
     }
-    down_tile<QTD, FC>(static_cast<const uint8_t*>(P.down_exps) + (int64_t)e * D * gm_row_bytes(QTD, FF), D, FF,
-                       tile, nm, src, dst, h, hs, gw, tab, yp);
+    down_rows<QTD, FC, NT>(static_cast<const uint8_t*>(P.down_exps) + (int64_t)e * D * gm_row_bytes(QTD, FF), D, FF,
+                           row0, nm, src, dst, h, hs, gw, tab, yp);
   }
 }
 
@@ -318,7 +357,7 @@ int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags,
   if (fast1) {
     if constexpr (FC <= 2) {
       const size_t wbytes = (size_t)k * 8 * gm_row_bytes(QTD, FF) + 8 * (size_t)gm_row_bytes(QTS, FF);
-      const size_t smem = ((size_t)(k + 1) * FF + 4) * 4 + ((wbytes + 16 + 15) & ~(size_t)15) +
+      const size_t smem = (size_t)(k + 2) * gm_limb_row_bytes(FF) + ((wbytes + 16 + 15) & ~(size_t)15) +
                           (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
       if (int rc = gm_set_smem(k_dec_down1<QTD, QTS, FC>, smem)) return rc;
       hipLaunchKernelGGL((k_dec_down1<QTD, QTS, FC>), dim3((D + 7) / 8), dim3(576), smem, s, *P, x, flags, a.grp,
@@ -327,12 +366,14 @@ int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags,
       return GM_OK;
     }
   }
-  const int n_tiles = (D + 63) / 64;
+  const int n_tg = (D + 64 * dn_tiles(FC) - 1) / (64 * dn_tiles(FC));
+  const int n_sh = P->down_sh ? n_tg : 0;
   const int max_u = T * k < P->E ? T * k : P->E;
-  const size_t smem = ((size_t)8 * FF + 4) * 4 + (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+  const size_t smem = 8 * (size_t)gm_limb_row_bytes(FF) + GM_LSUB +
+                      (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
   if (int rc = gm_set_smem(k_dec_down8<QTD, QTS, FC>, smem)) return rc;
-  hipLaunchKernelGGL((k_dec_down8<QTD, QTS, FC>), dim3((max_u + 1) * n_tiles), dim3(256), smem, s, *P, T, a.grp, a.h,
-                     a.yp, n_tiles);
+  hipLaunchKernelGGL((k_dec_down8<QTD, QTS, FC>), dim3(n_sh + max_u * n_tg), dim3(256), smem, s, *P, T, a.grp, a.h,
+                     a.yp, n_sh, n_tg);
   GM_TRY(hipGetLastError());
   hipLaunchKernelGGL(k_dec_combine, dim3((D + 255) / 256, T), dim3(256), 0, s, x, T, k, D, flags, a.ids, a.wts,
                      a.shg, P->down_sh ? 1 : 0, a.yp, y);

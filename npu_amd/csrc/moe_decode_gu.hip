@@ -24,11 +24,11 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
                                                      float* __restrict__ g_wts, int32_t* __restrict__ g_grp,
                                                      float* __restrict__ h, int n_chunks) {
   constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
-  extern __shared__ float smem[];
-  float* xs = smem;                                            // [D + 4] interleaved
-  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(smem + P.D + 4);     // IQ3 only
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int D = P.D, E = P.E, k = P.k, FF = P.FF, nsub = D / GM_SUB, rbytes = gm_limb_row_bytes(D);
+  uint8_t* xs = smem;                                          // limb row of x (+ a spare sub-block)
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(smem + rbytes + GM_LSUB);   // IQ3 only
   __shared__ int32_t s_sid[8], s_slot[8];                      // picks in ascending expert order
-  const int D = P.D, E = P.E, k = P.k, FF = P.FF, nsub = D / GM_SUB;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int u = blockIdx.x / n_chunks, chunk = blockIdx.x - u * n_chunks;
   uint32_t gw = 0;
@@ -57,7 +57,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
       if (lane == 0) g_grp[0] = k;
     }
   } else if (wave == 1) {
-    stage_x_wave<4 * DC>(x, D, P.norm_w, P.norm_eps, xs);     // concurrently with the top-k
+    stage_limbs_wave<4 * DC>(x, D, P.norm_w, P.norm_eps, xs);  // concurrently with the top-k
   }
   if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
   __syncthreads();
@@ -71,8 +71,8 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
   fetch_subs<QT, 32, DC>(fu, static_cast<const uint8_t*>(P.up_exps) + ((int64_t)e * FF + r) * rb, lane & 31, nsub);
   const int tok[1] = {0};
   float ag[1] = {0.f}, au[1] = {0.f};
-  dot_subs<QT, 32, DC, 1>(fg, lane & 31, nsub, xs, D, tok, 1, tab, ag);
-  dot_subs<QT, 32, DC, 1>(fu, lane & 31, nsub, xs, D, tok, 1, tab, au);
+  dot_subs_i8<QT, 32, DC, 1>(fg, lane & 31, nsub, xs, rbytes, tok, 1, tab, ag);
+  dot_subs_i8<QT, 32, DC, 1>(fu, lane & 31, nsub, xs, rbytes, tok, 1, tab, au);
   const float hv = gm_silu(row_sum<32>(ag[0])) * row_sum<32>(au[0]);
   if (live && (lane & 31) == 0) h[(int64_t)pair * FF + row] = hv;
 }
@@ -94,24 +94,25 @@ __global__ void __launch_bounds__(512) k_dec_route(const float* __restrict__ log
   for (int i = threadIdx.x; i < GM_GRP_WORDS; i += blockDim.x) g_grp[i] = grp[i];
 }
 
-// Rows r0 .. r0 + 8 NP - 1 of one gate/up pair for nm member tokens (xn rows tok[m],
-// h rows dst[m]), members staged MG = 2 at a time in LDS (most routed units
-// have one member; the shared unit takes T / 2 passes).  Block of 256 threads:
-// wave w, pass p -> rows r0 + 8p + 2w + (lane >> 5), 32 lanes per row.
+// Rows r0 .. r0 + 8 NP - 1 of one gate/up pair for nm member tokens (xn rows
+// tok[m], h rows dst[m]): all NP passes' raw rows are fetched first (wave w,
+// pass p -> rows r0 + 8p + 2w + (lane >> 5), 32 lanes per row), then the
+// members are staged MG = 2 at a time in LDS (most routed units have one
+// member; the shared unit takes T / 2 groups) and every pass is decoded.
 template <int QT, int DC, int NP>
-__device__ __forceinline__ void gateup_group(const uint8_t* __restrict__ gbase, const uint8_t* __restrict__ ubase,
-                                             int FF, int D, int r0, int nm, const int (&tok)[8], const int (&dst)[8],
-                                             const float* __restrict__ xn, float* __restrict__ xs, uint32_t gw,
-                                             Iq3Tab* __restrict__ tab, float* __restrict__ h) {
+__device__ __forceinline__ void gateup_rows(const uint8_t* __restrict__ gbase, const uint8_t* __restrict__ ubase,
+                                            int FF, int D, int r0, int nm, const int (&tok)[8], const int (&dst)[8],
+                                            const float* __restrict__ xn, uint8_t* __restrict__ xs, uint32_t gw,
+                                            Iq3Tab* __restrict__ tab, float* __restrict__ h) {
   constexpr int MG = 2;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane & 31, nsub = D / GM_SUB;
+  const int rbytes = gm_limb_row_bytes(D);
   const int64_t rb = gm_row_bytes(QT, D);
   RowFetch<QT, DC> fg[NP], fu[NP];
-  int rows[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    rows[p] = r0 + 8 * p + 2 * wave + (lane >> 5);
-    const int r = rows[p] < FF ? rows[p] : 0;
+    const int row = r0 + 8 * p + 2 * wave + (lane >> 5);
+    const int r = row < FF ? row : 0;
     fetch_subs<QT, 32, DC>(fg[p], gbase + r * rb, lir, nsub);
     fetch_subs<QT, 32, DC>(fu[p], ubase + r * rb, lir, nsub);
   }
@@ -130,7 +131,7 @@ __device__ __forceinline__ void gateup_group(const uint8_t* __restrict__ gbase, 
     load_x<MG, DC>(xr, xn, gt, ng, D, nullptr);
     if (g0 > 0) __syncthreads();                             // previous group's reads are done
     else if constexpr (QT == GM_QTYPE_IQ3_XXS) gm_iq3_tab_store(gw, tab);
-    stage_x_regs<MG, DC>(xr, ng, D, nullptr, 0.f, xs, nullptr);
+    stage_limbs_regs<MG, DC>(xr, ng, D, nullptr, 0.f, xs, nullptr);
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       opaque(fg[p]);
@@ -138,8 +139,9 @@ __device__ __forceinline__ void gateup_group(const uint8_t* __restrict__ gbase, 
       float ag[MG], au[MG];
 #pragma unroll
       for (int m = 0; m < MG; ++m) { ag[m] = 0.f; au[m] = 0.f; }
-      dot_subs<QT, 32, DC, MG>(fg[p], lir, nsub, xs, D, idx, ng, tab, ag);
-      dot_subs<QT, 32, DC, MG>(fu[p], lir, nsub, xs, D, idx, ng, tab, au);
+      dot_subs_i8<QT, 32, DC, MG>(fg[p], lir, nsub, xs, rbytes, idx, ng, tab, ag);
+      dot_subs_i8<QT, 32, DC, MG>(fu[p], lir, nsub, xs, rbytes, idx, ng, tab, au);
+      const int row = r0 + 8 * p + 2 * wave + (lane >> 5);
 #pragma unroll
       for (int m = 0; m < MG; ++m) {
         if (m < ng) {
@@ -147,7 +149,7 @@ __device__ __forceinline__ void gateup_group(const uint8_t* __restrict__ gbase, 
           int d = dst[0];
 #pragma unroll
           for (int q = 1; q < 8; ++q) d = g0 + m == q ? dst[q] : d;
-          if (rows[p] < FF && lir == 0) h[(int64_t)d * FF + rows[p]] = hv;
+          if (row < FF && lir == 0) h[(int64_t)d * FF + row] = hv;
         }
       }
       issue_fence();                                           // one pass's decoded rows live at a time
@@ -155,25 +157,27 @@ __device__ __forceinline__ void gateup_group(const uint8_t* __restrict__ gbase, 
   }
 }
 
-// Block = (unit u, 8 rows).  Units 0 .. nu-1 are the unique routed experts
-// (members from the grouping table), unit nu the shared expert (all T tokens,
-// h rows after the routed ones).  sh_mode 0: routed units, plus the shared
-// unit when its format is QT; sh_mode 1: the shared unit only (its own format).
+// Blocks [0, n_sh): the shared expert (all T tokens, h rows after the routed
+// ones); blocks [n_sh, ...): unit (b - n_sh) / n_rg of the unique routed
+// experts (members from the grouping table); 8 kGuPasses rows per block.  The
+// launcher sets n_sh = 0 when the shared expert is in another format, and
+// launches its blocks separately with that format.
+constexpr int kGuPasses = 2;
+
 template <int QT, int DC>
 __global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const float* __restrict__ xn, int T,
                                                      const int32_t* __restrict__ g_grp, float* __restrict__ h,
-                                                     int n_chunks, int sh_mode) {
+                                                     int n_sh, int n_rg) {
   constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
-  extern __shared__ float smem[];
-  float* xs = smem;                                            // [2][D] interleaved (+ 4)
-  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(smem + 2 * P.D + 4); // IQ3 only
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* xs = smem;                                          // 2 limb rows (+ a spare sub-block)
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(smem + 2 * gm_limb_row_bytes(P.D) + GM_LSUB);   // IQ3 only
   const int D = P.D, k = P.k, FF = P.FF, Ptot = T * k;
   const int nu = g_grp[0];
-  const int u = sh_mode ? nu : (int)blockIdx.x / n_chunks;
-  const int chunk = (int)blockIdx.x - (sh_mode ? 0 : u * n_chunks);
-  const bool shared = u == nu;
-  const bool sh_here = P.gate_sh != nullptr && (sh_mode || P.q_gate_sh == QT);
-  if (u > nu || (shared && !sh_here)) return;                  // uniform per block
+  const bool shared = (int)blockIdx.x < n_sh;
+  const int u = shared ? nu : ((int)blockIdx.x - n_sh) / n_rg;
+  const int chunk = shared ? (int)blockIdx.x : (int)blockIdx.x - n_sh - u * n_rg;
+  if (u > nu || (!shared && u == nu)) return;                  // uniform per block
   uint32_t gw = 0;
   if constexpr (IQ3) gw = gm_iq3_tab_load();
   const int64_t rb = gm_row_bytes(QT, D);
@@ -197,14 +201,14 @@ __global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const float
       tok[m] = dst[m] / k;
     }
   }
-  gateup_group<QT, DC, 1>(gbase, ubase, FF, D, chunk * 8, nm, tok, dst, xn, xs, gw, tab, h);
+  gateup_rows<QT, DC, kGuPasses>(gbase, ubase, FF, D, chunk * 8 * kGuPasses, nm, tok, dst, xn, xs, gw, tab, h);
 }
 
 template <int QT, int QTS, int DC>
 int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s) {
   if (fast1) {
     const int n_chunks = (P->FF + 7) / 8;
-    const size_t smem = ((size_t)P->D + 4) * 4 + (QT == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+    const size_t smem = (size_t)gm_limb_row_bytes(P->D) + GM_LSUB + (QT == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
     if (int rc = gm_set_smem(k_dec_gateup1<QT, DC, 4>, smem)) return rc;
     if (int rc = gm_set_smem(k_dec_gateup1<QT, DC, 8>, smem)) return rc;
     if (P->E <= 256)
@@ -221,20 +225,23 @@ int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const Gm
   else
     hipLaunchKernelGGL(k_dec_route<8>, dim3(1), dim3(512), 0, s, a.logits, T, P->E, P->k, a.ids, a.wts, a.grp);
   GM_TRY(hipGetLastError());
-  const int n_chunks = (P->FF + 7) / 8;
-  const int max_u = (T * P->k < P->E ? T * P->k : P->E) + 1;      // + the shared expert
+  const int n_rg = (P->FF + 8 * kGuPasses - 1) / (8 * kGuPasses);  // blocks per unit
+  const int n_sh = P->gate_sh ? n_rg : 0;
+  const int max_u = T * P->k < P->E ? T * P->k : P->E;
+  const bool sh_own = P->gate_sh && P->q_gate_sh != QT;            // shared expert in its own format
   {
-    const size_t smem = (2 * (size_t)P->D + 4) * 4 + (QT == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+    const size_t smem = 2 * (size_t)gm_limb_row_bytes(P->D) + GM_LSUB + (QT == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+    const int nsh = sh_own ? 0 : n_sh;
     if (int rc = gm_set_smem(k_dec_gateup8<QT, DC>, smem)) return rc;
-    hipLaunchKernelGGL((k_dec_gateup8<QT, DC>), dim3(max_u * n_chunks), dim3(256), smem, s, *P, a.xn, T, a.grp,
-                       a.h, n_chunks, 0);
+    hipLaunchKernelGGL((k_dec_gateup8<QT, DC>), dim3(nsh + max_u * n_rg), dim3(256), smem, s, *P, a.xn, T, a.grp,
+                       a.h, nsh, n_rg);
     GM_TRY(hipGetLastError());
   }
-  if (P->gate_sh && P->q_gate_sh != QT) {                         // shared expert in its own format
-    const size_t smem = (2 * (size_t)P->D + 4) * 4 + (QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+  if (sh_own) {
+    const size_t smem = 2 * (size_t)gm_limb_row_bytes(P->D) + GM_LSUB + (QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
     if (int rc = gm_set_smem(k_dec_gateup8<QTS, DC>, smem)) return rc;
-    hipLaunchKernelGGL((k_dec_gateup8<QTS, DC>), dim3(n_chunks), dim3(256), smem, s, *P, a.xn, T, a.grp, a.h,
-                       n_chunks, 1);
+    hipLaunchKernelGGL((k_dec_gateup8<QTS, DC>), dim3(n_sh), dim3(256), smem, s, *P, a.xn, T, a.grp, a.h, n_sh,
+                       n_rg);
   }
   GM_TRY(hipGetLastError());
   return GM_OK;
