@@ -48,7 +48,6 @@ GmMoeWs gm_moe_ws_layout(const gm_moe_layer* L, int T) {
   w.h = o; o = o + Tz * k * (size_t)L->FF * 4;     // FF % 256 == 0: h_sh starts 256-byte aligned
   w.hsh = o; o = align256(o + Tz * (size_t)(L->FF_sh > 0 ? L->FF_sh : 0) * 4);
   w.yp = o; o = align256(o + (T <= GM_DECODE_MAX_T ? (Tz * k + Tz) * (size_t)L->D * 4 : 0));
-  w.xn = o; o = align256(o + (T <= GM_DECODE_MAX_T ? Tz * (size_t)L->D * 4 : 0));
   w.counters = o; o = align256(o + 256);
   w.pre = o; o = align256(o + gm_prefill_scratch_bytes(L, T));     // every T: gm_moe_prefill takes any T
   w.total = o;

@@ -332,6 +332,54 @@ __device__ __forceinline__ uint32_t gm_pack_lo4(int a, int b, int c, int d) {
   return lo | hi;
 }
 
+// rne(v * up) and its three limb bytes, packed per plane for 4 values.
+__device__ __forceinline__ void gm_limb_planes(gm_f32x4 v, float up, uint32_t& p0, uint32_t& p1, uint32_t& p2) {
+  int q[4];
+  const float f[4] = {v.x * up, v.y * up, v.z * up, v.w * up};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q[i] = __float_as_int(f[i] + 12582912.0f) - 0x4B400000;   // rne, |f| < 2^22
+  int t1[4], t2[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { t1[i] = (q[i] + 128) >> 8; t2[i] = (t1[i] + 128) >> 8; }
+  p0 = gm_pack_lo4(q[0], q[1], q[2], q[3]);
+  p1 = gm_pack_lo4(t1[0], t1[1], t1[2], t1[3]);
+  p2 = gm_pack_lo4(t2[0], t2[1], t2[2], t2[3]);
+}
+
+// Exponent E (|a| < 2^E for the block max m, clamped below at -100) and the
+// quantisation factor 2^(22 - E) / sub-block scale 2^(E - 22); NaN scale for
+// a non-finite m.
+__device__ __forceinline__ void gm_limb_scale(float m, float& up, float& scale) {
+  const int E = m > 0.f && m <= 3.4e38f ? max(__builtin_amdgcn_frexp_expf(m), -100) : 0;
+  up = __builtin_ldexpf(1.0f, 22 - E);
+  scale = m <= 3.4e38f ? __builtin_ldexpf(1.0f, E - 22) : __builtin_nanf("");
+}
+
+__device__ __forceinline__ float gm_absmax4(gm_f32x4 v) {
+  const float ax = fabsf(v.x), ay = fabsf(v.y), az = fabsf(v.z), aw = fabsf(v.w);
+  const bool fin = ax <= 3.4e38f && ay <= 3.4e38f && az <= 3.4e38f && aw <= 3.4e38f;
+  return fin ? fmaxf(fmaxf(ax, ay), fmaxf(az, aw)) : __builtin_inff();
+}
+
+// Limbs of activations 4c .. 4c+7 (c even) of a row into `row`: as
+// gm_put_limbs4 with 4 lanes per sub-block (lanes 4j .. 4j+3, c / 2 % 4 ==
+// lane % 4).
+__device__ __forceinline__ void gm_put_limbs8(gm_f32x4 a, gm_f32x4 b, int c, uint8_t* __restrict__ row) {
+  float m = fmaxf(gm_absmax4(a), gm_absmax4(b));
+  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_1032));
+  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_2301));
+  float up, scale;
+  gm_limb_scale(m, up, scale);
+  uint32_t a0, a1, a2, b0, b1, b2;
+  gm_limb_planes(a, up, a0, a1, a2);
+  gm_limb_planes(b, up, b0, b1, b2);
+  uint8_t* sb = row + (c >> 3) * GM_LSUB + 4 * (c & 7);
+  *reinterpret_cast<uint2*>(sb) = make_uint2(a0, b0);
+  *reinterpret_cast<uint2*>(sb + 32) = make_uint2(a1, b1);
+  *reinterpret_cast<uint2*>(sb + 64) = make_uint2(a2, b2);
+  *reinterpret_cast<float*>(row + (c >> 3) * GM_LSUB + 96) = scale;     // same value from all 4 lanes
+}
+
 // Limbs of activations 4c .. 4c+3 of a row into `row` (limb layout).  The 8
 // lanes holding the float4s of one sub-block must be lanes 8j .. 8j+7 of one
 // wave (c % 8 == lane % 8), all executing this call (store to a spare
@@ -477,7 +525,9 @@ struct XRegs {
   gm_f32x4 w[XPT];
 };
 
-// Rows tok[m], m < nt (uniform), of x [.][D]; loads of rows past nt are skipped.
+// Rows tok[m], m < nt, of x [.][D]; rows past nt re-load row tok[0] (the
+// loads stay unconditional and straight-line: a load under a branch would
+// end in a full wait at the join).
 template <int NT, int XPT>
 __device__ __forceinline__ void load_x(XRegs<NT, XPT>& r, const float* __restrict__ x, const int (&tok)[NT], int nt,
                                        int D, const float* __restrict__ norm_w) {
@@ -485,12 +535,11 @@ __device__ __forceinline__ void load_x(XRegs<NT, XPT>& r, const float* __restric
   const gm_f32x4* x4 = reinterpret_cast<const gm_f32x4*>(x);
 #pragma unroll
   for (int m = 0; m < NT; ++m) {
-    if (m < nt) {
+    const int t = m < nt ? tok[m] : tok[0];
 #pragma unroll
-      for (int i = 0; i < XPT; ++i) {
-        const int c = threadIdx.x + 256 * i;
-        r.v[m][i] = x4[(int64_t)tok[m] * nq + (c < nq ? c : nq - 1)];
-      }
+    for (int i = 0; i < XPT; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      r.v[m][i] = x4[(int64_t)t * nq + (c < nq ? c : nq - 1)];
     }
   }
   if (norm_w != nullptr) {

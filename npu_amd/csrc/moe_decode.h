@@ -13,8 +13,14 @@ struct GmDecArgs {
   float* h;         // [T * k][FF], directly followed by hsh
   float* hsh;       // [T][FF]
   float* yp;        // [T * k + T][D] per-pair / shared partial outputs (general path)
-  float* xn;        // [T][D] RMSNorm'd input (general path)
+  float* part;      // [D / 512][T][gm_dec_part_ld] router partials (general path, inside yp)
+  float* ssq;       // [D / 512][T] partial sums of x^2 (general path, inside yp)
+  float* rms;       // [T] RMSNorm factors (general path, inside yp)
+  uint8_t* xl;      // [T + 1] limb rows of x w_norm (general path, inside yp)
 };
+
+// Row stride of the router partials: E rows + the shared gate row, padded to 4.
+inline int gm_dec_part_ld(const gm_moe_layer* P) { return (P->E + 1 + 3) & ~3; }
 
 // Weight-row chunk sizes: D and FF in units of 1024 and 512 elements.
 inline int gm_dec_dc(int D) { return D <= 1024 ? 1 : D <= 2048 ? 2 : 4; }

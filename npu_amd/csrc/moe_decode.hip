@@ -1,11 +1,13 @@
 // MoE block, decode path (T <= 8 tokens).  Reference semantics:
 // qwen/forward.py:563-665 (moe_forward).
 //
-// Stage 1  k_dec_router   router logits (bf16 W, fp32 RMSNorm'd x), the shared
-//                         scalar gate, and (T = 1 kernels) the shared expert's
-//                         gate/up + SwiGLU; none of it depends on the routing.
-//                         For the grouped T > 1 kernels it publishes xn instead
-//                         and the shared expert runs with the routed ones.
+// Stage 1  T = 1: k_dec_router: router logits (bf16 W, fp32 RMSNorm'd x), the
+//                         shared scalar gate, and the shared expert's gate/up +
+//                         SwiGLU; none of it depends on the routing.
+//          T > 1: k_dec_router_ks: partial router dot products over K ranges
+//                         (the routing kernel of stage 2 sums them and applies
+//                         the RMSNorm factor); the shared expert runs with the
+//                         routed ones.
 // Stage 2  (moe_decode_gu.hip) top-k, expert grouping, routed gate/up + SwiGLU.
 // Stage 3  (moe_decode_dn.hip) down projections, weighted combine in ascending
 //                         expert order, + sigmoid-gated shared expert (+ x).
@@ -26,7 +28,7 @@ namespace {
 template <int QTS, int NT, int DC>
 __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float* __restrict__ x, int T,
                                                     float* __restrict__ logits, float* __restrict__ shg,
-                                                    float* __restrict__ hsh, float* __restrict__ xn, int n_rb) {
+                                                    float* __restrict__ hsh, int n_rb) {
   constexpr int SPLR = DC > 1 ? DC / 2 : 1;
   constexpr bool IQ3 = QTS == GM_QTYPE_IQ3_XXS;
   extern __shared__ float smem[];
@@ -51,15 +53,6 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
     fetch_subs<GM_QTYPE_BF16, 64, SPLR>(f, wr, lane, nsub);
     issue_fence();
     stage_x_regs<NT, DC>(xr, T, D, P.norm_w, P.norm_eps, xs, red);
-    if (xn != nullptr && blockIdx.x == 0) {                    // publish xn [T][D] for the grouped kernels
-      const int nq = D >> 2;
-      const gm_f32x4* xs4 = reinterpret_cast<const gm_f32x4*>(xs);
-      gm_f32x4* xn4 = reinterpret_cast<gm_f32x4*>(xn);
-      for (int i = threadIdx.x; i < T * nq; i += 256) {
-        const int t = i / nq, c = i - t * nq;
-        xn4[i] = xs4[t * nq + il_index4(c & 7, c >> 3, nsub)];
-      }
-    }
     float acc[NT];
 #pragma unroll
     for (int m = 0; m < NT; ++m) acc[m] = 0.f;
@@ -102,8 +95,73 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
   }
 }
 
-// with_shared: the shared expert's gate/up run here (T = 1 kernels); otherwise
-// they run with the routed experts in k_dec_gateup8 and this kernel publishes xn.
+// T > 1: partial router dot products over K ranges, part[z][t][r] =
+// sum_{k in range z} (x[t][k] w_norm[k]) W[r][k] (row E: the shared gate
+// vector) and ssq[z][t] = sum_{k in range z} x[t][k]^2, so that no block loads
+// more than its range of the T input rows; k_dec_route applies the RMSNorm
+// factor (qwen/forward.py:58-61) to the summed partials.  Block = 4 rows (one
+// per wave) x one range of kr = min(D, 512) values; lane l takes k = 8l .. 8l+7.
+// Wave 0 of the first row block of each range also writes the limb rows of
+// x w_norm for the range (the RMSNorm factor is applied to the dot products
+// instead), so the grouped gate/up kernel only copies them.
+template <int NT>
+__global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const float* __restrict__ x, int T,
+                                                       float* __restrict__ part, float* __restrict__ ssq, int ldp,
+                                                       uint8_t* __restrict__ xl) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int D = P.D, E = P.E, nrows = E + (P.sh_gate_inp != nullptr ? 1 : 0);
+  const int kr = D < 512 ? D : 512, z = blockIdx.y, k0 = z * kr + 8 * lane;
+  const bool lv = 8 * lane < kr;
+  const int kk = lv ? k0 : z * kr;                              // lanes past the range re-read its start
+  const int row = blockIdx.x * 4 + wave;
+  const uint16_t* wr = row < E ? P.router + (int64_t)row * D : (row < nrows ? P.sh_gate_inp : P.router);
+  const gm_u32x4 wb = *reinterpret_cast<const gm_u32x4*>(wr + kk);        // 8 bf16
+  gm_f32x4 nw0 = {1.f, 1.f, 1.f, 1.f}, nw1 = nw0;
+  if (P.norm_w) {
+    nw0 = *reinterpret_cast<const gm_f32x4*>(P.norm_w + kk);
+    nw1 = *reinterpret_cast<const gm_f32x4*>(P.norm_w + kk + 4);
+  }
+  gm_f32x4 xa[NT], xb[NT];
+#pragma unroll
+  for (int m = 0; m < NT; ++m) {
+    const int t = m < T ? m : 0;
+    xa[m] = *reinterpret_cast<const gm_f32x4*>(x + (int64_t)t * D + kk);
+    xb[m] = *reinterpret_cast<const gm_f32x4*>(x + (int64_t)t * D + kk + 4);
+  }
+  const float w[8] = {gm_bf2f(wb.x & 0xffffu), gm_bf2f(wb.x >> 16), gm_bf2f(wb.y & 0xffffu), gm_bf2f(wb.y >> 16),
+                      gm_bf2f(wb.z & 0xffffu), gm_bf2f(wb.z >> 16), gm_bf2f(wb.w & 0xffffu), gm_bf2f(wb.w >> 16)};
+  if (blockIdx.x == 0 && wave == 0) {                           // uniform per wave
+    const int rbytes = gm_limb_row_bytes(D);
+#pragma unroll
+    for (int m = 0; m < NT; ++m) {
+      if (m < T) {
+        gm_f32x4 a = xa[m], b = xb[m];
+        a.x *= nw0.x; a.y *= nw0.y; a.z *= nw0.z; a.w *= nw0.w;
+        b.x *= nw1.x; b.y *= nw1.y; b.z *= nw1.z; b.w *= nw1.w;
+        // lanes past the range write a spare row (row T), quads stay whole
+        gm_put_limbs8(a, b, lv ? kk >> 2 : (kk >> 2) & 7, xl + (lv ? m : T) * rbytes);
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < NT; ++m) {
+    if (m < T) {                                                // uniform
+      const float xv[8] = {xa[m].x, xa[m].y, xa[m].z, xa[m].w, xb[m].x, xb[m].y, xb[m].z, xb[m].w};
+      const float nv[8] = {nw0.x, nw0.y, nw0.z, nw0.w, nw1.x, nw1.y, nw1.z, nw1.w};
+      float d = 0.f, q = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { d = fmaf(xv[i] * nv[i], w[i], d); q = fmaf(xv[i], xv[i], q); }
+      d = gm_wave_sum64(lv ? d : 0.f);
+      if (lane == 0 && row < nrows) part[((int64_t)z * T + m) * ldp + row] = d;
+      if (blockIdx.x == 0 && wave == 0) {
+        q = gm_wave_sum64(lv ? q : 0.f);
+        if (lane == 0) ssq[z * T + m] = q;
+      }
+    }
+  }
+}
+
+// with_shared: the shared expert's gate/up run here as well.
 template <int QTS, int NT, int DC>
 int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s,
                     bool with_shared) {
@@ -113,7 +171,7 @@ int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArg
   const size_t smem = ((size_t)NT * P->D + 4 + 4 * NT) * 4 + (QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
   if (int rc = gm_set_smem(k_dec_router<QTS, NT, DC>, smem)) return rc;
   hipLaunchKernelGGL((k_dec_router<QTS, NT, DC>), dim3(n_rb + n_sb), dim3(256), smem, s, *P, x, T, a.logits, a.shg,
-                     a.hsh, with_shared ? nullptr : a.xn, n_rb);
+                     a.hsh, n_rb);
   GM_TRY(hipGetLastError());
   return GM_OK;
 }
@@ -128,7 +186,14 @@ int launch_router_n(const gm_moe_layer* P, const float* x, int T, const GmDecArg
 }
 
 int launch_router(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s, bool fast1) {
-  if (!fast1) return launch_router_n<GM_QTYPE_IQ4_XS, 8>(P, x, T, a, s, false);   // router rows only
+  if (!fast1) {                                                      // router partials only
+    const int nrows = P->E + (P->sh_gate_inp ? 1 : 0);
+    const int kr = P->D < 512 ? P->D : 512;
+    hipLaunchKernelGGL(k_dec_router_ks<8>, dim3((nrows + 3) / 4, P->D / kr), dim3(256), 0, s, *P, x, T, a.part,
+                       a.ssq, gm_dec_part_ld(P), a.xl);
+    GM_TRY(hipGetLastError());
+    return GM_OK;
+  }
   if (!P->gate_sh) return launch_router_n<GM_QTYPE_IQ4_XS, 1>(P, x, T, a, s, true);
   switch (P->q_gate_sh) {
     case GM_QTYPE_IQ4_XS: return launch_router_n<GM_QTYPE_IQ4_XS, 1>(P, x, T, a, s, true);
@@ -156,7 +221,14 @@ int gm_dec_run(const gm_moe_layer* P, const float* x, float* y, int T, int flags
   a.h = reinterpret_cast<float*>(ws + lay.h);
   a.hsh = reinterpret_cast<float*>(ws + lay.hsh);
   a.yp = reinterpret_cast<float*>(ws + lay.yp);
-  a.xn = reinterpret_cast<float*>(ws + lay.xn);
+  // general path: router partials, x^2 partials, RMSNorm factors and the limb
+  // rows of x w_norm live in yp, which stage 3 overwrites only after stage 2
+  a.part = a.yp;
+  a.ssq = a.part + (size_t)(P->D / (P->D < 512 ? P->D : 512)) * T * gm_dec_part_ld(P);
+  a.rms = a.ssq + 8 * T;
+  a.xl = reinterpret_cast<uint8_t*>(a.rms + 16);
+  if (a.xl + (size_t)(T + 1) * gm_limb_row_bytes(P->D) > reinterpret_cast<uint8_t*>(a.yp + (size_t)(T * P->k + T) * P->D))
+    return gm_fail_arg("gm_moe_forward: internal workspace layout error (yp)");
   if (a.hsh != a.h + (size_t)T * P->k * P->FF) return gm_fail_arg("gm_moe_forward: internal workspace layout error");
   // The T = 1 down kernel stages (k + 1) rows of FF activations per block and
   // maps a wave's lanes onto 8 rows x FF/32 sub-blocks (FF/32 in {8, 16, 32}).

@@ -10,7 +10,8 @@
 // T > 1: k_dec_route (one block) runs the per-token top-k and groups the
 // (token, slot) pairs by expert; k_dec_gateup8 then runs (unit, 16-row chunk)
 // blocks, a unit being a unique routed expert over its member tokens only or
-// the shared expert over all T tokens, reading the RMSNorm'd xn of stage 1.
+// the shared expert over all T tokens, reading the limb rows of x that stage 1
+// wrote and the RMSNorm factors of the routing kernel.
 #include "moe_common.h"
 #include "moe_decode.h"
 
@@ -77,37 +78,93 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
   if (live && (lane & 31) == 0) h[(int64_t)pair * FF + row] = hv;
 }
 
-// One block: top-k of every token (wave t -> token t) and the grouping table.
+// One block: the router logits of every token from the partial sums of
+// k_dec_router_ks (fixed order), times the token's RMSNorm factor
+// 1 / sqrt(mean(x^2) + eps) (qwen/forward.py:58-61), + bias; the shared gate
+// sigmoid; the top-k (wave t -> token t) and the grouping table.
 template <int MAXV>
-__global__ void __launch_bounds__(512) k_dec_route(const float* __restrict__ logits, int T, int E, int k,
+__global__ void __launch_bounds__(512) k_dec_route(gm_moe_layer P, const float* __restrict__ part,
+                                                   const float* __restrict__ ssq, int nz, int ldp, int T,
+                                                   float* __restrict__ rmsv, float* __restrict__ logits,
+                                                   float* __restrict__ shg,
                                                    int32_t* __restrict__ g_ids, float* __restrict__ g_wts,
                                                    int32_t* __restrict__ g_grp) {
   __shared__ int32_t ids[64];
   __shared__ float wts[64];
   __shared__ int32_t grp[GM_GRP_WORDS];
   __shared__ uint32_t bits[16];
-  const int wave = threadIdx.x >> 6;
-  if (wave < T) wave_topk<MAXV>(logits + (int64_t)wave * E, E, k, ids + wave * k, wts + wave * k);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int E = P.E, k = P.k;
+  if (wave < T) {
+    // every partial is loaded before any is summed (nz <= 8; a load in a
+    // runtime loop would wait before the next one is issued)
+    float pv[MAXV][8], ps[8], pg[8];
+#pragma unroll
+    for (int z = 0; z < 8; ++z) {
+      const int zz = z < nz ? z : nz - 1;
+      const float* pz = part + ((int64_t)zz * T + wave) * ldp;
+#pragma unroll
+      for (int i = 0; i < MAXV; ++i) {
+        const int r = lane + 64 * i;
+        pv[i][z] = pz[r < E ? r : E - 1];
+      }
+      ps[z] = ssq[zz * T + wave];
+      pg[z] = pz[E];
+    }
+    float rms = 1.f;
+    if (P.norm_w) {
+      float q = 0.f;
+#pragma unroll
+      for (int z = 0; z < 8; ++z) q += z < nz ? ps[z] : 0.f;
+      rms = 1.0f / sqrtf(q / (float)P.D + P.norm_eps);
+    }
+    if (lane == 0) rmsv[wave] = rms;
+    float v[MAXV];
+    int ix[MAXV];
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+      ix[i] = lane + 64 * i;
+      const int r = ix[i] < E ? ix[i] : E - 1;
+      float a = 0.f;
+#pragma unroll
+      for (int z = 0; z < 8; ++z) a += z < nz ? pv[i][z] : 0.f;
+      v[i] = rms * a + (P.router_bias ? P.router_bias[r] : 0.f);
+      if (ix[i] < E) logits[(int64_t)wave * E + ix[i]] = v[i];
+    }
+    if (P.sh_gate_inp && lane == 0) {
+      float a = 0.f;
+#pragma unroll
+      for (int z = 0; z < 8; ++z) a += z < nz ? pg[z] : 0.f;
+      shg[wave] = gm_sigmoid(rms * a);
+    }
+    int id;
+    float w;
+    topk_finish<MAXV>(v, ix, E, k, id, w);
+    if (lane < k) { ids[wave * k + lane] = id; wts[wave * k + lane] = w; }
+  }
   __syncthreads();
   block_group(ids, T * k, E, grp, bits);
   for (int i = threadIdx.x; i < T * k; i += blockDim.x) { g_ids[i] = ids[i]; g_wts[i] = wts[i]; }
   for (int i = threadIdx.x; i < GM_GRP_WORDS; i += blockDim.x) g_grp[i] = grp[i];
 }
 
-// Rows r0 .. r0 + 8 NP - 1 of one gate/up pair for nm member tokens (xn rows
-// tok[m], h rows dst[m]): all NP passes' raw rows are fetched first (wave w,
-// pass p -> rows r0 + 8p + 2w + (lane >> 5), 32 lanes per row), then the
-// members are staged MG = 2 at a time in LDS (most routed units have one
-// member; the shared unit takes T / 2 groups) and every pass is decoded.
+// Rows r0 .. r0 + 8 NP - 1 of one gate/up pair for nm member tokens (limb
+// rows tok[m] of x w_norm in xl, RMSNorm factors rmsv; h rows dst[m]): all NP
+// passes' raw rows are fetched first (wave w, pass p -> rows r0 + 8p + 2w +
+// (lane >> 5), 32 lanes per row), then the members' limb rows are copied to
+// LDS MG = 2 at a time (most routed units have one member; the shared unit
+// takes T / 2 groups) and every pass is decoded.
 template <int QT, int DC, int NP>
 __device__ __forceinline__ void gateup_rows(const uint8_t* __restrict__ gbase, const uint8_t* __restrict__ ubase,
                                             int FF, int D, int r0, int nm, const int (&tok)[8], const int (&dst)[8],
-                                            const float* __restrict__ xn, uint8_t* __restrict__ xs, uint32_t gw,
-                                            Iq3Tab* __restrict__ tab, float* __restrict__ h) {
+                                            const uint8_t* __restrict__ xl, const float* __restrict__ rmsv,
+                                            uint8_t* __restrict__ xs, uint32_t gw, Iq3Tab* __restrict__ tab,
+                                            float* __restrict__ h) {
   constexpr int MG = 2;
+  constexpr int CPT = (MG * 32 * DC * GM_LSUB / 16 + 255) / 256;   // 16-byte chunks per thread (D <= 1024 DC)
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane & 31, nsub = D / GM_SUB;
-  const int rbytes = gm_limb_row_bytes(D);
   const int64_t rb = gm_row_bytes(QT, D);
+  const int rbytes = gm_limb_row_bytes(D), rch = rbytes >> 4;
   RowFetch<QT, DC> fg[NP], fu[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
@@ -118,6 +175,7 @@ __device__ __forceinline__ void gateup_rows(const uint8_t* __restrict__ gbase, c
   }
   for (int g0 = 0; g0 < nm; g0 += MG) {                      // usually one group
     int gt[MG], idx[MG];
+    float rs[MG];
 #pragma unroll
     for (int m = 0; m < MG; ++m) {
       int t = tok[0];
@@ -125,13 +183,24 @@ __device__ __forceinline__ void gateup_rows(const uint8_t* __restrict__ gbase, c
       for (int q = 1; q < 8; ++q) t = g0 + m == q ? tok[q] : t;
       gt[m] = t;
       idx[m] = m;
+      rs[m] = rmsv[t];
     }
     const int ng = nm - g0 < MG ? nm - g0 : MG;
-    XRegs<MG, DC> xr;
-    load_x<MG, DC>(xr, xn, gt, ng, D, nullptr);
+    gm_u32x4 cp[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + 256 * i;                   // chunk c of the ng rows
+      const int m = c < ng * rch ? c / rch : 0, cc = c < ng * rch ? c - m * rch : 0;
+      cp[i] = reinterpret_cast<const gm_u32x4*>(xl + (int64_t)(m == 0 ? gt[0] : gt[1]) * rbytes)[cc];
+    }
     if (g0 > 0) __syncthreads();                             // previous group's reads are done
     else if constexpr (QT == GM_QTYPE_IQ3_XXS) gm_iq3_tab_store(gw, tab);
-    stage_limbs_regs<MG, DC>(xr, ng, D, nullptr, 0.f, xs, nullptr);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      reinterpret_cast<gm_u32x4*>(xs)[c < ng * rch ? c : MG * rch] = cp[i];   // past the rows: spare chunk
+    }
+    __syncthreads();
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       opaque(fg[p]);
@@ -145,7 +214,7 @@ __device__ __forceinline__ void gateup_rows(const uint8_t* __restrict__ gbase, c
 #pragma unroll
       for (int m = 0; m < MG; ++m) {
         if (m < ng) {
-          const float hv = gm_silu(row_sum<32>(ag[m])) * row_sum<32>(au[m]);
+          const float hv = gm_silu(rs[m] * row_sum<32>(ag[m])) * (rs[m] * row_sum<32>(au[m]));
           int d = dst[0];
 #pragma unroll
           for (int q = 1; q < 8; ++q) d = g0 + m == q ? dst[q] : d;
@@ -165,7 +234,8 @@ __device__ __forceinline__ void gateup_rows(const uint8_t* __restrict__ gbase, c
 constexpr int kGuPasses = 2;
 
 template <int QT, int DC>
-__global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const float* __restrict__ xn, int T,
+__global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const uint8_t* __restrict__ xl,
+                                                     const float* __restrict__ rmsv, int T,
                                                      const int32_t* __restrict__ g_grp, float* __restrict__ h,
                                                      int n_sh, int n_rg) {
   constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
@@ -201,7 +271,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const float
       tok[m] = dst[m] / k;
     }
   }
-  gateup_rows<QT, DC, kGuPasses>(gbase, ubase, FF, D, chunk * 8 * kGuPasses, nm, tok, dst, xn, xs, gw, tab, h);
+  gateup_rows<QT, DC, kGuPasses>(gbase, ubase, FF, D, chunk * 8 * kGuPasses, nm, tok, dst, xl, rmsv, xs, gw, tab, h);
 }
 
 template <int QT, int QTS, int DC>
@@ -220,10 +290,13 @@ int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const Gm
     GM_TRY(hipGetLastError());
     return GM_OK;
   }
+  const int nz = P->D / (P->D < 512 ? P->D : 512);
   if (P->E <= 256)
-    hipLaunchKernelGGL(k_dec_route<4>, dim3(1), dim3(512), 0, s, a.logits, T, P->E, P->k, a.ids, a.wts, a.grp);
+    hipLaunchKernelGGL(k_dec_route<4>, dim3(1), dim3(512), 0, s, *P, a.part, a.ssq, nz, gm_dec_part_ld(P), T,
+                       a.rms, a.logits, a.shg, a.ids, a.wts, a.grp);
   else
-    hipLaunchKernelGGL(k_dec_route<8>, dim3(1), dim3(512), 0, s, a.logits, T, P->E, P->k, a.ids, a.wts, a.grp);
+    hipLaunchKernelGGL(k_dec_route<8>, dim3(1), dim3(512), 0, s, *P, a.part, a.ssq, nz, gm_dec_part_ld(P), T,
+                       a.rms, a.logits, a.shg, a.ids, a.wts, a.grp);
   GM_TRY(hipGetLastError());
   const int n_rg = (P->FF + 8 * kGuPasses - 1) / (8 * kGuPasses);  // blocks per unit
   const int n_sh = P->gate_sh ? n_rg : 0;
@@ -233,15 +306,15 @@ int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const Gm
     const size_t smem = 2 * (size_t)gm_limb_row_bytes(P->D) + GM_LSUB + (QT == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
     const int nsh = sh_own ? 0 : n_sh;
     if (int rc = gm_set_smem(k_dec_gateup8<QT, DC>, smem)) return rc;
-    hipLaunchKernelGGL((k_dec_gateup8<QT, DC>), dim3(nsh + max_u * n_rg), dim3(256), smem, s, *P, a.xn, T, a.grp,
-                       a.h, nsh, n_rg);
+    hipLaunchKernelGGL((k_dec_gateup8<QT, DC>), dim3(nsh + max_u * n_rg), dim3(256), smem, s, *P, a.xl, a.rms, T,
+                       a.grp, a.h, nsh, n_rg);
     GM_TRY(hipGetLastError());
   }
   if (sh_own) {
     const size_t smem = 2 * (size_t)gm_limb_row_bytes(P->D) + GM_LSUB + (QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
     if (int rc = gm_set_smem(k_dec_gateup8<QTS, DC>, smem)) return rc;
-    hipLaunchKernelGGL((k_dec_gateup8<QTS, DC>), dim3(n_sh), dim3(256), smem, s, *P, a.xn, T, a.grp, a.h, n_sh,
-                       n_rg);
+    hipLaunchKernelGGL((k_dec_gateup8<QTS, DC>), dim3(n_sh), dim3(256), smem, s, *P, a.xl, a.rms, T, a.grp, a.h,
+                       n_sh, n_rg);
   }
   GM_TRY(hipGetLastError());
   return GM_OK;
