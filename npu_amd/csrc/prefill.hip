@@ -352,14 +352,14 @@ __device__ __forceinline__ uint32_t lut_kvu(uint32_t nib) {
   return __builtin_amdgcn_perm(hi, lo, ((nib >> 1) & 0x04040404u) | 0x03020100u);
 }
 
-// Four unsigned bytes u -> two f16x2 holding (u - 128) * s exactly-then-once-rounded:
-// 0x6400 | u is the f16 1024 + u, and 1024 + u - 1152 is exact.
-__device__ __forceinline__ void u8x4_to_f16(uint32_t u, gm_f16x2 s, uint32_t& o0, uint32_t& o1) {
-  const gm_f16x2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+// Four unsigned bytes u -> two f16x2 holding (u - 128) * s, rounded once:
+// 0x6400 | u is the f16 1024 + u, and fma(1024 + u, s, c) with c = -1152 s
+// (exact in f16 for |s| <= 32: 9 s 2^7) is (u - 128) s in one rounding.
+__device__ __forceinline__ void u8x4_to_f16(uint32_t u, gm_f16x2 s, gm_f16x2 c, uint32_t& o0, uint32_t& o1) {
   const gm_f16x2 a = __builtin_bit_cast(gm_f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
   const gm_f16x2 b = __builtin_bit_cast(gm_f16x2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
-  o0 = __builtin_bit_cast(uint32_t, (a - off) * s);
-  o1 = __builtin_bit_cast(uint32_t, (b - off) * s);
+  o0 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(a, s, c));
+  o1 = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(b, s, c));
 }
 
 // IQ3_XXS sign table for k-step decode: entry i (7-bit ksigns index) holds
@@ -395,13 +395,14 @@ __device__ __forceinline__ void pf_stage_signs_bf16(gm_u32x4* tab) {
 //   IQ3_XXS: slot i -> k = 32s + 8g + i, g = j & 3
 // with s = 2q + (j >> 2).
 template <int QT>
-__device__ __forceinline__ gm_f16x8 a_f16(const PfRaw<QT>& r, int j, gm_f16x2 sc, const uint32_t* __restrict__ grid,
+__device__ __forceinline__ gm_f16x8 a_f16(const PfRaw<QT>& r, int j, gm_f16x2 sc, gm_f16x2 cc,
+                                          const uint32_t* __restrict__ grid,
                                           const gm_u32x4* __restrict__ sgn) {
   uint32_t o[4];
   if constexpr (QT == GM_QTYPE_IQ4_XS) {
     const uint32_t nib = r.q[4 * (j >> 2) + (j & 3)];
-    u8x4_to_f16(lut_kvu(nib & 0x0f0f0f0fu), sc, o[0], o[1]);
-    u8x4_to_f16(lut_kvu((nib >> 4) & 0x0f0f0f0fu), sc, o[2], o[3]);
+    u8x4_to_f16(lut_kvu(nib & 0x0f0f0f0fu), sc, cc, o[0], o[1]);
+    u8x4_to_f16(lut_kvu((nib >> 4) & 0x0f0f0f0fu), sc, cc, o[2], o[3]);
   } else {
     const int sl = j >> 2, g = j & 3;
     const uint32_t qw = r.q[2 * sl + (g >> 1)] >> (16 * (g & 1));
@@ -411,8 +412,8 @@ __device__ __forceinline__ gm_f16x8 a_f16(const PfRaw<QT>& r, int j, gm_f16x2 sc
     // signed magnitude + 128 per byte: |v| <= 62, so no byte carries into the next
     const uint32_t ua = ((ga ^ m.x) + m.z) ^ 0x80808080u;
     const uint32_t ub = ((gb ^ m.y) + m.w) ^ 0x80808080u;
-    u8x4_to_f16(ua, sc, o[0], o[1]);
-    u8x4_to_f16(ub, sc, o[2], o[3]);
+    u8x4_to_f16(ua, sc, cc, o[0], o[1]);
+    u8x4_to_f16(ub, sc, cc, o[2], o[3]);
   }
   return __builtin_bit_cast(gm_f16x8, gm_u32x4{o[0], o[1], o[2], o[3]});
 }
@@ -455,24 +456,22 @@ __device__ __forceinline__ gm_u32x4 b_lds(const uint8_t* __restrict__ row, int q
   return *reinterpret_cast<const gm_u32x4*>(row + 2 * (32 * (2 * q + (j >> 2)) + 8 * (j & 3)));
 }
 
-// One superblock column of the gate and up rows against NT token tiles:
-// f16 integer operands into per-superblock partial sums, then the partial
-// sums times the superblock factor of each accumulator row into ag / au.
-template <int QT, int NT>
-__device__ __forceinline__ void gu_superblock(const PfRaw<QT>& wg, const PfRaw<QT>& wu, int q, int l16,
-                                              const uint8_t* __restrict__ xb, const uint32_t* __restrict__ grid,
-                                              const gm_u32x4* __restrict__ sgn, gm_f32x4 (&ag)[4],
-                                              gm_f32x4 (&au)[4]) {
+// Half H (k-steps 4H .. 4H+3) of one superblock column of the gate and up
+// rows against NT token tiles: f16 integer operands into the superblock's
+// partial sums pg / pu.
+template <int QT, int NT, int H>
+__device__ __forceinline__ void gu_half(const PfRaw<QT>& wg, const PfRaw<QT>& wu, int q, int l16,
+                                        const uint8_t* __restrict__ xb, const uint32_t* __restrict__ grid,
+                                        const gm_u32x4* __restrict__ sgn, gm_f32x4 (&pg)[4], gm_f32x4 (&pu)[4]) {
   const gm_f32x2 sg2 = pf_int_scales<QT>(wg, q), su2 = pf_int_scales<QT>(wu, q);
-  gm_f32x4 pg[NT], pu[NT];
+  const float sgf = H ? sg2.y : sg2.x, suf = H ? su2.y : su2.x;
+  const gm_f16x2 sgh = {(_Float16)sgf, (_Float16)sgf}, suh = {(_Float16)suf, (_Float16)suf};
+  const gm_f16x2 cgh = {(_Float16)(-1152.f * sgf), (_Float16)(-1152.f * sgf)};
+  const gm_f16x2 cuh = {(_Float16)(-1152.f * suf), (_Float16)(-1152.f * suf)};
 #pragma unroll
-  for (int t = 0; t < NT; ++t) { pg[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; pu[t] = pg[t]; }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float sgf = j < 4 ? sg2.x : sg2.y, suf = j < 4 ? su2.x : su2.y;
-    const gm_f16x2 sgh = {(_Float16)sgf, (_Float16)sgf}, suh = {(_Float16)suf, (_Float16)suf};
-    const gm_f16x8 A = a_f16<QT>(wg, j, sgh, grid, sgn);
-    const gm_f16x8 U = a_f16<QT>(wu, j, suh, grid, sgn);
+  for (int j = 4 * H; j < 4 * H + 4; ++j) {
+    const gm_f16x8 A = a_f16<QT>(wg, j, sgh, cgh, grid, sgn);
+    const gm_f16x8 U = a_f16<QT>(wu, j, suh, cuh, grid, sgn);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const gm_f16x8 B = __builtin_bit_cast(gm_f16x8, b_lds(xb + (t * 16 + l16) * kPitchB, q, j));
@@ -481,7 +480,13 @@ __device__ __forceinline__ void gu_superblock(const PfRaw<QT>& wg, const PfRaw<Q
     }
     if (j & 1) issue_fence();                          // two k-steps' operands live at a time
   }
-  // superblock factors of the 4 accumulator rows 4q + i (held by lanes 4q + i)
+}
+
+// The superblock's partial sums times the superblock factor of each
+// accumulator row (rows 4q + i, whose factors lanes 4q + i hold) into ag / au.
+template <int QT, int NT>
+__device__ __forceinline__ void gu_fold(const PfRaw<QT>& wg, const PfRaw<QT>& wu, int q, const gm_f32x4 (&pg)[4],
+                                        const gm_f32x4 (&pu)[4], gm_f32x4 (&ag)[4], gm_f32x4 (&au)[4]) {
   const float dgl = pf_dscale<QT>(wg), dul = pf_dscale<QT>(wu);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -515,16 +520,18 @@ __device__ __forceinline__ void dn_superblock(const PfRaw<QT>& w0, const PfRaw<Q
   }
 }
 
-// Activation chunk [c0, c0 + 256) of the segment's rows -> registers: 64 rows x
-// 32 granules of 16 B, 8 per thread (rows past n repeat a valid row; their
-// output columns are never stored).
-struct ActRegs { gm_u32x4 v[8]; };
+// Activation chunk [c0, c0 + 256) of the segment's rows <-> registers: 64 rows
+// x 32 granules of 16 B, granule g = threadIdx + 256 i for i in [I0, I0 + N)
+// (rows past n repeat a valid row; their output columns are never stored).
+template <int N>
+struct ActRegs { gm_u32x4 v[N]; };
 
-__device__ __forceinline__ void act_load(ActRegs& a, const uint16_t* __restrict__ src, int K,
-                                         const int32_t* __restrict__ rows, int c0) {
+template <int N>
+__device__ __forceinline__ void act_load(ActRegs<N>& a, const uint16_t* __restrict__ src, int K,
+                                         const int32_t* __restrict__ rows, int c0, int i0 = 0) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int g = threadIdx.x + 256 * i, r = g >> 5, c = g & 31;
+  for (int i = 0; i < N; ++i) {
+    const int g = threadIdx.x + 256 * (i0 + i), r = g >> 5, c = g & 31;
     a.v[i] = *reinterpret_cast<const gm_u32x4*>(src + (int64_t)rows[r] * K + c0 + 8 * c);
   }
 }
@@ -533,11 +540,12 @@ __device__ __forceinline__ void act_load(ActRegs& a, const uint16_t* __restrict_
 // slot 8c + i and element 16 + 4c + i to slot 8c + 4 + i, so that the low- and
 // high-nibble halves of a k-step sit side by side.  Granule c (8 elements) of a
 // sub-block: elements 0-3 -> slot 16 (c & 1) + 4 (c >> 1), 4-7 -> that + 8.
-template <bool PERM>
-__device__ __forceinline__ void act_store(const ActRegs& a, uint8_t* __restrict__ buf, int pitch = kPitchB) {
+template <bool PERM, int N>
+__device__ __forceinline__ void act_store(const ActRegs<N>& a, uint8_t* __restrict__ buf, int pitch = kPitchB,
+                                          int i0 = 0) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int g = threadIdx.x + 256 * i, r = g >> 5, c = g & 31;
+  for (int i = 0; i < N; ++i) {
+    const int g = threadIdx.x + 256 * (i0 + i), r = g >> 5, c = g & 31;
     uint8_t* row = buf + r * pitch;
     if constexpr (PERM) {
       const int sub = c >> 2, gc = c & 3;
@@ -602,23 +610,41 @@ __global__ void __launch_bounds__(256, 2) k_pf_gateup(gm_moe_layer P, const int3
   gm_f32x4 ag[4], au[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) { ag[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; au[t] = ag[t]; }
-  ActRegs xa;
-  act_load(xa, xh, D, tok_row, 0);
+  constexpr bool PERM = QT == GM_QTYPE_IQ4_XS;
+  {
+    ActRegs<8> x0;
+    act_load<8>(x0, xh, D, tok_row, 0);
+    act_store<PERM, 8>(x0, xl);
+  }
   PfRaw<QT> wg = pf_load<QT>(grow, q), wu = pf_load<QT>(urow, q);
-  act_store<QT == GM_QTYPE_IQ4_XS>(xa, xl);
   __syncthreads();
   for (int sb = 0; sb < nsb; ++sb) {
-    const int sn = sb + 1 < nsb ? sb + 1 : sb;                   // next superblock (clamped)
-    act_load(xa, xh, D, tok_row, sn * kChunk);
+    // next superblock's raw rows, and its activation chunk in two halves (the
+    // other LDS buffer is free: its last reader finished before the barrier)
+    const int sn = sb + 1 < nsb ? sb + 1 : sb;                   // the last step re-reads itself
     const PfRaw<QT> wgn = pf_load<QT>(grow + sn * SBB, q), wun = pf_load<QT>(urow + sn * SBB, q);
+    uint8_t* xnext = xl + ((sb + 1) & 1) * kTileB;
     const uint8_t* xb = xl + (sb & 1) * kTileB;
+    ActRegs<4> xa;
+    act_load<4>(xa, xh, D, tok_row, sn * kChunk, 0);
+    gm_f32x4 pg[4], pu[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) { pg[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; pu[t] = pg[t]; }
     switch (ntiles) {
-      case 1: gu_superblock<QT, 1>(wg, wu, q, l16, xb, grid, sgn, ag, au); break;
-      case 2: gu_superblock<QT, 2>(wg, wu, q, l16, xb, grid, sgn, ag, au); break;
-      case 3: gu_superblock<QT, 3>(wg, wu, q, l16, xb, grid, sgn, ag, au); break;
-      default: gu_superblock<QT, 4>(wg, wu, q, l16, xb, grid, sgn, ag, au); break;
+      case 1: gu_half<QT, 1, 0>(wg, wu, q, l16, xb, grid, sgn, pg, pu); break;
+      case 2: gu_half<QT, 2, 0>(wg, wu, q, l16, xb, grid, sgn, pg, pu); break;
+      case 3: gu_half<QT, 3, 0>(wg, wu, q, l16, xb, grid, sgn, pg, pu); break;
+      default: gu_half<QT, 4, 0>(wg, wu, q, l16, xb, grid, sgn, pg, pu); break;
     }
-    if (sb + 1 < nsb) act_store<QT == GM_QTYPE_IQ4_XS>(xa, xl + ((sb + 1) & 1) * kTileB);
+    act_store<PERM, 4>(xa, xnext, kPitchB, 0);
+    act_load<4>(xa, xh, D, tok_row, sn * kChunk, 4);
+    switch (ntiles) {
+      case 1: gu_half<QT, 1, 1>(wg, wu, q, l16, xb, grid, sgn, pg, pu); gu_fold<QT, 1>(wg, wu, q, pg, pu, ag, au); break;
+      case 2: gu_half<QT, 2, 1>(wg, wu, q, l16, xb, grid, sgn, pg, pu); gu_fold<QT, 2>(wg, wu, q, pg, pu, ag, au); break;
+      case 3: gu_half<QT, 3, 1>(wg, wu, q, l16, xb, grid, sgn, pg, pu); gu_fold<QT, 3>(wg, wu, q, pg, pu, ag, au); break;
+      default: gu_half<QT, 4, 1>(wg, wu, q, l16, xb, grid, sgn, pg, pu); gu_fold<QT, 4>(wg, wu, q, pg, pu, ag, au); break;
+    }
+    act_store<PERM, 4>(xa, xnext, kPitchB, 4);
     wg = wgn;
     wu = wun;
     __syncthreads();
@@ -685,9 +711,9 @@ __global__ void __launch_bounds__(256, NSB == 4 ? 1 : 2) k_pf_down(gm_moe_layer 
     for (int sb = 0; sb < NSB; ++sb) wc[m][sb] = pf_load<QT>(row_ptr(g0, m) + sb * SBB, q);
 #pragma unroll
   for (int sb = 0; sb < NSB; ++sb) {
-    ActRegs ha;
-    act_load(ha, hb, FF, in_row, sb * kChunk);
-    act_store<QT == GM_QTYPE_IQ4_XS>(ha, hl + sb * 2 * kChunk, PITCH);
+    ActRegs<8> ha;
+    act_load<8>(ha, hb, FF, in_row, sb * kChunk);
+    act_store<QT == GM_QTYPE_IQ4_XS, 8>(ha, hl + sb * 2 * kChunk, PITCH);
   }
   __syncthreads();
   const int ntiles = (n + 15) >> 4;
