@@ -52,6 +52,8 @@ struct PfWs {
   uint16_t* xh;       // [T][D]     f16 xn (gate/up operand)
   float* part;        // [kRouterSplit][T][ldp]  partial router dot products
   uint16_t* hb;       // [P + T][FF]  bf16 SwiGLU rows (sorted pairs, then shared per token)
+  uint16_t* hh;       // [P + T][FF]  the same rows as scaled f16
+  float* hsc;         // [P + T]      their scales
   float* yp;          // [P + T][D]   fp32 per-pair / shared outputs
 };
 
@@ -81,6 +83,8 @@ PfWs pf_layout(const gm_moe_layer* L, int T, uint8_t* base, size_t* total) {
   w.xh = reinterpret_cast<uint16_t*>(take((size_t)T * L->D * 2));
   w.part = reinterpret_cast<float*>(take((size_t)kRouterSplit * T * router_ld(L) * 4));
   w.hb = reinterpret_cast<uint16_t*>(take((P + T) * (size_t)L->FF * 2));
+  w.hh = reinterpret_cast<uint16_t*>(take((P + T) * (size_t)L->FF * 2));
+  w.hsc = reinterpret_cast<float*>(take((P + T) * 4));
   w.yp = reinterpret_cast<float*>(take((P + T) * (size_t)L->D * 4));
   if (total) *total = o;
   return w;
@@ -378,17 +382,6 @@ __device__ __forceinline__ void pf_stage_signs_u8(gm_u32x4* tab) {
   }
 }
 
-// Same signs as bf16-pair sign bits: dword p has bit 15 = sign 2p, bit 31 = sign 2p+1.
-__device__ __forceinline__ void pf_stage_signs_bf16(gm_u32x4* tab) {
-  for (int i = threadIdx.x; i < 128; i += blockDim.x) {
-    const uint32_t s = gm_ksigns((uint32_t)i);
-    uint32_t m[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) m[p] = (((s >> (2 * p)) & 1u) << 15) | (((s >> (2 * p + 1)) & 1u) << 31);
-    tab[i] = gm_u32x4{m[0], m[1], m[2], m[3]};
-  }
-}
-
 // f16 A operand of k-step j: 8 weights (scale folded in) at the lane's k-slots.
 //   IQ4_XS: slot i < 4 -> k = 32s + 4c + i (low nibbles of qs bytes 16s+4c ..+3),
 //           slot i >= 4 -> k = 32s + 16 + 4c + (i - 4) (high nibbles), c = j & 3
@@ -416,37 +409,6 @@ __device__ __forceinline__ gm_f16x8 a_f16(const PfRaw<QT>& r, int j, gm_f16x2 sc
     u8x4_to_f16(ub, sc, cc, o[2], o[3]);
   }
   return __builtin_bit_cast(gm_f16x8, gm_u32x4{o[0], o[1], o[2], o[3]});
-}
-
-// bf16 A operand of k-step j (same k-slot map as a_f16).
-template <int QT>
-__device__ __forceinline__ gm_bf16x8 a_bf16(const PfRaw<QT>& r, int j, float sc, const uint32_t* __restrict__ grid,
-                                            const gm_u32x4* __restrict__ sgn) {
-  gm_f32x2 v[4];
-  uint32_t flip[4] = {0u, 0u, 0u, 0u};
-  if constexpr (QT == GM_QTYPE_IQ4_XS) {
-    const uint32_t nib = r.q[4 * (j >> 2) + (j & 3)];
-    const uint32_t lo = gm_iq4nl_lut4(nib & 0x0f0f0f0fu), hi = gm_iq4nl_lut4((nib >> 4) & 0x0f0f0f0fu);
-    v[0] = gm_f32x2{sc * gm_sbyte(lo, 0), sc * gm_sbyte(lo, 1)};
-    v[1] = gm_f32x2{sc * gm_sbyte(lo, 2), sc * gm_sbyte(lo, 3)};
-    v[2] = gm_f32x2{sc * gm_sbyte(hi, 0), sc * gm_sbyte(hi, 1)};
-    v[3] = gm_f32x2{sc * gm_sbyte(hi, 2), sc * gm_sbyte(hi, 3)};
-  } else {
-    const int sl = j >> 2, g = j & 3;
-    const uint32_t qw = r.q[2 * sl + (g >> 1)] >> (16 * (g & 1));
-    const uint32_t ga = grid[qw & 0xffu], gb = grid[(qw >> 8) & 0xffu];
-    const uint32_t w = sl ? r.w1 : r.w0;
-    const gm_u32x4 m = sgn[(w >> (7 * g)) & 127u];
-    flip[0] = m.x; flip[1] = m.y; flip[2] = m.z; flip[3] = m.w;
-    v[0] = gm_f32x2{sc * gm_ubyte(ga, 0), sc * gm_ubyte(ga, 1)};
-    v[1] = gm_f32x2{sc * gm_ubyte(ga, 2), sc * gm_ubyte(ga, 3)};
-    v[2] = gm_f32x2{sc * gm_ubyte(gb, 0), sc * gm_ubyte(gb, 1)};
-    v[3] = gm_f32x2{sc * gm_ubyte(gb, 2), sc * gm_ubyte(gb, 3)};
-  }
-  uint32_t o[4];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) o[p] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v[p], gm_bf16x2)) ^ flip[p];
-  return __builtin_bit_cast(gm_bf16x8, gm_u32x4{o[0], o[1], o[2], o[3]});
 }
 
 // B operand of k-step j from an LDS activation row: the 8 activations of the
@@ -499,25 +461,98 @@ __device__ __forceinline__ void gu_fold(const PfRaw<QT>& wg, const PfRaw<QT>& wu
   }
 }
 
-// One superblock column of two down row tiles against NT token tiles (bf16).
+// One superblock column of two down row tiles against NT token tiles: f16
+// integer operands into the superblock's partial sums, then the partial sums
+// times the superblock factor of each accumulator row into acc.
 template <int QT, int NT>
 __device__ __forceinline__ void dn_superblock(const PfRaw<QT>& w0, const PfRaw<QT>& w1, int q, int l16,
                                               const uint8_t* __restrict__ hbuf, int pitch,
                                               const uint32_t* __restrict__ grid, const gm_u32x4* __restrict__ sgn,
                                               gm_f32x4 (&acc)[2][4]) {
-  const gm_f32x2 s0 = pf_scales<QT>(w0, q), s1 = pf_scales<QT>(w1, q);
+  const gm_f32x2 s0 = pf_int_scales<QT>(w0, q), s1 = pf_int_scales<QT>(w1, q);
+  gm_f32x4 p0[NT], p1[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) { p0[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; p1[t] = p0[t]; }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const gm_bf16x8 A0 = a_bf16<QT>(w0, j, j < 4 ? s0.x : s0.y, grid, sgn);
-    const gm_bf16x8 A1 = a_bf16<QT>(w1, j, j < 4 ? s1.x : s1.y, grid, sgn);
+    const float f0 = j < 4 ? s0.x : s0.y, f1 = j < 4 ? s1.x : s1.y;
+    const gm_f16x2 h0 = {(_Float16)f0, (_Float16)f0}, h1 = {(_Float16)f1, (_Float16)f1};
+    const gm_f16x2 c0 = {(_Float16)(-1152.f * f0), (_Float16)(-1152.f * f0)};
+    const gm_f16x2 c1 = {(_Float16)(-1152.f * f1), (_Float16)(-1152.f * f1)};
+    const gm_f16x8 A0 = a_f16<QT>(w0, j, h0, c0, grid, sgn);
+    const gm_f16x8 A1 = a_f16<QT>(w1, j, h1, c1, grid, sgn);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const gm_bf16x8 B = __builtin_bit_cast(gm_bf16x8, b_lds(hbuf + (t * 16 + l16) * pitch, q, j));
-      acc[0][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B, acc[0][t], 0, 0, 0);
-      acc[1][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B, acc[1][t], 0, 0, 0);
+      const gm_f16x8 B = __builtin_bit_cast(gm_f16x8, b_lds(hbuf + (t * 16 + l16) * pitch, q, j));
+      p0[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B, p0[t], 0, 0, 0);
+      p1[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B, p1[t], 0, 0, 0);
     }
     if (j & 1) issue_fence();
   }
+  const float d0l = pf_dscale<QT>(w0), d1l = pf_dscale<QT>(w1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float d0 = __shfl(d0l, 4 * q + i, 64), d1 = __shfl(d1l, 4 * q + i, 64);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      acc[0][t][i] = fmaf(d0, p0[t][i], acc[0][t][i]);
+      acc[1][t][i] = fmaf(d1, p1[t][i], acc[1][t][i]);
+    }
+  }
+}
+
+// ------------------------------------------------------------- h to f16
+// One wave per SwiGLU row (FF <= 2048: 4 granules of 8 values per lane): the
+// bf16 row scaled by 2^-e, e chosen so that its largest |value| lands in
+// [2^14, 2^15), is exact in f16 (11 significand bits >= bf16's 8) for every
+// value above 2^-29 of the largest; hsc[row] = 2^e, which the down kernel
+// multiplies into its outputs.
+__global__ void __launch_bounds__(256) k_pf_h16(const uint16_t* __restrict__ hb, int rows, int FF,
+                                                uint16_t* __restrict__ hh, float* __restrict__ hsc) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const gm_u32x4* src = reinterpret_cast<const gm_u32x4*>(hb + (int64_t)r * FF);
+  gm_u32x4* dst = reinterpret_cast<gm_u32x4*>(hh + (int64_t)r * FF);
+  const int ng = FF >> 3;                                      // 16-byte granules per row
+  constexpr int G = 4;                                         // FF <= 2048
+  gm_u32x4 v[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = lane + 64 * i;
+    v[i] = src[g < ng ? g : ng - 1];
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      m = fmaxf(m, fmaxf(fabsf(gm_bf2f(w[c] & 0xffffu)), fabsf(gm_bf2f(w[c] >> 16))));
+  }
+  m = fmaxf(m, GM_DPP_F(m, GM_ROW_ROR8));
+  m = fmaxf(m, GM_DPP_F(m, GM_ROW_ROR4));
+  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_2301));
+  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_1032));
+  m = fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), 0)),
+                  __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), 16))),
+            fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), 32)),
+                  __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, m), 48))));
+  // m in [2^(E-1), 2^E): scale so that the largest value lands in [2^14, 2^15)
+  const int e = m > 0.f && m <= 3.4e38f ? __builtin_amdgcn_frexp_expf(m) - 15 : 0;
+  const float down = __builtin_ldexpf(1.0f, -e);
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = lane + 64 * i;
+    const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const gm_f32x2 f = {gm_bf2f(w[c] & 0xffffu) * down, gm_bf2f(w[c] >> 16) * down};
+      o[c] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, gm_f16x2));
+    }
+    if (g < ng) dst[g] = gm_u32x4{o[0], o[1], o[2], o[3]};
+  }
+  if (lane == 0) hsc[r] = m <= 3.4e38f ? __builtin_ldexpf(1.0f, e) : __builtin_nanf("");
 }
 
 // Activation chunk [c0, c0 + 256) of the segment's rows <-> registers: 64 rows
@@ -672,8 +707,8 @@ __global__ void __launch_bounds__(256, 2) k_pf_gateup(gm_moe_layer P, const int3
 template <int QT, int NSB>
 __global__ void __launch_bounds__(256, NSB == 4 ? 1 : 2) k_pf_down(gm_moe_layer P, const int32_t* __restrict__ segs,
                                                     const int32_t* __restrict__ offsets,
-                                                    const uint16_t* __restrict__ hb, float* __restrict__ yp, int T,
-                                                    int n_blk, int rg_per_blk) {
+                                                    const uint16_t* __restrict__ hh, const float* __restrict__ hsc,
+                                                    float* __restrict__ yp, int T, int n_blk, int rg_per_blk) {
   constexpr int PITCH = NSB * 2 * kChunk + 16;                          // bytes per LDS h row
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* hl = smem;                                                   // [64][PITCH]
@@ -689,7 +724,7 @@ __global__ void __launch_bounds__(256, NSB == 4 ? 1 : 2) k_pf_down(gm_moe_layer 
   const int row0 = shared ? T * k + start : offsets[e] + start;        // rows of hb / yp
   if constexpr (QT == GM_QTYPE_IQ3_XXS) {
     gm_stage_grid(grid);
-    pf_stage_signs_bf16(sgn);
+    pf_stage_signs_u8(sgn);
   }
   if (threadIdx.x < kSegTok) in_row[threadIdx.x] = row0 + (threadIdx.x < n ? threadIdx.x : 0);
   __syncthreads();
@@ -712,11 +747,14 @@ __global__ void __launch_bounds__(256, NSB == 4 ? 1 : 2) k_pf_down(gm_moe_layer 
 #pragma unroll
   for (int sb = 0; sb < NSB; ++sb) {
     ActRegs<8> ha;
-    act_load<8>(ha, hb, FF, in_row, sb * kChunk);
+    act_load<8>(ha, hh, FF, in_row, sb * kChunk);
     act_store<QT == GM_QTYPE_IQ4_XS, 8>(ha, hl + sb * 2 * kChunk, PITCH);
   }
   __syncthreads();
   const int ntiles = (n + 15) >> 4;
+  float cs[4];                                                          // h scale of each output column
+#pragma unroll
+  for (int t = 0; t < 4; ++t) cs[t] = hsc[in_row[t * 16 + l16]];
   for (int g = g0; g < g1; ++g) {
     const int gn = g + 1 < g1 ? g + 1 : g;
     PfRaw<QT> wn[2][NSB];
@@ -746,7 +784,8 @@ __global__ void __launch_bounds__(256, NSB == 4 ? 1 : 2) k_pf_down(gm_moe_layer 
       for (int t = 0; t < 4; ++t) {
         const int col = t * 16 + l16;
         if (t < ntiles && col < n && r0 < D)
-          *reinterpret_cast<gm_f32x4*>(yp + (int64_t)(row0 + col) * D + r0) = acc[m][t];
+          *reinterpret_cast<gm_f32x4*>(yp + (int64_t)(row0 + col) * D + r0) =
+              gm_f32x4{acc[m][t][0] * cs[t], acc[m][t][1] * cs[t], acc[m][t][2] * cs[t], acc[m][t][3] * cs[t]};
       }
     }
 #pragma unroll
@@ -846,6 +885,11 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
     GM_TRY(hipGetLastError());
   }
   {
+    const int rows = T * k + (has_sh ? T : 0);
+    hipLaunchKernelGGL(k_pf_h16, dim3((rows + 3) / 4), dim3(256), 0, s, w.hb, rows, FF, w.hh, w.hsc);
+    GM_TRY(hipGetLastError());
+  }
+  {
     constexpr int kGroupsPerBlock = 2;
     const int n_blk = ((D + 127) / 128 + kGroupsPerBlock - 1) / kGroupsPerBlock;
     const int nb = (nseg + 7) / 8 * 8 * n_blk;
@@ -853,18 +897,18 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
     switch (FF / kChunk) {
       case 1:
         if (int rc = gm_set_smem(k_pf_down<QTD, 1>, smem)) return rc;
-        hipLaunchKernelGGL((k_pf_down<QTD, 1>), dim3(nb), dim3(256), smem, s, *L, w.segs, w.offsets, w.hb, w.yp, T,
-                           n_blk, kGroupsPerBlock);
+        hipLaunchKernelGGL((k_pf_down<QTD, 1>), dim3(nb), dim3(256), smem, s, *L, w.segs, w.offsets, w.hh, w.hsc, w.yp,
+                           T, n_blk, kGroupsPerBlock);
         break;
       case 2:
         if (int rc = gm_set_smem(k_pf_down<QTD, 2>, smem)) return rc;
-        hipLaunchKernelGGL((k_pf_down<QTD, 2>), dim3(nb), dim3(256), smem, s, *L, w.segs, w.offsets, w.hb, w.yp, T,
-                           n_blk, kGroupsPerBlock);
+        hipLaunchKernelGGL((k_pf_down<QTD, 2>), dim3(nb), dim3(256), smem, s, *L, w.segs, w.offsets, w.hh, w.hsc, w.yp,
+                           T, n_blk, kGroupsPerBlock);
         break;
       default:
         if (int rc = gm_set_smem(k_pf_down<QTD, 4>, smem)) return rc;
-        hipLaunchKernelGGL((k_pf_down<QTD, 4>), dim3(nb), dim3(256), smem, s, *L, w.segs, w.offsets, w.hb, w.yp, T,
-                           n_blk, kGroupsPerBlock);
+        hipLaunchKernelGGL((k_pf_down<QTD, 4>), dim3(nb), dim3(256), smem, s, *L, w.segs, w.offsets, w.hh, w.hsc, w.yp,
+                           T, n_blk, kGroupsPerBlock);
         break;
     }
     GM_TRY(hipGetLastError());
