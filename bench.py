@@ -43,6 +43,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-layers", type=int, default=8, help="blocks in the bounded CPU sample")
     ap.add_argument("--no-extra", action="store_true", help="skip the batch-8 chain")
     ap.add_argument("--calib-copy", action="store_true", help="only run a plain 256 MiB copy (counter calibration)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only run the config-4 prefill measurement (8 layers), one JSON line")
     return ap.parse_args()
 
 
@@ -304,6 +306,11 @@ def main() -> int:
     _lib.lib()
     dev = torch.device("cuda:0")
 
+    if args.prefill_only:
+        layers = build_layers(8, dev)
+        torch.cuda.synchronize()
+        print(json.dumps({"prefill": run_prefill(layers)}))
+        return 0
     log(f"building {args.layers} layers of seeded synthetic weights on {torch.cuda.get_device_name(0)}")
     t0 = time.time()
     layers = build_layers(args.layers, dev)

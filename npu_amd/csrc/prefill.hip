@@ -25,6 +25,8 @@
 //
 // Reference semantics: the CPU loop of qwen/forward.py:563-665 (prefill takes
 // that path in the reference; its NPU kernels are T = 1 only).
+#include <type_traits>
+
 #include "moe_common.h"
 
 using namespace gm_moe;
@@ -37,10 +39,22 @@ typedef float gm_f32x2 __attribute__((ext_vector_type(2)));
 
 namespace {
 
-constexpr int kSegTok = 64;         // tokens per segment (4 MFMA column tiles)
+constexpr int kSegTok = 64;         // tokens per segment
+constexpr int kNT = kSegTok / 16;   // MFMA column tiles per segment
 constexpr int kChunk = 256;         // K elements per pipeline step (one superblock column)
 constexpr int kPitchB = 2 * kChunk + 16;   // bytes per LDS activation row (16 B of padding)
 constexpr int kTileB = kSegTok * kPitchB;  // one activation buffer
+constexpr int kGran = kSegTok * (2 * kChunk / 16) / 256;  // 16-byte granules per thread of one chunk
+
+// f(integral_constant<int, n>) for the segment's tile count n = ntiles in
+// [1, NT], as a chain of uniform branches (one instantiation per count).
+template <int NT, class F>
+__device__ __forceinline__ void nt_dispatch(int ntiles, F&& f) {
+  if constexpr (NT > 1) {
+    if (ntiles < NT) { nt_dispatch<NT - 1>(ntiles, f); return; }
+  }
+  f(std::integral_constant<int, NT>{});
+}
 
 struct PfWs {
   int32_t* counts;    // [E]
@@ -424,7 +438,7 @@ __device__ __forceinline__ gm_u32x4 b_lds(const uint8_t* __restrict__ row, int q
 template <int QT, int NT, int H>
 __device__ __forceinline__ void gu_half(const PfRaw<QT>& wg, const PfRaw<QT>& wu, int q, int l16,
                                         const uint8_t* __restrict__ xb, const uint32_t* __restrict__ grid,
-                                        const gm_u32x4* __restrict__ sgn, gm_f32x4 (&pg)[4], gm_f32x4 (&pu)[4]) {
+                                        const gm_u32x4* __restrict__ sgn, gm_f32x4 (&pg)[kNT], gm_f32x4 (&pu)[kNT]) {
   const gm_f32x2 sg2 = pf_int_scales<QT>(wg, q), su2 = pf_int_scales<QT>(wu, q);
   const float sgf = H ? sg2.y : sg2.x, suf = H ? su2.y : su2.x;
   const gm_f16x2 sgh = {(_Float16)sgf, (_Float16)sgf}, suh = {(_Float16)suf, (_Float16)suf};
@@ -447,8 +461,8 @@ __device__ __forceinline__ void gu_half(const PfRaw<QT>& wg, const PfRaw<QT>& wu
 // The superblock's partial sums times the superblock factor of each
 // accumulator row (rows 4q + i, whose factors lanes 4q + i hold) into ag / au.
 template <int QT, int NT>
-__device__ __forceinline__ void gu_fold(const PfRaw<QT>& wg, const PfRaw<QT>& wu, int q, const gm_f32x4 (&pg)[4],
-                                        const gm_f32x4 (&pu)[4], gm_f32x4 (&ag)[4], gm_f32x4 (&au)[4]) {
+__device__ __forceinline__ void gu_fold(const PfRaw<QT>& wg, const PfRaw<QT>& wu, int q, const gm_f32x4 (&pg)[kNT],
+                                        const gm_f32x4 (&pu)[kNT], gm_f32x4 (&ag)[kNT], gm_f32x4 (&au)[kNT]) {
   const float dgl = pf_dscale<QT>(wg), dul = pf_dscale<QT>(wu);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -468,7 +482,7 @@ template <int QT, int NT>
 __device__ __forceinline__ void dn_superblock(const PfRaw<QT>& w0, const PfRaw<QT>& w1, int q, int l16,
                                               const uint8_t* __restrict__ hbuf, int pitch,
                                               const uint32_t* __restrict__ grid, const gm_u32x4* __restrict__ sgn,
-                                              gm_f32x4 (&acc)[2][4]) {
+                                              gm_f32x4 (&acc)[2][kNT]) {
   const gm_f32x2 s0 = pf_int_scales<QT>(w0, q), s1 = pf_int_scales<QT>(w1, q);
   gm_f32x4 p0[NT], p1[NT];
 #pragma unroll
@@ -597,7 +611,7 @@ __device__ __forceinline__ void act_store(const ActRegs<N>& a, uint8_t* __restri
 // Block = (segment, 64 rows of FF); wave w -> rows 16w .. 16w+15 of both the
 // gate and the up matrix, all of the segment's token tiles.
 template <int QT>
-__global__ void __launch_bounds__(256, 2) k_pf_gateup(gm_moe_layer P, const int32_t* __restrict__ segs,
+__global__ void __launch_bounds__(256, kSegTok == 64 ? 2 : 4) k_pf_gateup(gm_moe_layer P, const int32_t* __restrict__ segs,
                                                       const int32_t* __restrict__ offsets,
                                                       const int32_t* __restrict__ sorted,
                                                       const uint16_t* __restrict__ xh, uint16_t* __restrict__ hb,
@@ -607,7 +621,7 @@ __global__ void __launch_bounds__(256, 2) k_pf_gateup(gm_moe_layer P, const int3
   uint32_t* grid = reinterpret_cast<uint32_t*>(smem + 2 * kTileB);      // [256] (IQ3)
   gm_u32x4* sgn = reinterpret_cast<gm_u32x4*>(grid + 256);              // [128] (IQ3)
   int32_t* tok_row = reinterpret_cast<int32_t*>(sgn + 128);             // [64]
-  int32_t* out_row = tok_row + kSegTok;                                 // [64]
+  int32_t* out_row = tok_row + kSegTok;                                 // [kSegTok]
   int seg, rt;
   xcd_tile(blockIdx.x, n_row_tiles, seg, rt);
   if (seg >= segs[0]) return;
@@ -642,14 +656,15 @@ __global__ void __launch_bounds__(256, 2) k_pf_gateup(gm_moe_layer P, const int3
   const uint8_t* urow = ubase + (int64_t)(row < FF ? row : 0) * rb;
   constexpr int SBB = QT == GM_QTYPE_IQ4_XS ? GM_IQ4XS_BYTES : GM_IQ3XXS_BYTES;
   const int nsb = D / kChunk, ntiles = (n + 15) >> 4;
-  gm_f32x4 ag[4], au[4];
+  gm_f32x4 ag[kNT], au[kNT];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) { ag[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; au[t] = ag[t]; }
+  for (int t = 0; t < kNT; ++t) { ag[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; au[t] = ag[t]; }
   constexpr bool PERM = QT == GM_QTYPE_IQ4_XS;
+  constexpr int GH = kGran / 2;                                         // granules per half chunk
   {
-    ActRegs<8> x0;
-    act_load<8>(x0, xh, D, tok_row, 0);
-    act_store<PERM, 8>(x0, xl);
+    ActRegs<kGran> x0;
+    act_load<kGran>(x0, xh, D, tok_row, 0);
+    act_store<PERM, kGran>(x0, xl);
   }
   PfRaw<QT> wg = pf_load<QT>(grow, q), wu = pf_load<QT>(urow, q);
   __syncthreads();
@@ -660,26 +675,19 @@ __global__ void __launch_bounds__(256, 2) k_pf_gateup(gm_moe_layer P, const int3
     const PfRaw<QT> wgn = pf_load<QT>(grow + sn * SBB, q), wun = pf_load<QT>(urow + sn * SBB, q);
     uint8_t* xnext = xl + ((sb + 1) & 1) * kTileB;
     const uint8_t* xb = xl + (sb & 1) * kTileB;
-    ActRegs<4> xa;
-    act_load<4>(xa, xh, D, tok_row, sn * kChunk, 0);
-    gm_f32x4 pg[4], pu[4];
+    ActRegs<GH> xa;
+    act_load<GH>(xa, xh, D, tok_row, sn * kChunk, 0);
+    gm_f32x4 pg[kNT], pu[kNT];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) { pg[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; pu[t] = pg[t]; }
-    switch (ntiles) {
-      case 1: gu_half<QT, 1, 0>(wg, wu, q, l16, xb, grid, sgn, pg, pu); break;
-      case 2: gu_half<QT, 2, 0>(wg, wu, q, l16, xb, grid, sgn, pg, pu); break;
-      case 3: gu_half<QT, 3, 0>(wg, wu, q, l16, xb, grid, sgn, pg, pu); break;
-      default: gu_half<QT, 4, 0>(wg, wu, q, l16, xb, grid, sgn, pg, pu); break;
-    }
-    act_store<PERM, 4>(xa, xnext, kPitchB, 0);
-    act_load<4>(xa, xh, D, tok_row, sn * kChunk, 4);
-    switch (ntiles) {
-      case 1: gu_half<QT, 1, 1>(wg, wu, q, l16, xb, grid, sgn, pg, pu); gu_fold<QT, 1>(wg, wu, q, pg, pu, ag, au); break;
-      case 2: gu_half<QT, 2, 1>(wg, wu, q, l16, xb, grid, sgn, pg, pu); gu_fold<QT, 2>(wg, wu, q, pg, pu, ag, au); break;
-      case 3: gu_half<QT, 3, 1>(wg, wu, q, l16, xb, grid, sgn, pg, pu); gu_fold<QT, 3>(wg, wu, q, pg, pu, ag, au); break;
-      default: gu_half<QT, 4, 1>(wg, wu, q, l16, xb, grid, sgn, pg, pu); gu_fold<QT, 4>(wg, wu, q, pg, pu, ag, au); break;
-    }
-    act_store<PERM, 4>(xa, xnext, kPitchB, 4);
+    for (int t = 0; t < kNT; ++t) { pg[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; pu[t] = pg[t]; }
+    nt_dispatch<kNT>(ntiles, [&](auto nt) { gu_half<QT, decltype(nt)::value, 0>(wg, wu, q, l16, xb, grid, sgn, pg, pu); });
+    act_store<PERM, GH>(xa, xnext, kPitchB, 0);
+    act_load<GH>(xa, xh, D, tok_row, sn * kChunk, GH);
+    nt_dispatch<kNT>(ntiles, [&](auto nt) {
+      gu_half<QT, decltype(nt)::value, 1>(wg, wu, q, l16, xb, grid, sgn, pg, pu);
+      gu_fold<QT, decltype(nt)::value>(wg, wu, q, pg, pu, ag, au);
+    });
+    act_store<PERM, GH>(xa, xnext, kPitchB, GH);
     wg = wgn;
     wu = wun;
     __syncthreads();
@@ -687,7 +695,7 @@ __global__ void __launch_bounds__(256, 2) k_pf_gateup(gm_moe_layer P, const int3
   // C layout: lane l holds rows 4 (l / 16) + i of the 16-row tile, column l % 16
   const int r0 = rt * 64 + wave * 16 + 4 * q;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < kNT; ++t) {
     const int col = t * 16 + l16;
     if (t < ntiles && col < n && r0 < FF) {
       gm_f32x2 h01 = {gm_silu(ag[t][0]) * au[t][0], gm_silu(ag[t][1]) * au[t][1]};
@@ -705,7 +713,7 @@ __global__ void __launch_bounds__(256, 2) k_pf_gateup(gm_moe_layer P, const int3
 // walks its row groups with the next group's raw superblocks in flight.
 // Wave w -> row tiles 2w, 2w+1 (16 rows each) of a group.
 template <int QT, int NSB>
-__global__ void __launch_bounds__(256, NSB == 4 ? 1 : 2) k_pf_down(gm_moe_layer P, const int32_t* __restrict__ segs,
+__global__ void __launch_bounds__(256, (NSB == 4 ? 1 : 2) * (64 / kSegTok)) k_pf_down(gm_moe_layer P, const int32_t* __restrict__ segs,
                                                     const int32_t* __restrict__ offsets,
                                                     const uint16_t* __restrict__ hh, const float* __restrict__ hsc,
                                                     float* __restrict__ yp, int T, int n_blk, int rg_per_blk) {
@@ -746,15 +754,15 @@ __global__ void __launch_bounds__(256, NSB == 4 ? 1 : 2) k_pf_down(gm_moe_layer 
     for (int sb = 0; sb < NSB; ++sb) wc[m][sb] = pf_load<QT>(row_ptr(g0, m) + sb * SBB, q);
 #pragma unroll
   for (int sb = 0; sb < NSB; ++sb) {
-    ActRegs<8> ha;
-    act_load<8>(ha, hh, FF, in_row, sb * kChunk);
-    act_store<QT == GM_QTYPE_IQ4_XS, 8>(ha, hl + sb * 2 * kChunk, PITCH);
+    ActRegs<kGran> ha;
+    act_load<kGran>(ha, hh, FF, in_row, sb * kChunk);
+    act_store<QT == GM_QTYPE_IQ4_XS, kGran>(ha, hl + sb * 2 * kChunk, PITCH);
   }
   __syncthreads();
   const int ntiles = (n + 15) >> 4;
-  float cs[4];                                                          // h scale of each output column
+  float cs[kNT];                                                        // h scale of each output column
 #pragma unroll
-  for (int t = 0; t < 4; ++t) cs[t] = hsc[in_row[t * 16 + l16]];
+  for (int t = 0; t < kNT; ++t) cs[t] = hsc[in_row[t * 16 + l16]];
   for (int g = g0; g < g1; ++g) {
     const int gn = g + 1 < g1 ? g + 1 : g;
     PfRaw<QT> wn[2][NSB];
@@ -762,26 +770,23 @@ __global__ void __launch_bounds__(256, NSB == 4 ? 1 : 2) k_pf_down(gm_moe_layer 
     for (int m = 0; m < 2; ++m)
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb) wn[m][sb] = pf_load<QT>(row_ptr(gn, m) + sb * SBB, q);
-    gm_f32x4 acc[2][4];
+    gm_f32x4 acc[2][kNT];
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) acc[m][t] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < kNT; ++t) acc[m][t] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb) {
       const uint8_t* hbuf = hl + sb * 2 * kChunk;
-      switch (ntiles) {
-        case 1: dn_superblock<QT, 1>(wc[0][sb], wc[1][sb], q, l16, hbuf, PITCH, grid, sgn, acc); break;
-        case 2: dn_superblock<QT, 2>(wc[0][sb], wc[1][sb], q, l16, hbuf, PITCH, grid, sgn, acc); break;
-        case 3: dn_superblock<QT, 3>(wc[0][sb], wc[1][sb], q, l16, hbuf, PITCH, grid, sgn, acc); break;
-        default: dn_superblock<QT, 4>(wc[0][sb], wc[1][sb], q, l16, hbuf, PITCH, grid, sgn, acc); break;
-      }
+      nt_dispatch<kNT>(ntiles, [&](auto nt) {
+        dn_superblock<QT, decltype(nt)::value>(wc[0][sb], wc[1][sb], q, l16, hbuf, PITCH, grid, sgn, acc);
+      });
     }
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const int r0 = g * 128 + wave * 32 + m * 16 + 4 * q;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < kNT; ++t) {
         const int col = t * 16 + l16;
         if (t < ntiles && col < n && r0 < D)
           *reinterpret_cast<gm_f32x4*>(yp + (int64_t)(row0 + col) * D + r0) =

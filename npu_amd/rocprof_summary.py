@@ -8,6 +8,11 @@ copy kernel of known size) and writes
   copy-calibrated HBM bytes per launch and the algorithmic bytes per launch;
 * ``<name>.md`` -- the same as a table, with the commands that produced the inputs.
 
+With ``--prefill-pmc P.csv`` it instead summarises the prefill kernels: rocprof
+durations and, from the counters ``MfmaUtil``, ``MfmaFlopsF16`` and ``MfmaFlopsBF16``
+(one ``--pmc`` pass), each kernel's MFMA busy fraction and issued MFMA TFLOP/s
+against the 2.5 PFLOP/s dense f16/bf16 peak (``<name>.md`` and ``prefill_mfma.json``).
+
 Calibration: the copy kernel moves ``calib_bytes`` each way per launch, so
 ``scale = calib_bytes / (counter KiB * 1024)`` for each counter; a kernel's HBM bytes
 per launch are ``FETCH * 1024 * scale_fetch + WRITE * 1024 * scale_write``.
@@ -69,19 +74,68 @@ def kernel_stats(path: str) -> dict[str, dict]:
     return out
 
 
+MFMA_PEAK_TFLOPS = 2500.0      # dense f16 / bf16 MFMA, MI355X
+
+
+def counter_table(path: str) -> dict[str, dict[str, float]]:
+    """Per kernel instance and counter: mean over dispatches."""
+    vals: dict[str, dict[str, list[float]]] = defaultdict(lambda: defaultdict(list))
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            vals[short(r["Kernel_Name"])][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return {k: {c: statistics.fmean(v) for c, v in d.items()} for k, d in vals.items()}
+
+
+def prefill_summary(a) -> None:
+    stats = kernel_stats(a.stats)
+    pmc = counter_table(a.prefill_pmc)
+    kernels = {}
+    for name, st in stats.items():
+        if not (family(name).startswith("k_pf_") or family(name) == "k_dispatch"):
+            continue
+        c = pmc.get(name, {})
+        flops = c.get("MfmaFlopsF16", 0.0) + c.get("MfmaFlopsBF16", 0.0)
+        tflops = flops / (st["avg_us"] * 1e-6) / 1e12
+        kernels[name] = {"calls": st["calls"], "rocprof_avg_us": st["avg_us"],
+                         "mfma_util_pct": c.get("MfmaUtil"), "mfma_flops_per_launch": flops,
+                         "mfma_TFLOPs_at_rocprof_avg": tflops, "frac_of_dense_peak": tflops / MFMA_PEAK_TFLOPS}
+    out = Path(a.out)
+    out.mkdir(parents=True, exist_ok=True)
+    (out / "prefill_mfma.json").write_text(json.dumps({"peak_TFLOPs": MFMA_PEAK_TFLOPS, "kernels": kernels},
+                                                      indent=1) + "\n")
+    total = sum(k["rocprof_avg_us"] * k["calls"] for k in kernels.values())
+    lines = [f"# {a.name}: prefill kernel durations and MFMA use", "", a.commands, "",
+             "| kernel | calls | rocprof avg us | share of prefill time | MfmaUtil % | MFMA GFLOP/launch | "
+             "MFMA TFLOP/s | of 2.5 PF dense |", "|---|---|---|---|---|---|---|---|"]
+    for name, k in sorted(kernels.items(), key=lambda kv: -kv[1]["rocprof_avg_us"]):
+        util = "-" if k["mfma_util_pct"] is None else f"{k['mfma_util_pct']:.1f}"
+        lines.append(f"| {name[:60]} | {k['calls']} | {k['rocprof_avg_us']:.2f} | "
+                     f"{k['rocprof_avg_us'] * k['calls'] / total:.3f} | {util} | "
+                     f"{k['mfma_flops_per_launch'] / 1e9:.3f} | {k['mfma_TFLOPs_at_rocprof_avg']:.1f} | "
+                     f"{k['frac_of_dense_peak']:.4f} |")
+    (out / f"{a.name}.md").write_text("\n".join(lines) + "\n")
+    print(json.dumps(kernels, indent=1))
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--stats", required=True)
-    ap.add_argument("--fetch", required=True)
-    ap.add_argument("--write", required=True)
-    ap.add_argument("--calib-fetch", required=True)
-    ap.add_argument("--calib-write", required=True)
+    ap.add_argument("--prefill-pmc", help="counter CSV of MfmaUtil/MfmaFlopsF16/MfmaFlopsBF16 (prefill mode)")
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
+    ap.add_argument("--calib-fetch")
+    ap.add_argument("--calib-write")
     ap.add_argument("--calib-bytes", type=int, default=256 << 20)
     ap.add_argument("--calib-kernel", default="__amd_rocclr_copyBuffer")
     ap.add_argument("--out", default="profiles")
     ap.add_argument("--name", default="moe_decode_config5")
     ap.add_argument("--commands", default="", help="text describing the commands (markdown)")
     a = ap.parse_args()
+    if a.prefill_pmc:
+        prefill_summary(a)
+        return
+    if not (a.fetch and a.write and a.calib_fetch and a.calib_write):
+        ap.error("decode mode needs --fetch, --write, --calib-fetch and --calib-write")
 
     stats = kernel_stats(a.stats)
     fetch, write = counter_means(a.fetch), counter_means(a.write)
