@@ -82,3 +82,34 @@ def test_stage_outputs(gpu):
     assert torch.equal(got["topk_ids"].long(), st["topk_ids"])
     assert torch.allclose(got["ffn_moe_weights_norm"], st["ffn_moe_weights_norm"], rtol=1e-5)
     assert torch.allclose(got["shared_expert_gate_sigmoid"], st["shared_expert_gate_sigmoid"], rtol=1e-5)
+
+
+@pytest.mark.parametrize("D,FF,E,k", [(1024, 1024, 64, 6), (2048, 256, 128, 8), (512, 512, 32, 2)])
+@pytest.mark.parametrize("shared", [True, False])
+def test_t1_shapes(gpu, D, FF, E, k, shared):
+    """T = 1 decode (the three-kernel fast path) at D / FF / E / k corners: FF in {256, 512,
+    1024}, k < 8, E < 256, with and without the shared expert, RMSNorm weight and residual."""
+    h = synth.host_moe_layer(30 + k, D=D, FF=FF, E=E, k=k, shared=shared, norm=True)
+    _check(gpu, h, 1, residual=True, seed=k, rmsnorm_input=False)
+
+
+def test_t1_graph_replays(gpu):
+    """The T = 1 decode captured in a hipGraph: every replay (with eager work on the same
+    workspace and synchronisations in between) matches the eager result."""
+    h = synth.host_moe_layer(41)
+    blk = GpuMoeBlock.from_host(h, device=gpu)
+    x = torch.from_numpy(synth.host_input(7, 1, h.D)).to(gpu)
+    y_eager = blk(x).clone()
+    y = torch.empty_like(x)
+    blk(x, out=y)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        blk(x, out=y)
+    for i in range(4):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_eager), f"replay {i}"
+        _ = blk(x + 0.0)                      # eager work on the same workspace between replays
+        torch.cuda.synchronize()
