@@ -24,6 +24,8 @@ def _dev(a, dtype=None, device="cuda") -> torch.Tensor | None:
         t = a.to(device)
     else:
         arr = np.ascontiguousarray(a)
+        if not arr.flags.writeable:           # e.g. a read-only memory map of a GGUF file
+            arr = arr.copy()
         if arr.dtype == np.uint16:
             arr = arr.view(np.int16)
         t = torch.from_numpy(arr).to(device)

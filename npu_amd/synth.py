@@ -154,3 +154,33 @@ def device_quant_matrix(gen: torch.Generator, qtype: int, M: int, K: int, n_expe
 
 def device_bf16_normal(gen: torch.Generator, shape, std: float, device="cuda") -> torch.Tensor:
     return (torch.randn(shape, device=device, generator=gen) * std).to(torch.bfloat16)
+
+
+# ------------------------------------------------------------------ files
+def write_gguf_model(path, layers, *, arch: str = "qwen3next", rms_eps: float = 1e-6) -> None:
+    """A GGUF file holding the MoE tensors of `layers` (``HostMoeLayer``) under the model's
+    tensor names (``blk.{i}.ffn_gate_exps.weight`` ...) and the metadata ``build_config``
+    reads: raw expert / shared-expert superblocks, the router and shared gate as F32 (the
+    bf16 values widened), the norm weight and router bias as F32."""
+    from npu_amd.gguf_file import write_gguf
+    h = layers[0]
+    kv = {"general.architecture": arch, f"{arch}.block_count": len(layers), f"{arch}.embedding_length": h.D,
+          f"{arch}.expert_count": h.E, f"{arch}.expert_used_count": h.k,
+          f"{arch}.expert_feed_forward_length": h.FF, f"{arch}.attention.layer_norm_rms_epsilon": rms_eps}
+    tensors = []
+    for i, L in enumerate(layers):
+        p = f"blk.{i}."
+        tensors += [(p + "ffn_gate_exps.weight", L.q_gate, (L.D, L.FF, L.E), L.gate),
+                    (p + "ffn_up_exps.weight", L.q_gate, (L.D, L.FF, L.E), L.up),
+                    (p + "ffn_down_exps.weight", L.q_down, (L.FF, L.D, L.E), L.down),
+                    (p + "ffn_gate_inp.weight", int(QT.F32), (L.D, L.E), from_bf16(L.router).reshape(L.E, L.D))]
+        if L.gate_sh is not None:
+            tensors += [(p + "ffn_gate_shexp.weight", L.q_gate, (L.D, L.FF), L.gate_sh),
+                        (p + "ffn_up_shexp.weight", L.q_gate, (L.D, L.FF), L.up_sh),
+                        (p + "ffn_down_shexp.weight", L.q_down, (L.FF, L.D), L.down_sh),
+                        (p + "ffn_gate_inp_shexp.weight", int(QT.F32), (L.D,), from_bf16(L.sh_gate_inp))]
+        if L.router_bias is not None:
+            tensors.append((p + "ffn_gate_inp.bias", int(QT.F32), (L.E,), L.router_bias))
+        if L.norm_w is not None:
+            tensors.append((p + "post_attention_norm.weight", int(QT.F32), (L.D,), L.norm_w))
+    write_gguf(path, kv, [(n, int(t), d, a) for n, t, d, a in tensors])

@@ -89,3 +89,25 @@ def test_qwen_moe_forward_dropin(gpu, T):
     g, u, d = layers[0].dequant_one(5)
     assert torch.equal(g, torch.from_numpy(Q.dequant_matrix(hs[0].gate[5], hs[0].q_gate, 512, 2048)))
     assert d.shape == (2048, 512)
+
+
+@pytest.mark.parametrize("T", [1, 12])
+def test_qwen_moe_forward_from_gguf_file(gpu, tmp_path, T):
+    """The MoE drop-in fed from a GGUF file read by npu_amd.gguf_file (the reference reads
+    its model through gguf-py's GGUFReader + TensorStore, qwen/model.py:164-277): raw
+    expert superblocks mapped from the file straight to HBM, router / shared gate from F32."""
+    from npu_amd import gguf_file
+    hs = [synth.host_moe_layer(60 + i, D=1024, FF=256, E=32, k=4, q_gate=q, q_down=d)
+          for i, (q, d) in enumerate([(QT.IQ4_XS, QT.IQ3_XXS), (QT.IQ3_XXS, QT.IQ4_XS)])]
+    path = tmp_path / "moe.gguf"
+    synth.write_gguf_model(path, hs)
+    ts = gguf_file.TensorStore(path)
+    assert ts.cfg.n_layer == 2 and ts.cfg.n_expert_used == 4
+    layers = [qwen_moe.MoELayer.load(ts, i) for i in range(2)]
+    x = torch.from_numpy(synth.host_input(11, T, 1024)).reshape(1, T, 1024)
+    for i, L in enumerate(layers):
+        y = qwen_moe.moe_forward(x, L, ts.cfg)
+        ref = OM.moe_forward(x, OM.OracleLayer(hs[i]))
+        assert OM.rel_err(y, ref) <= (1e-3 if T <= 8 else 1e-2), OM.rel_err(y, ref)
+    g = ts.get_expert("blk.1.ffn_gate_exps.weight", 3)
+    assert np.array_equal(g, Q.dequant_matrix(hs[1].gate[3], hs[1].q_gate, 256, 1024))
