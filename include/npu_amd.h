@@ -27,6 +27,10 @@ extern "C" {
 /* Weight formats: ggml type ids (gguf GGMLQuantizationType). */
 #define GM_QTYPE_F32 0
 #define GM_QTYPE_F16 1
+#define GM_QTYPE_Q8_0 8
+#define GM_QTYPE_Q4_K 12
+#define GM_QTYPE_Q5_K 13
+#define GM_QTYPE_Q6_K 14
 #define GM_QTYPE_IQ3_XXS 18
 #define GM_QTYPE_IQ4_XS 23
 #define GM_QTYPE_BF16 30
@@ -47,10 +51,13 @@ const char* gm_last_error(void);
 int gm_abi_version(void);
 
 /*
- * Dequantise n_superblocks raw superblocks of `qtype` (IQ4_XS or IQ3_XXS) to
- * fp32 (256 values per superblock).  Exact: every value is an fp32 product.
- * Replaces gguf.quants.dequantize as called by TensorStore.get_expert
- * (qwen/model.py:266) and npu/iq3_xxs.py:dequant_rows (97-119).
+ * Dequantise n_superblocks raw blocks of `qtype` to fp32: IQ4_XS, IQ3_XXS,
+ * Q4_K, Q5_K, Q6_K (256 values per block) or Q8_0 (32 values per block).
+ * Every product is exact in fp32; Q4_K / Q5_K round once when subtracting the
+ * min term.  Replaces gguf.quants.dequantize as called by TensorStore.get /
+ * get_expert (qwen/model.py:212, 266) and npu/iq3_xxs.py:dequant_rows (97-119).
+ * IQ4_XS / IQ3_XXS need raw 8-byte and out 16-byte aligned; the other types
+ * only 4-byte aligned out.
  */
 int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out, void* stream);
 

@@ -91,7 +91,12 @@ const char* gm_last_error(void) { return g_err; }
 int gm_abi_version(void) { return 1; }
 
 int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out, void* stream) {
-  if (!is_quant(qtype)) return gm_fail_arg("gm_dequant_f32: qtype %d is not IQ4_XS(23)/IQ3_XXS(18)", qtype);
+  if (gm_kquant_block(qtype).bytes)
+    return n_superblocks < 0 || !raw || !out ? gm_fail_arg("gm_dequant_f32: bad arguments")
+                                            : gm_launch_dequant_k(qtype, raw, n_superblocks, out, as_stream(stream));
+  if (!is_quant(qtype))
+    return gm_fail_arg("gm_dequant_f32: qtype %d is not IQ4_XS(23)/IQ3_XXS(18)/Q8_0(8)/Q4_K(12)/Q5_K(13)/Q6_K(14)",
+                       qtype);
   if (n_superblocks < 0) return gm_fail_arg("gm_dequant_f32: negative n_superblocks");
   if (n_superblocks == 0) return GM_OK;
   if (!raw || !out) return gm_fail_arg("gm_dequant_f32: NULL pointer");

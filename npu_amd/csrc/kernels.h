@@ -3,6 +3,19 @@
 #include "common.h"
 
 int gm_launch_dequant(int qtype, const void* raw, int64_t n_sb, float* out, hipStream_t s);
+
+// Q8_0 / Q4_K / Q5_K / Q6_K: weights and bytes per block (0 for other types).
+struct GmKBlock { int weights, bytes; };
+inline GmKBlock gm_kquant_block(int qtype) {
+  switch (qtype) {
+    case GM_QTYPE_Q8_0: return {32, 34};
+    case GM_QTYPE_Q4_K: return {256, 144};
+    case GM_QTYPE_Q5_K: return {256, 176};
+    case GM_QTYPE_Q6_K: return {256, 210};
+    default: return {0, 0};
+  }
+}
+int gm_launch_dequant_k(int qtype, const void* raw, int64_t n_blocks, float* out, hipStream_t s);
 int gm_launch_matvec(int qtype, const void* w, int M, int K, const float* x, int n_tok, float* y,
                      hipStream_t s);
 int gm_launch_gateup(int qtype, const void* wg, const void* wu, int FF, int D, const float* x, int n_tok,

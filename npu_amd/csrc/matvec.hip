@@ -43,6 +43,86 @@ int gm_launch_dequant(int qtype, const void* raw, int64_t n_sb, float* out, hipS
   return GM_OK;
 }
 
+// ggml K-quant / Q8_0 blocks (loader path; the MoE kernels take IQ4_XS / IQ3_XXS).
+// One thread per 32 outputs (one Q8_0 block, or one sub-block of a 256-weight
+// K-quant block); bytes are read one at a time, so no alignment is assumed.
+// Layouts (little-endian, fp16 d / dmin):
+//   Q8_0  d, int8 q[32]                                 y = d q
+//   Q4_K  d, dmin, scales[12], qs[128]                  y = (d sc_s) q - dmin m_s
+//   Q5_K  d, dmin, scales[12], qh[32], qs[128]          q += 16 bit s of qh[l]
+//   Q6_K  ql[128], qh[64], int8 sc[16], d               y = (d sc[e / 16]) (q - 32)
+// Sub-block s of Q4_K / Q5_K: weights 32s .. 32s + 31 are the low (s even) or
+// high (s odd) nibbles of qs[32 (s / 2) .. + 31]; its 6-bit scale and min come
+// from scales[12] (s < 4: bytes s and s + 4; s >= 4: byte s + 4 plus the top
+// two bits of bytes s - 4 and s).  Q6_K weight e = 128 n + 32 c + l: low four
+// bits from ql[64 n + 32 (c & 1) + l] (low nibble for c < 2), high two from
+// bits 2c .. 2c + 1 of qh[32 n + l].
+__device__ __forceinline__ float kq_h2f(const uint8_t* p) { return gm_h2f((uint32_t)p[0] | ((uint32_t)p[1] << 8)); }
+
+template <int QT>
+__global__ void __launch_bounds__(256) k_dequant_k(const uint8_t* __restrict__ raw, int64_t n_units,
+                                                   float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_units) return;
+  float* y = out + i * 32;
+  if constexpr (QT == GM_QTYPE_Q8_0) {
+    const uint8_t* b = raw + i * 34;
+    const float d = kq_h2f(b);
+#pragma unroll
+    for (int l = 0; l < 32; ++l) y[l] = d * (float)(int8_t)b[2 + l];
+  } else if constexpr (QT == GM_QTYPE_Q6_K) {
+    const int s = (int)(i & 7);
+    const uint8_t* b = raw + (i >> 3) * 210;
+    const float d = kq_h2f(b + 208);
+    const int n = s >> 2, c = s & 3;
+    const uint8_t* ql = b + 64 * n + 32 * (c & 1);
+    const uint8_t* qh = b + 128 + 32 * n;
+    const float d0 = d * (float)(int8_t)b[192 + 2 * s], d1 = d * (float)(int8_t)b[193 + 2 * s];
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      const int lo = c < 2 ? (ql[l] & 15) : (ql[l] >> 4);
+      const int q = (lo | (((qh[l] >> (2 * c)) & 3) << 4)) - 32;
+      y[l] = (l < 16 ? d0 : d1) * (float)q;
+    }
+  } else {
+    constexpr bool five = QT == GM_QTYPE_Q5_K;
+    constexpr int NB = five ? 176 : 144;
+    const int s = (int)(i & 7);
+    const uint8_t* b = raw + (i >> 3) * NB;
+    const float d = kq_h2f(b), dmin = kq_h2f(b + 2);
+    const uint8_t* sc = b + 4;
+    int scv, mv;
+    if (s < 4) { scv = sc[s] & 63; mv = sc[s + 4] & 63; }
+    else { scv = (sc[s + 4] & 15) | ((sc[s - 4] >> 6) << 4); mv = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4); }
+    const float dsc = d * (float)scv, dm = dmin * (float)mv;
+    const uint8_t* qs = b + (five ? 48 : 16) + 32 * (s >> 1);
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      int q = (s & 1) ? (qs[l] >> 4) : (qs[l] & 15);
+      if constexpr (five) q += ((b[16 + l] >> s) & 1) << 4;
+      y[l] = dsc * (float)q - dm;
+    }
+  }
+}
+
+int gm_launch_dequant_k(int qtype, const void* raw, int64_t n_blocks, float* out, hipStream_t s) {
+  const GmKBlock kb = gm_kquant_block(qtype);
+  const int64_t n_units = n_blocks * (kb.weights / 32);
+  if (n_units == 0) return GM_OK;
+  if (reinterpret_cast<uintptr_t>(out) % 4) return gm_fail_arg("gm_dequant_f32: out must be 4-byte aligned");
+  const dim3 grid((unsigned)((n_units + 255) / 256)), block(256);
+  const uint8_t* p = static_cast<const uint8_t*>(raw);
+  switch (qtype) {
+    case GM_QTYPE_Q8_0: hipLaunchKernelGGL(k_dequant_k<GM_QTYPE_Q8_0>, grid, block, 0, s, p, n_units, out); break;
+    case GM_QTYPE_Q4_K: hipLaunchKernelGGL(k_dequant_k<GM_QTYPE_Q4_K>, grid, block, 0, s, p, n_units, out); break;
+    case GM_QTYPE_Q5_K: hipLaunchKernelGGL(k_dequant_k<GM_QTYPE_Q5_K>, grid, block, 0, s, p, n_units, out); break;
+    case GM_QTYPE_Q6_K: hipLaunchKernelGGL(k_dequant_k<GM_QTYPE_Q6_K>, grid, block, 0, s, p, n_units, out); break;
+    default: return gm_fail_arg("gm_dequant_f32: unsupported qtype %d", qtype);
+  }
+  GM_TRY(hipGetLastError());
+  return GM_OK;
+}
+
 // --------------------------------------------------------------- matvec
 // Partial dot products of one lane for one row over its sub-blocks.
 template <int QT, int L, int NT>

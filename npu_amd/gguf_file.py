@@ -330,9 +330,9 @@ class TensorStore:
 
     ``raw(name)`` is the mapped tensor (what the device block uploads: quantised bytes are
     never converted on the host); ``get`` / ``get_expert`` return dequantised fp32 numpy
-    arrays in (out, in) order, through the device dequant kernels for IQ3_XXS / IQ4_XS and
-    by element conversion for F32 / F16 / BF16.  Other quant types raise
-    ``NotImplementedError``.
+    arrays in (out, in) order, through the device dequant kernels for IQ3_XXS / IQ4_XS /
+    Q8_0 / Q4_K / Q5_K / Q6_K and by element conversion for F32 / F16 / BF16.  Other
+    quant types raise ``NotImplementedError``.
     """
 
     def __init__(self, path: str | Path):
@@ -364,11 +364,14 @@ class TensorStore:
         if tt == QT.BF16:
             u = np.ascontiguousarray(data).view(np.uint16).astype(np.uint32) << 16
             return u.view(np.float32).reshape(np_shape)
-        if tt in (QT.IQ3_XXS, QT.IQ4_XS):
+        if tt in (QT.IQ3_XXS, QT.IQ4_XS, QT.Q8_0, QT.Q4_K, QT.Q5_K, QT.Q6_K):
             import torch
             from npu_amd import ops
             from npu_amd._dropin import device
-            flat = torch.from_numpy(np.ascontiguousarray(data).reshape(-1)).to(device())
+            flat = np.ascontiguousarray(data).reshape(-1)
+            if not flat.flags.writeable:                   # a read-only map of the file
+                flat = flat.copy()
+            flat = torch.from_numpy(flat).to(device())
             return ops.dequant(tt, flat).cpu().numpy().reshape(np_shape)
         raise NotImplementedError(f"dequantisation of ggml type {tt} is not implemented")
 

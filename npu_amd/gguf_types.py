@@ -54,25 +54,40 @@ class GGMLQuantizationType(enum.IntEnum):
     TQ2_0 = 35
 
 
-_BLOCK_BYTES = {
-    GGMLQuantizationType.IQ4_XS: 136,
-    GGMLQuantizationType.IQ3_XXS: 98,
-    GGMLQuantizationType.BF16: 2 * QK,
-    GGMLQuantizationType.F32: 4 * QK,
+# (weights, bytes) per block of the types the kernels here read
+_BLOCKS = {
+    GGMLQuantizationType.IQ4_XS: (QK, 136),
+    GGMLQuantizationType.IQ3_XXS: (QK, 98),
+    GGMLQuantizationType.Q8_0: (32, 34),
+    GGMLQuantizationType.Q4_K: (QK, 144),
+    GGMLQuantizationType.Q5_K: (QK, 176),
+    GGMLQuantizationType.Q6_K: (QK, 210),
+    GGMLQuantizationType.BF16: (QK, 2 * QK),
+    GGMLQuantizationType.F32: (QK, 4 * QK),
 }
 
 
-def block_bytes(qtype: int) -> int:
+def _block(qtype: int) -> tuple[int, int]:
     try:
-        return _BLOCK_BYTES[GGMLQuantizationType(int(qtype))]
+        return _BLOCKS[GGMLQuantizationType(int(qtype))]
     except (KeyError, ValueError):
         raise ValueError(f"unsupported ggml type {qtype}") from None
 
 
+def block_bytes(qtype: int) -> int:
+    """Bytes of one block (256 weights, or 32 for Q8_0)."""
+    return _block(qtype)[1]
+
+
+def block_weights(qtype: int) -> int:
+    return _block(qtype)[0]
+
+
 def row_bytes(qtype: int, K: int) -> int:
-    if K % QK:
-        raise ValueError(f"K={K} must be a multiple of {QK}")
-    return (K // QK) * block_bytes(qtype)
+    w = block_weights(qtype)
+    if K % w:
+        raise ValueError(f"K={K} must be a multiple of {w}")
+    return (K // w) * block_bytes(qtype)
 
 
 @dataclass

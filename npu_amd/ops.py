@@ -11,7 +11,7 @@ import ctypes
 import torch
 
 from npu_amd import _lib as L
-from npu_amd.gguf_types import QK, GGMLQuantizationType, block_bytes
+from npu_amd.gguf_types import QK, GGMLQuantizationType, block_bytes, block_weights
 
 
 def _as_bf16_bits(w: torch.Tensor) -> torch.Tensor:
@@ -23,7 +23,7 @@ def _as_bf16_bits(w: torch.Tensor) -> torch.Tensor:
 
 
 def dequant(qtype: int, raw: torch.Tensor, n_superblocks: int | None = None) -> torch.Tensor:
-    """Raw superblocks (uint8, on GPU) -> fp32 [n_superblocks * 256]."""
+    """Raw blocks (uint8, on GPU) -> fp32 [n_blocks * block weights] (256, or 32 for Q8_0)."""
     bb = block_bytes(qtype)
     if raw.dtype != torch.uint8:
         raise TypeError(f"raw must be uint8, got {raw.dtype}")
@@ -31,7 +31,7 @@ def dequant(qtype: int, raw: torch.Tensor, n_superblocks: int | None = None) -> 
         if raw.numel() % bb:
             raise ValueError(f"{raw.numel()} bytes is not a whole number of {bb}-byte superblocks")
         n_superblocks = raw.numel() // bb
-    out = torch.empty(n_superblocks * QK, dtype=torch.float32, device=raw.device)
+    out = torch.empty(n_superblocks * block_weights(qtype), dtype=torch.float32, device=raw.device)
     L.check(L.lib().gm_dequant_f32(int(qtype), L.ptr(raw), n_superblocks, L.ptr(out), L.stream_ptr()),
             "gm_dequant_f32")
     return out

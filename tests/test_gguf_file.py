@@ -110,11 +110,11 @@ def _moe_file(tmp_path, rng):
     router = rng.standard_normal((E, D)).astype(np.float32)
     gate_inp_sh = rng.standard_normal(D).astype(np.float16)
     bf = rng.integers(0, 2 ** 16, (FF, D), dtype=np.uint16)
-    q6 = _rand_bytes(rng, D * 210).reshape(D, 210)
+    q6 = _rand_bytes(rng, D * 66).reshape(D, 66)
     tensors = [("blk.0.ffn_gate_inp.weight", int(QT.F32), (D, E), router),
                ("blk.0.ffn_gate_inp_shexp.weight", int(QT.F16), (D,), gate_inp_sh),
                ("blk.0.ffn_up_shexp.weight", int(QT.BF16), (D, FF), bf),
-               ("blk.0.ffn_down_shexp.weight", int(QT.Q6_K), (FF, D), q6)]
+               ("blk.0.ffn_down_shexp.weight", int(QT.IQ2_XXS), (FF, D), q6)]
     p = tmp_path / "moe.gguf"
     G.write_gguf(p, kv, tensors)
     return p, router, gate_inp_sh, bf
@@ -137,7 +137,7 @@ def test_tensor_store_and_config(tmp_path):
     assert np.array_equal(ts.get("blk.0.ffn_up_shexp.weight").view(np.uint32), want_bf.view(np.uint32))
     assert ts.get("blk.0.ffn_up_shexp.weight", dtype="bf16").dtype == np.uint16
     assert ts.cache_bytes() > 0
-    with pytest.raises(NotImplementedError, match="type 14"):
+    with pytest.raises(NotImplementedError, match="type 16"):
         ts.get("blk.0.ffn_down_shexp.weight")
     with pytest.raises(ValueError, match="stacked"):
         ts.get_expert("blk.0.ffn_gate_inp.weight", 0)

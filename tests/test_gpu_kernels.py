@@ -124,3 +124,70 @@ def test_dispatch_stable_sort(gpu, T, k, E):
     assert np.array_equal(counts, np.bincount(flat, minlength=E))
     assert np.array_equal(offsets, np.concatenate([[0], np.cumsum(counts)]))
     assert np.array_equal(pairs, np.argsort(flat, kind="stable"))
+
+
+def _kquant_blocks(rng, qtype, n):
+    """Random blocks of a K-quant / Q8_0 type with finite fp16 d (and dmin)."""
+    from oracle import kquants as KQ
+    w, nb = KQ.BLOCK[qtype]
+    b = rng.integers(0, 256, (n, nb), dtype=np.uint8)
+    d = (rng.standard_normal(n) * 1e-2).astype(np.float16).view(np.uint8).reshape(n, 2)
+    if qtype == KQ.Q6_K:
+        b[:, 208:210] = d
+    else:
+        b[:, 0:2] = d
+        if qtype != KQ.Q8_0:
+            b[:, 2:4] = (np.abs(rng.standard_normal(n)) * 1e-2).astype(np.float16).view(np.uint8).reshape(n, 2)
+    return b
+
+
+@pytest.mark.parametrize("qtype", [QT.Q8_0, QT.Q4_K, QT.Q5_K, QT.Q6_K])
+def test_dequant_kquants_exact(gpu, qtype):
+    """Device dequant of the loader-path types equals the oracle restatement (float equality)."""
+    from oracle import kquants as KQ
+    rng = np.random.default_rng(int(qtype))
+    for n in (1, 7, 300):
+        b = _kquant_blocks(rng, int(qtype), n)
+        got = ops.dequant(int(qtype), torch.from_numpy(b.reshape(-1)).to(gpu)).cpu().numpy()
+        assert np.array_equal(got, KQ.dequant(b, int(qtype)))
+
+
+def test_tensor_store_kquant_shared_expert(gpu, tmp_path):
+    """A layer whose shared expert is Q6_K / Q8_0 in the file (as in the real model): the
+    store dequantises it on the device and the block runs it as a dense bf16 expert."""
+    from npu_amd import gguf_file, qwen_moe
+    from oracle import kquants as KQ
+    rng = np.random.default_rng(7)
+    D, FF, E = 256, 256, 8
+    h = synth.host_moe_layer(70, D=D, FF=FF, E=E, k=2, shared=False)
+    gate_sh = _kquant_blocks(rng, KQ.Q6_K, FF * D // 256).reshape(FF, -1)
+    up_sh = _kquant_blocks(rng, KQ.Q8_0, FF * D // 32).reshape(FF, -1)
+    down_sh = _kquant_blocks(rng, KQ.Q6_K, D * FF // 256).reshape(D, -1)
+    path = tmp_path / "k.gguf"
+    synth.write_gguf_model(path, [h])
+    r = gguf_file.GGUFReader(path)
+    kv = {k: f.contents() for k, f in r.fields.items()}
+    tensors = [(t.name, int(t.tensor_type), t.shape, np.array(t.data)) for t in r.tensors]
+    tensors += [("blk.0.ffn_gate_shexp.weight", int(QT.Q6_K), (D, FF), gate_sh),
+                ("blk.0.ffn_up_shexp.weight", int(QT.Q8_0), (D, FF), up_sh),
+                ("blk.0.ffn_down_shexp.weight", int(QT.Q6_K), (FF, D), down_sh),
+                ("blk.0.ffn_gate_inp_shexp.weight", int(QT.F32), (D,), np.full(D, 0.01, np.float32))]
+    gguf_file.write_gguf(path, kv, tensors)
+    ts = gguf_file.TensorStore(path)
+    g = ts.get("blk.0.ffn_gate_shexp.weight")
+    assert np.array_equal(g, KQ.dequant(gate_sh, KQ.Q6_K).reshape(FF, D))
+    assert np.array_equal(ts.get("blk.0.ffn_up_shexp.weight"), KQ.dequant(up_sh, KQ.Q8_0).reshape(FF, D))
+    layer = qwen_moe.MoELayer.load(ts, 0)
+    assert layer.w_gate_sh is not None and layer.w_gate_sh.shape == (FF, D)
+    x = torch.from_numpy(synth.host_input(3, 1, D)).reshape(1, 1, D)
+    y = qwen_moe.moe_forward(x, layer, ts.cfg)
+    # reference: routed part from the oracle, shared expert in fp64 from the dequantised weights
+    routed = OM.moe_forward(x, OM.OracleLayer(h)).double()
+    xs = x.reshape(1, D).double()
+    gs, us, ds = (torch.from_numpy(KQ.dequant(a, t).reshape(shp)).double() for a, t, shp in
+                  ((gate_sh, KQ.Q6_K, (FF, D)), (up_sh, KQ.Q8_0, (FF, D)), (down_sh, KQ.Q6_K, (D, FF))))
+    # the device block runs the dense shared expert in bf16 weights: compare at the bf16 bar
+    hsh = F.silu(xs @ gs.T) * (xs @ us.T)
+    sgate = torch.sigmoid(xs @ torch.full((D,), 0.01, dtype=torch.float64))
+    ref = routed.reshape(1, D) + sgate * (hsh @ ds.T)
+    assert OM.rel_err(y.reshape(1, D).double(), ref) <= 1e-2
