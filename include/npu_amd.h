@@ -140,7 +140,7 @@ int gm_moe_workspace_offsets(const gm_moe_layer* L, int T, size_t* off_logits, s
  * xn = rmsnorm(x) when L->norm_w != NULL.  Routing, dispatch, expert
  * products, shared expert and the combine all run on the device from
  * device-resident ids (no host synchronisation).  T <= 8 uses the decode
- * kernels (fp32 accumulate); larger T uses the grouped bf16-MFMA prefill.
+ * kernels (fp32 accumulate); larger T uses the grouped MFMA prefill.
  * x and y must not alias.  Replaces qwen/forward.py:moe_forward (563-665).
  */
 int gm_moe_forward(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
@@ -150,7 +150,7 @@ int gm_moe_forward(const gm_moe_layer* L, const float* x, float* y, int T, int f
  * gm_moe_forward forced onto one path.  gm_moe_decode: the fp32-accumulate
  * decode kernels, 1 <= T <= 8 (the reference's NPU expert path is T = 1:
  * qwen/forward.py:494-560 via _npu_routed_expert).  gm_moe_prefill: the
- * grouped bf16-MFMA GEMMs for any T >= 1 (the reference runs prefill through
+ * grouped f16/bf16-MFMA GEMMs for any T >= 1 (the reference runs prefill through
  * the CPU loop of qwen/forward.py:622-663).  Same workspace as gm_moe_forward.
  */
 int gm_moe_decode(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,

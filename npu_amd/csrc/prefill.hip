@@ -17,10 +17,13 @@
 //                     multiplies the fp32 partial sum of each superblock.  The
 //                     segment's activation tile is double-buffered in LDS.  h is
 //                     stored as bf16 in expert-sorted row order.
-//   5. k_pf_down:     per (segment, 256 weight rows): y_pair = Down_e h on
-//                     v_mfma_f32_16x16x32_bf16 (h keeps bf16's range), fp32 out;
-//                     the segment's h tile is staged in LDS once per block
-//   6. k_pf_combine:  y[t] = sum over t's experts in ascending id of w * y_pair
+//   5. k_pf_h16:      every h row scaled by a power of two into f16's range and
+//                     converted exactly (the scale is kept per row)
+//   6. k_pf_down:     per (segment, 2 x 128 weight rows): y_pair = Down_e h on
+//                     v_mfma_f32_16x16x32_f16 with f16 integer weight operands as in
+//                     4, fp32 out times the row's h scale; the segment's h tile is
+//                     staged in LDS once per block
+//   7. k_pf_combine:  y[t] = sum over t's experts in ascending id of w * y_pair
 //                     + sigmoid gate * y_shared (+ x); fixed order, no atomics
 //
 // Reference semantics: the CPU loop of qwen/forward.py:563-665 (prefill takes

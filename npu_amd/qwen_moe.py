@@ -8,7 +8,7 @@ MoE block (router, top-k, dispatch, expert products, shared expert, combine)
 executes on the GPU from raw GGUF expert bytes resident in HBM, with routing
 kept on the device (no ``picked.tolist()`` host loop).  There is no CPU path:
 ``moe_forward`` builds the device block on first use if ``enable_npu`` was not
-called.  Prefill (T > 8 tokens) uses the grouped bf16-MFMA kernels.
+called.  Prefill (T > 8 tokens) uses the grouped MFMA kernels.
 
 ``SyntheticTensorStore`` provides the ``TensorStore`` surface (``get``,
 ``raw``, ``get_expert``, ``cfg``) over seeded synthetic layers, since the
