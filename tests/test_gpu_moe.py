@@ -113,3 +113,12 @@ def test_t1_graph_replays(gpu):
         assert torch.equal(y, y_eager), f"replay {i}"
         _ = blk(x + 0.0)                      # eager work on the same workspace between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("D,FF,E,k", [(256, 256, 512, 8), (4096, 256, 16, 4), (256, 2048, 8, 2)])
+@pytest.mark.parametrize("T", [1, 8])
+def test_size_limits(gpu, D, FF, E, k, T):
+    """The limits the decode kernels accept: E up to 512 (the 8-values-per-lane top-k),
+    D up to 4096 (4 weight chunks per lane), FF up to 2048 (the general path at T = 1)."""
+    h = synth.host_moe_layer(100 + k, D=D, FF=FF, E=E, k=k, norm=True)
+    _check(gpu, h, T, residual=True, seed=T, rmsnorm_input=False)

@@ -1,4 +1,4 @@
-"""GPU parity of the MoE block prefill path (T > 8: grouped bf16-MFMA GEMMs).
+"""GPU parity of the MoE block prefill path (T > 8: grouped MFMA GEMMs).
 
 Oracle: oracle.moe.block_forward, the restatement of qwen/forward.py:563-665
 (the reference runs prefill through the same CPU loop).  Bar: top-k ids
@@ -103,3 +103,20 @@ def test_prefill_path_at_decode_sizes(gpu, T):
         assert OM.rel_err(yp, ref) <= REL_TOL
         assert OM.rel_err(yd, ref) <= 1e-3
         assert OM.rel_err(yp, yd) <= REL_TOL
+
+
+@pytest.mark.parametrize("D,FF,E,k,T", [(256, 256, 512, 8, 40), (4096, 256, 16, 4, 20), (256, 1024, 8, 2, 24)])
+def test_prefill_size_limits(gpu, D, FF, E, k, T):
+    """Prefill at the limits it accepts: E = 512 (dispatch histogram width, 8-per-lane top-k),
+    D = 4096, FF = 1024 (the 4-superblock h tile of the down kernel)."""
+    h = synth.host_moe_layer(110 + k, D=D, FF=FF, E=E, k=k, bias=True)
+    _check(gpu, h, T, seed=k)
+
+
+def test_prefill_rejects_wide_ff(gpu):
+    """FF > 1024 is outside the prefill kernels' h tile: a clear error, nothing launched."""
+    h = synth.host_moe_layer(120, D=256, FF=2048, E=4, k=2)
+    blk = GpuMoeBlock.from_host(h, device=gpu)
+    x = torch.from_numpy(synth.host_input(1, 12, h.D)).to(gpu)
+    with pytest.raises(ValueError, match="FF"):
+        blk(x, path="prefill")
