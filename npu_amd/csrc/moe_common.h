@@ -95,9 +95,7 @@ __device__ __forceinline__ void stage_rows_il(const float* __restrict__ src, int
 
 // ------------------------------------------------------------------ top-k
 // One wave: top-k of E logits (descending, ties -> lower id), softmax over all
-// E, renormalised top-k probabilities (qwen/forward.py:609-611).  Each lane
-// sorts its MAXV values once; every round takes the wave-wide best lane head
-// (DPP inside 16-lane rows, readlane across rows) and pops it.
+// E, renormalised top-k probabilities (qwen/forward.py:609-611).
 // Lane values of one wave's top-k input: logits lane + 64 i (clamped loads,
 // so every lane issues the same MAXV loads; out-of-range entries are masked
 // in topk_finish).
@@ -119,15 +117,6 @@ __device__ __forceinline__ int fkey(float f) {
 }
 __device__ __forceinline__ float fkey_inv(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7fffffff); }
 
-__device__ __forceinline__ int wave_max_int_uniform(int v) {
-  v = max(v, GM_DPP_I(v, GM_ROW_ROR8));
-  v = max(v, GM_DPP_I(v, GM_ROW_ROR4));
-  v = max(v, GM_DPP_I(v, GM_QPERM_2301));
-  v = max(v, GM_DPP_I(v, GM_QPERM_1032));
-  return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-             max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
-}
-
 __device__ __forceinline__ int wave_min_int_uniform(int v) {
   v = min(v, GM_DPP_I(v, GM_ROW_ROR8));
   v = min(v, GM_DPP_I(v, GM_ROW_ROR4));
@@ -137,58 +126,103 @@ __device__ __forceinline__ int wave_min_int_uniform(int v) {
              min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
-// Every round takes the wave-wide largest lane head (a max reduction, then a
-// ballot of the lanes holding it; an exact tie goes to the lowest expert id)
-// and pops it.  The softmax weights of the k winners are computed afterwards,
-// one per lane, in parallel.
-// Lane r < k ends with pick r: its expert id (out_id) and renormalised weight
-// (out_w); other lanes get INT_MAX / 0.
+// max(v, lane-shuffled v) in one DPP instruction; lanes the row mask leaves out
+// see INT_MIN, the identity of max, so they keep v.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_max_i(int v) {
+  return max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, CTRL, ROWS, 0xF, false));
+}
+
+// Wave-wide max: four steps inside each 16-lane row, then row_bcast15 /
+// row_bcast31 carry the row maxima up so that lane 63 holds the total.
+__device__ __forceinline__ int wave_max_int_l63(int v) {
+  v = dpp_max_i<GM_QPERM_1032, 0xF>(v);
+  v = dpp_max_i<GM_QPERM_2301, 0xF>(v);
+  v = dpp_max_i<0x141, 0xF>(v);                 // row_half_mirror
+  v = dpp_max_i<0x140, 0xF>(v);                 // row_mirror
+  v = dpp_max_i<0x142, 0xA>(v);                 // row_bcast15 -> rows 1 and 3
+  v = dpp_max_i<0x143, 0xC>(v);                 // row_bcast31 -> rows 2 and 3
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// Selection: each lane sorts its MAXV keys once (descending; the lane's
+// indices ascend, so equal keys keep the lower id first); every round takes
+// the wave-wide largest lane head, the lane holding it (an exact tie between
+// lanes goes to the lower expert id) pops it.  Lane r < k ends with pick r:
+// its expert id (out_id) and key (out_key); skey keeps the sorted keys for
+// topk_weights.  Other lanes get INT_MAX / INT_MIN.
 template <int MAXV>
-__device__ __forceinline__ void topk_finish(float (&v)[MAXV], int (&ix)[MAXV], int E, int k, int& out_id,
-                                            float& out_w) {
+__device__ __forceinline__ void topk_select(const float (&v)[MAXV], const int (&ix0)[MAXV], int E, int k,
+                                            int& out_id, int& out_key, int (&skey)[MAXV]) {
   const int lane = threadIdx.x & 63;
-  int key[MAXV];
+  int key[MAXV], ix[MAXV];
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i) key[i] = ix[i] < E ? fkey(v[i]) : INT_MIN;
-  // per-lane sort, descending (ties: lower index first)
+  for (int i = 0; i < MAXV; ++i) {
+    ix[i] = ix0[i];
+    key[i] = ix[i] < E ? fkey(v[i]) : INT_MIN;
+  }
 #pragma unroll
   for (int a = 0; a < MAXV; ++a)
 #pragma unroll
-    for (int b = MAXV - 1; b > a; --b)
-      if (key[b] > key[b - 1] || (key[b] == key[b - 1] && ix[b] < ix[b - 1])) {
-        const int tk = key[b]; key[b] = key[b - 1]; key[b - 1] = tk;
-        const int ti = ix[b]; ix[b] = ix[b - 1]; ix[b - 1] = ti;
-      }
-  // softmax normaliser over all E
-  const float m = fkey_inv(wave_max_int_uniform(key[0]));
+    for (int b = MAXV - 1; b > a; --b) {
+      const bool sw = key[b] > key[b - 1];
+      const int tk = key[b], ti = ix[b];
+      key[b] = sw ? key[b - 1] : key[b];
+      ix[b] = sw ? ix[b - 1] : ix[b];
+      key[b - 1] = sw ? tk : key[b - 1];
+      ix[b - 1] = sw ? ti : ix[b - 1];
+    }
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) skey[i] = key[i];
+  int mykey = INT_MIN, myid = 0x7fffffff;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    if (r >= k) break;
+    const int hm = wave_max_int_l63(key[0]);
+    const uint64_t bal = __ballot(key[0] == hm);
+    int wl = (int)__builtin_ctzll(bal);
+    if (__builtin_expect((bal & (bal - 1)) != 0, 0))
+      wl = wave_min_int_uniform(key[0] == hm ? ix[0] : 0x7fffffff) & 63;
+    const int wi = __builtin_amdgcn_readlane(ix[0], wl);
+    mykey = lane == r ? hm : mykey;
+    myid = lane == r ? wi : myid;
+    const bool pop = lane == wl;
+#pragma unroll
+    for (int i = 0; i + 1 < MAXV; ++i) {
+      key[i] = pop ? key[i + 1] : key[i];
+      ix[i] = pop ? ix[i + 1] : ix[i];
+    }
+    key[MAXV - 1] = pop ? INT_MIN : key[MAXV - 1];
+    ix[MAXV - 1] = pop ? 0x7fffffff : ix[MAXV - 1];
+  }
+  out_id = myid;
+  out_key = mykey;
+}
+
+// Renormalised softmax probability of the pick in lane r < k (0 elsewhere):
+// softmax over all E (the normaliser summed over skey, lane-sorted), then
+// p / max(sum of the k picks, 1e-20).  Pick 0 is the maximum logit.
+template <int MAXV>
+__device__ __forceinline__ float topk_weights(const int (&skey)[MAXV], int k, int mykey) {
+  const int lane = threadIdx.x & 63;
+  const float m = fkey_inv(__builtin_amdgcn_readlane(mykey, 0));
   float z = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXV; ++i)
-    if (key[i] != INT_MIN) z += expf(fkey_inv(key[i]) - m);
+    if (skey[i] != INT_MIN) z += expf(fkey_inv(skey[i]) - m);
   z = gm_wave_sum64(z);
-  int mykey = INT_MIN, myid = 0;
-  for (int r = 0; r < k; ++r) {
-    const int hm = wave_max_int_uniform(key[0]);
-    const uint64_t bal = __ballot(key[0] == hm);
-    int wl;
-    if (__popcll(bal) == 1) {
-      wl = __ffsll((unsigned long long)bal) - 1;
-    } else {                        // exact tie: lowest expert id among the tied heads
-      wl = wave_min_int_uniform(key[0] == hm ? ix[0] : 0x7fffffff) & 63;
-    }
-    const int wi = __builtin_amdgcn_readlane(ix[0], wl);
-    if (lane == r) { mykey = hm; myid = wi; }
-    if (lane == wl) {               // pop the winner's head
-#pragma unroll
-      for (int i = 0; i + 1 < MAXV; ++i) { key[i] = key[i + 1]; ix[i] = ix[i + 1]; }
-      key[MAXV - 1] = INT_MIN;
-      ix[MAXV - 1] = 0x7fffffff;
-    }
-  }
   const float p = lane < k ? expf(fkey_inv(mykey) - m) / z : 0.f;
   const float den = fmaxf(gm_wave_sum64(p), 1e-20f);
-  out_id = lane < k ? myid : 0x7fffffff;
-  out_w = p / den;
+  return p / den;
+}
+
+// Both: lane r < k ends with pick r's expert id and renormalised weight.
+template <int MAXV>
+__device__ __forceinline__ void topk_finish(const float (&v)[MAXV], const int (&ix)[MAXV], int E, int k,
+                                            int& out_id, float& out_w) {
+  int key, skey[MAXV];
+  topk_select<MAXV>(v, ix, E, k, out_id, key, skey);
+  out_w = topk_weights<MAXV>(skey, k, key);
 }
 
 template <int MAXV>

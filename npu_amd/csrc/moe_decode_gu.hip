@@ -1,10 +1,11 @@
 // MoE decode, stage 2: top-k routing, expert grouping, routed gate/up + SwiGLU.
 //
-// T = 1 (k_dec_gateup1): every block recomputes the token's top-k from the
-// router logits (wave 0, while wave 1 stages x) instead of waiting for a
-// separate routing kernel, picks the expert of rank `u` among the k picks
+// T = 1 (k_dec_gateup1): every block recomputes the token's top-k selection
+// from the router logits (wave 0, while wave 1 stages x) instead of waiting for
+// a separate routing kernel, picks the expert of rank `u` among the k picks
 // (ascending id, the order of torch.unique in qwen/forward.py:612) and runs 8
-// SwiGLU rows of it.  Block 0 publishes ids, weights and the grouping table
+// SwiGLU rows of it.  Block 0 also computes the routing weights, once its
+// weight rows are in flight, and publishes ids, weights and the grouping table
 // for stage 3.
 //
 // T > 1: k_dec_route (one block) runs the per-token top-k and groups the
@@ -34,29 +35,17 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
   const int u = blockIdx.x / n_chunks, chunk = blockIdx.x - u * n_chunks;
   uint32_t gw = 0;
   if constexpr (IQ3) gw = gm_iq3_tab_load();
+  int myid = 0, mykey = 0, rk = 0, skey[MAXV];
   if (wave == 0) {
-    // top-k of the router logits; lane j < k holds pick j
+    // top-k selection of the router logits; lane j < k holds pick j
     float v[MAXV];
     int ix[MAXV];
     topk_load<MAXV>(logits, E, v, ix);
-    int myid;
-    float myw;
-    topk_finish<MAXV>(v, ix, E, k, myid, myw);
-    int rk = 0;                                                // rank of the pick among the k (distinct) ids
+    topk_select<MAXV>(v, ix, E, k, myid, mykey, skey);
+    // rank of the pick among the k (distinct) ids
 #pragma unroll
     for (int i = 0; i < 8; ++i) rk += __builtin_amdgcn_readlane(myid, i) < myid ? 1 : 0;
     if (lane < k) { s_sid[rk] = myid; s_slot[rk] = lane; }
-    if (blockIdx.x == 0) {                                     // publish for stage 3 and the caller
-      if (lane < k) {
-        g_ids[lane] = myid;
-        g_wts[lane] = myw;
-        g_grp[1 + rk] = myid;
-        g_grp[1 + GM_GRP_MAXU + rk] = 1;
-        g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * rk] = lane;
-        g_grp[GM_GRP_WORDS + rk] = __float_as_int(myw);
-      }
-      if (lane == 0) g_grp[0] = k;
-    }
   } else if (wave == 1) {
     stage_limbs_wave<4 * DC>(x, D, P.norm_w, P.norm_eps, xs);  // concurrently with the top-k
   }
@@ -70,6 +59,21 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
   RowFetch<QT, DC> fg, fu;
   fetch_subs<QT, 32, DC>(fg, static_cast<const uint8_t*>(P.gate_exps) + ((int64_t)e * FF + r) * rb, lane & 31, nsub);
   fetch_subs<QT, 32, DC>(fu, static_cast<const uint8_t*>(P.up_exps) + ((int64_t)e * FF + r) * rb, lane & 31, nsub);
+  if (blockIdx.x == 0 && wave == 0) {
+    // publish ids, weights and the grouping table for stage 3 and the caller
+    // (the softmax weights are needed by nobody else, so they are computed
+    // while this block's weight rows are in flight)
+    const float myw = topk_weights<MAXV>(skey, k, mykey);
+    if (lane < k) {
+      g_ids[lane] = myid;
+      g_wts[lane] = myw;
+      g_grp[1 + rk] = myid;
+      g_grp[1 + GM_GRP_MAXU + rk] = 1;
+      g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * rk] = lane;
+      g_grp[GM_GRP_WORDS + rk] = __float_as_int(myw);
+    }
+    if (lane == 0) g_grp[0] = k;
+  }
   const int tok[1] = {0};
   float ag[1] = {0.f}, au[1] = {0.f};
   dot_subs_i8<QT, 32, DC, 1>(fg, lane & 31, nsub, xs, rbytes, tok, 1, tab, ag);
