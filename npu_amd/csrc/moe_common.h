@@ -479,6 +479,29 @@ __device__ __forceinline__ void stage_limbs_wave(const float* __restrict__ x, in
   }
 }
 
+// One wave copies a limb row of D <= 1024 DC activations (rbytes bytes) from
+// global memory into the LDS row `row` (+ its spare sub-block): every lane
+// issues all of its 16-byte loads before its first store.
+template <int DC>
+__device__ __forceinline__ void copy_limbs_wave(const uint8_t* __restrict__ src, int rbytes,
+                                                uint8_t* __restrict__ row) {
+  constexpr int CPL = (32 * DC * GM_LSUB / 16 + 63) / 64;
+  const int lane = threadIdx.x & 63, n16 = rbytes >> 4;
+  const gm_u32x4* s4 = reinterpret_cast<const gm_u32x4*>(src);
+  gm_u32x4* d4 = reinterpret_cast<gm_u32x4*>(row);
+  gm_u32x4 r[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = lane + 64 * i;
+    r[i] = s4[c < n16 ? c : n16 - 1];
+  }
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = lane + 64 * i;
+    d4[c < n16 ? c : n16 + (c & 3)] = r[i];
+  }
+}
+
 // acc[m] += W_row . act[idx[m]] over the fetched sub-blocks, m < nt; act rows
 // are limb rows of row_bytes bytes.  BF16 weights (a shared expert kept in
 // bf16) take the activations back to fp32 from their limbs.

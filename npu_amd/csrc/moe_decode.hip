@@ -24,11 +24,12 @@ namespace {
 
 // Blocks [0, n_rb): one router row per wave (64 lanes; row E is the shared
 // scalar gate).  Blocks [n_rb, ...): two shared gate/up rows per wave (32 lanes
-// per row).  DC = ceil(D / 1024).
+// per row); block n_rb also writes its limb rows of the RMSNorm'd x to xl_out
+// (when set) for the gate/up kernel.  DC = ceil(D / 1024).
 template <int QTS, int NT, int DC>
 __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float* __restrict__ x, int T,
                                                     float* __restrict__ logits, float* __restrict__ shg,
-                                                    float* __restrict__ hsh, int n_rb) {
+                                                    float* __restrict__ hsh, int n_rb, uint8_t* __restrict__ xl_out) {
   constexpr int SPLR = DC > 1 ? DC / 2 : 1;
   constexpr bool IQ3 = QTS == GM_QTYPE_IQ3_XXS;
   extern __shared__ float smem[];
@@ -92,6 +93,11 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
   for (int m = 0; m < NT; ++m) {
     const float hv = gm_silu(row_sum<32>(ag[m])) * row_sum<32>(au[m]);
     if (live && (lane & 31) == 0 && m < T) hsh[m * FFs + row] = hv;
+  }
+  if (xl_out != nullptr && (int)blockIdx.x == n_rb) {         // the limb rows for the gate/up kernel
+    const gm_u32x4* src = reinterpret_cast<const gm_u32x4*>(xl);
+    gm_u32x4* dst = reinterpret_cast<gm_u32x4*>(xl_out);
+    for (int c = threadIdx.x; c < NT * (rbytes >> 4); c += 256) dst[c] = src[c];
   }
 }
 
@@ -171,7 +177,7 @@ int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArg
   const size_t smem = ((size_t)NT * P->D + 4 + 4 * NT) * 4 + (QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
   if (int rc = gm_set_smem(k_dec_router<QTS, NT, DC>, smem)) return rc;
   hipLaunchKernelGGL((k_dec_router<QTS, NT, DC>), dim3(n_rb + n_sb), dim3(256), smem, s, *P, x, T, a.logits, a.shg,
-                     a.hsh, n_rb);
+                     a.hsh, n_rb, n_sb > 0 ? a.xl : nullptr);
   GM_TRY(hipGetLastError());
   return GM_OK;
 }

@@ -1,7 +1,8 @@
 // MoE decode, stage 2: top-k routing, expert grouping, routed gate/up + SwiGLU.
 //
 // T = 1 (k_dec_gateup1): every block recomputes the token's top-k selection
-// from the router logits (wave 0, while wave 1 stages x) instead of waiting for
+// from the router logits (wave 0, while wave 1 copies the limb row of x that
+// the router kernel wrote, or stages it itself) instead of waiting for
 // a separate routing kernel, picks the expert of rank `u` among the k picks
 // (ascending id, the order of torch.unique in qwen/forward.py:612) and runs 8
 // SwiGLU rows of it.  Block 0 also computes the routing weights, once its
@@ -24,7 +25,8 @@ template <int QT, int DC, int MAXV>
 __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float* __restrict__ x,
                                                      const float* __restrict__ logits, int32_t* __restrict__ g_ids,
                                                      float* __restrict__ g_wts, int32_t* __restrict__ g_grp,
-                                                     float* __restrict__ h, int n_chunks) {
+                                                     float* __restrict__ h, int n_chunks,
+                                                     const uint8_t* __restrict__ xl) {
   constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int D = P.D, E = P.E, k = P.k, FF = P.FF, nsub = D / GM_SUB, rbytes = gm_limb_row_bytes(D);
@@ -46,8 +48,9 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
 #pragma unroll
     for (int i = 0; i < 8; ++i) rk += __builtin_amdgcn_readlane(myid, i) < myid ? 1 : 0;
     if (lane < k) { s_sid[rk] = myid; s_slot[rk] = lane; }
-  } else if (wave == 1) {
-    stage_limbs_wave<4 * DC>(x, D, P.norm_w, P.norm_eps, xs);  // concurrently with the top-k
+  } else if (wave == 1) {                                     // concurrently with the top-k
+    if (xl != nullptr) copy_limbs_wave<DC>(xl, rbytes, xs);
+    else stage_limbs_wave<4 * DC>(x, D, P.norm_w, P.norm_eps, xs);
   }
   if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
   __syncthreads();
@@ -285,12 +288,13 @@ int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const Gm
     const size_t smem = (size_t)gm_limb_row_bytes(P->D) + GM_LSUB + (QT == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
     if (int rc = gm_set_smem(k_dec_gateup1<QT, DC, 4>, smem)) return rc;
     if (int rc = gm_set_smem(k_dec_gateup1<QT, DC, 8>, smem)) return rc;
+    const uint8_t* xl = P->gate_sh ? a.xl : nullptr;           // written by the router kernel's shared blocks
     if (P->E <= 256)
       hipLaunchKernelGGL((k_dec_gateup1<QT, DC, 4>), dim3(P->k * n_chunks), dim3(256), smem, s, *P, x, a.logits,
-                         a.ids, a.wts, a.grp, a.h, n_chunks);
+                         a.ids, a.wts, a.grp, a.h, n_chunks, xl);
     else
       hipLaunchKernelGGL((k_dec_gateup1<QT, DC, 8>), dim3(P->k * n_chunks), dim3(256), smem, s, *P, x, a.logits,
-                         a.ids, a.wts, a.grp, a.h, n_chunks);
+                         a.ids, a.wts, a.grp, a.h, n_chunks, xl);
     GM_TRY(hipGetLastError());
     return GM_OK;
   }
