@@ -62,6 +62,17 @@ def test_small_blocks(gpu, q_gate, q_down, T, shared):
     _check(gpu, h, T, seed=T)
 
 
+@pytest.mark.parametrize("q_gate", [QT.IQ4_XS, QT.IQ3_XXS])
+@pytest.mark.parametrize("T", [2, 5, 8])
+@pytest.mark.parametrize("shared", [True, False])
+def test_grouped_d2048(gpu, q_gate, T, shared):
+    """The config-5 width (D = 2048) at T > 1 with E = 16 and top-4: units of several
+    member tokens in the grouped gate/up and down kernels, with and without the shared
+    expert."""
+    h = synth.host_moe_layer(30 + T, D=2048, FF=256, E=16, k=4, q_gate=q_gate, q_down=QT.IQ3_XXS, shared=shared)
+    _check(gpu, h, T, seed=T + 1)
+
+
 @pytest.mark.parametrize("T", [1, 8])
 def test_norm_and_residual(gpu, T):
     """RMSNorm fused in front (weight != 1) and the residual add of qwen/forward.py:880-884."""
