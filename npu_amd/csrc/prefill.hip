@@ -76,10 +76,11 @@ struct PfWs {
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-constexpr int kRouterSplit = 8;   // most K ranges of the router GEMM (partials summed in k_pf_topk)
+constexpr int kRouterSplit = 16;  // most K ranges of the router GEMM (partials summed in k_pf_topk)
 
-// K ranges actually used: each must hold an even number of 32-wide k-steps.
-int router_split(int D) { return D % (64 * kRouterSplit) == 0 ? kRouterSplit : 4; }
+// K ranges actually used: 512 wide (4 k-steps per wave) when D allows, else 256.
+int router_krange(int D) { return D % 512 == 0 ? 512 : 256; }
+int router_split(int D) { return D / router_krange(D); }
 
 // Row stride of the router partials: E rows + the shared gate row, padded to 4.
 int router_ld(const gm_moe_layer* L) { return (L->E + 1 + 3) & ~3; }
@@ -159,12 +160,14 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
 }
 
 // ---------------------------------------------------------------- router
-// Partial router dot products part[z][t][r] = xn[t] . W[r] over the z-th of
-// gridDim.z equal K ranges (each an even number of k-steps), rows r < E of W and row E = the shared gate vector
-// (qwen/forward.py:599-600, 608).  Block: 64 rows x 64 tokens x one K range;
-// wave w takes tokens 16w .. 16w+15 against the 4 row tiles.  MFMA operand
-// layout (16x16x32): lane l holds row / column l % 16 at k = 8 (l / 16) .. +7.
-// Operands are fetched two k-steps ahead.
+// Partial router dot products part[z][t][r] = xn[t] . W[r] over the z-th K range
+// of kr = 128 NK values (rows r < E of W and row E = the shared gate vector,
+// qwen/forward.py:599-600, 608).  Block: 64 rows x 16 tokens x one K range;
+// wave w takes the w-th quarter of the range for all four 16-row tiles, and
+// issues every operand load of its NK k-steps before its first MFMA (one
+// memory round trip).  The four waves' tiles are added in LDS in wave order.
+// MFMA operand layout (16x16x32): lane l holds row / column l % 16 at
+// k = 8 (l / 16) .. +7.
 
 __device__ __forceinline__ void router_step(const gm_u32x4 (&a)[4], const gm_u32x4 (&b)[3], gm_f32x4 (&acc)[4]) {
 #pragma unroll
@@ -175,46 +178,47 @@ __device__ __forceinline__ void router_step(const gm_u32x4 (&a)[4], const gm_u32
                                                         __builtin_bit_cast(gm_bf16x8, b[p]), acc[rt], 0, 0, 0);
 }
 
+template <int NK>
 __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ w, const uint16_t* __restrict__ wsh,
                                                    const uint16_t* __restrict__ xr, int T, int D, int E, int ldp,
                                                    float* __restrict__ part) {
+  __shared__ gm_f32x4 red[3][4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
   const int nrows = E + (wsh ? 1 : 0);
   const int r0 = blockIdx.x * 64;
-  const int tok = blockIdx.y * 64 + wave * 16 + l16;
+  const int tok = blockIdx.y * 16 + l16;
   const int tokc = tok < T ? tok : T - 1;
-  const int kr = D / (int)gridDim.z, k0 = blockIdx.z * kr, nk = kr / 32;
-  const gm_u32x4* arow[4];
+  const int k0 = (blockIdx.z * 4 + wave) * (32 * NK);
+  const int64_t plane = (int64_t)T * D / 8;                     // in 16-byte units
+  const gm_u32x4* brow = reinterpret_cast<const gm_u32x4*>(xr + (int64_t)tokc * D + k0 + 8 * q);
+  gm_u32x4 a[NK][4], b[NK][3];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) {
     const int row = r0 + rt * 16 + l16;
-    const uint16_t* p = row < E ? w + (int64_t)row * D : (row == E && wsh ? wsh : w);
-    arow[rt] = reinterpret_cast<const gm_u32x4*>(p + k0 + 8 * q);
+    const uint16_t* pr = row < E ? w + (int64_t)row * D : (row == E && wsh ? wsh : w);
+    const gm_u32x4* ar = reinterpret_cast<const gm_u32x4*>(pr + k0 + 8 * q);
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) a[ks][rt] = ar[4 * ks];
   }
-  const int64_t plane = (int64_t)T * D / 8;                     // in 16-byte units
-  const gm_u32x4* brow = reinterpret_cast<const gm_u32x4*>(xr + (int64_t)tokc * D + k0 + 8 * q);
+#pragma unroll
+  for (int ks = 0; ks < NK; ++ks)
+#pragma unroll
+    for (int p = 0; p < 3; ++p) b[ks][p] = brow[p * plane + 4 * ks];
   gm_f32x4 acc[4];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) acc[rt] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
-  gm_u32x4 a0[4], b0[3], a1[4], b1[3];
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) { a0[rt] = arow[rt][0]; a1[rt] = arow[rt][4]; }
+  for (int ks = 0; ks < NK; ++ks) router_step(a[ks], b[ks], acc);
+  if (wave > 0) {
 #pragma unroll
-  for (int p = 0; p < 3; ++p) { b0[p] = brow[p * plane]; b1[p] = brow[p * plane + 4]; }
-  for (int ks = 0; ks < nk; ks += 2) {                          // nk is even
-    const int n0 = (ks + 2 < nk ? ks + 2 : ks) * 4, n1 = (ks + 3 < nk ? ks + 3 : ks + 1) * 4;
-    router_step(a0, b0, acc);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) a0[rt] = arow[rt][n0];
-#pragma unroll
-    for (int p = 0; p < 3; ++p) b0[p] = brow[p * plane + n0];
-    router_step(a1, b1, acc);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) a1[rt] = arow[rt][n1];
-#pragma unroll
-    for (int p = 0; p < 3; ++p) b1[p] = brow[p * plane + n1];
+    for (int rt = 0; rt < 4; ++rt) red[wave - 1][rt][lane] = acc[rt];
   }
-  if (tok >= T) return;
+  __syncthreads();
+  if (wave > 0 || tok >= T) return;
+#pragma unroll
+  for (int v = 0; v < 3; ++v)
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) acc[rt] += red[v][rt][lane];
   float* out = part + ((int64_t)blockIdx.z * T + tok) * ldp;
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) {
@@ -227,10 +231,11 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
   }
 }
 
-// One wave per token: logits = sum of the nsplit partials (fixed order)
+// One wave per token: logits = sum of the nsplit <= NZ partials (fixed order)
 // + bias, the shared gate sigmoid, and the top-k (ties -> lower id) with
-// renormalised softmax weights (qwen/forward.py:609-611).
-template <int MAXV>
+// renormalised softmax weights (qwen/forward.py:609-611).  Every partial is
+// loaded (clamped index) before any is summed.
+template <int MAXV, int NZ>
 __global__ void __launch_bounds__(256) k_pf_topk(const float* __restrict__ part, int ldp, int nsplit, int T, int E, int k,
                                                  int has_gate, const float* __restrict__ bias,
                                                  float* __restrict__ logits, float* __restrict__ shg,
@@ -239,22 +244,32 @@ __global__ void __launch_bounds__(256) k_pf_topk(const float* __restrict__ part,
   if (t >= T) return;
   const int64_t zs = (int64_t)T * ldp;
   const float* pt = part + (int64_t)t * ldp;
-  float v[MAXV];
+  float v[MAXV], pv[MAXV][NZ], pg[NZ];
   int ix[MAXV];
+#pragma unroll
+  for (int z = 0; z < NZ; ++z) {
+    const int64_t zo = (int64_t)(z < nsplit ? z : nsplit - 1) * zs;
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+      const int r = lane + 64 * i;
+      pv[i][z] = pt[zo + (r < E ? r : E - 1)];
+    }
+    pg[z] = pt[zo + E];
+  }
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
     ix[i] = lane + 64 * i;
     const int r = ix[i] < E ? ix[i] : E - 1;
     float acc = 0.f;
 #pragma unroll
-    for (int z = 0; z < nsplit; ++z) acc += pt[z * zs + r];
+    for (int z = 0; z < NZ; ++z) acc += z < nsplit ? pv[i][z] : 0.f;
     v[i] = acc + (bias ? bias[r] : 0.f);
     if (ix[i] < E) logits[(int64_t)t * E + ix[i]] = v[i];
   }
   if (has_gate && lane == 0) {
     float g = 0.f;
 #pragma unroll
-    for (int z = 0; z < nsplit; ++z) g += pt[z * zs + E];
+    for (int z = 0; z < NZ; ++z) g += z < nsplit ? pg[z] : 0.f;
     shg[t] = gm_sigmoid(g);
   }
   int id;
@@ -870,15 +885,32 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
   GM_TRY(hipGetLastError());
   const int ldp = router_ld(L);
   const int nsplit = router_split(D);
-  hipLaunchKernelGGL(k_pf_router, dim3((nrows + 63) / 64, (T + 63) / 64, nsplit), dim3(256), 0, s, L->router,
-                     L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
-  GM_TRY(hipGetLastError());
-  if (E <= 256)
-    hipLaunchKernelGGL(k_pf_topk<4>, dim3((T + 3) / 4), dim3(256), 0, s, w.part, ldp, nsplit, T, E, k,
-                       L->sh_gate_inp ? 1 : 0, L->router_bias, logits, shg, ids, wts);
+  if (router_krange(D) == 512)
+    hipLaunchKernelGGL(k_pf_router<4>, dim3((nrows + 63) / 64, (T + 15) / 16, nsplit), dim3(256), 0, s, L->router,
+                       L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
   else
-    hipLaunchKernelGGL(k_pf_topk<8>, dim3((T + 3) / 4), dim3(256), 0, s, w.part, ldp, nsplit, T, E, k,
-                       L->sh_gate_inp ? 1 : 0, L->router_bias, logits, shg, ids, wts);
+    hipLaunchKernelGGL(k_pf_router<2>, dim3((nrows + 63) / 64, (T + 15) / 16, nsplit), dim3(256), 0, s, L->router,
+                       L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
+  GM_TRY(hipGetLastError());
+  {
+    const int hg = L->sh_gate_inp ? 1 : 0;
+    const dim3 g((T + 3) / 4);
+    if (E <= 256 && nsplit <= 4)
+      hipLaunchKernelGGL((k_pf_topk<4, 4>), g, dim3(256), 0, s, w.part, ldp, nsplit, T, E, k, hg, L->router_bias,
+                         logits, shg, ids, wts);
+    else if (E <= 256 && nsplit <= 8)
+      hipLaunchKernelGGL((k_pf_topk<4, 8>), g, dim3(256), 0, s, w.part, ldp, nsplit, T, E, k, hg, L->router_bias,
+                         logits, shg, ids, wts);
+    else if (E <= 256)
+      hipLaunchKernelGGL((k_pf_topk<4, 16>), g, dim3(256), 0, s, w.part, ldp, nsplit, T, E, k, hg, L->router_bias,
+                         logits, shg, ids, wts);
+    else if (nsplit <= 8)
+      hipLaunchKernelGGL((k_pf_topk<8, 8>), g, dim3(256), 0, s, w.part, ldp, nsplit, T, E, k, hg, L->router_bias,
+                         logits, shg, ids, wts);
+    else
+      hipLaunchKernelGGL((k_pf_topk<8, 16>), g, dim3(256), 0, s, w.part, ldp, nsplit, T, E, k, hg, L->router_bias,
+                         logits, shg, ids, wts);
+  }
   GM_TRY(hipGetLastError());
   if (int rc = gm_launch_dispatch_seg(ids, T, k, E, w.counts, w.offsets, w.sorted, w.inv, w.segs, kSegTok,
                                      has_sh ? T : 0, s))
