@@ -106,7 +106,13 @@ int gm_router_topk(const uint16_t* w_router, const float* bias, const float* x, 
 int gm_moe_dispatch(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,
                     int32_t* sorted_pairs, void* stream);
 
-/* One MoE block's resident weights (device pointers) and shape. */
+/*
+ * One MoE block's resident weights (device pointers) and shape.  Routed and
+ * shared formats: IQ4_XS or IQ3_XXS superblocks, or BF16 rows (how experts
+ * stored in Q8_0 / Q4_K / Q5_K / Q6_K are held: dequantised once at load, as
+ * the reference keeps its Q5_K / Q6_K outlier layers on a dequant + F.linear
+ * path, qwen/forward.py:495-498).  gate and up share one format.
+ */
 typedef struct gm_moe_layer {
   const void* gate_exps;        /* [E][FF][row_bytes(q_gate, D)]  raw GGUF bytes */
   const void* up_exps;          /* [E][FF][row_bytes(q_up, D)] */
@@ -151,7 +157,9 @@ int gm_moe_forward(const gm_moe_layer* L, const float* x, float* y, int T, int f
  * decode kernels, 1 <= T <= 8 (the reference's NPU expert path is T = 1:
  * qwen/forward.py:494-560 via _npu_routed_expert).  gm_moe_prefill: the
  * grouped f16/bf16-MFMA GEMMs for any T >= 1 (the reference runs prefill through
- * the CPU loop of qwen/forward.py:622-663).  Same workspace as gm_moe_forward.
+ * the CPU loop of qwen/forward.py:622-663); a layer with BF16 routed experts
+ * runs its tokens as decode chunks of at most 8 instead.  Same workspace as
+ * gm_moe_forward.
  */
 int gm_moe_decode(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
                   size_t ws_bytes, void* stream);

@@ -47,7 +47,8 @@ GmMoeWs gm_moe_ws_layout(const gm_moe_layer* L, int T) {
   w.grp = o; o = align256(o + ((size_t)GM_GRP_WORDS + 8 + 2 * E + 1 + Tz * k) * 4);
   w.h = o; o = o + Tz * k * (size_t)L->FF * 4;     // FF % 256 == 0: h_sh starts 256-byte aligned
   w.hsh = o; o = align256(o + Tz * (size_t)(L->FF_sh > 0 ? L->FF_sh : 0) * 4);
-  w.yp = o; o = align256(o + (T <= GM_DECODE_MAX_T ? (Tz * k + Tz) * (size_t)L->D * 4 : 0));
+  const size_t Td = T < GM_DECODE_MAX_T ? Tz : (size_t)GM_DECODE_MAX_T;   // decode chunk (bf16 routed experts)
+  w.yp = o; o = align256(o + (Td * k + Td) * (size_t)L->D * 4);
   w.counters = o; o = align256(o + 256);
   w.pre = o; o = align256(o + gm_prefill_scratch_bytes(L, T));     // every T: gm_moe_prefill takes any T
   w.total = o;
@@ -62,9 +63,9 @@ static int check_layer(const gm_moe_layer* L) {
   if (L->E > 512) return gm_fail_arg("gm_moe_forward: E=%d > 512 is not supported", L->E);
   if (!L->gate_exps || !L->up_exps || !L->down_exps || !L->router)
     return gm_fail_arg("gm_moe_forward: routed expert / router weights must be non-NULL");
-  if (!is_quant(L->q_gate) || L->q_up != L->q_gate || !is_quant(L->q_down))
+  if (!is_weight_fmt(L->q_gate) || L->q_up != L->q_gate || !is_weight_fmt(L->q_down))
     return gm_fail_arg("gm_moe_forward: routed formats gate %d up %d down %d unsupported (gate == up, "
-                       "IQ4_XS or IQ3_XXS)", L->q_gate, L->q_up, L->q_down);
+                       "IQ4_XS, IQ3_XXS or BF16)", L->q_gate, L->q_up, L->q_down);
   if (L->D % GM_QK || L->FF % GM_QK)
     return gm_fail_arg("gm_moe_forward: D=%d and FF=%d must be multiples of %d", L->D, L->FF, GM_QK);
   const bool has_sh = L->gate_sh || L->up_sh || L->down_sh;
@@ -215,5 +216,24 @@ static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int
   const bool decode = path == kPathDecode || (path == kPathAuto && T <= GM_DECODE_MAX_T && T * L->k <= GM_GRP_MAXU);
   if (decode) return gm_dec_run(L, x, y, T, flags, w, lay, s, stage);
   if (stage != 0) return gm_fail_arg("gm_moe_forward_stage: stages are only defined for the decode path (T <= 8)");
+  if (L->q_gate == GM_QTYPE_BF16 || L->q_down == GM_QTYPE_BF16) {
+    // Routed experts held as bf16 (K-quant expert tensors dequantised at load):
+    // the prefill GEMMs take superblock formats only, so the tokens run as
+    // decode chunks of at most 8 (every token's MoE output is independent of
+    // the others).  Each chunk writes its logits / ids / weights / shared gate
+    // into its rows of the full-T arrays.
+    const int D = L->D, E = L->E, k = L->k;
+    for (int t0 = 0; t0 < T; t0 += GM_DECODE_MAX_T) {
+      const int tc = T - t0 < GM_DECODE_MAX_T ? T - t0 : GM_DECODE_MAX_T;
+      GmMoeWs lc = lay;
+      lc.logits += (size_t)t0 * E * 4;
+      lc.shg += (size_t)t0 * 4;
+      lc.ids += (size_t)t0 * k * 4;
+      lc.wts += (size_t)t0 * k * 4;
+      lc.hsh = lc.h + (size_t)tc * k * L->FF * 4;                      // h_sh directly after the chunk's h
+      if (int rc = gm_dec_run(L, x + (size_t)t0 * D, y + (size_t)t0 * D, tc, flags, w, lc, s, 0)) return rc;
+    }
+    return GM_OK;
+  }
   return gm_pf_run(L, x, y, T, flags, w, lay, s);
 }

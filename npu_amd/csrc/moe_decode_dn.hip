@@ -44,7 +44,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   constexpr bool IQ3 = QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS;
   constexpr int RMAX = 2 * FC;                                 // rows per lane, FF <= 512 FC
   constexpr int HPT = (9 * 128 * FC + NTH - 1) / NTH;          // float4 of the k + 1 SwiGLU rows per thread
-  constexpr int RB_MAX = 2 * FC * GM_IQ4XS_BYTES;              // widest routed row
+  constexpr int RB_MAX = QTD == GM_QTYPE_BF16 ? 1024 * FC : 2 * FC * GM_IQ4XS_BYTES;   // widest routed row
   constexpr int CR = (8 * 8 * RB_MAX / 16 + NTH - 1) / NTH;    // routed 16-byte chunks per thread
   constexpr int RBS_MAX = QTS == GM_QTYPE_BF16 ? 1024 * FC : RB_MAX;
   constexpr int CS = (8 * RBS_MAX / 16 + NTH - 1) / NTH;       // shared 16-byte chunks per thread
@@ -355,7 +355,7 @@ int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags,
               hipStream_t s) {
   const int D = P->D, FF = P->FF, k = P->k;
   if (fast1) {
-    if constexpr (FC <= 2) {
+    if constexpr (FC <= (QTD == GM_QTYPE_BF16 ? 1 : 2)) {                // bf16 routed rows: 8 KB per 8-row slice
       const size_t wbytes = (size_t)k * 8 * gm_row_bytes(QTD, FF) + 8 * (size_t)gm_row_bytes(QTS, FF);
       const size_t smem = (size_t)(k + 2) * gm_limb_row_bytes(FF) + ((wbytes + 16 + 15) & ~(size_t)15) +
                           (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
@@ -410,6 +410,7 @@ int gm_dec_down(const gm_moe_layer* P, const float* x, float* y, int T, int flag
   switch (P->q_down) {
     case GM_QTYPE_IQ4_XS: return launch_dn_s<GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s);
     case GM_QTYPE_IQ3_XXS: return launch_dn_s<GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s);
+    case GM_QTYPE_BF16: return launch_dn_s<GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s);
     default: return gm_fail_arg("gm_moe_forward: routed down format %d unsupported", P->q_down);
   }
 }

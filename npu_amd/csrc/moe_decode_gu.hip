@@ -354,6 +354,7 @@ int gm_dec_gateup(const gm_moe_layer* P, const float* x, int T, bool fast1, cons
   switch (P->q_gate) {
     case GM_QTYPE_IQ4_XS: return launch_gu_s<GM_QTYPE_IQ4_XS>(P, x, T, fast1, a, s);
     case GM_QTYPE_IQ3_XXS: return launch_gu_s<GM_QTYPE_IQ3_XXS>(P, x, T, fast1, a, s);
+    case GM_QTYPE_BF16: return launch_gu_s<GM_QTYPE_BF16>(P, x, T, fast1, a, s);
     default: return gm_fail_arg("gm_moe_forward: routed gate/up format %d unsupported", P->q_gate);
   }
 }

@@ -34,6 +34,24 @@ def _dev(a, dtype=None, device="cuda") -> torch.Tensor | None:
     return t.contiguous()
 
 
+# Expert tensors in these types (the Q5_K / Q6_K outliers of the reference model,
+# qwen/forward.py:495-498, and Q8_0 / Q4_K) are dequantised on the device once,
+# at load, and kept as bf16 rows: the decode kernels take bf16 weights, so the
+# routed path stays the same device path for every layer.
+_KQUANTS = (QT.Q8_0, QT.Q4_K, QT.Q5_K, QT.Q6_K)
+
+
+def _kquant_to_bf16(raw: torch.Tensor, q: int, n: int, M: int, K: int) -> torch.Tensor:
+    """uint8 [n?, M, row_bytes] K-quant rows on the GPU -> bf16 bits (int16) [n?, M, K], one
+    matrix at a time through ``gm_dequant_f32`` (fp32, exact) and a round to nearest even."""
+    flat = raw.reshape(n, -1)
+    out = torch.empty((n, M, K), dtype=torch.bfloat16, device=raw.device)
+    for e in range(n):
+        out[e] = ops.dequant(q, flat[e].contiguous()).view(M, K).to(torch.bfloat16)
+    out = out.view(torch.int16)
+    return out if raw.dim() == 3 else out[0]
+
+
 class GpuMoeBlock:
     """One MoE block resident on the GPU."""
 
@@ -59,6 +77,25 @@ class GpuMoeBlock:
             self.gate_sh, self.up_sh = self.gate_sh.view(torch.int16), self.up_sh.view(torch.int16)
         if self.q_down_sh == QT.BF16 and self.down_sh is not None and self.down_sh.dtype == torch.bfloat16:
             self.down_sh = self.down_sh.view(torch.int16)
+        # K-quant experts (routed and shared) -> bf16 rows on the device
+        if self.q_gate in _KQUANTS:
+            self.gate = _kquant_to_bf16(self.gate, self.q_gate, self.E, self.FF, self.D)
+            self.up = _kquant_to_bf16(self.up, self.q_gate, self.E, self.FF, self.D)
+            self.q_gate = int(QT.BF16)
+        if self.q_down in _KQUANTS:
+            self.down = _kquant_to_bf16(self.down, self.q_down, self.E, self.D, self.FF)
+            self.q_down = int(QT.BF16)
+        if self.gate_sh is not None and self.q_gate_sh in _KQUANTS:
+            self.gate_sh = _kquant_to_bf16(self.gate_sh, self.q_gate_sh, 1, self.FF, self.D)
+            self.up_sh = _kquant_to_bf16(self.up_sh, self.q_gate_sh, 1, self.FF, self.D)
+            self.q_gate_sh = int(QT.BF16)
+        if self.down_sh is not None and self.q_down_sh in _KQUANTS:
+            self.down_sh = _kquant_to_bf16(self.down_sh, self.q_down_sh, 1, self.D, self.FF)
+            self.q_down_sh = int(QT.BF16)
+        if self.q_gate == QT.BF16 and self.gate.dtype == torch.bfloat16:
+            self.gate, self.up = self.gate.view(torch.int16), self.up.view(torch.int16)
+        if self.q_down == QT.BF16 and self.down.dtype == torch.bfloat16:
+            self.down = self.down.view(torch.int16)
         self.sh_gate_inp = _dev(sh_gate_inp, device=device)
         if self.sh_gate_inp is not None and self.sh_gate_inp.dtype == torch.bfloat16:
             self.sh_gate_inp = self.sh_gate_inp.view(torch.int16)
@@ -82,14 +119,14 @@ class GpuMoeBlock:
 
     def _check_shapes(self) -> None:
         D, FF, E = self.D, self.FF, self.E
-        want = {
-            "gate": (E, FF, row_bytes(self.q_gate, D)), "up": (E, FF, row_bytes(self.q_gate, D)),
-            "down": (E, D, row_bytes(self.q_down, FF)),
-        }
-        for name, shp in want.items():
+
+        def want(q, M, K):                     # raw rows, or bf16 bits [.., M, K]
+            return ((E, M, K), torch.int16) if q == QT.BF16 else ((E, M, row_bytes(q, K)), torch.uint8)
+        for name, (shp, dt) in {"gate": want(self.q_gate, FF, D), "up": want(self.q_gate, FF, D),
+                                "down": want(self.q_down, D, FF)}.items():
             t = getattr(self, name)
-            if tuple(t.shape) != shp or t.dtype != torch.uint8:
-                raise ValueError(f"{name}: expected uint8 {shp}, got {t.dtype} {tuple(t.shape)}")
+            if tuple(t.shape) != shp or t.dtype != dt:
+                raise ValueError(f"{name}: expected {dt} {shp}, got {t.dtype} {tuple(t.shape)}")
         if tuple(self.router.shape) != (E, D):
             raise ValueError(f"router: expected ({E}, {D}), got {tuple(self.router.shape)}")
         if self.gate_sh is not None:

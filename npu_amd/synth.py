@@ -54,9 +54,31 @@ def host_superblocks(g: np.random.Generator, qtype: int, n_sb: int) -> np.ndarra
     return out
 
 
+# Byte offsets of the fp16 scale fields of the K-quant blocks (d, and dmin where
+# the format has one), and each block's (weights, bytes).
+_KQ_FIELDS = {QT.Q8_0: (0,), QT.Q4_K: (0, 2), QT.Q5_K: (0, 2), QT.Q6_K: (208,)}
+_KQ_BLOCK = {QT.Q8_0: (32, 34), QT.Q4_K: (256, 144), QT.Q5_K: (256, 176), QT.Q6_K: (256, 210)}
+
+
+def host_kquant_blocks(g: np.random.Generator, qtype: int, n_blocks: int) -> np.ndarray:
+    """uint8 [n_blocks, bytes] of a K-quant type: uniform random quants / scales, fp16 d
+    (and dmin) = |N(0,1)| * 2e-3 (the IQ superblocks' distribution of d)."""
+    nb = _KQ_BLOCK[int(qtype)][1]
+    out = g.integers(0, 256, size=(n_blocks, nb), dtype=np.uint8)
+    for off in _KQ_FIELDS[int(qtype)]:
+        v = (np.abs(g.standard_normal(n_blocks)) * D_SCALE).astype(np.float16)
+        out[:, off:off + 2] = v.view(np.uint8).reshape(n_blocks, 2)
+    return out
+
+
 def host_quant_matrix(g: np.random.Generator, qtype: int, M: int, K: int, n_expert: int | None = None) -> np.ndarray:
     """Raw weight bytes [n_expert?, M, row_bytes] for an [M x K] matrix (per expert)."""
     E = 1 if n_expert is None else n_expert
+    if int(qtype) in _KQ_BLOCK:
+        w = _KQ_BLOCK[int(qtype)][0]
+        sb = host_kquant_blocks(g, qtype, E * M * (K // w))
+        shape = (M, row_bytes(qtype, K)) if n_expert is None else (E, M, row_bytes(qtype, K))
+        return sb.reshape(shape)
     sb = host_superblocks(g, qtype, E * M * (K // QK))
     shape = (M, row_bytes(qtype, K)) if n_expert is None else (E, M, row_bytes(qtype, K))
     return sb.reshape(shape)

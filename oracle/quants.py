@@ -117,11 +117,19 @@ def block_bytes(qtype: int) -> int:
 
 
 def dequant_matrix(raw: np.ndarray, qtype: int, M: int, K: int) -> np.ndarray:
-    """Raw row-major [M, K/256 superblocks] bytes -> float32 [M, K] (torch Linear layout)."""
+    """Raw row-major [M, K/256 superblocks] bytes -> float32 [M, K] (torch Linear layout).
+    Q8_0 / Q4_K / Q5_K / Q6_K rows go through ``oracle.kquants`` (its own restatement)."""
     if K % QK:
         raise ValueError(f"K={K} must be a multiple of {QK}")
-    need = M * (K // QK) * block_bytes(qtype)
+    from oracle import kquants
     flat = np.ascontiguousarray(raw).view(np.uint8).reshape(-1)
+    if int(qtype) in kquants.BLOCK:
+        w, nb = kquants.BLOCK[int(qtype)]
+        need = M * (K // w) * nb
+        if flat.size != need:
+            raise ValueError(f"{flat.size} bytes, expected {need} for M={M} K={K}")
+        return kquants.dequant(flat, qtype).reshape(M, K)
+    need = M * (K // QK) * block_bytes(qtype)
     if flat.size != need:
         raise ValueError(f"{flat.size} bytes, expected {need} for M={M} K={K}")
     return dequant(flat, qtype).reshape(M, K)

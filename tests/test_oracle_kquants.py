@@ -89,3 +89,19 @@ def test_multi_block_and_errors():
         K.dequant_q6_k(np.zeros(211, np.uint8))
     with pytest.raises(ValueError):
         K.dequant(np.zeros(34, np.uint8), 99)
+
+
+def test_dequant_matrix_takes_kquant_rows():
+    """oracle.quants.dequant_matrix (the OracleLayer's per-call expert dequant) hands
+    K-quant rows to this module, row-major, and rejects a byte count that is not
+    M x K / block weights blocks."""
+    from npu_amd import synth
+    from oracle import quants as Q
+    g = np.random.default_rng(3)
+    for q in (K.Q8_0, K.Q4_K, K.Q5_K, K.Q6_K):
+        raw = synth.host_quant_matrix(g, q, 3, 512)
+        m = Q.dequant_matrix(raw, q, 3, 512)
+        assert m.shape == (3, 512) and np.isfinite(m).all()
+        assert np.array_equal(m, K.dequant(raw.reshape(-1), q).reshape(3, 512))
+        with pytest.raises(ValueError):
+            Q.dequant_matrix(raw.reshape(-1)[:-1], q, 3, 512)
