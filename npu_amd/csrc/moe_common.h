@@ -247,8 +247,8 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int E, i
 // g[129 + 8u + m] = pair index t*k + j of member m (pairs ascending).  Wave 0
 // does the work (P <= 64 pairs, one per lane): the lanes sharing a lane's
 // expert are found with one ballot per bit of the id, the rank of the expert
-// among the unique ones from an LDS bitmap.  All threads call; ends with a
-// barrier.
+// among the unique ones from an LDS bitmap (bits[0..15]) and its prefix counts
+// (bits[16..31]; E <= 512).  All threads call; ends with a barrier.
 __device__ __forceinline__ void block_group(const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ g,
                                             uint32_t* __restrict__ bits) {
   if (threadIdx.x < 64) {
@@ -265,11 +265,19 @@ __device__ __forceinline__ void block_group(const int32_t* __restrict__ ids, int
     const int m = __popcll(same & ((1ull << lane) - 1ull));   // members of my expert before me
     const int cnt = __popcll(same);
     if (e >= 0 && m == 0) atomicOr(&bits[e >> 5], 1u << (e & 31));   // same wave: LDS ops stay in order
-    int rank = 0;
-    if (e >= 0) {
-      for (int w = 0; w < (e >> 5); ++w) rank += __builtin_popcount(bits[w]);
-      rank += __builtin_popcount(bits[e >> 5] & ((1u << (e & 31)) - 1u));
+    // prefix popcounts of the bitmap words (lane w < 16 holds the count of
+    // unique experts below word w), then one read of each per lane
+    const uint32_t bw = lane < 16 ? bits[lane] : 0u;
+    const int pc = lane < nwords ? __builtin_popcount(bw) : 0;
+    int incl = pc;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int up = __shfl_up(incl, o, 64);
+      incl += (lane & 15) >= o ? up : 0;
     }
+    if (lane < 16) bits[16 + lane] = (uint32_t)(incl - pc);
+    int rank = 0;
+    if (e >= 0) rank = (int)bits[16 + (e >> 5)] + __builtin_popcount(bits[e >> 5] & ((1u << (e & 31)) - 1u));
     const int nu = __popcll(__ballot(e >= 0 && m == 0));       // ballot with every lane active
     if (lane == 0) g[0] = nu;
     if (e >= 0) {

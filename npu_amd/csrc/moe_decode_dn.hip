@@ -316,21 +316,31 @@ __global__ void __launch_bounds__(256) k_dec_down8(gm_moe_layer P, int T, const 
 }
 
 // y[t] = sum over t's top-k slots in ascending expert id of w * yp[t*k + j]
-//        + sigmoid gate * yp[T*k + t]  (+ x[t]).
+//        + sigmoid gate * yp[T*k + t]  (+ x[t]).  Every slot's partial row (and
+// the shared one and x) is loaded before the slots are sorted by expert id, so
+// the block waits on one round of loads; the sort then reorders the loaded
+// values with the ids and weights.
 __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ x, int T, int k, int D, int flags,
                                                      const int32_t* __restrict__ g_ids,
                                                      const float* __restrict__ g_wts, const float* __restrict__ shg,
                                                      int has_sh, const float* __restrict__ yp, float* __restrict__ y) {
   const int t = blockIdx.y;
   const int d = blockIdx.x * 256 + threadIdx.x;
-  int id[8], sl[8];
-  float w[8];
+  const int dc = d < D ? d : D - 1;
+  int id[8];
+  float w[8], v[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    id[j] = j < k ? g_ids[t * k + j] : 0x7fffffff;
-    w[j] = j < k ? g_wts[t * k + j] : 0.f;
-    sl[j] = j;
+    const int jj = j < k ? j : k - 1;
+    id[j] = g_ids[t * k + jj];
+    w[j] = g_wts[t * k + jj];
+    v[j] = yp[(int64_t)(t * k + jj) * D + dc];
   }
+  const float vs = has_sh ? yp[(int64_t)(T * k + t) * D + dc] : 0.f;
+  const float gs = has_sh ? shg[t] : 0.f;
+  const float xr = (flags & GM_MOE_RESIDUAL) ? x[(int64_t)t * D + dc] : 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) id[j] = j < k ? id[j] : 0x7fffffff;
 #pragma unroll
   for (int i = 1; i < 8; ++i)
 #pragma unroll
@@ -338,15 +348,15 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ x
       if (id[j] < id[j - 1]) {
         const int ti = id[j]; id[j] = id[j - 1]; id[j - 1] = ti;
         const float tw = w[j]; w[j] = w[j - 1]; w[j - 1] = tw;
-        const int ts = sl[j]; sl[j] = sl[j - 1]; sl[j - 1] = ts;
+        const float tv = v[j]; v[j] = v[j - 1]; v[j - 1] = tv;
       }
   if (d >= D) return;
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < 8; ++j)
-    if (j < k) acc = fmaf(w[j], yp[(int64_t)(t * k + sl[j]) * D + d], acc);
-  if (has_sh) acc = fmaf(shg[t], yp[(int64_t)(T * k + t) * D + d], acc);
-  if (flags & GM_MOE_RESIDUAL) acc = x[(int64_t)t * D + d] + acc;
+    if (j < k) acc = fmaf(w[j], v[j], acc);
+  if (has_sh) acc = fmaf(gs, vs, acc);
+  if (flags & GM_MOE_RESIDUAL) acc = xr + acc;
   y[(int64_t)t * D + d] = acc;
 }
 

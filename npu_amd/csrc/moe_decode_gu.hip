@@ -99,7 +99,7 @@ __global__ void __launch_bounds__(512) k_dec_route(gm_moe_layer P, const float* 
   __shared__ int32_t ids[64];
   __shared__ float wts[64];
   __shared__ int32_t grp[GM_GRP_WORDS];
-  __shared__ uint32_t bits[16];
+  __shared__ uint32_t bits[32];                                 // expert bitmap, then its prefix counts
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = P.E, k = P.k;
   if (wave < T) {
