@@ -45,6 +45,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--calib-copy", action="store_true", help="only run a plain 256 MiB copy (counter calibration)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the config-4 prefill measurement (8 layers), one JSON line")
+    ap.add_argument("--batch8-only", action="store_true",
+                    help="only run the config-5 batch-8 chain over --layers layers, one JSON line")
     return ap.parse_args()
 
 
@@ -310,6 +312,13 @@ def main() -> int:
         layers = build_layers(8, dev)
         torch.cuda.synchronize()
         print(json.dumps({"prefill": run_prefill(layers)}))
+        return 0
+    if args.batch8_only:
+        layers = build_layers(args.layers, dev)
+        torch.cuda.synchronize()
+        ms8, nu8, ok8 = run_chain(layers, 8, args.steps, args.warmup, SEED + 8)
+        print(json.dumps({"batch8": {"layers": args.layers, "ms_per_step": ms8, "tokens_per_s": 8e3 / ms8,
+                                     "mean_unique_experts_per_layer": sum(nu8) / len(nu8), "finite": ok8}}))
         return 0
     log(f"building {args.layers} layers of seeded synthetic weights on {torch.cuda.get_device_name(0)}")
     t0 = time.time()

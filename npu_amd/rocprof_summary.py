@@ -8,6 +8,11 @@ copy kernel of known size) and writes
   copy-calibrated HBM bytes per launch and the algorithmic bytes per launch;
 * ``<name>.md`` -- the same as a table, with the commands that produced the inputs.
 
+With ``--inst-pmc I.csv`` it instead tabulates, per kernel, rocprof durations and the
+instruction counters of one ``--pmc`` pass (``SQ_WAVES``, ``SQ_INSTS_VALU``,
+``SQ_INSTS_SALU``, ``SQ_INSTS_LDS``, ``SQ_INSTS_VMEM_RD``: device totals per dispatch),
+with the VALU issue time they imply (``<name>.md``).
+
 With ``--prefill-pmc P.csv`` it instead summarises the prefill kernels: rocprof
 durations and, from the counters ``MfmaUtil``, ``MfmaFlopsF16`` and ``MfmaFlopsBF16``
 (one ``--pmc`` pass), each kernel's MFMA busy fraction and issued MFMA TFLOP/s
@@ -117,10 +122,40 @@ def prefill_summary(a) -> None:
     print(json.dumps(kernels, indent=1))
 
 
+def inst_summary(a) -> None:
+    """Durations and instruction counters per kernel family of the decode chain.  A wave64
+    VALU instruction occupies a 16-lane SIMD for 4 cycles, so the VALU issue time of a
+    dispatch is at least VALU instructions x 4 / (SIMDs x clock)."""
+    stats = kernel_stats(a.stats)
+    pmc = counter_table(a.inst_pmc)
+    lines = [f"# {a.name}: kernel durations and instruction counts", "", a.commands, "",
+             "Counters are device totals per dispatch (mean over dispatches). VALU issue time = "
+             f"SQ_INSTS_VALU x 4 cycles / ({a.simds} SIMDs x {a.sclk_ghz} GHz): the time the kernel needs "
+             "if every SIMD issued a VALU instruction every 4 cycles.", "",
+             "| kernel | calls | rocprof avg us | waves | VALU / wave | SALU / wave | LDS / wave | VMEM rd / wave | "
+             "VALU issue us |", "|---|---|---|---|---|---|---|---|---|"]
+    for name, st in sorted(stats.items(), key=lambda kv: -kv[1]["calls"] * kv[1]["avg_us"]):
+        c = pmc.get(name)
+        if not c or "SQ_WAVES" not in c or c["SQ_WAVES"] <= 0:
+            continue
+        w = c["SQ_WAVES"]
+        valu_us = c.get("SQ_INSTS_VALU", 0.0) * 4 / (a.simds * a.sclk_ghz * 1e3)
+        lines.append(f"| {name[:60]} | {st['calls']} | {st['avg_us']:.2f} | {w:.0f} | "
+                     f"{c.get('SQ_INSTS_VALU', 0) / w:.0f} | {c.get('SQ_INSTS_SALU', 0) / w:.0f} | "
+                     f"{c.get('SQ_INSTS_LDS', 0) / w:.0f} | {c.get('SQ_INSTS_VMEM_RD', 0) / w:.0f} | {valu_us:.2f} |")
+    out = Path(a.out)
+    out.mkdir(parents=True, exist_ok=True)
+    (out / f"{a.name}.md").write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--stats", required=True)
     ap.add_argument("--prefill-pmc", help="counter CSV of MfmaUtil/MfmaFlopsF16/MfmaFlopsBF16 (prefill mode)")
+    ap.add_argument("--inst-pmc", help="counter CSV of SQ_WAVES/SQ_INSTS_* (instruction mode)")
+    ap.add_argument("--simds", type=int, default=1024, help="SIMDs of the device (256 CUs x 4 on MI355X)")
+    ap.add_argument("--sclk-ghz", type=float, default=2.4, help="shader clock for the VALU issue time")
     ap.add_argument("--fetch")
     ap.add_argument("--write")
     ap.add_argument("--calib-fetch")
@@ -133,6 +168,9 @@ def main() -> None:
     a = ap.parse_args()
     if a.prefill_pmc:
         prefill_summary(a)
+        return
+    if a.inst_pmc:
+        inst_summary(a)
         return
     if not (a.fetch and a.write and a.calib_fetch and a.calib_write):
         ap.error("decode mode needs --fetch, --write, --calib-fetch and --calib-write")
