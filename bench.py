@@ -47,6 +47,8 @@ def parse() -> argparse.Namespace:
                     help="only run the config-4 prefill measurement (8 layers), one JSON line")
     ap.add_argument("--batch8-only", action="store_true",
                     help="only run the config-5 batch-8 chain over --layers layers, one JSON line")
+    ap.add_argument("--dense-only", action="store_true",
+                    help="only run the dense bf16 projection matvec measurement, one JSON line")
     return ap.parse_args()
 
 
@@ -207,6 +209,73 @@ def run_prefill(layers, T: int = 512, n_blocks: int = 8, reps: int = 5):
             "mfma_util_vs_bf16_dense_peak": flops / (us * 1e-6) / 2.5e15, "finite": finite}
 
 
+DENSE_SHAPES = (("ssm_in", 8192, 2048), ("ssm_gate", 4096, 2048), ("ssm_out", 2048, 4096))
+
+
+def run_dense_mv(dev, n_layers: int = 30, reps: int = 20):
+    """The dense bf16 projections NpuMatVec serves (qwen/forward.py:827-831): the Gated
+    DeltaNet layer's w_in 8192x2048, w_gate 4096x2048 and w_out 2048x4096
+    (qwen/test_npu_ssm.py), bf16 weights N(0, 0.02) for `n_layers` distinct layers
+    (1.9 GB, beyond the Infinity Cache), fp32 x.  Per shape and token count, one hipGraph
+    holds that projection's gm_matvec for every layer; the replay period per launch
+    gives the effective weight GB/s (weight bytes / time; x and y are < 0.5% of them).
+    torch's bf16 F.linear (x rounded to bf16) on the same weights is timed the same way
+    for scale."""
+    import torch
+    from npu_amd import _lib as L
+    from npu_amd.gguf_types import GGMLQuantizationType as QT
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 30)
+    Ws = {name: [(torch.randn(M, K, generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(n_layers)]
+          for name, M, K in DENSE_SHAPES}
+    lib = L.lib()
+
+    def period_us(fn):
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * n_layers)
+
+    out = {"workload": f"SSM projections (qwen/test_npu_ssm.py shapes), bf16 weights, {n_layers} distinct layers",
+           "shapes": {}}
+    for name, M, K in DENSE_SHAPES:
+        wbytes = M * K * 2
+        for T in (1, 8):
+            x = torch.randn(T, K, generator=gen, device=dev)
+            y = torch.empty(T, M, device=dev)
+            xb = x.to(torch.bfloat16)
+
+            def ours():
+                s = L.stream_ptr()
+                for W in Ws[name]:
+                    L.check(lib.gm_matvec(int(QT.BF16), L.ptr(W), M, K, L.ptr(x), T, L.ptr(y), s), "gm_matvec")
+
+            def torch_linear():
+                for W in Ws[name]:
+                    torch.nn.functional.linear(xb, W)
+
+            us = period_us(ours)
+            ref = x.double() @ Ws[name][-1].double().T
+            rel = float((y.double() - ref).abs().max() / ref.abs().max())
+            tus = period_us(torch_linear)
+            gbps = (wbytes + T * (K + M) * 4) / (us * 1e-6) / 1e9
+            out["shapes"][f"{name}_T{T}"] = {
+                "M": M, "K": K, "T": T, "us_per_launch": us, "weight_GBps": wbytes / (us * 1e-6) / 1e9,
+                "algorithmic_GBps": gbps, "hbm_frac": gbps / HBM_PEAK_GBPS, "rel_err_vs_f64": rel,
+                "torch_bf16_linear_us": tus}
+    return out
+
+
 def cpu_baseline(layers, n_sample: int, budget_s: float = 12.0):
     """The oracle (a port of the CPU branch of qwen/forward.py:moe_forward) on a bounded
     sample: the first `n_sample` blocks of the chain, B=1, run back to back (each output
@@ -313,6 +382,9 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"prefill": run_prefill(layers)}))
         return 0
+    if args.dense_only:
+        print(json.dumps({"dense_mv": run_dense_mv(dev)}))
+        return 0
     if args.batch8_only:
         layers = build_layers(args.layers, dev)
         torch.cuda.synchronize()
@@ -358,6 +430,8 @@ def main() -> int:
         log(f"B=8: {extra['batch8']}")
         extra["prefill"] = run_prefill(layers)
         log(f"prefill: {extra['prefill']}")
+        extra["dense_mv"] = run_dense_mv(dev)
+        log(f"dense bf16 matvec: {extra['dense_mv']}")
 
     cpu = None
     if not args.no_cpu_baseline:

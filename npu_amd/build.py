@@ -16,7 +16,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libnpu_amd.so"
 SOURCES = ["capi.hip", "matvec.hip", "router.hip", "moe_decode.hip", "moe_decode_gu.hip", "moe_decode_dn.hip",
-           "dispatch.hip", "prefill.hip"]
+           "dispatch.hip", "prefill.hip", "mv_bf16.hip"]
 ARCH = os.environ.get("NPU_AMD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

@@ -16,6 +16,17 @@
 // which then issues every load right before its store.
 typedef float gm_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t gm_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gm_u32x2 __attribute__((ext_vector_type(2)));
+
+// Weight loads.  ST = true for bytes a launch streams once and no later
+// launch of the step reads again (routed experts, dense projection rows):
+// a nontemporal load, which does not displace reused data (activations, the
+// router and shared-expert weights every token reads) from the caches.
+template <bool ST, typename T>
+__device__ __forceinline__ T gm_ld(const T* p) {
+  if constexpr (ST) return __builtin_nontemporal_load(p);
+  else return *p;
+}
 
 // Host-side launch-check helper: every entry point returns an int status.
 #define GM_TRY(expr)                                   \

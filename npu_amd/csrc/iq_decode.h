@@ -46,11 +46,12 @@ struct RawIq4 {
   uint32_t q[4];        // 16 qs bytes of the sub-block
 };
 
+template <bool ST = false>
 __device__ __forceinline__ RawIq4 gm_load_iq4(const uint8_t* __restrict__ row, int sub) {
   const uint8_t* blk = row + (sub >> 3) * GM_IQ4XS_BYTES;     // 8-byte aligned
-  const uint2 h = *reinterpret_cast<const uint2*>(blk);
-  const uint2* qp = reinterpret_cast<const uint2*>(blk + 8 + 16 * (sub & 7));
-  const uint2 a = qp[0], b = qp[1];
+  const gm_u32x2 h = gm_ld<ST>(reinterpret_cast<const gm_u32x2*>(blk));
+  const gm_u32x2* qp = reinterpret_cast<const gm_u32x2*>(blk + 8 + 16 * (sub & 7));
+  const gm_u32x2 a = gm_ld<ST>(qp), b = gm_ld<ST>(qp + 1);
   RawIq4 r;
   r.h0 = h.x; r.h1 = h.y;
   r.q[0] = a.x; r.q[1] = a.y; r.q[2] = b.x; r.q[3] = b.y;
@@ -93,22 +94,24 @@ struct RawIq3 {
 // 2 mod 4.  Fields are fetched with aligned dword loads (global memory or
 // LDS) and re-aligned with v_alignbyte_b32; every dword read contains at
 // least one byte of this superblock, so no load crosses into an unmapped page.
+template <bool ST = false>
 __device__ __forceinline__ RawIq3 gm_load_iq3(const uint8_t* __restrict__ row, int sub) {
   const int sb = sub >> 3, s = sub & 7;
   const uint8_t* base = row + sb * GM_IQ3XXS_BYTES;
   const int odd = (int)((reinterpret_cast<uintptr_t>(base) >> 1) & 1);   // base % 4 == 2 * odd
   const uint32_t* dp = reinterpret_cast<const uint32_t*>(base - 2 * odd);
   RawIq3 r;
-  r.d = odd ? (dp[0] >> 16) : (dp[0] & 0xffffu);
+  const uint32_t d0 = gm_ld<ST>(dp);
+  r.d = odd ? (d0 >> 16) : (d0 & 0xffffu);
   // qs at base + 2 + 8s: offset % 4 == 2 when sb is even, 0 when odd
   const int rq = odd ? 0 : 2;
   const uint32_t* qp = reinterpret_cast<const uint32_t*>(base + 2 + 8 * s - rq);
-  const uint32_t q0 = qp[0], q1 = qp[1], q2 = qp[rq ? 2 : 1];
+  const uint32_t q0 = gm_ld<ST>(qp), q1 = gm_ld<ST>(qp + 1), q2 = gm_ld<ST>(qp + (rq ? 2 : 1));
   r.q0 = __builtin_amdgcn_alignbyte(q1, q0, rq);
   r.q1 = __builtin_amdgcn_alignbyte(q2, q1, rq);
   // word at base + 66 + 4s: same parity rule
   const uint32_t* wp = reinterpret_cast<const uint32_t*>(base + 66 + 4 * s - rq);
-  const uint32_t w0 = wp[0], w1 = wp[rq ? 1 : 0];
+  const uint32_t w0 = gm_ld<ST>(wp), w1 = gm_ld<ST>(wp + (rq ? 1 : 0));
   r.w = __builtin_amdgcn_alignbyte(w1, w0, rq);
   return r;
 }
@@ -143,11 +146,15 @@ struct RawBf16 {
   uint4 v[4];   // 32 bf16 values
 };
 
+template <bool ST = false>
 __device__ __forceinline__ RawBf16 gm_load_bf16(const uint8_t* __restrict__ row, int sub) {
-  const uint4* p = reinterpret_cast<const uint4*>(row + sub * 64);
+  const gm_u32x4* p = reinterpret_cast<const gm_u32x4*>(row + sub * 64);
   RawBf16 r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) r.v[i] = p[i];
+  for (int i = 0; i < 4; ++i) {
+    const gm_u32x4 v = gm_ld<ST>(p + i);
+    r.v[i] = uint4{v.x, v.y, v.z, v.w};
+  }
   return r;
 }
 
@@ -170,11 +177,11 @@ template <> struct RawSub<GM_QTYPE_IQ4_XS> { using T = RawIq4; };
 template <> struct RawSub<GM_QTYPE_IQ3_XXS> { using T = RawIq3; };
 template <> struct RawSub<GM_QTYPE_BF16> { using T = RawBf16; };
 
-template <int QT>
+template <int QT, bool ST = false>
 __device__ __forceinline__ typename RawSub<QT>::T gm_load_sub(const uint8_t* __restrict__ row, int sub) {
-  if constexpr (QT == GM_QTYPE_IQ4_XS) return gm_load_iq4(row, sub);
-  else if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_load_iq3(row, sub);
-  else return gm_load_bf16(row, sub);
+  if constexpr (QT == GM_QTYPE_IQ4_XS) return gm_load_iq4<ST>(row, sub);
+  else if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_load_iq3<ST>(row, sub);
+  else return gm_load_bf16<ST>(row, sub);
 }
 
 template <int QT>

@@ -130,7 +130,7 @@ __device__ __forceinline__ void gm_row_partial(const uint8_t* __restrict__ row, 
                                                const float* __restrict__ xs, int xstride, int nt,
                                                const uint32_t* __restrict__ grid, float (&acc)[NT]) {
   for (int sub = lane_in_row; sub < nsub; sub += L) {
-    const auto r = gm_load_sub<QT>(row, sub);
+    const auto r = gm_load_sub<QT, true>(row, sub);
     float wv[32];
     const float sc = gm_decode_sub<QT>(r, sub, grid, wv);
 #pragma unroll
@@ -221,7 +221,7 @@ int gm_launch_matvec(int qtype, const void* w, int M, int K, const float* x, int
   switch (qtype) {
     case GM_QTYPE_IQ4_XS: return launch_matvec_q<GM_QTYPE_IQ4_XS>(p, M, K, x, n_tok, y, s);
     case GM_QTYPE_IQ3_XXS: return launch_matvec_q<GM_QTYPE_IQ3_XXS>(p, M, K, x, n_tok, y, s);
-    case GM_QTYPE_BF16: return launch_matvec_q<GM_QTYPE_BF16>(p, M, K, x, n_tok, y, s);
+    case GM_QTYPE_BF16: return gm_launch_mv_bf16(static_cast<const uint16_t*>(w), M, K, x, n_tok, y, s);
     default: return gm_fail_arg("gm_matvec: unsupported qtype %d", qtype);
   }
 }

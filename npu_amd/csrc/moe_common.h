@@ -307,12 +307,12 @@ struct RowFetch {
   typename RawSub<QT>::T r[SPL];
 };
 
-template <int QT, int LR, int SPL>
+template <int QT, int LR, int SPL, bool ST = false>
 __device__ __forceinline__ void fetch_subs(RowFetch<QT, SPL>& f, const uint8_t* __restrict__ row, int lir, int nsub) {
 #pragma unroll
   for (int i = 0; i < SPL; ++i) {
     const int sub = lir + LR * i;
-    f.r[i] = gm_load_sub<QT>(row, sub < nsub ? sub : nsub - 1);
+    f.r[i] = gm_load_sub<QT, ST>(row, sub < nsub ? sub : nsub - 1);
   }
 }
 

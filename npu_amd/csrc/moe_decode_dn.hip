@@ -124,8 +124,8 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
       int e = ex[0];
 #pragma unroll
       for (int q = 1; q < 8; ++q) e = m == q ? ex[q] : e;
-      rr[i] = *reinterpret_cast<const gm_u32x4*>(static_cast<const uint8_t*>(P.down_exps) +
-                                                  ((int64_t)e * D + r0) * rbd + 16 * j);
+      rr[i] = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(static_cast<const uint8_t*>(P.down_exps) +
+                                                           ((int64_t)e * D + r0) * rbd + 16 * j));
       dst[i] = c < total ? m * 8 * rbd + 16 * j : trash;
     }
     issue_fence();
@@ -227,7 +227,7 @@ __device__ __forceinline__ void down_rows(const uint8_t* __restrict__ wbase, int
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int row = row0 + 64 * t + wave * 16 + q * 4 + (lane >> 4);
-      fetch_subs<QTW, 16, FC>(f[t][q], wbase + (int64_t)(row < D ? row : 0) * rb, lir, nsub);
+      fetch_subs<QTW, 16, FC, true>(f[t][q], wbase + (int64_t)(row < D ? row : 0) * rb, lir, nsub);
     }
   const int nqr = FF >> 2, nq = nm * nqr;
   const gm_f32x4* h4 = reinterpret_cast<const gm_f32x4*>(h);

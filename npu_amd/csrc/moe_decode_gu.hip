@@ -60,8 +60,10 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
   const bool live = row < FF;
   const int r = live ? row : 0;
   RowFetch<QT, DC> fg, fu;
-  fetch_subs<QT, 32, DC>(fg, static_cast<const uint8_t*>(P.gate_exps) + ((int64_t)e * FF + r) * rb, lane & 31, nsub);
-  fetch_subs<QT, 32, DC>(fu, static_cast<const uint8_t*>(P.up_exps) + ((int64_t)e * FF + r) * rb, lane & 31, nsub);
+  fetch_subs<QT, 32, DC, true>(fg, static_cast<const uint8_t*>(P.gate_exps) + ((int64_t)e * FF + r) * rb, lane & 31,
+                               nsub);
+  fetch_subs<QT, 32, DC, true>(fu, static_cast<const uint8_t*>(P.up_exps) + ((int64_t)e * FF + r) * rb, lane & 31,
+                               nsub);
   if (blockIdx.x == 0 && wave == 0) {
     // publish ids, weights and the grouping table for stage 3 and the caller
     // (the softmax weights are needed by nobody else, so they are computed
@@ -177,8 +179,8 @@ __device__ __forceinline__ void gateup_rows(const uint8_t* __restrict__ gbase, c
   for (int p = 0; p < NP; ++p) {
     const int row = r0 + 8 * p + 2 * wave + (lane >> 5);
     const int r = row < FF ? row : 0;
-    fetch_subs<QT, 32, DC>(fg[p], gbase + r * rb, lir, nsub);
-    fetch_subs<QT, 32, DC>(fu[p], ubase + r * rb, lir, nsub);
+    fetch_subs<QT, 32, DC, true>(fg[p], gbase + r * rb, lir, nsub);
+    fetch_subs<QT, 32, DC, true>(fu[p], ubase + r * rb, lir, nsub);
   }
   for (int g0 = 0; g0 < nm; g0 += MG) {                      // usually one group
     int gt[MG], idx[MG];

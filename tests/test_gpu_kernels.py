@@ -65,13 +65,21 @@ def test_matvec(gpu, qtype, M, K, n_tok):
     assert OM.rel_err(y, ref64) <= 1e-5
 
 
-def test_matvec_bf16(gpu):
-    M, K = 256, 2048
-    W = synth.host_bf16_normal(_g(1), (M, K), 0.02)
-    x = torch.from_numpy(_g(2).standard_normal((2, K)).astype(np.float32))
+# The projection shapes of qwen/test_npu_ssm.py and test_npu_attn_o.py (8192 x 2048,
+# 4096 x 2048, 2048 x 4096), plus ragged M, K tails inside a 512-wide slot, and K
+# large enough for two passes over the row.
+@pytest.mark.parametrize("M,K", [(8192, 2048), (4096, 2048), (2048, 4096), (33, 256), (100, 768),
+                                 (17, 12288), (5, 16384), (256, 2048)])
+@pytest.mark.parametrize("n_tok", [1, 2, 3, 8, 13])
+def test_matvec_bf16(gpu, M, K, n_tok):
+    W = synth.host_bf16_normal(_g(M + K), (M, K), 0.02)
+    x = torch.from_numpy(_g(2).standard_normal((n_tok, K)).astype(np.float32))
     y = ops.matvec(QT.BF16, torch.from_numpy(W.view(np.int16)).to(gpu), M, K, x.to(gpu)).cpu()
     ref = x.double() @ torch.from_numpy(synth.from_bf16(W)).double().T
+    assert y.shape == (n_tok, M)
     assert OM.rel_err(y, ref) <= 1e-5
+    # every row is its own dot product: a row or token mix-up moves one entry, not the max
+    assert float(((y.double() - ref).abs() / ref.abs().amax(dim=1, keepdim=True)).max()) <= 1e-5
 
 
 @pytest.mark.parametrize("q_gu,q_d", [(QT.IQ4_XS, QT.IQ3_XXS), (QT.IQ3_XXS, QT.IQ4_XS)])
