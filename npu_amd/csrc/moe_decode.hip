@@ -51,7 +51,7 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
     const uint8_t* wr = row < E ? reinterpret_cast<const uint8_t*>(P.router) + (int64_t)row * D * 2
                                 : reinterpret_cast<const uint8_t*>(row < nrows ? P.sh_gate_inp : P.router);
     RowFetch<GM_QTYPE_BF16, SPLR> f;
-    fetch_subs<GM_QTYPE_BF16, 64, SPLR>(f, wr, lane, nsub);
+    fetch_subs<GM_QTYPE_BF16, 64, SPLR, true>(f, wr, lane, nsub);
     issue_fence();
     stage_x_regs<NT, DC>(xr, T, D, P.norm_w, P.norm_eps, xs, red);
     float acc[NT];
@@ -78,8 +78,8 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
   const bool live = row < FFs;
   const int r = live ? row : 0;
   RowFetch<QTS, DC> fg, fu;
-  fetch_subs<QTS, 32, DC>(fg, static_cast<const uint8_t*>(P.gate_sh) + r * rb, lane & 31, nsub);
-  fetch_subs<QTS, 32, DC>(fu, static_cast<const uint8_t*>(P.up_sh) + r * rb, lane & 31, nsub);
+  fetch_subs<QTS, 32, DC, true>(fg, static_cast<const uint8_t*>(P.gate_sh) + r * rb, lane & 31, nsub);
+  fetch_subs<QTS, 32, DC, true>(fu, static_cast<const uint8_t*>(P.up_sh) + r * rb, lane & 31, nsub);
   issue_fence();
   uint8_t* xl = reinterpret_cast<uint8_t*>(xs);                // limb rows (fit in the fp32 rows' space)
   stage_limbs_regs<NT, DC>(xr, T, D, P.norm_w, P.norm_eps, xl, red);

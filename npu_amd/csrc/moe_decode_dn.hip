@@ -90,7 +90,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
 #pragma unroll
   for (int i = 0; i < CS; ++i) {
     const int c = tid + NTH * i;
-    sr[i] = *reinterpret_cast<const gm_u32x4*>(sbase + 16 * (c < n16s ? c : n16s - 1));
+    sr[i] = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(sbase + 16 * (c < n16s ? c : n16s - 1)));
   }
   issue_fence();
   // --- B: stage them
