@@ -49,6 +49,8 @@ def parse() -> argparse.Namespace:
                     help="only run the config-5 batch-8 chain over --layers layers, one JSON line")
     ap.add_argument("--dense-only", action="store_true",
                     help="only run the dense bf16 projection matvec measurement, one JSON line")
+    ap.add_argument("--dense-shapes", default="ssm_in,ssm_gate,ssm_out", help="projections for --dense-only")
+    ap.add_argument("--dense-tokens", default="1,8", help="token counts for --dense-only")
     return ap.parse_args()
 
 
@@ -212,7 +214,7 @@ def run_prefill(layers, T: int = 512, n_blocks: int = 8, reps: int = 5):
 DENSE_SHAPES = (("ssm_in", 8192, 2048), ("ssm_gate", 4096, 2048), ("ssm_out", 2048, 4096))
 
 
-def run_dense_mv(dev, n_layers: int = 30, reps: int = 20):
+def run_dense_mv(dev, n_layers: int = 30, reps: int = 20, shapes=None, tokens=(1, 8)):
     """The dense bf16 projections NpuMatVec serves (qwen/forward.py:827-831): the Gated
     DeltaNet layer's w_in 8192x2048, w_gate 4096x2048 and w_out 2048x4096
     (qwen/test_npu_ssm.py), bf16 weights N(0, 0.02) for `n_layers` distinct layers
@@ -226,8 +228,9 @@ def run_dense_mv(dev, n_layers: int = 30, reps: int = 20):
     from npu_amd.gguf_types import GGMLQuantizationType as QT
     gen = torch.Generator(device=dev)
     gen.manual_seed(SEED + 30)
+    todo = [sh for sh in DENSE_SHAPES if shapes is None or sh[0] in shapes]
     Ws = {name: [(torch.randn(M, K, generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(n_layers)]
-          for name, M, K in DENSE_SHAPES}
+          for name, M, K in todo}
     lib = L.lib()
 
     def period_us(fn):
@@ -248,9 +251,9 @@ def run_dense_mv(dev, n_layers: int = 30, reps: int = 20):
 
     out = {"workload": f"SSM projections (qwen/test_npu_ssm.py shapes), bf16 weights, {n_layers} distinct layers",
            "shapes": {}}
-    for name, M, K in DENSE_SHAPES:
+    for name, M, K in todo:
         wbytes = M * K * 2
-        for T in (1, 8):
+        for T in tokens:
             x = torch.randn(T, K, generator=gen, device=dev)
             y = torch.empty(T, M, device=dev)
             xb = x.to(torch.bfloat16)
@@ -383,7 +386,8 @@ def main() -> int:
         print(json.dumps({"prefill": run_prefill(layers)}))
         return 0
     if args.dense_only:
-        print(json.dumps({"dense_mv": run_dense_mv(dev)}))
+        print(json.dumps({"dense_mv": run_dense_mv(dev, shapes=args.dense_shapes.split(","),
+                                                   tokens=[int(t) for t in args.dense_tokens.split(",")])}))
         return 0
     if args.batch8_only:
         layers = build_layers(args.layers, dev)

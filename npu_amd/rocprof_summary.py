@@ -165,6 +165,10 @@ def main() -> None:
     ap.add_argument("--out", default="profiles")
     ap.add_argument("--name", default="moe_decode_config5")
     ap.add_argument("--commands", default="", help="text describing the commands (markdown)")
+    ap.add_argument("--algo", action="append", default=[],
+                    help="KERNEL=BYTES: algorithmic bytes per launch of a kernel family (replaces the "
+                         "T = 1 decode table; repeatable)")
+    ap.add_argument("--json", default="hbm_traffic.json", help="name of the JSON written to --out")
     a = ap.parse_args()
     if a.prefill_pmc:
         prefill_summary(a)
@@ -179,7 +183,7 @@ def main() -> None:
     fetch, write = counter_means(a.fetch), counter_means(a.write)
     cf, cw = counter_means(a.calib_fetch)[a.calib_kernel], counter_means(a.calib_write)[a.calib_kernel]
     s_fetch, s_write = a.calib_bytes / (cf * 1024), a.calib_bytes / (cw * 1024)
-    algo = algorithmic_bytes()
+    algo = dict((kv.split("=")[0], int(kv.split("=")[1])) for kv in a.algo) if a.algo else algorithmic_bytes()
     kernels = {}
     for name, st in stats.items():
         fam = family(name)
@@ -198,7 +202,7 @@ def main() -> None:
     doc = {"calibration": {"kernel": a.calib_kernel, "bytes_each_way": a.calib_bytes, "fetch_kib": cf,
                            "write_kib": cw, "fetch_scale": s_fetch, "write_scale": s_write},
            "kernels": kernels}
-    (out / "hbm_traffic.json").write_text(json.dumps(doc, indent=1) + "\n")
+    (out / a.json).write_text(json.dumps(doc, indent=1) + "\n")
     lines = [f"# {a.name}: kernel durations and HBM traffic", "", a.commands, "",
              f"Copy calibration ({a.calib_kernel}, {a.calib_bytes} B each way): FETCH_SIZE reads "
              f"{cf:.1f} KiB (scale {s_fetch:.4f}), WRITE_SIZE {cw:.1f} KiB (scale {s_write:.4f}).", "",
