@@ -11,7 +11,17 @@
 // is staged in LDS once per block (after the weight loads are issued) and
 // read per slot, shared by the R rows.  Every product is an fp32 FMA of the
 // exact bf16 weight and the fp32 activation; each lane's partial sum is
-// reduced over the wave with DPP.
+// reduced over the wave with DPP.  This path serves one token.
+//
+// Two or more tokens (k_mv_bf16_mfma): v_mfma_f32_16x16x32_bf16 with the
+// weight rows as A (lane l: row l % 16, k = 8 (l / 16) .. +7 of each 32-wide
+// k-step, one 16-byte nontemporal load) and the token columns as B.  Every
+// lane splits its column's 8 fp32 activations into three bf16 planes,
+// x = h + m + l exactly (h = x truncated to bf16, m = (x - h) truncated,
+// l = x - h - m, which has at most 8 significant bits), so the three MFMAs
+// per A operand add exact bf16 x bf16 products in fp32 and x loses nothing.
+// A block holds 16 RT rows; its WPB waves split K, each issuing NC k-steps'
+// loads at a time, and their tiles are summed in LDS in wave order.
 #include "common.h"
 #include "kernels.h"
 
@@ -100,6 +110,120 @@ __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w,
   }
 }
 
+typedef __bf16 gm_bf16x8 __attribute__((ext_vector_type(8)));
+
+// x = h + m + l over 8 fp32 values -> three bf16x8 planes (exact split, see above).
+__device__ __forceinline__ void split3(const gm_f32x4& xa, const gm_f32x4& xb, gm_u32x4 (&pl)[3]) {
+  const float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+  uint32_t hb[8], mb[8], lb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    hb[i] = __float_as_uint(v[i]) & 0xffff0000u;
+    const float r = v[i] - __uint_as_float(hb[i]);
+    mb[i] = __float_as_uint(r) & 0xffff0000u;
+    lb[i] = __float_as_uint(r - __uint_as_float(mb[i]));     // low 16 bits are zero
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    pl[0][d] = __builtin_amdgcn_perm(hb[2 * d + 1], hb[2 * d], 0x07060302u);
+    pl[1][d] = __builtin_amdgcn_perm(mb[2 * d + 1], mb[2 * d], 0x07060302u);
+    pl[2][d] = __builtin_amdgcn_perm(lb[2 * d + 1], lb[2 * d], 0x07060302u);
+  }
+}
+
+template <int RT, int WPB, int NC>
+__global__ void __launch_bounds__(64 * WPB) k_mv_bf16_mfma(const uint16_t* __restrict__ w, int M, int K,
+                                                        const float* __restrict__ x, int n_tok,
+                                                        float* __restrict__ y) {
+  __shared__ gm_f32x4 red[WPB - 1][RT][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
+  const int row0 = blockIdx.x * 16 * RT;
+  const int tok = blockIdx.y * 16 + l16;
+  const int kw = K / WPB, kbeg = wave * kw;                      // this wave's K range
+  const gm_u32x4* ar[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = min(row0 + rt * 16 + l16, M - 1);           // rows past M: loaded, never stored
+    ar[rt] = reinterpret_cast<const gm_u32x4*>(w + (int64_t)row * K + kbeg + 8 * q);
+  }
+  const gm_f32x4* xr = reinterpret_cast<const gm_f32x4*>(x + (int64_t)min(tok, n_tok - 1) * K + kbeg + 8 * q);
+  gm_f32x4 acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < kw; c0 += 32 * NC) {
+    gm_u32x4 a[RT][NC];
+    gm_f32x4 xa[NC], xb[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) a[rt][c] = gm_ld<true>(ar[rt] + (c0 + 32 * c) / 8);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      xa[c] = xr[(c0 + 32 * c) / 4];
+      xb[c] = xr[(c0 + 32 * c) / 4 + 1];
+    }
+    __builtin_amdgcn_sched_barrier(0);                          // every load of the chunk before the first use
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      gm_u32x4 pl[3];
+      split3(xa[c], xb[c], pl);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+          acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gm_bf16x8, a[rt][c]),
+                                                            __builtin_bit_cast(gm_bf16x8, pl[p]), acc[rt], 0, 0, 0);
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) red[wave - 1][rt][lane] = acc[rt];
+  }
+  __syncthreads();
+  if (wave > 0 || tok >= n_tok) return;
+#pragma unroll
+  for (int v = 0; v < WPB - 1; ++v)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt] += red[v][rt][lane];
+  // C layout: lane l holds rows 4 (l / 16) + i of the tile, column (token) l % 16
+  float* out = y + (int64_t)tok * M;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = row0 + rt * 16 + 4 * q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (row + i < M) out[row + i] = acc[rt][i];
+  }
+}
+
+template <int RT, int WPB>
+int launch_mfma_w(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
+  const dim3 grid((unsigned)((M + 16 * RT - 1) / (16 * RT)), (unsigned)((n_tok + 15) / 16));
+  const int steps = K / (32 * WPB);                              // k-steps per wave (K % 256 == 0)
+#define GM_MV_GO(NC)                                                                               \
+  hipLaunchKernelGGL((k_mv_bf16_mfma<RT, WPB, NC>), grid, dim3(64 * WPB), 0, s, w, M, K, x, n_tok, y); \
+  break;
+  switch (steps % 8 == 0 ? 8 : steps % 4 == 0 ? 4 : steps % 2 == 0 ? 2 : 1) {
+    case 8: GM_MV_GO(8)
+    case 4: GM_MV_GO(4)
+    case 2: GM_MV_GO(2)
+    default: GM_MV_GO(1)
+  }
+#undef GM_MV_GO
+  GM_TRY(hipGetLastError());
+  return GM_OK;
+}
+
+// Two row tiles per block for tall matrices, else one; waves per block so that
+// the grid holds about 1024 waves.
+int launch_mfma(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
+  const int rt = M >= 8192 ? 2 : 1;
+  const int blocks = (M + 16 * rt - 1) / (16 * rt);
+  const bool w8 = blocks < 256;
+  if (rt == 2) return w8 ? launch_mfma_w<2, 8>(w, M, K, x, n_tok, y, s) : launch_mfma_w<2, 4>(w, M, K, x, n_tok, y, s);
+  return w8 ? launch_mfma_w<1, 8>(w, M, K, x, n_tok, y, s) : launch_mfma_w<1, 4>(w, M, K, x, n_tok, y, s);
+}
+
 template <int NT, int R, int S>
 int launch_mv(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
   const size_t smem = (size_t)NT * K * sizeof(float);
@@ -110,28 +234,23 @@ int launch_mv(const uint16_t* w, int M, int K, const float* x, int n_tok, float*
   return GM_OK;
 }
 
-// S = the row's slots (at most 16 per pass).  One row per wave for one token
-// (the most waves, each with the whole row in flight, was the fastest launch
-// shape on MI355X); two rows per wave for a token tile, whose LDS copy of x
-// is then shared by 8 rows per block.
-template <int NT, int R>
-int launch_mv_r(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
+// S = the row's slots (at most 16 per pass), one row per wave (the most
+// waves, each with its whole row in flight, was the fastest launch shape).
+int launch_mv1(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
   const int slots = (K + kSlotK - 1) / kSlotK;
-  if (slots <= 1) return launch_mv<NT, R, 1>(w, M, K, x, n_tok, y, s);
-  if (slots <= 2) return launch_mv<NT, R, 2>(w, M, K, x, n_tok, y, s);
-  if (slots <= 4) return launch_mv<NT, R, 4>(w, M, K, x, n_tok, y, s);
-  if (slots <= 8) return launch_mv<NT, R, 8>(w, M, K, x, n_tok, y, s);
-  return launch_mv<NT, R, 16>(w, M, K, x, n_tok, y, s);
+  if (slots <= 1) return launch_mv<1, 1, 1>(w, M, K, x, n_tok, y, s);
+  if (slots <= 2) return launch_mv<1, 1, 2>(w, M, K, x, n_tok, y, s);
+  if (slots <= 4) return launch_mv<1, 1, 4>(w, M, K, x, n_tok, y, s);
+  if (slots <= 8) return launch_mv<1, 1, 8>(w, M, K, x, n_tok, y, s);
+  return launch_mv<1, 1, 16>(w, M, K, x, n_tok, y, s);
 }
 
 }  // namespace
 
 // K a multiple of 256 and <= 16384, w and x 16-byte aligned (checked by the
-// caller).  The token tile is sized so that NT x K fp32 values fit 64 KB of LDS.
+// caller).  One token: the streaming FMA kernel; more: the MFMA kernel, 16
+// tokens per column tile.
 int gm_launch_mv_bf16(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
-  const int nt_lds = 16384 / K;                                   // 1 .. 64
-  if (n_tok == 1) return launch_mv_r<1, 1>(w, M, K, x, n_tok, y, s);
-  if (n_tok == 2 || nt_lds < 4) return launch_mv_r<2, 2>(w, M, K, x, n_tok, y, s);
-  if (n_tok <= 4 || nt_lds < 8) return launch_mv_r<4, 2>(w, M, K, x, n_tok, y, s);
-  return launch_mv_r<8, 2>(w, M, K, x, n_tok, y, s);
+  if (n_tok == 1) return launch_mv1(w, M, K, x, n_tok, y, s);
+  return launch_mfma(w, M, K, x, n_tok, y, s);
 }
