@@ -20,6 +20,7 @@ namespace {
 
 constexpr int kWaves = 16;
 constexpr int kMaxE = 512;
+constexpr int kBatch = 4;                   // 64-pair steps whose ids are loaded together
 
 __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ ids, int P, int E,
                                                    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
@@ -33,9 +34,16 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ i
   __syncthreads();
   const int chunk = (P + kWaves - 1) / kWaves;
   const int p0 = wave * chunk, p1 = min(P, p0 + chunk);
-  for (int p = p0 + lane; p < p1; p += 64) {
-    const int e = ids[p];
-    if (e >= 0 && e < E) atomicAdd(&cnt[wave * E + e], 1);
+  for (int b = p0; b < p1; b += 64 * kBatch) {
+    int eb[kBatch];                          // every load of the batch before the first use
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int p = b + 64 * j + lane;
+      eb[j] = p < p1 ? ids[p] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      if (eb[j] >= 0 && eb[j] < E) atomicAdd(&cnt[wave * E + eb[j]], 1);
   }
   __syncthreads();
   // per-expert totals (thread e) and their exclusive scan across the block
@@ -73,26 +81,37 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ i
   __syncthreads();
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
-  for (int b = p0; b < p1; b += 64) {
-    const int p = b + lane;
-    int e = p < p1 ? ids[p] : -1;
-    if (e >= E) e = -1;
-    uint64_t same = __ballot(e >= 0);
-    for (int i = 0; i < nbits; ++i) {
-      const uint64_t m = __ballot((e >> i) & 1);
-      same &= ((e >> i) & 1) ? m : ~m;
+  for (int b0 = p0; b0 < p1; b0 += 64 * kBatch) {
+    int eb[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int p = b0 + 64 * j + lane;
+      eb[j] = p < p1 ? ids[p] : -1;
     }
-    const int r = __popcll(same & ((1ull << lane) - 1ull));
-    const bool last = (same >> lane) >> 1 == 0;          // no same-expert lane above
-    int pos = 0;
-    if (e >= 0) pos = cnt[wave * E + e] + r;
-    __builtin_amdgcn_wave_barrier();
-    if (e >= 0) {
-      sorted[pos] = p;
-      if (inv) inv[p] = pos;
-      if (last) cnt[wave * E + e] = pos + 1;
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int b = b0 + 64 * j;
+      if (b >= p1) break;                      // wave-uniform
+      const int p = b + lane;
+      int e = eb[j];
+      if (e >= E) e = -1;
+      uint64_t same = __ballot(e >= 0);
+      for (int i = 0; i < nbits; ++i) {
+        const uint64_t m = __ballot((e >> i) & 1);
+        same &= ((e >> i) & 1) ? m : ~m;
+      }
+      const int r = __popcll(same & ((1ull << lane) - 1ull));
+      const bool last = (same >> lane) >> 1 == 0;          // no same-expert lane above
+      int pos = 0;
+      if (e >= 0) pos = cnt[wave * E + e] + r;
+      __builtin_amdgcn_wave_barrier();
+      if (e >= 0) {
+        sorted[pos] = p;
+        if (inv) inv[p] = pos;
+        if (last) cnt[wave * E + e] = pos + 1;
+      }
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_wave_barrier();
   }
   if (!segs) return;
   // segments: unit u < E is expert u, unit E the shared one; exclusive scan of nseg
