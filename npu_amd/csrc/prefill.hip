@@ -847,24 +847,37 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ x,
   const float sg = has_sh ? shg[t] : 0.f;
   const int Ptot = T * k, nq = D >> 2;
   const gm_f32x4* yp4 = reinterpret_cast<const gm_f32x4*>(yp);
-  for (int c = threadIdx.x; c < nq; c += 256) {
-    gm_f32x4 v[9];
+  const gm_f32x4* x4 = reinterpret_cast<const gm_f32x4*>(x + (int64_t)t * D);
+  constexpr int CS = 2;                      // column steps whose loads are issued together
+  for (int c0 = threadIdx.x; c0 < nq; c0 += 256 * CS) {
+    gm_f32x4 v[CS][9], xv[CS];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = yp4[(int64_t)(j < k ? pos[j] : pos[0]) * nq + c];
-    v[8] = yp4[(int64_t)(has_sh ? Ptot + t : pos[0]) * nq + c];
-    gm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < CS; ++u) {
+      const int c = min(c0 + 256 * u, nq - 1);                   // past the row: a duplicate, not stored
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (j < k) {
-        acc.x = fmaf(w[j], v[j].x, acc.x); acc.y = fmaf(w[j], v[j].y, acc.y);
-        acc.z = fmaf(w[j], v[j].z, acc.z); acc.w = fmaf(w[j], v[j].w, acc.w);
-      }
-    if (has_sh) { acc.x += sg * v[8].x; acc.y += sg * v[8].y; acc.z += sg * v[8].z; acc.w += sg * v[8].w; }
-    if (flags & GM_MOE_RESIDUAL) {
-      const gm_f32x4 xv = reinterpret_cast<const gm_f32x4*>(x + (int64_t)t * D)[c];
-      acc.x = xv.x + acc.x; acc.y = xv.y + acc.y; acc.z = xv.z + acc.z; acc.w = xv.w + acc.w;
+      for (int j = 0; j < 8; ++j) v[u][j] = yp4[(int64_t)(j < k ? pos[j] : pos[0]) * nq + c];
+      v[u][8] = yp4[(int64_t)(has_sh ? Ptot + t : pos[0]) * nq + c];
+      xv[u] = (flags & GM_MOE_RESIDUAL) ? x4[c] : gm_f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    reinterpret_cast<gm_f32x4*>(y + (int64_t)t * D)[c] = acc;
+#pragma unroll
+    for (int u = 0; u < CS; ++u) {
+      const int c = c0 + 256 * u;
+      if (c >= nq) break;
+      gm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < k) {
+          acc.x = fmaf(w[j], v[u][j].x, acc.x); acc.y = fmaf(w[j], v[u][j].y, acc.y);
+          acc.z = fmaf(w[j], v[u][j].z, acc.z); acc.w = fmaf(w[j], v[u][j].w, acc.w);
+        }
+      if (has_sh) {
+        acc.x += sg * v[u][8].x; acc.y += sg * v[u][8].y; acc.z += sg * v[u][8].z; acc.w += sg * v[u][8].w;
+      }
+      if (flags & GM_MOE_RESIDUAL) {
+        acc.x = xv[u].x + acc.x; acc.y = xv[u].y + acc.y; acc.z = xv[u].z + acc.z; acc.w = xv[u].w + acc.w;
+      }
+      reinterpret_cast<gm_f32x4*>(y + (int64_t)t * D)[c] = acc;
+    }
   }
 }
 
