@@ -147,7 +147,9 @@ int gm_moe_workspace_offsets(const gm_moe_layer* L, int T, size_t* off_logits, s
  * products, shared expert and the combine all run on the device from
  * device-resident ids (no host synchronisation).  T <= 8 uses the decode
  * kernels (fp32 accumulate); larger T uses the grouped MFMA prefill.
- * x and y must not alias.  Replaces qwen/forward.py:moe_forward (563-665).
+ * x and y must not alias.  x, y, the weight pointers, L->norm_w and
+ * L->sh_gate_inp must be 16-byte aligned (torch allocations are).
+ * Replaces qwen/forward.py:moe_forward (563-665).
  */
 int gm_moe_forward(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
                    size_t ws_bytes, void* stream);

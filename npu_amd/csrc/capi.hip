@@ -78,10 +78,11 @@ static int check_layer(const gm_moe_layer* L) {
                          L->q_up_sh, L->q_down_sh);
   }
   if (L->norm_w && !(L->norm_eps >= 0.f)) return gm_fail_arg("gm_moe_forward: norm_eps must be >= 0");
-  const void* wptrs[] = {L->gate_exps, L->up_exps, L->down_exps, L->gate_sh, L->up_sh, L->down_sh, L->router};
+  const void* wptrs[] = {L->gate_exps, L->up_exps, L->down_exps, L->gate_sh,     L->up_sh,
+                         L->down_sh,    L->router, L->norm_w,    L->sh_gate_inp};
   for (const void* p : wptrs)
     if (reinterpret_cast<uintptr_t>(p) % 16)
-      return gm_fail_arg("gm_moe_forward: weight pointers must be 16-byte aligned");
+      return gm_fail_arg("gm_moe_forward: weight, norm_w and sh_gate_inp pointers must be 16-byte aligned");
   return GM_OK;
 }
 
@@ -207,6 +208,8 @@ static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int
   if (T == 0) return GM_OK;
   if (!x || !y || !ws) return gm_fail_arg("gm_moe_forward: NULL pointer");
   if (x == y) return gm_fail_arg("gm_moe_forward: x and y must not alias");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 16)
+    return gm_fail_arg("gm_moe_forward: x and y must be 16-byte aligned");
   const GmMoeWs lay = gm_moe_ws_layout(L, T);
   if (ws_bytes < lay.total)
     return gm_fail_arg("gm_moe_forward: workspace %zu bytes < %zu needed", ws_bytes, lay.total), GM_EWORKSPACE;

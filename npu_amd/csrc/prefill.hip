@@ -130,6 +130,60 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
   const int t = blockIdx.x;
   const gm_f32x2* x2 = reinterpret_cast<const gm_f32x2*>(x + (int64_t)t * D);
   const int n2 = D >> 1;
+  if (D <= 4096) {                                             // uniform: the row held in registers
+    constexpr int NQ = 4;                                      // 16-byte granules per thread
+    const int n4 = D >> 2;
+    const gm_f32x4* x4 = reinterpret_cast<const gm_f32x4*>(x + (int64_t)t * D);
+    gm_f32x4 v[NQ], wv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {                             // every load before the first use
+      const int c = min((int)threadIdx.x + 256 * i, n4 - 1);   // past the row: a duplicate, not used
+      v[i] = x4[c];
+      wv[i] = norm_w ? reinterpret_cast<const gm_f32x4*>(norm_w)[c] : gm_f32x4{1.f, 1.f, 1.f, 1.f};
+    }
+    float rms = 1.f;
+    if (norm_w) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < NQ; ++i)
+        if ((int)threadIdx.x + 256 * i < n4)
+          ss = fmaf(v[i].x, v[i].x, fmaf(v[i].y, v[i].y, fmaf(v[i].z, v[i].z, fmaf(v[i].w, v[i].w, ss))));
+      ss = gm_wave_sum64(ss);
+      if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+      __syncthreads();
+      rms = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)D + eps);
+    }
+    uint2* q0 = reinterpret_cast<uint2*>(xr) + (int64_t)t * n4;
+    uint2* q1 = q0 + (int64_t)T * n4;
+    uint2* q2 = q1 + (int64_t)T * n4;
+    uint2* qh = reinterpret_cast<uint2*>(xh) + (int64_t)t * n4;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int c = (int)threadIdx.x + 256 * i;
+      if (c >= n4) break;
+      gm_f32x2 h[2] = {gm_f32x2{v[i].x, v[i].y}, gm_f32x2{v[i].z, v[i].w}};
+      const gm_f32x2 w[2] = {gm_f32x2{wv[i].x, wv[i].y}, gm_f32x2{wv[i].z, wv[i].w}};
+      uint32_t o0[2], o1[2], o2[2], oh[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (norm_w) { h[j].x = (h[j].x * rms) * w[j].x; h[j].y = (h[j].y * rms) * w[j].y; }
+        const gm_bf16x2 b0 = __builtin_convertvector(h[j], gm_bf16x2);
+        const gm_f32x2 r0 = h[j] - __builtin_convertvector(b0, gm_f32x2);
+        const gm_bf16x2 b1 = __builtin_convertvector(r0, gm_bf16x2);
+        const gm_f32x2 r1 = r0 - __builtin_convertvector(b1, gm_f32x2);
+        const gm_bf16x2 b2 = __builtin_convertvector(r1, gm_bf16x2);
+        o0[j] = __builtin_bit_cast(uint32_t, b0);
+        o1[j] = __builtin_bit_cast(uint32_t, b1);
+        o2[j] = __builtin_bit_cast(uint32_t, b2);
+        oh[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(h[j], gm_f16x2));
+      }
+      q0[c] = make_uint2(o0[0], o0[1]);
+      q1[c] = make_uint2(o1[0], o1[1]);
+      q2[c] = make_uint2(o2[0], o2[1]);
+      qh[c] = make_uint2(oh[0], oh[1]);
+    }
+    return;
+  }
   float rms = 1.f;
   if (norm_w) {
     float ss = 0.f;
