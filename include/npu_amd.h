@@ -77,7 +77,9 @@ int gm_matvec(int qtype, const void* w, int M, int K, const float* x, int n_tok,
 /*
  * SwiGLU MLP: y[t] = W_down (silu(W_gate x[t]) * (W_up x[t])), gate/up
  * [FF][D] of qtype q_gu, down [D][FF] of qtype q_down; h is an fp32
- * [n_tok][FF] scratch buffer.  Replaces NpuFusedMLP.__call__
+ * [n_tok][FF] scratch buffer.  Weights aligned to 16 (bf16), 8 (IQ4_XS) or
+ * 2 (IQ3_XXS) bytes; h 16-byte aligned when the down matrix is bf16.
+ * Replaces NpuFusedMLP.__call__
  * (npu/mlp.py:413-466) and the shared-expert F.linear chain
  * (qwen/forward.py:592-598).
  */

@@ -129,6 +129,13 @@ int gm_swiglu_mlp(int q_gu, const void* w_gate, const void* w_up, int q_down, co
   if (n_tok < 0) return gm_fail_arg("gm_swiglu_mlp: negative n_tok");
   if (n_tok == 0) return GM_OK;
   if (!w_gate || !w_up || !w_down || !x || !h || !y) return gm_fail_arg("gm_swiglu_mlp: NULL pointer");
+  // each weight aligned to its format's load width; h is read with 16-byte loads by the bf16 down kernel
+  auto width = [](int q) -> uintptr_t { return q == GM_QTYPE_BF16 ? 16 : q == GM_QTYPE_IQ4_XS ? 8 : 2; };
+  if (reinterpret_cast<uintptr_t>(w_gate) % width(q_gu) || reinterpret_cast<uintptr_t>(w_up) % width(q_gu) ||
+      reinterpret_cast<uintptr_t>(w_down) % width(q_down) ||
+      (q_down == GM_QTYPE_BF16 && reinterpret_cast<uintptr_t>(h) % 16))
+    return gm_fail_arg("gm_swiglu_mlp: weights must be aligned to 16 (bf16), 8 (IQ4_XS) or 2 (IQ3_XXS) bytes, "
+                       "and h to 16 bytes when the down matrix is bf16");
   hipStream_t s = as_stream(stream);
   if (int rc = gm_launch_gateup(q_gu, w_gate, w_up, FF, D, x, n_tok, h, s)) return rc;
   return gm_launch_matvec(q_down, w_down, D, FF, h, n_tok, y, s);

@@ -79,6 +79,8 @@ def test_workspace_sizing_and_layer_validation():
     # the kernels read x, norm_w and the weights with 16-byte loads
     rc = lib.gm_moe_forward(ctypes.byref(s), 1028, 2048, 1, 0, 4096, 1 << 30, None)
     assert rc == L.GM_EINVAL and "x and y must be 16-byte aligned" in L.last_error()
+    rc = lib.gm_swiglu_mlp(L.GM_QTYPE_IQ4_XS, 256, 256, L.GM_QTYPE_BF16, 264, 2048, 512, 1024, 1, 2048, 4096, None)
+    assert rc == L.GM_EINVAL and "aligned" in L.last_error()
     bad = _layer(norm_w=4100)
     rc = lib.gm_moe_forward(ctypes.byref(bad), 1024, 2048, 1, 0, 4096, 1 << 30, None)
     assert rc == L.GM_EINVAL and "16-byte aligned" in L.last_error()
