@@ -81,6 +81,11 @@ def test_workspace_sizing_and_layer_validation():
     assert rc == L.GM_EINVAL and "x and y must be 16-byte aligned" in L.last_error()
     rc = lib.gm_swiglu_mlp(L.GM_QTYPE_IQ4_XS, 256, 256, L.GM_QTYPE_BF16, 264, 2048, 512, 1024, 1, 2048, 4096, None)
     assert rc == L.GM_EINVAL and "aligned" in L.last_error()
+    # the prefill router keeps at most 16 K-range partials: D = 4352 would need 17
+    wide = _layer(D=4352)
+    need = lib.gm_moe_workspace_bytes(ctypes.byref(wide), 16)
+    rc = lib.gm_moe_prefill(ctypes.byref(wide), 1024, 1 << 20, 16, 0, 1 << 24, need, None)
+    assert rc == L.GM_EINVAL and "prefill supports D <= 8192" in L.last_error()
     bad = _layer(norm_w=4100)
     rc = lib.gm_moe_forward(ctypes.byref(bad), 1024, 2048, 1, 0, 4096, 1 << 30, None)
     assert rc == L.GM_EINVAL and "16-byte aligned" in L.last_error()
