@@ -55,29 +55,8 @@ def parse() -> argparse.Namespace:
 
 
 def build_layers(n_layers: int, device):
-    import torch
     from npu_amd import synth
-    from npu_amd.gguf_types import GGMLQuantizationType as QT
-    from npu_amd.moe import GpuMoeBlock
-
-    gen = torch.Generator(device=device)
-    gen.manual_seed(SEED)
-    layers = []
-    for _ in range(n_layers):
-        gate = synth.device_quant_matrix(gen, QT.IQ4_XS, FF, D, E, device)
-        up = synth.device_quant_matrix(gen, QT.IQ4_XS, FF, D, E, device)
-        down = synth.device_quant_matrix(gen, QT.IQ3_XXS, D, FF, E, device)
-        router = synth.device_bf16_normal(gen, (E, D), synth.ROUTER_STD, device)
-        gate_sh = synth.device_quant_matrix(gen, QT.IQ4_XS, FF, D, None, device)
-        up_sh = synth.device_quant_matrix(gen, QT.IQ4_XS, FF, D, None, device)
-        down_sh = synth.device_quant_matrix(gen, QT.IQ3_XXS, D, FF, None, device)
-        sh_inp = synth.device_bf16_normal(gen, (D,), synth.ROUTER_STD, device)
-        norm_w = torch.ones(D, dtype=torch.float32, device=device)
-        layers.append(GpuMoeBlock(gate=gate, up=up, down=down, router=router, q_gate=QT.IQ4_XS,
-                                  q_down=QT.IQ3_XXS, D=D, FF=FF, E=E, k=K_TOP, gate_sh=gate_sh, up_sh=up_sh,
-                                  down_sh=down_sh, sh_gate_inp=sh_inp, norm_w=norm_w, norm_eps=1e-6,
-                                  device=device))
-    return layers
+    return synth.device_config5_layers(n_layers, device, SEED)
 
 
 def unique_experts(blk, T: int) -> int:

@@ -8,11 +8,14 @@ present the calls raise.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().with_name("libnpu_amd.so")
+# NPU_AMD_LIB=timeline selects the timestamped profiling build (libnpu_amd_tl.so).
+LIB_PATH = Path(__file__).resolve().with_name(
+    "libnpu_amd_tl.so" if os.environ.get("NPU_AMD_LIB") == "timeline" else "libnpu_amd.so")
 
 GM_QTYPE_F32 = 0
 GM_QTYPE_F16 = 1

@@ -2,6 +2,8 @@
 
 Usage: ``python -m npu_amd.build`` (or ``npu_amd.build.build()``).  The library
 is written next to this file, in-tree, so it travels with the source tree.
+``python -m npu_amd.build --timeline`` builds the profiling variant
+``libnpu_amd_tl.so`` (per-block timestamps, see csrc/timeline.h) instead.
 """
 from __future__ import annotations
 
@@ -15,6 +17,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libnpu_amd.so"
+LIB_TL = HERE / "libnpu_amd_tl.so"
 SOURCES = ["capi.hip", "matvec.hip", "router.hip", "moe_decode.hip", "moe_decode_gu.hip", "moe_decode_dn.hip",
            "dispatch.hip", "prefill.hip", "mv_bf16.hip"]
 ARCH = os.environ.get("NPU_AMD_ARCH", "gfx950")
@@ -38,12 +41,14 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source to an object in parallel, then link the library."""
-    objdir = HERE / "_build"
+def build(verbose: bool = False, timeline: bool = False) -> Path:
+    """Compile every source to an object in parallel, then link the library
+    (the timestamped profiling variant when ``timeline``)."""
+    objdir = HERE / ("_build_tl" if timeline else "_build")
     objdir.mkdir(exist_ok=True)
     inc = ["-I", str(HERE.parent / "include")]
-    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"] + (["-DGM_TIMELINE=1"] if timeline else [])
+    out_lib = LIB_TL if timeline else LIB
 
     def compile_one(src: str):
         obj = objdir / (Path(src).stem + ".o")
@@ -55,7 +60,7 @@ def build(verbose: bool = False) -> Path:
     jobs = max(1, min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8"))))
     with ThreadPoolExecutor(jobs) as ex:
         results = list(ex.map(compile_one, SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = out_lib.with_suffix(".so.tmp")
     link = [hipcc(), *HIPCC_FLAGS, *[str(o) for o, _ in results], "-o", str(tmp)]
     results.append((None, subprocess.run(link, capture_output=True, text=True)))
     for _, res in results:
@@ -65,9 +70,9 @@ def build(verbose: bool = False) -> Path:
             raise RuntimeError(f"hipcc failed ({res.returncode}):\n{out}")
         if verbose and out:
             print(out)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out_lib)
+    return out_lib
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, timeline="--timeline" in sys.argv))

@@ -1,6 +1,7 @@
 // Internal launchers (host side).  All return GM_OK or an error status.
 #pragma once
 #include "common.h"
+#include "timeline.h"
 
 int gm_launch_dequant(int qtype, const void* raw, int64_t n_sb, float* out, hipStream_t s);
 
@@ -35,6 +36,7 @@ struct GmMoeWs {
   size_t yp;       // f32 [T * k + T][D]  per-pair / shared partial outputs (decode, T > 1)
   size_t counters; // u32 [64]   self-resetting counters
   size_t pre;      // prefill scratch (see prefill.hip)
+  size_t tl;       // per-block timestamps (profiling build only, else empty)
   size_t total;
 };
 

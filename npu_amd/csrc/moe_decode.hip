@@ -29,7 +29,7 @@ namespace {
 template <int QTS, int NT, int DC>
 __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float* __restrict__ x, int T,
                                                     float* __restrict__ logits, float* __restrict__ shg,
-                                                    float* __restrict__ hsh, int n_rb, uint8_t* __restrict__ xl_out) {
+                                                    float* __restrict__ hsh, int n_rb, uint8_t* __restrict__ xl_out GM_TL_PARAM) {
   constexpr int SPLR = DC > 1 ? DC / 2 : 1;
   constexpr bool IQ3 = QTS == GM_QTYPE_IQ3_XXS;
   extern __shared__ float smem[];
@@ -38,6 +38,7 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
   Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(red + 4 * NT);       // IQ3 shared expert only
   const int D = P.D, E = P.E, nsub = D / GM_SUB;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  GM_TL_BEGIN();
   int tok[NT];
 #pragma unroll
   for (int m = 0; m < NT; ++m) tok[m] = m;
@@ -54,10 +55,12 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
     fetch_subs<GM_QTYPE_BF16, 64, SPLR, true>(f, wr, lane, nsub);
     issue_fence();
     stage_x_regs<NT, DC>(xr, T, D, P.norm_w, P.norm_eps, xs, red);
+    GM_TL_MARK1(xs[0]);
     float acc[NT];
 #pragma unroll
     for (int m = 0; m < NT; ++m) acc[m] = 0.f;
     dot_subs<GM_QTYPE_BF16, 64, SPLR, NT>(f, lane, nsub, xs, D, tok, T, nullptr, acc);
+    GM_TL_MARK2(acc[0]);
 #pragma unroll
     for (int m = 0; m < NT; ++m) acc[m] = gm_wave_sum64(acc[m]);
     if (row < nrows && lane == 0) {
@@ -69,6 +72,7 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
         }
       }
     }
+    GM_TL_END(0);
     return;
   }
   if constexpr (IQ3) gm_iq3_tab_store(gw, tab);                // visible after stage_x_regs' barrier
@@ -83,12 +87,14 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
   issue_fence();
   uint8_t* xl = reinterpret_cast<uint8_t*>(xs);                // limb rows (fit in the fp32 rows' space)
   stage_limbs_regs<NT, DC>(xr, T, D, P.norm_w, P.norm_eps, xl, red);
+  GM_TL_MARK1(xl[0]);
   float ag[NT], au[NT];
 #pragma unroll
   for (int m = 0; m < NT; ++m) { ag[m] = 0.f; au[m] = 0.f; }
   const int rbytes = gm_limb_row_bytes(D);
   dot_subs_i8<QTS, 32, DC, NT>(fg, lane & 31, nsub, xl, rbytes, tok, T, tab, ag);
   dot_subs_i8<QTS, 32, DC, NT>(fu, lane & 31, nsub, xl, rbytes, tok, T, tab, au);
+  GM_TL_MARK2(au[0]);
 #pragma unroll
   for (int m = 0; m < NT; ++m) {
     const float hv = gm_silu(row_sum<32>(ag[m])) * row_sum<32>(au[m]);
@@ -99,6 +105,7 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
     gm_u32x4* dst = reinterpret_cast<gm_u32x4*>(xl_out);
     for (int c = threadIdx.x; c < NT * (rbytes >> 4); c += 256) dst[c] = src[c];
   }
+  GM_TL_END(0);
 }
 
 // T > 1: partial router dot products over K ranges, part[z][t][r] =
@@ -106,17 +113,18 @@ __global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float*
 // vector) and ssq[z][t] = sum_{k in range z} x[t][k]^2, so that no block loads
 // more than its range of the T input rows; k_dec_route applies the RMSNorm
 // factor (qwen/forward.py:58-61) to the summed partials.  Block = 4 rows (one
-// per wave) x one range of kr = min(D, 512) values; lane l takes k = 8l .. 8l+7.
+// per wave) x one range of kr = gm_dec_kr(D) values (512, or 256 when 512 does
+// not divide D); lane l takes k = 8l .. 8l+7.
 // Wave 0 of the first row block of each range also writes the limb rows of
 // x w_norm for the range (the RMSNorm factor is applied to the dot products
 // instead), so the grouped gate/up kernel only copies them.
 template <int NT>
 __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const float* __restrict__ x, int T,
                                                        float* __restrict__ part, float* __restrict__ ssq, int ldp,
-                                                       uint8_t* __restrict__ xl) {
+                                                       int kr, uint8_t* __restrict__ xl) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int D = P.D, E = P.E, nrows = E + (P.sh_gate_inp != nullptr ? 1 : 0);
-  const int kr = D < 512 ? D : 512, z = blockIdx.y, k0 = z * kr + 8 * lane;
+  const int z = blockIdx.y, k0 = z * kr + 8 * lane;
   const bool lv = 8 * lane < kr;
   const int kk = lv ? k0 : z * kr;                              // lanes past the range re-read its start
   const int row = blockIdx.x * 4 + wave;
@@ -177,7 +185,7 @@ int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArg
   const size_t smem = ((size_t)NT * P->D + 4 + 4 * NT) * 4 + (QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
   if (int rc = gm_set_smem(k_dec_router<QTS, NT, DC>, smem)) return rc;
   hipLaunchKernelGGL((k_dec_router<QTS, NT, DC>), dim3(n_rb + n_sb), dim3(256), smem, s, *P, x, T, a.logits, a.shg,
-                     a.hsh, n_rb, n_sb > 0 ? a.xl : nullptr);
+                     a.hsh, n_rb, n_sb > 0 ? a.xl : nullptr GM_TL_ARG(a.tl));
   GM_TRY(hipGetLastError());
   return GM_OK;
 }
@@ -194,9 +202,9 @@ int launch_router_n(const gm_moe_layer* P, const float* x, int T, const GmDecArg
 int launch_router(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s, bool fast1) {
   if (!fast1) {                                                      // router partials only
     const int nrows = P->E + (P->sh_gate_inp ? 1 : 0);
-    const int kr = P->D < 512 ? P->D : 512;
+    const int kr = gm_dec_kr(P->D);
     hipLaunchKernelGGL(k_dec_router_ks<8>, dim3((nrows + 3) / 4, P->D / kr), dim3(256), 0, s, *P, x, T, a.part,
-                       a.ssq, gm_dec_part_ld(P), a.xl);
+                       a.ssq, gm_dec_part_ld(P), kr, a.xl);
     GM_TRY(hipGetLastError());
     return GM_OK;
   }
@@ -227,11 +235,12 @@ int gm_dec_run(const gm_moe_layer* P, const float* x, float* y, int T, int flags
   a.h = reinterpret_cast<float*>(ws + lay.h);
   a.hsh = reinterpret_cast<float*>(ws + lay.hsh);
   a.yp = reinterpret_cast<float*>(ws + lay.yp);
+  a.tl = reinterpret_cast<uint64_t*>(ws + lay.tl);
   // general path: router partials, x^2 partials, RMSNorm factors and the limb
   // rows of x w_norm live in yp, which stage 3 overwrites only after stage 2
   a.part = a.yp;
-  a.ssq = a.part + (size_t)(P->D / (P->D < 512 ? P->D : 512)) * T * gm_dec_part_ld(P);
-  a.rms = a.ssq + 8 * T;
+  a.ssq = a.part + (size_t)gm_dec_nz(P->D) * T * gm_dec_part_ld(P);
+  a.rms = a.ssq + GM_DEC_MAX_NZ * T;
   a.xl = reinterpret_cast<uint8_t*>(a.rms + 16);
   if (a.xl + (size_t)(T + 1) * gm_limb_row_bytes(P->D) > reinterpret_cast<uint8_t*>(a.yp + (size_t)(T * P->k + T) * P->D))
     return gm_fail_arg("gm_moe_forward: internal workspace layout error (yp)");

@@ -39,8 +39,9 @@ __device__ __forceinline__ float group_sum(float v, int n) {
 template <int QTD, int QTS, int FC>
 __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* __restrict__ x, int flags,
                                                    const int32_t* __restrict__ g_grp, const float* __restrict__ h,
-                                                   const float* __restrict__ shg, float* __restrict__ y) {
+                                                   const float* __restrict__ shg, float* __restrict__ y GM_TL_PARAM) {
   constexpr int NTH = 576;
+  GM_TL_BEGIN();
   constexpr bool IQ3 = QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS;
   constexpr int RMAX = 2 * FC;                                 // rows per lane, FF <= 512 FC
   constexpr int HPT = (9 * 128 * FC + NTH - 1) / NTH;          // float4 of the k + 1 SwiGLU rows per thread
@@ -72,6 +73,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   const int my_pr = g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * jj];
   const float my_wj = __int_as_float(g_grp[GM_GRP_WORDS + jj]);
   const float sg = has_sh ? shg[0] : 0.f;
+  GM_TL_MARK1(ex[0]);
   const float xres = (flags & GM_MOE_RESIDUAL) ? x[r0 + (tid & 7)] : 0.f;
   uint32_t gw = 0;
   if constexpr (IQ3) gw = gm_iq3_tab_load();
@@ -133,6 +135,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
     for (int i = 0; i < CR; ++i) *reinterpret_cast<gm_u32x4*>(wr + dst[i]) = rr[i];
   }
   __syncthreads();
+  GM_TL_MARK2(s_pr[0]);
   // --- D: decode from LDS; wave w -> matrix w
   const bool routed = wave < k, shared = has_sh && wave == k;
   if (routed || shared) {
@@ -205,6 +208,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
     if (has_sh) acc += s_part[k][tid];
     if (r0 + tid < D) y[r0 + tid] = (flags & GM_MOE_RESIDUAL) ? xres + acc : acc;
   }
+  GM_TL_END(2);
 }
 
 // 64 rows of one down matrix for nm <= 8 member rows of hsrc (global rows
@@ -371,7 +375,7 @@ int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags,
                           (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
       if (int rc = gm_set_smem(k_dec_down1<QTD, QTS, FC>, smem)) return rc;
       hipLaunchKernelGGL((k_dec_down1<QTD, QTS, FC>), dim3((D + 7) / 8), dim3(576), smem, s, *P, x, flags, a.grp,
-                         a.h, a.shg, y);
+                         a.h, a.shg, y GM_TL_ARG(a.tl));
       GM_TRY(hipGetLastError());
       return GM_OK;
     }

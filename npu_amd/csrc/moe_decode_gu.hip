@@ -26,8 +26,9 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
                                                      const float* __restrict__ logits, int32_t* __restrict__ g_ids,
                                                      float* __restrict__ g_wts, int32_t* __restrict__ g_grp,
                                                      float* __restrict__ h, int n_chunks,
-                                                     const uint8_t* __restrict__ xl) {
+                                                     const uint8_t* __restrict__ xl GM_TL_PARAM) {
   constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
+  GM_TL_BEGIN();
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int D = P.D, E = P.E, k = P.k, FF = P.FF, nsub = D / GM_SUB, rbytes = gm_limb_row_bytes(D);
   uint8_t* xs = smem;                                          // limb row of x (+ a spare sub-block)
@@ -55,6 +56,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
   if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
   __syncthreads();
   const int e = s_sid[u], pair = s_slot[u];
+  GM_TL_MARK1(e);
   const int64_t rb = gm_row_bytes(QT, D);
   const int row = chunk * 8 + wave * 2 + (lane >> 5);
   const bool live = row < FF;
@@ -83,15 +85,17 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
   float ag[1] = {0.f}, au[1] = {0.f};
   dot_subs_i8<QT, 32, DC, 1>(fg, lane & 31, nsub, xs, rbytes, tok, 1, tab, ag);
   dot_subs_i8<QT, 32, DC, 1>(fu, lane & 31, nsub, xs, rbytes, tok, 1, tab, au);
+  GM_TL_MARK2(au[0]);
   const float hv = gm_silu(row_sum<32>(ag[0])) * row_sum<32>(au[0]);
   if (live && (lane & 31) == 0) h[(int64_t)pair * FF + row] = hv;
+  GM_TL_END(1);
 }
 
 // One block: the router logits of every token from the partial sums of
 // k_dec_router_ks (fixed order), times the token's RMSNorm factor
 // 1 / sqrt(mean(x^2) + eps) (qwen/forward.py:58-61), + bias; the shared gate
 // sigmoid; the top-k (wave t -> token t) and the grouping table.
-template <int MAXV>
+template <int MAXV, int NZ>
 __global__ void __launch_bounds__(512) k_dec_route(gm_moe_layer P, const float* __restrict__ part,
                                                    const float* __restrict__ ssq, int nz, int ldp, int T,
                                                    float* __restrict__ rmsv, float* __restrict__ logits,
@@ -105,11 +109,11 @@ __global__ void __launch_bounds__(512) k_dec_route(gm_moe_layer P, const float* 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = P.E, k = P.k;
   if (wave < T) {
-    // every partial is loaded before any is summed (nz <= 8; a load in a
+    // every partial is loaded before any is summed (nz <= NZ; a load in a
     // runtime loop would wait before the next one is issued)
-    float pv[MAXV][8], ps[8], pg[8];
+    float pv[MAXV][NZ], ps[NZ], pg[NZ];
 #pragma unroll
-    for (int z = 0; z < 8; ++z) {
+    for (int z = 0; z < NZ; ++z) {
       const int zz = z < nz ? z : nz - 1;
       const float* pz = part + ((int64_t)zz * T + wave) * ldp;
 #pragma unroll
@@ -124,7 +128,7 @@ __global__ void __launch_bounds__(512) k_dec_route(gm_moe_layer P, const float* 
     if (P.norm_w) {
       float q = 0.f;
 #pragma unroll
-      for (int z = 0; z < 8; ++z) q += z < nz ? ps[z] : 0.f;
+      for (int z = 0; z < NZ; ++z) q += z < nz ? ps[z] : 0.f;
       rms = 1.0f / sqrtf(q / (float)P.D + P.norm_eps);
     }
     if (lane == 0) rmsv[wave] = rms;
@@ -136,14 +140,14 @@ __global__ void __launch_bounds__(512) k_dec_route(gm_moe_layer P, const float* 
       const int r = ix[i] < E ? ix[i] : E - 1;
       float a = 0.f;
 #pragma unroll
-      for (int z = 0; z < 8; ++z) a += z < nz ? pv[i][z] : 0.f;
+      for (int z = 0; z < NZ; ++z) a += z < nz ? pv[i][z] : 0.f;
       v[i] = rms * a + (P.router_bias ? P.router_bias[r] : 0.f);
       if (ix[i] < E) logits[(int64_t)wave * E + ix[i]] = v[i];
     }
     if (P.sh_gate_inp && lane == 0) {
       float a = 0.f;
 #pragma unroll
-      for (int z = 0; z < 8; ++z) a += z < nz ? pg[z] : 0.f;
+      for (int z = 0; z < NZ; ++z) a += z < nz ? pg[z] : 0.f;
       shg[wave] = gm_sigmoid(rms * a);
     }
     int id;
@@ -293,20 +297,19 @@ int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const Gm
     const uint8_t* xl = P->gate_sh ? a.xl : nullptr;           // written by the router kernel's shared blocks
     if (P->E <= 256)
       hipLaunchKernelGGL((k_dec_gateup1<QT, DC, 4>), dim3(P->k * n_chunks), dim3(256), smem, s, *P, x, a.logits,
-                         a.ids, a.wts, a.grp, a.h, n_chunks, xl);
+                         a.ids, a.wts, a.grp, a.h, n_chunks, xl GM_TL_ARG(a.tl));
     else
       hipLaunchKernelGGL((k_dec_gateup1<QT, DC, 8>), dim3(P->k * n_chunks), dim3(256), smem, s, *P, x, a.logits,
-                         a.ids, a.wts, a.grp, a.h, n_chunks, xl);
+                         a.ids, a.wts, a.grp, a.h, n_chunks, xl GM_TL_ARG(a.tl));
     GM_TRY(hipGetLastError());
     return GM_OK;
   }
-  const int nz = P->D / (P->D < 512 ? P->D : 512);
-  if (P->E <= 256)
-    hipLaunchKernelGGL(k_dec_route<4>, dim3(1), dim3(512), 0, s, *P, a.part, a.ssq, nz, gm_dec_part_ld(P), T,
-                       a.rms, a.logits, a.shg, a.ids, a.wts, a.grp);
-  else
-    hipLaunchKernelGGL(k_dec_route<8>, dim3(1), dim3(512), 0, s, *P, a.part, a.ssq, nz, gm_dec_part_ld(P), T,
-                       a.rms, a.logits, a.shg, a.ids, a.wts, a.grp);
+  const int nz = gm_dec_nz(P->D);                                  // <= GM_DEC_MAX_NZ for D <= 4096
+  if (nz > GM_DEC_MAX_NZ) return gm_fail_arg("gm_moe_forward: D=%d needs more than %d router ranges", P->D, GM_DEC_MAX_NZ);
+  auto route = nz <= 8 ? (P->E <= 256 ? k_dec_route<4, 8> : k_dec_route<8, 8>)
+                       : (P->E <= 256 ? k_dec_route<4, 16> : k_dec_route<8, 16>);
+  hipLaunchKernelGGL(route, dim3(1), dim3(512), 0, s, *P, a.part, a.ssq, nz, gm_dec_part_ld(P), T, a.rms, a.logits,
+                     a.shg, a.ids, a.wts, a.grp);
   GM_TRY(hipGetLastError());
   const int n_rg = (P->FF + 8 * kGuPasses - 1) / (8 * kGuPasses);  // blocks per unit
   const int n_sh = P->gate_sh ? n_rg : 0;

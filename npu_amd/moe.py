@@ -115,7 +115,7 @@ class GpuMoeBlock:
         s.q_down_sh = self.q_down_sh
         s.D, s.FF, s.FF_sh, s.E, s.k = self.D, self.FF, self.FF if self.gate_sh is not None else 0, self.E, self.k
         self.struct = s
-        self._ws: dict[int, torch.Tensor] = {}
+        self._ws: torch.Tensor | None = None
 
     def _check_shapes(self) -> None:
         D, FF, E = self.D, self.FF, self.E
@@ -147,12 +147,15 @@ class GpuMoeBlock:
 
     # ------------------------------------------------------------------
     def workspace(self, T: int) -> torch.Tensor:
-        ws = self._ws.get(T)
-        if ws is None:
-            n = ops.moe_workspace_bytes(self.struct, T)
-            ws = torch.zeros(n, dtype=torch.uint8, device=self.gate.device)
-            self._ws[T] = ws
-        return ws
+        """The block's one workspace, grown (never shrunk) to the largest T seen.  Offsets
+        inside it are recomputed from T on every call, so every smaller T reuses it.  A
+        call with a larger T replaces the buffer: graphs captured before then hold the
+        old one and must be captured again."""
+        n = ops.moe_workspace_bytes(self.struct, T)
+        if self._ws is None or self._ws.numel() < n:
+            self._ws = None                      # release the old buffer before allocating
+            self._ws = torch.zeros(n, dtype=torch.uint8, device=self.gate.device)
+        return self._ws
 
     def forward(self, x: torch.Tensor, *, residual: bool = False, out: torch.Tensor | None = None,
                 stage: int = 0, path: str = "auto") -> torch.Tensor:

@@ -178,6 +178,35 @@ def device_bf16_normal(gen: torch.Generator, shape, std: float, device="cuda") -
     return (torch.randn(shape, device=device, generator=gen) * std).to(torch.bfloat16)
 
 
+CONFIG5 = dict(D=2048, FF=512, E=256, k=8)
+
+
+def device_config5_layers(n_layers: int, device, seed: int):
+    """``n_layers`` BASELINE config-5 blocks generated on the device: IQ4_XS gate/up and
+    IQ3_XXS down experts (E=256, D=2048, FF=512), a shared expert in the same formats,
+    bf16 router and shared gate N(0, 0.02), RMSNorm weight 1, eps 1e-6."""
+    from npu_amd.moe import GpuMoeBlock
+    D, FF, E, k = CONFIG5["D"], CONFIG5["FF"], CONFIG5["E"], CONFIG5["k"]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    layers = []
+    for _ in range(n_layers):
+        gate = device_quant_matrix(gen, QT.IQ4_XS, FF, D, E, device)
+        up = device_quant_matrix(gen, QT.IQ4_XS, FF, D, E, device)
+        down = device_quant_matrix(gen, QT.IQ3_XXS, D, FF, E, device)
+        router = device_bf16_normal(gen, (E, D), ROUTER_STD, device)
+        gate_sh = device_quant_matrix(gen, QT.IQ4_XS, FF, D, None, device)
+        up_sh = device_quant_matrix(gen, QT.IQ4_XS, FF, D, None, device)
+        down_sh = device_quant_matrix(gen, QT.IQ3_XXS, D, FF, None, device)
+        sh_inp = device_bf16_normal(gen, (D,), ROUTER_STD, device)
+        norm_w = torch.ones(D, dtype=torch.float32, device=device)
+        layers.append(GpuMoeBlock(gate=gate, up=up, down=down, router=router, q_gate=QT.IQ4_XS,
+                                  q_down=QT.IQ3_XXS, D=D, FF=FF, E=E, k=k, gate_sh=gate_sh, up_sh=up_sh,
+                                  down_sh=down_sh, sh_gate_inp=sh_inp, norm_w=norm_w, norm_eps=1e-6,
+                                  device=device))
+    return layers
+
+
 # ------------------------------------------------------------------ files
 def write_gguf_model(path, layers, *, arch: str = "qwen3next", rms_eps: float = 1e-6) -> None:
     """A GGUF file holding the MoE tensors of `layers` (``HostMoeLayer``) under the model's

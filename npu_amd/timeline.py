@@ -1,0 +1,148 @@
+"""Per-block timeline of the decode kernels over a chain of config-5 blocks.
+
+The profiling build (``python -m npu_amd.build --timeline`` -> libnpu_amd_tl.so)
+has every decode kernel write, from thread 0 of each block, the chip-wide
+100 MHz ``s_memrealtime`` counter at block entry, at two kernel-specific marks
+and at the end, into the layer's own workspace (csrc/timeline.h).  This script
+replays the config-5 chain (40 blocks, T = 1 or 8, hipGraph, as bench.py does)
+and summarises, per kernel and relative to the start of each block's first
+kernel: when blocks enter, reach each mark and end, and the gaps between the
+last block of one kernel ending and the first block of the next entering.
+
+    python -m npu_amd.build --timeline
+    NPU_AMD_LIB=timeline python -m npu_amd.timeline [--layers 40] [--T 1] [--out FILE]
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import statistics
+import sys
+
+os.environ.setdefault("NPU_AMD_LIB", "timeline")
+
+TICK_US = 0.01            # s_memrealtime runs at 100 MHz
+N_SLOTS, MAXB, REC = 4, 1024, 8
+SEED = 20261201
+
+
+def _layer_records(blk, T: int):
+    """[slot] -> list of (entry, mark1, mark2, end, hwid) for the blocks that wrote one."""
+    import torch
+    from npu_amd import ops
+    need = ops.moe_workspace_bytes(blk.struct, T)
+    nbytes = N_SLOTS * MAXB * REC * 8
+    raw = blk.workspace(T)[need - nbytes:need].view(torch.int64).view(N_SLOTS, MAXB, REC).cpu().numpy()
+    out = []
+    for s in range(N_SLOTS):
+        rows = raw[s]
+        out.append([tuple(int(v) for v in r[:5]) for r in rows if r[0] != 0])
+    return out
+
+
+def _zero_records(blk, T: int) -> None:
+    from npu_amd import ops
+    need = ops.moe_workspace_bytes(blk.struct, T)
+    blk.workspace(T)[need - N_SLOTS * MAXB * REC * 8:need].zero_()
+
+
+def run(n_layers: int, T: int, replays: int):
+    import torch
+    from npu_amd import _lib, synth
+    if not _lib.LIB_PATH.name.endswith("_tl.so"):
+        raise RuntimeError("set NPU_AMD_LIB=timeline (the timestamped build) before importing npu_amd")
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    layers = synth.device_config5_layers(n_layers, dev, SEED)
+    D = layers[0].D
+    x0 = torch.from_numpy(synth.host_input(SEED, T, D, rmsnorm=False)).to(dev)
+    bufs = [x0.clone(), torch.empty_like(x0)]
+    for i, blk in enumerate(layers):
+        blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i, blk in enumerate(layers):
+            blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
+    for _ in range(replays):
+        g.replay()
+    torch.cuda.synchronize()
+    for blk in layers:
+        _zero_records(blk, T)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    return [_layer_records(blk, T) for blk in layers]
+
+
+def summarise(recs, names):
+    """Per kernel slot: medians over the inner layers of block-level statistics (us)."""
+    inner = recs[1:-1] if len(recs) > 2 else recs
+    stats = {}
+    gaps_in, gaps_between = {}, []
+    for li, layer in enumerate(inner):
+        slots = [s for s in range(N_SLOTS) if layer[s]]
+        t0 = min(r[0] for r in layer[slots[0]])
+        for s in slots:
+            rs = layer[s]
+            e = sorted(r[0] for r in rs)
+            m1 = sorted(r[1] for r in rs)
+            m2 = sorted(r[2] for r in rs)
+            en = sorted(r[3] for r in rs)
+            d = {"blocks": len(rs), "entry_first": e[0] - t0, "entry_median": e[len(e) // 2] - t0,
+                 "entry_last": e[-1] - t0, "mark1_median": m1[len(m1) // 2] - t0, "mark1_last": m1[-1] - t0,
+                 "mark2_median": m2[len(m2) // 2] - t0, "mark2_last": m2[-1] - t0,
+                 "end_median": en[len(en) // 2] - t0, "end_last": en[-1] - t0,
+                 "block_median": sorted(r[3] - r[0] for r in rs)[len(rs) // 2],
+                 "xccs": len({r[4] >> 32 for r in rs})}
+            for kk, v in d.items():
+                stats.setdefault(s, {}).setdefault(kk, []).append(v)
+        for a, b in zip(slots, slots[1:]):
+            gaps_in.setdefault((a, b), []).append(min(r[0] for r in layer[b]) - max(r[3] for r in layer[a]))
+        nxt = recs[li + 2] if len(recs) > 2 else None
+        if nxt is not None:
+            ns = [s for s in range(N_SLOTS) if nxt[s]]
+            gaps_between.append(min(r[0] for r in nxt[ns[0]]) - max(r[3] for r in layer[slots[-1]]))
+    med = lambda v: statistics.median(v) * TICK_US
+    lines = ["| kernel | blocks | XCDs | entry first / median / last | mark 1 median / last | "
+             "mark 2 median / last | end median / last | block duration (median) |",
+             "|---|---|---|---|---|---|---|---|"]
+    for s, d in stats.items():
+        lines.append(
+            f"| {names.get(s, s)} | {int(statistics.median(d['blocks']))} | {int(statistics.median(d['xccs']))} | "
+            f"{med(d['entry_first']):.2f} / {med(d['entry_median']):.2f} / {med(d['entry_last']):.2f} | "
+            f"{med(d['mark1_median']):.2f} / {med(d['mark1_last']):.2f} | "
+            f"{med(d['mark2_median']):.2f} / {med(d['mark2_last']):.2f} | "
+            f"{med(d['end_median']):.2f} / {med(d['end_last']):.2f} | {med(d['block_median']):.2f} |")
+    lines.append("")
+    for (a, b), v in gaps_in.items():
+        lines.append(f"- gap {names.get(a, a)} last end -> {names.get(b, b)} first entry: {med(v):.2f} us (median)")
+    if gaps_between:
+        lines.append(f"- gap last kernel of block l -> first kernel of block l+1: {med(gaps_between):.2f} us (median)")
+    per_block = [min(r[0] for r in nxt[[s for s in range(N_SLOTS) if nxt[s]][0]]) -
+                 min(r[0] for r in cur[[s for s in range(N_SLOTS) if cur[s]][0]])
+                 for cur, nxt in zip(recs[1:-1], recs[2:])]
+    if per_block:
+        lines.append(f"- block period (first entry to next block's first entry): {med(per_block):.2f} us (median)")
+    return "\n".join(lines)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--T", type=int, default=1)
+    ap.add_argument("--replays", type=int, default=5)
+    ap.add_argument("--out", default=None, help="also write the summary to this file")
+    args = ap.parse_args()
+    recs = run(args.layers, args.T, args.replays)
+    names = {0: "router (stage 1)", 1: "gate/up (stage 2)", 2: "down (stage 3)", 3: "extra"}
+    text = summarise(recs, names)
+    print(text)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(text + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

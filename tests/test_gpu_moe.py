@@ -31,12 +31,16 @@ def _check(gpu, h, T, residual=False, seed=5, rmsnorm_input=True, tol=REL_TOL):
     ref = OM.block_forward(x, ol, residual=residual, stages=st)
     margin = OM.topk_margin(OM.router_logits64(x, ol), h.k)
     clear = margin > 1e-5
+    # Near-ties (k-th / (k+1)-th logit closer than 1e-5, where fp32 rounding may
+    # swap the picks) are about 1 in 6,000 tokens at these shapes; every case here
+    # uses a fixed seed with none, so the id and output checks always run in full.
+    assert bool(clear.all()), f"{int((~clear).sum())} near-tie token(s): choose another seed"
     ids_gpu = st_gpu["topk_ids"].long()
-    assert torch.equal(ids_gpu[clear], st["topk_ids"][clear]), "top-k ids differ"
-    if bool(clear.all()):
-        assert OM.rel_err(y, ref) <= tol, OM.rel_err(y, ref)
+    assert torch.equal(ids_gpu, st["topk_ids"]), "top-k ids differ"
+    rel = OM.rel_err(y, ref)
+    assert rel <= tol, rel
     assert torch.equal(y, y2), "repeat calls must be bit-identical"
-    return OM.rel_err(y, ref)
+    return rel
 
 
 @pytest.mark.parametrize("T", [1, 2, 8])
@@ -151,3 +155,18 @@ def test_size_limits(gpu, D, FF, E, k, T):
     D up to 4096 (4 weight chunks per lane), FF up to 2048 (the general path at T = 1)."""
     h = synth.host_moe_layer(100 + k, D=D, FF=FF, E=E, k=k, norm=True)
     _check(gpu, h, T, residual=True, seed=T, rmsnorm_input=False)
+
+
+@pytest.mark.parametrize("D", [768, 1280])
+@pytest.mark.parametrize("T,FF", [(1, 512), (1, 768), (2, 256), (8, 256)])
+def test_d_not_multiple_of_512(gpu, D, T, FF):
+    """D a multiple of 256 but not of 512: the router partials of the general decode path
+    (T > 1, and T = 1 with FF = 768) run over 256-wide K ranges, D / 256 of them."""
+    h = synth.host_moe_layer(140 + D // 256 + T, D=D, FF=FF, E=32, k=4, norm=True)
+    _check(gpu, h, T, residual=True, seed=T, rmsnorm_input=False)
+
+
+def test_fifteen_router_ranges(gpu):
+    """D = 3840: fifteen 256-wide router ranges, the 16-partial routing kernel."""
+    h = synth.host_moe_layer(150, D=3840, FF=256, E=16, k=4, norm=True)
+    _check(gpu, h, 8, residual=True, seed=3, rmsnorm_input=False)

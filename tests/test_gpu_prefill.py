@@ -105,10 +105,14 @@ def test_prefill_path_at_decode_sizes(gpu, T):
         assert OM.rel_err(yp, yd) <= REL_TOL
 
 
-@pytest.mark.parametrize("D,FF,E,k,T", [(256, 256, 512, 8, 40), (4096, 256, 16, 4, 20), (256, 1024, 8, 2, 24)])
+@pytest.mark.parametrize("D,FF,E,k,T", [(256, 256, 512, 8, 40), (4096, 256, 16, 4, 20), (256, 1024, 8, 2, 24),
+                                        (2304, 256, 64, 4, 20), (2304, 256, 320, 8, 24), (8192, 256, 16, 4, 12),
+                                        (8192, 256, 260, 8, 9)])
 def test_prefill_size_limits(gpu, D, FF, E, k, T):
     """Prefill at the limits it accepts: E = 512 (dispatch histogram width, 8-per-lane top-k),
-    D = 4096, FF = 1024 (the 4-superblock h tile of the down kernel)."""
+    D = 4096, FF = 1024 (the 4-superblock h tile of the down kernel); D = 2304 (nine
+    256-wide router ranges) and D = 8192 (sixteen 512-wide ranges, the prep kernel's
+    two-pass branch for D > 4096), each with E <= 256 and E > 256."""
     h = synth.host_moe_layer(110 + k, D=D, FF=FF, E=E, k=k, bias=True)
     _check(gpu, h, T, seed=k)
 
