@@ -47,7 +47,7 @@ extern "C" {
 /* Message for the last failing call on this thread ("" if none). */
 const char* gm_last_error(void);
 
-/* ABI version (bumped on any signature change). */
+/* ABI version (bumped on any signature or struct change). */
 int gm_abi_version(void);
 
 /*

@@ -228,12 +228,26 @@ __device__ __forceinline__ void gm_iq3_tab_store(uint32_t g, Iq3Tab* __restrict_
   }
 }
 
+// Sign byte masks of a 7-bit ksigns index computed in registers: the byte
+// with the parity bit (bit 7) is s = idx | (popcount(idx) & 1) << 7; byte i
+// of o0 / o1 is bit i / i + 4 of s (the multiply spreads 4 bits to the low
+// bit of 4 bytes without carries), and m0 / m1 are those bytes times 0xff.
+// The same values as Iq3Tab::sgn[idx], for kernels where LDS traffic, not
+// VALU issue, is the limit.
+__device__ __forceinline__ gm_u32x4 gm_iq3_sign_masks(uint32_t idx7) {
+  const uint32_t s = idx7 | ((__builtin_popcount(idx7) & 1u) << 7);
+  const uint32_t o0 = ((s & 15u) * 0x00204081u) & 0x01010101u;
+  const uint32_t o1 = ((s >> 4) * 0x00204081u) & 0x01010101u;
+  return gm_u32x4{o0 * 0xffu, o1 * 0xffu, o0, o1};
+}
+
 // Signed int8 weights of one sub-block in k order (byte i of w[c] is weight
 // 4c + i) and the sub-block scale: weight[k] == scale * int8 exactly.
 //   IQ4_XS: kvalues (npu/quant_mv_iq4.py:194-197), scale d (ls - 32);
 //   IQ3_XXS: +-grid magnitude (<= 62, never 0, so the byte negation
-//            (g ^ 0xff) + 1 cannot carry), scale d (0.5 + s4) / 2.
-template <int QT>
+//            (g ^ 0xff) + 1 cannot carry), scale d (0.5 + s4) / 2; the sign
+//            masks from the LDS table, or computed (ARITH).
+template <int QT, bool ARITH = false>
 __device__ __forceinline__ float gm_decode_i8(const typename RawSub<QT>::T& r, int sub, const Iq3Tab* __restrict__ tab,
                                               uint32_t (&w)[8]) {
   if constexpr (QT == GM_QTYPE_IQ4_XS) {
@@ -254,7 +268,7 @@ __device__ __forceinline__ float gm_decode_i8(const typename RawSub<QT>::T& r, i
     for (int g = 0; g < 4; ++g) {
       const uint32_t qw = (g < 2 ? r.q0 : r.q1) >> (16 * (g & 1));
       const uint32_t ga = tab->grid[qw & 0xffu], gb = tab->grid[(qw >> 8) & 0xffu];
-      const gm_u32x4 m = tab->sgn[(r.w >> (7 * g)) & 127u];
+      const gm_u32x4 m = ARITH ? gm_iq3_sign_masks((r.w >> (7 * g)) & 127u) : tab->sgn[(r.w >> (7 * g)) & 127u];
       w[2 * g] = (ga ^ m.x) + m.z;
       w[2 * g + 1] = (gb ^ m.y) + m.w;
     }

@@ -98,7 +98,7 @@ __device__ __forceinline__ void stage_rows_il(const float* __restrict__ src, int
 // E, renormalised top-k probabilities (qwen/forward.py:609-611).
 // Lane values of one wave's top-k input: logits lane + 64 i (clamped loads,
 // so every lane issues the same MAXV loads; out-of-range entries are masked
-// in topk_finish).
+// by topk_keys).
 template <int MAXV>
 __device__ __forceinline__ void topk_load(const float* __restrict__ lg, int E, float (&v)[MAXV], int (&ix)[MAXV]) {
   const int lane = threadIdx.x & 63;
@@ -109,120 +109,189 @@ __device__ __forceinline__ void topk_load(const float* __restrict__ lg, int E, f
   }
 }
 
-// Float <-> int32 key with the same order (an involution): the top-k runs on
-// integer keys so that every max/min step is one fused DPP instruction.
-__device__ __forceinline__ int fkey(float f) {
-  const int b = __float_as_int(f);
-  return b >= 0 ? b : b ^ 0x7fffffff;
-}
-__device__ __forceinline__ float fkey_inv(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7fffffff); }
-
-__device__ __forceinline__ int wave_min_int_uniform(int v) {
-  v = min(v, GM_DPP_I(v, GM_ROW_ROR8));
-  v = min(v, GM_DPP_I(v, GM_ROW_ROR4));
-  v = min(v, GM_DPP_I(v, GM_QPERM_2301));
-  v = min(v, GM_DPP_I(v, GM_QPERM_1032));
-  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+// Unsigned key with the order of the float values: NaN of either sign is the
+// largest (torch.topk ranks NaN above every number), -0 and +0 are equal, and
+// every value has a key >= 0x007fffff (-inf), so 0 marks an absent entry.
+__device__ __forceinline__ uint32_t ukey(float f) {
+  const uint32_t b = __float_as_uint(f);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;
+  if (b == 0x80000000u) return 0x80000000u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// max(v, lane-shuffled v) in one DPP instruction; lanes the row mask leaves out
-// see INT_MIN, the identity of max, so they keep v.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ int dpp_max_i(int v) {
-  return max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, CTRL, ROWS, 0xF, false));
+// Value back from a key (NaN keys give a NaN, -0 comes back as +0).
+__device__ __forceinline__ float ukey_inv(uint32_t u) {
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
 }
 
-// Wave-wide max: four steps inside each 16-lane row, then row_bcast15 /
-// row_bcast31 carry the row maxima up so that lane 63 holds the total.
-__device__ __forceinline__ int wave_max_int_l63(int v) {
-  v = dpp_max_i<GM_QPERM_1032, 0xF>(v);
-  v = dpp_max_i<GM_QPERM_2301, 0xF>(v);
-  v = dpp_max_i<0x141, 0xF>(v);                 // row_half_mirror
-  v = dpp_max_i<0x140, 0xF>(v);                 // row_mirror
-  v = dpp_max_i<0x142, 0xA>(v);                 // row_bcast15 -> rows 1 and 3
-  v = dpp_max_i<0x143, 0xC>(v);                 // row_bcast31 -> rows 2 and 3
-  return __builtin_amdgcn_readlane(v, 63);
-}
-
-// Selection: each lane sorts its MAXV keys once (descending; the lane's
-// indices ascend, so equal keys keep the lower id first); every round takes
-// the wave-wide largest lane head, the lane holding it (an exact tie between
-// lanes goes to the lower expert id) pops it.  Lane r < k ends with pick r:
-// its expert id (out_id) and key (out_key); skey keeps the sorted keys for
-// topk_weights.  Other lanes get INT_MAX / INT_MIN.
 template <int MAXV>
-__device__ __forceinline__ void topk_select(const float (&v)[MAXV], const int (&ix0)[MAXV], int E, int k,
-                                            int& out_id, int& out_key, int (&skey)[MAXV]) {
-  const int lane = threadIdx.x & 63;
-  int key[MAXV], ix[MAXV];
+__device__ __forceinline__ void topk_keys(const float (&v)[MAXV], const int (&ix)[MAXV], int E, uint32_t (&u)[MAXV]) {
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) u[i] = ix[i] < E ? ukey(v[i]) : 0u;
+}
+
+// Wave-uniform selection: on return bit l of sel[i] is set iff entry
+// lane l + 64 i is one of the k largest keys, exact ties at the k-th value
+// going to the lowest ids.  Bisection over the key bits, most significant
+// first, for a threshold with exactly k keys at or above it: each step is one
+// compare and ballot per value and scalar popcounts, and it stops as soon as
+// such a threshold is found (after about 14 of the 32 steps for random
+// logits).  If the k-th and (k+1)-th keys are equal it ends with the k-th key
+// itself, and the keys equal to it are taken in ascending id order.
+template <int MAXV>
+__device__ __forceinline__ void topk_masks(const uint32_t (&u)[MAXV], int k, uint64_t (&sel)[MAXV]) {
+  uint32_t ans = 0;
+  int cnt = 0x7fffffff;                                  // keys >= ans (once ans > 0)
+  for (uint32_t bit = 0x80000000u; bit != 0u; bit >>= 1) {
+    // the threshold is wave-uniform: readfirstlane keeps it (and the loop) scalar
+    const uint32_t cand = (uint32_t)__builtin_amdgcn_readfirstlane((int)(ans | bit));
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) c += __popcll(__ballot(u[i] >= cand));
+    if (c >= k) {
+      ans = cand;
+      cnt = c;
+      if (c == k) break;
+    }
+  }
+  if (cnt == k) {
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) sel[i] = __ballot(u[i] >= ans);
+    return;
+  }
+  int need = k;
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
-    ix[i] = ix0[i];
-    key[i] = ix[i] < E ? fkey(v[i]) : INT_MIN;
+    sel[i] = __ballot(u[i] > ans);
+    need -= __popcll(sel[i]);
   }
 #pragma unroll
-  for (int a = 0; a < MAXV; ++a)
-#pragma unroll
-    for (int b = MAXV - 1; b > a; --b) {
-      const bool sw = key[b] > key[b - 1];
-      const int tk = key[b], ti = ix[b];
-      key[b] = sw ? key[b - 1] : key[b];
-      ix[b] = sw ? ix[b - 1] : ix[b];
-      key[b - 1] = sw ? tk : key[b - 1];
-      ix[b - 1] = sw ? ti : ix[b - 1];
+  for (int i = 0; i < MAXV; ++i) {
+    uint64_t eq = __ballot(u[i] == ans);
+    while (need > 0 && eq != 0) {
+      const uint64_t low = eq & (~eq + 1ull);
+      sel[i] |= low;
+      eq ^= low;
+      --need;
     }
-#pragma unroll
-  for (int i = 0; i < MAXV; ++i) skey[i] = key[i];
-  int mykey = INT_MIN, myid = 0x7fffffff;
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    if (r >= k) break;
-    const int hm = wave_max_int_l63(key[0]);
-    const uint64_t bal = __ballot(key[0] == hm);
-    int wl = (int)__builtin_ctzll(bal);
-    if (__builtin_expect((bal & (bal - 1)) != 0, 0))
-      wl = wave_min_int_uniform(key[0] == hm ? ix[0] : 0x7fffffff) & 63;
-    const int wi = __builtin_amdgcn_readlane(ix[0], wl);
-    mykey = lane == r ? hm : mykey;
-    myid = lane == r ? wi : myid;
-    const bool pop = lane == wl;
-#pragma unroll
-    for (int i = 0; i + 1 < MAXV; ++i) {
-      key[i] = pop ? key[i + 1] : key[i];
-      ix[i] = pop ? ix[i + 1] : ix[i];
-    }
-    key[MAXV - 1] = pop ? INT_MIN : key[MAXV - 1];
-    ix[MAXV - 1] = pop ? 0x7fffffff : ix[MAXV - 1];
   }
-  out_id = myid;
-  out_key = mykey;
 }
 
-// Renormalised softmax probability of the pick in lane r < k (0 elsewhere):
-// softmax over all E (the normaliser summed over skey, lane-sorted), then
-// p / max(sum of the k picks, 1e-20).  Pick 0 is the maximum logit.
+// Expert id of rank r (0-based, ascending id) among the selected entries
+// (wave-uniform r).
 template <int MAXV>
-__device__ __forceinline__ float topk_weights(const int (&skey)[MAXV], int k, int mykey) {
+__device__ __forceinline__ int topk_rank_id(const uint64_t (&sel)[MAXV], int r) {
+  int id = 0;
+  bool done = false;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int c = __popcll(sel[i]);
+    if (!done && r < c) {
+      uint64_t m = sel[i];
+      for (int j = 0; j < r; ++j) m &= m - 1ull;
+      id = 64 * i + __builtin_ctzll(m);
+      done = true;
+    }
+    if (!done) r -= c;
+  }
+  return id;
+}
+
+// Lane r < k gets the selected entry of rank r (ascending id): its id and key
+// (other lanes: id 0x7fffffff, key 0).
+template <int MAXV>
+__device__ __forceinline__ void topk_gather_rank(const uint64_t (&sel)[MAXV], const uint32_t (&u)[MAXV], int k,
+                                                 int& rid, uint32_t& rkey) {
   const int lane = threadIdx.x & 63;
-  const float m = fkey_inv(__builtin_amdgcn_readlane(mykey, 0));
+  int pre = 0, src = 0, si = 0;
+  bool hit = false;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int c = __popcll(sel[i]);
+    const int j = lane - pre;
+    if (!hit && j >= 0 && j < c) {
+      uint64_t m = sel[i];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) m = t < j ? (m & (m - 1ull)) : m;
+      src = __builtin_ctzll(m);
+      si = i;
+      hit = true;
+    }
+    pre += c;
+  }
+  uint32_t key = 0;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const uint32_t g = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)u[i]);
+    key = si == i ? g : key;
+  }
+  const bool ok = lane < k && hit;
+  rid = ok ? src + 64 * si : 0x7fffffff;
+  rkey = ok ? key : 0u;
+}
+
+// Descending position of each rank's pick: larger keys first, equal keys in
+// ascending id order (lanes r < k; the others get 0x7fffffff).
+__device__ __forceinline__ int topk_slot(int rid, uint32_t rkey, int k) {
+  const int lane = threadIdx.x & 63;
+  int slot = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j < k) {
+      const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)rkey, j);
+      const int ij = __builtin_amdgcn_readlane(rid, j);
+      slot += (kj > rkey || (kj == rkey && ij < rid)) ? 1 : 0;
+    }
+  }
+  return lane < k ? slot : 0x7fffffff;
+}
+
+// Renormalised softmax weight of the pick in lane r < k (key rkey): softmax
+// over all valid entries (maximum = the largest selected key), then
+// p / max(sum of the k picks, 1e-20).  Other lanes return 0.
+template <int MAXV>
+__device__ __forceinline__ float topk_rank_weight(const uint32_t (&u)[MAXV], uint32_t rkey, int k) {
+  const int lane = threadIdx.x & 63;
+  uint32_t mk = lane < k ? rkey : 0u;
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) {
+    const uint32_t t = (uint32_t)__shfl_xor((int)mk, o, 64);
+    mk = t > mk ? t : mk;
+  }
+  const float m = ukey_inv((uint32_t)__builtin_amdgcn_readfirstlane((int)mk));
   float z = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXV; ++i)
-    if (skey[i] != INT_MIN) z += expf(fkey_inv(skey[i]) - m);
+    if (u[i] != 0u) z += expf(ukey_inv(u[i]) - m);
   z = gm_wave_sum64(z);
-  const float p = lane < k ? expf(fkey_inv(mykey) - m) / z : 0.f;
+  const float p = lane < k ? expf(ukey_inv(rkey) - m) / z : 0.f;
   const float den = fmaxf(gm_wave_sum64(p), 1e-20f);
   return p / den;
 }
 
-// Both: lane r < k ends with pick r's expert id and renormalised weight.
+// Lane s < k ends with pick s in descending order: its expert id and
+// renormalised weight (other lanes: id 0x7fffffff, weight 0).
 template <int MAXV>
 __device__ __forceinline__ void topk_finish(const float (&v)[MAXV], const int (&ix)[MAXV], int E, int k,
                                             int& out_id, float& out_w) {
-  int key, skey[MAXV];
-  topk_select<MAXV>(v, ix, E, k, out_id, key, skey);
-  out_w = topk_weights<MAXV>(skey, k, key);
+  const int lane = threadIdx.x & 63;
+  uint32_t u[MAXV];
+  uint64_t sel[MAXV];
+  topk_keys<MAXV>(v, ix, E, u);
+  topk_masks<MAXV>(u, k, sel);
+  int rid;
+  uint32_t rkey;
+  topk_gather_rank<MAXV>(sel, u, k, rid, rkey);
+  const int slot = topk_slot(rid, rkey, k);
+  const float w = topk_rank_weight<MAXV>(u, rkey, k);
+  int src = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j < k) src = __builtin_amdgcn_readlane(slot, j) == lane ? j : src;
+  const int id = __builtin_amdgcn_ds_bpermute(src << 2, rid);
+  const float wt = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(w)));
+  out_id = lane < k ? id : 0x7fffffff;
+  out_w = lane < k ? wt : 0.f;
 }
 
 template <int MAXV>
@@ -513,7 +582,7 @@ __device__ __forceinline__ void copy_limbs_wave(const uint8_t* __restrict__ src,
 // acc[m] += W_row . act[idx[m]] over the fetched sub-blocks, m < nt; act rows
 // are limb rows of row_bytes bytes.  BF16 weights (a shared expert kept in
 // bf16) take the activations back to fp32 from their limbs.
-template <int QT, int LR, int SPL, int NT>
+template <int QT, int LR, int SPL, int NT, bool ARITH = false>
 __device__ __forceinline__ void dot_subs_i8(const RowFetch<QT, SPL>& f, int lir, int nsub,
                                             const uint8_t* __restrict__ act, int row_bytes, const int (&idx)[NT],
                                             int nt, const Iq3Tab* __restrict__ tab, float (&acc)[NT]) {
@@ -546,7 +615,7 @@ __device__ __forceinline__ void dot_subs_i8(const RowFetch<QT, SPL>& f, int lir,
         }
       } else {
         uint32_t w[8];
-        const float ws = gm_decode_i8<QT>(f.r[i], sub, tab, w);
+        const float ws = gm_decode_i8<QT, ARITH>(f.r[i], sub, tab, w);
 #pragma unroll
         for (int m = 0; m < NT; ++m) {
           if (m < nt) {

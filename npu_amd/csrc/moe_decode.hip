@@ -1,14 +1,15 @@
 // MoE block, decode path (T <= 8 tokens).  Reference semantics:
 // qwen/forward.py:563-665 (moe_forward).
 //
-// Stage 1  T = 1: k_dec_router: router logits (bf16 W, fp32 RMSNorm'd x), the
-//                         shared scalar gate, and the shared expert's gate/up +
-//                         SwiGLU; none of it depends on the routing.
+// Stage 1  T = 1: k_dec_router1: router logits (bf16 W, fp32 RMSNorm'd x), the
+//                         shared scalar gate and the limb row of the RMSNorm'd
+//                         x for the gate/up kernel.
 //          T > 1: k_dec_router_ks: partial router dot products over K ranges
 //                         (the routing kernel of stage 2 sums them and applies
 //                         the RMSNorm factor); the shared expert runs with the
 //                         routed ones.
-// Stage 2  (moe_decode_gu.hip) top-k, expert grouping, routed gate/up + SwiGLU.
+// Stage 2  (moe_decode_gu.hip) top-k, expert grouping, routed gate/up + SwiGLU
+//                         (T = 1: also the shared expert's gate/up).
 // Stage 3  (moe_decode_dn.hip) down projections, weighted combine in ascending
 //                         expert order, + sigmoid-gated shared expert (+ x).
 //
@@ -22,88 +23,76 @@ using namespace gm_moe;
 
 namespace {
 
-// Blocks [0, n_rb): one router row per wave (64 lanes; row E is the shared
-// scalar gate).  Blocks [n_rb, ...): two shared gate/up rows per wave (32 lanes
-// per row); block n_rb also writes its limb rows of the RMSNorm'd x to xl_out
-// (when set) for the gate/up kernel.  DC = ceil(D / 1024).
-template <int QTS, int NT, int DC>
-__global__ void __launch_bounds__(256) k_dec_router(gm_moe_layer P, const float* __restrict__ x, int T,
-                                                    float* __restrict__ logits, float* __restrict__ shg,
-                                                    float* __restrict__ hsh, int n_rb, uint8_t* __restrict__ xl_out GM_TL_PARAM) {
-  constexpr int SPLR = DC > 1 ? DC / 2 : 1;
-  constexpr bool IQ3 = QTS == GM_QTYPE_IQ3_XXS;
-  extern __shared__ float smem[];
-  float* xs = smem;                                            // NT interleaved rows of D (+ 4)
-  float* red = smem + NT * P.D + 4;                            // [4 * NT]
-  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(red + 4 * NT);       // IQ3 shared expert only
-  const int D = P.D, E = P.E, nsub = D / GM_SUB;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+// T = 1: one router row per wave (row E: the shared scalar gate), two waves per
+// block, no LDS and no barrier.  Lane l of a wave holds x, the RMSNorm weight
+// and the row at k = 512 i + 8 l .. +7 for the NCH = ceil(D / 512) chunks i;
+// all of them are loaded before anything waits, so the row costs one round
+// trip.  Every wave sums x^2 over its own copy of x, so the RMSNorm factor
+// rms = 1 / sqrt(mean(x^2) + eps) (qwen/forward.py:58-61) needs no block
+// reduction; it scales the finished dot product W . (x * w_norm).  Global waves
+// i < NCH also write chunk i of the limb row of xn = (x * rms) * w_norm that
+// the gate/up kernel multiplies with.
+template <int NCH>
+__global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float* __restrict__ x,
+                                                     float* __restrict__ logits, float* __restrict__ shg,
+                                                     uint8_t* __restrict__ xl_out GM_TL_PARAM) {
   GM_TL_BEGIN();
-  int tok[NT];
+  const int lane = threadIdx.x & 63, gw = blockIdx.x * 2 + (threadIdx.x >> 6);
+  const int D = P.D, E = P.E, nrows = E + (P.sh_gate_inp != nullptr ? 1 : 0);
+  const int row = gw < nrows ? gw : nrows - 1;                  // spare waves redo the last row
+  const uint16_t* wr = row < E ? P.router + (int64_t)row * D : P.sh_gate_inp;
+  gm_u32x4 wb[NCH];
+  gm_f32x4 xa[NCH], xb[NCH], na[NCH], nb[NCH];
 #pragma unroll
-  for (int m = 0; m < NT; ++m) tok[m] = m;
-  XRegs<NT, DC> xr;
-  load_x<NT, DC>(xr, x, tok, T, D, P.norm_w);
-  uint32_t gw = 0;
-  if constexpr (IQ3) gw = gm_iq3_tab_load();
-  if ((int)blockIdx.x < n_rb) {
-    const int row = blockIdx.x * 4 + wave;
-    const int nrows = E + (P.sh_gate_inp != nullptr ? 1 : 0);
-    const uint8_t* wr = row < E ? reinterpret_cast<const uint8_t*>(P.router) + (int64_t)row * D * 2
-                                : reinterpret_cast<const uint8_t*>(row < nrows ? P.sh_gate_inp : P.router);
-    RowFetch<GM_QTYPE_BF16, SPLR> f;
-    fetch_subs<GM_QTYPE_BF16, 64, SPLR, true>(f, wr, lane, nsub);
-    issue_fence();
-    stage_x_regs<NT, DC>(xr, T, D, P.norm_w, P.norm_eps, xs, red);
-    GM_TL_MARK1(xs[0]);
-    float acc[NT];
+  for (int i = 0; i < NCH; ++i) {
+    const int kk = 512 * i + 8 * lane < D ? 512 * i + 8 * lane : D - 8;   // lanes past D re-read the end
+    wb[i] = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(wr + kk));
+    xa[i] = *reinterpret_cast<const gm_f32x4*>(x + kk);
+    xb[i] = *reinterpret_cast<const gm_f32x4*>(x + kk + 4);
+    if (P.norm_w) {
+      na[i] = *reinterpret_cast<const gm_f32x4*>(P.norm_w + kk);
+      nb[i] = *reinterpret_cast<const gm_f32x4*>(P.norm_w + kk + 4);
+    } else {
+      na[i] = gm_f32x4{1.f, 1.f, 1.f, 1.f};
+      nb[i] = na[i];
+    }
+  }
+  const float bias = P.router_bias != nullptr && row < E ? P.router_bias[row] : 0.f;
+  float dot = 0.f, ss = 0.f;
 #pragma unroll
-    for (int m = 0; m < NT; ++m) acc[m] = 0.f;
-    dot_subs<GM_QTYPE_BF16, 64, SPLR, NT>(f, lane, nsub, xs, D, tok, T, nullptr, acc);
-    GM_TL_MARK2(acc[0]);
+  for (int i = 0; i < NCH; ++i) {
+    if (512 * i + 8 * lane < D) {
+      const float xv[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
+      const float nv[8] = {na[i].x, na[i].y, na[i].z, na[i].w, nb[i].x, nb[i].y, nb[i].z, nb[i].w};
+      const uint32_t wv[4] = {wb[i].x, wb[i].y, wb[i].z, wb[i].w};
 #pragma unroll
-    for (int m = 0; m < NT; ++m) acc[m] = gm_wave_sum64(acc[m]);
-    if (row < nrows && lane == 0) {
-#pragma unroll
-      for (int m = 0; m < NT; ++m) {
-        if (m < T) {
-          if (row < E) logits[m * E + row] = acc[m] + (P.router_bias ? P.router_bias[row] : 0.f);
-          else shg[m] = gm_sigmoid(acc[m]);
-        }
+      for (int j = 0; j < 8; ++j) {
+        const float w = (j & 1) ? __uint_as_float(wv[j >> 1] & 0xffff0000u) : __uint_as_float(wv[j >> 1] << 16);
+        dot = fmaf(w, xv[j] * nv[j], dot);
+        ss = fmaf(xv[j], xv[j], ss);
       }
     }
-    GM_TL_END(0);
-    return;
   }
-  if constexpr (IQ3) gm_iq3_tab_store(gw, tab);                // visible after stage_x_regs' barrier
-  const int FFs = P.FF_sh;
-  const int64_t rb = gm_row_bytes(QTS, D);
-  const int row = ((blockIdx.x - n_rb) * 4 + wave) * 2 + (lane >> 5);
-  const bool live = row < FFs;
-  const int r = live ? row : 0;
-  RowFetch<QTS, DC> fg, fu;
-  fetch_subs<QTS, 32, DC, true>(fg, static_cast<const uint8_t*>(P.gate_sh) + r * rb, lane & 31, nsub);
-  fetch_subs<QTS, 32, DC, true>(fu, static_cast<const uint8_t*>(P.up_sh) + r * rb, lane & 31, nsub);
-  issue_fence();
-  uint8_t* xl = reinterpret_cast<uint8_t*>(xs);                // limb rows (fit in the fp32 rows' space)
-  stage_limbs_regs<NT, DC>(xr, T, D, P.norm_w, P.norm_eps, xl, red);
-  GM_TL_MARK1(xl[0]);
-  float ag[NT], au[NT];
-#pragma unroll
-  for (int m = 0; m < NT; ++m) { ag[m] = 0.f; au[m] = 0.f; }
-  const int rbytes = gm_limb_row_bytes(D);
-  dot_subs_i8<QTS, 32, DC, NT>(fg, lane & 31, nsub, xl, rbytes, tok, T, tab, ag);
-  dot_subs_i8<QTS, 32, DC, NT>(fu, lane & 31, nsub, xl, rbytes, tok, T, tab, au);
-  GM_TL_MARK2(au[0]);
-#pragma unroll
-  for (int m = 0; m < NT; ++m) {
-    const float hv = gm_silu(row_sum<32>(ag[m])) * row_sum<32>(au[m]);
-    if (live && (lane & 31) == 0 && m < T) hsh[m * FFs + row] = hv;
+  GM_TL_MARK1(dot);
+  dot = gm_wave_sum64(dot);
+  ss = gm_wave_sum64(ss);
+  const float rms = P.norm_w != nullptr ? 1.0f / sqrtf(ss / (float)D + P.norm_eps) : 1.0f;
+  GM_TL_MARK2(rms);
+  if (gw < nrows && lane == 0) {
+    if (row < E) logits[row] = rms * dot + bias;
+    else shg[0] = gm_sigmoid(rms * dot);
   }
-  if (xl_out != nullptr && (int)blockIdx.x == n_rb) {         // the limb rows for the gate/up kernel
-    const gm_u32x4* src = reinterpret_cast<const gm_u32x4*>(xl);
-    gm_u32x4* dst = reinterpret_cast<gm_u32x4*>(xl_out);
-    for (int c = threadIdx.x; c < NT * (rbytes >> 4); c += 256) dst[c] = src[c];
+  if (xl_out != nullptr && gw < NCH && 512 * gw < D) {          // uniform per wave
+    const int i = gw;
+    gm_f32x4 a = xa[0], b = xb[0], wa = na[0], wb2 = nb[0];
+#pragma unroll
+    for (int q = 1; q < NCH; ++q)
+      if (q == i) { a = xa[q]; b = xb[q]; wa = na[q]; wb2 = nb[q]; }
+    a.x = (a.x * rms) * wa.x; a.y = (a.y * rms) * wa.y; a.z = (a.z * rms) * wa.z; a.w = (a.w * rms) * wa.w;
+    b.x = (b.x * rms) * wb2.x; b.y = (b.y * rms) * wb2.y; b.z = (b.z * rms) * wb2.z; b.w = (b.w * rms) * wb2.w;
+    const int c = (512 * i + 8 * lane) >> 2;                     // float4 index, even
+    // lanes past D write the spare sub-block after the row
+    gm_put_limbs8(a, b, 512 * i + 8 * lane < D ? c : (D >> 2) + (c & 7), xl_out);
   }
   GM_TL_END(0);
 }
@@ -175,46 +164,28 @@ __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const flo
   }
 }
 
-// with_shared: the shared expert's gate/up run here as well.
-template <int QTS, int NT, int DC>
-int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s,
-                    bool with_shared) {
-  const int nrows = P->E + (P->sh_gate_inp ? 1 : 0);
-  const int n_rb = (nrows + 3) / 4;
-  const int n_sb = P->gate_sh && with_shared ? (P->FF_sh + 7) / 8 : 0;
-  const size_t smem = ((size_t)NT * P->D + 4 + 4 * NT) * 4 + (QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
-  if (int rc = gm_set_smem(k_dec_router<QTS, NT, DC>, smem)) return rc;
-  hipLaunchKernelGGL((k_dec_router<QTS, NT, DC>), dim3(n_rb + n_sb), dim3(256), smem, s, *P, x, T, a.logits, a.shg,
-                     a.hsh, n_rb, n_sb > 0 ? a.xl : nullptr GM_TL_ARG(a.tl));
-  GM_TRY(hipGetLastError());
-  return GM_OK;
-}
-
-template <int QTS, int NT>
-int launch_router_n(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s, bool ws) {
-  switch (gm_dec_dc(P->D)) {
-    case 1: return launch_router_t<QTS, NT, 1>(P, x, T, a, s, ws);
-    case 2: return launch_router_t<QTS, NT, 2>(P, x, T, a, s, ws);
-    default: return launch_router_t<QTS, NT, 4>(P, x, T, a, s, ws);
-  }
-}
-
 int launch_router(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s, bool fast1) {
+  const int nrows = P->E + (P->sh_gate_inp ? 1 : 0);
   if (!fast1) {                                                      // router partials only
-    const int nrows = P->E + (P->sh_gate_inp ? 1 : 0);
     const int kr = gm_dec_kr(P->D);
     hipLaunchKernelGGL(k_dec_router_ks<8>, dim3((nrows + 3) / 4, P->D / kr), dim3(256), 0, s, *P, x, T, a.part,
                        a.ssq, gm_dec_part_ld(P), kr, a.xl);
     GM_TRY(hipGetLastError());
     return GM_OK;
   }
-  if (!P->gate_sh) return launch_router_n<GM_QTYPE_IQ4_XS, 1>(P, x, T, a, s, true);
-  switch (P->q_gate_sh) {
-    case GM_QTYPE_IQ4_XS: return launch_router_n<GM_QTYPE_IQ4_XS, 1>(P, x, T, a, s, true);
-    case GM_QTYPE_IQ3_XXS: return launch_router_n<GM_QTYPE_IQ3_XXS, 1>(P, x, T, a, s, true);
-    case GM_QTYPE_BF16: return launch_router_n<GM_QTYPE_BF16, 1>(P, x, T, a, s, true);
-    default: return gm_fail_arg("gm_moe_forward: shared gate/up format %d unsupported", P->q_gate_sh);
+  const dim3 grid((nrows + 1) / 2);
+  switch ((P->D + 511) / 512) {
+    case 1: hipLaunchKernelGGL(k_dec_router1<1>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
+    case 2: hipLaunchKernelGGL(k_dec_router1<2>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
+    case 3: hipLaunchKernelGGL(k_dec_router1<3>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
+    case 4: hipLaunchKernelGGL(k_dec_router1<4>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
+    case 5: hipLaunchKernelGGL(k_dec_router1<5>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
+    case 6: hipLaunchKernelGGL(k_dec_router1<6>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
+    case 7: hipLaunchKernelGGL(k_dec_router1<7>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
+    default: hipLaunchKernelGGL(k_dec_router1<8>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
   }
+  GM_TRY(hipGetLastError());
+  return GM_OK;
 }
 
 }  // namespace

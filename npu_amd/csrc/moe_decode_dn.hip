@@ -65,7 +65,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   const int r0 = blockIdx.x * 8;
   const bool has_sh = P.down_sh != nullptr;
   const int trash = wbytes;                                            // spare 16 bytes
-  // --- A: loads that do not depend on the routing
+  // --- A: the ids, then the loads that do not depend on the routing
   int ex[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) ex[j] = g_grp[1 + (j < k ? j : k - 1)];
@@ -73,7 +73,6 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   const int my_pr = g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * jj];
   const float my_wj = __int_as_float(g_grp[GM_GRP_WORDS + jj]);
   const float sg = has_sh ? shg[0] : 0.f;
-  GM_TL_MARK1(ex[0]);
   const float xres = (flags & GM_MOE_RESIDUAL) ? x[r0 + (tid & 7)] : 0.f;
   uint32_t gw = 0;
   if constexpr (IQ3) gw = gm_iq3_tab_load();
@@ -94,8 +93,29 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
     const int c = tid + NTH * i;
     sr[i] = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(sbase + 16 * (c < n16s ? c : n16s - 1)));
   }
+  // --- B: routed rows, addresses from the routing: issued as soon as the ids
+  // are in, before anything else is waited for
+  const int n16 = 8 * rbd / 16, total = k * n16;
+  gm_u32x4 rr[CR];
+  int dst[CR];
+  {
+    const uint32_t magic = 0xffffffffu / (uint32_t)n16 + 1u;
+#pragma unroll
+    for (int i = 0; i < CR; ++i) {
+      const int c = tid + NTH * i;
+      const int cc = c < total ? c : total - 1;
+      const int m = (int)__umulhi((uint32_t)cc, magic), j = cc - m * n16;
+      int e = ex[0];
+#pragma unroll
+      for (int q = 1; q < 8; ++q) e = m == q ? ex[q] : e;
+      rr[i] = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(static_cast<const uint8_t*>(P.down_exps) +
+                                                           ((int64_t)e * D + r0) * rbd + 16 * j));
+      dst[i] = c < total ? m * 8 * rbd + 16 * j : trash;
+    }
+  }
+  GM_TL_MARK1(ex[0]);
   issue_fence();
-  // --- B: stage them
+  // --- C: stage the SwiGLU rows and the shared rows, then the routed rows
   if (tid < 8) { s_pr[tid] = my_pr; s_wj[tid] = my_wj; }
   if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
   {
@@ -112,28 +132,8 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
     const int c = tid + NTH * i;
     *reinterpret_cast<gm_u32x4*>(wr + (c < n16s && has_sh ? k * 8 * rbd + 16 * c : trash)) = sr[i];
   }
-  // --- C: routed rows (addresses from the routing)
-  {
-    const int n16 = 8 * rbd / 16, total = k * n16;
-    const uint32_t magic = 0xffffffffu / (uint32_t)n16 + 1u;
-    gm_u32x4 rr[CR];
-    int dst[CR];
 #pragma unroll
-    for (int i = 0; i < CR; ++i) {
-      const int c = tid + NTH * i;
-      const int cc = c < total ? c : total - 1;
-      const int m = (int)__umulhi((uint32_t)cc, magic), j = cc - m * n16;
-      int e = ex[0];
-#pragma unroll
-      for (int q = 1; q < 8; ++q) e = m == q ? ex[q] : e;
-      rr[i] = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(static_cast<const uint8_t*>(P.down_exps) +
-                                                           ((int64_t)e * D + r0) * rbd + 16 * j));
-      dst[i] = c < total ? m * 8 * rbd + 16 * j : trash;
-    }
-    issue_fence();
-#pragma unroll
-    for (int i = 0; i < CR; ++i) *reinterpret_cast<gm_u32x4*>(wr + dst[i]) = rr[i];
-  }
+  for (int i = 0; i < CR; ++i) *reinterpret_cast<gm_u32x4*>(wr + dst[i]) = rr[i];
   __syncthreads();
   GM_TL_MARK2(s_pr[0]);
   // --- D: decode from LDS; wave w -> matrix w
@@ -141,7 +141,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   if (routed || shared) {
     const int lg = nsub == 8 ? 3 : nsub == 16 ? 4 : 5;
     const int R = nsub >> 3, rg = lane >> lg, sub = lane & (nsub - 1);
-    const int hrow = routed ? s_pr[wave] : k;
+    const int hrow = routed ? s_pr[wave] : k;                   // h row of rank w (the gate/up kernel's order)
     // limbs and scale of this sub-block of the SwiGLU row
     const uint8_t* hsub = hs + hrow * hbytes + sub * GM_LSUB;
     const gm_u32x4* hp = reinterpret_cast<const gm_u32x4*>(hsub);
@@ -192,6 +192,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
         }
       }
     }
+    GM_TL_MARK3(part[0]);
     const float wgt = routed ? s_wj[wave] : sg;
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {

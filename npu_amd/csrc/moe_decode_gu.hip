@@ -1,13 +1,13 @@
 // MoE decode, stage 2: top-k routing, expert grouping, routed gate/up + SwiGLU.
 //
-// T = 1 (k_dec_gateup1): every block recomputes the token's top-k selection
-// from the router logits (wave 0, while wave 1 copies the limb row of x that
-// the router kernel wrote, or stages it itself) instead of waiting for
-// a separate routing kernel, picks the expert of rank `u` among the k picks
+// T = 1 (k_dec_gateup1): every wave of every routed block recomputes the
+// token's top-k selection from the router logits instead of waiting for a
+// separate routing kernel, picks the expert of rank `u` among the k picks
 // (ascending id, the order of torch.unique in qwen/forward.py:612) and runs 8
-// SwiGLU rows of it.  Block 0 also computes the routing weights, once its
-// weight rows are in flight, and publishes ids, weights and the grouping table
-// for stage 3.
+// SwiGLU rows of it; the shared expert's rows run in blocks of their own.
+// The first routed block also computes the routing weights, once its weight
+// rows are in flight, and publishes ids, weights and the grouping table for
+// stage 3.
 //
 // T > 1: k_dec_route (one block) runs the per-token top-k and groups the
 // (token, slot) pairs by expert; k_dec_gateup8 then runs (unit, 16-row chunk)
@@ -21,73 +21,114 @@ using namespace gm_moe;
 
 namespace {
 
-template <int QT, int DC, int MAXV>
-__global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float* __restrict__ x,
-                                                     const float* __restrict__ logits, int32_t* __restrict__ g_ids,
-                                                     float* __restrict__ g_wts, int32_t* __restrict__ g_grp,
-                                                     float* __restrict__ h, int n_chunks,
+// Blocks [0, n_sh): 8 rows of the shared expert's gate/up pair (format QTS),
+// which do not depend on the routing.  Blocks [n_sh, ...): unit u = (b - n_sh)
+// / n_chunks, the pick of rank u in ascending expert id (the order of
+// torch.unique, qwen/forward.py:612), rows 8 c .. 8 c + 7 of its gate/up pair
+// (c = chunk).  In a routed block wave 0 runs the top-k of the logits
+// (topk_masks, wave-uniform) while every thread loads its chunks of the limb
+// row of xn that the router kernel wrote; the expert id reaches the other
+// waves through LDS at the block's one barrier, after which every wave issues
+// its weight loads.  Shared blocks issue theirs before the barrier.  The first
+// routed block also publishes the ids and renormalised weights (in
+// descending order) and the grouping table (ascending id; the SwiGLU row of
+// rank u is h row u) once its weight loads are in flight.
+template <int QT, int QTS, int DC, int MAXV>
+__global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float* __restrict__ logits,
+                                                     int32_t* __restrict__ g_ids, float* __restrict__ g_wts,
+                                                     int32_t* __restrict__ g_grp, float* __restrict__ h,
+                                                     float* __restrict__ hsh, int n_chunks, int n_sh,
                                                      const uint8_t* __restrict__ xl GM_TL_PARAM) {
-  constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
   GM_TL_BEGIN();
+  constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS;
+  constexpr int CPT = (32 * DC * GM_LSUB / 16 + 255) / 256;     // 16-byte limb chunks per thread
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int32_t s_e;
   const int D = P.D, E = P.E, k = P.k, FF = P.FF, nsub = D / GM_SUB, rbytes = gm_limb_row_bytes(D);
-  uint8_t* xs = smem;                                          // limb row of x (+ a spare sub-block)
-  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(smem + rbytes + GM_LSUB);   // IQ3 only
-  __shared__ int32_t s_sid[8], s_slot[8];                      // picks in ascending expert order
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int u = blockIdx.x / n_chunks, chunk = blockIdx.x - u * n_chunks;
+  uint8_t* xs = smem;                                           // limb row of xn (+ a spare chunk)
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(smem + rbytes + GM_LSUB);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane & 31;
+  const bool shared = (int)blockIdx.x < n_sh;                   // uniform per block
+  const int rch = rbytes >> 4;
+  gm_u32x4 cp[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    cp[i] = reinterpret_cast<const gm_u32x4*>(xl)[c < rch ? c : rch - 1];
+  }
   uint32_t gw = 0;
   if constexpr (IQ3) gw = gm_iq3_tab_load();
-  int myid = 0, mykey = 0, rk = 0, skey[MAXV];
-  if (wave == 0) {
-    // top-k selection of the router logits; lane j < k holds pick j
-    float v[MAXV];
-    int ix[MAXV];
-    topk_load<MAXV>(logits, E, v, ix);
-    topk_select<MAXV>(v, ix, E, k, myid, mykey, skey);
-    // rank of the pick among the k (distinct) ids
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rk += __builtin_amdgcn_readlane(myid, i) < myid ? 1 : 0;
-    if (lane < k) { s_sid[rk] = myid; s_slot[rk] = lane; }
-  } else if (wave == 1) {                                     // concurrently with the top-k
-    if (xl != nullptr) copy_limbs_wave<DC>(xl, rbytes, xs);
-    else stage_limbs_wave<4 * DC>(x, D, P.norm_w, P.norm_eps, xs);
-  }
-  if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
-  __syncthreads();
-  const int e = s_sid[u], pair = s_slot[u];
-  GM_TL_MARK1(e);
-  const int64_t rb = gm_row_bytes(QT, D);
+  const int b = (int)blockIdx.x - n_sh;
+  const int u = shared ? 0 : b / n_chunks, chunk = shared ? (int)blockIdx.x : b - u * n_chunks;
   const int row = chunk * 8 + wave * 2 + (lane >> 5);
   const bool live = row < FF;
   const int r = live ? row : 0;
   RowFetch<QT, DC> fg, fu;
-  fetch_subs<QT, 32, DC, true>(fg, static_cast<const uint8_t*>(P.gate_exps) + ((int64_t)e * FF + r) * rb, lane & 31,
-                               nsub);
-  fetch_subs<QT, 32, DC, true>(fu, static_cast<const uint8_t*>(P.up_exps) + ((int64_t)e * FF + r) * rb, lane & 31,
-                               nsub);
-  if (blockIdx.x == 0 && wave == 0) {
-    // publish ids, weights and the grouping table for stage 3 and the caller
-    // (the softmax weights are needed by nobody else, so they are computed
-    // while this block's weight rows are in flight)
-    const float myw = topk_weights<MAXV>(skey, k, mykey);
-    if (lane < k) {
-      g_ids[lane] = myid;
-      g_wts[lane] = myw;
-      g_grp[1 + rk] = myid;
-      g_grp[1 + GM_GRP_MAXU + rk] = 1;
-      g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * rk] = lane;
-      g_grp[GM_GRP_WORDS + rk] = __float_as_int(myw);
+  RowFetch<QTS, DC> sg, su;
+  uint32_t uk[MAXV];
+  uint64_t sel[MAXV];
+  if (shared) {
+    const int64_t rbs = gm_row_bytes(QTS, D);
+    fetch_subs<QTS, 32, DC, true>(sg, static_cast<const uint8_t*>(P.gate_sh) + r * rbs, lir, nsub);
+    fetch_subs<QTS, 32, DC, true>(su, static_cast<const uint8_t*>(P.up_sh) + r * rbs, lir, nsub);
+  } else if (wave == 0) {
+    float v[MAXV];
+    int ix[MAXV];
+    topk_load<MAXV>(logits, E, v, ix);
+    GM_TL_MARK3(v[0]);
+    topk_keys<MAXV>(v, ix, E, uk);
+    topk_masks<MAXV>(uk, k, sel);
+    if (lane == 0) s_e = topk_rank_id<MAXV>(sel, u);
+  }
+  issue_fence();
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    reinterpret_cast<gm_u32x4*>(xs)[c < rch ? c : rch] = cp[i];   // past the row: the spare chunk
+  }
+  if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
+  __syncthreads();
+  if (!shared) {
+    const int e = s_e;
+    GM_TL_MARK1(e);
+    const int64_t rb = gm_row_bytes(QT, D);
+    fetch_subs<QT, 32, DC, true>(fg, static_cast<const uint8_t*>(P.gate_exps) + ((int64_t)e * FF + r) * rb, lir,
+                                 nsub);
+    fetch_subs<QT, 32, DC, true>(fu, static_cast<const uint8_t*>(P.up_exps) + ((int64_t)e * FF + r) * rb, lir,
+                                 nsub);
+    if (b == 0 && wave == 0) {
+      // publish for stage 3 and the caller while this block's rows are in flight
+      int rid;
+      uint32_t rkey;
+      topk_gather_rank<MAXV>(sel, uk, k, rid, rkey);
+      const int slot = topk_slot(rid, rkey, k);
+      const float w = topk_rank_weight<MAXV>(uk, rkey, k);
+      if (lane < k) {
+        g_ids[slot] = rid;
+        g_wts[slot] = w;
+        g_grp[1 + lane] = rid;
+        g_grp[1 + GM_GRP_MAXU + lane] = 1;
+        g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * lane] = lane;
+        g_grp[GM_GRP_WORDS + lane] = __float_as_int(w);
+      }
+      if (lane == 0) g_grp[0] = k;
     }
-    if (lane == 0) g_grp[0] = k;
   }
   const int tok[1] = {0};
   float ag[1] = {0.f}, au[1] = {0.f};
-  dot_subs_i8<QT, 32, DC, 1>(fg, lane & 31, nsub, xs, rbytes, tok, 1, tab, ag);
-  dot_subs_i8<QT, 32, DC, 1>(fu, lane & 31, nsub, xs, rbytes, tok, 1, tab, au);
+  if (shared) {
+    dot_subs_i8<QTS, 32, DC, 1>(sg, lir, nsub, xs, rbytes, tok, 1, tab, ag);
+    dot_subs_i8<QTS, 32, DC, 1>(su, lir, nsub, xs, rbytes, tok, 1, tab, au);
+  } else {
+    dot_subs_i8<QT, 32, DC, 1>(fg, lir, nsub, xs, rbytes, tok, 1, tab, ag);
+    dot_subs_i8<QT, 32, DC, 1>(fu, lir, nsub, xs, rbytes, tok, 1, tab, au);
+  }
   GM_TL_MARK2(au[0]);
   const float hv = gm_silu(row_sum<32>(ag[0])) * row_sum<32>(au[0]);
-  if (live && (lane & 31) == 0) h[(int64_t)pair * FF + row] = hv;
+  if (live && lir == 0) {
+    if (shared) hsh[row] = hv;
+    else h[(int64_t)u * FF + row] = hv;
+  }
   GM_TL_END(1);
 }
 
@@ -291,16 +332,13 @@ template <int QT, int QTS, int DC>
 int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s) {
   if (fast1) {
     const int n_chunks = (P->FF + 7) / 8;
-    const size_t smem = (size_t)gm_limb_row_bytes(P->D) + GM_LSUB + (QT == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
-    if (int rc = gm_set_smem(k_dec_gateup1<QT, DC, 4>, smem)) return rc;
-    if (int rc = gm_set_smem(k_dec_gateup1<QT, DC, 8>, smem)) return rc;
-    const uint8_t* xl = P->gate_sh ? a.xl : nullptr;           // written by the router kernel's shared blocks
-    if (P->E <= 256)
-      hipLaunchKernelGGL((k_dec_gateup1<QT, DC, 4>), dim3(P->k * n_chunks), dim3(256), smem, s, *P, x, a.logits,
-                         a.ids, a.wts, a.grp, a.h, n_chunks, xl GM_TL_ARG(a.tl));
-    else
-      hipLaunchKernelGGL((k_dec_gateup1<QT, DC, 8>), dim3(P->k * n_chunks), dim3(256), smem, s, *P, x, a.logits,
-                         a.ids, a.wts, a.grp, a.h, n_chunks, xl GM_TL_ARG(a.tl));
+    const int n_sh = P->gate_sh ? (P->FF_sh + 7) / 8 : 0;
+    const size_t smem = (size_t)gm_limb_row_bytes(P->D) + GM_LSUB +
+                        (QT == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+    auto kern = P->E <= 256 ? k_dec_gateup1<QT, QTS, DC, 4> : k_dec_gateup1<QT, QTS, DC, 8>;
+    if (int rc = gm_set_smem(kern, smem)) return rc;
+    hipLaunchKernelGGL(kern, dim3(n_sh + P->k * n_chunks), dim3(256), smem, s, *P, a.logits, a.ids, a.wts, a.grp,
+                       a.h, a.hsh, n_chunks, n_sh, a.xl GM_TL_ARG(a.tl));
     GM_TRY(hipGetLastError());
     return GM_OK;
   }
@@ -344,7 +382,7 @@ int launch_gu_q(const gm_moe_layer* P, const float* x, int T, bool fast1, const 
 
 template <int QT>
 int launch_gu_s(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s) {
-  if (fast1 || !P->gate_sh) return launch_gu_q<QT, QT>(P, x, T, fast1, a, s);   // shared gate/up run in stage 1
+  if (!P->gate_sh) return launch_gu_q<QT, QT>(P, x, T, fast1, a, s);
   switch (P->q_gate_sh) {
     case GM_QTYPE_IQ4_XS: return launch_gu_q<QT, GM_QTYPE_IQ4_XS>(P, x, T, fast1, a, s);
     case GM_QTYPE_IQ3_XXS: return launch_gu_q<QT, GM_QTYPE_IQ3_XXS>(P, x, T, fast1, a, s);

@@ -7,6 +7,8 @@
 // whole chip) at block entry, at two kernel-specific marks, and at the end,
 // plus the HW_ID and XCC_ID registers of the wave.  Record layout (u64):
 //   [0] entry  [1] mark 1  [2] mark 2  [3] end  [4] HW_ID | XCC_ID << 32
+//   [5] s_memtime (shader clock) at entry  [6] s_memtime at the end
+//   [7] mark 3 (an optional earlier mark, 0 if unused)
 // Each workspace holds GM_TL_KERNELS x GM_TL_MAXB records, so every layer of
 // a chain keeps its own stamps.  In the normal build the macros expand to
 // nothing and the kernels are unchanged.
@@ -34,9 +36,16 @@ __device__ __forceinline__ uint64_t gm_tl_after(const T& dep) {
   return gm_tl_now();
 }
 
+__device__ __forceinline__ uint64_t gm_tl_clock() {
+  uint64_t t;
+  asm volatile("s_memtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t)::"memory");
+  return t;
+}
+
 __device__ __forceinline__ void gm_tl_flush(uint64_t* __restrict__ buf, int slot, uint64_t t0, uint64_t t1,
-                                            uint64_t t2) {
+                                            uint64_t t2, uint64_t c0, uint64_t t3m) {
   const uint64_t t3 = gm_tl_now();
+  const uint64_t c1 = gm_tl_clock();
   if (threadIdx.x == 0 && blockIdx.x < GM_TL_MAXB) {
     const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);     // HW_ID
     const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);   // XCC_ID
@@ -46,15 +55,19 @@ __device__ __forceinline__ void gm_tl_flush(uint64_t* __restrict__ buf, int slot
     r[2] = t2;
     r[3] = t3;
     r[4] = (uint64_t)hw | ((uint64_t)xcc << 32);
+    r[5] = c0;
+    r[6] = c1;
+    r[7] = t3m;
   }
 }
 
 #define GM_TL_PARAM , uint64_t* __restrict__ gm_tl
 #define GM_TL_ARG(p) , (p)
-#define GM_TL_BEGIN() uint64_t gm_tl_t0 = gm_tl_now(), gm_tl_t1 = 0, gm_tl_t2 = 0
+#define GM_TL_BEGIN() uint64_t gm_tl_t0 = gm_tl_now(), gm_tl_c0 = gm_tl_clock(), gm_tl_t1 = 0, gm_tl_t2 = 0, gm_tl_t3 = 0
 #define GM_TL_MARK1(dep) (gm_tl_t1 = gm_tl_after(dep))
 #define GM_TL_MARK2(dep) (gm_tl_t2 = gm_tl_after(dep))
-#define GM_TL_END(slot) gm_tl_flush(gm_tl, (slot), gm_tl_t0, gm_tl_t1, gm_tl_t2)
+#define GM_TL_MARK3(dep) (gm_tl_t3 = gm_tl_after(dep))
+#define GM_TL_END(slot) gm_tl_flush(gm_tl, (slot), gm_tl_t0, gm_tl_t1, gm_tl_t2, gm_tl_c0, gm_tl_t3)
 #define GM_TL_BYTES ((size_t)GM_TL_KERNELS * GM_TL_MAXB * GM_TL_REC * 8)
 
 #else
@@ -64,6 +77,7 @@ __device__ __forceinline__ void gm_tl_flush(uint64_t* __restrict__ buf, int slot
 #define GM_TL_BEGIN() ((void)0)
 #define GM_TL_MARK1(dep) ((void)0)
 #define GM_TL_MARK2(dep) ((void)0)
+#define GM_TL_MARK3(dep) ((void)0)
 #define GM_TL_END(slot) ((void)0)
 #define GM_TL_BYTES ((size_t)0)
 

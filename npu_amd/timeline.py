@@ -27,7 +27,7 @@ SEED = 20261201
 
 
 def _layer_records(blk, T: int):
-    """[slot] -> list of (entry, mark1, mark2, end, hwid) for the blocks that wrote one."""
+    """[slot] -> list of (entry, mark1, mark2, end, hwid, clock0, clock1) for the blocks that wrote one."""
     import torch
     from npu_amd import ops
     need = ops.moe_workspace_bytes(blk.struct, T)
@@ -36,7 +36,7 @@ def _layer_records(blk, T: int):
     out = []
     for s in range(N_SLOTS):
         rows = raw[s]
-        out.append([tuple(int(v) for v in r[:5]) for r in rows if r[0] != 0])
+        out.append([tuple(int(v) for v in r[:8]) for r in rows if r[0] != 0])
     return out
 
 
@@ -89,11 +89,14 @@ def summarise(recs, names):
             m1 = sorted(r[1] for r in rs)
             m2 = sorted(r[2] for r in rs)
             en = sorted(r[3] for r in rs)
+            m3 = sorted(r[7] for r in rs if r[7] != 0)
             d = {"blocks": len(rs), "entry_first": e[0] - t0, "entry_median": e[len(e) // 2] - t0,
+                 "mark3_median": (m3[len(m3) // 2] - t0) if m3 else 0, "mark3_last": (m3[-1] - t0) if m3 else 0,
                  "entry_last": e[-1] - t0, "mark1_median": m1[len(m1) // 2] - t0, "mark1_last": m1[-1] - t0,
                  "mark2_median": m2[len(m2) // 2] - t0, "mark2_last": m2[-1] - t0,
                  "end_median": en[len(en) // 2] - t0, "end_last": en[-1] - t0,
                  "block_median": sorted(r[3] - r[0] for r in rs)[len(rs) // 2],
+                 "mhz": sorted((r[6] - r[5]) * 100.0 / max(r[3] - r[0], 1) for r in rs)[len(rs) // 2],
                  "xccs": len({r[4] >> 32 for r in rs})}
             for kk, v in d.items():
                 stats.setdefault(s, {}).setdefault(kk, []).append(v)
@@ -104,16 +107,18 @@ def summarise(recs, names):
             ns = [s for s in range(N_SLOTS) if nxt[s]]
             gaps_between.append(min(r[0] for r in nxt[ns[0]]) - max(r[3] for r in layer[slots[-1]]))
     med = lambda v: statistics.median(v) * TICK_US
-    lines = ["| kernel | blocks | XCDs | entry first / median / last | mark 1 median / last | "
-             "mark 2 median / last | end median / last | block duration (median) |",
-             "|---|---|---|---|---|---|---|---|"]
+    lines = ["| kernel | blocks | XCDs | entry first / median / last | mark 3 median / last | mark 1 median / last | "
+             "mark 2 median / last | end median / last | block duration (median) | shader clock MHz (median) |",
+             "|---|---|---|---|---|---|---|---|---|---|"]
     for s, d in stats.items():
         lines.append(
             f"| {names.get(s, s)} | {int(statistics.median(d['blocks']))} | {int(statistics.median(d['xccs']))} | "
             f"{med(d['entry_first']):.2f} / {med(d['entry_median']):.2f} / {med(d['entry_last']):.2f} | "
+            f"{med(d['mark3_median']):.2f} / {med(d['mark3_last']):.2f} | "
             f"{med(d['mark1_median']):.2f} / {med(d['mark1_last']):.2f} | "
             f"{med(d['mark2_median']):.2f} / {med(d['mark2_last']):.2f} | "
-            f"{med(d['end_median']):.2f} / {med(d['end_last']):.2f} | {med(d['block_median']):.2f} |")
+            f"{med(d['end_median']):.2f} / {med(d['end_last']):.2f} | {med(d['block_median']):.2f} | "
+            f"{statistics.median(d['mhz']):.0f} |")
     lines.append("")
     for (a, b), v in gaps_in.items():
         lines.append(f"- gap {names.get(a, a)} last end -> {names.get(b, b)} first entry: {med(v):.2f} us (median)")
@@ -133,8 +138,15 @@ def main() -> int:
     ap.add_argument("--T", type=int, default=1)
     ap.add_argument("--replays", type=int, default=5)
     ap.add_argument("--out", default=None, help="also write the summary to this file")
+    ap.add_argument("--npz", default=None, help="also save every record (layer, kernel, block) to this .npz")
     args = ap.parse_args()
     recs = run(args.layers, args.T, args.replays)
+    if args.npz:
+        import numpy as np
+        rows = [(li, s, *r) for li, layer in enumerate(recs) for s in range(N_SLOTS) for r in layer[s]]
+        np.savez_compressed(args.npz, records=np.array(rows, dtype=np.int64),
+                            columns=np.array(["layer", "kernel", "entry", "mark1", "mark2", "end", "hwid",
+                                              "clock0", "clock1", "mark3"]))
     names = {0: "router (stage 1)", 1: "gate/up (stage 2)", 2: "down (stage 3)", 3: "extra"}
     text = summarise(recs, names)
     print(text)

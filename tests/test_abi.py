@@ -34,7 +34,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layout_matches_header():
     fields = re.search(r"typedef struct gm_moe_layer \{(.*?)\} gm_moe_layer;", HEADER, re.S).group(1)
-    names = re.findall(r"(\w+)(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?;", fields)
+    fields = re.sub(r"/\*.*?\*/", "", fields, flags=re.S)
+    names =re.findall(r"(\w+)(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?;", fields)
     flat = [n for grp in names for n in grp if n]
     assert flat == [f for f, _ in L.GmMoeLayer._fields_]
 
