@@ -61,13 +61,6 @@ __device__ __forceinline__ float gm_bf2f(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 bits (NaN-preserving).
-__device__ __forceinline__ uint32_t gm_f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
-
 __device__ __forceinline__ float gm_silu(float g) { return g / (1.0f + __expf(-g)); }
 
 __device__ __forceinline__ float gm_sigmoid(float g) { return 1.0f / (1.0f + __expf(-g)); }

@@ -28,9 +28,13 @@ ROUTER_STD = 0.02
 
 
 def to_bf16(a: np.ndarray) -> np.ndarray:
-    """fp32 -> bf16 bits (uint16), round to nearest even (as qwen/model.py:280-289)."""
+    """fp32 -> bf16 bits (uint16), round to nearest even (as qwen/model.py:280-289).
+    A NaN stays a NaN (its top mantissa bit is set, as torch's bf16 cast does); the
+    rounding add alone would carry a NaN with a small payload into +-inf."""
     u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
 
 
 def from_bf16(b: np.ndarray) -> np.ndarray:

@@ -114,11 +114,10 @@ def test_router_topk(gpu, T, E, k, bias):
     xn = OM.rms_norm(x, ol.norm_w, 1e-6)
     OM.moe_forward(xn.unsqueeze(0), ol, stages=st)
     margin = OM.topk_margin(OM.router_logits64(x, ol), k)
-    clear = margin > 1e-5
-    assert bool(clear.any())
-    assert torch.equal(ids.cpu().long()[clear], st["topk_ids"][clear])
+    assert bool((margin > 1e-5).all()), "near-tie token: choose another seed"
+    assert torch.equal(ids.cpu().long(), st["topk_ids"])
     assert torch.allclose(logits.cpu(), st["ffn_moe_logits"], rtol=0, atol=2e-5)
-    assert torch.allclose(wts.cpu()[clear], st["ffn_moe_weights_norm"][clear], rtol=1e-5, atol=1e-6)
+    assert torch.allclose(wts.cpu(), st["ffn_moe_weights_norm"], rtol=1e-5, atol=1e-6)
     assert torch.allclose(shg.cpu(), st["shared_expert_gate_sigmoid"], rtol=1e-5, atol=1e-6)
 
 
