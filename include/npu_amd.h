@@ -181,6 +181,25 @@ int gm_moe_prefill(const gm_moe_layer* L, const float* x, float* y, int T, int f
 int gm_moe_forward_stage(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
                          size_t ws_bytes, int stage, void* stream);
 
+/* Size of the static scratch gm_moe_forward_noalloc works in: 16 MiB per GPU. */
+#define GM_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+/*
+ * gm_moe_forward without a workspace argument and without any allocation
+ * (no hipMalloc / hipFree, no allocating library call): the workspace is a
+ * static device array of GM_NOALLOC_SCRATCH_BYTES that every GPU running the
+ * library holds until the process ends.  No counterpart in the reference; it
+ * is for callers that cannot allocate (code under stream / graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same kernels and
+ * results as gm_moe_forward.  Returns GM_EWORKSPACE when
+ * gm_moe_workspace_bytes(L, T) > GM_NOALLOC_SCRATCH_BYTES (config 5: T <= 8
+ * needs 1.7 MiB, prefill fits up to T = 111).  stream must belong to the
+ * current device.  All calls on one GPU share that GPU's array, which keeps
+ * the last call's contents: calls that overlap on one GPU (other streams,
+ * other threads) race and must be serialised by the caller.
+ */
+int gm_moe_forward_noalloc(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

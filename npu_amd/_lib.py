@@ -29,6 +29,7 @@ GM_EUNSUPPORTED = -2
 GM_EWORKSPACE = -3
 
 GM_MOE_RESIDUAL = 1
+GM_NOALLOC_SCRATCH_BYTES = 16 << 20   # gm_moe_forward_noalloc's static scratch per GPU
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -65,6 +66,7 @@ SIGNATURES = {
                                         ctypes.POINTER(_sz), ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "gm_moe_forward": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _vp]),
     "gm_moe_forward_stage": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _i32, _vp]),
+    "gm_moe_forward_noalloc": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp]),
     "gm_moe_decode": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _vp]),
     "gm_moe_prefill": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _vp]),
 }

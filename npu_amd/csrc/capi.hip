@@ -3,6 +3,7 @@
 // prefill.hip.
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "kernels.h"
 
@@ -208,6 +209,58 @@ int gm_moe_forward_stage(const gm_moe_layer* L, const float* x, float* y, int T,
 }
 
 }  // extern "C"
+
+// gm_moe_forward_noalloc's workspace: a file-scope device array.  Every GPU that
+// loads this code object holds its own copy, at its own address, until the
+// process ends.  In host code `scratch` names a host-side stand-in, never the
+// device memory: the per-device address comes from hipGetSymbolAddress once, on
+// the first call on each device, and only that address is passed on.
+static __device__ __align__(256) uint8_t scratch[GM_NOALLOC_SCRATCH_BYTES];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_address(int dev, void** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return gm_fail_hip(e, "gm_moe_forward_noalloc: hipGetSymbolAddress(scratch)");
+    if (!ptr || reinterpret_cast<uintptr_t>(ptr) % 256)
+      return gm_fail_arg("gm_moe_forward_noalloc: scratch address %p is not 256-byte aligned", ptr);
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GM_OK;
+}
+
+extern "C" int gm_moe_forward_noalloc(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
+                                      void* stream) {
+  if (int rc = check_layer(L)) return rc;
+  if (T < 0) return gm_fail_arg("gm_moe_forward_noalloc: negative T");
+  const size_t need = gm_moe_ws_layout(L, T).total;
+  if (need > GM_NOALLOC_SCRATCH_BYTES)
+    return gm_fail_arg("gm_moe_forward_noalloc: T=%d needs %zu workspace bytes, more than the %zu of the static "
+                       "scratch (use gm_moe_forward with a workspace)", T, need, (size_t)GM_NOALLOC_SCRATCH_BYTES),
+           GM_EWORKSPACE;
+  if (T == 0) return GM_OK;
+  int dev = -1;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return gm_fail_hip(e, "gm_moe_forward_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return gm_fail_arg("gm_moe_forward_noalloc: device %d >= %d", dev, kMaxDevices);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipError_t e = hipStreamGetDevice(as_stream(stream), &sdev); e != hipSuccess)
+      return gm_fail_hip(e, "gm_moe_forward_noalloc: hipStreamGetDevice");
+    if (sdev != dev)
+      return gm_fail_arg("gm_moe_forward_noalloc: stream is on device %d but device %d is current", (int)sdev, dev);
+  }
+  void* ptr = nullptr;
+  if (int rc = scratch_address(dev, &ptr)) return rc;
+  // No region of the workspace has to start at zero: every kernel writes what it
+  // later reads within the same call.
+  return moe_forward_impl(L, x, y, T, flags, ptr, GM_NOALLOC_SCRATCH_BYTES, 0, kPathAuto, stream);
+}
 
 static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
                             size_t ws_bytes, int stage, int path, void* stream) {

@@ -87,6 +87,12 @@ def test_workspace_sizing_and_layer_validation():
     need = lib.gm_moe_workspace_bytes(ctypes.byref(wide), 16)
     rc = lib.gm_moe_prefill(ctypes.byref(wide), 1024, 1 << 20, 16, 0, 1 << 24, need, None)
     assert rc == L.GM_EINVAL and "prefill supports D <= 8192" in L.last_error()
+    # the no-allocation variant rejects a T whose workspace exceeds its static scratch
+    assert lib.gm_moe_workspace_bytes(ctypes.byref(s), 200) > L.GM_NOALLOC_SCRATCH_BYTES
+    rc = lib.gm_moe_forward_noalloc(ctypes.byref(s), 1024, 1 << 24, 200, 0, None)
+    assert rc == L.GM_EWORKSPACE and "static scratch" in L.last_error()
+    m = re.search(r"#define GM_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", HEADER)
+    assert int(m.group(1)) << int(m.group(2)) == L.GM_NOALLOC_SCRATCH_BYTES
     bad = _layer(norm_w=4100)
     rc = lib.gm_moe_forward(ctypes.byref(bad), 1024, 2048, 1, 0, 4096, 1 << 30, None)
     assert rc == L.GM_EINVAL and "16-byte aligned" in L.last_error()
