@@ -49,6 +49,9 @@ def parse() -> argparse.Namespace:
                     help="only run the config-5 batch-8 chain over --layers layers, one JSON line")
     ap.add_argument("--dense-only", action="store_true",
                     help="only run the dense bf16 projection matvec measurement, one JSON line")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the per-stage graphs the roofline is measured on (for rocprof)")
+    ap.add_argument("--chain-only", action="store_true", help="only the B=1 chain (for rocprof)")
     ap.add_argument("--dense-shapes", default="ssm_in,ssm_gate,ssm_out", help="projections for --dense-only")
     ap.add_argument("--dense-tokens", default="1,8", help="token counts for --dense-only")
     return ap.parse_args()
@@ -132,6 +135,22 @@ def time_stages(layers, T: int, reps: int = 20):
         torch.cuda.synchronize()
         out[name] = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
     return out
+
+
+def roofline(layers, stages):
+    """The dominant kernel, k_dec_gateup1 (top-k, routed and shared gate/up, SwiGLU, T = 1):
+    its algorithmic bytes per launch (npu_amd.rocprof_summary.algorithmic_bytes: the k
+    routed and the shared experts' raw gate and up rows, the limb row of the normalised x,
+    the router logits, the k + 1 SwiGLU rows it writes) over the launch period measured by
+    time_stages."""
+    from npu_amd.rocprof_summary import algorithmic_bytes
+    b = layers[0]
+    n = algorithmic_bytes(D, FF, E, K_TOP)["k_dec_gateup1"]
+    assert b.gate[0].numel() == FF * (D // 256 * 136) and b.down[0].numel() == D * (FF // 256 * 98)
+    gbps = n / (stages["gateup_us"] * 1e-6) / 1e9
+    return {"bound": "hbm", "kernel": "k_dec_gateup1 (top-k + routed and shared gate/up + SwiGLU, T=1)",
+            "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gbps / HBM_PEAK_GBPS,
+            "traffic": traffic_bytes("k_dec_gateup1"), "bytes_per_launch": n, "avg_launch_us": stages["gateup_us"]}
 
 
 def run_prefill(layers, T: int = 512, n_blocks: int = 8, reps: int = 5):
@@ -271,7 +290,7 @@ def cpu_baseline(layers, n_sample: int, budget_s: float = 12.0):
     from npu_amd import synth
     from oracle import moe as OM
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_share()
     torch.set_num_threads(threads)
     hosts = []
     for blk in layers[:n_sample]:
@@ -283,7 +302,10 @@ def cpu_baseline(layers, n_sample: int, budget_s: float = 12.0):
             sh_gate_inp=blk.sh_gate_inp.cpu().numpy().view(np.uint16), norm_w=blk.norm_w.cpu().numpy())
         hosts.append(OM.OracleLayer(h))
     x0 = torch.from_numpy(synth.host_input(SEED, 1, D, rmsnorm=False))
-    OM.block_forward(x0, hosts[0], residual=True)          # warm-up (allocations)
+    for _ in range(2):                                      # two untimed warm-up passes over the sample
+        y = x0
+        for L in hosts:
+            y = OM.block_forward(y, L, residual=True)
 
     def passes(pre, budget):
         times, t_start = [], time.perf_counter()
@@ -315,8 +337,29 @@ def cpu_baseline(layers, n_sample: int, budget_s: float = 12.0):
         "block_ms": per_block * 1e3,
         "pre_dequantised_block_ms": statistics.median(t_pre) * 1e3,
         "pre_dequantised_tokens_per_s": 1.0 / (statistics.median(t_pre) * N_LAYERS),
-        "cpu": platform.processor() or platform.machine(), "os_cpu_count": os.cpu_count(),
+        "cpu": cpu_model(), "os_cpu_count": os.cpu_count(), "warmup_passes": 2,
     }
+
+
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo (the architecture where it has none)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_share() -> int:
+    """Threads for the CPU baseline: every core this process may run on.  A GPU host's job
+    scheduler may pin the process to a share of the host (then OMP_NUM_THREADS says how
+    many cores that share holds); without either, all of os.cpu_count()."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(omp)) if omp.isdigit() and int(omp) > 0 else n
 
 
 def traffic_bytes(kernel: str):
@@ -368,6 +411,18 @@ def main() -> int:
         print(json.dumps({"dense_mv": run_dense_mv(dev, shapes=args.dense_shapes.split(","),
                                                    tokens=[int(t) for t in args.dense_tokens.split(",")])}))
         return 0
+    if args.roofline_only:
+        layers = build_layers(args.layers, dev)
+        torch.cuda.synchronize()
+        stages = time_stages(layers, 1)
+        print(json.dumps({"roofline": roofline(layers, stages), "stage_us": stages}))
+        return 0
+    if args.chain_only:
+        layers = build_layers(args.layers, dev)
+        torch.cuda.synchronize()
+        ms1, _, ok1 = run_chain(layers, 1, args.steps, args.warmup, SEED)
+        print(json.dumps({"ms_per_step": ms1, "block_us": ms1 * 1e3 / args.layers, "finite": ok1}))
+        return 0
     if args.batch8_only:
         layers = build_layers(args.layers, dev)
         torch.cuda.synchronize()
@@ -385,7 +440,6 @@ def main() -> int:
     log(f"built {weight_gb:.2f} GB resident in {time.time() - t0:.1f} s")
 
     per_expert = layers[0].gate[0].numel() + layers[0].up[0].numel() + layers[0].down[0].numel()
-    gu_bytes = layers[0].gate[0].numel() + layers[0].up[0].numel()
     fixed = (sum(t.numel() for t in (layers[0].gate_sh, layers[0].up_sh, layers[0].down_sh))
              + layers[0].router.numel() * 2 + layers[0].sh_gate_inp.numel() * 2)
 
@@ -397,10 +451,6 @@ def main() -> int:
     log(f"B=1: {ms1 * 1e3:.1f} us/step, {tok_s:.1f} tok/s, {eff_gbps:.1f} GB/s effective, finite={ok1}")
 
     stages = time_stages(layers, 1)
-    # k_dec_gateup1 algorithmic bytes: the k routed experts' raw gate+up rows, x, the
-    # router logits and the SwiGLU rows it writes
-    gu_launch_bytes = K_TOP * gu_bytes + D * 4 + E * 4 + K_TOP * FF * 4
-    gu_gbps = gu_launch_bytes / (stages["gateup_us"] * 1e-6) / 1e9
     log(f"stages (us): {stages}")
 
     extra = {}
@@ -435,10 +485,7 @@ def main() -> int:
         "effective_weight_frac_of_peak": eff_gbps / HBM_PEAK_GBPS,
         "block_us": ms1 * 1e3 / args.layers,
         "weight_bytes_per_step": bytes1,
-        "roofline": {"bound": "hbm", "kernel": "k_dec_gateup1 (top-k + routed gate/up + SwiGLU, T=1)",
-                     "achieved": gu_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gu_gbps / HBM_PEAK_GBPS,
-                     "traffic": traffic_bytes("k_dec_gateup1"), "bytes_per_launch": gu_launch_bytes,
-                     "avg_launch_us": stages["gateup_us"]},
+        "roofline": roofline(layers, stages),
         "stage_us": stages,
         "cpu_baseline": cpu,
         "finite": ok1,

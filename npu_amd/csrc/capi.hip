@@ -280,9 +280,12 @@ static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int
   const bool decode = path == kPathDecode || (path == kPathAuto && T <= GM_DECODE_MAX_T && T * L->k <= GM_GRP_MAXU);
   if (decode) return gm_dec_run(L, x, y, T, flags, w, lay, s, stage);
   if (stage != 0) return gm_fail_arg("gm_moe_forward_stage: stages are only defined for the decode path (T <= 8)");
-  if (L->q_gate == GM_QTYPE_BF16 || L->q_down == GM_QTYPE_BF16) {
-    // Routed experts held as bf16 (K-quant expert tensors dequantised at load):
-    // the prefill GEMMs take superblock formats only, so the tokens run as
+  const bool sh_mixed = L->gate_sh && (L->q_gate_sh != L->q_gate || L->q_down_sh != L->q_down);
+  if (L->q_gate == GM_QTYPE_BF16 || L->q_down == GM_QTYPE_BF16 || sh_mixed) {
+    // Routed experts held as bf16 (K-quant expert tensors dequantised at load),
+    // or a shared expert in other formats than the routed ones (a dense bf16
+    // shared expert beside IQ routed experts): the prefill GEMMs run the shared
+    // expert as a ninth unit of the routed formats only, so the tokens run as
     // decode chunks of at most 8 (every token's MoE output is independent of
     // the others).  Each chunk writes its logits / ids / weights / shared gate
     // into its rows of the full-T arrays.

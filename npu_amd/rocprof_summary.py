@@ -36,17 +36,24 @@ from pathlib import Path
 
 # Config-5 block shape (BASELINE configs 3 and 5).
 D, FF, E, K = 2048, 512, 256, 8
-IQ4_ROW = D // 256 * 136          # gate/up row, IQ4_XS
-IQ3_ROW = FF // 256 * 98          # down row, IQ3_XXS
 
 
-def algorithmic_bytes() -> dict[str, int]:
+def algorithmic_bytes(d: int = D, ff: int = FF, e: int = E, k: int = K) -> dict[str, int]:
     """Bytes each T = 1 decode kernel must move at least once (weights read, activations
-    read once, outputs written once)."""
+    read once, outputs written once), for a block with IQ4_XS gate/up, IQ3_XXS down, the
+    shared expert in the same formats and an RMSNorm weight.  The limb row of the
+    normalised x is d / 32 sub-blocks of 112 bytes (three int8 planes and a scale).
+      k_dec_router1: router [e, d] bf16, shared scalar gate [d] bf16, x and the RMSNorm
+        weight fp32; writes logits [e], the shared gate and the limb row.
+      k_dec_gateup1: the k routed and the shared experts' gate and up rows, the limb row
+        and the logits; writes k + 1 SwiGLU rows [ff] fp32 and the ids and weights.
+      k_dec_down1: the k routed and the shared down rows, the k + 1 SwiGLU rows, the
+        weights, the shared gate and x (residual); writes y [d]."""
+    iq4_row, iq3_row, limb = d // 256 * 136, ff // 256 * 98, d // 32 * 112
     return {
-        "k_dec_router": E * D * 2 + D * 2 + 2 * FF * IQ4_ROW + D * 4 + E * 4 + 4 + FF * 4,
-        "k_dec_gateup1": K * 2 * FF * IQ4_ROW + D * 4 + E * 4 + K * FF * 4,
-        "k_dec_down1": K * D * IQ3_ROW + D * IQ3_ROW + (K + 1) * FF * 4 + D * 4 + D * 4,
+        "k_dec_router1": e * d * 2 + d * 2 + d * 4 + d * 4 + e * 4 + 4 + limb,
+        "k_dec_gateup1": (k + 1) * 2 * ff * iq4_row + limb + e * 4 + (k + 1) * ff * 4 + 2 * k * 4,
+        "k_dec_down1": (k + 1) * d * iq3_row + (k + 1) * ff * 4 + k * 4 + 4 + d * 4 + d * 4,
     }
 
 

@@ -159,9 +159,11 @@ def test_dequant_kquants_exact(gpu, qtype):
         assert np.array_equal(got, KQ.dequant(b, int(qtype)))
 
 
-def test_tensor_store_kquant_shared_expert(gpu, tmp_path):
+@pytest.mark.parametrize("T", [1, 12])
+def test_tensor_store_kquant_shared_expert(gpu, tmp_path, T):
     """A layer whose shared expert is Q6_K / Q8_0 in the file (as in the real model): the
-    store dequantises it on the device and the block runs it as a dense bf16 expert."""
+    store dequantises it on the device and the block runs it as a dense bf16 expert beside
+    the IQ routed experts, also for T > 8 (decode chunks)."""
     from npu_amd import gguf_file, qwen_moe
     from oracle import kquants as KQ
     rng = np.random.default_rng(7)
@@ -186,15 +188,17 @@ def test_tensor_store_kquant_shared_expert(gpu, tmp_path):
     assert np.array_equal(ts.get("blk.0.ffn_up_shexp.weight"), KQ.dequant(up_sh, KQ.Q8_0).reshape(FF, D))
     layer = qwen_moe.MoELayer.load(ts, 0)
     assert layer.w_gate_sh is not None and layer.w_gate_sh.shape == (FF, D)
-    x = torch.from_numpy(synth.host_input(3, 1, D)).reshape(1, 1, D)
+    x = torch.from_numpy(synth.host_input(3, T, D)).reshape(1, T, D)
+    ol = OM.OracleLayer(h)
+    assert bool((OM.topk_margin(OM.router_logits64(x.reshape(T, D), ol), h.k) > 1e-5).all())
     y = qwen_moe.moe_forward(x, layer, ts.cfg)
     # reference: routed part from the oracle, shared expert in fp64 from the dequantised weights
-    routed = OM.moe_forward(x, OM.OracleLayer(h)).double()
-    xs = x.reshape(1, D).double()
+    routed = OM.moe_forward(x, ol).double()
+    xs = x.reshape(T, D).double()
     gs, us, ds = (torch.from_numpy(KQ.dequant(a, t).reshape(shp)).double() for a, t, shp in
                   ((gate_sh, KQ.Q6_K, (FF, D)), (up_sh, KQ.Q8_0, (FF, D)), (down_sh, KQ.Q6_K, (D, FF))))
     # the device block runs the dense shared expert in bf16 weights: compare at the bf16 bar
     hsh = F.silu(xs @ gs.T) * (xs @ us.T)
     sgate = torch.sigmoid(xs @ torch.full((D,), 0.01, dtype=torch.float64))
-    ref = routed.reshape(1, D) + sgate * (hsh @ ds.T)
-    assert OM.rel_err(y.reshape(1, D).double(), ref) <= 1e-2
+    ref = routed.reshape(T, D) + sgate[:, None] * (hsh @ ds.T)
+    assert OM.rel_err(y.reshape(T, D).double(), ref) <= 1e-2
