@@ -122,14 +122,15 @@ typedef struct gm_moe_layer {
   const void* gate_sh;          /* [FF_sh][row_bytes(q_gate_sh, D)] */
   const void* up_sh;            /* [FF_sh][row_bytes(q_up_sh, D)] */
   const void* down_sh;          /* [D][row_bytes(q_down_sh, FF_sh)] */
-  const uint16_t* router;       /* bf16 bits [E][D] */
-  const uint16_t* sh_gate_inp;  /* bf16 bits [D] (shared-expert scalar gate) */
+  const void* router;           /* [E][D] in q_router: bf16 bits, or fp32 as the GGUF holds it */
+  const void* sh_gate_inp;      /* [D] in q_router (shared-expert scalar gate), or NULL */
   const float* router_bias;     /* [E] added to logits, or NULL (not in the reference model) */
   const float* norm_w;          /* [D] RMSNorm weight applied to x, or NULL */
   float norm_eps;
   int32_t q_gate, q_up, q_down;
   int32_t q_gate_sh, q_up_sh, q_down_sh;
   int32_t D, FF, FF_sh, E, k;
+  int32_t q_router;             /* GM_QTYPE_BF16 or GM_QTYPE_F32 (= 0): format of router and sh_gate_inp */
 } gm_moe_layer;
 
 /* Workspace bytes gm_moe_forward needs for T tokens (0 on bad arguments). */

@@ -49,6 +49,7 @@ class GmMoeLayer(ctypes.Structure):
         ("q_gate", _i32), ("q_up", _i32), ("q_down", _i32),
         ("q_gate_sh", _i32), ("q_up_sh", _i32), ("q_down_sh", _i32),
         ("D", _i32), ("FF", _i32), ("FF_sh", _i32), ("E", _i32), ("k", _i32),
+        ("q_router", _i32),
     ]
 
 
@@ -85,7 +86,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(h, name)
             fn.restype = res
             fn.argtypes = args
-        if h.gm_abi_version() != 1:
+        if h.gm_abi_version() != 2:
             raise RuntimeError("libnpu_amd.so ABI version mismatch; rebuild it")
         _LIB = h
     return _LIB

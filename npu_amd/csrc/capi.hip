@@ -70,6 +70,8 @@ static int check_layer(const gm_moe_layer* L) {
                        "IQ4_XS, IQ3_XXS or BF16)", L->q_gate, L->q_up, L->q_down);
   if (L->D % GM_QK || L->FF % GM_QK)
     return gm_fail_arg("gm_moe_forward: D=%d and FF=%d must be multiples of %d", L->D, L->FF, GM_QK);
+  if (L->q_router != GM_QTYPE_BF16 && L->q_router != GM_QTYPE_F32)
+    return gm_fail_arg("gm_moe_forward: q_router=%d must be GM_QTYPE_BF16 or GM_QTYPE_F32", L->q_router);
   const bool has_sh = L->gate_sh || L->up_sh || L->down_sh;
   if (has_sh) {
     if (!L->gate_sh || !L->up_sh || !L->down_sh)
@@ -92,7 +94,7 @@ extern "C" {
 
 const char* gm_last_error(void) { return g_err; }
 
-int gm_abi_version(void) { return 1; }
+int gm_abi_version(void) { return 2; }
 
 int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out, void* stream) {
   if (gm_kquant_block(qtype).bytes)

@@ -365,6 +365,48 @@ __device__ __forceinline__ void block_group(const int32_t* __restrict__ ids, int
 // independent passes to bound register pressure.
 __device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// ------------------------------------------------------------ router rows
+// The router and the shared scalar gate come as bf16 bits or as fp32
+// (gm_moe_layer.q_router; the reference reads both in fp32,
+// qwen/forward.py:41-47, 599, 608).  A lane takes 8 consecutive values of a
+// row: one 16-byte load of bf16, two of fp32.
+template <bool F32>
+using RouterChunk = gm_u32x4[F32 ? 2 : 1];
+
+template <bool F32>
+__device__ __forceinline__ const void* router_row(const void* base, int64_t row, int D) {
+  return static_cast<const char*>(base) + row * D * (F32 ? 4 : 2);
+}
+
+template <bool F32, bool ST>
+__device__ __forceinline__ void router_load8(const void* row, int kk, RouterChunk<F32>& r) {
+  if constexpr (F32) {
+    const gm_u32x4* p = reinterpret_cast<const gm_u32x4*>(static_cast<const float*>(row) + kk);
+    r[0] = gm_ld<ST>(p);
+    r[1] = gm_ld<ST>(p + 1);
+  } else {
+    r[0] = gm_ld<ST>(reinterpret_cast<const gm_u32x4*>(static_cast<const uint16_t*>(row) + kk));
+  }
+}
+
+template <bool F32>
+__device__ __forceinline__ void router_unpack8(const RouterChunk<F32>& r, float (&w)[8]) {
+  if constexpr (F32) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      w[4 * h + 0] = __uint_as_float(r[h].x);
+      w[4 * h + 1] = __uint_as_float(r[h].y);
+      w[4 * h + 2] = __uint_as_float(r[h].z);
+      w[4 * h + 3] = __uint_as_float(r[h].w);
+    }
+  } else {
+    const uint32_t v[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      w[j] = (j & 1) ? __uint_as_float(v[j >> 1] & 0xffff0000u) : __uint_as_float(v[j >> 1] << 16);
+  }
+}
+
 // --------------------------------------------------------- row streaming
 // The decode kernels issue every weight load a lane needs before they wait on
 // anything: SPL sub-blocks per lane and row, at sub = lir + LR * i.  Indices

@@ -1,7 +1,7 @@
 // MoE block, decode path (T <= 8 tokens).  Reference semantics:
 // qwen/forward.py:563-665 (moe_forward).
 //
-// Stage 1  T = 1: k_dec_router1: router logits (bf16 W, fp32 RMSNorm'd x), the
+// Stage 1  T = 1: k_dec_router1: router logits (bf16 or fp32 W, fp32 RMSNorm'd x), the
 //                         shared scalar gate and the limb row of the RMSNorm'd
 //                         x for the gate/up kernel.
 //          T > 1: k_dec_router_ks: partial router dot products over K ranges
@@ -32,7 +32,7 @@ namespace {
 // reduction; it scales the finished dot product W . (x * w_norm).  Global waves
 // i < NCH also write chunk i of the limb row of xn = (x * rms) * w_norm that
 // the gate/up kernel multiplies with.
-template <int NCH>
+template <int NCH, bool RF32>
 __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float* __restrict__ x,
                                                      float* __restrict__ logits, float* __restrict__ shg,
                                                      uint8_t* __restrict__ xl_out GM_TL_PARAM) {
@@ -40,13 +40,13 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
   const int lane = threadIdx.x & 63, gw = blockIdx.x * 2 + (threadIdx.x >> 6);
   const int D = P.D, E = P.E, nrows = E + (P.sh_gate_inp != nullptr ? 1 : 0);
   const int row = gw < nrows ? gw : nrows - 1;                  // spare waves redo the last row
-  const uint16_t* wr = row < E ? P.router + (int64_t)row * D : P.sh_gate_inp;
-  gm_u32x4 wb[NCH];
+  const void* wr = row < E ? router_row<RF32>(P.router, row, D) : P.sh_gate_inp;
+  RouterChunk<RF32> wb[NCH];
   gm_f32x4 xa[NCH], xb[NCH], na[NCH], nb[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int kk = 512 * i + 8 * lane < D ? 512 * i + 8 * lane : D - 8;   // lanes past D re-read the end
-    wb[i] = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(wr + kk));
+    router_load8<RF32, true>(wr, kk, wb[i]);
     xa[i] = *reinterpret_cast<const gm_f32x4*>(x + kk);
     xb[i] = *reinterpret_cast<const gm_f32x4*>(x + kk + 4);
     if (P.norm_w) {
@@ -64,11 +64,11 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
     if (512 * i + 8 * lane < D) {
       const float xv[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
       const float nv[8] = {na[i].x, na[i].y, na[i].z, na[i].w, nb[i].x, nb[i].y, nb[i].z, nb[i].w};
-      const uint32_t wv[4] = {wb[i].x, wb[i].y, wb[i].z, wb[i].w};
+      float w[8];
+      router_unpack8<RF32>(wb[i], w);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float w = (j & 1) ? __uint_as_float(wv[j >> 1] & 0xffff0000u) : __uint_as_float(wv[j >> 1] << 16);
-        dot = fmaf(w, xv[j] * nv[j], dot);
+        dot = fmaf(w[j], xv[j] * nv[j], dot);
         ss = fmaf(xv[j], xv[j], ss);
       }
     }
@@ -107,7 +107,7 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
 // Wave 0 of the first row block of each range also writes the limb rows of
 // x w_norm for the range (the RMSNorm factor is applied to the dot products
 // instead), so the grouped gate/up kernel only copies them.
-template <int NT>
+template <int NT, bool RF32>
 __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const float* __restrict__ x, int T,
                                                        float* __restrict__ part, float* __restrict__ ssq, int ldp,
                                                        int kr, uint8_t* __restrict__ xl) {
@@ -117,8 +117,9 @@ __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const flo
   const bool lv = 8 * lane < kr;
   const int kk = lv ? k0 : z * kr;                              // lanes past the range re-read its start
   const int row = blockIdx.x * 4 + wave;
-  const uint16_t* wr = row < E ? P.router + (int64_t)row * D : (row < nrows ? P.sh_gate_inp : P.router);
-  const gm_u32x4 wb = *reinterpret_cast<const gm_u32x4*>(wr + kk);        // 8 bf16
+  const void* wr = row < E ? router_row<RF32>(P.router, row, D) : (row < nrows ? P.sh_gate_inp : P.router);
+  RouterChunk<RF32> wb;
+  router_load8<RF32, false>(wr, kk, wb);
   gm_f32x4 nw0 = {1.f, 1.f, 1.f, 1.f}, nw1 = nw0;
   if (P.norm_w) {
     nw0 = *reinterpret_cast<const gm_f32x4*>(P.norm_w + kk);
@@ -131,8 +132,8 @@ __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const flo
     xa[m] = *reinterpret_cast<const gm_f32x4*>(x + (int64_t)t * D + kk);
     xb[m] = *reinterpret_cast<const gm_f32x4*>(x + (int64_t)t * D + kk + 4);
   }
-  const float w[8] = {gm_bf2f(wb.x & 0xffffu), gm_bf2f(wb.x >> 16), gm_bf2f(wb.y & 0xffffu), gm_bf2f(wb.y >> 16),
-                      gm_bf2f(wb.z & 0xffffu), gm_bf2f(wb.z >> 16), gm_bf2f(wb.w & 0xffffu), gm_bf2f(wb.w >> 16)};
+  float w[8];
+  router_unpack8<RF32>(wb, w);
   if (blockIdx.x == 0 && wave == 0) {                           // uniform per wave
     const int rbytes = gm_limb_row_bytes(D);
 #pragma unroll
@@ -164,28 +165,36 @@ __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const flo
   }
 }
 
-int launch_router(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s, bool fast1) {
+template <bool RF32>
+int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s, bool fast1) {
   const int nrows = P->E + (P->sh_gate_inp ? 1 : 0);
   if (!fast1) {                                                      // router partials only
     const int kr = gm_dec_kr(P->D);
-    hipLaunchKernelGGL(k_dec_router_ks<8>, dim3((nrows + 3) / 4, P->D / kr), dim3(256), 0, s, *P, x, T, a.part,
-                       a.ssq, gm_dec_part_ld(P), kr, a.xl);
+    hipLaunchKernelGGL((k_dec_router_ks<8, RF32>), dim3((nrows + 3) / 4, P->D / kr), dim3(256), 0, s, *P, x, T,
+                       a.part, a.ssq, gm_dec_part_ld(P), kr, a.xl);
     GM_TRY(hipGetLastError());
     return GM_OK;
   }
   const dim3 grid((nrows + 1) / 2);
+#define GM_R1(n) hipLaunchKernelGGL((k_dec_router1<n, RF32>), grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl))
   switch ((P->D + 511) / 512) {
-    case 1: hipLaunchKernelGGL(k_dec_router1<1>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
-    case 2: hipLaunchKernelGGL(k_dec_router1<2>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
-    case 3: hipLaunchKernelGGL(k_dec_router1<3>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
-    case 4: hipLaunchKernelGGL(k_dec_router1<4>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
-    case 5: hipLaunchKernelGGL(k_dec_router1<5>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
-    case 6: hipLaunchKernelGGL(k_dec_router1<6>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
-    case 7: hipLaunchKernelGGL(k_dec_router1<7>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
-    default: hipLaunchKernelGGL(k_dec_router1<8>, grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl)); break;
+    case 1: GM_R1(1); break;
+    case 2: GM_R1(2); break;
+    case 3: GM_R1(3); break;
+    case 4: GM_R1(4); break;
+    case 5: GM_R1(5); break;
+    case 6: GM_R1(6); break;
+    case 7: GM_R1(7); break;
+    default: GM_R1(8); break;
   }
+#undef GM_R1
   GM_TRY(hipGetLastError());
   return GM_OK;
+}
+
+int launch_router(const gm_moe_layer* P, const float* x, int T, const GmDecArgs& a, hipStream_t s, bool fast1) {
+  return P->q_router == GM_QTYPE_F32 ? launch_router_t<true>(P, x, T, a, s, fast1)
+                                     : launch_router_t<false>(P, x, T, a, s, fast1);
 }
 
 }  // namespace

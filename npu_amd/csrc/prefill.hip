@@ -39,6 +39,7 @@ typedef __bf16 gm_bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 gm_f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 gm_f16x2 __attribute__((ext_vector_type(2)));
 typedef float gm_f32x2 __attribute__((ext_vector_type(2)));
+typedef float gm_f32x8 __attribute__((ext_vector_type(8)));
 
 namespace {
 
@@ -225,17 +226,48 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
 // MFMA operand layout (16x16x32): lane l holds row / column l % 16 at
 // k = 8 (l / 16) .. +7.
 
-__device__ __forceinline__ void router_step(const gm_u32x4 (&a)[4], const gm_u32x4 (&b)[3], gm_f32x4 (&acc)[4]) {
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int p = 0; p < 3; ++p)
-      acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gm_bf16x8, a[rt]),
-                                                        __builtin_bit_cast(gm_bf16x8, b[p]), acc[rt], 0, 0, 0);
+// An fp32 router (RF32) is split in registers into three bf16 pieces,
+// w = w0 + w1 + w2 exactly (each piece holds the next 8 significant bits of
+// the 24; exact unless |w| < 2^-100, where bf16 subnormals cut the last
+// piece), and all nine piece products are accumulated.
+__device__ __forceinline__ void split3_bf16(const gm_u32x4 (&r)[2], gm_bf16x8 (&o)[3]) {
+  gm_f32x8 v;
+  v[0] = __uint_as_float(r[0].x); v[1] = __uint_as_float(r[0].y);
+  v[2] = __uint_as_float(r[0].z); v[3] = __uint_as_float(r[0].w);
+  v[4] = __uint_as_float(r[1].x); v[5] = __uint_as_float(r[1].y);
+  v[6] = __uint_as_float(r[1].z); v[7] = __uint_as_float(r[1].w);
+  o[0] = __builtin_convertvector(v, gm_bf16x8);
+  const gm_f32x8 r0 = v - __builtin_convertvector(o[0], gm_f32x8);
+  o[1] = __builtin_convertvector(r0, gm_bf16x8);
+  const gm_f32x8 r1 = r0 - __builtin_convertvector(o[1], gm_f32x8);
+  o[2] = __builtin_convertvector(r1, gm_bf16x8);
 }
 
-template <int NK>
-__global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ w, const uint16_t* __restrict__ wsh,
+template <bool RF32>
+__device__ __forceinline__ void router_step(const gm_u32x4 (&a)[4][RF32 ? 2 : 1], const gm_u32x4 (&b)[3],
+                                            gm_f32x4 (&acc)[4]) {
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) {
+    if constexpr (RF32) {
+      gm_bf16x8 ap[3];
+      split3_bf16(a[rt], ap);
+#pragma unroll
+      for (int pa = 0; pa < 3; ++pa)
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+          acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap[pa], __builtin_bit_cast(gm_bf16x8, b[p]), acc[rt], 0,
+                                                            0, 0);
+    } else {
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gm_bf16x8, a[rt][0]),
+                                                          __builtin_bit_cast(gm_bf16x8, b[p]), acc[rt], 0, 0, 0);
+    }
+  }
+}
+
+template <int NK, bool RF32>
+__global__ void __launch_bounds__(256) k_pf_router(const void* __restrict__ w, const void* __restrict__ wsh,
                                                    const uint16_t* __restrict__ xr, int T, int D, int E, int ldp,
                                                    float* __restrict__ part) {
   __shared__ gm_f32x4 red[3][4][64];
@@ -247,14 +279,17 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
   const int k0 = (blockIdx.z * 4 + wave) * (32 * NK);
   const int64_t plane = (int64_t)T * D / 8;                     // in 16-byte units
   const gm_u32x4* brow = reinterpret_cast<const gm_u32x4*>(xr + (int64_t)tokc * D + k0 + 8 * q);
-  gm_u32x4 a[NK][4], b[NK][3];
+  constexpr int RW = RF32 ? 2 : 1;                              // 16-byte loads per 8 weights
+  gm_u32x4 a[NK][4][RW], b[NK][3];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) {
     const int row = r0 + rt * 16 + l16;
-    const uint16_t* pr = row < E ? w + (int64_t)row * D : (row == E && wsh ? wsh : w);
-    const gm_u32x4* ar = reinterpret_cast<const gm_u32x4*>(pr + k0 + 8 * q);
+    const void* pr = row < E ? router_row<RF32>(w, row, D) : (row == E && wsh ? wsh : w);
+    const gm_u32x4* ar = reinterpret_cast<const gm_u32x4*>(static_cast<const char*>(pr) + (k0 + 8 * q) * 2 * RW);
 #pragma unroll
-    for (int ks = 0; ks < NK; ++ks) a[ks][rt] = ar[4 * ks];
+    for (int ks = 0; ks < NK; ++ks)
+#pragma unroll
+      for (int h = 0; h < RW; ++h) a[ks][rt][h] = ar[4 * RW * ks + h];
   }
 #pragma unroll
   for (int ks = 0; ks < NK; ++ks)
@@ -264,7 +299,7 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) acc[rt] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < NK; ++ks) router_step(a[ks], b[ks], acc);
+  for (int ks = 0; ks < NK; ++ks) router_step<RF32>(a[ks], b[ks], acc);
   if (wave > 0) {
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) red[wave - 1][rt][lane] = acc[rt];
@@ -954,12 +989,18 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
   GM_TRY(hipGetLastError());
   const int ldp = router_ld(L);
   const int nsplit = router_split(D);
-  if (router_krange(D) == 512)
-    hipLaunchKernelGGL(k_pf_router<4>, dim3((nrows + 63) / 64, (T + 15) / 16, nsplit), dim3(256), 0, s, L->router,
-                       L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
-  else
-    hipLaunchKernelGGL(k_pf_router<2>, dim3((nrows + 63) / 64, (T + 15) / 16, nsplit), dim3(256), 0, s, L->router,
-                       L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
+  {
+    const dim3 g((nrows + 63) / 64, (T + 15) / 16, nsplit);
+    const bool f32 = L->q_router == GM_QTYPE_F32;
+    if (router_krange(D) == 512 && f32)
+      hipLaunchKernelGGL((k_pf_router<4, true>), g, dim3(256), 0, s, L->router, L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
+    else if (router_krange(D) == 512)
+      hipLaunchKernelGGL((k_pf_router<4, false>), g, dim3(256), 0, s, L->router, L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
+    else if (f32)
+      hipLaunchKernelGGL((k_pf_router<2, true>), g, dim3(256), 0, s, L->router, L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
+    else
+      hipLaunchKernelGGL((k_pf_router<2, false>), g, dim3(256), 0, s, L->router, L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
+  }
   GM_TRY(hipGetLastError());
   {
     const int hg = L->sh_gate_inp ? 1 : 0;

@@ -52,6 +52,19 @@ def _kquant_to_bf16(raw: torch.Tensor, q: int, n: int, M: int, K: int) -> torch.
     return out if raw.dim() == 3 else out[0]
 
 
+def _router_fmt(t: torch.Tensor | None, f32: bool) -> torch.Tensor | None:
+    """bf16 bits (int16) or fp32 on the device; bf16 input widened exactly when f32."""
+    if t is None:
+        return None
+    if t.dtype in (torch.int16, torch.uint16):
+        t = t.view(torch.bfloat16) if t.dtype == torch.int16 else t.view(torch.int16).view(torch.bfloat16)
+    if f32:
+        return t.to(torch.float32).contiguous()
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"router / sh_gate_inp: expected bf16 or fp32, got {t.dtype}")
+    return t.contiguous().view(torch.int16)
+
+
 class GpuMoeBlock:
     """One MoE block resident on the GPU."""
 
@@ -67,9 +80,17 @@ class GpuMoeBlock:
         self.gate = _dev(gate, device=device)
         self.up = _dev(up, device=device)
         self.down = _dev(down, device=device)
+        # Router and shared scalar gate: bf16 (bits as int16 / uint16, or torch.bfloat16) or
+        # fp32, as the file holds them (the reference reads both in fp32,
+        # qwen/forward.py:41-47).  Both go to the device in one format: fp32 when
+        # either is fp32 (widening bf16 is exact).
         self.router = _dev(router, device=device)
-        if self.router.dtype == torch.bfloat16:
-            self.router = self.router.view(torch.int16)
+        self.sh_gate_inp = _dev(sh_gate_inp, device=device)
+        f32 = self.router.dtype == torch.float32 or (self.sh_gate_inp is not None
+                                                      and self.sh_gate_inp.dtype == torch.float32)
+        self.q_router = QT.F32 if f32 else QT.BF16
+        self.router = _router_fmt(self.router, f32)
+        self.sh_gate_inp = _router_fmt(self.sh_gate_inp, f32)
         self.gate_sh = _dev(gate_sh, device=device)
         self.up_sh = _dev(up_sh, device=device)
         self.down_sh = _dev(down_sh, device=device)
@@ -96,9 +117,6 @@ class GpuMoeBlock:
             self.gate, self.up = self.gate.view(torch.int16), self.up.view(torch.int16)
         if self.q_down == QT.BF16 and self.down.dtype == torch.bfloat16:
             self.down = self.down.view(torch.int16)
-        self.sh_gate_inp = _dev(sh_gate_inp, device=device)
-        if self.sh_gate_inp is not None and self.sh_gate_inp.dtype == torch.bfloat16:
-            self.sh_gate_inp = self.sh_gate_inp.view(torch.int16)
         self.router_bias = _dev(router_bias, torch.float32, device)
         self.norm_w = _dev(norm_w, torch.float32, device)
         self.norm_eps = float(norm_eps)
@@ -114,6 +132,7 @@ class GpuMoeBlock:
         s.q_gate_sh = s.q_up_sh = self.q_gate_sh
         s.q_down_sh = self.q_down_sh
         s.D, s.FF, s.FF_sh, s.E, s.k = self.D, self.FF, self.FF if self.gate_sh is not None else 0, self.E, self.k
+        s.q_router = int(self.q_router)
         self.struct = s
         self._ws: torch.Tensor | None = None
 
@@ -194,5 +213,5 @@ class GpuMoeBlock:
         sh = 0
         if self.gate_sh is not None:
             sh = sum(t.numel() * t.element_size() for t in (self.gate_sh, self.up_sh, self.down_sh))
-        g = 0 if self.sh_gate_inp is None else self.sh_gate_inp.numel() * 2
-        return self.k * per_exp + sh + self.router.numel() * 2 + g
+        g = 0 if self.sh_gate_inp is None else self.sh_gate_inp.numel() * self.sh_gate_inp.element_size()
+        return self.k * per_exp + sh + self.router.numel() * self.router.element_size() + g

@@ -76,10 +76,10 @@ class SyntheticTensorStore:
                 self._raw[p + "ffn_gate_shexp.weight"] = QuantTensor(p + "ffn_gate_shexp.weight", L.q_gate, (L.D, L.FF), L.gate_sh)
                 self._raw[p + "ffn_up_shexp.weight"] = QuantTensor(p + "ffn_up_shexp.weight", L.q_gate, (L.D, L.FF), L.up_sh)
                 self._raw[p + "ffn_down_shexp.weight"] = QuantTensor(p + "ffn_down_shexp.weight", L.q_down, (L.FF, L.D), L.down_sh)
-            from npu_amd.synth import from_bf16
-            self._dense[p + "ffn_gate_inp.weight"] = from_bf16(L.router).reshape(L.E, L.D)
+            from npu_amd.synth import as_f32
+            self._dense[p + "ffn_gate_inp.weight"] = as_f32(L.router).reshape(L.E, L.D)
             if L.sh_gate_inp is not None:
-                self._dense[p + "ffn_gate_inp_shexp.weight"] = from_bf16(L.sh_gate_inp)
+                self._dense[p + "ffn_gate_inp_shexp.weight"] = as_f32(L.sh_gate_inp)
             if L.norm_w is not None:
                 self._dense[p + "post_attention_norm.weight"] = L.norm_w
             if L.router_bias is not None:
@@ -167,6 +167,14 @@ class MoELayer:
         return tuple(out)
 
 
+def _exact_bf16_or_f32(w: torch.Tensor) -> torch.Tensor:
+    """fp32 weights as bf16 when every value is a bf16 value (half the bytes, same
+    numbers), else unchanged fp32."""
+    w = torch.as_tensor(w).float().contiguous()
+    b = w.to(torch.bfloat16)
+    return b if torch.equal(b.float(), w) else w
+
+
 def _build_block(layer: MoELayer) -> GpuMoeBlock:
     ts = layer.ts
     p = f"blk.{layer.i}."
@@ -176,7 +184,9 @@ def _build_block(layer: MoELayer) -> GpuMoeBlock:
     D, FF, E = int(g.shape[0]), int(g.shape[1]), int(g.shape[2])
     cfg = getattr(ts, "cfg", None)
     k = int(getattr(cfg, "n_expert_used", 8))
-    router = torch.from_numpy(np.ascontiguousarray(layer.w_router.float().numpy())).to(torch.bfloat16)
+    # The router and the shared gate keep the fp32 values the reference computes with
+    # (qwen/forward.py:41-47, 599, 608); they are stored as bf16 only when that is exact.
+    router = _exact_bf16_or_f32(layer.w_router)
     kw = {}
     if layer.w_gate_sh is not None:              # dense shared expert (the real model): bf16
         kw.update(gate_sh=layer.w_gate_sh.to(torch.bfloat16), up_sh=layer.w_up_sh.to(torch.bfloat16),
@@ -188,7 +198,7 @@ def _build_block(layer: MoELayer) -> GpuMoeBlock:
                   q_down_sh=int(ds.tensor_type))
     sh_inp = None
     if layer.w_gate_inp_sh is not None:
-        sh_inp = layer.w_gate_inp_sh.float().to(torch.bfloat16)
+        sh_inp = _exact_bf16_or_f32(layer.w_gate_inp_sh)
     bias = torch.from_numpy(ts.get(p + "ffn_gate_inp.bias")) if ts.has(p + "ffn_gate_inp.bias") else None
     return GpuMoeBlock(gate=g.data, up=u.data, down=d.data, router=router, q_gate=int(g.tensor_type),
                        q_down=int(d.tensor_type), D=D, FF=FF, E=E, k=k, sh_gate_inp=sh_inp, router_bias=bias,

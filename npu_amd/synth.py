@@ -41,6 +41,11 @@ def from_bf16(b: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def as_f32(a: np.ndarray) -> np.ndarray:
+    """A router / shared-gate array held as bf16 bits (uint16) or fp32, as fp32."""
+    return np.ascontiguousarray(a) if np.asarray(a).dtype == np.float32 else from_bf16(a)
+
+
 def _gen(seed: int, *stream: int) -> np.random.Generator:
     return np.random.Generator(np.random.PCG64(np.random.SeedSequence([int(seed), *map(int, stream)])))
 
@@ -117,11 +122,11 @@ class HostMoeLayer:
     gate: np.ndarray          # uint8 [E, FF, row_bytes(q_gate, D)]
     up: np.ndarray            # uint8 [E, FF, row_bytes(q_gate, D)]
     down: np.ndarray          # uint8 [E, D, row_bytes(q_down, FF)]
-    router: np.ndarray        # uint16 bf16 bits [E, D]
+    router: np.ndarray        # [E, D] bf16 bits (uint16) or float32
     gate_sh: np.ndarray | None = None   # uint8 [FF, row_bytes(q_gate, D)]
     up_sh: np.ndarray | None = None
     down_sh: np.ndarray | None = None   # uint8 [D, row_bytes(q_down, FF)]
-    sh_gate_inp: np.ndarray | None = None  # uint16 bf16 bits [D]
+    sh_gate_inp: np.ndarray | None = None  # [D] bf16 bits (uint16) or float32
     router_bias: np.ndarray | None = None  # float32 [E]
     norm_w: np.ndarray | None = None       # float32 [D]
     meta: dict = field(default_factory=dict)
@@ -140,20 +145,26 @@ class HostMoeLayer:
 
 def host_moe_layer(seed: int, *, D: int = 2048, FF: int = 512, E: int = 256, k: int = 8,
                    q_gate: int = QT.IQ4_XS, q_down: int = QT.IQ3_XXS, shared: bool = True,
-                   bias: bool = False, norm: bool = False) -> HostMoeLayer:
-    """Config-3/4 style MoE block (defaults: BASELINE's IQ4_XS gate/up, IQ3_XXS down)."""
+                   bias: bool = False, norm: bool = False, router_f32: bool = False) -> HostMoeLayer:
+    """Config-3/4 style MoE block (defaults: BASELINE's IQ4_XS gate/up, IQ3_XXS down, bf16
+    router and shared gate).  ``router_f32``: router and shared gate N(0, 0.02) in fp32, as
+    a GGUF file's F32 ``ffn_gate_inp`` holds them (values that bf16 cannot represent)."""
+    def small(gen, shape):
+        if router_f32:
+            return (gen.standard_normal(shape) * ROUTER_STD).astype(np.float32)
+        return host_bf16_normal(gen, shape, ROUTER_STD)
     L = HostMoeLayer(
         D=D, FF=FF, E=E, k=k, q_gate=int(q_gate), q_down=int(q_down),
         gate=host_quant_matrix(_gen(seed, 1), q_gate, FF, D, E),
         up=host_quant_matrix(_gen(seed, 2), q_gate, FF, D, E),
         down=host_quant_matrix(_gen(seed, 3), q_down, D, FF, E),
-        router=host_bf16_normal(_gen(seed, 4), (E, D), ROUTER_STD),
+        router=small(_gen(seed, 4), (E, D)),
     )
     if shared:
         L.gate_sh = host_quant_matrix(_gen(seed, 5), q_gate, FF, D)
         L.up_sh = host_quant_matrix(_gen(seed, 6), q_gate, FF, D)
         L.down_sh = host_quant_matrix(_gen(seed, 7), q_down, D, FF)
-        L.sh_gate_inp = host_bf16_normal(_gen(seed, 8), (D,), ROUTER_STD)
+        L.sh_gate_inp = small(_gen(seed, 8), (D,))
     if bias:
         L.router_bias = _gen(seed, 9).standard_normal(E).astype(np.float32)
     if norm:
@@ -228,12 +239,12 @@ def write_gguf_model(path, layers, *, arch: str = "qwen3next", rms_eps: float = 
         tensors += [(p + "ffn_gate_exps.weight", L.q_gate, (L.D, L.FF, L.E), L.gate),
                     (p + "ffn_up_exps.weight", L.q_gate, (L.D, L.FF, L.E), L.up),
                     (p + "ffn_down_exps.weight", L.q_down, (L.FF, L.D, L.E), L.down),
-                    (p + "ffn_gate_inp.weight", int(QT.F32), (L.D, L.E), from_bf16(L.router).reshape(L.E, L.D))]
+                    (p + "ffn_gate_inp.weight", int(QT.F32), (L.D, L.E), as_f32(L.router).reshape(L.E, L.D))]
         if L.gate_sh is not None:
             tensors += [(p + "ffn_gate_shexp.weight", L.q_gate, (L.D, L.FF), L.gate_sh),
                         (p + "ffn_up_shexp.weight", L.q_gate, (L.D, L.FF), L.up_sh),
                         (p + "ffn_down_shexp.weight", L.q_down, (L.FF, L.D), L.down_sh),
-                        (p + "ffn_gate_inp_shexp.weight", int(QT.F32), (L.D,), from_bf16(L.sh_gate_inp))]
+                        (p + "ffn_gate_inp_shexp.weight", int(QT.F32), (L.D,), as_f32(L.sh_gate_inp))]
         if L.router_bias is not None:
             tensors.append((p + "ffn_gate_inp.bias", int(QT.F32), (L.E,), L.router_bias))
         if L.norm_w is not None:

@@ -39,6 +39,12 @@ def from_bf16(b: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(b).view(np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def _f32(a: np.ndarray) -> np.ndarray:
+    """Router / shared-gate weights as fp32: fp32 arrays as they are, bf16 bits widened
+    (the reference reads both tensors in fp32, qwen/forward.py:41-47)."""
+    return np.ascontiguousarray(a, dtype=np.float32) if np.asarray(a).dtype == np.float32 else from_bf16(a)
+
+
 def rms_norm(x: torch.Tensor, w: torch.Tensor | None, eps: float) -> torch.Tensor:
     """qwen/forward.py:58-61 (w=None means weight 1)."""
     x_f = x.float()
@@ -54,8 +60,8 @@ class OracleLayer:
 
     def __init__(self, h):
         self.h = h
-        self.w_router = torch.from_numpy(from_bf16(h.router).reshape(h.E, h.D).copy())
-        self.w_gate_inp_sh = (torch.from_numpy(from_bf16(h.sh_gate_inp).copy())
+        self.w_router = torch.from_numpy(_f32(h.router).reshape(h.E, h.D).copy())
+        self.w_gate_inp_sh = (torch.from_numpy(_f32(h.sh_gate_inp).copy())
                               if h.sh_gate_inp is not None else None)
         self.has_shared = h.gate_sh is not None
         self.bias = torch.from_numpy(h.router_bias.copy()) if h.router_bias is not None else None

@@ -95,9 +95,11 @@ def test_qwen_moe_forward_dropin(gpu, T):
 def test_qwen_moe_forward_from_gguf_file(gpu, tmp_path, T):
     """The MoE drop-in fed from a GGUF file read by npu_amd.gguf_file (the reference reads
     its model through gguf-py's GGUFReader + TensorStore, qwen/model.py:164-277): raw
-    expert superblocks mapped from the file straight to HBM, router / shared gate from F32."""
+    expert superblocks mapped from the file straight to HBM, router / shared gate from F32
+    tensors holding values bf16 cannot represent (kept in fp32 on the device: top-k ids
+    equal to the oracle's, which reads them in fp32 as the reference does)."""
     from npu_amd import gguf_file
-    hs = [synth.host_moe_layer(60 + i, D=1024, FF=256, E=32, k=4, q_gate=q, q_down=d)
+    hs = [synth.host_moe_layer(60 + i, D=1024, FF=256, E=32, k=4, q_gate=q, q_down=d, router_f32=True)
           for i, (q, d) in enumerate([(QT.IQ4_XS, QT.IQ3_XXS), (QT.IQ3_XXS, QT.IQ4_XS)])]
     path = tmp_path / "moe.gguf"
     synth.write_gguf_model(path, hs)
@@ -107,8 +109,13 @@ def test_qwen_moe_forward_from_gguf_file(gpu, tmp_path, T):
     x = torch.from_numpy(synth.host_input(11, T, 1024)).reshape(1, T, 1024)
     for i, L in enumerate(layers):
         y = qwen_moe.moe_forward(x, L, ts.cfg)
-        ref = OM.moe_forward(x, OM.OracleLayer(hs[i]))
+        ol, st = OM.OracleLayer(hs[i]), {}
+        ref = OM.moe_forward(x, ol, stages=st)
         assert OM.rel_err(y, ref) <= (1e-3 if T <= 8 else 1e-2), OM.rel_err(y, ref)
+        assert bool((OM.topk_margin(OM.router_logits64(x.reshape(T, 1024), ol), 4) > 1e-5).all())
+        blk = L.npu["moe_block"]
+        assert blk.q_router == QT.F32
+        assert torch.equal(blk.stages(T)["topk_ids"].cpu().long(), st["topk_ids"]), f"layer {i}: ids differ"
     g = ts.get_expert("blk.1.ffn_gate_exps.weight", 3)
     assert np.array_equal(g, Q.dequant_matrix(hs[1].gate[3], hs[1].q_gate, 256, 1024))
 

@@ -43,6 +43,22 @@ def _check(gpu, h, T, residual=False, seed=5, rmsnorm_input=True, tol=REL_TOL):
     return rel
 
 
+@pytest.mark.parametrize("D,T,bias", [(2048, 1, False), (2048, 3, True), (2048, 8, False), (768, 1, True),
+                                      (768, 5, False)])
+def test_fp32_router(gpu, D, T, bias):
+    """Router and shared scalar gate in fp32 with values bf16 cannot hold, as a GGUF
+    file's F32 ffn_gate_inp / ffn_gate_inp_shexp tensors carry them (the reference reads
+    both in fp32, qwen/forward.py:41-47, 599, 608): the T = 1 router kernel and the
+    K-range partials of T > 1 (512- and 256-wide ranges) read them as fp32."""
+    h = synth.host_moe_layer(80 + T, D=D, FF=512 if D == 2048 else 256, E=256, k=8, router_f32=True, norm=True,
+                             bias=bias)
+    assert h.router.dtype == np.float32 and h.sh_gate_inp.dtype == np.float32
+    assert not np.array_equal(synth.from_bf16(synth.to_bf16(h.router)), h.router)
+    blk = GpuMoeBlock.from_host(h, device=gpu)
+    assert blk.q_router == QT.F32 and blk.router.dtype == torch.float32
+    _check(gpu, h, T, seed=90 + T)
+
+
 @pytest.mark.parametrize("T", [1, 2, 8])
 def test_config3_block(gpu, T):
     """BASELINE config 3 shape: D=2048, FF=512, E=256, top-8, IQ4_XS gate/up, IQ3_XXS down."""
