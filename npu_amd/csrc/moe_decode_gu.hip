@@ -72,6 +72,9 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
     fetch_subs<QTS, 32, DC, true>(sg, static_cast<const uint8_t*>(P.gate_sh) + r * rbs, lir, nsub);
     fetch_subs<QTS, 32, DC, true>(su, static_cast<const uint8_t*>(P.up_sh) + r * rbs, lir, nsub);
   } else if (wave == 0) {
+    // The selection is a dependent chain of one wave that every wave of the
+    // block waits for: it issues ahead of the co-resident blocks' decode.
+    __builtin_amdgcn_s_setprio(3);
     float v[MAXV];
     int ix[MAXV];
     topk_load<MAXV>(logits, E, v, ix);
@@ -79,6 +82,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
     topk_keys<MAXV>(v, ix, E, uk);
     topk_masks<MAXV>(uk, k, sel);
     if (lane == 0) s_e = topk_rank_id<MAXV>(sel, u);
+    __builtin_amdgcn_s_setprio(0);
   }
   issue_fence();
 #pragma unroll
