@@ -52,6 +52,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the per-stage graphs the roofline is measured on (for rocprof)")
     ap.add_argument("--chain-only", action="store_true", help="only the B=1 chain (for rocprof)")
+    ap.add_argument("--matvec-only", action="store_true", help="only BASELINE configs 1-2 (quantised matvec)")
     ap.add_argument("--dense-shapes", default="ssm_in,ssm_gate,ssm_out", help="projections for --dense-only")
     ap.add_argument("--dense-tokens", default="1,8", help="token counts for --dense-only")
     return ap.parse_args()
@@ -277,6 +278,81 @@ def run_dense_mv(dev, n_layers: int = 30, reps: int = 20, shapes=None, tokens=(1
     return out
 
 
+QUANT_MV_SHAPES = (("config1_iq4xs_512x2048", 23, 512, 2048), ("config2_iq3xxs_2048x512", 18, 2048, 512),
+                   ("config2_iq3xxs_512x2048", 18, 512, 2048))
+
+
+def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330):
+    """BASELINE configs 1 and 2: one y = W x with W a raw IQ4_XS [512 x 2048] or IQ3_XXS
+    [2048 x 512] / [512 x 2048] matrix (the reference's NpuIQ4MatVec / NpuQuantMatVec
+    call, npu/quant_mv.py:419-463), fp32 x ~ N(0, 1), seeded device-generated
+    superblocks.  Enough distinct matrices for ~330 MB (beyond the 256 MB Infinity Cache)
+    are resident; one hipGraph holds one gm_matvec per matrix (the back-to-back calls of
+    the configs), replayed `reps` times: period per call.  Batched variant: `batch`
+    consecutive matrices are one [batch M x K] raw matrix, so one launch computes their
+    products with the same x.  Algorithmic bytes per call: W + x + y."""
+    import torch
+    from npu_amd import _lib as L
+    from npu_amd import ops, synth
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED + 40)
+    lib = L.lib()
+    out = {}
+    for name, qt, M, K in QUANT_MV_SHAPES:
+        rb = (K // 256) * (136 if qt == 23 else 98)
+        n = max(batch, (total_mb << 20) // (M * rb) // batch * batch)
+        W = synth.device_quant_matrix(gen, qt, M, K, n, dev)                  # [n, M, rb] uint8
+        x = torch.randn(K, generator=gen, device=dev)
+        y = torch.empty(n, M, device=dev)
+        yb = torch.empty(n // batch, batch * M, device=dev)
+
+        def per_call():
+            s = L.stream_ptr()
+            for i in range(n):
+                L.check(lib.gm_matvec(qt, L.ptr(W[i]), M, K, L.ptr(x), 1, L.ptr(y[i]), s), "gm_matvec")
+
+        def batched():
+            s = L.stream_ptr()
+            for j in range(n // batch):
+                L.check(lib.gm_matvec(qt, L.ptr(W[j * batch]), batch * M, K, L.ptr(x), 1, L.ptr(yb[j]), s),
+                        "gm_matvec")
+
+        def period_us(fn, launches):
+            fn()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn()
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / (reps * launches)
+
+        us = period_us(per_call, n)
+        ub = period_us(batched, n // batch)
+        # the last matrix against its device dequant (gm_dequant_f32, exact) in float64
+        Wd = ops.dequant(qt, W[n - 1].reshape(-1)).view(M, K).double()
+        ref = Wd @ x.double()
+        rel = float((y[n - 1].double() - ref).abs().max() / ref.abs().max())
+        same = bool(torch.equal(yb.view(n, M), y))
+        algo = M * rb + K * 4 + M * 4
+        out[name] = {"M": M, "K": K, "distinct_matrices": n, "resident_MB": n * M * rb / 2**20,
+                     "algorithmic_bytes_per_call": algo,
+                     "graph_us_per_call": us, "graph_GBps": algo / (us * 1e-6) / 1e9,
+                     "graph_frac": algo / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+                     "batched_matrices_per_launch": batch, "batched_us_per_launch": ub,
+                     "batched_GBps": batch * algo / (ub * 1e-6) / 1e9,
+                     "batched_frac": batch * algo / (ub * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+                     "rel_err_vs_f64": rel, "batched_equals_per_call": same}
+        del W, y, yb
+    return out
+
+
 def cpu_baseline(layers, n_sample: int, budget_s: float = 12.0):
     """The oracle (a port of the CPU branch of qwen/forward.py:moe_forward) on a bounded
     sample: the first `n_sample` blocks of the chain, B=1, run back to back (each output
@@ -411,6 +487,9 @@ def main() -> int:
         print(json.dumps({"dense_mv": run_dense_mv(dev, shapes=args.dense_shapes.split(","),
                                                    tokens=[int(t) for t in args.dense_tokens.split(",")])}))
         return 0
+    if args.matvec_only:
+        print(json.dumps({"quant_mv": run_quant_mv(dev)}))
+        return 0
     if args.roofline_only:
         layers = build_layers(args.layers, dev)
         torch.cuda.synchronize()
@@ -465,6 +544,8 @@ def main() -> int:
         log(f"prefill: {extra['prefill']}")
         extra["dense_mv"] = run_dense_mv(dev)
         log(f"dense bf16 matvec: {extra['dense_mv']}")
+        extra["quant_mv"] = run_quant_mv(dev)
+        log(f"quant matvec (configs 1-2): {extra['quant_mv']}")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -13,9 +13,11 @@ from pathlib import Path
 
 import torch
 
-# NPU_AMD_LIB=timeline selects the timestamped profiling build (libnpu_amd_tl.so).
+# NPU_AMD_LIB=timeline selects the timestamped profiling build (libnpu_amd_tl.so),
+# NPU_AMD_LIB=asan the host-only AddressSanitizer build (libnpu_amd_asan.so; CPU tests).
 LIB_PATH = Path(__file__).resolve().with_name(
-    "libnpu_amd_tl.so" if os.environ.get("NPU_AMD_LIB") == "timeline" else "libnpu_amd.so")
+    {"timeline": "libnpu_amd_tl.so", "asan": "libnpu_amd_asan.so"}.get(os.environ.get("NPU_AMD_LIB", ""),
+                                                                      "libnpu_amd.so"))
 
 GM_QTYPE_F32 = 0
 GM_QTYPE_F16 = 1

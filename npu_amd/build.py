@@ -4,6 +4,11 @@ Usage: ``python -m npu_amd.build`` (or ``npu_amd.build.build()``).  The library
 is written next to this file, in-tree, so it travels with the source tree.
 ``python -m npu_amd.build --timeline`` builds the profiling variant
 ``libnpu_amd_tl.so`` (per-block timestamps, see csrc/timeline.h) instead.
+``python -m npu_amd.build --asan`` builds ``libnpu_amd_asan.so``: the same
+library with its host code (argument checks, workspace layout, error reporting)
+instrumented with AddressSanitizer, for the C-ABI tests on the CPU; the device
+code is built as usual.  A process loads it with the clang ASan runtime preloaded
+(``asan_runtime()``) and ``NPU_AMD_LIB=asan``.
 """
 from __future__ import annotations
 
@@ -18,6 +23,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libnpu_amd.so"
 LIB_TL = HERE / "libnpu_amd_tl.so"
+LIB_ASAN = HERE / "libnpu_amd_asan.so"
 SOURCES = ["capi.hip", "matvec.hip", "router.hip", "moe_decode.hip", "moe_decode_gu.hip", "moe_decode_dn.hip",
            "dispatch.hip", "prefill.hip", "mv_bf16.hip"]
 ARCH = os.environ.get("NPU_AMD_ARCH", "gfx950")
@@ -41,14 +47,40 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False, timeline: bool = False) -> Path:
+# Host-side AddressSanitizer: every sanitizer flag goes to the host compile only.
+ASAN_FLAGS = ["-Xarch_host", "-g", "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def is_stale(lib: Path) -> bool:
+    """True when ``lib`` is missing or older than a source or header it is built from."""
+    if not lib.exists():
+        return True
+    t = lib.stat().st_mtime
+    deps = [*CSRC.glob("*.hip"), *CSRC.glob("*.h"), *(HERE.parent / "include").glob("*.h")]
+    return any(d.stat().st_mtime > t for d in deps)
+
+
+def asan_runtime() -> str | None:
+    """The clang ASan runtime that a process loading ``libnpu_amd_asan.so`` preloads."""
+    for root in ("/opt/rocm/lib/llvm/lib/clang", "/opt/rocm/llvm/lib/clang"):
+        p = Path(root)
+        if p.is_dir():
+            for cand in sorted(p.glob("*/lib/linux/libclang_rt.asan-x86_64.so")):
+                return str(cand)
+    return None
+
+
+def build(verbose: bool = False, timeline: bool = False, asan: bool = False) -> Path:
     """Compile every source to an object in parallel, then link the library
-    (the timestamped profiling variant when ``timeline``)."""
-    objdir = HERE / ("_build_tl" if timeline else "_build")
+    (the timestamped profiling variant when ``timeline``, the host-only ASan
+    variant when ``asan``)."""
+    objdir = HERE / ("_build_tl" if timeline else "_build_asan" if asan else "_build")
     objdir.mkdir(exist_ok=True)
     inc = ["-I", str(HERE.parent / "include")]
     compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"] + (["-DGM_TIMELINE=1"] if timeline else [])
-    out_lib = LIB_TL if timeline else LIB
+    if asan:
+        compile_flags = compile_flags + ASAN_FLAGS
+    out_lib = LIB_TL if timeline else LIB_ASAN if asan else LIB
 
     def compile_one(src: str):
         obj = objdir / (Path(src).stem + ".o")
@@ -61,7 +93,8 @@ def build(verbose: bool = False, timeline: bool = False) -> Path:
     with ThreadPoolExecutor(jobs) as ex:
         results = list(ex.map(compile_one, SOURCES))
     tmp = out_lib.with_suffix(".so.tmp")
-    link = [hipcc(), *HIPCC_FLAGS, *[str(o) for o, _ in results], "-o", str(tmp)]
+    link = [hipcc(), *HIPCC_FLAGS, *(["-Xarch_host", "-fsanitize=address"] if asan else []),
+            *[str(o) for o, _ in results], "-o", str(tmp)]
     results.append((None, subprocess.run(link, capture_output=True, text=True)))
     for _, res in results:
         out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
@@ -75,4 +108,4 @@ def build(verbose: bool = False, timeline: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv, timeline="--timeline" in sys.argv))
+    print(build(verbose="-v" in sys.argv, timeline="--timeline" in sys.argv, asan="--asan" in sys.argv))

@@ -7,6 +7,7 @@
 // staged in LDS; weights are decoded in registers and never written back.
 #include "iq_decode.h"
 #include "kernels.h"
+#include "moe_common.h"
 
 // ------------------------------------------------------------- dequant
 template <int QT>
@@ -202,9 +203,79 @@ static int launch_matvec_l(const uint8_t* w, int M, int K, const float* x, int n
   return launch_matvec_t<QT, L, 1>(w, M, K, x, n_tok, y, s);
 }
 
+// One token (BASELINE configs 1 and 2, the reference's NpuQuantMatVec /
+// NpuIQ4MatVec call, npu/quant_mv.py:419-463): LR lanes per row, 64 / LR rows
+// per wave.  Every thread first loads its 8 values of x per 2048-wide pass,
+// then every lane issues the loads of all SPL sub-blocks of its row, so the
+// wait for x (vmcnt retires in issue order) never waits for weights; the
+// block converts x into the int8-limb row in LDS while the weights are in
+// flight, then multiplies on v_dot4_i32_i8 as the MoE decode kernels do.
+constexpr int kMv1MaxK = 8192;
+
+template <int QT, int LR, int SPL>
+__global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int M, int K, int64_t rb,
+                                              const float* __restrict__ x, float* __restrict__ y) {
+  using namespace gm_moe;
+  constexpr int NXP = kMv1MaxK / 2048;                           // passes of 8 values per thread
+  constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
+  extern __shared__ float smem[];                                  // the limb row, then the IQ3 tables
+  const int nsub = K / GM_SUB, rbytes = gm_limb_row_bytes(K);
+  uint8_t* xs = reinterpret_cast<uint8_t*>(smem);
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(xs + rbytes);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane % LR;
+  const int row = (blockIdx.x * 4 + wave) * (64 / LR) + lane / LR;
+  gm_f32x4 xa[NXP], xb[NXP];
+#pragma unroll
+  for (int p = 0; p < NXP; ++p) {
+    const int k0 = 2048 * p + 8 * (int)threadIdx.x;
+    const int kc = k0 < K ? k0 : K - 8;                          // past K: a duplicate load, not stored
+    xa[p] = *reinterpret_cast<const gm_f32x4*>(x + kc);
+    xb[p] = *reinterpret_cast<const gm_f32x4*>(x + kc + 4);
+  }
+  uint32_t gw = 0;
+  if constexpr (IQ3) gw = gm_iq3_tab_load();
+  RowFetch<QT, SPL> f;
+  fetch_subs<QT, LR, SPL, true>(f, w + (int64_t)(row < M ? row : M - 1) * rb, lir, nsub);
+  issue_fence();
+#pragma unroll
+  for (int p = 0; p < NXP; ++p) {
+    const int k0 = 2048 * p + 8 * (int)threadIdx.x;
+    if (k0 < K) gm_put_limbs8(xa[p], xb[p], k0 >> 2, xs);      // uniform per quad (K % 32 == 0)
+  }
+  if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
+  __syncthreads();
+  const int tok[1] = {0};
+  float acc[1] = {0.f};
+  dot_subs_i8<QT, LR, SPL, 1>(f, lir, nsub, xs, rbytes, tok, 1, tab, acc);
+  const float v = row_sum<LR>(acc[0]);
+  if (row < M && lir == 0) y[row] = v;
+}
+
+template <int QT, int LR, int SPL>
+static int launch_mv1q_t(const uint8_t* w, int M, int K, const float* x, float* y, hipStream_t s) {
+  const int rows_per_block = 4 * (64 / LR);
+  const size_t smem = (size_t)gm_moe::gm_limb_row_bytes(K) + sizeof(Iq3Tab);
+  if (int rc = gm_set_smem(k_mv1q<QT, LR, SPL>, smem)) return rc;
+  hipLaunchKernelGGL((k_mv1q<QT, LR, SPL>), dim3((unsigned)((M + rows_per_block - 1) / rows_per_block)), dim3(256),
+                     smem, s, w, M, K, gm_row_bytes(QT, K), x, y);
+  GM_TRY(hipGetLastError());
+  return GM_OK;
+}
+
+template <int QT>
+static int launch_mv1q(const uint8_t* w, int M, int K, const float* x, float* y, hipStream_t s) {
+  const int nsub = K / GM_SUB;                                   // 8 .. 256
+  if (nsub <= 16) return launch_mv1q_t<QT, 16, 1>(w, M, K, x, y, s);
+  if (nsub <= 32) return launch_mv1q_t<QT, 32, 1>(w, M, K, x, y, s);
+  if (nsub <= 64) return launch_mv1q_t<QT, 64, 1>(w, M, K, x, y, s);
+  if (nsub <= 128) return launch_mv1q_t<QT, 64, 2>(w, M, K, x, y, s);
+  return launch_mv1q_t<QT, 64, 4>(w, M, K, x, y, s);
+}
+
 template <int QT>
 static int launch_matvec_q(const uint8_t* w, int M, int K, const float* x, int n_tok, float* y,
                            hipStream_t s) {
+  if (n_tok == 1 && K <= kMv1MaxK) return launch_mv1q<QT>(w, M, K, x, y, s);
   const int nsub = K / GM_SUB;
   if (nsub >= 64) return launch_matvec_l<QT, 64>(w, M, K, x, n_tok, y, s);
   if (nsub >= 32) return launch_matvec_l<QT, 32>(w, M, K, x, n_tok, y, s);

@@ -135,11 +135,11 @@ template <int RT, int WPB, int NC>
 __global__ void __launch_bounds__(64 * WPB) k_mv_bf16_mfma(const uint16_t* __restrict__ w, int M, int K,
                                                         const float* __restrict__ x, int n_tok,
                                                         float* __restrict__ y) {
-  __shared__ gm_f32x4 red[WPB - 1][RT][64];
+  __shared__ gm_f32x4 red[WPB > 1 ? WPB - 1 : 1][RT][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
   const int row0 = blockIdx.x * 16 * RT;
   const int tok = blockIdx.y * 16 + l16;
-  const int kw = K / WPB, kbeg = wave * kw;                      // this wave's K range
+  const int kw = K / WPB, kbeg = wave * kw;                      // this wave's K range (K % (32 WPB) == 0)
   const gm_u32x4* ar[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -199,7 +199,7 @@ __global__ void __launch_bounds__(64 * WPB) k_mv_bf16_mfma(const uint16_t* __res
 template <int RT, int WPB>
 int launch_mfma_w(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
   const dim3 grid((unsigned)((M + 16 * RT - 1) / (16 * RT)), (unsigned)((n_tok + 15) / 16));
-  const int steps = K / (32 * WPB);                              // k-steps per wave (K % 256 == 0)
+  const int steps = K / (32 * WPB);                              // k-steps per wave (exact: WPB divides K / 32)
 #define GM_MV_GO(NC)                                                                               \
   hipLaunchKernelGGL((k_mv_bf16_mfma<RT, WPB, NC>), grid, dim3(64 * WPB), 0, s, w, M, K, x, n_tok, y); \
   break;
@@ -215,13 +215,24 @@ int launch_mfma_w(const uint16_t* w, int M, int K, const float* x, int n_tok, fl
 }
 
 // Two row tiles per block for tall matrices, else one; waves per block so that
-// the grid holds about 1024 waves.
+// the grid holds about 1024 waves, each wave taking an equal number of 32-wide
+// k-steps: the largest of 8 (4 for grids of >= 256 blocks), 4, 2, 1 that divides
+// K / 32 (K = 576: 2 waves of 9 steps).
 int launch_mfma(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
   const int rt = M >= 8192 ? 2 : 1;
   const int blocks = (M + 16 * rt - 1) / (16 * rt);
-  const bool w8 = blocks < 256;
-  if (rt == 2) return w8 ? launch_mfma_w<2, 8>(w, M, K, x, n_tok, y, s) : launch_mfma_w<2, 4>(w, M, K, x, n_tok, y, s);
-  return w8 ? launch_mfma_w<1, 8>(w, M, K, x, n_tok, y, s) : launch_mfma_w<1, 4>(w, M, K, x, n_tok, y, s);
+  int wpb = blocks < 256 ? 8 : 4;
+  while ((K / 32) % wpb) wpb >>= 1;
+#define GM_MV_W(R)                                              \
+  switch (wpb) {                                                \
+    case 8: return launch_mfma_w<R, 8>(w, M, K, x, n_tok, y, s); \
+    case 4: return launch_mfma_w<R, 4>(w, M, K, x, n_tok, y, s); \
+    case 2: return launch_mfma_w<R, 2>(w, M, K, x, n_tok, y, s); \
+    default: return launch_mfma_w<R, 1>(w, M, K, x, n_tok, y, s); \
+  }
+  if (rt == 2) GM_MV_W(2)
+  GM_MV_W(1)
+#undef GM_MV_W
 }
 
 template <int NT, int R, int S>
@@ -247,7 +258,7 @@ int launch_mv1(const uint16_t* w, int M, int K, const float* x, int n_tok, float
 
 }  // namespace
 
-// K a multiple of 256 and <= 16384, w and x 16-byte aligned (checked by the
+// K a multiple of 32 and <= 16384, w and x 16-byte aligned (checked by the
 // caller).  One token: the streaming FMA kernel; more: the MFMA kernel, 16
 // tokens per column tile.
 int gm_launch_mv_bf16(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {

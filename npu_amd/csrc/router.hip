@@ -61,6 +61,8 @@ __global__ void __launch_bounds__(256) k_router_only(const uint16_t* __restrict_
   }
 }
 
+constexpr size_t kMaxLds = 160 * 1024;    // LDS per workgroup on gfx950
+
 template <int L>
 int launch_router_l(const uint16_t* w, const float* bias, const float* x, int T, int D, int E,
                     const uint16_t* wsh, const float* nw, float eps, float* logits, float* shg,
@@ -68,15 +70,18 @@ int launch_router_l(const uint16_t* w, const float* bias, const float* x, int T,
   constexpr int RPS = 64 / L;
   const int nrows = E + (wsh ? 1 : 0);
   const int nb = (nrows + 4 * RPS - 1) / (4 * RPS);
-  if (T == 1) {
-    const size_t smem = (16 + (size_t)D) * 4;
-    hipLaunchKernelGGL((k_router_only<L, 1>), dim3(nb, 1), dim3(256), smem, s, w, bias, x, T, D, E, wsh, nw,
-                       eps, logits, shg);
+  const size_t smem1 = (16 + (size_t)D) * 4, smem8 = (16 + 8 * (size_t)D) * 4;
+  if (T == 1 || smem8 > kMaxLds) {
+    // one token per launch: x staged once (D <= 16384: at most 64 KiB + 64 B);
+    // T > 1 with D > 5088, where 8 staged rows of x exceed the LDS, loops over
+    // the tokens
+    if (int rc = gm_set_smem(k_router_only<L, 1>, smem1)) return rc;
+    for (int t = 0; t < T; ++t)
+      hipLaunchKernelGGL((k_router_only<L, 1>), dim3(nb, 1), dim3(256), smem1, s, w, bias, x + (int64_t)t * D, 1, D,
+                         E, wsh, nw, eps, logits + (int64_t)t * E, shg ? shg + t : nullptr);
   } else {
-    const size_t smem = (16 + 8 * (size_t)D) * 4;
-    int rc = gm_set_smem(k_router_only<L, 8>, smem);
-    if (rc) return rc;
-    hipLaunchKernelGGL((k_router_only<L, 8>), dim3(nb, (T + 7) / 8), dim3(256), smem, s, w, bias, x, T, D, E,
+    if (int rc = gm_set_smem(k_router_only<L, 8>, smem8)) return rc;
+    hipLaunchKernelGGL((k_router_only<L, 8>), dim3(nb, (T + 7) / 8), dim3(256), smem8, s, w, bias, x, T, D, E,
                        wsh, nw, eps, logits, shg);
   }
   GM_TRY(hipGetLastError());

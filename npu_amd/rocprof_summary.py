@@ -156,9 +156,34 @@ def inst_summary(a) -> None:
     print("\n".join(lines))
 
 
+def trace_by_grid(a) -> None:
+    """Per kernel and launch shape (grid size): dispatches and duration statistics from a
+    ``--kernel-trace`` CSV, for runs that launch one kernel at several sizes."""
+    rows: dict[tuple[str, int], list[float]] = defaultdict(list)
+    with open(a.trace) as f:
+        for r in csv.DictReader(f):
+            name = short(r["Kernel_Name"])
+            if a.kernel and a.kernel not in name:
+                continue
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            rows[(name, grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    lines = [f"# {a.name}: kernel durations by launch shape", "", a.commands, "",
+             "| kernel | grid (work-items) | dispatches | avg us | median us | min us | max us |",
+             "|---|---|---|---|---|---|---|"]
+    for (name, grid), d in sorted(rows.items()):
+        lines.append(f"| {name[:80]} | {grid} | {len(d)} | {statistics.fmean(d):.2f} | {statistics.median(d):.2f} | "
+                     f"{min(d):.2f} | {max(d):.2f} |")
+    out = Path(a.out)
+    out.mkdir(parents=True, exist_ok=True)
+    (out / f"{a.name}.md").write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--stats", required=True)
+    ap.add_argument("--trace", help="kernel-trace CSV: durations per kernel and grid size (trace mode)")
+    ap.add_argument("--kernel", default="", help="trace mode: only kernels whose name contains this")
+    ap.add_argument("--stats")
     ap.add_argument("--prefill-pmc", help="counter CSV of MfmaUtil/MfmaFlopsF16/MfmaFlopsBF16 (prefill mode)")
     ap.add_argument("--inst-pmc", help="counter CSV of SQ_WAVES/SQ_INSTS_* (instruction mode)")
     ap.add_argument("--simds", type=int, default=1024, help="SIMDs of the device (256 CUs x 4 on MI355X)")
@@ -177,6 +202,11 @@ def main() -> None:
                          "T = 1 decode table; repeatable)")
     ap.add_argument("--json", default="hbm_traffic.json", help="name of the JSON written to --out")
     a = ap.parse_args()
+    if a.trace:
+        trace_by_grid(a)
+        return
+    if not a.stats:
+        ap.error("--stats is required outside trace mode")
     if a.prefill_pmc:
         prefill_summary(a)
         return

@@ -50,6 +50,28 @@ def test_npu_matvec_and_concat(gpu):
     assert op.out_splits == (256, 64, 32) and OM.rel_err(yc, refc) <= 1e-5
 
 
+@pytest.mark.parametrize("shape", [(1, 256), (1,), (3,), (2, 13)])
+@pytest.mark.parametrize("out_f,in_f", [(576, 576), (1536, 576), (576, 1536), (300, 2048)])
+def test_npu_linear(gpu, shape, out_f, in_f):
+    """NpuLinear (npu/linear.py:147-244) against float64 F.linear of the bf16 weight and
+    the fp32 input, at the reference self-test's shape (576 x 576, x [1, 256, 576]) and
+    SmolLM2's projection shapes; one token runs the VALU matvec, more the MFMA kernel."""
+    from npu_amd.linear import NpuLinear
+    g = torch.Generator().manual_seed(out_f + in_f + len(shape))
+    W = torch.randn(out_f, in_f, generator=g, dtype=torch.bfloat16)
+    x = torch.randn(*shape, in_f, generator=g)
+    lin = NpuLinear(W)
+    y = lin(x)
+    assert y.dtype == torch.float32 and y.shape == (*shape, out_f) and not y.is_cuda
+    ref = F.linear(x.double(), W.double())
+    assert OM.rel_err(y.double(), ref) <= 1e-5
+    # the reference self-test's own bar (npu/linear.py:258-262), bf16 input
+    xb = x.to(torch.bfloat16)
+    assert float((lin(xb) - F.linear(xb.float(), W.float())).abs().max()) < 5e-2
+    yd = lin(x.to(gpu))
+    assert yd.is_cuda and torch.equal(yd.cpu(), y)
+
+
 @pytest.mark.parametrize("stacked", [False, True])
 def test_npu_fused_mlp(gpu, stacked):
     g = torch.Generator().manual_seed(2)

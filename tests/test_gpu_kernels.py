@@ -53,6 +53,9 @@ def _ref_matvec(w_raw, qtype, M, K, x):
     (QT.IQ4_XS, 2048, 512),    # model's down shape
     (QT.IQ4_XS, 40, 256),
     (QT.IQ3_XXS, 33, 4096),
+    (QT.IQ4_XS, 70, 1024),     # one-token kernel: every lanes-per-row / sub-blocks-per-lane branch
+    (QT.IQ3_XXS, 9, 8192),
+    (QT.IQ4_XS, 3, 12288),     # one token past the one-token kernel's K limit
 ])
 @pytest.mark.parametrize("n_tok", [1, 3, 8, 13])
 def test_matvec(gpu, qtype, M, K, n_tok):
@@ -63,13 +66,15 @@ def test_matvec(gpu, qtype, M, K, n_tok):
     assert y.shape == (n_tok, M)
     assert OM.rel_err(y, ref32) <= REL_TOL
     assert OM.rel_err(y, ref64) <= 1e-5
+    # per-token relative error: a row or token mix-up moves one entry, not the max
+    assert float(((y.double() - ref64).abs() / ref64.abs().amax(dim=1, keepdim=True)).max()) <= 1e-5
 
 
 # The projection shapes of qwen/test_npu_ssm.py and test_npu_attn_o.py (8192 x 2048,
 # 4096 x 2048, 2048 x 4096), plus ragged M, K tails inside a 512-wide slot, and K
 # large enough for two passes over the row.
 @pytest.mark.parametrize("M,K", [(8192, 2048), (4096, 2048), (2048, 4096), (33, 256), (100, 768),
-                                 (17, 12288), (5, 16384), (256, 2048)])
+                                 (17, 12288), (5, 16384), (256, 2048), (576, 576), (40, 800), (9000, 96)])
 @pytest.mark.parametrize("n_tok", [1, 2, 3, 8, 13, 17])
 def test_matvec_bf16(gpu, M, K, n_tok):
     W = synth.host_bf16_normal(_g(M + K), (M, K), 0.02)
@@ -118,6 +123,25 @@ def test_router_topk(gpu, T, E, k, bias):
     assert torch.equal(ids.cpu().long(), st["topk_ids"])
     assert torch.allclose(logits.cpu(), st["ffn_moe_logits"], rtol=0, atol=2e-5)
     assert torch.allclose(wts.cpu(), st["ffn_moe_weights_norm"], rtol=1e-5, atol=1e-6)
+    assert torch.allclose(shg.cpu(), st["shared_expert_gate_sigmoid"], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("T,D", [(1, 16384), (3, 8192), (8, 4864), (9, 5120)])
+def test_router_topk_wide_d(gpu, T, D):
+    """gm_router_topk at its advertised width limits: one token at D = 16384 (x staged in
+    64 KiB + 64 B of LDS), eight tokens at D = 4864 (8 staged rows in 152 KiB, near the
+    160 KiB limit), and T > 1 beyond that (one launch per token)."""
+    h = synth.host_moe_layer(50 + T, D=D, FF=256, E=64, k=4, shared=True, norm=True)
+    ol = OM.OracleLayer(h)
+    x = torch.from_numpy(synth.host_input(6 + T, T, D, rmsnorm=False))
+    dev = lambda a: torch.from_numpy(a.view(np.int16) if a.dtype == np.uint16 else a).to(gpu)
+    ids, wts, logits, shg = ops.router_topk(dev(h.router), x.to(gpu), 4, w_sh_gate=dev(h.sh_gate_inp),
+                                            norm_w=dev(h.norm_w), eps=1e-6)
+    st = {}
+    OM.moe_forward(OM.rms_norm(x, ol.norm_w, 1e-6).unsqueeze(0), ol, stages=st)
+    assert bool((OM.topk_margin(OM.router_logits64(x, ol), 4) > 1e-5).all())
+    assert torch.equal(ids.cpu().long(), st["topk_ids"])
+    assert torch.allclose(logits.cpu(), st["ffn_moe_logits"], rtol=0, atol=5e-5)
     assert torch.allclose(shg.cpu(), st["shared_expert_gate_sigmoid"], rtol=1e-5, atol=1e-6)
 
 
