@@ -67,7 +67,8 @@ struct PfWs {
   int32_t* inv;       // [P]   position of pair p in sorted order
   int32_t* segs;      // [1 + 4 * max_seg]  n_seg, then (expert, start, n, unused)
   uint16_t* xr;       // [3][T][D]  bf16 planes of xn (router operand)
-  uint16_t* xh;       // [T][D]     f16 xn (gate/up operand)
+  uint16_t* xh;       // [T][D]     f16 xn 2^s (gate/up operand)
+  float* xsc;         // [T]        2^-s per token
   float* part;        // [kRouterSplit][T][ldp]  partial router dot products
   uint16_t* hb;       // [P + T][FF]  bf16 SwiGLU rows (sorted pairs, then shared per token)
   uint16_t* hh;       // [P + T][FF]  the same rows as scaled f16
@@ -102,6 +103,7 @@ PfWs pf_layout(const gm_moe_layer* L, int T, uint8_t* base, size_t* total) {
   w.segs = reinterpret_cast<int32_t*>(take((1 + 4 * (size_t)max_segments(T, L->k, L->E)) * 4));
   w.xr = reinterpret_cast<uint16_t*>(take(3 * (size_t)T * L->D * 2));
   w.xh = reinterpret_cast<uint16_t*>(take((size_t)T * L->D * 2));
+  w.xsc = reinterpret_cast<float*>(take((size_t)T * 4));
   w.part = reinterpret_cast<float*>(take((size_t)kRouterSplit * T * router_ld(L) * 4));
   w.hb = reinterpret_cast<uint16_t*>(take((P + T) * (size_t)L->FF * 2));
   w.hh = reinterpret_cast<uint16_t*>(take((P + T) * (size_t)L->FF * 2));
@@ -125,14 +127,48 @@ __device__ __forceinline__ void xcd_tile(int b, int nrt, int& seg, int& rt) {
 // ---------------------------------------------------------------- prep x
 // xn = (x * rms) * w (qwen/forward.py:58-61) or x; planes p0 = bf16(xn),
 // p1 = bf16(xn - p0), p2 = bf16(xn - p0 - p1) (each difference exact in fp32);
-// xh = f16(xn).  One block per token.
+// xh = f16(xn 2^s) with the per-token power of two that puts max |xn| in
+// [2^14, 2^15) (no f16 overflow whatever the input scale, and f16's 11 bits
+// for every value down to 2^-10 of the token's maximum; rows below 2^-100 are
+// scaled as if their maximum were 2^-100), and xsc[t] = 2^-s, which the
+// gate/up kernel multiplies into its sums.  One block per token.
+__device__ __forceinline__ float pf_block_max(float m, float* red4) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = m;
+  __syncthreads();
+  return fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
+}
+
+// 2^s for a row whose largest magnitude is m (m >= 0): m 2^s in [2^14, 2^15).
+__device__ __forceinline__ int pf_f16_shift(float m) {
+  const int E = m > 0.f && m <= 3.4e38f ? max(__builtin_amdgcn_frexp_expf(m), -100) : 0;
+  return 15 - E;
+}
+
+__device__ __forceinline__ void pf_put_planes(gm_f32x2 v, int sh, uint32_t& o0, uint32_t& o1, uint32_t& o2,
+                                              uint32_t& oh) {
+  const gm_bf16x2 b0 = __builtin_convertvector(v, gm_bf16x2);
+  const gm_f32x2 r0 = v - __builtin_convertvector(b0, gm_f32x2);
+  const gm_bf16x2 b1 = __builtin_convertvector(r0, gm_bf16x2);
+  const gm_f32x2 r1 = r0 - __builtin_convertvector(b1, gm_f32x2);
+  const gm_bf16x2 b2 = __builtin_convertvector(r1, gm_bf16x2);
+  o0 = __builtin_bit_cast(uint32_t, b0);
+  o1 = __builtin_bit_cast(uint32_t, b1);
+  o2 = __builtin_bit_cast(uint32_t, b2);
+  const gm_f32x2 vs = {__builtin_ldexpf(v.x, sh), __builtin_ldexpf(v.y, sh)};
+  oh = __builtin_bit_cast(uint32_t, __builtin_convertvector(vs, gm_f16x2));
+}
+
 __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, int T, int D,
                                                  const float* __restrict__ norm_w, float eps,
-                                                 uint16_t* __restrict__ xr, uint16_t* __restrict__ xh) {
-  __shared__ float red[4];
+                                                 uint16_t* __restrict__ xr, uint16_t* __restrict__ xh,
+                                                 float* __restrict__ xsc) {
+  __shared__ float red[4], redm[4];
   const int t = blockIdx.x;
   const gm_f32x2* x2 = reinterpret_cast<const gm_f32x2*>(x + (int64_t)t * D);
   const int n2 = D >> 1;
+  int sh;
   if (D <= 4096) {                                             // uniform: the row held in registers
     constexpr int NQ = 4;                                      // 16-byte granules per thread
     const int n4 = D >> 2;
@@ -156,6 +192,17 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
       __syncthreads();
       rms = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)D + eps);
     }
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      if (norm_w) {
+        v[i].x = (v[i].x * rms) * wv[i].x; v[i].y = (v[i].y * rms) * wv[i].y;
+        v[i].z = (v[i].z * rms) * wv[i].z; v[i].w = (v[i].w * rms) * wv[i].w;
+      }
+      if ((int)threadIdx.x + 256 * i < n4)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
+    sh = pf_f16_shift(pf_block_max(m, redm));
     uint2* q0 = reinterpret_cast<uint2*>(xr) + (int64_t)t * n4;
     uint2* q1 = q0 + (int64_t)T * n4;
     uint2* q2 = q1 + (int64_t)T * n4;
@@ -164,56 +211,44 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
     for (int i = 0; i < NQ; ++i) {
       const int c = (int)threadIdx.x + 256 * i;
       if (c >= n4) break;
-      gm_f32x2 h[2] = {gm_f32x2{v[i].x, v[i].y}, gm_f32x2{v[i].z, v[i].w}};
-      const gm_f32x2 w[2] = {gm_f32x2{wv[i].x, wv[i].y}, gm_f32x2{wv[i].z, wv[i].w}};
       uint32_t o0[2], o1[2], o2[2], oh[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (norm_w) { h[j].x = (h[j].x * rms) * w[j].x; h[j].y = (h[j].y * rms) * w[j].y; }
-        const gm_bf16x2 b0 = __builtin_convertvector(h[j], gm_bf16x2);
-        const gm_f32x2 r0 = h[j] - __builtin_convertvector(b0, gm_f32x2);
-        const gm_bf16x2 b1 = __builtin_convertvector(r0, gm_bf16x2);
-        const gm_f32x2 r1 = r0 - __builtin_convertvector(b1, gm_f32x2);
-        const gm_bf16x2 b2 = __builtin_convertvector(r1, gm_bf16x2);
-        o0[j] = __builtin_bit_cast(uint32_t, b0);
-        o1[j] = __builtin_bit_cast(uint32_t, b1);
-        o2[j] = __builtin_bit_cast(uint32_t, b2);
-        oh[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(h[j], gm_f16x2));
-      }
+      pf_put_planes(gm_f32x2{v[i].x, v[i].y}, sh, o0[0], o1[0], o2[0], oh[0]);
+      pf_put_planes(gm_f32x2{v[i].z, v[i].w}, sh, o0[1], o1[1], o2[1], oh[1]);
       q0[c] = make_uint2(o0[0], o0[1]);
       q1[c] = make_uint2(o1[0], o1[1]);
       q2[c] = make_uint2(o2[0], o2[1]);
       qh[c] = make_uint2(oh[0], oh[1]);
     }
-    return;
+  } else {
+    // two passes over the row: x^2 and max |x w| (rms > 0 scales the maximum
+    // exactly up to rounding, and the target range leaves a factor 2 of f16 room)
+    const gm_f32x2* w2 = reinterpret_cast<const gm_f32x2*>(norm_w);
+    float ss = 0.f, m = 0.f;
+    for (int i = threadIdx.x; i < n2; i += 256) {
+      const gm_f32x2 v = x2[i];
+      const gm_f32x2 w = norm_w ? w2[i] : gm_f32x2{1.f, 1.f};
+      ss = fmaf(v.x, v.x, fmaf(v.y, v.y, ss));
+      m = fmaxf(m, fmaxf(fabsf(v.x * w.x), fabsf(v.y * w.y)));
+    }
+    float rms = 1.f;
+    if (norm_w) {
+      ss = gm_wave_sum64(ss);
+      if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+      __syncthreads();
+      rms = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)D + eps);
+    }
+    sh = pf_f16_shift(pf_block_max(m, redm) * rms);
+    uint32_t* p0 = reinterpret_cast<uint32_t*>(xr) + (int64_t)t * n2;
+    uint32_t* p1 = p0 + (int64_t)T * n2;
+    uint32_t* p2 = p1 + (int64_t)T * n2;
+    uint32_t* ph = reinterpret_cast<uint32_t*>(xh) + (int64_t)t * n2;
+    for (int i = threadIdx.x; i < n2; i += 256) {
+      gm_f32x2 v = x2[i];
+      if (norm_w) { const gm_f32x2 w = w2[i]; v.x = (v.x * rms) * w.x; v.y = (v.y * rms) * w.y; }
+      pf_put_planes(v, sh, p0[i], p1[i], p2[i], ph[i]);
+    }
   }
-  float rms = 1.f;
-  if (norm_w) {
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < n2; i += 256) { const gm_f32x2 v = x2[i]; ss = fmaf(v.x, v.x, fmaf(v.y, v.y, ss)); }
-    ss = gm_wave_sum64(ss);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    rms = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)D + eps);
-  }
-  const gm_f32x2* w2 = reinterpret_cast<const gm_f32x2*>(norm_w);
-  uint32_t* p0 = reinterpret_cast<uint32_t*>(xr) + (int64_t)t * n2;
-  uint32_t* p1 = p0 + (int64_t)T * n2;
-  uint32_t* p2 = p1 + (int64_t)T * n2;
-  uint32_t* ph = reinterpret_cast<uint32_t*>(xh) + (int64_t)t * n2;
-  for (int i = threadIdx.x; i < n2; i += 256) {
-    gm_f32x2 v = x2[i];
-    if (norm_w) { const gm_f32x2 w = w2[i]; v.x = (v.x * rms) * w.x; v.y = (v.y * rms) * w.y; }
-    const gm_bf16x2 b0 = __builtin_convertvector(v, gm_bf16x2);
-    const gm_f32x2 r0 = v - __builtin_convertvector(b0, gm_f32x2);
-    const gm_bf16x2 b1 = __builtin_convertvector(r0, gm_bf16x2);
-    const gm_f32x2 r1 = r0 - __builtin_convertvector(b1, gm_f32x2);
-    const gm_bf16x2 b2 = __builtin_convertvector(r1, gm_bf16x2);
-    p0[i] = __builtin_bit_cast(uint32_t, b0);
-    p1[i] = __builtin_bit_cast(uint32_t, b1);
-    p2[i] = __builtin_bit_cast(uint32_t, b2);
-    ph[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, gm_f16x2));
-  }
+  if (threadIdx.x == 0) xsc[t] = __builtin_ldexpf(1.0f, -sh);
 }
 
 // ---------------------------------------------------------------- router
@@ -723,7 +758,8 @@ template <int QT>
 __global__ void __launch_bounds__(256, kSegTok == 64 ? 2 : 4) k_pf_gateup(gm_moe_layer P, const int32_t* __restrict__ segs,
                                                       const int32_t* __restrict__ offsets,
                                                       const int32_t* __restrict__ sorted,
-                                                      const uint16_t* __restrict__ xh, uint16_t* __restrict__ hb,
+                                                      const uint16_t* __restrict__ xh,
+                                                      const float* __restrict__ xsc, uint16_t* __restrict__ hb,
                                                       int T, int n_row_tiles) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* xl = smem;                                                   // [2][64][kPitchB]
@@ -807,8 +843,10 @@ __global__ void __launch_bounds__(256, kSegTok == 64 ? 2 : 4) k_pf_gateup(gm_moe
   for (int t = 0; t < kNT; ++t) {
     const int col = t * 16 + l16;
     if (t < ntiles && col < n && r0 < FF) {
-      gm_f32x2 h01 = {gm_silu(ag[t][0]) * au[t][0], gm_silu(ag[t][1]) * au[t][1]};
-      gm_f32x2 h23 = {gm_silu(ag[t][2]) * au[t][2], gm_silu(ag[t][3]) * au[t][3]};
+      const float ds = xsc[tok_row[col]];                        // the token's f16 scale, undone exactly
+      const gm_f32x4 g = ag[t] * ds, u = au[t] * ds;
+      gm_f32x2 h01 = {gm_silu(g[0]) * u[0], gm_silu(g[1]) * u[1]};
+      gm_f32x2 h23 = {gm_silu(g[2]) * u[2], gm_silu(g[3]) * u[3]};
       *reinterpret_cast<uint2*>(hb + (int64_t)out_row[col] * FF + r0) =
           make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(h01, gm_bf16x2)),
                      __builtin_bit_cast(uint32_t, __builtin_convertvector(h23, gm_bf16x2)));
@@ -985,7 +1023,7 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
   PfWs w = pf_layout(L, T, ws + lay.pre, nullptr);
   const bool has_sh = L->gate_sh != nullptr;
   const int nrows = E + (L->sh_gate_inp ? 1 : 0);
-  hipLaunchKernelGGL(k_pf_prep, dim3(T), dim3(256), 0, s, x, T, D, L->norm_w, L->norm_eps, w.xr, w.xh);
+  hipLaunchKernelGGL(k_pf_prep, dim3(T), dim3(256), 0, s, x, T, D, L->norm_w, L->norm_eps, w.xr, w.xh, w.xsc);
   GM_TRY(hipGetLastError());
   const int ldp = router_ld(L);
   const int nsplit = router_split(D);
@@ -1031,7 +1069,7 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
     const int nb = (nseg + 7) / 8 * 8 * nrt;
     if (int rc = gm_set_smem(k_pf_gateup<QTG>, kGemmSmem)) return rc;
     hipLaunchKernelGGL(k_pf_gateup<QTG>, dim3(nb), dim3(256), kGemmSmem, s, *L, w.segs, w.offsets, w.sorted, w.xh,
-                       w.hb, T, nrt);
+                       w.xsc, w.hb, T, nrt);
     GM_TRY(hipGetLastError());
   }
   {

@@ -19,11 +19,11 @@ pytestmark = pytest.mark.gpu
 REL_TOL = 1e-2
 
 
-def _check(gpu, h, T, residual=False, seed=5, rmsnorm_input=True, logits_atol=None):
+def _check(gpu, h, T, residual=False, seed=5, rmsnorm_input=True, logits_atol=None, x_scale=1.0):
     print(f"prefill case D={h.D} FF={h.FF} E={h.E} k={h.k} T={T} q=({h.q_gate},{h.q_down}) "
           f"shared={h.gate_sh is not None} residual={residual}", flush=True)
     ol = OM.OracleLayer(h)
-    x = torch.from_numpy(synth.host_input(seed, T, h.D, rmsnorm=rmsnorm_input))
+    x = torch.from_numpy(synth.host_input(seed, T, h.D, rmsnorm=rmsnorm_input)) * x_scale
     blk = GpuMoeBlock.from_host(h, device=gpu)
     y = blk(x.to(gpu), residual=residual)
     y2 = blk(x.to(gpu), residual=residual)
@@ -130,6 +130,23 @@ def test_prefill_fp32_router(gpu, D, E, k, T):
     h = synth.host_moe_layer(130 + T, D=D, FF=256, E=E, k=k, router_f32=True, bias=True)
     assert not np.array_equal(synth.from_bf16(synth.to_bf16(h.router)), h.router)
     _check(gpu, h, T, seed=T, logits_atol=2e-5)
+
+
+@pytest.mark.parametrize("D,E,k,T", [(1024, 64, 8, 40), (8192, 16, 4, 12)])
+@pytest.mark.parametrize("x_scale", [1e6, 3e-8])
+def test_prefill_input_scale(gpu, D, E, k, T, x_scale):
+    """Inputs far outside f16's range and no RMSNorm weight (the way the drop-in builds its
+    blocks): x 1e6 would overflow f16 (65504) and x 3e-8 would fall into f16 subnormals
+    if the gate/up operand were f16(x) itself.  The operand is f16(x 2^s) with a
+    per-token power of two, undone exactly after the products; D = 8192 takes the prep
+    kernel's two-pass branch.  The router and shared gate (fp32) are divided by the
+    same factor so that the logits keep their usual size: at logits of 1e6 every
+    softmax probability but the largest underflows to an exact 0, and torch.topk
+    orders such ties arbitrarily."""
+    h = synth.host_moe_layer(150 + k, D=D, FF=256, E=E, k=k, bias=True)
+    h.router = (synth.as_f32(h.router) / x_scale).astype(np.float32)
+    h.sh_gate_inp = (synth.as_f32(h.sh_gate_inp) / x_scale).astype(np.float32)
+    _check(gpu, h, T, seed=k, rmsnorm_input=False, x_scale=x_scale)
 
 
 def test_prefill_rejects_wide_ff(gpu):
