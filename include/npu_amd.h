@@ -34,6 +34,10 @@ extern "C" {
 #define GM_QTYPE_IQ3_XXS 18
 #define GM_QTYPE_IQ4_XS 23
 #define GM_QTYPE_BF16 30
+/* Not a GGML type: K-quant / Q8_0 rows transcoded by gm_transcode_i8.  Per 32
+ * weights 48 bytes: int8 q[32], fp32 s0 (scale of q[0..15]), fp32 s1 (scale of
+ * q[16..31]), fp32 off, 4 zero bytes; weight k = s_{k/16} * q[k] + off. */
+#define GM_QTYPE_I8 100
 
 /* Status codes (negative = argument errors). */
 #define GM_OK 0
@@ -60,6 +64,18 @@ int gm_abi_version(void);
  * only 4-byte aligned out.
  */
 int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out, void* stream);
+
+/*
+ * Transcode n_blocks raw Q8_0 / Q4_K / Q5_K / Q6_K blocks into GM_QTYPE_I8
+ * sub-blocks (48 bytes per 32 weights, in weight order, so a row of K weights
+ * becomes a row of K / 32 * 48 bytes).  s * q + off reproduces gm_dequant_f32
+ * bit for bit.  The MoE kernels multiply I8 rows on v_dot4_i32_i8 with the
+ * int8 activation limbs.  Replaces the per-call dequant of K-quant expert and
+ * shared-expert tensors (qwen/forward.py:480-491 dequant_one, :495-498 for the
+ * Q5_K / Q6_K outlier layers, :465-468 for the shared expert).  out must be
+ * 16-byte aligned.
+ */
+int gm_transcode_i8(int qtype, const void* raw, int64_t n_blocks, void* out, void* stream);
 
 /*
  * y[t][m] = sum_k W[m][k] * x[t][k] for t < n_tok, W given as M rows of raw

@@ -24,6 +24,7 @@ GM_QTYPE_F16 = 1
 GM_QTYPE_IQ3_XXS = 18
 GM_QTYPE_IQ4_XS = 23
 GM_QTYPE_BF16 = 30
+GM_QTYPE_I8 = 100        # transcoded K-quant rows (gm_transcode_i8)
 
 GM_OK = 0
 GM_EINVAL = -1
@@ -60,6 +61,7 @@ SIGNATURES = {
     "gm_last_error": (ctypes.c_char_p, []),
     "gm_abi_version": (_i32, []),
     "gm_dequant_f32": (_i32, [_i32, _vp, _i64, _vp, _vp]),
+    "gm_transcode_i8": (_i32, [_i32, _vp, _i64, _vp, _vp]),
     "gm_matvec": (_i32, [_i32, _vp, _i32, _i32, _vp, _i32, _vp, _vp]),
     "gm_swiglu_mlp": (_i32, [_i32, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp]),
     "gm_router_topk": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp]),
@@ -88,7 +90,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(h, name)
             fn.restype = res
             fn.argtypes = args
-        if h.gm_abi_version() != 2:
+        if h.gm_abi_version() != 3:
             raise RuntimeError("libnpu_amd.so ABI version mismatch; rebuild it")
         _LIB = h
     return _LIB

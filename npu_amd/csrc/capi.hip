@@ -27,7 +27,7 @@ static inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream
 static inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 static bool is_quant(int q) { return q == GM_QTYPE_IQ4_XS || q == GM_QTYPE_IQ3_XXS; }
-static bool is_weight_fmt(int q) { return is_quant(q) || q == GM_QTYPE_BF16; }
+static bool is_weight_fmt(int q) { return is_quant(q) || q == GM_QTYPE_BF16 || q == GM_QTYPE_I8; }
 
 // K must be a multiple of 256 for superblock formats and of 32 for bf16.
 static int check_k(const char* fn, int qtype, int K) {
@@ -67,7 +67,7 @@ static int check_layer(const gm_moe_layer* L) {
     return gm_fail_arg("gm_moe_forward: routed expert / router weights must be non-NULL");
   if (!is_weight_fmt(L->q_gate) || L->q_up != L->q_gate || !is_weight_fmt(L->q_down))
     return gm_fail_arg("gm_moe_forward: routed formats gate %d up %d down %d unsupported (gate == up, "
-                       "IQ4_XS, IQ3_XXS or BF16)", L->q_gate, L->q_up, L->q_down);
+                       "IQ4_XS, IQ3_XXS, BF16 or I8)", L->q_gate, L->q_up, L->q_down);
   if (L->D % GM_QK || L->FF % GM_QK)
     return gm_fail_arg("gm_moe_forward: D=%d and FF=%d must be multiples of %d", L->D, L->FF, GM_QK);
   if (L->q_router != GM_QTYPE_BF16 && L->q_router != GM_QTYPE_F32)
@@ -94,7 +94,7 @@ extern "C" {
 
 const char* gm_last_error(void) { return g_err; }
 
-int gm_abi_version(void) { return 2; }
+int gm_abi_version(void) { return 3; }
 
 int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out, void* stream) {
   if (gm_kquant_block(qtype).bytes)
@@ -111,8 +111,18 @@ int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out
   return gm_launch_dequant(qtype, raw, n_superblocks, out, as_stream(stream));
 }
 
+int gm_transcode_i8(int qtype, const void* raw, int64_t n_blocks, void* out, void* stream) {
+  if (!gm_kquant_block(qtype).bytes)
+    return gm_fail_arg("gm_transcode_i8: qtype %d is not Q8_0(8)/Q4_K(12)/Q5_K(13)/Q6_K(14)", qtype);
+  if (n_blocks < 0) return gm_fail_arg("gm_transcode_i8: negative n_blocks");
+  if (n_blocks == 0) return GM_OK;
+  if (!raw || !out) return gm_fail_arg("gm_transcode_i8: NULL pointer");
+  if (reinterpret_cast<uintptr_t>(out) % 16) return gm_fail_arg("gm_transcode_i8: out must be 16-byte aligned");
+  return gm_launch_transcode_i8(qtype, raw, n_blocks, out, as_stream(stream));
+}
+
 int gm_matvec(int qtype, const void* w, int M, int K, const float* x, int n_tok, float* y, void* stream) {
-  if (!is_weight_fmt(qtype)) return gm_fail_arg("gm_matvec: unsupported qtype %d", qtype);
+  if (!is_quant(qtype) && qtype != GM_QTYPE_BF16) return gm_fail_arg("gm_matvec: unsupported qtype %d", qtype);
   if (int rc = check_k("gm_matvec", qtype, K)) return rc;
   if (M < 0 || n_tok < 0) return gm_fail_arg("gm_matvec: negative size");
   if (M == 0 || n_tok == 0) return GM_OK;
@@ -283,8 +293,8 @@ static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int
   if (decode) return gm_dec_run(L, x, y, T, flags, w, lay, s, stage);
   if (stage != 0) return gm_fail_arg("gm_moe_forward_stage: stages are only defined for the decode path (T <= 8)");
   const bool sh_mixed = L->gate_sh && (L->q_gate_sh != L->q_gate || L->q_down_sh != L->q_down);
-  if (L->q_gate == GM_QTYPE_BF16 || L->q_down == GM_QTYPE_BF16 || sh_mixed) {
-    // Routed experts held as bf16 (K-quant expert tensors dequantised at load),
+  if (!is_quant(L->q_gate) || !is_quant(L->q_down) || sh_mixed) {
+    // Routed experts held as bf16 or I8 rows (K-quant expert tensors),
     // or a shared expert in other formats than the routed ones (a dense bf16
     // shared expert beside IQ routed experts): the prefill GEMMs run the shared
     // expert as a ninth unit of the routed formats only, so the tokens run as

@@ -45,6 +45,7 @@ __host__ __device__ inline int gm_block_bytes(int qtype) {
   return qtype == GM_QTYPE_IQ4_XS ? GM_IQ4XS_BYTES
        : qtype == GM_QTYPE_IQ3_XXS ? GM_IQ3XXS_BYTES
        : qtype == GM_QTYPE_BF16 ? 2 * GM_QK
+       : qtype == GM_QTYPE_I8 ? 384
        : qtype == GM_QTYPE_F32 ? 4 * GM_QK : 0;
 }
 

@@ -171,16 +171,43 @@ __device__ __forceinline__ float gm_decode_bf16(const RawBf16& r, float (&wv)[32
   return 1.0f;
 }
 
+// -------------------------------------------------------------------- I8
+// Transcoded K-quant / Q8_0 rows (GM_QTYPE_I8, written by k_transcode_i8): a
+// 32-weight sub-block is 48 bytes, int8 q[32] (weight k = byte k), fp32 s0
+// (scale of weights 0-15), fp32 s1 (16-31), fp32 off, 4 zero bytes;
+// weight k = s_{k / 16} q[k] + off.
+struct RawI8 {
+  gm_u32x4 q0, q1, s;   // q[0..15], q[16..31], {s0, s1, off, 0}
+};
+
+template <bool ST = false>
+__device__ __forceinline__ RawI8 gm_load_i8(const uint8_t* __restrict__ row, int sub) {
+  const gm_u32x4* p = reinterpret_cast<const gm_u32x4*>(row + sub * 48);
+  return RawI8{gm_ld<ST>(p), gm_ld<ST>(p + 1), gm_ld<ST>(p + 2)};
+}
+
+__device__ __forceinline__ float gm_decode_i8row(const RawI8& r, float (&wv)[32]) {
+  const float s0 = __uint_as_float(r.s.x), s1 = __uint_as_float(r.s.y), off = __uint_as_float(r.s.z);
+  const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wv[4 * c + i] = fmaf(c < 4 ? s0 : s1, gm_sbyte(q[c], i), off);
+  return 1.0f;
+}
+
 // ---------------------------------------------------------- generic front
 template <int QT> struct RawSub;
 template <> struct RawSub<GM_QTYPE_IQ4_XS> { using T = RawIq4; };
 template <> struct RawSub<GM_QTYPE_IQ3_XXS> { using T = RawIq3; };
 template <> struct RawSub<GM_QTYPE_BF16> { using T = RawBf16; };
+template <> struct RawSub<GM_QTYPE_I8> { using T = RawI8; };
 
 template <int QT, bool ST = false>
 __device__ __forceinline__ typename RawSub<QT>::T gm_load_sub(const uint8_t* __restrict__ row, int sub) {
   if constexpr (QT == GM_QTYPE_IQ4_XS) return gm_load_iq4<ST>(row, sub);
   else if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_load_iq3<ST>(row, sub);
+  else if constexpr (QT == GM_QTYPE_I8) return gm_load_i8<ST>(row, sub);
   else return gm_load_bf16<ST>(row, sub);
 }
 
@@ -189,6 +216,7 @@ __device__ __forceinline__ float gm_decode_sub(const typename RawSub<QT>::T& r, 
                                                const uint32_t* __restrict__ grid, float (&wv)[32]) {
   if constexpr (QT == GM_QTYPE_IQ4_XS) return gm_decode_iq4(r, sub, wv);
   else if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_decode_iq3(r, grid, wv);
+  else if constexpr (QT == GM_QTYPE_I8) return gm_decode_i8row(r, wv);
   else return gm_decode_bf16(r, wv);
 }
 

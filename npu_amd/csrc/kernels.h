@@ -17,6 +17,7 @@ inline GmKBlock gm_kquant_block(int qtype) {
   }
 }
 int gm_launch_dequant_k(int qtype, const void* raw, int64_t n_blocks, float* out, hipStream_t s);
+int gm_launch_transcode_i8(int qtype, const void* raw, int64_t n_blocks, void* out, hipStream_t s);
 int gm_launch_matvec(int qtype, const void* w, int M, int K, const float* x, int n_tok, float* y,
                      hipStream_t s);
 // Dense bf16 matvec (K % 256 == 0, K <= 16384, 16-byte aligned w and x).

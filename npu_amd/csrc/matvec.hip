@@ -124,6 +124,89 @@ int gm_launch_dequant_k(int qtype, const void* raw, int64_t n_blocks, float* out
   return GM_OK;
 }
 
+// K-quant / Q8_0 rows -> I8 rows (GM_QTYPE_I8), one thread per 32-weight
+// sub-block: int8 quants in weight order, fp32 scales of weights 0-15 and
+// 16-31, fp32 offset, 4 zero bytes (48 bytes):
+//   Q8_0  q,                s0 = s1 = d,                 off = 0
+//   Q4_K  q (0..15),        s0 = s1 = d sc_s,            off = -(dmin m_s)
+//   Q5_K  q (0..31),        s0 = s1 = d sc_s,            off = -(dmin m_s)
+//   Q6_K  value - 32,       s0 = d sc[2s], s1 = d sc[2s+1], off = 0
+// The products d sc are exact in fp32, so s q + off is the dequantised weight
+// of k_dequant_k bit for bit (Q4_K / Q5_K: the same single rounding).
+template <int QT>
+__global__ void __launch_bounds__(256) k_transcode_i8(const uint8_t* __restrict__ raw, int64_t n_units,
+                                                      uint8_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_units) return;
+  int q[32];
+  float s0, s1, off = 0.f;
+  if constexpr (QT == GM_QTYPE_Q8_0) {
+    const uint8_t* b = raw + i * 34;
+    s0 = s1 = kq_h2f(b);
+#pragma unroll
+    for (int l = 0; l < 32; ++l) q[l] = (int8_t)b[2 + l];
+  } else if constexpr (QT == GM_QTYPE_Q6_K) {
+    const int s = (int)(i & 7);
+    const uint8_t* b = raw + (i >> 3) * 210;
+    const float d = kq_h2f(b + 208);
+    const int n = s >> 2, c = s & 3;
+    const uint8_t* ql = b + 64 * n + 32 * (c & 1);
+    const uint8_t* qh = b + 128 + 32 * n;
+    s0 = d * (float)(int8_t)b[192 + 2 * s];
+    s1 = d * (float)(int8_t)b[193 + 2 * s];
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      const int lo = c < 2 ? (ql[l] & 15) : (ql[l] >> 4);
+      q[l] = (lo | (((qh[l] >> (2 * c)) & 3) << 4)) - 32;
+    }
+  } else {
+    constexpr bool five = QT == GM_QTYPE_Q5_K;
+    constexpr int NB = five ? 176 : 144;
+    const int s = (int)(i & 7);
+    const uint8_t* b = raw + (i >> 3) * NB;
+    const float d = kq_h2f(b), dmin = kq_h2f(b + 2);
+    const uint8_t* sc = b + 4;
+    int scv, mv;
+    if (s < 4) { scv = sc[s] & 63; mv = sc[s + 4] & 63; }
+    else { scv = (sc[s + 4] & 15) | ((sc[s - 4] >> 6) << 4); mv = (sc[s + 4] >> 4) | ((sc[s] >> 6) << 4); }
+    s0 = s1 = d * (float)scv;
+    off = -(dmin * (float)mv);
+    const uint8_t* qs = b + (five ? 48 : 16) + 32 * (s >> 1);
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      q[l] = (s & 1) ? (qs[l] >> 4) : (qs[l] & 15);
+      if constexpr (five) q[l] += ((b[16 + l] >> s) & 1) << 4;
+    }
+  }
+  uint32_t w[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    w[c] = (uint32_t)(q[4 * c] & 255) | ((uint32_t)(q[4 * c + 1] & 255) << 8) | ((uint32_t)(q[4 * c + 2] & 255) << 16) |
+           ((uint32_t)(q[4 * c + 3] & 255) << 24);
+  gm_u32x4* o = reinterpret_cast<gm_u32x4*>(out + i * 48);
+  o[0] = gm_u32x4{w[0], w[1], w[2], w[3]};
+  o[1] = gm_u32x4{w[4], w[5], w[6], w[7]};
+  o[2] = gm_u32x4{__float_as_uint(s0), __float_as_uint(s1), __float_as_uint(off), 0u};
+}
+
+int gm_launch_transcode_i8(int qtype, const void* raw, int64_t n_blocks, void* out, hipStream_t s) {
+  const GmKBlock kb = gm_kquant_block(qtype);
+  const int64_t n_units = n_blocks * (kb.weights / 32);
+  if (n_units == 0) return GM_OK;
+  const dim3 grid((unsigned)((n_units + 255) / 256)), block(256);
+  const uint8_t* p = static_cast<const uint8_t*>(raw);
+  uint8_t* o = static_cast<uint8_t*>(out);
+  switch (qtype) {
+    case GM_QTYPE_Q8_0: hipLaunchKernelGGL(k_transcode_i8<GM_QTYPE_Q8_0>, grid, block, 0, s, p, n_units, o); break;
+    case GM_QTYPE_Q4_K: hipLaunchKernelGGL(k_transcode_i8<GM_QTYPE_Q4_K>, grid, block, 0, s, p, n_units, o); break;
+    case GM_QTYPE_Q5_K: hipLaunchKernelGGL(k_transcode_i8<GM_QTYPE_Q5_K>, grid, block, 0, s, p, n_units, o); break;
+    case GM_QTYPE_Q6_K: hipLaunchKernelGGL(k_transcode_i8<GM_QTYPE_Q6_K>, grid, block, 0, s, p, n_units, o); break;
+    default: return gm_fail_arg("gm_transcode_i8: unsupported qtype %d", qtype);
+  }
+  GM_TRY(hipGetLastError());
+  return GM_OK;
+}
+
 // --------------------------------------------------------------- matvec
 // Partial dot products of one lane for one row over its sub-blocks.
 template <int QT, int L, int NT>

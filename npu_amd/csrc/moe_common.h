@@ -407,6 +407,41 @@ __device__ __forceinline__ void router_unpack8(const RouterChunk<F32>& r, float 
   }
 }
 
+// --------------------------------------------------------- I8 x limbs
+// One I8 sub-block (int8 q, scales s0 / s1 of its halves, offset off) against
+// the limbs of one activation sub-block: s0 sum_{k<16} q_k a_k + s1 sum_{k>=16}
+// q_k a_k + off sum_k a_k, the products on v_dot4_i32_i8 (exact int32 sums per
+// half and limb), the activation sum stored with the limbs.
+__device__ __forceinline__ float gm_i8_limb_dot(const RawI8& r, const uint32_t (&l0)[8], const uint32_t (&l1)[8],
+                                               const uint32_t (&l2)[8], float hscale, float asum) {
+  const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+  int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    a0 = __builtin_amdgcn_sdot4((int)q[c], (int)l0[c], a0, false);
+    a1 = __builtin_amdgcn_sdot4((int)q[c], (int)l1[c], a1, false);
+    a2 = __builtin_amdgcn_sdot4((int)q[c], (int)l2[c], a2, false);
+    b0 = __builtin_amdgcn_sdot4((int)q[4 + c], (int)l0[4 + c], b0, false);
+    b1 = __builtin_amdgcn_sdot4((int)q[4 + c], (int)l1[4 + c], b1, false);
+    b2 = __builtin_amdgcn_sdot4((int)q[4 + c], (int)l2[4 + c], b2, false);
+  }
+  const float va = fmaf((float)a2, 65536.f, fmaf((float)a1, 256.f, (float)a0));
+  const float vb = fmaf((float)b2, 65536.f, fmaf((float)b1, 256.f, (float)b0));
+  const float s0 = __uint_as_float(r.s.x), s1 = __uint_as_float(r.s.y), off = __uint_as_float(r.s.z);
+  return fmaf(hscale, fmaf(s0, va, s1 * vb), off * asum);
+}
+
+// The same with the activation sub-block read from its limb row (LDS).
+__device__ __forceinline__ float gm_i8_dot_limbs(const RawI8& r, const uint8_t* __restrict__ s) {
+  const gm_u32x4* p = reinterpret_cast<const gm_u32x4*>(s);
+  const gm_u32x4 l0a = p[0], l0b = p[1], l1a = p[2], l1b = p[3], l2a = p[4], l2b = p[5];
+  const uint32_t l0[8] = {l0a.x, l0a.y, l0a.z, l0a.w, l0b.x, l0b.y, l0b.z, l0b.w};
+  const uint32_t l1[8] = {l1a.x, l1a.y, l1a.z, l1a.w, l1b.x, l1b.y, l1b.z, l1b.w};
+  const uint32_t l2[8] = {l2a.x, l2a.y, l2a.z, l2a.w, l2b.x, l2b.y, l2b.z, l2b.w};
+  const float2 hs = *reinterpret_cast<const float2*>(s + 96);
+  return gm_i8_limb_dot(r, l0, l1, l2, hs.x, hs.y);
+}
+
 // --------------------------------------------------------- row streaming
 // The decode kernels issue every weight load a lane needs before they wait on
 // anything: SPL sub-blocks per lane and row, at sub = lir + LR * i.  Indices
@@ -466,7 +501,8 @@ __device__ __forceinline__ void dot_subs(const RowFetch<QT, SPL>& f, int lir, in
 // sum_k w_k L_k (|w| <= 127, 32 terms) is an exact int32 below 2^24.
 // LDS layout per sub-block, GM_LSUB = 112 bytes (a 28-dword stride spreads 16
 // consecutive sub-blocks over all 64 banks): plane L0 (32 bytes, byte i of
-// dword c = k 4c + i), plane L1, plane L2, float 2^(E-22), 12 spare bytes.
+// dword c = k 4c + i), plane L1, plane L2, float 2^(E-22), float sum of the
+// 32 activations (the offset term of I8 weights), 8 spare bytes.
 constexpr int GM_LSUB = 112;
 
 __host__ __device__ inline int gm_limb_row_bytes(int K) { return (K / GM_SUB) * GM_LSUB; }
@@ -476,6 +512,14 @@ __device__ __forceinline__ float gm_max8(float m) {
   m = fmaxf(m, GM_DPP_F(m, GM_QPERM_1032));
   m = fmaxf(m, GM_DPP_F(m, GM_QPERM_2301));
   return fmaxf(m, GM_DPP_F(m, 0x141));                       // row_half_mirror
+}
+
+// Sum over lanes 8j .. 8j+7 (the same value in all of them: each step adds a
+// lane's partner, so all 8 lanes add the same terms, in the same order per pair).
+__device__ __forceinline__ float gm_sum8(float v) {
+  v += GM_DPP_F(v, GM_QPERM_1032);
+  v += GM_DPP_F(v, GM_QPERM_2301);
+  return v + GM_DPP_F(v, 0x141);                             // row_half_mirror
 }
 
 // Low bytes of four int32 -> one dword.
@@ -526,11 +570,14 @@ __device__ __forceinline__ void gm_put_limbs8(gm_f32x4 a, gm_f32x4 b, int c, uin
   uint32_t a0, a1, a2, b0, b1, b2;
   gm_limb_planes(a, up, a0, a1, a2);
   gm_limb_planes(b, up, b0, b1, b2);
+  float sum = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+  sum += GM_DPP_F(sum, GM_QPERM_1032);
+  sum += GM_DPP_F(sum, GM_QPERM_2301);
   uint8_t* sb = row + (c >> 3) * GM_LSUB + 4 * (c & 7);
   *reinterpret_cast<uint2*>(sb) = make_uint2(a0, b0);
   *reinterpret_cast<uint2*>(sb + 32) = make_uint2(a1, b1);
   *reinterpret_cast<uint2*>(sb + 64) = make_uint2(a2, b2);
-  *reinterpret_cast<float*>(row + (c >> 3) * GM_LSUB + 96) = scale;     // same value from all 4 lanes
+  *reinterpret_cast<float2*>(row + (c >> 3) * GM_LSUB + 96) = make_float2(scale, sum);   // same from all 4 lanes
 }
 
 // Limbs of activations 4c .. 4c+3 of a row into `row` (limb layout).  The 8
@@ -553,11 +600,12 @@ __device__ __forceinline__ void gm_put_limbs4(gm_f32x4 v, int c, uint8_t* __rest
   int t1[4], t2[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) { t1[i] = (q[i] + 128) >> 8; t2[i] = (t1[i] + 128) >> 8; }
+  const float sum = gm_sum8((v.x + v.y) + (v.z + v.w));
   uint8_t* sb = row + (c >> 3) * GM_LSUB + 4 * (c & 7);
   *reinterpret_cast<uint32_t*>(sb) = gm_pack_lo4(q[0], q[1], q[2], q[3]);
   *reinterpret_cast<uint32_t*>(sb + 32) = gm_pack_lo4(t1[0], t1[1], t1[2], t1[3]);
   *reinterpret_cast<uint32_t*>(sb + 64) = gm_pack_lo4(t2[0], t2[1], t2[2], t2[3]);
-  *reinterpret_cast<float*>(row + (c >> 3) * GM_LSUB + 96) = scale;     // same value from all 8 lanes
+  *reinterpret_cast<float2*>(row + (c >> 3) * GM_LSUB + 96) = make_float2(scale, sum);   // same from all 8 lanes
 }
 
 // One wave stages x [D] (XW float4 per lane, RMSNorm'd when norm_w != NULL)
@@ -632,7 +680,11 @@ __device__ __forceinline__ void dot_subs_i8(const RowFetch<QT, SPL>& f, int lir,
   for (int i = 0; i < SPL; ++i) {
     const int sub = lir + LR * i;
     if (sub < nsub) {
-      if constexpr (QT == GM_QTYPE_BF16) {
+      if constexpr (QT == GM_QTYPE_I8) {
+#pragma unroll
+        for (int m = 0; m < NT; ++m)
+          if (m < nt) acc[m] += gm_i8_dot_limbs(f.r[i], act + idx[m] * row_bytes + sub * GM_LSUB);
+      } else if constexpr (QT == GM_QTYPE_BF16) {
         float wv[32];
         gm_decode_bf16(f.r[i], wv);
 #pragma unroll

@@ -227,8 +227,9 @@ int gm_dec_run(const gm_moe_layer* P, const float* x, float* y, int T, int flags
   if (a.hsh != a.h + (size_t)T * P->k * P->FF) return gm_fail_arg("gm_moe_forward: internal workspace layout error");
   // The T = 1 down kernel stages (k + 1) rows of FF activations per block and
   // maps a wave's lanes onto 8 rows x FF/32 sub-blocks (FF/32 in {8, 16, 32}).
-  // (bf16 routed down rows fit the down kernel's LDS slices up to FF = 512)
-  const bool fast1 = T == 1 && (P->FF == 256 || P->FF == 512 || (P->FF == 1024 && P->q_down != GM_QTYPE_BF16));
+  // (bf16 and I8 routed down rows fit the down kernel's LDS slices up to FF = 512)
+  const bool fast1 = T == 1 && (P->FF == 256 || P->FF == 512 ||
+                                (P->FF == 1024 && P->q_down != GM_QTYPE_BF16 && P->q_down != GM_QTYPE_I8));
   if (stage == 0 || stage == 1)
     if (int rc = launch_router(P, x, T, a, s, fast1)) return rc;
   if (stage == 0 || stage == 2)

@@ -36,6 +36,40 @@ __device__ __forceinline__ float group_sum(float v, int n) {
 // The 8-row slices of the k + 1 down matrices are contiguous, 16-byte aligned
 // runs of raw superblocks: they are copied to LDS with 16-byte loads and
 // decoded from there.  The 9 x 8 partial sums are added in a fixed order.
+// One sub-block of a staged down row (LDS) against the limbs of the SwiGLU
+// sub-block: bf16 rows in fp32 (activations rebuilt from the limbs), I8 rows
+// with their half scales and offset, IQ rows on v_dot4 with one scale.
+template <int Q>
+__device__ __forceinline__ float down_sub_dot(const uint8_t* __restrict__ rowp, int sub, const Iq3Tab* __restrict__ tab,
+                                              const uint32_t (&l0)[8], const uint32_t (&l1)[8],
+                                              const uint32_t (&l2)[8], float2 hsa) {
+  const typename RawSub<Q>::T raw = gm_load_sub<Q>(rowp, sub);
+  if constexpr (Q == GM_QTYPE_BF16) {
+    float wv[32];
+    const float sc = gm_decode_sub_t<Q>(raw, sub, tab, wv);
+    float a = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        a = fmaf(wv[4 * c + b], fmaf(gm_sbyte(l2[c], b), 65536.f, fmaf(gm_sbyte(l1[c], b), 256.f, gm_sbyte(l0[c], b))), a);
+    return sc * hsa.x * a;
+  } else if constexpr (Q == GM_QTYPE_I8) {
+    return gm_i8_limb_dot(raw, l0, l1, l2, hsa.x, hsa.y);
+  } else {
+    uint32_t w[8];
+    const float sc = gm_decode_i8<Q>(raw, sub, tab, w);
+    int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      s0 = __builtin_amdgcn_sdot4((int)w[c], (int)l0[c], s0, false);
+      s1 = __builtin_amdgcn_sdot4((int)w[c], (int)l1[c], s1, false);
+      s2 = __builtin_amdgcn_sdot4((int)w[c], (int)l2[c], s2, false);
+    }
+    return sc * hsa.x * fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0));
+  }
+}
+
 template <int QTD, int QTS, int FC>
 __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* __restrict__ x, int flags,
                                                    const int32_t* __restrict__ g_grp, const float* __restrict__ h,
@@ -45,9 +79,10 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   constexpr bool IQ3 = QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS;
   constexpr int RMAX = 2 * FC;                                 // rows per lane, FF <= 512 FC
   constexpr int HPT = (9 * 128 * FC + NTH - 1) / NTH;          // float4 of the k + 1 SwiGLU rows per thread
-  constexpr int RB_MAX = QTD == GM_QTYPE_BF16 ? 1024 * FC : 2 * FC * GM_IQ4XS_BYTES;   // widest routed row
+  constexpr int RB_MAX = QTD == GM_QTYPE_BF16 ? 1024 * FC : QTD == GM_QTYPE_I8 ? 768 * FC
+                                                          : 2 * FC * GM_IQ4XS_BYTES;   // widest routed row
   constexpr int CR = (8 * 8 * RB_MAX / 16 + NTH - 1) / NTH;    // routed 16-byte chunks per thread
-  constexpr int RBS_MAX = QTS == GM_QTYPE_BF16 ? 1024 * FC : RB_MAX;
+  constexpr int RBS_MAX = QTS == GM_QTYPE_BF16 ? 1024 * FC : QTS == GM_QTYPE_I8 ? 768 * FC : RB_MAX;
   constexpr int CS = (8 * RBS_MAX / 16 + NTH - 1) / NTH;       // shared 16-byte chunks per thread
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ float s_wj[8];        // routing weight and h row of routed matrix m
@@ -149,47 +184,14 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
     const uint32_t l0[8] = {l0a.x, l0a.y, l0a.z, l0a.w, l0b.x, l0b.y, l0b.z, l0b.w};
     const uint32_t l1[8] = {l1a.x, l1a.y, l1a.z, l1a.w, l1b.x, l1b.y, l1b.z, l1b.w};
     const uint32_t l2[8] = {l2a.x, l2a.y, l2a.z, l2a.w, l2b.x, l2b.y, l2b.z, l2b.w};
-    const float hscale = *reinterpret_cast<const float*>(hsub + 96);
+    const float2 hsa = *reinterpret_cast<const float2*>(hsub + 96);   // limb scale, activation sum
     float part[RMAX];
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {
       part[r] = 0.f;
       if (r < R) {
-        if constexpr (QTD == GM_QTYPE_BF16 || QTS == GM_QTYPE_BF16) {
-          float wv[32], sc;                                    // bf16 matrices: fp32 activations from the limbs
-          if (routed) {
-            const typename RawSub<QTD>::T raw = gm_load_sub<QTD>(wr + (wave * 8 + rg * R + r) * rbd, sub);
-            sc = gm_decode_sub_t<QTD>(raw, sub, tab, wv);
-          } else {
-            const typename RawSub<QTS>::T raw = gm_load_sub<QTS>(wr + k * 8 * rbd + (rg * R + r) * rbs, sub);
-            sc = gm_decode_sub_t<QTS>(raw, sub, tab, wv);
-          }
-          float a = 0.f;
-#pragma unroll
-          for (int c = 0; c < 8; ++c)
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-              a = fmaf(wv[4 * c + b], fmaf(gm_sbyte(l2[c], b), 65536.f, fmaf(gm_sbyte(l1[c], b), 256.f, gm_sbyte(l0[c], b))), a);
-          part[r] = sc * hscale * a;
-        } else {
-          uint32_t w[8];
-          float sc;
-          if (routed) {
-            const typename RawSub<QTD>::T raw = gm_load_sub<QTD>(wr + (wave * 8 + rg * R + r) * rbd, sub);
-            sc = gm_decode_i8<QTD>(raw, sub, tab, w);
-          } else {
-            const typename RawSub<QTS>::T raw = gm_load_sub<QTS>(wr + k * 8 * rbd + (rg * R + r) * rbs, sub);
-            sc = gm_decode_i8<QTS>(raw, sub, tab, w);
-          }
-          int s0 = 0, s1 = 0, s2 = 0;
-#pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            s0 = __builtin_amdgcn_sdot4((int)w[c], (int)l0[c], s0, false);
-            s1 = __builtin_amdgcn_sdot4((int)w[c], (int)l1[c], s1, false);
-            s2 = __builtin_amdgcn_sdot4((int)w[c], (int)l2[c], s2, false);
-          }
-          part[r] = sc * hscale * fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0));
-        }
+        part[r] = routed ? down_sub_dot<QTD>(wr + (wave * 8 + rg * R + r) * rbd, sub, tab, l0, l1, l2, hsa)
+                         : down_sub_dot<QTS>(wr + k * 8 * rbd + (rg * R + r) * rbs, sub, tab, l0, l1, l2, hsa);
       }
     }
     GM_TL_MARK3(part[0]);
@@ -370,7 +372,7 @@ int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags,
               hipStream_t s) {
   const int D = P->D, FF = P->FF, k = P->k;
   if (fast1) {
-    if constexpr (FC <= (QTD == GM_QTYPE_BF16 ? 1 : 2)) {                // bf16 routed rows: 8 KB per 8-row slice
+    if constexpr (FC <= (QTD == GM_QTYPE_BF16 || QTD == GM_QTYPE_I8 ? 1 : 2)) {   // bf16 / I8 rows: 8 / 6 KB per slice
       const size_t wbytes = (size_t)k * 8 * gm_row_bytes(QTD, FF) + 8 * (size_t)gm_row_bytes(QTS, FF);
       const size_t smem = (size_t)(k + 2) * gm_limb_row_bytes(FF) + ((wbytes + 16 + 15) & ~(size_t)15) +
                           (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
@@ -414,6 +416,7 @@ int launch_dn_s(const gm_moe_layer* P, const float* x, float* y, int T, int flag
     case GM_QTYPE_IQ4_XS: return launch_dn_f<QTD, GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s);
     case GM_QTYPE_IQ3_XXS: return launch_dn_f<QTD, GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s);
     case GM_QTYPE_BF16: return launch_dn_f<QTD, GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s);
+    case GM_QTYPE_I8: return launch_dn_f<QTD, GM_QTYPE_I8>(P, x, y, T, flags, fast1, a, s);
     default: return gm_fail_arg("gm_moe_forward: shared down format %d unsupported", P->q_down_sh);
   }
 }
@@ -426,6 +429,7 @@ int gm_dec_down(const gm_moe_layer* P, const float* x, float* y, int T, int flag
     case GM_QTYPE_IQ4_XS: return launch_dn_s<GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s);
     case GM_QTYPE_IQ3_XXS: return launch_dn_s<GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s);
     case GM_QTYPE_BF16: return launch_dn_s<GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s);
+    case GM_QTYPE_I8: return launch_dn_s<GM_QTYPE_I8>(P, x, y, T, flags, fast1, a, s);
     default: return gm_fail_arg("gm_moe_forward: routed down format %d unsupported", P->q_down);
   }
 }

@@ -391,6 +391,7 @@ int launch_gu_s(const gm_moe_layer* P, const float* x, int T, bool fast1, const 
     case GM_QTYPE_IQ4_XS: return launch_gu_q<QT, GM_QTYPE_IQ4_XS>(P, x, T, fast1, a, s);
     case GM_QTYPE_IQ3_XXS: return launch_gu_q<QT, GM_QTYPE_IQ3_XXS>(P, x, T, fast1, a, s);
     case GM_QTYPE_BF16: return launch_gu_q<QT, GM_QTYPE_BF16>(P, x, T, fast1, a, s);
+    case GM_QTYPE_I8: return launch_gu_q<QT, GM_QTYPE_I8>(P, x, T, fast1, a, s);
     default: return gm_fail_arg("gm_moe_forward: shared gate/up format %d unsupported", P->q_gate_sh);
   }
 }
@@ -402,6 +403,7 @@ int gm_dec_gateup(const gm_moe_layer* P, const float* x, int T, bool fast1, cons
     case GM_QTYPE_IQ4_XS: return launch_gu_s<GM_QTYPE_IQ4_XS>(P, x, T, fast1, a, s);
     case GM_QTYPE_IQ3_XXS: return launch_gu_s<GM_QTYPE_IQ3_XXS>(P, x, T, fast1, a, s);
     case GM_QTYPE_BF16: return launch_gu_s<GM_QTYPE_BF16>(P, x, T, fast1, a, s);
+    case GM_QTYPE_I8: return launch_gu_s<GM_QTYPE_I8>(P, x, T, fast1, a, s);
     default: return gm_fail_arg("gm_moe_forward: routed gate/up format %d unsupported", P->q_gate);
   }
 }

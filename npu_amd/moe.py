@@ -35,21 +35,22 @@ def _dev(a, dtype=None, device="cuda") -> torch.Tensor | None:
 
 
 # Expert tensors in these types (the Q5_K / Q6_K outliers of the reference model,
-# qwen/forward.py:495-498, and Q8_0 / Q4_K) are dequantised on the device once,
-# at load, and kept as bf16 rows: the decode kernels take bf16 weights, so the
-# routed path stays the same device path for every layer.
+# qwen/forward.py:495-498, Q8_0 / Q6_K shared experts, and Q4_K) are transcoded on
+# the device once, at load, into I8 rows (int8 quants, fp32 scales per 16 weights,
+# an fp32 offset per 32; exact): the decode kernels multiply them on v_dot4 like the
+# IQ formats.
 _KQUANTS = (QT.Q8_0, QT.Q4_K, QT.Q5_K, QT.Q6_K)
+I8 = L.GM_QTYPE_I8
 
 
-def _kquant_to_bf16(raw: torch.Tensor, q: int, n: int, M: int, K: int) -> torch.Tensor:
-    """uint8 [n?, M, row_bytes] K-quant rows on the GPU -> bf16 bits (int16) [n?, M, K], one
-    matrix at a time through ``gm_dequant_f32`` (fp32, exact) and a round to nearest even."""
-    flat = raw.reshape(n, -1)
-    out = torch.empty((n, M, K), dtype=torch.bfloat16, device=raw.device)
-    for e in range(n):
-        out[e] = ops.dequant(q, flat[e].contiguous()).view(M, K).to(torch.bfloat16)
-    out = out.view(torch.int16)
-    return out if raw.dim() == 3 else out[0]
+def _row_bytes(q: int, K: int) -> int:
+    return K // 32 * 48 if q == I8 else row_bytes(q, K)
+
+
+def _kquant_to_i8(raw: torch.Tensor, q: int, M: int, K: int) -> torch.Tensor:
+    """uint8 [n?, M, row_bytes] K-quant rows on the GPU -> I8 rows uint8 [n?, M, K / 32 * 48]."""
+    out = ops.transcode_i8(q, raw.contiguous().reshape(-1))
+    return out.view(*raw.shape[:-2], M, K // 32 * 48)
 
 
 def _router_fmt(t: torch.Tensor | None, f32: bool) -> torch.Tensor | None:
@@ -98,21 +99,21 @@ class GpuMoeBlock:
             self.gate_sh, self.up_sh = self.gate_sh.view(torch.int16), self.up_sh.view(torch.int16)
         if self.q_down_sh == QT.BF16 and self.down_sh is not None and self.down_sh.dtype == torch.bfloat16:
             self.down_sh = self.down_sh.view(torch.int16)
-        # K-quant experts (routed and shared) -> bf16 rows on the device
+        # K-quant experts (routed and shared) -> I8 rows on the device
         if self.q_gate in _KQUANTS:
-            self.gate = _kquant_to_bf16(self.gate, self.q_gate, self.E, self.FF, self.D)
-            self.up = _kquant_to_bf16(self.up, self.q_gate, self.E, self.FF, self.D)
-            self.q_gate = int(QT.BF16)
+            self.gate = _kquant_to_i8(self.gate, self.q_gate, self.FF, self.D)
+            self.up = _kquant_to_i8(self.up, self.q_gate, self.FF, self.D)
+            self.q_gate = I8
         if self.q_down in _KQUANTS:
-            self.down = _kquant_to_bf16(self.down, self.q_down, self.E, self.D, self.FF)
-            self.q_down = int(QT.BF16)
+            self.down = _kquant_to_i8(self.down, self.q_down, self.D, self.FF)
+            self.q_down = I8
         if self.gate_sh is not None and self.q_gate_sh in _KQUANTS:
-            self.gate_sh = _kquant_to_bf16(self.gate_sh, self.q_gate_sh, 1, self.FF, self.D)
-            self.up_sh = _kquant_to_bf16(self.up_sh, self.q_gate_sh, 1, self.FF, self.D)
-            self.q_gate_sh = int(QT.BF16)
+            self.gate_sh = _kquant_to_i8(self.gate_sh, self.q_gate_sh, self.FF, self.D)
+            self.up_sh = _kquant_to_i8(self.up_sh, self.q_gate_sh, self.FF, self.D)
+            self.q_gate_sh = I8
         if self.down_sh is not None and self.q_down_sh in _KQUANTS:
-            self.down_sh = _kquant_to_bf16(self.down_sh, self.q_down_sh, 1, self.D, self.FF)
-            self.q_down_sh = int(QT.BF16)
+            self.down_sh = _kquant_to_i8(self.down_sh, self.q_down_sh, self.D, self.FF)
+            self.q_down_sh = I8
         if self.q_gate == QT.BF16 and self.gate.dtype == torch.bfloat16:
             self.gate, self.up = self.gate.view(torch.int16), self.up.view(torch.int16)
         if self.q_down == QT.BF16 and self.down.dtype == torch.bfloat16:
@@ -139,8 +140,8 @@ class GpuMoeBlock:
     def _check_shapes(self) -> None:
         D, FF, E = self.D, self.FF, self.E
 
-        def want(q, M, K):                     # raw rows, or bf16 bits [.., M, K]
-            return ((E, M, K), torch.int16) if q == QT.BF16 else ((E, M, row_bytes(q, K)), torch.uint8)
+        def want(q, M, K):                     # raw or I8 rows, or bf16 bits [.., M, K]
+            return ((E, M, K), torch.int16) if q == QT.BF16 else ((E, M, _row_bytes(q, K)), torch.uint8)
         for name, (shp, dt) in {"gate": want(self.q_gate, FF, D), "up": want(self.q_gate, FF, D),
                                 "down": want(self.q_down, D, FF)}.items():
             t = getattr(self, name)
@@ -149,7 +150,7 @@ class GpuMoeBlock:
         if tuple(self.router.shape) != (E, D):
             raise ValueError(f"router: expected ({E}, {D}), got {tuple(self.router.shape)}")
         if self.gate_sh is not None:
-            rb = (lambda q, K: row_bytes(q, K) if q != QT.BF16 else 2 * K)
+            rb = (lambda q, K: _row_bytes(q, K) if q != QT.BF16 else 2 * K)
             g_elt = 1 if self.gate_sh.dtype == torch.uint8 else 2
             if self.gate_sh.numel() * g_elt != FF * rb(self.q_gate_sh, D):
                 raise ValueError("gate_sh size does not match FF x D")

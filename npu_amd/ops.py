@@ -37,6 +37,21 @@ def dequant(qtype: int, raw: torch.Tensor, n_superblocks: int | None = None) -> 
     return out
 
 
+def transcode_i8(qtype: int, raw: torch.Tensor) -> torch.Tensor:
+    """Raw Q8_0 / Q4_K / Q5_K / Q6_K blocks (uint8, on GPU) -> I8 sub-blocks (uint8, 48 bytes
+    per 32 weights, in weight order; ``gm_transcode_i8``)."""
+    bb, bw = block_bytes(qtype), block_weights(qtype)
+    if raw.dtype != torch.uint8:
+        raise TypeError(f"raw must be uint8, got {raw.dtype}")
+    if raw.numel() % bb:
+        raise ValueError(f"{raw.numel()} bytes is not a whole number of {bb}-byte blocks")
+    n = raw.numel() // bb
+    out = torch.empty(n * bw // 32 * 48, dtype=torch.uint8, device=raw.device)
+    L.check(L.lib().gm_transcode_i8(int(qtype), L.ptr(raw.contiguous()), n, L.ptr(out), L.stream_ptr()),
+            "gm_transcode_i8")
+    return out
+
+
 def matvec(qtype: int, w: torch.Tensor, M: int, K: int, x: torch.Tensor) -> torch.Tensor:
     """y[..., M] = W[M, K] @ x[..., K] with W raw (IQ4_XS/IQ3_XXS) or bf16."""
     if qtype == GGMLQuantizationType.BF16:

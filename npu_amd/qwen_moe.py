@@ -23,6 +23,7 @@ from typing import Sequence
 import numpy as np
 import torch
 
+from npu_amd import _lib as L
 from npu_amd import ops
 from npu_amd._dropin import device
 from npu_amd.gguf_types import GGMLQuantizationType as QT, QuantTensor, row_bytes
@@ -167,6 +168,42 @@ class MoELayer:
         return tuple(out)
 
 
+_IQ = (int(QT.IQ4_XS), int(QT.IQ3_XXS))
+_KQ = (int(QT.Q8_0), int(QT.Q4_K), int(QT.Q5_K), int(QT.Q6_K))
+
+
+def _shared_raw(ts, names, D: int, FF: int) -> dict | None:
+    """The shared expert from the file's raw bytes when its formats run natively: gate and
+    up both IQ4_XS / IQ3_XXS of one type (kept raw), or both K-quants (each transcoded to
+    I8 rows, so Q6_K gate with Q8_0 up works); down IQ (raw) or a K-quant (I8).  None
+    when the tensors are absent or in other types (then the dense fp32 copy is used)."""
+    if not all(ts.has(n) for n in names):
+        return None
+    gs, us, ds = (ts.raw(n) for n in names)
+    tg, tu, td = int(gs.tensor_type), int(us.tensor_type), int(ds.tensor_type)
+
+    def dev(t):
+        a = np.ascontiguousarray(t.data).reshape(-1)
+        return torch.from_numpy(a if a.flags.writeable else a.copy()).to(device())
+
+    def i8(t, q, M, K):
+        return ops.transcode_i8(q, dev(t)).view(M, K // 32 * 48)
+
+    if tg == tu and tg in _IQ:
+        out = dict(gate_sh=gs.data, up_sh=us.data, q_gate_sh=tg)
+    elif tg in _KQ and tu in _KQ:
+        out = dict(gate_sh=i8(gs, tg, FF, D), up_sh=i8(us, tu, FF, D), q_gate_sh=L.GM_QTYPE_I8)
+    else:
+        return None
+    if td in _IQ:
+        out.update(down_sh=ds.data, q_down_sh=td)
+    elif td in _KQ:
+        out.update(down_sh=i8(ds, td, D, FF), q_down_sh=L.GM_QTYPE_I8)
+    else:
+        return None
+    return out
+
+
 def _exact_bf16_or_f32(w: torch.Tensor) -> torch.Tensor:
     """fp32 weights as bf16 when every value is a bf16 value (half the bytes, same
     numbers), else unchanged fp32."""
@@ -188,14 +225,13 @@ def _build_block(layer: MoELayer) -> GpuMoeBlock:
     # (qwen/forward.py:41-47, 599, 608); they are stored as bf16 only when that is exact.
     router = _exact_bf16_or_f32(layer.w_router)
     kw = {}
-    if layer.w_gate_sh is not None:              # dense shared expert (the real model): bf16
+    sh_names = tuple(p + n for n in ("ffn_gate_shexp.weight", "ffn_up_shexp.weight", "ffn_down_shexp.weight"))
+    sh_raw = _shared_raw(ts, sh_names, D, FF)
+    if sh_raw is not None:                       # the file's shared expert bytes: IQ kept raw, K-quants as I8
+        kw.update(sh_raw)
+    elif layer.w_gate_sh is not None:            # a dense shared expert without raw bytes: bf16
         kw.update(gate_sh=layer.w_gate_sh.to(torch.bfloat16), up_sh=layer.w_up_sh.to(torch.bfloat16),
                   down_sh=layer.w_down_sh.to(torch.bfloat16), q_gate_sh=QT.BF16, q_down_sh=QT.BF16)
-    elif ts.has(p + "ffn_gate_shexp.weight"):     # quantised shared expert kept raw
-        gs, us, ds = (ts.raw(p + n) for n in ("ffn_gate_shexp.weight", "ffn_up_shexp.weight",
-                                               "ffn_down_shexp.weight"))
-        kw.update(gate_sh=gs.data, up_sh=us.data, down_sh=ds.data, q_gate_sh=int(gs.tensor_type),
-                  q_down_sh=int(ds.tensor_type))
     sh_inp = None
     if layer.w_gate_inp_sh is not None:
         sh_inp = _exact_bf16_or_f32(layer.w_gate_inp_sh)

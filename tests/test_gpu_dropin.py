@@ -146,9 +146,9 @@ def test_qwen_moe_forward_from_gguf_file(gpu, tmp_path, T):
 def test_qwen_moe_forward_kquant_layers(gpu, tmp_path, T):
     """A model file whose second layer holds Q5_K gate/up and Q6_K down experts, as the
     reference model's blk.1 / blk.34 outliers (qwen/forward.py:495-498): the drop-in runs
-    every layer on the device (the K-quant experts dequantised once to bf16 rows), where
-    the reference keeps a per-expert CPU dequant + F.linear for them.  Bar: 1e-2 for the
-    bf16-held layer, 1e-3 for the IQ layer at T <= 8."""
+    every layer on the device (the K-quant experts transcoded once to I8 rows), where
+    the reference keeps a per-expert CPU dequant + F.linear for them.  Bar: 1e-3, except
+    the IQ layer at T > 8 (the prefill GEMMs, 1e-2)."""
     from npu_amd import gguf_file
     hs = [synth.host_moe_layer(70, D=1024, FF=256, E=32, k=4, q_gate=QT.IQ3_XXS, q_down=QT.IQ4_XS),
           synth.host_moe_layer(71, D=1024, FF=256, E=32, k=4, q_gate=QT.Q5_K, q_down=QT.Q6_K)]
@@ -161,6 +161,6 @@ def test_qwen_moe_forward_kquant_layers(gpu, tmp_path, T):
     for i, L in enumerate(layers):
         y = qwen_moe.moe_forward(x, L, ts.cfg)
         ref = OM.moe_forward(x, OM.OracleLayer(hs[i]))
-        bar = 1e-3 if (i == 0 and T <= 8) else 1e-2
+        bar = 1e-2 if (i == 0 and T > 8) else 1e-3
         assert OM.rel_err(y, ref) <= bar, (i, OM.rel_err(y, ref))
 
