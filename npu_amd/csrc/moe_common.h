@@ -561,23 +561,39 @@ __device__ __forceinline__ float gm_absmax4(gm_f32x4 v) {
 // Limbs of activations 4c .. 4c+7 (c even) of a row into `row`: as
 // gm_put_limbs4 with 4 lanes per sub-block (lanes 4j .. 4j+3, c / 2 % 4 ==
 // lane % 4).
-__device__ __forceinline__ void gm_put_limbs8(gm_f32x4 a, gm_f32x4 b, int c, uint8_t* __restrict__ row) {
+// The limbs, scale and activation sum of 8 values (a, b), computed by 4 lanes
+// per sub-block as gm_put_limbs8 describes; stored with gm_store_limbs8.
+struct GmLimbs8 {
+  uint32_t a0, a1, a2, b0, b1, b2;
+  float scale, sum;
+};
+
+__device__ __forceinline__ GmLimbs8 gm_limbs8(gm_f32x4 a, gm_f32x4 b) {
   float m = fmaxf(gm_absmax4(a), gm_absmax4(b));
   m = fmaxf(m, GM_DPP_F(m, GM_QPERM_1032));
   m = fmaxf(m, GM_DPP_F(m, GM_QPERM_2301));
-  float up, scale;
-  gm_limb_scale(m, up, scale);
-  uint32_t a0, a1, a2, b0, b1, b2;
-  gm_limb_planes(a, up, a0, a1, a2);
-  gm_limb_planes(b, up, b0, b1, b2);
+  float up;
+  GmLimbs8 l;
+  gm_limb_scale(m, up, l.scale);
+  gm_limb_planes(a, up, l.a0, l.a1, l.a2);
+  gm_limb_planes(b, up, l.b0, l.b1, l.b2);
   float sum = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
   sum += GM_DPP_F(sum, GM_QPERM_1032);
   sum += GM_DPP_F(sum, GM_QPERM_2301);
+  l.sum = sum;
+  return l;
+}
+
+__device__ __forceinline__ void gm_store_limbs8(const GmLimbs8& l, int c, uint8_t* __restrict__ row) {
   uint8_t* sb = row + (c >> 3) * GM_LSUB + 4 * (c & 7);
-  *reinterpret_cast<uint2*>(sb) = make_uint2(a0, b0);
-  *reinterpret_cast<uint2*>(sb + 32) = make_uint2(a1, b1);
-  *reinterpret_cast<uint2*>(sb + 64) = make_uint2(a2, b2);
-  *reinterpret_cast<float2*>(row + (c >> 3) * GM_LSUB + 96) = make_float2(scale, sum);   // same from all 4 lanes
+  *reinterpret_cast<uint2*>(sb) = make_uint2(l.a0, l.b0);
+  *reinterpret_cast<uint2*>(sb + 32) = make_uint2(l.a1, l.b1);
+  *reinterpret_cast<uint2*>(sb + 64) = make_uint2(l.a2, l.b2);
+  *reinterpret_cast<float2*>(row + (c >> 3) * GM_LSUB + 96) = make_float2(l.scale, l.sum);   // same from all 4 lanes
+}
+
+__device__ __forceinline__ void gm_put_limbs8(gm_f32x4 a, gm_f32x4 b, int c, uint8_t* __restrict__ row) {
+  gm_store_limbs8(gm_limbs8(a, b), c, row);
 }
 
 // Limbs of activations 4c .. 4c+3 of a row into `row` (limb layout).  The 8

@@ -29,9 +29,11 @@ namespace {
 // all of them are loaded before anything waits, so the row costs one round
 // trip.  Every wave sums x^2 over its own copy of x, so the RMSNorm factor
 // rms = 1 / sqrt(mean(x^2) + eps) (qwen/forward.py:58-61) needs no block
-// reduction; it scales the finished dot product W . (x * w_norm).  Global waves
-// i < NCH also write chunk i of the limb row of xn = (x * rms) * w_norm that
-// the gate/up kernel multiplies with.
+// reduction; it scales the finished dot product W . (x * w_norm).  The first
+// NL = NCH global waves (when xl_out is set) load no router row: wave i writes
+// chunk i of the limb row of xn = (x * rms) * w_norm that the gate/up kernel
+// multiplies with, a dependent chain of about 0.35 us that a row wave would
+// otherwise add to its dot product.
 template <int NCH, bool RF32>
 __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float* __restrict__ x,
                                                      float* __restrict__ logits, float* __restrict__ shg,
@@ -39,14 +41,18 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
   GM_TL_BEGIN();
   const int lane = threadIdx.x & 63, gw = blockIdx.x * 2 + (threadIdx.x >> 6);
   const int D = P.D, E = P.E, nrows = E + (P.sh_gate_inp != nullptr ? 1 : 0);
-  const int row = gw < nrows ? gw : nrows - 1;                  // spare waves redo the last row
+  const int nl = xl_out != nullptr ? NCH : 0;
+  const bool limb_wave = gw < nl;                               // uniform per wave
+  const int r = gw - nl;
+  const int row = r < nrows ? (r < 0 ? 0 : r) : nrows - 1;    // spare waves redo the last row
   const void* wr = row < E ? router_row<RF32>(P.router, row, D) : P.sh_gate_inp;
   RouterChunk<RF32> wb[NCH];
   gm_f32x4 xa[NCH], xb[NCH], na[NCH], nb[NCH];
+  // x and the RMSNorm weight first: the wait for them (vmcnt retires in issue
+  // order) then never waits for the router row
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int kk = 512 * i + 8 * lane < D ? 512 * i + 8 * lane : D - 8;   // lanes past D re-read the end
-    router_load8<RF32, true>(wr, kk, wb[i]);
     xa[i] = *reinterpret_cast<const gm_f32x4*>(x + kk);
     xb[i] = *reinterpret_cast<const gm_f32x4*>(x + kk + 4);
     if (P.norm_w) {
@@ -57,42 +63,62 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
       nb[i] = na[i];
     }
   }
-  const float bias = P.router_bias != nullptr && row < E ? P.router_bias[row] : 0.f;
-  float dot = 0.f, ss = 0.f;
+  if (!limb_wave) {
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    if (512 * i + 8 * lane < D) {
-      const float xv[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
-      const float nv[8] = {na[i].x, na[i].y, na[i].z, na[i].w, nb[i].x, nb[i].y, nb[i].z, nb[i].w};
-      float w[8];
-      router_unpack8<RF32>(wb[i], w);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        dot = fmaf(w[j], xv[j] * nv[j], dot);
-        ss = fmaf(xv[j], xv[j], ss);
-      }
+    for (int i = 0; i < NCH; ++i) {
+      const int kk = 512 * i + 8 * lane < D ? 512 * i + 8 * lane : D - 8;
+      router_load8<RF32, true>(wr, kk, wb[i]);
     }
   }
-  GM_TL_MARK1(dot);
-  dot = gm_wave_sum64(dot);
+  const float bias = P.router_bias != nullptr && row < E ? P.router_bias[row] : 0.f;
+  issue_fence();
+  // branch-free sums (lanes past D select 0): a branch per chunk made the
+  // compiler wait for every outstanding memory operation
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const float xv[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
+    float p = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p = fmaf(xv[j], xv[j], p);
+    ss += 512 * i + 8 * lane < D ? p : 0.f;
+  }
   ss = gm_wave_sum64(ss);
   const float rms = P.norm_w != nullptr ? 1.0f / sqrtf(ss / (float)D + P.norm_eps) : 1.0f;
-  GM_TL_MARK2(rms);
-  if (gw < nrows && lane == 0) {
+  GM_TL_MARK1(rms);
+  if (limb_wave) {
+    if (512 * gw < D) {
+      const int i = gw;
+      gm_f32x4 a = xa[0], b = xb[0], wa = na[0], wb2 = nb[0];
+#pragma unroll
+      for (int q = 1; q < NCH; ++q)
+        if (q == i) { a = xa[q]; b = xb[q]; wa = na[q]; wb2 = nb[q]; }
+      a.x = (a.x * rms) * wa.x; a.y = (a.y * rms) * wa.y; a.z = (a.z * rms) * wa.z; a.w = (a.w * rms) * wa.w;
+      b.x = (b.x * rms) * wb2.x; b.y = (b.y * rms) * wb2.y; b.z = (b.z * rms) * wb2.z; b.w = (b.w * rms) * wb2.w;
+      const int c = (512 * i + 8 * lane) >> 2;                   // float4 index, even
+      // lanes past D write the spare sub-block after the row
+      gm_put_limbs8(a, b, 512 * i + 8 * lane < D ? c : (D >> 2) + (c & 7), xl_out);
+    }
+    GM_TL_END(0);
+    return;
+  }
+  float dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const float xv[8] = {xa[i].x, xa[i].y, xa[i].z, xa[i].w, xb[i].x, xb[i].y, xb[i].z, xb[i].w};
+    const float nv[8] = {na[i].x, na[i].y, na[i].z, na[i].w, nb[i].x, nb[i].y, nb[i].z, nb[i].w};
+    float w[8];
+    router_unpack8<RF32>(wb[i], w);
+    float p = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p = fmaf(w[j], xv[j] * nv[j], p);
+    dot += 512 * i + 8 * lane < D ? p : 0.f;
+  }
+  dot = gm_wave_sum64(dot);
+  GM_TL_MARK2(dot);
+  if (r < nrows && lane == 0) {
     if (row < E) logits[row] = rms * dot + bias;
     else shg[0] = gm_sigmoid(rms * dot);
-  }
-  if (xl_out != nullptr && gw < NCH && 512 * gw < D) {          // uniform per wave
-    const int i = gw;
-    gm_f32x4 a = xa[0], b = xb[0], wa = na[0], wb2 = nb[0];
-#pragma unroll
-    for (int q = 1; q < NCH; ++q)
-      if (q == i) { a = xa[q]; b = xb[q]; wa = na[q]; wb2 = nb[q]; }
-    a.x = (a.x * rms) * wa.x; a.y = (a.y * rms) * wa.y; a.z = (a.z * rms) * wa.z; a.w = (a.w * rms) * wa.w;
-    b.x = (b.x * rms) * wb2.x; b.y = (b.y * rms) * wb2.y; b.z = (b.z * rms) * wb2.z; b.w = (b.w * rms) * wb2.w;
-    const int c = (512 * i + 8 * lane) >> 2;                     // float4 index, even
-    // lanes past D write the spare sub-block after the row
-    gm_put_limbs8(a, b, 512 * i + 8 * lane < D ? c : (D >> 2) + (c & 7), xl_out);
   }
   GM_TL_END(0);
 }
@@ -175,7 +201,7 @@ int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArg
     GM_TRY(hipGetLastError());
     return GM_OK;
   }
-  const dim3 grid((nrows + 1) / 2);
+  const dim3 grid((nrows + (P->D + 511) / 512 + 1) / 2);            // limb waves, then one wave per row
 #define GM_R1(n) hipLaunchKernelGGL((k_dec_router1<n, RF32>), grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl))
   switch ((P->D + 511) / 512) {
     case 1: GM_R1(1); break;
