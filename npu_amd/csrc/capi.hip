@@ -50,7 +50,6 @@ GmMoeWs gm_moe_ws_layout(const gm_moe_layer* L, int T) {
   w.hsh = o; o = align256(o + Tz * (size_t)(L->FF_sh > 0 ? L->FF_sh : 0) * 4);
   const size_t Td = T < GM_DECODE_MAX_T ? Tz : (size_t)GM_DECODE_MAX_T;   // decode chunk (bf16 routed experts)
   w.yp = o; o = align256(o + (Td * k + Td) * (size_t)L->D * 4);
-  w.counters = o; o = align256(o + 256);
   w.pre = o; o = align256(o + gm_prefill_scratch_bytes(L, T));     // every T: gm_moe_prefill takes any T
   w.tl = o; o = align256(o + GM_TL_BYTES);
   w.total = o;

@@ -35,7 +35,6 @@ struct GmMoeWs {
   size_t h;        // f32 [T][k][FF]  routed SwiGLU activations (decode)
   size_t hsh;      // f32 [T][FF_sh]  shared SwiGLU activations (directly after h)
   size_t yp;       // f32 [T * k + T][D]  per-pair / shared partial outputs (decode, T > 1)
-  size_t counters; // u32 [64]   self-resetting counters
   size_t pre;      // prefill scratch (see prefill.hip)
   size_t tl;       // per-block timestamps (profiling build only, else empty)
   size_t total;

@@ -45,6 +45,7 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
   const bool limb_wave = gw < nl;                               // uniform per wave
   const int r = gw - nl;
   const int row = r < nrows ? (r < 0 ? 0 : r) : nrows - 1;    // spare waves redo the last row
+  if (gw == 0 && lane == 0 && P.sh_gate_inp == nullptr) shg[0] = 1.f;   // no gate row: ungated shared expert
   const void* wr = row < E ? router_row<RF32>(P.router, row, D) : P.sh_gate_inp;
   RouterChunk<RF32> wb[NCH];
   gm_f32x4 xa[NCH], xb[NCH], na[NCH], nb[NCH];

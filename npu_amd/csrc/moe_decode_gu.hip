@@ -189,11 +189,11 @@ __global__ void __launch_bounds__(512) k_dec_route(gm_moe_layer P, const float* 
       v[i] = rms * a + (P.router_bias ? P.router_bias[r] : 0.f);
       if (ix[i] < E) logits[(int64_t)wave * E + ix[i]] = v[i];
     }
-    if (P.sh_gate_inp && lane == 0) {
+    if (lane == 0) {                                            // no gate row: the shared expert is ungated
       float a = 0.f;
 #pragma unroll
       for (int z = 0; z < NZ; ++z) a += z < nz ? pg[z] : 0.f;
-      shg[wave] = gm_sigmoid(rms * a);
+      shg[wave] = P.sh_gate_inp ? gm_sigmoid(rms * a) : 1.f;
     }
     int id;
     float w;

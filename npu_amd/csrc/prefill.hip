@@ -392,11 +392,11 @@ __global__ void __launch_bounds__(256) k_pf_topk(const float* __restrict__ part,
     v[i] = acc + (bias ? bias[r] : 0.f);
     if (ix[i] < E) logits[(int64_t)t * E + ix[i]] = v[i];
   }
-  if (has_gate && lane == 0) {
+  if (lane == 0) {                                          // no gate row: the shared expert is ungated
     float g = 0.f;
 #pragma unroll
     for (int z = 0; z < NZ; ++z) g += z < nsplit ? pg[z] : 0.f;
-    shg[t] = gm_sigmoid(g);
+    shg[t] = has_gate ? gm_sigmoid(g) : 1.f;
   }
   int id;
   float wt;

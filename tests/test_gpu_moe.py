@@ -195,3 +195,21 @@ def test_fifteen_router_ranges(gpu):
     """D = 3840: fifteen 256-wide router ranges, the 16-partial routing kernel."""
     h = synth.host_moe_layer(150, D=3840, FF=256, E=16, k=4, norm=True)
     _check(gpu, h, 8, residual=True, seed=3, rmsnorm_input=False)
+
+
+@pytest.mark.parametrize("T,path", [(1, "decode"), (3, "decode"), (12, "prefill")])
+def test_shared_expert_without_gate(gpu, T, path):
+    """A shared expert without a ffn_gate_inp_shexp row is added ungated, as the oracle
+    (and qwen/forward.py:592-600 with no gate tensor) does: every path writes a shared
+    gate of 1.0 instead of leaving the workspace word unset."""
+    h = synth.host_moe_layer(95 + T, norm=True)
+    h.sh_gate_inp = None
+    ol = OM.OracleLayer(h)
+    x = torch.from_numpy(synth.host_input(41 + T, T, h.D))
+    blk = GpuMoeBlock.from_host(h, device=gpu)
+    blk.workspace(T).fill_(0x7f)                  # a stale gate word would show as a wrong output
+    y = blk(x.to(gpu), path=path).cpu()
+    assert torch.equal(blk.stages(T)["shared_expert_gate_sigmoid"].cpu(), torch.ones(T))
+    ref = OM.block_forward(x, ol)
+    assert bool((OM.topk_margin(OM.router_logits64(x, ol), h.k) > 1e-5).all()), "near-tie: choose another seed"
+    assert OM.rel_err(y, ref) <= (1e-3 if path == "decode" else 1e-2), OM.rel_err(y, ref)
