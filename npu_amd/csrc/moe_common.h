@@ -93,6 +93,21 @@ __device__ __forceinline__ void stage_rows_il(const float* __restrict__ src, int
     for (int c = threadIdx.x; c < nq; c += blockDim.x) d4[r * nq + il_index4(c & 7, c >> 3, nsub)] = s4[(int64_t)r * nq + c];
 }
 
+// Max over lanes 8j .. 8j+7: the two quad swaps, then the half-row mirror.
+__device__ __forceinline__ float gm_max8(float m) {
+  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_1032));
+  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_2301));
+  return fmaxf(m, GM_DPP_F(m, 0x141));                       // row_half_mirror
+}
+
+// Sum over lanes 8j .. 8j+7 (the same value in all of them: each step adds a
+// lane's partner, so all 8 lanes add the same terms, in the same order per pair).
+__device__ __forceinline__ float gm_sum8(float v) {
+  v += GM_DPP_F(v, GM_QPERM_1032);
+  v += GM_DPP_F(v, GM_QPERM_2301);
+  return v + GM_DPP_F(v, 0x141);                             // row_half_mirror
+}
+
 // ------------------------------------------------------------------ top-k
 // One wave: top-k of E logits (descending, ties -> lower id), softmax over all
 // E, renormalised top-k probabilities (qwen/forward.py:609-611).
@@ -112,11 +127,13 @@ __device__ __forceinline__ void topk_load(const float* __restrict__ lg, int E, f
 // Unsigned key with the order of the float values: NaN of either sign is the
 // largest (torch.topk ranks NaN above every number), -0 and +0 are equal, and
 // every value has a key >= 0x007fffff (-inf), so 0 marks an absent entry.
+// Branch-free (selects only), so a wave's keys cost a few VALU per value.
 __device__ __forceinline__ uint32_t ukey(float f) {
   const uint32_t b = __float_as_uint(f);
-  if ((b & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;
-  if (b == 0x80000000u) return 0x80000000u;
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  const uint32_t flip = (uint32_t)((int32_t)b >> 31) | 0x80000000u;   // negative: all bits, else the sign bit
+  uint32_t k = b ^ flip;
+  k = b == 0x80000000u ? 0x80000000u : k;                             // -0: the key of +0
+  return (b & 0x7fffffffu) > 0x7f800000u ? 0xffffffffu : k;          // NaN of either sign: the largest
 }
 
 // Value back from a key (NaN keys give a NaN, -0 comes back as +0).
@@ -127,7 +144,10 @@ __device__ __forceinline__ float ukey_inv(uint32_t u) {
 template <int MAXV>
 __device__ __forceinline__ void topk_keys(const float (&v)[MAXV], const int (&ix)[MAXV], int E, uint32_t (&u)[MAXV]) {
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i) u[i] = ix[i] < E ? ukey(v[i]) : 0u;
+  for (int i = 0; i < MAXV; ++i) {
+    const uint32_t kv = ukey(v[i]);                      // computed for every lane, then masked
+    u[i] = ix[i] < E ? kv : 0u;
+  }
 }
 
 // Wave-uniform selection: on return bit l of sel[i] is set iff entry
@@ -197,80 +217,89 @@ __device__ __forceinline__ int topk_rank_id(const uint64_t (&sel)[MAXV], int r) 
   return id;
 }
 
-// Lane r < k gets the selected entry of rank r (ascending id): its id and key
-// (other lanes: id 0x7fffffff, key 0).
+// Lane r < k ends with the selected entry of rank r in ascending id order: its
+// key and id (other lanes: key 0, id 0x7fffffff).  Per key word, each lane
+// pushes its selected entry to lane (selected entries before it) with
+// ds_permute; unselected lanes push to lane 63, which holds no rank (k <= 8).
 template <int MAXV>
-__device__ __forceinline__ void topk_gather_rank(const uint64_t (&sel)[MAXV], const uint32_t (&u)[MAXV], int k,
-                                                 int& rid, uint32_t& rkey) {
+__device__ __forceinline__ void topk_compact(const uint64_t (&sel)[MAXV], const uint32_t (&u)[MAXV], int k,
+                                             uint32_t& rkey, int& rid) {
   const int lane = threadIdx.x & 63;
-  int pre = 0, src = 0, si = 0;
-  bool hit = false;
+  uint32_t key = 0u;
+  int id = 0x7fffffff;
+  int base = 0;
 #pragma unroll
   for (int i = 0; i < MAXV; ++i) {
-    const int c = __popcll(sel[i]);
-    const int j = lane - pre;
-    if (!hit && j >= 0 && j < c) {
-      uint64_t m = sel[i];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) m = t < j ? (m & (m - 1ull)) : m;
-      src = __builtin_ctzll(m);
-      si = i;
-      hit = true;
-    }
-    pre += c;
+    const uint64_t m = sel[i];
+    const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    const int dst = ((m >> lane) & 1ull) ? base + below : 63;
+    const uint32_t kv = (uint32_t)__builtin_amdgcn_ds_permute(dst << 2, (int)u[i]);
+    const int iv = __builtin_amdgcn_ds_permute(dst << 2, lane + 64 * i);
+    const int cnt = __popcll(m);
+    const bool here = lane >= base && lane < base + cnt;
+    key = here ? kv : key;
+    id = here ? iv : id;
+    base += cnt;
   }
-  uint32_t key = 0;
-#pragma unroll
-  for (int i = 0; i < MAXV; ++i) {
-    const uint32_t g = (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)u[i]);
-    key = si == i ? g : key;
-  }
-  const bool ok = lane < k && hit;
-  rid = ok ? src + 64 * si : 0x7fffffff;
-  rkey = ok ? key : 0u;
+  rkey = lane < k ? key : 0u;
+  rid = lane < k ? id : 0x7fffffff;
 }
 
-// Descending position of each rank's pick: larger keys first, equal keys in
-// ascending id order (lanes r < k; the others get 0x7fffffff).
-__device__ __forceinline__ int topk_slot(int rid, uint32_t rkey, int k) {
-  const int lane = threadIdx.x & 63;
-  int slot = 0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (j < k) {
-      const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)rkey, j);
-      const int ij = __builtin_amdgcn_readlane(rid, j);
-      slot += (kj > rkey || (kj == rkey && ij < rid)) ? 1 : 0;
-    }
-  }
-  return lane < k ? slot : 0x7fffffff;
-}
-
-// Renormalised softmax weight of the pick in lane r < k (key rkey): softmax
-// over all valid entries (maximum = the largest selected key), then
-// p / max(sum of the k picks, 1e-20).  Other lanes return 0.
+// Renormalised softmax weight of the pick in lane r < k (key rkey, lanes >= k
+// hold key 0): softmax over all valid entries with the largest key as the
+// maximum, then p / max(sum of the k picks, 1e-20) (qwen/forward.py:609-611).
+// Other lanes return 0.
 template <int MAXV>
-__device__ __forceinline__ float topk_rank_weight(const uint32_t (&u)[MAXV], uint32_t rkey, int k) {
+__device__ __forceinline__ float topk_weight(const uint32_t (&u)[MAXV], uint32_t rkey, int k) {
   const int lane = threadIdx.x & 63;
-  uint32_t mk = lane < k ? rkey : 0u;
-#pragma unroll
-  for (int o = 1; o < 8; o <<= 1) {
-    const uint32_t t = (uint32_t)__shfl_xor((int)mk, o, 64);
-    mk = t > mk ? t : mk;
-  }
-  const float m = ukey_inv((uint32_t)__builtin_amdgcn_readfirstlane((int)mk));
+  uint32_t mk = rkey;                                     // max over lanes 0 .. 7 (the picks)
+  mk = max(mk, (uint32_t)GM_DPP_I((int)mk, GM_QPERM_1032));
+  mk = max(mk, (uint32_t)GM_DPP_I((int)mk, GM_QPERM_2301));
+  mk = max(mk, (uint32_t)GM_DPP_I((int)mk, 0x141));       // row_half_mirror
+  const float m = ukey_inv((uint32_t)__builtin_amdgcn_readlane((int)mk, 0));
   float z = 0.f;
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i)
-    if (u[i] != 0u) z += expf(ukey_inv(u[i]) - m);
+  for (int i = 0; i < MAXV; ++i) {
+    const float e = expf(ukey_inv(u[i]) - m);
+    z += u[i] != 0u ? e : 0.f;
+  }
   z = gm_wave_sum64(z);
   const float p = lane < k ? expf(ukey_inv(rkey) - m) / z : 0.f;
-  const float den = fmaxf(gm_wave_sum64(p), 1e-20f);
+  const float den = fmaxf(gm_sum8(p), 1e-20f);           // lanes 0 .. 7: the sum of the k picks
   return p / den;
 }
 
-// Lane s < k ends with pick s in descending order: its expert id and
-// renormalised weight (other lanes: id 0x7fffffff, weight 0).
+// One compare-exchange stage of an 8-lane bitonic sort: the partner's pick via
+// DPP (CTRL), the lower lane of the pair keeps the better one (larger key,
+// then lower id).
+template <int CTRL>
+__device__ __forceinline__ void sort8_stage(uint32_t& key, int& id, float& w, bool lower) {
+  const uint32_t pk = (uint32_t)GM_DPP_I((int)key, CTRL);
+  const int pi = GM_DPP_I(id, CTRL);
+  const float pw = GM_DPP_F(w, CTRL);
+  const bool pbetter = pk > key || (pk == key && pi < id);
+  const bool take = lower ? pbetter : !pbetter;
+  key = take ? pk : key;
+  id = take ? pi : id;
+  w = take ? pw : w;
+}
+
+// Sorts each group of 8 lanes by (key descending, id ascending), carrying w:
+// bitonic merges of 2, 4 and 8 lanes, each opened by a mirrored compare
+// (partner 2^s - 1 - i) so that every stage sorts in the same direction.
+__device__ __forceinline__ void topk_sort8(uint32_t& key, int& id, float& w) {
+  const int l = threadIdx.x & 7;
+  sort8_stage<GM_QPERM_1032>(key, id, w, (l & 1) == 0);   // pairs (mirror of 2 = xor 1)
+  sort8_stage<0x1B>(key, id, w, (l & 3) < 2);              // quads: quad_perm [3,2,1,0]
+  sort8_stage<GM_QPERM_1032>(key, id, w, (l & 1) == 0);
+  sort8_stage<0x141>(key, id, w, l < 4);                   // eights: row_half_mirror
+  sort8_stage<GM_QPERM_2301>(key, id, w, (l & 2) == 0);
+  sort8_stage<GM_QPERM_1032>(key, id, w, (l & 1) == 0);
+}
+
+// Lane s < k ends with pick s in descending order (larger keys first, equal
+// keys in ascending id order): its expert id and renormalised weight (other
+// lanes: id 0x7fffffff, weight 0).
 template <int MAXV>
 __device__ __forceinline__ void topk_finish(const float (&v)[MAXV], const int (&ix)[MAXV], int E, int k,
                                             int& out_id, float& out_w) {
@@ -279,19 +308,13 @@ __device__ __forceinline__ void topk_finish(const float (&v)[MAXV], const int (&
   uint64_t sel[MAXV];
   topk_keys<MAXV>(v, ix, E, u);
   topk_masks<MAXV>(u, k, sel);
-  int rid;
-  uint32_t rkey;
-  topk_gather_rank<MAXV>(sel, u, k, rid, rkey);
-  const int slot = topk_slot(rid, rkey, k);
-  const float w = topk_rank_weight<MAXV>(u, rkey, k);
-  int src = 0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if (j < k) src = __builtin_amdgcn_readlane(slot, j) == lane ? j : src;
-  const int id = __builtin_amdgcn_ds_bpermute(src << 2, rid);
-  const float wt = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(w)));
+  uint32_t key;
+  int id;
+  topk_compact<MAXV>(sel, u, k, key, id);
+  float w = topk_weight<MAXV>(u, key, k);
+  topk_sort8(key, id, w);
   out_id = lane < k ? id : 0x7fffffff;
-  out_w = lane < k ? wt : 0.f;
+  out_w = lane < k ? w : 0.f;
 }
 
 template <int MAXV>
@@ -506,21 +529,6 @@ __device__ __forceinline__ void dot_subs(const RowFetch<QT, SPL>& f, int lir, in
 constexpr int GM_LSUB = 112;
 
 __host__ __device__ inline int gm_limb_row_bytes(int K) { return (K / GM_SUB) * GM_LSUB; }
-
-// Max over lanes 8j .. 8j+7: the two quad swaps, then the half-row mirror.
-__device__ __forceinline__ float gm_max8(float m) {
-  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_1032));
-  m = fmaxf(m, GM_DPP_F(m, GM_QPERM_2301));
-  return fmaxf(m, GM_DPP_F(m, 0x141));                       // row_half_mirror
-}
-
-// Sum over lanes 8j .. 8j+7 (the same value in all of them: each step adds a
-// lane's partner, so all 8 lanes add the same terms, in the same order per pair).
-__device__ __forceinline__ float gm_sum8(float v) {
-  v += GM_DPP_F(v, GM_QPERM_1032);
-  v += GM_DPP_F(v, GM_QPERM_2301);
-  return v + GM_DPP_F(v, 0x141);                             // row_half_mirror
-}
 
 // Low bytes of four int32 -> one dword.
 __device__ __forceinline__ uint32_t gm_pack_lo4(int a, int b, int c, int d) {

@@ -137,7 +137,8 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
 template <int NT, bool RF32>
 __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const float* __restrict__ x, int T,
                                                        float* __restrict__ part, float* __restrict__ ssq, int ldp,
-                                                       int kr, uint8_t* __restrict__ xl) {
+                                                       int kr, uint8_t* __restrict__ xl GM_TL_PARAM) {
+  GM_TL_BEGIN();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int D = P.D, E = P.E, nrows = E + (P.sh_gate_inp != nullptr ? 1 : 0);
   const int z = blockIdx.y, k0 = z * kr + 8 * lane;
@@ -190,6 +191,7 @@ __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const flo
       }
     }
   }
+  GM_TL_END(4);
 }
 
 template <bool RF32>
@@ -198,7 +200,7 @@ int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArg
   if (!fast1) {                                                      // router partials only
     const int kr = gm_dec_kr(P->D);
     hipLaunchKernelGGL((k_dec_router_ks<8, RF32>), dim3((nrows + 3) / 4, P->D / kr), dim3(256), 0, s, *P, x, T,
-                       a.part, a.ssq, gm_dec_part_ld(P), kr, a.xl);
+                       a.part, a.ssq, gm_dec_part_ld(P), kr, a.xl GM_TL_ARG(a.tl));
     GM_TRY(hipGetLastError());
     return GM_OK;
   }

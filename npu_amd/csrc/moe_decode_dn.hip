@@ -291,7 +291,8 @@ constexpr int dn_tiles(int fc) { return 1; }
 template <int QTD, int QTS, int FC>
 __global__ void __launch_bounds__(256) k_dec_down8(gm_moe_layer P, int T, const int32_t* __restrict__ g_grp,
                                                    const float* __restrict__ h, float* __restrict__ yp,
-                                                   int n_sh, int n_tg) {
+                                                   int n_sh, int n_tg GM_TL_PARAM) {
+  GM_TL_BEGIN();
   extern __shared__ __attribute__((aligned(16))) uint8_t hs[];   // 8 limb rows of FF (+ a spare sub-block)
   Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(hs + 8 * gm_limb_row_bytes(P.FF) + GM_LSUB);
   const int D = P.D, FF = P.FF, k = P.k, Ptot = T * k;
@@ -320,6 +321,7 @@ __global__ void __launch_bounds__(256) k_dec_down8(gm_moe_layer P, int T, const 
     down_rows<QTD, FC, NT>(static_cast<const uint8_t*>(P.down_exps) + (int64_t)e * D * gm_row_bytes(QTD, FF), D, FF,
                            row0, nm, src, dst, h, hs, gw, tab, yp);
   }
+  GM_TL_END(7);
 }
 
 // y[t] = sum over t's top-k slots in ascending expert id of w * yp[t*k + j]
@@ -330,7 +332,9 @@ __global__ void __launch_bounds__(256) k_dec_down8(gm_moe_layer P, int T, const 
 __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ x, int T, int k, int D, int flags,
                                                      const int32_t* __restrict__ g_ids,
                                                      const float* __restrict__ g_wts, const float* __restrict__ shg,
-                                                     int has_sh, const float* __restrict__ yp, float* __restrict__ y) {
+                                                     int has_sh, const float* __restrict__ yp,
+                                                     float* __restrict__ y GM_TL_PARAM) {
+  GM_TL_BEGIN();
   const int t = blockIdx.y;
   const int d = blockIdx.x * 256 + threadIdx.x;
   const int dc = d < D ? d : D - 1;
@@ -365,6 +369,7 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ x
   if (has_sh) acc = fmaf(gs, vs, acc);
   if (flags & GM_MOE_RESIDUAL) acc = xr + acc;
   y[(int64_t)t * D + d] = acc;
+  GM_TL_END(3);
 }
 
 template <int QTD, int QTS, int FC>
@@ -390,10 +395,10 @@ int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags,
                       (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
   if (int rc = gm_set_smem(k_dec_down8<QTD, QTS, FC>, smem)) return rc;
   hipLaunchKernelGGL((k_dec_down8<QTD, QTS, FC>), dim3(n_sh + max_u * n_tg), dim3(256), smem, s, *P, T, a.grp, a.h,
-                     a.yp, n_sh, n_tg);
+                     a.yp, n_sh, n_tg GM_TL_ARG(a.tl));
   GM_TRY(hipGetLastError());
   hipLaunchKernelGGL(k_dec_combine, dim3((D + 255) / 256, T), dim3(256), 0, s, x, T, k, D, flags, a.ids, a.wts,
-                     a.shg, P->down_sh ? 1 : 0, a.yp, y);
+                     a.shg, P->down_sh ? 1 : 0, a.yp, y GM_TL_ARG(a.tl));
   GM_TRY(hipGetLastError());
   return GM_OK;
 }

@@ -104,12 +104,15 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
       // publish for stage 3 and the caller while this block's rows are in flight
       int rid;
       uint32_t rkey;
-      topk_gather_rank<MAXV>(sel, uk, k, rid, rkey);
-      const int slot = topk_slot(rid, rkey, k);
-      const float w = topk_rank_weight<MAXV>(uk, rkey, k);
+      topk_compact<MAXV>(sel, uk, k, rkey, rid);               // lane r: pick of rank r (ascending id)
+      const float w = topk_weight<MAXV>(uk, rkey, k);
+      uint32_t sk = rkey;
+      int sid = rid;
+      float sw = w;
+      topk_sort8(sk, sid, sw);                                  // lane s: pick s in descending order
       if (lane < k) {
-        g_ids[slot] = rid;
-        g_wts[slot] = w;
+        g_ids[lane] = sid;
+        g_wts[lane] = sw;
         g_grp[1 + lane] = rid;
         g_grp[1 + GM_GRP_MAXU + lane] = 1;
         g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * lane] = lane;
@@ -146,7 +149,8 @@ __global__ void __launch_bounds__(512) k_dec_route(gm_moe_layer P, const float* 
                                                    float* __restrict__ rmsv, float* __restrict__ logits,
                                                    float* __restrict__ shg,
                                                    int32_t* __restrict__ g_ids, float* __restrict__ g_wts,
-                                                   int32_t* __restrict__ g_grp) {
+                                                   int32_t* __restrict__ g_grp GM_TL_PARAM) {
+  GM_TL_BEGIN();
   __shared__ int32_t ids[64];
   __shared__ float wts[64];
   __shared__ int32_t grp[GM_GRP_WORDS];
@@ -189,6 +193,7 @@ __global__ void __launch_bounds__(512) k_dec_route(gm_moe_layer P, const float* 
       v[i] = rms * a + (P.router_bias ? P.router_bias[r] : 0.f);
       if (ix[i] < E) logits[(int64_t)wave * E + ix[i]] = v[i];
     }
+    GM_TL_MARK3(v[0]);
     if (lane == 0) {                                            // no gate row: the shared expert is ungated
       float a = 0.f;
 #pragma unroll
@@ -201,9 +206,11 @@ __global__ void __launch_bounds__(512) k_dec_route(gm_moe_layer P, const float* 
     if (lane < k) { ids[wave * k + lane] = id; wts[wave * k + lane] = w; }
   }
   __syncthreads();
+  GM_TL_MARK1(ids[0]);
   block_group(ids, T * k, E, grp, bits);
   for (int i = threadIdx.x; i < T * k; i += blockDim.x) { g_ids[i] = ids[i]; g_wts[i] = wts[i]; }
   for (int i = threadIdx.x; i < GM_GRP_WORDS; i += blockDim.x) g_grp[i] = grp[i];
+  GM_TL_END(5);
 }
 
 // Rows r0 .. r0 + 8 NP - 1 of one gate/up pair for nm member tokens (limb
@@ -295,7 +302,8 @@ template <int QT, int DC>
 __global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const uint8_t* __restrict__ xl,
                                                      const float* __restrict__ rmsv, int T,
                                                      const int32_t* __restrict__ g_grp, float* __restrict__ h,
-                                                     int n_sh, int n_rg) {
+                                                     int n_sh, int n_rg GM_TL_PARAM) {
+  GM_TL_BEGIN();
   constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* xs = smem;                                          // 2 limb rows (+ a spare sub-block)
@@ -330,6 +338,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const uint8
     }
   }
   gateup_rows<QT, DC, kGuPasses>(gbase, ubase, FF, D, chunk * 8 * kGuPasses, nm, tok, dst, xl, rmsv, xs, gw, tab, h);
+  GM_TL_END(6);
 }
 
 template <int QT, int QTS, int DC>
@@ -351,7 +360,7 @@ int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const Gm
   auto route = nz <= 8 ? (P->E <= 256 ? k_dec_route<4, 8> : k_dec_route<8, 8>)
                        : (P->E <= 256 ? k_dec_route<4, 16> : k_dec_route<8, 16>);
   hipLaunchKernelGGL(route, dim3(1), dim3(512), 0, s, *P, a.part, a.ssq, nz, gm_dec_part_ld(P), T, a.rms, a.logits,
-                     a.shg, a.ids, a.wts, a.grp);
+                     a.shg, a.ids, a.wts, a.grp GM_TL_ARG(a.tl));
   GM_TRY(hipGetLastError());
   const int n_rg = (P->FF + 8 * kGuPasses - 1) / (8 * kGuPasses);  // blocks per unit
   const int n_sh = P->gate_sh ? n_rg : 0;
@@ -362,14 +371,14 @@ int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const Gm
     const int nsh = sh_own ? 0 : n_sh;
     if (int rc = gm_set_smem(k_dec_gateup8<QT, DC>, smem)) return rc;
     hipLaunchKernelGGL((k_dec_gateup8<QT, DC>), dim3(nsh + max_u * n_rg), dim3(256), smem, s, *P, a.xl, a.rms, T,
-                       a.grp, a.h, nsh, n_rg);
+                       a.grp, a.h, nsh, n_rg GM_TL_ARG(a.tl));
     GM_TRY(hipGetLastError());
   }
   if (sh_own) {
     const size_t smem = 2 * (size_t)gm_limb_row_bytes(P->D) + GM_LSUB + (QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
     if (int rc = gm_set_smem(k_dec_gateup8<QTS, DC>, smem)) return rc;
     hipLaunchKernelGGL((k_dec_gateup8<QTS, DC>), dim3(n_sh), dim3(256), smem, s, *P, a.xl, a.rms, T, a.grp, a.h,
-                       n_sh, n_rg);
+                       n_sh, n_rg GM_TL_ARG(a.tl));
   }
   GM_TRY(hipGetLastError());
   return GM_OK;

@@ -10,14 +10,15 @@
 //   [5] s_memtime (shader clock) at entry  [6] s_memtime at the end
 //   [7] mark 3 (an optional earlier mark, 0 if unused)
 // Each workspace holds GM_TL_KERNELS x GM_TL_MAXB records, so every layer of
-// a chain keeps its own stamps.  In the normal build the macros expand to
+// a chain keeps its own stamps.  Slots: T = 1 router 0, gate/up 1, down 2;
+// T > 1 router partials 4, routing 5, gate/up 6, down 7, combine 3.  In the normal build the macros expand to
 // nothing and the kernels are unchanged.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#define GM_TL_KERNELS 4
-#define GM_TL_MAXB 1024
+#define GM_TL_KERNELS 8
+#define GM_TL_MAXB 2560
 #define GM_TL_REC 8   // u64 per record
 
 #if defined(GM_TIMELINE) && GM_TIMELINE

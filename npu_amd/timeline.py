@@ -22,7 +22,7 @@ import sys
 os.environ.setdefault("NPU_AMD_LIB", "timeline")
 
 TICK_US = 0.01            # s_memrealtime runs at 100 MHz
-N_SLOTS, MAXB, REC = 4, 1024, 8
+N_SLOTS, MAXB, REC = 8, 2560, 8
 SEED = 20261201
 
 
@@ -81,7 +81,8 @@ def summarise(recs, names):
     stats = {}
     gaps_in, gaps_between = {}, []
     for li, layer in enumerate(inner):
-        slots = [s for s in range(N_SLOTS) if layer[s]]
+        # kernels in the order they ran (slot numbers do not follow the launch order)
+        slots = sorted((s for s in range(N_SLOTS) if layer[s]), key=lambda s: min(r[0] for r in layer[s]))
         t0 = min(r[0] for r in layer[slots[0]])
         for s in slots:
             rs = layer[s]
@@ -104,7 +105,7 @@ def summarise(recs, names):
             gaps_in.setdefault((a, b), []).append(min(r[0] for r in layer[b]) - max(r[3] for r in layer[a]))
         nxt = recs[li + 2] if len(recs) > 2 else None
         if nxt is not None:
-            ns = [s for s in range(N_SLOTS) if nxt[s]]
+            ns = sorted((s for s in range(N_SLOTS) if nxt[s]), key=lambda s: min(r[0] for r in nxt[s]))
             gaps_between.append(min(r[0] for r in nxt[ns[0]]) - max(r[3] for r in layer[slots[-1]]))
     med = lambda v: statistics.median(v) * TICK_US
     lines = ["| kernel | blocks | XCDs | entry first / median / last | mark 3 median / last | mark 1 median / last | "
@@ -124,9 +125,8 @@ def summarise(recs, names):
         lines.append(f"- gap {names.get(a, a)} last end -> {names.get(b, b)} first entry: {med(v):.2f} us (median)")
     if gaps_between:
         lines.append(f"- gap last kernel of block l -> first kernel of block l+1: {med(gaps_between):.2f} us (median)")
-    per_block = [min(r[0] for r in nxt[[s for s in range(N_SLOTS) if nxt[s]][0]]) -
-                 min(r[0] for r in cur[[s for s in range(N_SLOTS) if cur[s]][0]])
-                 for cur, nxt in zip(recs[1:-1], recs[2:])]
+    first = lambda layer: min(r[0] for s in range(N_SLOTS) for r in layer[s])
+    per_block = [first(nxt) - first(cur) for cur, nxt in zip(recs[1:-1], recs[2:])]
     if per_block:
         lines.append(f"- block period (first entry to next block's first entry): {med(per_block):.2f} us (median)")
     return "\n".join(lines)
@@ -147,7 +147,8 @@ def main() -> int:
         np.savez_compressed(args.npz, records=np.array(rows, dtype=np.int64),
                             columns=np.array(["layer", "kernel", "entry", "mark1", "mark2", "end", "hwid",
                                               "clock0", "clock1", "mark3"]))
-    names = {0: "router (stage 1)", 1: "gate/up (stage 2)", 2: "down (stage 3)", 3: "extra"}
+    names = {0: "router (stage 1)", 1: "gate/up (stage 2)", 2: "down (stage 3)", 3: "combine (T > 1)",
+             4: "router partials (T > 1)", 5: "routing (T > 1)", 6: "gate/up (T > 1)", 7: "down (T > 1)"}
     text = summarise(recs, names)
     print(text)
     if args.out:
