@@ -131,9 +131,12 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
 // factor (qwen/forward.py:58-61) to the summed partials.  Block = 4 rows (one
 // per wave) x one range of kr = gm_dec_kr(D) values (512, or 256 when 512 does
 // not divide D); lane l takes k = 8l .. 8l+7.
-// Wave 0 of the first row block of each range also writes the limb rows of
-// x w_norm for the range (the RMSNorm factor is applied to the dot products
-// instead), so the grouped gate/up kernel only copies them.
+// Wave 0 of row block b of each range also writes, for the tokens t with
+// t % gridDim.x == b (one token per block when there are at least T row
+// blocks), the limb row of x w_norm over the range (the RMSNorm factor is
+// applied to the dot products instead), so that the grouped gate/up kernel
+// only copies them, and the range's sum of x^2.  With all T tokens on one
+// block that block ended 3 us after the others.
 template <int NT, bool RF32>
 __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const float* __restrict__ x, int T,
                                                        float* __restrict__ part, float* __restrict__ ssq, int ldp,
@@ -162,11 +165,12 @@ __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const flo
   }
   float w[8];
   router_unpack8<RF32>(wb, w);
-  if (blockIdx.x == 0 && wave == 0) {                           // uniform per wave
+  const int nb = gridDim.x, b0 = blockIdx.x;
+  if (wave == 0) {                                              // uniform per wave
     const int rbytes = gm_limb_row_bytes(D);
 #pragma unroll
     for (int m = 0; m < NT; ++m) {
-      if (m < T) {
+      if (m < T && m % nb == b0) {
         gm_f32x4 a = xa[m], b = xb[m];
         a.x *= nw0.x; a.y *= nw0.y; a.z *= nw0.z; a.w *= nw0.w;
         b.x *= nw1.x; b.y *= nw1.y; b.z *= nw1.z; b.w *= nw1.w;
@@ -185,7 +189,7 @@ __global__ void __launch_bounds__(256) k_dec_router_ks(gm_moe_layer P, const flo
       for (int i = 0; i < 8; ++i) { d = fmaf(xv[i] * nv[i], w[i], d); q = fmaf(xv[i], xv[i], q); }
       d = gm_wave_sum64(lv ? d : 0.f);
       if (lane == 0 && row < nrows) part[((int64_t)z * T + m) * ldp + row] = d;
-      if (blockIdx.x == 0 && wave == 0) {
+      if (m % nb == b0 && wave == 0) {
         q = gm_wave_sum64(lv ? q : 0.f);
         if (lane == 0) ssq[z * T + m] = q;
       }

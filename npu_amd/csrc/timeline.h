@@ -47,10 +47,11 @@ __device__ __forceinline__ void gm_tl_flush(uint64_t* __restrict__ buf, int slot
                                             uint64_t t2, uint64_t c0, uint64_t t3m) {
   const uint64_t t3 = gm_tl_now();
   const uint64_t c1 = gm_tl_clock();
-  if (threadIdx.x == 0 && blockIdx.x < GM_TL_MAXB) {
+  const uint32_t blk = blockIdx.x + blockIdx.y * gridDim.x;           // linear block id (2-D grids)
+  if (threadIdx.x == 0 && blk < GM_TL_MAXB) {
     const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);     // HW_ID
     const uint32_t xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);   // XCC_ID
-    uint64_t* r = buf + ((int64_t)slot * GM_TL_MAXB + blockIdx.x) * GM_TL_REC;
+    uint64_t* r = buf + ((int64_t)slot * GM_TL_MAXB + blk) * GM_TL_REC;
     r[0] = t0;
     r[1] = t1;
     r[2] = t2;
