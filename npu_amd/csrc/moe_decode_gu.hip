@@ -139,6 +139,120 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
   GM_TL_END(1);
 }
 
+// T = 1, one block per CU: block b runs rows 16c .. 16c + 15 (c = b % n_chunks)
+// of the pick of rank u = b / n_chunks on waves 0-7 (two rows per wave, 32
+// lanes per row) and, on wave 8, shared rows 2b and 2b + 1, whose loads are in
+// flight from the block's start while wave 0 runs the top-k.  With k n_chunks
+// = 256 blocks every block starts at once: in the 8-row layout above, 576
+// blocks made 2-3 per CU, and the last ones dispatched ended up to 1.5 us after
+// the median.  The selection, hand-off and publishing are those of
+// k_dec_gateup1.
+template <int QT, int QTS, int DC, int MAXV>
+__global__ void __launch_bounds__(576) k_dec_gateup1w(gm_moe_layer P, const float* __restrict__ logits,
+                                                      int32_t* __restrict__ g_ids, float* __restrict__ g_wts,
+                                                      int32_t* __restrict__ g_grp, float* __restrict__ h,
+                                                      float* __restrict__ hsh, int n_chunks,
+                                                      const uint8_t* __restrict__ xl GM_TL_PARAM) {
+  GM_TL_BEGIN();
+  constexpr int NTH = 576;
+  constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS;
+  constexpr int CPT = (32 * DC * GM_LSUB / 16 + NTH - 1) / NTH;   // 16-byte limb chunks per thread
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int32_t s_e;
+  const int D = P.D, E = P.E, k = P.k, FF = P.FF, nsub = D / GM_SUB, rbytes = gm_limb_row_bytes(D);
+  uint8_t* xs = smem;                                           // limb row of xn (+ a spare chunk)
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(smem + rbytes + GM_LSUB);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane & 31;
+  const int b = blockIdx.x, u = b / n_chunks, chunk = b - u * n_chunks;
+  const bool shw = wave == 8;                                   // uniform per wave
+  const int rch = rbytes >> 4;
+  gm_u32x4 cp[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + NTH * i;
+    cp[i] = reinterpret_cast<const gm_u32x4*>(xl)[c < rch ? c : rch - 1];
+  }
+  uint32_t gw = 0;
+  if constexpr (IQ3) gw = gm_iq3_tab_load();
+  const int srow = 2 * b + (lane >> 5);                         // wave 8: shared row
+  const bool slive = P.gate_sh != nullptr && srow < P.FF_sh;
+  const int row = shw ? srow : chunk * 16 + wave * 2 + (lane >> 5);
+  const bool live = shw ? slive : row < FF;
+  const int r = live ? row : 0;
+  RowFetch<QT, DC> fg, fu;
+  RowFetch<QTS, DC> sg, su;
+  uint32_t uk[MAXV];
+  uint64_t sel[MAXV];
+  if (shw) {
+    if (P.gate_sh != nullptr) {
+      const int64_t rbs = gm_row_bytes(QTS, D);
+      fetch_subs<QTS, 32, DC, true>(sg, static_cast<const uint8_t*>(P.gate_sh) + r * rbs, lir, nsub);
+      fetch_subs<QTS, 32, DC, true>(su, static_cast<const uint8_t*>(P.up_sh) + r * rbs, lir, nsub);
+    }
+  } else if (wave == 0) {
+    __builtin_amdgcn_s_setprio(3);
+    float v[MAXV];
+    int ix[MAXV];
+    topk_load<MAXV>(logits, E, v, ix);
+    GM_TL_MARK3(v[0]);
+    topk_keys<MAXV>(v, ix, E, uk);
+    topk_masks<MAXV>(uk, k, sel);
+    if (lane == 0) s_e = topk_rank_id<MAXV>(sel, u);
+    __builtin_amdgcn_s_setprio(0);
+  }
+  issue_fence();
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + NTH * i;
+    reinterpret_cast<gm_u32x4*>(xs)[c < rch ? c : rch] = cp[i];   // past the row: the spare chunk
+  }
+  if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
+  __syncthreads();
+  const int tok[1] = {0};
+  float ag[1] = {0.f}, au[1] = {0.f};
+  if (!shw) {
+    const int e = s_e;
+    GM_TL_MARK1(e);
+    const int64_t rb = gm_row_bytes(QT, D);
+    fetch_subs<QT, 32, DC, true>(fg, static_cast<const uint8_t*>(P.gate_exps) + ((int64_t)e * FF + r) * rb, lir,
+                                 nsub);
+    fetch_subs<QT, 32, DC, true>(fu, static_cast<const uint8_t*>(P.up_exps) + ((int64_t)e * FF + r) * rb, lir,
+                                 nsub);
+    if (b == 0 && wave == 0) {
+      // publish for stage 3 and the caller while this block's rows are in flight
+      int rid;
+      uint32_t rkey;
+      topk_compact<MAXV>(sel, uk, k, rkey, rid);               // lane r: pick of rank r (ascending id)
+      const float w = topk_weight<MAXV>(uk, rkey, k);
+      uint32_t sk = rkey;
+      int sid = rid;
+      float sw = w;
+      topk_sort8(sk, sid, sw);                                  // lane s: pick s in descending order
+      if (lane < k) {
+        g_ids[lane] = sid;
+        g_wts[lane] = sw;
+        g_grp[1 + lane] = rid;
+        g_grp[1 + GM_GRP_MAXU + lane] = 1;
+        g_grp[1 + 2 * GM_GRP_MAXU + GM_GRP_MAXM * lane] = lane;
+        g_grp[GM_GRP_WORDS + lane] = __float_as_int(w);
+      }
+      if (lane == 0) g_grp[0] = k;
+    }
+    dot_subs_i8<QT, 32, DC, 1>(fg, lir, nsub, xs, rbytes, tok, 1, tab, ag);
+    dot_subs_i8<QT, 32, DC, 1>(fu, lir, nsub, xs, rbytes, tok, 1, tab, au);
+  } else if (P.gate_sh != nullptr) {
+    dot_subs_i8<QTS, 32, DC, 1>(sg, lir, nsub, xs, rbytes, tok, 1, tab, ag);
+    dot_subs_i8<QTS, 32, DC, 1>(su, lir, nsub, xs, rbytes, tok, 1, tab, au);
+  }
+  GM_TL_MARK2(au[0]);
+  const float hv = gm_silu(row_sum<32>(ag[0])) * row_sum<32>(au[0]);
+  if (live && lir == 0) {
+    if (shw) hsh[row] = hv;
+    else h[(int64_t)u * FF + row] = hv;
+  }
+  GM_TL_END(1);
+}
+
 // One block: the router logits of every token from the partial sums of
 // k_dec_router_ks (fixed order), times the token's RMSNorm factor
 // 1 / sqrt(mean(x^2) + eps) (qwen/forward.py:58-61), + bias; the shared gate
@@ -344,6 +458,18 @@ __global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const uint8
 template <int QT, int QTS, int DC>
 int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s) {
   if (fast1) {
+    // one block per CU: 16 routed rows per block, two shared rows on a ninth wave
+    const int n16 = P->FF / 16, nblk = P->k * n16;
+    if (P->FF % 16 == 0 && nblk >= 192 && nblk <= 1024 && (!P->gate_sh || P->FF_sh <= 2 * nblk)) {
+      const size_t smem = (size_t)gm_limb_row_bytes(P->D) + GM_LSUB +
+                          (QT == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
+      auto kern = P->E <= 256 ? k_dec_gateup1w<QT, QTS, DC, 4> : k_dec_gateup1w<QT, QTS, DC, 8>;
+      if (int rc = gm_set_smem(kern, smem)) return rc;
+      hipLaunchKernelGGL(kern, dim3(nblk), dim3(576), smem, s, *P, a.logits, a.ids, a.wts, a.grp, a.h, a.hsh, n16,
+                         a.xl GM_TL_ARG(a.tl));
+      GM_TRY(hipGetLastError());
+      return GM_OK;
+    }
     const int n_chunks = (P->FF + 7) / 8;
     const int n_sh = P->gate_sh ? (P->FF_sh + 7) / 8 : 0;
     const size_t smem = (size_t)gm_limb_row_bytes(P->D) + GM_LSUB +
