@@ -8,7 +8,7 @@
 //   3. k_pf_topk sums the router partials, then dispatch (dispatch.hip):
 //      histogram -> exclusive scan -> stable scatter of (token, slot) pairs by
 //      expert, the inverse permutation, and every expert's token list (and the
-//      shared expert's, which takes all T tokens) cut into segments of <= 64
+//      shared expert's, which takes all T tokens) cut into segments of <= kSegTok
 //   4. k_pf_gateup:   per (segment, 64 weight rows): h = silu(G x) * (U x).  The raw
 //                     superblocks are fetched one superblock ahead into registers
 //                     and decoded to f16 integers (kvalue or grid magnitude times
@@ -43,7 +43,11 @@ typedef float gm_f32x8 __attribute__((ext_vector_type(8)));
 
 namespace {
 
-constexpr int kSegTok = 64;         // tokens per segment
+// Tokens per segment.  32 (two MFMA column tiles) leaves the GEMM kernels at
+// 168 VGPRs, three waves per SIMD: config 4 227 -> 219 us per block against 64
+// tokens (four tiles, 2 waves per SIMD), although the 512-token shared unit
+// then decodes its weights for 16 segments instead of 8.
+constexpr int kSegTok = 32;
 constexpr int kNT = kSegTok / 16;   // MFMA column tiles per segment
 constexpr int kChunk = 256;         // K elements per pipeline step (one superblock column)
 constexpr int kPitchB = 2 * kChunk + 16;   // bytes per LDS activation row (16 B of padding)
@@ -755,7 +759,7 @@ __device__ __forceinline__ void act_store(const ActRegs<N>& a, uint8_t* __restri
 // Block = (segment, 64 rows of FF); wave w -> rows 16w .. 16w+15 of both the
 // gate and the up matrix, all of the segment's token tiles.
 template <int QT>
-__global__ void __launch_bounds__(256, kSegTok == 64 ? 2 : 4) k_pf_gateup(gm_moe_layer P, const int32_t* __restrict__ segs,
+__global__ void __launch_bounds__(256, kSegTok == 64 ? 2 : 3) k_pf_gateup(gm_moe_layer P, const int32_t* __restrict__ segs,
                                                       const int32_t* __restrict__ offsets,
                                                       const int32_t* __restrict__ sorted,
                                                       const uint16_t* __restrict__ xh,
@@ -860,7 +864,7 @@ __global__ void __launch_bounds__(256, kSegTok == 64 ? 2 : 4) k_pf_gateup(gm_moe
 // walks its row groups with the next group's raw superblocks in flight.
 // Wave w -> row tiles 2w, 2w+1 (16 rows each) of a group.
 template <int QT, int NSB>
-__global__ void __launch_bounds__(256, (NSB == 4 ? 1 : 2) * (64 / kSegTok)) k_pf_down(gm_moe_layer P, const int32_t* __restrict__ segs,
+__global__ void __launch_bounds__(256, NSB == 4 ? 1 : (kSegTok == 64 || QT == GM_QTYPE_IQ4_XS ? 2 : 3)) k_pf_down(gm_moe_layer P, const int32_t* __restrict__ segs,
                                                     const int32_t* __restrict__ offsets,
                                                     const uint16_t* __restrict__ hh, const float* __restrict__ hsc,
                                                     float* __restrict__ yp, int T, int n_blk, int rg_per_blk) {
