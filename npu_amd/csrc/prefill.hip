@@ -717,7 +717,7 @@ __global__ void __launch_bounds__(256) k_pf_h16(const uint16_t* __restrict__ hb,
   if (lane == 0) hsc[r] = m <= 3.4e38f ? __builtin_ldexpf(1.0f, e) : __builtin_nanf("");
 }
 
-// Activation chunk [c0, c0 + 256) of the segment's rows <-> registers: 64 rows
+// Activation chunk [c0, c0 + 256) of the segment's rows <-> registers: kSegTok rows
 // x 32 granules of 16 B, granule g = threadIdx + 256 i for i in [I0, I0 + N)
 // (rows past n repeat a valid row; their output columns are never stored).
 template <int N>
@@ -860,7 +860,7 @@ __global__ void __launch_bounds__(256, kSegTok == 64 ? 2 : 3) k_pf_gateup(gm_moe
 
 // ------------------------------------------------------------------ down
 // Block = (segment, rg_per_blk groups of 128 rows of D).  The segment's whole
-// h tile (64 rows x FF, FF = 256 NSB) is staged in LDS once; the block then
+// h tile (kSegTok rows x FF, FF = 256 NSB) is staged in LDS once; the block then
 // walks its row groups with the next group's raw superblocks in flight.
 // Wave w -> row tiles 2w, 2w+1 (16 rows each) of a group.
 template <int QT, int NSB>
