@@ -139,19 +139,19 @@ def time_stages(layers, T: int, reps: int = 20):
 
 
 def roofline(layers, stages):
-    """The dominant kernel, k_dec_gateup1 (top-k, routed and shared gate/up, SwiGLU, T = 1):
+    """The dominant kernel, k_dec_gateup1w (top-k, routed and shared gate/up, SwiGLU, T = 1):
     its algorithmic bytes per launch (npu_amd.rocprof_summary.algorithmic_bytes: the k
     routed and the shared experts' raw gate and up rows, the limb row of the normalised x,
     the router logits, the k + 1 SwiGLU rows it writes) over the launch period measured by
     time_stages."""
     from npu_amd.rocprof_summary import algorithmic_bytes
     b = layers[0]
-    n = algorithmic_bytes(D, FF, E, K_TOP)["k_dec_gateup1"]
+    n = algorithmic_bytes(D, FF, E, K_TOP)["k_dec_gateup1w"]
     assert b.gate[0].numel() == FF * (D // 256 * 136) and b.down[0].numel() == D * (FF // 256 * 98)
     gbps = n / (stages["gateup_us"] * 1e-6) / 1e9
-    return {"bound": "hbm", "kernel": "k_dec_gateup1 (top-k + routed and shared gate/up + SwiGLU, T=1)",
+    return {"bound": "hbm", "kernel": "k_dec_gateup1w (top-k + routed and shared gate/up + SwiGLU, T=1)",
             "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gbps / HBM_PEAK_GBPS,
-            "traffic": traffic_bytes("k_dec_gateup1"), "bytes_per_launch": n, "avg_launch_us": stages["gateup_us"]}
+            "traffic": traffic_bytes("k_dec_gateup1w"), "bytes_per_launch": n, "avg_launch_us": stages["gateup_us"]}
 
 
 def run_prefill(layers, T: int = 512, n_blocks: int = 8, reps: int = 5):

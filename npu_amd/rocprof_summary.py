@@ -45,14 +45,14 @@ def algorithmic_bytes(d: int = D, ff: int = FF, e: int = E, k: int = K) -> dict[
     normalised x is d / 32 sub-blocks of 112 bytes (three int8 planes and a scale).
       k_dec_router1: router [e, d] bf16, shared scalar gate [d] bf16, x and the RMSNorm
         weight fp32; writes logits [e], the shared gate and the limb row.
-      k_dec_gateup1: the k routed and the shared experts' gate and up rows, the limb row
+      k_dec_gateup1w: the k routed and the shared experts' gate and up rows, the limb row
         and the logits; writes k + 1 SwiGLU rows [ff] fp32 and the ids and weights.
       k_dec_down1: the k routed and the shared down rows, the k + 1 SwiGLU rows, the
         weights, the shared gate and x (residual); writes y [d]."""
     iq4_row, iq3_row, limb = d // 256 * 136, ff // 256 * 98, d // 32 * 112
     return {
         "k_dec_router1": e * d * 2 + d * 2 + d * 4 + d * 4 + e * 4 + 4 + limb,
-        "k_dec_gateup1": (k + 1) * 2 * ff * iq4_row + limb + e * 4 + (k + 1) * ff * 4 + 2 * k * 4,
+        "k_dec_gateup1w": (k + 1) * 2 * ff * iq4_row + limb + e * 4 + (k + 1) * ff * 4 + 2 * k * 4,
         "k_dec_down1": (k + 1) * d * iq3_row + (k + 1) * ff * 4 + k * 4 + 4 + d * 4 + d * 4,
     }
 

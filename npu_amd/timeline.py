@@ -87,14 +87,15 @@ def summarise(recs, names):
         for s in slots:
             rs = layer[s]
             e = sorted(r[0] for r in rs)
-            m1 = sorted(r[1] for r in rs)
-            m2 = sorted(r[2] for r in rs)
+            m1 = sorted(r[1] for r in rs if r[1] != 0)               # marks a kernel does not set stay 0
+            m2 = sorted(r[2] for r in rs if r[2] != 0)
             en = sorted(r[3] for r in rs)
             m3 = sorted(r[7] for r in rs if r[7] != 0)
             d = {"blocks": len(rs), "entry_first": e[0] - t0, "entry_median": e[len(e) // 2] - t0,
-                 "mark3_median": (m3[len(m3) // 2] - t0) if m3 else 0, "mark3_last": (m3[-1] - t0) if m3 else 0,
-                 "entry_last": e[-1] - t0, "mark1_median": m1[len(m1) // 2] - t0, "mark1_last": m1[-1] - t0,
-                 "mark2_median": m2[len(m2) // 2] - t0, "mark2_last": m2[-1] - t0,
+                 "mark3_median": (m3[len(m3) // 2] - t0) if m3 else None, "mark3_last": (m3[-1] - t0) if m3 else None,
+                 "entry_last": e[-1] - t0,
+                 "mark1_median": (m1[len(m1) // 2] - t0) if m1 else None, "mark1_last": (m1[-1] - t0) if m1 else None,
+                 "mark2_median": (m2[len(m2) // 2] - t0) if m2 else None, "mark2_last": (m2[-1] - t0) if m2 else None,
                  "end_median": en[len(en) // 2] - t0, "end_last": en[-1] - t0,
                  "block_median": sorted(r[3] - r[0] for r in rs)[len(rs) // 2],
                  "mhz": sorted((r[6] - r[5]) * 100.0 / max(r[3] - r[0], 1) for r in rs)[len(rs) // 2],
@@ -108,6 +109,11 @@ def summarise(recs, names):
             ns = sorted((s for s in range(N_SLOTS) if nxt[s]), key=lambda s: min(r[0] for r in nxt[s]))
             gaps_between.append(min(r[0] for r in nxt[ns[0]]) - max(r[3] for r in layer[slots[-1]]))
     med = lambda v: statistics.median(v) * TICK_US
+
+    def pair(d, a, b):                                           # "median / last", "-" for an unset mark
+        va, vb = [x for x in d[a] if x is not None], [x for x in d[b] if x is not None]
+        return f"{med(va):.2f} / {med(vb):.2f}" if va and vb else "-"
+
     lines = ["| kernel | blocks | XCDs | entry first / median / last | mark 3 median / last | mark 1 median / last | "
              "mark 2 median / last | end median / last | block duration (median) | shader clock MHz (median) |",
              "|---|---|---|---|---|---|---|---|---|---|"]
@@ -115,9 +121,8 @@ def summarise(recs, names):
         lines.append(
             f"| {names.get(s, s)} | {int(statistics.median(d['blocks']))} | {int(statistics.median(d['xccs']))} | "
             f"{med(d['entry_first']):.2f} / {med(d['entry_median']):.2f} / {med(d['entry_last']):.2f} | "
-            f"{med(d['mark3_median']):.2f} / {med(d['mark3_last']):.2f} | "
-            f"{med(d['mark1_median']):.2f} / {med(d['mark1_last']):.2f} | "
-            f"{med(d['mark2_median']):.2f} / {med(d['mark2_last']):.2f} | "
+            f"{pair(d, 'mark3_median', 'mark3_last')} | {pair(d, 'mark1_median', 'mark1_last')} | "
+            f"{pair(d, 'mark2_median', 'mark2_last')} | "
             f"{med(d['end_median']):.2f} / {med(d['end_last']):.2f} | {med(d['block_median']):.2f} | "
             f"{statistics.median(d['mhz']):.0f} |")
     lines.append("")
