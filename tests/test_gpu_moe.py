@@ -151,6 +151,16 @@ def test_t1_shapes(gpu, D, FF, E, k, shared):
     _check(gpu, h, 1, residual=True, seed=k, rmsnorm_input=False)
 
 
+@pytest.mark.parametrize("D,FF,E,k,shared", [(2048, 512, 512, 8, True), (2048, 512, 256, 6, False),
+                                              (1024, 1024, 64, 8, True), (2048, 512, 100, 7, False)])
+def test_t1_one_block_per_cu(gpu, D, FF, E, k, shared):
+    """T = 1 gate/up in the one-block-per-CU layout (k FF / 16 >= 192 blocks, two shared rows
+    per block at most): E = 512 (eight keys per lane in the top-k), k < 8 without a shared
+    expert, FF = 1024 (64 blocks per pick), E not a multiple of 64."""
+    h = synth.host_moe_layer(50 + k + E, D=D, FF=FF, E=E, k=k, shared=shared, norm=True)
+    _check(gpu, h, 1, residual=True, seed=k + 3, rmsnorm_input=False)
+
+
 def test_t1_graph_replays(gpu):
     """The T = 1 decode captured in a hipGraph: every replay (with eager work on the same
     workspace and synchronisations in between) matches the eager result."""
