@@ -50,8 +50,8 @@ namespace {
 constexpr int kSegTok = 32;
 constexpr int kNT = kSegTok / 16;   // MFMA column tiles per segment
 constexpr int kChunk = 256;         // K elements per pipeline step (one superblock column)
-constexpr int kPitchB = 2 * kChunk + 16;   // bytes per LDS activation row (16 B of padding)
-constexpr int kTileB = kSegTok * kPitchB;  // one activation buffer
+constexpr int kRowB = 2 * kChunk;          // bytes per gate/up LDS activation row (f16, swizzled)
+constexpr int kTileG = kSegTok * kRowB;    // one gate/up activation buffer
 constexpr int kGran = kSegTok * (2 * kChunk / 16) / 256;  // 16-byte granules per thread of one chunk
 
 // f(integral_constant<int, n>) for the segment's tile count n = ntiles in
@@ -544,20 +544,21 @@ __device__ __forceinline__ void pf_stage_signs_u8(gm_u32x4* tab) {
   }
 }
 
-// f16 A operand of k-step j: 8 weights (scale folded in) at the lane's k-slots.
-//   IQ4_XS: slot i < 4 -> k = 32s + 4c + i (low nibbles of qs bytes 16s+4c ..+3),
-//           slot i >= 4 -> k = 32s + 16 + 4c + (i - 4) (high nibbles), c = j & 3
-//   IQ3_XXS: slot i -> k = 32s + 8g + i, g = j & 3
-// with s = 2q + (j >> 2).
+// f16 A operand of k-step j: 8 weights (scale folded in) at the lane's k-slots
+// k = 32s + 8c + i (i < 8), s = 2q + (j >> 2), c = j & 3, so that the matching
+// activations are 8 consecutive values:
+//   IQ4_XS: the low (c < 2) or high (c >= 2) nibbles of qs bytes 8 (c & 1) .. + 7
+//   IQ3_XXS: grid points 2c, 2c + 1 of the sub-block
 template <int QT>
 __device__ __forceinline__ gm_f16x8 a_f16(const PfRaw<QT>& r, int j, gm_f16x2 sc, gm_f16x2 cc,
                                           const uint32_t* __restrict__ grid,
                                           const gm_u32x4* __restrict__ sgn) {
   uint32_t o[4];
   if constexpr (QT == GM_QTYPE_IQ4_XS) {
-    const uint32_t nib = r.q[4 * (j >> 2) + (j & 3)];
-    u8x4_to_f16(lut_kvu(nib & 0x0f0f0f0fu), sc, cc, o[0], o[1]);
-    u8x4_to_f16(lut_kvu((nib >> 4) & 0x0f0f0f0fu), sc, cc, o[2], o[3]);
+    const int sl = j >> 2, c = j & 3, sh = 4 * (c >> 1);
+    const uint32_t w0 = r.q[4 * sl + 2 * (c & 1)], w1 = r.q[4 * sl + 2 * (c & 1) + 1];
+    u8x4_to_f16(lut_kvu((w0 >> sh) & 0x0f0f0f0fu), sc, cc, o[0], o[1]);
+    u8x4_to_f16(lut_kvu((w1 >> sh) & 0x0f0f0f0fu), sc, cc, o[2], o[3]);
   } else {
     const int sl = j >> 2, g = j & 3;
     const uint32_t qw = r.q[2 * sl + (g >> 1)] >> (16 * (g & 1));
@@ -574,10 +575,17 @@ __device__ __forceinline__ gm_f16x8 a_f16(const PfRaw<QT>& r, int j, gm_f16x2 sc
 }
 
 // B operand of k-step j from an LDS activation row: the 8 activations of the
-// lane's k-slots are contiguous (for IQ4_XS the chunk is stored permuted
-// within every 32-element sub-block, see act_store), so one 16-byte read.
+// lane's k-slots are contiguous, so one 16-byte read.
 __device__ __forceinline__ gm_u32x4 b_lds(const uint8_t* __restrict__ row, int q, int j) {
   return *reinterpret_cast<const gm_u32x4*>(row + 2 * (32 * (2 * q + (j >> 2)) + 8 * (j & 3)));
+}
+
+// The same from row r of a gate/up activation tile, whose granule g (8 values)
+// of row r sits at slot g ^ (r & 15): the 16 rows a wave reads at once then hit
+// 16 different 16-byte bank groups without padding the 512-byte rows.
+__device__ __forceinline__ gm_u32x4 b_lds_swz(const uint8_t* __restrict__ tile, int r, int q, int j) {
+  const int g = 4 * (2 * q + (j >> 2)) + (j & 3);
+  return *reinterpret_cast<const gm_u32x4*>(tile + r * kRowB + 16 * (g ^ (r & 15)));
 }
 
 // Half H (k-steps 4H .. 4H+3) of one superblock column of the gate and up
@@ -598,7 +606,7 @@ __device__ __forceinline__ void gu_half(const PfRaw<QT>& wg, const PfRaw<QT>& wu
     const gm_f16x8 U = a_f16<QT>(wu, j, suh, cuh, grid, sgn);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const gm_f16x8 B = __builtin_bit_cast(gm_f16x8, b_lds(xb + (t * 16 + l16) * kPitchB, q, j));
+      const gm_f16x8 B = __builtin_bit_cast(gm_f16x8, b_lds_swz(xb, t * 16 + l16, q, j));
       pg[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, pg[t], 0, 0, 0);
       pu[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(U, B, pu[t], 0, 0, 0);
     }
@@ -733,25 +741,28 @@ __device__ __forceinline__ void act_load(ActRegs<N>& a, const uint16_t* __restri
   }
 }
 
-// IQ4 (PERM): within each sub-block, element 4c + i (c < 4, i < 4) goes to
-// slot 8c + i and element 16 + 4c + i to slot 8c + 4 + i, so that the low- and
-// high-nibble halves of a k-step sit side by side.  Granule c (8 elements) of a
-// sub-block: elements 0-3 -> slot 16 (c & 1) + 4 (c >> 1), 4-7 -> that + 8.
-template <bool PERM, int N>
-__device__ __forceinline__ void act_store(const ActRegs<N>& a, uint8_t* __restrict__ buf, int pitch = kPitchB,
-                                          int i0 = 0) {
+template <int N>
+__device__ __forceinline__ void act_store(const ActRegs<N>& a, uint8_t* __restrict__ buf, int pitch, int i0 = 0) {
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const int g = threadIdx.x + 256 * (i0 + i), r = g >> 5, c = g & 31;
-    uint8_t* row = buf + r * pitch;
-    if constexpr (PERM) {
-      const int sub = c >> 2, gc = c & 3;
-      const int slot = 32 * sub + 16 * (gc & 1) + 4 * (gc >> 1);
-      *reinterpret_cast<uint2*>(row + 2 * slot) = make_uint2(a.v[i].x, a.v[i].y);
-      *reinterpret_cast<uint2*>(row + 2 * (slot + 8)) = make_uint2(a.v[i].z, a.v[i].w);
-    } else {
-      *reinterpret_cast<gm_u32x4*>(row + 16 * c) = a.v[i];
-    }
+    *reinterpret_cast<gm_u32x4*>(buf + r * pitch + 16 * c) = a.v[i];
+  }
+}
+
+// Chunk [c0, c0 + kChunk) of the segment's kSegTok f16 activation rows into the
+// swizzled tile with global -> LDS loads (no registers, no wait here): wave
+// instruction m of wave w writes 1 KB, rows 2 mi and 2 mi + 1 (mi = NI w + m);
+// lane i lands at slot i & 31 of row 2 mi + (i >> 5) and so loads granule
+// (i & 31) ^ (row & 15) of that row.
+__device__ __forceinline__ void act_lds_load(const uint16_t* __restrict__ src, int K,
+                                             const int32_t* __restrict__ rows, int c0, uint8_t* __restrict__ tile) {
+  constexpr int NI = kSegTok * (kRowB / 16) / 256;                     // 1 KB loads per wave
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < NI; ++m) {
+    const int mi = wave * NI + m, r = 2 * mi + (lane >> 5), c = (lane & 31) ^ (r & 15);
+    __builtin_amdgcn_global_load_lds(src + (int64_t)rows[r] * K + c0 + 8 * c, tile + mi * 1024, 16, 0, 0);
   }
 }
 
@@ -766,8 +777,8 @@ __global__ void __launch_bounds__(256, kSegTok == 64 ? 2 : 3) k_pf_gateup(gm_moe
                                                       const float* __restrict__ xsc, uint16_t* __restrict__ hb,
                                                       int T, int n_row_tiles) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* xl = smem;                                                   // [2][64][kPitchB]
-  uint32_t* grid = reinterpret_cast<uint32_t*>(smem + 2 * kTileB);      // [256] (IQ3)
+  uint8_t* xl = smem;                                                   // [2][kSegTok][kRowB]
+  uint32_t* grid = reinterpret_cast<uint32_t*>(smem + 2 * kTileG);      // [256] (IQ3)
   gm_u32x4* sgn = reinterpret_cast<gm_u32x4*>(grid + 256);              // [128] (IQ3)
   int32_t* tok_row = reinterpret_cast<int32_t*>(sgn + 128);             // [64]
   int32_t* out_row = tok_row + kSegTok;                                 // [kSegTok]
@@ -808,37 +819,28 @@ __global__ void __launch_bounds__(256, kSegTok == 64 ? 2 : 3) k_pf_gateup(gm_moe
   gm_f32x4 ag[kNT], au[kNT];
 #pragma unroll
   for (int t = 0; t < kNT; ++t) { ag[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; au[t] = ag[t]; }
-  constexpr bool PERM = QT == GM_QTYPE_IQ4_XS;
-  constexpr int GH = kGran / 2;                                         // granules per half chunk
-  {
-    ActRegs<kGran> x0;
-    act_load<kGran>(x0, xh, D, tok_row, 0);
-    act_store<PERM, kGran>(x0, xl);
-  }
+  act_lds_load(xh, D, tok_row, 0, xl);
   PfRaw<QT> wg = pf_load<QT>(grow, q), wu = pf_load<QT>(urow, q);
+  __builtin_amdgcn_s_waitcnt(0);                                        // the first chunk is in LDS
   __syncthreads();
   for (int sb = 0; sb < nsb; ++sb) {
-    // next superblock's raw rows, and its activation chunk in two halves (the
-    // other LDS buffer is free: its last reader finished before the barrier)
+    // next superblock's raw rows and, straight into the other LDS buffer, its
+    // activation chunk (that buffer's last reader finished before the barrier)
     const int sn = sb + 1 < nsb ? sb + 1 : sb;                   // the last step re-reads itself
     const PfRaw<QT> wgn = pf_load<QT>(grow + sn * SBB, q), wun = pf_load<QT>(urow + sn * SBB, q);
-    uint8_t* xnext = xl + ((sb + 1) & 1) * kTileB;
-    const uint8_t* xb = xl + (sb & 1) * kTileB;
-    ActRegs<GH> xa;
-    act_load<GH>(xa, xh, D, tok_row, sn * kChunk, 0);
+    const uint8_t* xb = xl + (sb & 1) * kTileG;
+    if (sb + 1 < nsb) act_lds_load(xh, D, tok_row, (sb + 1) * kChunk, xl + ((sb + 1) & 1) * kTileG);
     gm_f32x4 pg[kNT], pu[kNT];
 #pragma unroll
     for (int t = 0; t < kNT; ++t) { pg[t] = gm_f32x4{0.f, 0.f, 0.f, 0.f}; pu[t] = pg[t]; }
     nt_dispatch<kNT>(ntiles, [&](auto nt) { gu_half<QT, decltype(nt)::value, 0>(wg, wu, q, l16, xb, grid, sgn, pg, pu); });
-    act_store<PERM, GH>(xa, xnext, kPitchB, 0);
-    act_load<GH>(xa, xh, D, tok_row, sn * kChunk, GH);
     nt_dispatch<kNT>(ntiles, [&](auto nt) {
       gu_half<QT, decltype(nt)::value, 1>(wg, wu, q, l16, xb, grid, sgn, pg, pu);
       gu_fold<QT, decltype(nt)::value>(wg, wu, q, pg, pu, ag, au);
     });
-    act_store<PERM, GH>(xa, xnext, kPitchB, GH);
     wg = wgn;
     wu = wun;
+    __builtin_amdgcn_s_waitcnt(0);                                      // the next chunk is in LDS
     __syncthreads();
   }
   // C layout: lane l holds rows 4 (l / 16) + i of the 16-row tile, column l % 16
@@ -907,7 +909,7 @@ __global__ void __launch_bounds__(256, NSB == 4 ? 1 : (kSegTok == 64 || QT == GM
   for (int sb = 0; sb < NSB; ++sb) {
     ActRegs<kGran> ha;
     act_load<kGran>(ha, hh, FF, in_row, sb * kChunk);
-    act_store<QT == GM_QTYPE_IQ4_XS, kGran>(ha, hl + sb * 2 * kChunk, PITCH);
+    act_store<kGran>(ha, hl + sb * 2 * kChunk, PITCH);
   }
   __syncthreads();
   const int ntiles = (n + 15) >> 4;
@@ -1014,7 +1016,7 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ x,
   }
 }
 
-constexpr size_t kGemmSmem = 2 * (size_t)kTileB + 256 * 4 + 128 * 16 + 2 * kSegTok * 4;
+constexpr size_t kGemmSmem = 2 * (size_t)kTileG + 256 * 4 + 128 * 16 + 2 * kSegTok * 4;
 
 template <int QTG, int QTD>
 int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws, const GmMoeWs& lay,
