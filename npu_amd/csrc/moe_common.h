@@ -159,7 +159,7 @@ __device__ __forceinline__ void topk_keys(const float (&v)[MAXV], const int (&ix
 // logits).  If the k-th and (k+1)-th keys are equal it ends with the k-th key
 // itself, and the keys equal to it are taken in ascending id order.
 template <int MAXV>
-__device__ __forceinline__ void topk_masks(const uint32_t (&u)[MAXV], int k, uint64_t (&sel)[MAXV]) {
+__device__ __forceinline__ void topk_masks_bisect(const uint32_t (&u)[MAXV], int k, uint64_t (&sel)[MAXV]) {
   uint32_t ans = 0;
   int cnt = 0x7fffffff;                                  // keys >= ans (once ans > 0)
   for (uint32_t bit = 0x80000000u; bit != 0u; bit >>= 1) {
@@ -195,6 +195,120 @@ __device__ __forceinline__ void topk_masks(const uint32_t (&u)[MAXV], int k, uin
       --need;
     }
   }
+}
+
+// Candidate network (the fast path of topk_masks).  An entry is a pair (key,
+// id) held as two words, hi = key and lo = ~id: the order of the 64-bit value
+// hi:lo is the selection order (larger key first, then lower id).
+__device__ __forceinline__ uint64_t tk_pair(uint32_t hi, uint32_t lo) { return ((uint64_t)hi << 32) | lo; }
+
+// Compare-exchange with the partner's pair (phi, plo): a lane with `up` set
+// keeps the smaller pair, any other lane the larger.
+__device__ __forceinline__ void tk_ce(uint32_t& hi, uint32_t& lo, uint32_t phi, uint32_t plo, bool up) {
+  const bool take = (tk_pair(phi, plo) > tk_pair(hi, lo)) != up;
+  hi = take ? phi : hi;
+  lo = take ? plo : lo;
+}
+
+// DPP move; a lane whose source lies outside its row reads 0 (bound_ctrl), so
+// no old value has to be set up.
+template <int CTRL>
+__device__ __forceinline__ uint32_t tk_dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+
+// Partner through one DPP pattern.
+template <int CTRL>
+__device__ __forceinline__ void tk_stage(uint32_t& hi, uint32_t& lo, bool up) {
+  tk_ce(hi, lo, tk_dpp<CTRL>(hi), tk_dpp<CTRL>(lo), up);
+}
+
+// Partner lane ^ 4 within 8 lanes: row_shl:4 brings lane + 4 to the lower
+// four, row_shr:4 lane - 4 to the upper four (the upper four keep the smaller).
+__device__ __forceinline__ void tk_stage_x4(uint32_t& hi, uint32_t& lo) {
+  const bool up = (threadIdx.x & 4) != 0;
+  const uint32_t ah = tk_dpp<0x104>(hi), al = tk_dpp<0x104>(lo);
+  const uint32_t bh = tk_dpp<0x114>(hi), bl = tk_dpp<0x114>(lo);
+  tk_ce(hi, lo, up ? bh : ah, up ? bl : al, up);
+}
+
+// Fast path of topk_masks.  t0 = the smallest of the eight 8-lane group
+// maxima: the eight maxima are distinct entries >= t0, so the k <= 8 largest
+// entries are all >= t0.  When at most 32 entries are >= t0 they are compacted
+// into lanes 0 .. 31 (ds_permute, other lanes hold 0:0) and a bitonic network
+// on DPP leaves the 8 largest pairs, sorted, in lanes 0 .. 7: each 8-lane
+// group is sorted, then groups are merged two at a time (a mirrored compare
+// keeps the larger half in the lower group, then half-cleaners at distances
+// 4, 2, 1).  Merges that only meet empty groups are skipped.  The k-th pair
+// then selects, exactly as the bisection does.  Returns false (sel untouched)
+// when a group holds no entry or more than 32 entries are >= t0.
+template <int MAXV>
+__device__ __forceinline__ bool topk_masks_net(const uint32_t (&u)[MAXV], int k, uint64_t (&sel)[MAXV]) {
+  const int lane = threadIdx.x & 63;
+  uint32_t m = u[0];
+#pragma unroll
+  for (int i = 1; i < MAXV; ++i) m = max(m, u[i]);
+  m = max(m, (uint32_t)GM_DPP_I((int)m, GM_QPERM_1032));
+  m = max(m, (uint32_t)GM_DPP_I((int)m, GM_QPERM_2301));
+  m = max(m, (uint32_t)GM_DPP_I((int)m, 0x141));             // row_half_mirror: the 8-lane group maximum
+  m = min(m, (uint32_t)GM_DPP_I((int)m, 0x140));             // row_mirror: the smaller of the row's two groups
+  const uint32_t t0 = min(min((uint32_t)__builtin_amdgcn_readlane((int)m, 0), (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
+                          min((uint32_t)__builtin_amdgcn_readlane((int)m, 32), (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
+  if (t0 == 0u) return false;                                // a group without entries
+  uint64_t cm[MAXV];
+  int cnt = 0;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    cm[i] = __ballot(u[i] >= t0);
+    cnt += __popcll(cm[i]);
+  }
+  if (cnt > 32) return false;
+  uint32_t hi = 0u, lo = 0u;
+  int base = 0;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const uint64_t c = cm[i];
+    const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(c >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)c, 0u));
+    const int dst = ((c >> lane) & 1ull) ? base + below : 63;   // lane 63 receives no candidate
+    const uint32_t kv = (uint32_t)__builtin_amdgcn_ds_permute(dst << 2, (int)u[i]);
+    const uint32_t iv = (uint32_t)__builtin_amdgcn_ds_permute(dst << 2, ~(lane + 64 * i));
+    const int n = __popcll(c);
+    const bool here = lane >= base && lane < base + n;
+    hi = here ? kv : hi;
+    lo = here ? iv : lo;
+    base += n;
+  }
+  const int l = lane & 7;
+  tk_stage<GM_QPERM_1032>(hi, lo, (l & 1) != 0);             // sort 8: pairs
+  tk_stage<0x1B>(hi, lo, (l & 3) >= 2);                      // quads: quad_perm [3,2,1,0]
+  tk_stage<GM_QPERM_1032>(hi, lo, (l & 1) != 0);
+  tk_stage<0x141>(hi, lo, l >= 4);                           // eights: row_half_mirror
+  tk_stage<GM_QPERM_2301>(hi, lo, (l & 2) != 0);
+  tk_stage<GM_QPERM_1032>(hi, lo, (l & 1) != 0);
+  if (cnt > 8) {                                             // lanes 8j .. 8j+7 with 8j+8 < 16: merge 16
+    tk_stage<0x140>(hi, lo, (lane & 8) != 0);                // row_mirror
+    tk_stage_x4(hi, lo);
+    tk_stage<GM_QPERM_2301>(hi, lo, (l & 2) != 0);
+    tk_stage<GM_QPERM_1032>(hi, lo, (l & 1) != 0);
+  }
+  if (cnt > 16) {                                            // lanes 0 .. 7 with lanes 23 .. 16 (lane ^ 0x17)
+    const uint32_t phi = (uint32_t)__builtin_amdgcn_ds_swizzle((int)hi, 0x5C1F);
+    const uint32_t plo = (uint32_t)__builtin_amdgcn_ds_swizzle((int)lo, 0x5C1F);
+    tk_ce(hi, lo, phi, plo, (lane & 16) != 0);
+    tk_stage_x4(hi, lo);
+    tk_stage<GM_QPERM_2301>(hi, lo, (l & 2) != 0);
+    tk_stage<GM_QPERM_1032>(hi, lo, (l & 1) != 0);
+  }
+  const uint64_t kth = tk_pair((uint32_t)__builtin_amdgcn_readlane((int)hi, k - 1),
+                               (uint32_t)__builtin_amdgcn_readlane((int)lo, k - 1));
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) sel[i] = __ballot(tk_pair(u[i], ~(uint32_t)(lane + 64 * i)) >= kth);
+  return true;
+}
+
+template <int MAXV>
+__device__ __forceinline__ void topk_masks(const uint32_t (&u)[MAXV], int k, uint64_t (&sel)[MAXV]) {
+  if (!topk_masks_net<MAXV>(u, k, sel)) topk_masks_bisect<MAXV>(u, k, sel);
 }
 
 // Expert id of rank r (0-based, ascending id) among the selected entries

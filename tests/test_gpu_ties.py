@@ -77,6 +77,48 @@ def test_ties_at_the_kth_pick(gpu):
     _check_ties(_sites(gpu, _layer(c)), c, exp)
 
 
+# One row in each of the eight 8-lane groups of the selection's first pass
+# (lane l holds ids l + 64 i, so id 8 g lies in group g).  The selection takes
+# as candidates the rows at or above the smallest group maximum and sorts them
+# in a network when there are at most 32; these cases put the ties there.
+ANCHORS = [0, 8, 16, 24, 32, 40, 48, 56]
+
+
+def test_ties_in_the_candidate_network(gpu):
+    """18 candidates (the anchors at 0.5 set the threshold): five rows tie for the
+    last three picks inside the 32-lane merge."""
+    c = np.full(E, -1.0)
+    c[[10, 50, 200]] = 4.0
+    c[[7, 90]] = 2.0
+    c[[255, 3, 100, 31, 30]] = 1.0
+    c[ANCHORS] = 0.5
+    exp = _expected(c)
+    assert exp == [10, 50, 200, 7, 90, 3, 30, 31]
+    _check_ties(_sites(gpu, _layer(c)), c, exp)
+
+
+def test_ties_with_the_threshold_rows(gpu):
+    """13 candidates (16-lane merge): the anchors tie with two more rows at the
+    threshold value itself, and the five lowest ids of the ten fill the last picks."""
+    c = np.full(E, -1.0)
+    c[[10, 50]] = 4.0
+    c[7] = 2.0
+    c[[255, 100]] = 1.0
+    c[ANCHORS] = 1.0
+    exp = _expected(c)
+    assert exp == [10, 50, 7, 0, 8, 16, 24, 32]
+    _check_ties(_sites(gpu, _layer(c)), c, exp)
+
+
+def test_eight_tied_candidates(gpu):
+    """Exactly eight candidates, all tied (the 8-lane sort alone): picks in id order."""
+    c = np.full(E, -1.0)
+    c[ANCHORS] = 1.0
+    exp = _expected(c)
+    assert exp == ANCHORS
+    _check_ties(_sites(gpu, _layer(c)), c, exp)
+
+
 def test_zero_logits_at_the_boundary(gpu):
     """Six positive logits, four exact +0.0 logits from zero rows, the rest negative:
     the two lowest-id zero rows fill the last picks."""
