@@ -75,32 +75,35 @@ def unique_experts(blk, T: int) -> int:
 
 
 def run_chain(layers, T: int, steps: int, warmup: int, seed: int):
-    """Capture one decode step (all layers, ping-pong buffers) and time `steps` replays."""
+    """Capture decode steps through gm_moe_chain (all layers in one call: at T = 1 one router
+    launch, then gate/up and down per layer, each down kernel computing the next layer's
+    router dot products) and time `steps` of them.  The graph holds two steps, the first
+    from bufs[0] to bufs[1] and the second back, so every step's output is the next step's
+    input and routing changes step to step; a step is half a replay."""
     import torch
     from npu_amd import synth
+    from npu_amd.moe import GpuMoeChain
     dev = layers[0].gate.device
     x0 = torch.from_numpy(synth.host_input(seed, T, D, rmsnorm=False)).to(dev)
     bufs = [x0.clone(), torch.empty_like(x0)]
-    for i, blk in enumerate(layers):             # eager pass: workspaces, attributes
-        blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
+    chain = GpuMoeChain(layers)
+    chain(bufs[0], residual=True, out=bufs[1])   # eager pass: workspaces, attributes
     torch.cuda.synchronize()
-    bufs[0].copy_(x0)
-    if len(layers) % 2:
-        raise ValueError("the ping-pong chain needs an even layer count")
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for i, blk in enumerate(layers):
-            blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
-    for _ in range(warmup):
+        chain(bufs[0], residual=True, out=bufs[1])
+        chain(bufs[1], residual=True, out=bufs[0])
+    reps, wreps = (steps + 1) // 2, (warmup + 1) // 2
+    for _ in range(wreps):
         g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(steps):
+    for _ in range(reps):
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    ms = e0.elapsed_time(e1) / (2 * reps)
     n_unique = [unique_experts(blk, T) for blk in layers]
     finite = bool(torch.isfinite(bufs[0]).all())
     return ms, n_unique, finite

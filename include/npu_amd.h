@@ -147,6 +147,12 @@ typedef struct gm_moe_layer {
   int32_t q_gate_sh, q_up_sh, q_down_sh;
   int32_t D, FF, FF_sh, E, k;
   int32_t q_router;             /* GM_QTYPE_BF16 or GM_QTYPE_F32 (= 0): format of router and sh_gate_inp */
+  /* Optional (NULL allowed): router and shared gate vector transposed in groups
+   * of 8 columns, [D/8][E+1][8] in q_router: group j holds columns 8j .. 8j+7 of
+   * router rows 0 .. E-1, then of sh_gate_inp (zeros without one).  Only
+   * gm_moe_chain reads it (layers 1 .. n-1 at T = 1); without it the chain runs
+   * its layers one gm_moe_forward at a time. */
+  const void* router_t;
 } gm_moe_layer;
 
 /* Workspace bytes gm_moe_forward needs for T tokens (0 on bad arguments). */
@@ -198,6 +204,28 @@ int gm_moe_prefill(const gm_moe_layer* L, const float* x, float* y, int T, int f
  */
 int gm_moe_forward_stage(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
                          size_t ws_bytes, int stage, void* stream);
+
+/*
+ * n_layers MoE blocks in sequence (the decoder loop's MoE
+ * step x = x + moe_forward(rms_norm(x)) of qwen/forward.py:880-884 repeated
+ * over consecutive layers): x_{l+1} = moe_l(x_l) (+ x_l with
+ * GM_MOE_RESIDUAL), x_0 = x, x_n written to y.  Layer l writes y when
+ * n_layers - 1 - l is even and buf otherwise (buf: [T][D], may be NULL for one
+ * layer); x is not written.  ws[l] is layer l's workspace of ws_bytes[l] >=
+ * gm_moe_workspace_bytes(&layers[l], T) bytes (the same workspace may serve
+ * every layer).  Every layer must have the same D.  At T = 1, when all layers
+ * share E, fit the one-block-per-CU gate/up kernel (e.g. FF = 512, k = 8) and
+ * layers 1 .. n-1 carry router_t,
+ * each layer's down kernel also computes the next layer's router dot products
+ * (fp64 accumulators in the next layer's workspace), so the chain runs one
+ * router launch and then two launches per layer; results equal gm_moe_forward
+ * layer by layer to fp32 rounding (the logits are the same dot products added
+ * in another order).  Otherwise each layer runs as gm_moe_forward.  After the
+ * call each workspace holds its layer's intermediates
+ * (gm_moe_workspace_offsets) when the layers' workspaces are distinct.
+ */
+int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float* y, float* buf, int T,
+                 int flags, void* const* ws, const size_t* ws_bytes, void* stream);
 
 /* Size of the static scratch gm_moe_forward_noalloc works in: 16 MiB per GPU. */
 #define GM_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)

@@ -53,6 +53,7 @@ class GmMoeLayer(ctypes.Structure):
         ("q_gate_sh", _i32), ("q_up_sh", _i32), ("q_down_sh", _i32),
         ("D", _i32), ("FF", _i32), ("FF_sh", _i32), ("E", _i32), ("k", _i32),
         ("q_router", _i32),
+        ("router_t", _vp),
     ]
 
 
@@ -74,6 +75,8 @@ SIGNATURES = {
     "gm_moe_forward_noalloc": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp]),
     "gm_moe_decode": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _vp]),
     "gm_moe_prefill": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _vp]),
+    "gm_moe_chain": (_i32, [ctypes.POINTER(GmMoeLayer), _i32, _vp, _vp, _vp, _i32, _i32,
+                            ctypes.POINTER(_vp), ctypes.POINTER(_sz), _vp]),
 }
 
 _LIB: ctypes.CDLL | None = None
@@ -90,7 +93,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(h, name)
             fn.restype = res
             fn.argtypes = args
-        if h.gm_abi_version() != 3:
+        if h.gm_abi_version() != 4:
             raise RuntimeError("libnpu_amd.so ABI version mismatch; rebuild it")
         _LIB = h
     return _LIB

@@ -6,6 +6,7 @@
 #include <mutex>
 
 #include "kernels.h"
+#include "moe_decode.h"
 
 static thread_local char g_err[512] = "";
 
@@ -51,7 +52,8 @@ GmMoeWs gm_moe_ws_layout(const gm_moe_layer* L, int T) {
   const size_t Td = T < GM_DECODE_MAX_T ? Tz : (size_t)GM_DECODE_MAX_T;   // decode chunk (bf16 routed experts)
   w.yp = o; o = align256(o + (Td * k + Td) * (size_t)L->D * 4);
   w.pre = o; o = align256(o + gm_prefill_scratch_bytes(L, T));     // every T: gm_moe_prefill takes any T
-  w.tl = o; o = align256(o + GM_TL_BYTES);
+  w.acc = o; o = align256(o + 2 * gm_acc_bytes(L->E));
+  w.tl = o; o = align256(o + GM_TL_BYTES);                   // last: the timeline tool reads the end
   w.total = o;
   return w;
 }
@@ -93,7 +95,7 @@ extern "C" {
 
 const char* gm_last_error(void) { return g_err; }
 
-int gm_abi_version(void) { return 3; }
+int gm_abi_version(void) { return 4; }
 
 int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out, void* stream) {
   if (gm_kquant_block(qtype).bytes)
@@ -217,6 +219,75 @@ int gm_moe_forward_stage(const gm_moe_layer* L, const float* x, float* y, int T,
                          size_t ws_bytes, int stage, void* stream) {
   if (stage < 0 || stage > 3) return gm_fail_arg("gm_moe_forward_stage: stage %d not in 0..3", stage);
   return moe_forward_impl(L, x, y, T, flags, ws, ws_bytes, stage, kPathAuto, stream);
+}
+
+// Layers l = 0 .. n-1 in sequence: x_{l+1} = moe_l(x_l) (+ x_l with
+// GM_MOE_RESIDUAL), x_0 = x; layer l writes y when n - 1 - l is even, else
+// buf, so that the last layer writes y.  At T = 1, when every layer fits the
+// accumulator kernels and the layers agree on D and E, the router runs once
+// (layer 0) and each layer's down kernel adds the next layer's router dot
+// products into accumulators in that layer's workspace (buffer l % 2, cleared
+// by layer l - 1's gate/up kernel): two launches per layer instead of three.
+// Otherwise every layer runs as gm_moe_forward.
+int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float* y, float* buf, int T, int flags,
+                 void* const* ws, const size_t* ws_bytes, void* stream) {
+  if (!layers || !ws || !ws_bytes) return gm_fail_arg("gm_moe_chain: NULL layers or workspace array");
+  if (n_layers < 1) return gm_fail_arg("gm_moe_chain: n_layers=%d < 1", n_layers);
+  if (T < 0) return gm_fail_arg("gm_moe_chain: negative T");
+  if (!x || !y || (n_layers > 1 && !buf)) return gm_fail_arg("gm_moe_chain: NULL x, y or buf");
+  if (x == y || x == buf || y == buf) return gm_fail_arg("gm_moe_chain: x, y and buf must not alias");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 16 ||
+      reinterpret_cast<uintptr_t>(buf) % 16)
+    return gm_fail_arg("gm_moe_chain: x, y and buf must be 16-byte aligned");
+  bool fused = T == 1;
+  for (int l = 0; l < n_layers; ++l) {
+    const gm_moe_layer* L = layers + l;
+    if (int rc = check_layer(L)) return rc;
+    if (L->D != layers[0].D) return gm_fail_arg("gm_moe_chain: layer %d has D=%d, layer 0 D=%d", l, L->D, layers[0].D);
+    if (!ws[l]) return gm_fail_arg("gm_moe_chain: workspace %d is NULL", l);
+    if (reinterpret_cast<uintptr_t>(ws[l]) % 256) return gm_fail_arg("gm_moe_chain: workspace %d not 256-byte aligned", l);
+    const size_t need = gm_moe_ws_layout(L, T).total;
+    if (ws_bytes[l] < need)
+      return gm_fail_arg("gm_moe_chain: workspace %d has %zu bytes < %zu needed", l, ws_bytes[l], need), GM_EWORKSPACE;
+    fused = fused && L->E == layers[0].E && L->D <= 4096 && L->FF <= 2048 && L->k <= 8 && gm_dec_chain_ok(L) &&
+            (l == 0 || L->router_t != nullptr);
+    if (L->router_t && reinterpret_cast<uintptr_t>(L->router_t) % 16)
+      return gm_fail_arg("gm_moe_chain: layer %d router_t must be 16-byte aligned", l);
+  }
+  if (T == 0) return GM_OK;
+  hipStream_t s = as_stream(stream);
+  const float* in = x;
+  for (int l = 0; l < n_layers; ++l) {
+    const gm_moe_layer* L = layers + l;
+    float* out = (n_layers - 1 - l) % 2 == 0 ? y : buf;
+    uint8_t* w = static_cast<uint8_t*>(ws[l]);
+    const GmMoeWs lay = gm_moe_ws_layout(L, T);
+    if (!fused) {
+      if (int rc = moe_forward_impl(L, in, out, T, flags, w, ws_bytes[l], 0, kPathAuto, stream)) return rc;
+    } else {
+      auto acc_of = [&](int j) {
+        const GmMoeWs lj = gm_moe_ws_layout(layers + j, T);
+        return reinterpret_cast<double*>(static_cast<uint8_t*>(ws[j]) + lj.acc) +
+               (size_t)(j % 2) * gm_acc_bytes(layers[j].E) / sizeof(double);
+      };
+      GmNextRouter nx{};
+      GmChainStep cs{acc_of(l), nullptr, nullptr, l == 0};
+      if (l + 1 < n_layers) {
+        const gm_moe_layer* N = layers + l + 1;
+        nx.w = N->router_t;
+        nx.nw = N->norm_w;
+        nx.acc = acc_of(l + 1);
+        nx.E = N->E;
+        nx.ld = gm_acc_ld(N->E);
+        nx.f32 = N->q_router == GM_QTYPE_F32 ? 1 : 0;
+        cs.acc_zero = nx.acc;
+        cs.next = &nx;
+      }
+      if (int rc = gm_dec_run(L, in, out, T, flags, w, lay, s, 0, &cs)) return rc;
+    }
+    in = out;
+  }
+  return GM_OK;
 }
 
 }  // extern "C"

@@ -36,9 +36,29 @@ struct GmMoeWs {
   size_t hsh;      // f32 [T][FF_sh]  shared SwiGLU activations (directly after h)
   size_t yp;       // f32 [T * k + T][D]  per-pair / shared partial outputs (decode, T > 1)
   size_t pre;      // prefill scratch (see prefill.hip)
-  size_t tl;       // per-block timestamps (profiling build only, else empty)
+  size_t acc;      // T = 1 router accumulators, two buffers of gm_acc_bytes(E) (moe_decode.h)
+  size_t tl;       // per-block timestamps (profiling build only, else empty); last region
   size_t total;
 };
+
+// T = 1 router accumulators (layout in moe_decode.h): GM_ACC_COPIES copies of
+// gm_acc_ld(E) doubles.
+constexpr int GM_ACC_COPIES = 8;
+inline int gm_acc_ld(int E) { return (E + 2 + 7) & ~7; }
+inline size_t gm_acc_bytes(int E) { return (size_t)GM_ACC_COPIES * gm_acc_ld(E) * sizeof(double); }
+
+// One layer of gm_moe_chain's T = 1 accumulator path: the router accumulators
+// the gate/up kernel reads (acc), those it clears for the next layer (acc_zero,
+// or NULL), the next layer for the down kernel (or NULL), and whether the
+// router kernel runs first (the chain's first layer).
+struct GmNextRouter;
+struct GmChainStep {
+  double* acc;
+  double* acc_zero;
+  const GmNextRouter* next;
+  bool router;
+};
+bool gm_dec_chain_ok(const gm_moe_layer* P);
 
 GmMoeWs gm_moe_ws_layout(const gm_moe_layer* L, int T);
 size_t gm_prefill_scratch_bytes(const gm_moe_layer* L, int T);
@@ -59,7 +79,7 @@ int gm_launch_router(const uint16_t* w_router, const float* bias, const float* x
                      float* sh_gate, hipStream_t s);
 int gm_launch_topk(const float* logits, int T, int E, int k, int32_t* ids, float* wts, hipStream_t s);
 int gm_dec_run(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
-                  const GmMoeWs& lay, hipStream_t s, int stage = 0);
+                  const GmMoeWs& lay, hipStream_t s, int stage = 0, const GmChainStep* cs = nullptr);
 int gm_pf_run(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws,
                    const GmMoeWs& lay, hipStream_t s);
 int gm_launch_dispatch(const int32_t* ids, int T, int k, int E, int32_t* counts, int32_t* offsets,

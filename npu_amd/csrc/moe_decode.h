@@ -18,7 +18,36 @@ struct GmDecArgs {
   float* rms;       // [T] RMSNorm factors (general path, inside yp)
   uint8_t* xl;      // [T + 1] limb rows of x w_norm (general path, inside yp)
   uint64_t* tl;     // per-block timestamps (profiling build)
+  double* acc;      // T = 1 router accumulators of this layer (see gm_acc_ld), read by the gate/up kernel
+  double* acc_zero; // accumulators the gate/up kernel clears for the next layer's down kernel (or NULL)
 };
+
+// T = 1 router accumulators: GM_ACC_COPIES copies of gm_acc_ld(E) doubles.
+// Word e < E: the raw router dot product sum_d W[e][d] (x[d] w_norm[d]) of
+// expert e (no RMSNorm factor, no bias); word E: the same for the shared gate
+// vector; word E + 1: sum_d x[d]^2.  The value of a word is the fp64 sum of
+// its copies, added in copy order.  Either the router kernel writes copy 0 and
+// zeros the others, or the previous layer's down kernel (block b) adds its
+// rows' fp32 partials into copy b % 8 with fp64 atomics, which spreads the
+// 256-way contention on one address over 8 addresses.  An fp64 sum of fp32
+// terms is exact, hence independent of the order the atomics land in, unless
+// the terms span more than 29 binades.
+// (GM_ACC_COPIES, gm_acc_ld and gm_acc_bytes are in kernels.h.)
+
+// The next layer's router, for the T = 1 down kernel of a chain: block b adds
+// its 8 output rows' share of the next layer's accumulators (router rows and
+// the shared gate vector at columns r0 .. r0 + 7, times the next layer's
+// RMSNorm weight, and the sum of squares of the rows).
+struct GmNextRouter {
+  const void* w;     // gm_moe_layer.router_t: [D/8][E+1][8], bf16 bits or fp32 (f32 != 0)
+  const float* nw;   // [D] RMSNorm weight, or NULL
+  double* acc;       // GM_ACC_COPIES x ld accumulators, zeroed by this layer's gate/up kernel
+  int E, ld, f32;
+};
+
+// gm_dec_chain_ok (kernels.h): the T = 1 layers that run on the accumulator
+// kernels (router, k_dec_gateup1w, k_dec_down1), which a chain links by the
+// down kernel feeding the next layer's accumulators.
 
 // Row stride of the router partials: E rows + the shared gate row, padded to 4.
 inline int gm_dec_part_ld(const gm_moe_layer* P) { return (P->E + 1 + 3) & ~3; }
@@ -39,4 +68,4 @@ inline int gm_dec_fc(int FF) { return FF <= 512 ? 1 : FF <= 1024 ? 2 : 4; }
 int gm_dec_gateup(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s);
 // Stage 3: down projections and the weighted combine (+ shared expert, + x).
 int gm_dec_down(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
-                hipStream_t s);
+                hipStream_t s, const GmNextRouter* next = nullptr);

@@ -34,10 +34,16 @@ namespace {
 // chunk i of the limb row of xn = (x * rms) * w_norm that the gate/up kernel
 // multiplies with, a dependent chain of about 0.35 us that a row wave would
 // otherwise add to its dot product.
+// With acc set (the accumulator kernels of the T = 1 gate/up launch that
+// k_dec_gateup1w runs) the raw dot products W . (x * w_norm) go to copy 0 of
+// the accumulators instead (word E: the shared gate row, word E + 1: the sum of
+// x^2), lanes 1-7 clear the other copies, and no limb row is written: the
+// gate/up kernel applies the RMSNorm factor and the bias itself.
 template <int NCH, bool RF32>
 __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float* __restrict__ x,
                                                      float* __restrict__ logits, float* __restrict__ shg,
-                                                     uint8_t* __restrict__ xl_out GM_TL_PARAM) {
+                                                     uint8_t* __restrict__ xl_out, double* __restrict__ acc,
+                                                     int acc_ld GM_TL_PARAM) {
   GM_TL_BEGIN();
   const int lane = threadIdx.x & 63, gw = blockIdx.x * 2 + (threadIdx.x >> 6);
   const int D = P.D, E = P.E, nrows = E + (P.sh_gate_inp != nullptr ? 1 : 0);
@@ -45,7 +51,7 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
   const bool limb_wave = gw < nl;                               // uniform per wave
   const int r = gw - nl;
   const int row = r < nrows ? (r < 0 ? 0 : r) : nrows - 1;    // spare waves redo the last row
-  if (gw == 0 && lane == 0 && P.sh_gate_inp == nullptr) shg[0] = 1.f;   // no gate row: ungated shared expert
+  if (gw == 0 && lane == 0 && P.sh_gate_inp == nullptr && acc == nullptr) shg[0] = 1.f;   // ungated shared expert
   const void* wr = row < E ? router_row<RF32>(P.router, row, D) : P.sh_gate_inp;
   RouterChunk<RF32> wb[NCH];
   gm_f32x4 xa[NCH], xb[NCH], na[NCH], nb[NCH];
@@ -117,7 +123,12 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
   }
   dot = gm_wave_sum64(dot);
   GM_TL_MARK2(dot);
-  if (r < nrows && lane == 0) {
+  if (acc != nullptr) {
+    if (lane < GM_ACC_COPIES) {
+      if (r < nrows) acc[lane * acc_ld + row] = lane == 0 ? (double)dot : 0.0;
+      if (r == 0) acc[lane * acc_ld + E + 1] = lane == 0 ? (double)ss : 0.0;
+    }
+  } else if (r < nrows && lane == 0) {
     if (row < E) logits[row] = rms * dot + bias;
     else shg[0] = gm_sigmoid(rms * dot);
   }
@@ -208,8 +219,13 @@ int launch_router_t(const gm_moe_layer* P, const float* x, int T, const GmDecArg
     GM_TRY(hipGetLastError());
     return GM_OK;
   }
-  const dim3 grid((nrows + (P->D + 511) / 512 + 1) / 2);            // limb waves, then one wave per row
-#define GM_R1(n) hipLaunchKernelGGL((k_dec_router1<n, RF32>), grid, dim3(128), 0, s, *P, x, a.logits, a.shg, a.xl GM_TL_ARG(a.tl))
+  // limb waves (not with the accumulators), then one wave per row
+  const int nl = a.acc != nullptr ? 0 : (P->D + 511) / 512;
+  const dim3 grid((nrows + nl + 1) / 2);
+  uint8_t* xl = a.acc != nullptr ? nullptr : a.xl;
+  const int ld = gm_acc_ld(P->E);
+#define GM_R1(n) hipLaunchKernelGGL((k_dec_router1<n, RF32>), grid, dim3(128), 0, s, *P, x, a.logits, a.shg, xl, \
+                                    a.acc, ld GM_TL_ARG(a.tl))
   switch ((P->D + 511) / 512) {
     case 1: GM_R1(1); break;
     case 2: GM_R1(2); break;
@@ -232,8 +248,15 @@ int launch_router(const gm_moe_layer* P, const float* x, int T, const GmDecArgs&
 
 }  // namespace
 
+bool gm_dec_chain_ok(const gm_moe_layer* P) {
+  const bool fast1 = P->FF == 256 || P->FF == 512 ||
+                     (P->FF == 1024 && P->q_down != GM_QTYPE_BF16 && P->q_down != GM_QTYPE_I8);
+  const int nblk = P->k * (P->FF / 16);
+  return fast1 && P->FF % 16 == 0 && nblk >= 192 && nblk <= 1024 && (!P->gate_sh || P->FF_sh <= 2 * nblk);
+}
+
 int gm_dec_run(const gm_moe_layer* P, const float* x, float* y, int T, int flags, uint8_t* ws,
-                  const GmMoeWs& lay, hipStream_t s, int stage) {
+                  const GmMoeWs& lay, hipStream_t s, int stage, const GmChainStep* cs) {
   if (T < 1 || T > GM_DECODE_MAX_T) return gm_fail_arg("gm_moe_forward: decode path needs 1 <= T <= 8 (T=%d)", T);
   if (P->D % 256 || P->FF % 256) return gm_fail_arg("gm_moe_forward: D and FF must be multiples of 256");
   if (P->D > 4096 || P->FF > 2048)
@@ -263,11 +286,26 @@ int gm_dec_run(const gm_moe_layer* P, const float* x, float* y, int T, int flags
   // (bf16 and I8 routed down rows fit the down kernel's LDS slices up to FF = 512)
   const bool fast1 = T == 1 && (P->FF == 256 || P->FF == 512 ||
                                 (P->FF == 1024 && P->q_down != GM_QTYPE_BF16 && P->q_down != GM_QTYPE_I8));
-  if (stage == 0 || stage == 1)
+  // T = 1 shapes of k_dec_gateup1w: the router kernel writes raw dot products
+  // into the accumulators of buffer 0 (in a chain: the buffers cs names)
+  a.acc = nullptr;
+  a.acc_zero = nullptr;
+  const GmNextRouter* next = nullptr;
+  bool run_router = stage == 0 || stage == 1;
+  if (cs != nullptr) {
+    if (!(fast1 && gm_dec_chain_ok(P)) || stage != 0) return gm_fail_arg("gm_moe_chain: internal error (chain step)");
+    a.acc = cs->acc;
+    a.acc_zero = cs->acc_zero;
+    next = cs->next;
+    run_router = cs->router;
+  } else if (fast1 && gm_dec_chain_ok(P)) {
+    a.acc = reinterpret_cast<double*>(ws + lay.acc);
+  }
+  if (run_router)
     if (int rc = launch_router(P, x, T, a, s, fast1)) return rc;
   if (stage == 0 || stage == 2)
     if (int rc = gm_dec_gateup(P, x, T, fast1, a, s)) return rc;
   if (stage == 0 || stage == 3)
-    if (int rc = gm_dec_down(P, x, y, T, flags, fast1, a, s)) return rc;
+    if (int rc = gm_dec_down(P, x, y, T, flags, fast1, a, s, next)) return rc;
   return GM_OK;
 }

@@ -70,10 +70,19 @@ __device__ __forceinline__ float down_sub_dot(const uint8_t* __restrict__ rowp, 
   }
 }
 
-template <int QTD, int QTS, int FC>
+// With NXT (a chain's next layer, nx): thread t <= E of the next layer also
+// loads its router row t (row E: the shared gate vector) at columns r0 .. r0+7
+// from the grouped transpose router_t (one contiguous run per block) and,
+// once the block's 8 outputs y are final, adds
+// sum_i W[t][r0 + i] (y[r0 + i] w_norm[r0 + i]) and (thread E + 1) the sum of
+// y^2 over the 8 rows to copy blockIdx % 8 of the next layer's router
+// accumulators with fp64 atomics.  That replaces the next layer's router
+// launch (qwen/forward.py:608 on rms_norm of this block's output).
+template <int QTD, int QTS, int FC, bool NXT>
 __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* __restrict__ x, int flags,
                                                    const int32_t* __restrict__ g_grp, const float* __restrict__ h,
-                                                   const float* __restrict__ shg, float* __restrict__ y GM_TL_PARAM) {
+                                                   const float* __restrict__ shg, float* __restrict__ y,
+                                                   GmNextRouter nx GM_TL_PARAM) {
   constexpr int NTH = 576;
   GM_TL_BEGIN();
   constexpr bool IQ3 = QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS;
@@ -88,6 +97,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   __shared__ float s_wj[8];        // routing weight and h row of routed matrix m
   __shared__ int32_t s_pr[8];
   __shared__ float s_part[9][8];
+  __shared__ float s_y[8];
   const int D = P.D, FF = P.FF, k = P.k, nsub = FF / GM_SUB;
   const int rbd = (int)gm_row_bytes(QTD, FF), rbs = (int)gm_row_bytes(QTS, FF);
   const int nqr = FF >> 2;
@@ -147,6 +157,23 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
                                                            ((int64_t)e * D + r0) * rbd + 16 * j));
       dst[i] = c < total ? m * 8 * rbd + 16 * j : trash;
     }
+  }
+  // the next layer's router columns r0 .. r0 + 7 (needed only at the end)
+  gm_u32x4 nr0{}, nr1{};
+  gm_f32x4 nwa{}, nwb{};
+  if constexpr (NXT) {
+    const int t = tid <= nx.E ? tid : 0;
+    const int es = nx.f32 ? 4 : 2;
+    const uint8_t* p = static_cast<const uint8_t*>(nx.w) + ((int64_t)blockIdx.x * (nx.E + 1) + t) * 8 * es;
+    nr0 = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(p));
+    nr1 = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(p + (nx.f32 ? 16 : 0)));
+    // without a norm weight the loads read the router's first 32 bytes and are replaced by ones
+    const bool hn = nx.nw != nullptr;
+    const float* nwp = hn ? nx.nw + r0 : static_cast<const float*>(nx.w);
+    const gm_f32x4 la = *reinterpret_cast<const gm_f32x4*>(nwp), lb = *reinterpret_cast<const gm_f32x4*>(nwp + 4);
+    const gm_f32x4 one{1.f, 1.f, 1.f, 1.f};
+    nwa = hn ? la : one;
+    nwb = hn ? lb : one;
   }
   GM_TL_MARK1(ex[0]);
   issue_fence();
@@ -209,7 +236,38 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
     float acc = 0.f;
     for (int w = 0; w < k; ++w) acc += s_part[w][tid];
     if (has_sh) acc += s_part[k][tid];
-    if (r0 + tid < D) y[r0 + tid] = (flags & GM_MOE_RESIDUAL) ? xres + acc : acc;
+    const float yv = (flags & GM_MOE_RESIDUAL) ? xres + acc : acc;
+    if (r0 + tid < D) y[r0 + tid] = yv;
+    if constexpr (NXT) s_y[tid] = yv;
+  }
+  if constexpr (NXT) {
+    __syncthreads();
+    if (tid <= nx.E + 1) {
+      const float yv[8] = {s_y[0], s_y[1], s_y[2], s_y[3], s_y[4], s_y[5], s_y[6], s_y[7]};
+      const float nv[8] = {nwa.x, nwa.y, nwa.z, nwa.w, nwb.x, nwb.y, nwb.z, nwb.w};
+      float wv[8];
+      if (nx.f32) {
+        const uint32_t q[8] = {nr0.x, nr0.y, nr0.z, nr0.w, nr1.x, nr1.y, nr1.z, nr1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wv[i] = __uint_as_float(q[i]);
+      } else {
+        const uint32_t q[4] = {nr0.x, nr0.y, nr0.z, nr0.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          wv[2 * i] = __uint_as_float(q[i] << 16);
+          wv[2 * i + 1] = __uint_as_float(q[i] & 0xffff0000u);
+        }
+      }
+      float p = 0.f;
+      if (tid <= nx.E) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p = fmaf(wv[i], yv[i] * nv[i], p);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p = fmaf(yv[i], yv[i], p);
+      }
+      unsafeAtomicAdd(nx.acc + (blockIdx.x & (GM_ACC_COPIES - 1)) * nx.ld + tid, (double)p);
+    }
   }
   GM_TL_END(2);
 }
@@ -374,16 +432,22 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ x
 
 template <int QTD, int QTS, int FC>
 int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
-              hipStream_t s) {
+              hipStream_t s, const GmNextRouter* next) {
   const int D = P->D, FF = P->FF, k = P->k;
   if (fast1) {
     if constexpr (FC <= (QTD == GM_QTYPE_BF16 || QTD == GM_QTYPE_I8 ? 1 : 2)) {   // bf16 / I8 rows: 8 / 6 KB per slice
       const size_t wbytes = (size_t)k * 8 * gm_row_bytes(QTD, FF) + 8 * (size_t)gm_row_bytes(QTS, FF);
       const size_t smem = (size_t)(k + 2) * gm_limb_row_bytes(FF) + ((wbytes + 16 + 15) & ~(size_t)15) +
                           (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
-      if (int rc = gm_set_smem(k_dec_down1<QTD, QTS, FC>, smem)) return rc;
-      hipLaunchKernelGGL((k_dec_down1<QTD, QTS, FC>), dim3((D + 7) / 8), dim3(576), smem, s, *P, x, flags, a.grp,
-                         a.h, a.shg, y GM_TL_ARG(a.tl));
+      if (next != nullptr) {
+        if (int rc = gm_set_smem(k_dec_down1<QTD, QTS, FC, true>, smem)) return rc;
+        hipLaunchKernelGGL((k_dec_down1<QTD, QTS, FC, true>), dim3((D + 7) / 8), dim3(576), smem, s, *P, x, flags,
+                           a.grp, a.h, a.shg, y, *next GM_TL_ARG(a.tl));
+      } else {
+        if (int rc = gm_set_smem(k_dec_down1<QTD, QTS, FC, false>, smem)) return rc;
+        hipLaunchKernelGGL((k_dec_down1<QTD, QTS, FC, false>), dim3((D + 7) / 8), dim3(576), smem, s, *P, x, flags,
+                           a.grp, a.h, a.shg, y, GmNextRouter{} GM_TL_ARG(a.tl));
+      }
       GM_TRY(hipGetLastError());
       return GM_OK;
     }
@@ -405,23 +469,23 @@ int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags,
 
 template <int QTD, int QTS>
 int launch_dn_f(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
-                hipStream_t s) {
+                hipStream_t s, const GmNextRouter* next) {
   switch (gm_dec_fc(P->FF)) {
-    case 1: return launch_dn<QTD, QTS, 1>(P, x, y, T, flags, fast1, a, s);
-    case 2: return launch_dn<QTD, QTS, 2>(P, x, y, T, flags, fast1, a, s);
-    default: return launch_dn<QTD, QTS, 4>(P, x, y, T, flags, fast1, a, s);
+    case 1: return launch_dn<QTD, QTS, 1>(P, x, y, T, flags, fast1, a, s, next);
+    case 2: return launch_dn<QTD, QTS, 2>(P, x, y, T, flags, fast1, a, s, next);
+    default: return launch_dn<QTD, QTS, 4>(P, x, y, T, flags, fast1, a, s, next);
   }
 }
 
 template <int QTD>
 int launch_dn_s(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
-                hipStream_t s) {
-  if (!P->down_sh) return launch_dn_f<QTD, QTD>(P, x, y, T, flags, fast1, a, s);
+                hipStream_t s, const GmNextRouter* next) {
+  if (!P->down_sh) return launch_dn_f<QTD, QTD>(P, x, y, T, flags, fast1, a, s, next);
   switch (P->q_down_sh) {
-    case GM_QTYPE_IQ4_XS: return launch_dn_f<QTD, GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s);
-    case GM_QTYPE_IQ3_XXS: return launch_dn_f<QTD, GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s);
-    case GM_QTYPE_BF16: return launch_dn_f<QTD, GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s);
-    case GM_QTYPE_I8: return launch_dn_f<QTD, GM_QTYPE_I8>(P, x, y, T, flags, fast1, a, s);
+    case GM_QTYPE_IQ4_XS: return launch_dn_f<QTD, GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s, next);
+    case GM_QTYPE_IQ3_XXS: return launch_dn_f<QTD, GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s, next);
+    case GM_QTYPE_BF16: return launch_dn_f<QTD, GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s, next);
+    case GM_QTYPE_I8: return launch_dn_f<QTD, GM_QTYPE_I8>(P, x, y, T, flags, fast1, a, s, next);
     default: return gm_fail_arg("gm_moe_forward: shared down format %d unsupported", P->q_down_sh);
   }
 }
@@ -429,12 +493,13 @@ int launch_dn_s(const gm_moe_layer* P, const float* x, float* y, int T, int flag
 }  // namespace
 
 int gm_dec_down(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
-                hipStream_t s) {
+                hipStream_t s, const GmNextRouter* next) {
+  if (next != nullptr && !(fast1 && T == 1)) return gm_fail_arg("gm_moe_chain: internal error (next router off T = 1)");
   switch (P->q_down) {
-    case GM_QTYPE_IQ4_XS: return launch_dn_s<GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s);
-    case GM_QTYPE_IQ3_XXS: return launch_dn_s<GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s);
-    case GM_QTYPE_BF16: return launch_dn_s<GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s);
-    case GM_QTYPE_I8: return launch_dn_s<GM_QTYPE_I8>(P, x, y, T, flags, fast1, a, s);
+    case GM_QTYPE_IQ4_XS: return launch_dn_s<GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s, next);
+    case GM_QTYPE_IQ3_XXS: return launch_dn_s<GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s, next);
+    case GM_QTYPE_BF16: return launch_dn_s<GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s, next);
+    case GM_QTYPE_I8: return launch_dn_s<GM_QTYPE_I8>(P, x, y, T, flags, fast1, a, s, next);
     default: return gm_fail_arg("gm_moe_forward: routed down format %d unsupported", P->q_down);
   }
 }

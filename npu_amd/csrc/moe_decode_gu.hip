@@ -145,32 +145,43 @@ __global__ void __launch_bounds__(256) k_dec_gateup1(gm_moe_layer P, const float
 // flight from the block's start while wave 0 runs the top-k.  With k n_chunks
 // = 256 blocks every block starts at once: in the 8-row layout above, 576
 // blocks made 2-3 per CU, and the last ones dispatched ended up to 1.5 us after
-// the median.  The selection, hand-off and publishing are those of
-// k_dec_gateup1.
+// the median.
+// Routing input: the router accumulators (raw dot products W . (x w_norm) of
+// the E rows and the shared gate row, and the sum of x^2, each the fp64 sum of
+// GM_ACC_COPIES copies, written by the router kernel or by the previous
+// layer's down kernel).  Wave 0 adds the copies in copy order, forms the
+// logits rms * S_e + bias (rms = 1 / sqrt(mean(x^2) + eps), qwen/forward.py:
+// 58-61) and selects, while waves 1-7 build the limb row of x * w_norm in LDS
+// (the gate and up sums are scaled by rms instead).  A variant where waves
+// 1-7 added the copies into LDS ahead of a second barrier took 0.45 us longer
+// to the top-k.  Block 0
+// publishes the ids, weights, grouping table, logits and shared gate once its
+// rows are in flight; every block clears its share of the next layer's
+// accumulators (acc_zero) for the down kernel that follows.
 template <int QT, int QTS, int DC, int MAXV>
-__global__ void __launch_bounds__(576) k_dec_gateup1w(gm_moe_layer P, const float* __restrict__ logits,
-                                                      int32_t* __restrict__ g_ids, float* __restrict__ g_wts,
-                                                      int32_t* __restrict__ g_grp, float* __restrict__ h,
-                                                      float* __restrict__ hsh, int n_chunks,
-                                                      const uint8_t* __restrict__ xl GM_TL_PARAM) {
+__global__ void __launch_bounds__(576) k_dec_gateup1w(gm_moe_layer P, const float* __restrict__ x,
+                                                      const double* __restrict__ acc, double* __restrict__ acc_zero,
+                                                      int acc_ld, float* __restrict__ logits,
+                                                      float* __restrict__ shg, int32_t* __restrict__ g_ids,
+                                                      float* __restrict__ g_wts, int32_t* __restrict__ g_grp,
+                                                      float* __restrict__ h, float* __restrict__ hsh,
+                                                      int n_chunks GM_TL_PARAM) {
   GM_TL_BEGIN();
   constexpr int NTH = 576;
   constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS;
-  constexpr int CPT = (32 * DC * GM_LSUB / 16 + NTH - 1) / NTH;   // 16-byte limb chunks per thread
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int32_t s_e;
+  __shared__ float s_rms;
   const int D = P.D, E = P.E, k = P.k, FF = P.FF, nsub = D / GM_SUB, rbytes = gm_limb_row_bytes(D);
-  uint8_t* xs = smem;                                           // limb row of xn (+ a spare chunk)
+  uint8_t* xs = smem;                                           // limb row of x w_norm (+ a spare chunk)
   Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(smem + rbytes + GM_LSUB);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane & 31;
   const int b = blockIdx.x, u = b / n_chunks, chunk = b - u * n_chunks;
   const bool shw = wave == 8;                                   // uniform per wave
-  const int rch = rbytes >> 4;
-  gm_u32x4 cp[CPT];
-#pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    const int c = threadIdx.x + NTH * i;
-    cp[i] = reinterpret_cast<const gm_u32x4*>(xl)[c < rch ? c : rch - 1];
+  if (acc_zero != nullptr) {                                    // this block's share of the next layer's accumulators
+    const int n16 = GM_ACC_COPIES * acc_ld / 2, per = (n16 + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int c = b * per + (int)threadIdx.x;
+    if ((int)threadIdx.x < per && c < n16) reinterpret_cast<gm_u32x4*>(acc_zero)[c] = gm_u32x4{0u, 0u, 0u, 0u};
   }
   uint32_t gw = 0;
   if constexpr (IQ3) gw = gm_iq3_tab_load();
@@ -191,23 +202,77 @@ __global__ void __launch_bounds__(576) k_dec_gateup1w(gm_moe_layer P, const floa
     }
   } else if (wave == 0) {
     __builtin_amdgcn_s_setprio(3);
+    // the copies of the lane's E / 64 words, of the shared gate word and of the
+    // sum of squares, loaded a batch of CB copies at a time (all 8 at E <= 256)
+    // before any is added; the copies are added in copy order
+    constexpr int CB = MAXV > 4 ? 4 : GM_ACC_COPIES;
+    double sd[MAXV], ssd = 0.0, sgd = 0.0;
+#pragma unroll
+    for (int c0 = 0; c0 < GM_ACC_COPIES; c0 += CB) {
+      double a[CB][MAXV], ag[CB], aq[CB];
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+#pragma unroll
+        for (int i = 0; i < MAXV; ++i) {
+          const int e = lane + 64 * i;
+          a[c][i] = acc[(c0 + c) * acc_ld + (e < E ? e : E - 1)];
+        }
+        ag[c] = acc[(c0 + c) * acc_ld + E];
+        aq[c] = acc[(c0 + c) * acc_ld + E + 1];
+      }
+#pragma unroll
+      for (int c = 0; c < CB; ++c) {
+        ssd = c0 + c == 0 ? aq[c] : ssd + aq[c];
+        sgd = c0 + c == 0 ? ag[c] : sgd + ag[c];
+#pragma unroll
+        for (int i = 0; i < MAXV; ++i) sd[i] = c0 + c == 0 ? a[c][i] : sd[i] + a[c][i];
+      }
+      issue_fence();
+    }
+    const float rms = P.norm_w != nullptr ? 1.0f / sqrtf((float)ssd / (float)D + P.norm_eps) : 1.0f;
     float v[MAXV];
     int ix[MAXV];
-    topk_load<MAXV>(logits, E, v, ix);
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+      ix[i] = lane + 64 * i;
+      const float bias = P.router_bias != nullptr ? P.router_bias[ix[i] < E ? ix[i] : E - 1] : 0.f;
+      v[i] = rms * (float)sd[i] + bias;
+    }
     GM_TL_MARK3(v[0]);
     topk_keys<MAXV>(v, ix, E, uk);
     topk_masks<MAXV>(uk, k, sel);
-    if (lane == 0) s_e = topk_rank_id<MAXV>(sel, u);
+    if (lane == 0) {
+      s_e = topk_rank_id<MAXV>(sel, u);
+      s_rms = rms;
+    }
     __builtin_amdgcn_s_setprio(0);
+    if (b == 0) {                                               // logits and shared gate, for stage 3 and the caller
+#pragma unroll
+      for (int i = 0; i < MAXV; ++i)
+        if (ix[i] < E) logits[ix[i]] = v[i];
+      if (lane == 0) shg[0] = P.sh_gate_inp != nullptr ? gm_sigmoid(rms * (float)sgd) : 1.f;
+    }
+  } else if (512 * (wave - 1) < D) {
+    // waves 1-7: chunks of 512 values (wave - 1 + 7 j) of the limb row of x w_norm;
+    // lanes past D write the spare sub-block after the row
+    const gm_f32x4* x4 = reinterpret_cast<const gm_f32x4*>(x);
+    const gm_f32x4* w4 = reinterpret_cast<const gm_f32x4*>(P.norm_w);
+    for (int i = wave - 1; 512 * i < D; i += 7) {
+      const int kk = 512 * i + 8 * lane, c = kk >> 2;             // float4 index, even
+      const int cl = kk < D ? c : (D >> 2) - 2;                   // lanes past D re-read the end
+      gm_f32x4 va = x4[cl], vb = x4[cl + 1];
+      if (P.norm_w != nullptr) {
+        const gm_f32x4 wa = w4[cl], wb = w4[cl + 1];
+        va.x *= wa.x; va.y *= wa.y; va.z *= wa.z; va.w *= wa.w;
+        vb.x *= wb.x; vb.y *= wb.y; vb.z *= wb.z; vb.w *= wb.w;
+      }
+      gm_put_limbs8(va, vb, kk < D ? c : (D >> 2) + (c & 7), xs);
+    }
   }
   issue_fence();
-#pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    const int c = threadIdx.x + NTH * i;
-    reinterpret_cast<gm_u32x4*>(xs)[c < rch ? c : rch] = cp[i];   // past the row: the spare chunk
-  }
   if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
   __syncthreads();
+  const float rms = s_rms;
   const int tok[1] = {0};
   float ag[1] = {0.f}, au[1] = {0.f};
   if (!shw) {
@@ -245,7 +310,7 @@ __global__ void __launch_bounds__(576) k_dec_gateup1w(gm_moe_layer P, const floa
     dot_subs_i8<QTS, 32, DC, 1>(su, lir, nsub, xs, rbytes, tok, 1, tab, au);
   }
   GM_TL_MARK2(au[0]);
-  const float hv = gm_silu(row_sum<32>(ag[0])) * row_sum<32>(au[0]);
+  const float hv = gm_silu(rms * row_sum<32>(ag[0])) * (rms * row_sum<32>(au[0]));
   if (live && lir == 0) {
     if (shw) hsh[row] = hv;
     else h[(int64_t)u * FF + row] = hv;
@@ -458,15 +523,16 @@ __global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const uint8
 template <int QT, int QTS, int DC>
 int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s) {
   if (fast1) {
-    // one block per CU: 16 routed rows per block, two shared rows on a ninth wave
-    const int n16 = P->FF / 16, nblk = P->k * n16;
-    if (P->FF % 16 == 0 && nblk >= 192 && nblk <= 1024 && (!P->gate_sh || P->FF_sh <= 2 * nblk)) {
+    if (a.acc != nullptr) {
+      // one block per CU: 16 routed rows per block, two shared rows on a ninth wave
+      // (gm_dec_chain_ok checked the shape)
+      const int n16 = P->FF / 16, nblk = P->k * n16;
       const size_t smem = (size_t)gm_limb_row_bytes(P->D) + GM_LSUB +
                           (QT == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS ? sizeof(Iq3Tab) : 0);
       auto kern = P->E <= 256 ? k_dec_gateup1w<QT, QTS, DC, 4> : k_dec_gateup1w<QT, QTS, DC, 8>;
       if (int rc = gm_set_smem(kern, smem)) return rc;
-      hipLaunchKernelGGL(kern, dim3(nblk), dim3(576), smem, s, *P, a.logits, a.ids, a.wts, a.grp, a.h, a.hsh, n16,
-                         a.xl GM_TL_ARG(a.tl));
+      hipLaunchKernelGGL(kern, dim3(nblk), dim3(576), smem, s, *P, x, a.acc, a.acc_zero, gm_acc_ld(P->E), a.logits,
+                         a.shg, a.ids, a.wts, a.grp, a.h, a.hsh, n16 GM_TL_ARG(a.tl));
       GM_TRY(hipGetLastError());
       return GM_OK;
     }

@@ -134,6 +134,14 @@ class GpuMoeBlock:
         s.q_down_sh = self.q_down_sh
         s.D, s.FF, s.FF_sh, s.E, s.k = self.D, self.FF, self.FF if self.gate_sh is not None else 0, self.E, self.k
         s.q_router = int(self.q_router)
+        # [D/8][E+1][8]: router and shared gate columns in groups of 8 (gm_moe_chain's
+        # down kernels read the next layer's router 8 columns at a time)
+        rt = torch.zeros(self.E + 1, self.D, dtype=self.router.dtype, device=self.router.device)
+        rt[:self.E] = self.router
+        if self.sh_gate_inp is not None:
+            rt[self.E] = self.sh_gate_inp
+        self.router_t = rt.view(self.E + 1, self.D // 8, 8).permute(1, 0, 2).contiguous()
+        s.router_t = L.ptr(self.router_t)
         self.struct = s
         self._ws: torch.Tensor | None = None
 
@@ -216,3 +224,34 @@ class GpuMoeBlock:
             sh = sum(t.numel() * t.element_size() for t in (self.gate_sh, self.up_sh, self.down_sh))
         g = 0 if self.sh_gate_inp is None else self.sh_gate_inp.numel() * self.sh_gate_inp.element_size()
         return self.k * per_exp + sh + self.router.numel() * self.router.element_size() + g
+
+
+class GpuMoeChain:
+    """Consecutive ``GpuMoeBlock`` layers run by one ``gm_moe_chain`` call: x_{l+1} =
+    x_l + moe_l(rmsnorm_l(x_l)) (the MoE step of the decoder loop,
+    qwen/forward.py:880-884).  At T = 1 the library links the layers through router
+    accumulators (each layer's down kernel computes the next layer's router dot
+    products), so the chain costs one router launch plus two launches per layer.  Each
+    layer keeps its own workspace, so ``blocks[l].stages(T)`` shows layer l's ids and
+    weights after a call."""
+
+    def __init__(self, blocks: list[GpuMoeBlock]):
+        if not blocks:
+            raise ValueError("GpuMoeChain needs at least one block")
+        if len({b.D for b in blocks}) != 1:
+            raise ValueError("every block of a chain must have the same D")
+        self.blocks = list(blocks)
+        self.D = blocks[0].D
+        self._buf: torch.Tensor | None = None
+
+    def __call__(self, x: torch.Tensor, *, residual: bool = True, out: torch.Tensor | None = None) -> torch.Tensor:
+        if x.dim() != 2 or x.shape[1] != self.D:
+            raise ValueError(f"x must be [T, {self.D}], got {tuple(x.shape)}")
+        x = x.to(torch.float32).contiguous()
+        T = x.shape[0]
+        y = out if out is not None else torch.empty_like(x)
+        if self._buf is None or self._buf.shape != x.shape or self._buf.device != x.device:
+            self._buf = torch.empty_like(x)
+        ops.moe_chain_raw([b.struct for b in self.blocks], x, y, self._buf,
+                          [b.workspace(T) for b in self.blocks], residual=residual)
+        return y

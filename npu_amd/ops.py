@@ -151,3 +151,21 @@ def moe_forward_raw(layer: L.GmMoeLayer, x: torch.Tensor, y: torch.Tensor, ws: t
         rc = L.lib().gm_moe_forward_stage(ctypes.byref(layer), L.ptr(x), L.ptr(y), T, flags, L.ptr(ws),
                                           ws.numel(), stage, L.stream_ptr())
     L.check(rc, "gm_moe_forward")
+
+
+def moe_chain_raw(layers, x: torch.Tensor, y: torch.Tensor, buf: torch.Tensor | None, workspaces,
+                  residual: bool = False) -> None:
+    """Enqueue gm_moe_chain over ``layers`` (GmMoeLayer structs) with one workspace per layer:
+    x_{l+1} = moe_l(rmsnorm_l(x_l)) (+ x_l); the last layer writes y, the others alternate
+    between y and buf."""
+    n = len(layers)
+    if n < 1 or len(workspaces) != n:
+        raise ValueError("moe_chain_raw: one workspace per layer")
+    arr = (L.GmMoeLayer * n)(*layers)
+    wsp = (ctypes.c_void_p * n)(*[L.ptr(w) for w in workspaces])
+    wsb = (ctypes.c_size_t * n)(*[w.numel() for w in workspaces])
+    flags = L.GM_MOE_RESIDUAL if residual else 0
+    rc = L.lib().gm_moe_chain(arr, n, L.ptr(x), L.ptr(y), L.ptr(buf) if buf is not None else None, x.shape[0],
+                              flags, wsp, wsb, L.stream_ptr())
+    L.check(rc, "gm_moe_chain")
+

@@ -10,7 +10,7 @@ kernel: when blocks enter, reach each mark and end, and the gaps between the
 last block of one kernel ending and the first block of the next entering.
 
     python -m npu_amd.build --timeline
-    NPU_AMD_LIB=timeline python -m npu_amd.timeline [--layers 40] [--T 1] [--out FILE]
+    NPU_AMD_LIB=timeline python -m npu_amd.timeline [--layers 40] [--T 1] [--chain] [--out FILE]
 """
 from __future__ import annotations
 
@@ -46,7 +46,7 @@ def _zero_records(blk, T: int) -> None:
     blk.workspace(T)[need - N_SLOTS * MAXB * REC * 8:need].zero_()
 
 
-def run(n_layers: int, T: int, replays: int):
+def run(n_layers: int, T: int, replays: int, chain: bool = False):
     import torch
     from npu_amd import _lib, synth
     if not _lib.LIB_PATH.name.endswith("_tl.so"):
@@ -57,13 +57,20 @@ def run(n_layers: int, T: int, replays: int):
     D = layers[0].D
     x0 = torch.from_numpy(synth.host_input(SEED, T, D, rmsnorm=False)).to(dev)
     bufs = [x0.clone(), torch.empty_like(x0)]
-    for i, blk in enumerate(layers):
-        blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
+    from npu_amd.moe import GpuMoeChain
+    ch = GpuMoeChain(layers)
+
+    def step():
+        if chain:                                   # gm_moe_chain (bench.py's timed step)
+            ch(bufs[0], residual=True, out=bufs[1])
+        else:                                       # one gm_moe_forward per layer
+            for i, blk in enumerate(layers):
+                blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
+    step()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for i, blk in enumerate(layers):
-            blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
+        step()
     for _ in range(replays):
         g.replay()
     torch.cuda.synchronize()
@@ -143,9 +150,10 @@ def main() -> int:
     ap.add_argument("--T", type=int, default=1)
     ap.add_argument("--replays", type=int, default=5)
     ap.add_argument("--out", default=None, help="also write the summary to this file")
+    ap.add_argument("--chain", action="store_true", help="time gm_moe_chain instead of per-layer calls")
     ap.add_argument("--npz", default=None, help="also save every record (layer, kernel, block) to this .npz")
     args = ap.parse_args()
-    recs = run(args.layers, args.T, args.replays)
+    recs = run(args.layers, args.T, args.replays, chain=args.chain)
     if args.npz:
         import numpy as np
         rows = [(li, s, *r) for li, layer in enumerate(recs) for s in range(N_SLOTS) for r in layer[s]]

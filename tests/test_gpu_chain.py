@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from npu_amd import synth
-from npu_amd.moe import GpuMoeBlock
+from npu_amd.moe import GpuMoeBlock, GpuMoeChain
 from oracle import moe as OM
 
 pytestmark = pytest.mark.gpu
@@ -28,7 +28,10 @@ def chain(gpu):
 
 
 def _oracle_chain(hosts, x0, k):
-    """Per-layer top-k ids and the chain output; asserts every layer's input is near-tie free."""
+    """Per-layer top-k ids and the chain output; asserts every layer's input is near-tie free
+    and that the k-th and (k+1)-th softmax probabilities differ in fp32 (the reference takes
+    the top-k of the probabilities, which underflow to equal zeros when logits spread by
+    more than ~100)."""
     ids, x = [], x0
     for li, h in enumerate(hosts):
         ol = OM.OracleLayer(h)
@@ -36,6 +39,8 @@ def _oracle_chain(hosts, x0, k):
         assert bool((margin > 1e-5).all()), f"layer {li}: near-tie input, choose another seed"
         st = {}
         x = OM.block_forward(x, ol, residual=True, stages=st)
+        pv = torch.topk(st["ffn_moe_probs"], k + 1, dim=-1).values
+        assert bool((pv[:, k - 1] > pv[:, k]).all()), f"layer {li}: k-th probability ties (underflow)"
         ids.append(st["topk_ids"])
     return ids, x
 
@@ -74,4 +79,70 @@ def test_config5_chain_graph(gpu, chain, T):
             assert torch.equal(y, first), f"replay {rep} differs from replay 0"
         # eager work on the same workspaces between replays
         blocks[0](torch.randn_like(x0).to(gpu), residual=True)
+        torch.cuda.synchronize()
+
+
+# gm_moe_chain: the same chains through the library's chain entry point.  At T = 1 each
+# layer's down kernel computes the next layer's router dot products (fp64 accumulators),
+# so this checks the routing of layers 1.. computed that way against the oracle.
+CHAIN_VARIANTS = {
+    "config5": dict(norm=True),
+    "f32_router_bias": dict(norm=True, router_f32=True, bias=True),
+    "no_norm_no_shared": dict(shared=False, layers=2),   # without RMSNorm activations grow fast per layer
+    "ungated_shared": dict(norm=True, ungated=True),
+}
+
+
+@pytest.fixture(scope="module", params=sorted(CHAIN_VARIANTS))
+def variant_chain(request, gpu):
+    kw = dict(CHAIN_VARIANTS[request.param])
+    ungated = kw.pop("ungated", False)
+    hosts = []
+    for i in range(kw.pop("layers", N_LAYERS)):
+        h = synth.host_moe_layer(400 + 10 * sorted(CHAIN_VARIANTS).index(request.param) + i, **kw)
+        if ungated:
+            h.sh_gate_inp = None
+        hosts.append(h)
+    return request.param, hosts, [GpuMoeBlock.from_host(h, device=gpu) for h in hosts]
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_gm_moe_chain(gpu, variant_chain, T):
+    name, hosts, blocks = variant_chain
+    n = len(hosts)
+    print(f"gm_moe_chain case {name} T={T} layers={n}", flush=True)
+    x0 = torch.from_numpy(synth.host_input(500 + T, T, hosts[0].D, rmsnorm=hosts[0].norm_w is None))
+    if hosts[0].norm_w is None:
+        x0 = x0 * 0.01           # without RMSNorm the block amplifies ~x^2: keeps layer 1's logits spread ~10
+    ids_ref, y_ref = _oracle_chain(hosts, x0, hosts[0].k)
+    ch = GpuMoeChain(blocks)
+    xd = x0.to(gpu)
+    y_eager = ch(xd, residual=True)
+    torch.cuda.synchronize()
+    for li in range(n):
+        st = blocks[li].stages(T)
+        ids = st["topk_ids"].cpu().long()
+        if not torch.equal(ids, ids_ref[li]):
+            lg = st["ffn_moe_logits"].cpu()
+            print(f"layer {li}: ids {ids.tolist()} vs {ids_ref[li].tolist()}; logits[0,:8] {lg[0, :8].tolist()}")
+        assert torch.equal(ids, ids_ref[li]), f"layer {li} top-k ids differ"
+    rel = OM.rel_err(y_eager.cpu(), y_ref)
+    assert rel <= 1e-3, f"chain rel {rel:.3e}"
+    # the per-layer entry point computes the same function
+    bufs = [xd.clone(), torch.empty_like(xd)]
+    for i, blk in enumerate(blocks):
+        blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
+    torch.cuda.synchronize()
+    rel_pl = OM.rel_err(y_eager.cpu(), bufs[n % 2].cpu())
+    assert rel_pl <= 1e-5, f"chain vs per-layer gm_moe_forward rel {rel_pl:.3e}"
+    # captured once, replayed with other work on the workspaces in between: bit-identical
+    out = torch.empty_like(xd)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ch(xd, residual=True, out=out)
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y_eager), f"replay {rep} differs from the eager chain"
+        blocks[0](torch.randn_like(xd), residual=True)
         torch.cuda.synchronize()
