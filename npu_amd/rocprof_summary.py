@@ -41,19 +41,28 @@ D, FF, E, K = 2048, 512, 256, 8
 def algorithmic_bytes(d: int = D, ff: int = FF, e: int = E, k: int = K) -> dict[str, int]:
     """Bytes each T = 1 decode kernel must move at least once (weights read, activations
     read once, outputs written once), for a block with IQ4_XS gate/up, IQ3_XXS down, the
-    shared expert in the same formats and an RMSNorm weight.  The limb row of the
-    normalised x is d / 32 sub-blocks of 112 bytes (three int8 planes and a scale).
+    shared expert in the same formats, an RMSNorm weight and a shared scalar gate.  The
+    router accumulators are 8 copies of e + 2 fp64 words (raw router dot products, the
+    shared gate's, the sum of x^2).
       k_dec_router1: router [e, d] bf16, shared scalar gate [d] bf16, x and the RMSNorm
-        weight fp32; writes logits [e], the shared gate and the limb row.
-      k_dec_gateup1w: the k routed and the shared experts' gate and up rows, the limb row
-        and the logits; writes k + 1 SwiGLU rows [ff] fp32 and the ids and weights.
+        weight fp32; writes the 8 accumulator copies (copy 0 and zeros).
+      k_dec_gateup1w: the k routed and the shared experts' gate and up rows, x and the
+        RMSNorm weight (the limb row is built in LDS), the 8 accumulator copies; writes
+        k + 1 SwiGLU rows [ff] fp32, the logits, the ids and weights and the shared gate.
       k_dec_down1: the k routed and the shared down rows, the k + 1 SwiGLU rows, the
-        weights, the shared gate and x (residual); writes y [d]."""
-    iq4_row, iq3_row, limb = d // 256 * 136, ff // 256 * 98, d // 32 * 112
+        weights, the shared gate and x (residual); writes y [d].
+      k_dec_down1 in a chain (k_dec_down1_next): also the next layer's router and shared
+        gate [e + 1, d] bf16 (router_t) and RMSNorm weight, and one fp64 atomic per
+        accumulator word per block of 8 rows (d / 8 blocks)."""
+    iq4_row, iq3_row = d // 256 * 136, ff // 256 * 98
+    acc = 8 * (e + 2) * 8
+    down = (k + 1) * d * iq3_row + (k + 1) * ff * 4 + k * 4 + 4 + d * 4 + d * 4
     return {
-        "k_dec_router1": e * d * 2 + d * 2 + d * 4 + d * 4 + e * 4 + 4 + limb,
-        "k_dec_gateup1w": (k + 1) * 2 * ff * iq4_row + limb + e * 4 + (k + 1) * ff * 4 + 2 * k * 4,
-        "k_dec_down1": (k + 1) * d * iq3_row + (k + 1) * ff * 4 + k * 4 + 4 + d * 4 + d * 4,
+        "k_dec_router1": e * d * 2 + d * 2 + d * 4 + d * 4 + acc,
+        "k_dec_gateup1w": (k + 1) * 2 * ff * iq4_row + d * 4 + d * 4 + acc + (k + 1) * ff * 4 + e * 4
+                          + 2 * k * 4 + 4,
+        "k_dec_down1": down,
+        "k_dec_down1_next": down + (e + 1) * d * 2 + d * 4 + d // 8 * (e + 2) * 8,
     }
 
 
