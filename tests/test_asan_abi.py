@@ -72,6 +72,21 @@ assert lib.gm_dequant_f32(L.GM_QTYPE_IQ3_XXS, None, 0, None, None) == L.GM_OK
 assert lib.gm_moe_dispatch(None, -1, 8, 256, None, None, None, None) == L.GM_EINVAL
 assert lib.gm_swiglu_mlp(L.GM_QTYPE_IQ4_XS, 256, 256, L.GM_QTYPE_BF16, 264, 2048, 512, 1024, 1, 2048, 4096,
                          None) == L.GM_EINVAL
+# gm_moe_chain argument errors (host checks before any GPU call)
+arr = (L.GmMoeLayer * 2)(layer(), layer())
+wsp = (ctypes.c_void_p * 2)(1 << 24, 1 << 24)
+big = (ctypes.c_size_t * 2)(1 << 30, 1 << 30)
+small = (ctypes.c_size_t * 2)(16, 16)
+assert lib.gm_moe_chain(arr, 0, 1024, 2048, 4096, 1, 1, wsp, big, None) == L.GM_EINVAL
+assert lib.gm_moe_chain(None, 2, 1024, 2048, 4096, 1, 1, wsp, big, None) == L.GM_EINVAL
+assert lib.gm_moe_chain(arr, 2, 1024, 1024, 4096, 1, 1, wsp, big, None) == L.GM_EINVAL        # x aliases y
+assert lib.gm_moe_chain(arr, 2, 1024, 2048, None, 1, 1, wsp, big, None) == L.GM_EINVAL        # no buf
+assert lib.gm_moe_chain(arr, 2, 1024, 2048, 4104, 1, 1, wsp, big, None) == L.GM_EINVAL        # buf alignment
+assert lib.gm_moe_chain(arr, 2, 1024, 2048, 4096, 1, 1, wsp, small, None) == L.GM_EWORKSPACE
+assert lib.gm_moe_chain(arr, 2, 1024, 2048, 4096, 0, 1, wsp, big, None) == L.GM_OK             # T = 0
+mixed = (L.GmMoeLayer * 2)(layer(), layer(D=1024))
+assert lib.gm_moe_chain(mixed, 2, 1024, 2048, 4096, 1, 1, wsp, big, None) == L.GM_EINVAL
+assert "same" in L.last_error() or "D=" in L.last_error()
 print("asan child ok", n)
 '''
 
