@@ -15,6 +15,7 @@
 // struct: a struct load + store pair is turned into a memcpy by the optimiser,
 // which then issues every load right before its store.
 typedef float gm_f32x4 __attribute__((ext_vector_type(4)));
+typedef double gm_f64x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t gm_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t gm_u32x2 __attribute__((ext_vector_type(2)));
 

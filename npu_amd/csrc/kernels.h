@@ -42,9 +42,18 @@ struct GmMoeWs {
 };
 
 // T = 1 router accumulators (layout in moe_decode.h): GM_ACC_COPIES copies of
-// gm_acc_ld(E) doubles.
+// gm_acc_ld(E) doubles, each copy a whole number of 128-byte lines.  Word e < E
+// (expert e) sits at position MV (e % 64) + e / 64 (MV = 4 for E <= 256, else
+// 8), so that lane l of the selecting wave reads its words l, l + 64, ... as
+// MV consecutive doubles; words E (shared gate) and E + 1 (sum of squares)
+// follow at 64 MV and 64 MV + 1.
 constexpr int GM_ACC_COPIES = 8;
-inline int gm_acc_ld(int E) { return (E + 2 + 7) & ~7; }
+__host__ __device__ inline int gm_acc_mv(int E) { return E <= 256 ? 4 : 8; }
+__host__ __device__ inline int gm_acc_ld(int E) { return 64 * gm_acc_mv(E) + 16; }
+__host__ __device__ inline int gm_acc_pos(int e, int E) {
+  const int mv = gm_acc_mv(E);
+  return e < E ? mv * (e & 63) + (e >> 6) : 64 * mv + (e - E);
+}
 inline size_t gm_acc_bytes(int E) { return (size_t)GM_ACC_COPIES * gm_acc_ld(E) * sizeof(double); }
 
 // One layer of gm_moe_chain's T = 1 accumulator path: the router accumulators

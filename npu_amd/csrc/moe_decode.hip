@@ -125,8 +125,8 @@ __global__ void __launch_bounds__(128) k_dec_router1(gm_moe_layer P, const float
   GM_TL_MARK2(dot);
   if (acc != nullptr) {
     if (lane < GM_ACC_COPIES) {
-      if (r < nrows) acc[lane * acc_ld + row] = lane == 0 ? (double)dot : 0.0;
-      if (r == 0) acc[lane * acc_ld + E + 1] = lane == 0 ? (double)ss : 0.0;
+      if (r < nrows) acc[lane * acc_ld + gm_acc_pos(row, E)] = lane == 0 ? (double)dot : 0.0;
+      if (r == 0) acc[lane * acc_ld + gm_acc_pos(E + 1, E)] = lane == 0 ? (double)ss : 0.0;
     }
   } else if (r < nrows && lane == 0) {
     if (row < E) logits[row] = rms * dot + bias;

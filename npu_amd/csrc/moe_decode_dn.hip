@@ -161,8 +161,14 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   // the next layer's router columns r0 .. r0 + 7 (needed only at the end)
   gm_u32x4 nr0{}, nr1{};
   gm_f32x4 nwa{}, nwb{};
+  // thread tid adds the accumulator word at position tid (gm_acc_pos), so that a
+  // wave's atomics fall on consecutive words: word nw_e = 64 (tid % MV) + tid / MV
+  // below 64 MV, then E (shared gate row) and E + 1 (sum of squares)
+  const int mvn = gm_acc_mv(nx.E);
+  const int nw_e = tid < 64 * mvn ? 64 * (tid % mvn) + tid / mvn : nx.E + (tid - 64 * mvn);
+  const bool nw_live = tid < 64 * mvn ? nw_e < nx.E : nw_e <= nx.E + 1;
   if constexpr (NXT) {
-    const int t = tid <= nx.E ? tid : 0;
+    const int t = nw_e <= nx.E ? nw_e : 0;
     const int es = nx.f32 ? 4 : 2;
     const uint8_t* p = static_cast<const uint8_t*>(nx.w) + ((int64_t)blockIdx.x * (nx.E + 1) + t) * 8 * es;
     nr0 = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(p));
@@ -242,7 +248,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
   }
   if constexpr (NXT) {
     __syncthreads();
-    if (tid <= nx.E + 1) {
+    if (nw_live) {
       const float yv[8] = {s_y[0], s_y[1], s_y[2], s_y[3], s_y[4], s_y[5], s_y[6], s_y[7]};
       const float nv[8] = {nwa.x, nwa.y, nwa.z, nwa.w, nwb.x, nwb.y, nwb.z, nwb.w};
       float wv[8];
@@ -259,7 +265,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
         }
       }
       float p = 0.f;
-      if (tid <= nx.E) {
+      if (nw_e <= nx.E) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) p = fmaf(wv[i], yv[i] * nv[i], p);
       } else {

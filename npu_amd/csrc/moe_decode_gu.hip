@@ -202,30 +202,32 @@ __global__ void __launch_bounds__(576) k_dec_gateup1w(gm_moe_layer P, const floa
     }
   } else if (wave == 0) {
     __builtin_amdgcn_s_setprio(3);
-    // the copies of the lane's E / 64 words, of the shared gate word and of the
-    // sum of squares, loaded a batch of CB copies at a time (all 8 at E <= 256)
-    // before any is added; the copies are added in copy order
+    // the copies of the lane's words lane + 64 i (MAXV consecutive doubles, see
+    // gm_acc_pos), of the shared gate word and of the sum of squares, loaded a
+    // batch of CB copies at a time (all 8 at E <= 256) before any is added; the
+    // copies are added in copy order
+    static_assert(MAXV == 4 || MAXV == 8, "accumulator layout: MAXV = gm_acc_mv(E)");
     constexpr int CB = MAXV > 4 ? 4 : GM_ACC_COPIES;
     double sd[MAXV], ssd = 0.0, sgd = 0.0;
 #pragma unroll
     for (int c0 = 0; c0 < GM_ACC_COPIES; c0 += CB) {
-      double a[CB][MAXV], ag[CB], aq[CB];
+      gm_f64x2 a[CB][MAXV / 2], gq[CB];
 #pragma unroll
       for (int c = 0; c < CB; ++c) {
+        const gm_f64x2* cp = reinterpret_cast<const gm_f64x2*>(acc + (c0 + c) * acc_ld);
 #pragma unroll
-        for (int i = 0; i < MAXV; ++i) {
-          const int e = lane + 64 * i;
-          a[c][i] = acc[(c0 + c) * acc_ld + (e < E ? e : E - 1)];
-        }
-        ag[c] = acc[(c0 + c) * acc_ld + E];
-        aq[c] = acc[(c0 + c) * acc_ld + E + 1];
+        for (int i = 0; i < MAXV / 2; ++i) a[c][i] = cp[(MAXV / 2) * lane + i];
+        gq[c] = cp[32 * MAXV];                                    // words E, E + 1
       }
 #pragma unroll
       for (int c = 0; c < CB; ++c) {
-        ssd = c0 + c == 0 ? aq[c] : ssd + aq[c];
-        sgd = c0 + c == 0 ? ag[c] : sgd + ag[c];
+        sgd = c0 + c == 0 ? gq[c].x : sgd + gq[c].x;
+        ssd = c0 + c == 0 ? gq[c].y : ssd + gq[c].y;
 #pragma unroll
-        for (int i = 0; i < MAXV; ++i) sd[i] = c0 + c == 0 ? a[c][i] : sd[i] + a[c][i];
+        for (int i = 0; i < MAXV / 2; ++i) {
+          sd[2 * i] = c0 + c == 0 ? a[c][i].x : sd[2 * i] + a[c][i].x;
+          sd[2 * i + 1] = c0 + c == 0 ? a[c][i].y : sd[2 * i + 1] + a[c][i].y;
+        }
       }
       issue_fence();
     }

@@ -43,7 +43,7 @@ def algorithmic_bytes(d: int = D, ff: int = FF, e: int = E, k: int = K) -> dict[
     read once, outputs written once), for a block with IQ4_XS gate/up, IQ3_XXS down, the
     shared expert in the same formats, an RMSNorm weight and a shared scalar gate.  The
     router accumulators are 8 copies of e + 2 fp64 words (raw router dot products, the
-    shared gate's, the sum of x^2).
+    shared gate's, the sum of x^2) in runs of 4 x 64 + 16 words at e <= 256.
       k_dec_router1: router [e, d] bf16, shared scalar gate [d] bf16, x and the RMSNorm
         weight fp32; writes the 8 accumulator copies (copy 0 and zeros).
       k_dec_gateup1w: the k routed and the shared experts' gate and up rows, x and the
@@ -55,7 +55,7 @@ def algorithmic_bytes(d: int = D, ff: int = FF, e: int = E, k: int = K) -> dict[
         gate [e + 1, d] bf16 (router_t) and RMSNorm weight, and one fp64 atomic per
         accumulator word per block of 8 rows (d / 8 blocks)."""
     iq4_row, iq3_row = d // 256 * 136, ff // 256 * 98
-    acc = 8 * (e + 2) * 8
+    acc = 8 * (e + 2) * 8                      # the words read; the runs are padded to whole lines
     down = (k + 1) * d * iq3_row + (k + 1) * ff * 4 + k * 4 + 4 + d * 4 + d * 4
     return {
         "k_dec_router1": e * d * 2 + d * 2 + d * 4 + d * 4 + acc,
