@@ -85,21 +85,24 @@ def test_config5_chain_graph(gpu, chain, T):
 # gm_moe_chain: the same chains through the library's chain entry point.  At T = 1 each
 # layer's down kernel computes the next layer's router dot products (fp64 accumulators),
 # so this checks the routing of layers 1.. computed that way against the oracle.
-CHAIN_VARIANTS = {
-    "config5": dict(norm=True),
-    "f32_router_bias": dict(norm=True, router_f32=True, bias=True),
-    "no_norm_no_shared": dict(shared=False, layers=2),   # without RMSNorm activations grow fast per layer
-    "ungated_shared": dict(norm=True, ungated=True),
+CHAIN_VARIANTS = {                                        # name: (seed base, layer arguments)
+    "config5": (400, dict(norm=True)),
+    "f32_router_bias": (410, dict(norm=True, router_f32=True, bias=True)),
+    "no_norm_no_shared": (420, dict(shared=False, layers=2)),   # without RMSNorm activations grow fast
+    "ungated_shared": (430, dict(norm=True, ungated=True)),
+    "e512": (440, dict(norm=True, E=512)),                 # 8 accumulator words per lane
+    "d1280": (450, dict(norm=True, D=1280)),               # D not a multiple of 512
 }
 
 
 @pytest.fixture(scope="module", params=sorted(CHAIN_VARIANTS))
 def variant_chain(request, gpu):
-    kw = dict(CHAIN_VARIANTS[request.param])
+    seed, kw = CHAIN_VARIANTS[request.param]
+    kw = dict(kw)
     ungated = kw.pop("ungated", False)
     hosts = []
     for i in range(kw.pop("layers", N_LAYERS)):
-        h = synth.host_moe_layer(400 + 10 * sorted(CHAIN_VARIANTS).index(request.param) + i, **kw)
+        h = synth.host_moe_layer(seed + i, **kw)
         if ungated:
             h.sh_gate_inp = None
         hosts.append(h)
