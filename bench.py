@@ -53,6 +53,8 @@ def parse() -> argparse.Namespace:
                     help="only the per-stage graphs the roofline is measured on (for rocprof)")
     ap.add_argument("--chain-only", action="store_true", help="only the B=1 chain (for rocprof)")
     ap.add_argument("--matvec-only", action="store_true", help="only BASELINE configs 1-2 (quantised matvec)")
+    ap.add_argument("--quant-shapes", default=None,
+                    help="comma-separated subset of the configs 1-2 shapes for --matvec-only")
     ap.add_argument("--dense-shapes", default="ssm_in,ssm_gate,ssm_out", help="projections for --dense-only")
     ap.add_argument("--dense-tokens", default="1,8", help="token counts for --dense-only")
     return ap.parse_args()
@@ -109,6 +111,31 @@ def run_chain(layers, T: int, steps: int, warmup: int, seed: int):
     return ms, n_unique, finite
 
 
+def check_chain(layers):
+    """The headline workload's own output: one eager gm_moe_chain call from the timed input
+    against the same layers run one gm_moe_forward at a time.  Reports whether the chain ran
+    the accumulator-linked kernels, whether the top-k ids agree at every layer, and the
+    output's rel error (the logits are the same dot products added in another order)."""
+    import torch
+    from npu_amd import synth
+    from npu_amd.moe import GpuMoeChain
+    dev = layers[0].gate.device
+    x0 = torch.from_numpy(synth.host_input(SEED, 1, D, rmsnorm=False)).to(dev)
+    ch = GpuMoeChain(layers)
+    y = ch(x0, residual=True)
+    torch.cuda.synchronize()
+    ids_c = [blk.stages(1)["topk_ids"].clone() for blk in layers]
+    x = x0
+    same = True
+    for blk, ic in zip(layers, ids_c):
+        x = blk(x, residual=True)
+        same = same and bool(torch.equal(blk.stages(1)["topk_ids"], ic))
+    torch.cuda.synchronize()
+    rel = float((y.double() - x.double()).abs().max() / x.double().abs().max())
+    return {"fused_path": ch.fused(1), "ids_equal_every_layer": same, "rel_vs_per_layer": rel,
+            "finite": bool(torch.isfinite(y).all())}
+
+
 def time_stages(layers, T: int, reps: int = 20):
     """Average launch period of each decode stage kernel: one hipGraph per stage holding
     that stage's launch for every layer (distinct weights), replayed `reps` times between
@@ -141,23 +168,57 @@ def time_stages(layers, T: int, reps: int = 20):
     return out
 
 
-def roofline(layers, stages):
+def time_stage_launches(layers, T: int, stage: int = 2, batches: int = 10):
+    """Average launch duration of one decode stage's kernel, measured with HIP events on the
+    launch stream: each batch holds that stage's launch for every layer (distinct weights),
+    enqueued eagerly behind a spin kernel (torch.cuda._sleep) so that the host is ahead of
+    the GPU and the launches run back to back; two events bracket the batch, and the
+    duration is the batch time over its launches.  The first batch is a warm-up.  The
+    layers' workspaces are prepared by stage 1 alone (stage 2 reads only its results), so
+    every launch of the stage's kernel in a run of `bench.py --roofline-only` is a timed
+    one: rocprofv3's average duration for the kernel over that run covers the same
+    launches (the graph period of time_stages also holds the dependent-dispatch gap, and
+    under tracing its launches stretch)."""
+    import torch
+    from npu_amd import synth
+    dev = layers[0].gate.device
+    x = torch.from_numpy(synth.host_input(SEED + 1, T, D, rmsnorm=False)).to(dev)
+    y = torch.empty_like(x)
+    for blk in layers:
+        blk(x, residual=True, out=y, stage=1)
+    torch.cuda.synchronize()
+    periods = []
+    for _ in range(batches + 1):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(20_000_000)
+        e0.record()
+        for blk in layers:
+            blk(x, residual=True, out=y, stage=stage)
+        e1.record()
+        torch.cuda.synchronize()
+        periods.append(e0.elapsed_time(e1) * 1e3 / len(layers))
+    timed = periods[1:]
+    return sum(timed) / len(timed)
+
+
+def roofline(layers, launch_us: float, graph_period_us: float | None = None):
     """The dominant kernel, k_dec_gateup1w (top-k, routed and shared gate/up, SwiGLU, T = 1):
     its algorithmic bytes per launch (npu_amd.rocprof_summary.algorithmic_bytes: the k
-    routed and the shared experts' raw gate and up rows, the limb row of the normalised x,
-    the router logits, the k + 1 SwiGLU rows it writes) over the launch period measured by
-    time_stages."""
+    routed and the shared experts' raw gate and up rows, x and the RMSNorm weight, the
+    router accumulators, the logits and the k + 1 SwiGLU rows it writes) over its average
+    launch duration from time_stage_launches."""
     from npu_amd.rocprof_summary import algorithmic_bytes
     b = layers[0]
     n = algorithmic_bytes(D, FF, E, K_TOP)["k_dec_gateup1w"]
     assert b.gate[0].numel() == FF * (D // 256 * 136) and b.down[0].numel() == D * (FF // 256 * 98)
-    gbps = n / (stages["gateup_us"] * 1e-6) / 1e9
+    gbps = n / (launch_us * 1e-6) / 1e9
     return {"bound": "hbm", "kernel": "k_dec_gateup1w (top-k + routed and shared gate/up + SwiGLU, T=1)",
             "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": gbps / HBM_PEAK_GBPS,
-            "traffic": traffic_bytes("k_dec_gateup1w"), "bytes_per_launch": n, "avg_launch_us": stages["gateup_us"]}
+            "traffic": traffic_bytes("k_dec_gateup1w"), "bytes_per_launch": n, "avg_launch_us": launch_us,
+            "graph_period_us": graph_period_us}
 
 
-def run_prefill(layers, T: int = 512, n_blocks: int = 8, reps: int = 5):
+def run_prefill(layers, T: int = 512, n_blocks: int = 8, reps: int = 5, samples: dict | None = None):
     """BASELINE config 4 on the chain's first `n_blocks` layers (distinct weights, so the
     ~250 MB of experts one block touches does not stay in the Infinity Cache): a per-expert
     router bias ~ N(0,1) skews the routing, inputs are N(0,1) [T, D].  Reports the mean
@@ -175,6 +236,8 @@ def run_prefill(layers, T: int = 512, n_blocks: int = 8, reps: int = 5):
         for b in blocks:
             b.router_bias = torch.randn(E, generator=gen, device=dev, dtype=torch.float32)
             b.struct.router_bias = L.ptr(b.router_bias)
+        if samples is not None:                     # the CPU baseline's config-4 leg runs layer 0 with its bias
+            samples["prefill_bias"] = blocks[0].router_bias.cpu()
         x = torch.from_numpy(synth.host_input(SEED + 5, T, D, rmsnorm=False)).to(dev)
         y = torch.empty_like(x)
         for b in blocks:
@@ -285,7 +348,8 @@ QUANT_MV_SHAPES = (("config1_iq4xs_512x2048", 23, 512, 2048), ("config2_iq3xxs_2
                    ("config2_iq3xxs_512x2048", 18, 512, 2048))
 
 
-def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330):
+def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330, samples: dict | None = None,
+                 shapes=None):
     """BASELINE configs 1 and 2: one y = W x with W a raw IQ4_XS [512 x 2048] or IQ3_XXS
     [2048 x 512] / [512 x 2048] matrix (the reference's NpuIQ4MatVec / NpuQuantMatVec
     call, npu/quant_mv.py:419-463), fp32 x ~ N(0, 1), seeded device-generated
@@ -302,6 +366,8 @@ def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330):
     lib = L.lib()
     out = {}
     for name, qt, M, K in QUANT_MV_SHAPES:
+        if shapes is not None and name not in shapes:
+            continue
         rb = (K // 256) * (136 if qt == 23 else 98)
         n = max(batch, (total_mb << 20) // (M * rb) // batch * batch)
         W = synth.device_quant_matrix(gen, qt, M, K, n, dev)                  # [n, M, rb] uint8
@@ -343,6 +409,8 @@ def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330):
         ref = Wd @ x.double()
         rel = float((y[n - 1].double() - ref).abs().max() / ref.abs().max())
         same = bool(torch.equal(yb.view(n, M), y))
+        if samples is not None:                     # the CPU baseline's leg: the last matrix and x
+            samples.setdefault("quant_mv", {})[name] = (qt, M, K, W[n - 1].cpu().numpy(), x.cpu().numpy())
         algo = M * rb + K * 4 + M * 4
         out[name] = {"M": M, "K": K, "distinct_matrices": n, "resident_MB": n * M * rb / 2**20,
                      "algorithmic_bytes_per_call": algo,
@@ -356,30 +424,73 @@ def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330):
     return out
 
 
-def cpu_baseline(layers, n_sample: int, budget_s: float = 12.0):
-    """The oracle (a port of the CPU branch of qwen/forward.py:moe_forward) on a bounded
-    sample: the first `n_sample` blocks of the chain, B=1, run back to back (each output
-    feeding the next block) for about `budget_s` seconds; the median per-block time is
-    scaled to the 40-block step.  Per-call dequant of every picked expert, as the
-    reference's dequant_one does; a second, shorter pass times the same blocks with those
-    experts dequantised up front (the CPU's best case)."""
+def _median_ms(fn, runs: int = 5, warmup: int = 2) -> tuple[float, int]:
+    """Median wall time of ``fn`` in ms over ``runs`` timed calls after ``warmup`` untimed
+    ones (time.perf_counter_ns), and the number of timed calls."""
     import statistics
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter_ns()
+        fn()
+        times.append((time.perf_counter_ns() - t0) * 1e-6)
+    return statistics.median(times), runs
+
+
+def _host_layers(layers):
     import numpy as np
-    import torch
     from npu_amd import synth
     from oracle import moe as OM
-
-    threads = cpu_share()
-    torch.set_num_threads(threads)
-    hosts = []
-    for blk in layers[:n_sample]:
+    out = []
+    for blk in layers:
         h = synth.HostMoeLayer(
             D=D, FF=FF, E=E, k=K_TOP, q_gate=blk.q_gate, q_down=blk.q_down,
             gate=blk.gate.cpu().numpy(), up=blk.up.cpu().numpy(), down=blk.down.cpu().numpy(),
             router=blk.router.cpu().numpy().view(np.uint16), gate_sh=blk.gate_sh.cpu().numpy(),
             up_sh=blk.up_sh.cpu().numpy(), down_sh=blk.down_sh.cpu().numpy(),
             sh_gate_inp=blk.sh_gate_inp.cpu().numpy().view(np.uint16), norm_w=blk.norm_w.cpu().numpy())
-        hosts.append(OM.OracleLayer(h))
+        out.append(OM.OracleLayer(h))
+    return out
+
+
+def _pre_dequant(hosts, x0, T_residual=True):
+    """Per layer, the experts one pass from x0 routes to (and the shared expert), dequantised."""
+    import torch
+    from oracle import moe as OM
+    pre, y = [], x0
+    for L in hosts:
+        st = {}
+        y_next = OM.block_forward(y, L, residual=T_residual, stages=st)
+        d = {int(e): L.dequant_one(int(e)) for e in torch.unique(st["topk_ids"]).tolist()}
+        d["shared"] = L.shared_weights()
+        pre.append(d)
+        y = y_next
+    return pre
+
+
+def cpu_baseline(layers, n_sample: int, budget_s: float = 12.0, prefill_bias=None, quant_mv=None):
+    """The reference's CPU path, restated by the oracle (a port of qwen/forward.py:moe_forward's
+    CPU branch, 652-663, and of the dequant + F.linear of the quantised operators), timed on
+    this host's cores beside the GPU figures.  Headline (config 5, B = 1): the first
+    `n_sample` blocks of the chain run back to back (each output feeding the next block) for
+    about `budget_s` seconds, the median per-block time scaled to the 40-block step, with
+    per-call dequant of every picked expert as dequant_one does, and again with those experts
+    dequantised up front (the CPU's best case).  ``configs`` holds the other BASELINE configs,
+    each the median of 5 runs after 2 warm-ups in both variants: 1 and 2 (one quantised
+    matvec, dequant + F.linear), 3 (one block at T = 1), 4 (one block at T = 512 with the
+    bench's router bias) and 5 at B = 8 (4 chained blocks)."""
+    import statistics
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+    from npu_amd import synth
+    from oracle import moe as OM
+    from oracle import quants as Q
+
+    threads = cpu_share()
+    torch.set_num_threads(threads)
+    hosts = _host_layers(layers[:n_sample])
     x0 = torch.from_numpy(synth.host_input(SEED, 1, D, rmsnorm=False))
     for _ in range(2):                                      # two untimed warm-up passes over the sample
         y = x0
@@ -397,26 +508,76 @@ def cpu_baseline(layers, n_sample: int, budget_s: float = 12.0):
         return times, time.perf_counter() - t_start
 
     t_call, wall_call = passes(None, budget_s)
-    # pre-dequantised variant: the experts the sample routes to, plus the shared expert
-    pre, y = [], x0
-    for L in hosts:
-        st = {}
-        y_next = OM.block_forward(y, L, residual=True, stages=st)
-        d = {int(e): L.dequant_one(int(e)) for e in torch.unique(st["topk_ids"]).tolist()}
-        d["shared"] = L.shared_weights()
-        pre.append(d)
-        y = y_next
-    t_pre, wall_pre = passes(pre, budget_s / 4)
+    t_pre, wall_pre = passes(_pre_dequant(hosts, x0), budget_s / 4)
     per_block = statistics.median(t_call)
+    per_block_pre = statistics.median(t_pre)
+    blk_bytes = layers[0].weight_bytes_per_token()          # k experts + shared + router + shared gate
+    configs = {"config3_block_T1": {
+        "per_call_dequant_ms": per_block * 1e3, "pre_dequantised_ms": per_block_pre * 1e3,
+        "effective_weight_GBps": blk_bytes / per_block / 1e9,
+        "sample": f"the headline sample's per-block median ({len(t_call)} passes of {n_sample} blocks)"}}
+
+    # configs 1 and 2: one quantised matvec, dequant + F.linear (and F.linear on the fp32 matrix)
+    if quant_mv is not None:
+        for name, (qt, M, K, raw, x) in quant_mv.items():
+            x_t = torch.from_numpy(x)
+            def per_call():
+                F.linear(x_t, torch.from_numpy(Q.dequant_matrix(raw, qt, M, K)))
+            Wf = torch.from_numpy(Q.dequant_matrix(raw, qt, M, K))
+            ms_call, n = _median_ms(per_call, runs=21)
+            ms_pre, _ = _median_ms(lambda: F.linear(x_t, Wf), runs=21)
+            algo = raw.size + 4 * (K + M)
+            configs[name] = {"per_call_dequant_ms": ms_call, "pre_dequantised_ms": ms_pre,
+                             "effective_GBps": algo / (ms_call * 1e-3) / 1e9, "runs": n,
+                             "sample": "one matrix of the GPU leg's set, its x"}
+
+    # config 4: one block at T = 512, router bias ~ N(0, 1) (the GPU leg's first layer and bias)
+    if prefill_bias is not None:
+        L0 = hosts[0]
+        L4 = OM.OracleLayer(L0.h)
+        L4.bias = prefill_bias.float().cpu()
+        xp = torch.from_numpy(synth.host_input(SEED + 5, 512, D, rmsnorm=False))
+        st = {}
+        OM.block_forward(xp, L4, stages=st)
+        uniq = torch.unique(st["topk_ids"]).tolist()
+        ms_call, n = _median_ms(lambda: OM.block_forward(xp, L4))
+        pre4 = {int(e): L4.dequant_one(int(e)) for e in uniq}
+        pre4["shared"] = L4.shared_weights()
+        ms_pre, _ = _median_ms(lambda: OM.block_forward(xp, L4, pre_dequant=pre4))
+        per_exp = layers[0].gate[0].numel() + layers[0].up[0].numel() + layers[0].down[0].numel()
+        wb = len(uniq) * per_exp + blk_bytes - K_TOP * per_exp
+        configs["config4_prefill_T512"] = {
+            "per_call_dequant_ms": ms_call, "pre_dequantised_ms": ms_pre, "tokens_per_s": 512 / (ms_call * 1e-3),
+            "pre_dequantised_tokens_per_s": 512 / (ms_pre * 1e-3), "unique_experts": len(uniq),
+            "effective_weight_GBps": wb / (ms_call * 1e-3) / 1e9, "runs": n,
+            "sample": "layer 0 with the GPU leg's router bias, x = N(0, 1) [512, 2048]"}
+
+    # config 5 at B = 8: 4 chained blocks, per-block median scaled to the 40-block step
+    h8 = hosts[:4]
+    x8 = torch.from_numpy(synth.host_input(SEED + 8, 8, D, rmsnorm=False))
+
+    def chain8(pre=None):
+        y = x8
+        for i, L in enumerate(h8):
+            y = OM.block_forward(y, L, residual=True, pre_dequant=None if pre is None else pre[i])
+    ms_call, n = _median_ms(chain8)
+    pre8 = _pre_dequant(h8, x8)
+    ms_pre, _ = _median_ms(lambda: chain8(pre8))
+    step_ms = ms_call / len(h8) * N_LAYERS
+    configs["config5_b8"] = {"per_call_dequant_step_ms": step_ms, "tokens_per_s": 8 / (step_ms * 1e-3),
+                             "pre_dequantised_step_ms": ms_pre / len(h8) * N_LAYERS,
+                             "pre_dequantised_tokens_per_s": 8 / (ms_pre / len(h8) * N_LAYERS * 1e-3),
+                             "runs": n, "sample": f"{len(h8)} chained config-5 blocks, B = 8, x {N_LAYERS} / {len(h8)}"}
     return {
         "value": 1.0 / (per_block * N_LAYERS), "unit": "tokens/s", "cores": threads, "kind": "port",
         "sample": (f"oracle restatement of moe_forward, B=1: {n_sample} chained config-5 blocks x {len(t_call)} "
                    f"passes ({wall_call:.1f} s), median per-block time x {N_LAYERS} blocks; per-call dequant "
                    f"of each picked expert (numpy) + torch fp32 F.linear, {threads} threads"),
         "block_ms": per_block * 1e3,
-        "pre_dequantised_block_ms": statistics.median(t_pre) * 1e3,
-        "pre_dequantised_tokens_per_s": 1.0 / (statistics.median(t_pre) * N_LAYERS),
+        "pre_dequantised_block_ms": per_block_pre * 1e3,
+        "pre_dequantised_tokens_per_s": 1.0 / (per_block_pre * N_LAYERS),
         "cpu": cpu_model(), "os_cpu_count": os.cpu_count(), "warmup_passes": 2,
+        "configs": configs,
     }
 
 
@@ -491,13 +652,14 @@ def main() -> int:
                                                    tokens=[int(t) for t in args.dense_tokens.split(",")])}))
         return 0
     if args.matvec_only:
-        print(json.dumps({"quant_mv": run_quant_mv(dev)}))
+        shapes = None if args.quant_shapes is None else args.quant_shapes.split(",")
+        print(json.dumps({"quant_mv": run_quant_mv(dev, shapes=shapes)}))
         return 0
     if args.roofline_only:
         layers = build_layers(args.layers, dev)
         torch.cuda.synchronize()
-        stages = time_stages(layers, 1)
-        print(json.dumps({"roofline": roofline(layers, stages), "stage_us": stages}))
+        launch_us = time_stage_launches(layers, 1)
+        print(json.dumps({"roofline": roofline(layers, launch_us)}))
         return 0
     if args.chain_only:
         layers = build_layers(args.layers, dev)
@@ -532,10 +694,12 @@ def main() -> int:
     eff_gbps = bytes1 / (ms1 * 1e-3) / 1e9
     log(f"B=1: {ms1 * 1e3:.1f} us/step, {tok_s:.1f} tok/s, {eff_gbps:.1f} GB/s effective, finite={ok1}")
 
+    chain_ok = check_chain(layers)
+    log(f"40-layer chain vs per-layer gm_moe_forward: {chain_ok}")
     stages = time_stages(layers, 1)
     log(f"stages (us): {stages}")
 
-    extra = {}
+    extra, samples = {}, {}
     if not args.no_extra:
         ms8, nu8, ok8 = run_chain(layers, 8, max(20, args.steps // 4), max(2, args.warmup // 4), SEED + 8)
         bytes8 = sum(n * per_expert + fixed for n in nu8)
@@ -543,17 +707,18 @@ def main() -> int:
                            "effective_weight_GBps": bytes8 / (ms8 * 1e-3) / 1e9,
                            "mean_unique_experts_per_layer": sum(nu8) / len(nu8), "finite": ok8}
         log(f"B=8: {extra['batch8']}")
-        extra["prefill"] = run_prefill(layers)
+        extra["prefill"] = run_prefill(layers, samples=samples)
         log(f"prefill: {extra['prefill']}")
         extra["dense_mv"] = run_dense_mv(dev)
         log(f"dense bf16 matvec: {extra['dense_mv']}")
-        extra["quant_mv"] = run_quant_mv(dev)
+        extra["quant_mv"] = run_quant_mv(dev, samples=samples)
         log(f"quant matvec (configs 1-2): {extra['quant_mv']}")
 
     cpu = None
     if not args.no_cpu_baseline:
         log(f"CPU baseline: {args.cpu_layers} blocks of the oracle")
-        cpu = cpu_baseline(layers, args.cpu_layers)
+        cpu = cpu_baseline(layers, args.cpu_layers, prefill_bias=samples.get("prefill_bias"),
+                           quant_mv=samples.get("quant_mv"))
         log(f"CPU: {cpu}")
 
     out = {
@@ -569,10 +734,11 @@ def main() -> int:
         "effective_weight_frac_of_peak": eff_gbps / HBM_PEAK_GBPS,
         "block_us": ms1 * 1e3 / args.layers,
         "weight_bytes_per_step": bytes1,
-        "roofline": roofline(layers, stages),
+        "roofline": roofline(layers, time_stage_launches(layers, 1), stages["gateup_us"]),
         "stage_us": stages,
         "cpu_baseline": cpu,
         "finite": ok1,
+        "chain_check": chain_ok,
     }
     out.update(extra)
     print(json.dumps(out))

@@ -227,6 +227,16 @@ int gm_moe_forward_stage(const gm_moe_layer* L, const float* x, float* y, int T,
 int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float* y, float* buf, int T,
                  int flags, void* const* ws, const size_t* ws_bytes, void* stream);
 
+/*
+ * Which path gm_moe_chain takes for these layers and T, without running it:
+ * 1 = the accumulator-linked T = 1 kernels (one router launch, then two
+ * launches per layer), 0 = one gm_moe_forward per layer, negative = a
+ * rejected layer (GM_E*).  No counterpart in the reference (its decoder loop
+ * runs one block at a time); for callers and tests that must know the fast
+ * path is the one that runs.
+ */
+int gm_moe_chain_fused(const gm_moe_layer* layers, int n_layers, int T);
+
 /* Size of the static scratch gm_moe_forward_noalloc works in: 16 MiB per GPU. */
 #define GM_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
 
@@ -240,7 +250,9 @@ int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float
  * results as gm_moe_forward.  Returns GM_EWORKSPACE when
  * gm_moe_workspace_bytes(L, T) > GM_NOALLOC_SCRATCH_BYTES (config 5: T <= 8
  * needs 1.7 MiB, prefill fits up to T = 111).  stream must belong to the
- * current device.  All calls on one GPU share that GPU's array, which keeps
+ * current device.  The first call on each device resolves the array's address
+ * (hipGetSymbolAddress, which may load the code object) and so must happen
+ * outside stream capture; later calls may be captured.  All calls on one GPU share that GPU's array, which keeps
  * the last call's contents: calls that overlap on one GPU (other streams,
  * other threads) race and must be serialised by the caller.
  */

@@ -77,6 +77,7 @@ SIGNATURES = {
     "gm_moe_prefill": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _i32, _vp, _sz, _vp]),
     "gm_moe_chain": (_i32, [ctypes.POINTER(GmMoeLayer), _i32, _vp, _vp, _vp, _i32, _i32,
                             ctypes.POINTER(_vp), ctypes.POINTER(_sz), _vp]),
+    "gm_moe_chain_fused": (_i32, [ctypes.POINTER(GmMoeLayer), _i32, _i32]),
 }
 
 _LIB: ctypes.CDLL | None = None
@@ -93,7 +94,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(h, name)
             fn.restype = res
             fn.argtypes = args
-        if h.gm_abi_version() != 4:
+        if h.gm_abi_version() != 5:
             raise RuntimeError("libnpu_amd.so ABI version mismatch; rebuild it")
         _LIB = h
     return _LIB

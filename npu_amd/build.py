@@ -70,10 +70,11 @@ def asan_runtime() -> str | None:
     return None
 
 
-def build(verbose: bool = False, timeline: bool = False, asan: bool = False) -> Path:
+def build(verbose: bool = False, timeline: bool = False, asan: bool = False, incremental: bool = False) -> Path:
     """Compile every source to an object in parallel, then link the library
     (the timestamped profiling variant when ``timeline``, the host-only ASan
-    variant when ``asan``)."""
+    variant when ``asan``).  ``incremental`` recompiles only the objects older
+    than their source or any header."""
     objdir = HERE / ("_build_tl" if timeline else "_build_asan" if asan else "_build")
     objdir.mkdir(exist_ok=True)
     inc = ["-I", str(HERE.parent / "include")]
@@ -82,8 +83,18 @@ def build(verbose: bool = False, timeline: bool = False, asan: bool = False) -> 
         compile_flags = compile_flags + ASAN_FLAGS
     out_lib = LIB_TL if timeline else LIB_ASAN if asan else LIB
 
+    headers = [*CSRC.glob("*.h"), *(HERE.parent / "include").glob("*.h")]
+
+    def fresh(obj: Path, src: Path) -> bool:
+        if not (incremental and obj.exists()):
+            return False
+        t = obj.stat().st_mtime
+        return all(d.stat().st_mtime <= t for d in (src, *headers))
+
     def compile_one(src: str):
         obj = objdir / (Path(src).stem + ".o")
+        if fresh(obj, CSRC / src):
+            return obj, subprocess.CompletedProcess([], 0, "", "")
         cmd = [hipcc(), *compile_flags, *inc, "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
@@ -108,4 +119,5 @@ def build(verbose: bool = False, timeline: bool = False, asan: bool = False) -> 
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv, timeline="--timeline" in sys.argv, asan="--asan" in sys.argv))
+    print(build(verbose="-v" in sys.argv, timeline="--timeline" in sys.argv, asan="--asan" in sys.argv,
+                incremental="--incremental" in sys.argv))

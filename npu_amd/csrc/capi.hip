@@ -95,7 +95,7 @@ extern "C" {
 
 const char* gm_last_error(void) { return g_err; }
 
-int gm_abi_version(void) { return 4; }
+int gm_abi_version(void) { return 5; }
 
 int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out, void* stream) {
   if (gm_kquant_block(qtype).bytes)
@@ -229,6 +229,23 @@ int gm_moe_forward_stage(const gm_moe_layer* L, const float* x, float* y, int T,
 // products into accumulators in that layer's workspace (buffer l % 2, cleared
 // by layer l - 1's gate/up kernel): two launches per layer instead of three.
 // Otherwise every layer runs as gm_moe_forward.
+// Whether layer l of a T-token chain can run on the accumulator-linked kernels.
+static bool chain_layer_fused(const gm_moe_layer* layers, int l, int T) {
+  const gm_moe_layer* L = layers + l;
+  return T == 1 && L->E == layers[0].E && L->D <= 4096 && L->FF <= 2048 && L->k <= 8 && gm_dec_chain_ok(L) &&
+         (l == 0 || L->router_t != nullptr);
+}
+
+int gm_moe_chain_fused(const gm_moe_layer* layers, int n_layers, int T) {
+  if (!layers || n_layers < 1 || T < 0) return gm_fail_arg("gm_moe_chain_fused: bad arguments");
+  bool fused = true;
+  for (int l = 0; l < n_layers; ++l) {
+    if (int rc = check_layer(layers + l)) return rc;
+    fused = fused && chain_layer_fused(layers, l, T);
+  }
+  return fused ? 1 : 0;
+}
+
 int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float* y, float* buf, int T, int flags,
                  void* const* ws, const size_t* ws_bytes, void* stream) {
   if (!layers || !ws || !ws_bytes) return gm_fail_arg("gm_moe_chain: NULL layers or workspace array");
@@ -249,8 +266,7 @@ int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float
     const size_t need = gm_moe_ws_layout(L, T).total;
     if (ws_bytes[l] < need)
       return gm_fail_arg("gm_moe_chain: workspace %d has %zu bytes < %zu needed", l, ws_bytes[l], need), GM_EWORKSPACE;
-    fused = fused && L->E == layers[0].E && L->D <= 4096 && L->FF <= 2048 && L->k <= 8 && gm_dec_chain_ok(L) &&
-            (l == 0 || L->router_t != nullptr);
+    fused = fused && chain_layer_fused(layers, l, T);
     if (L->router_t && reinterpret_cast<uintptr_t>(L->router_t) % 16)
       return gm_fail_arg("gm_moe_chain: layer %d router_t must be 16-byte aligned", l);
   }

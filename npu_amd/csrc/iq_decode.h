@@ -17,16 +17,59 @@ constexpr uint32_t kGmKv[4] = {GM_IQ4NL_PACKED_INIT};
 #define GM_KV2 kGmKv[2]
 #define GM_KV3 kGmKv[3]
 
-// Four IQ4 nibbles (one per byte, values 0..15) -> four int8 kvalues.
-// v_perm_b32 picks bytes from an 8-byte pool, so the 16-entry table is
-// looked up as two 8-entry halves and bit 3 of each nibble selects the half.
-__device__ __forceinline__ uint32_t gm_iq4nl_lut4(uint32_t nib) {
-  const uint32_t sel = nib & 0x07070707u;
-  const uint32_t lo = __builtin_amdgcn_perm(GM_KV1, GM_KV0, sel);
-  const uint32_t hi = __builtin_amdgcn_perm(GM_KV3, GM_KV2, sel);
-  const uint32_t pick = ((nib >> 1) & 0x04040404u) | 0x03020100u;
-  return __builtin_amdgcn_perm(hi, lo, pick);
+// Four IQ4 nibbles (one per byte, values 0..15) -> four int8 kvalues, in two
+// v_perm_b32 lookups and an XOR.  v_perm_b32 picks bytes 0..7 of an 8-byte
+// pool for selector bytes 0..7 and returns fixed bytes for the others: 8..11
+// the sign of pool byte 1, 3, 5, 7 spread to 0x00 / 0xff, 12 zero, >= 13
+// 0xff.  With selector n the pool P answers nibbles n < 8 and gives such a
+// fixed byte f(n) for n >= 8; with selector n ^ 8 the pool Q answers n >= 8
+// and gives a fixed byte g(n) for n < 8.  So P[n] = kv[n] ^ g(n) and
+// Q[n - 8] = kv[n] ^ f(n) make perm(P, n) ^ perm(Q, n ^ 8) = kv[n] for every
+// n.  f reads the signs of P[1, 3, 5, 7] and g those of Q[1, 3, 5, 7]; the
+// entries are solved in dependency order below (those with a constant f or g
+// first) and the result is checked for all 16 nibbles at compile time.
+namespace gm_iq4_xor {
+struct Tabs { uint32_t p0, p1, q0, q1; };
+
+// Table entry n of a 16-byte table given as 4 words (entry n in byte n % 4 of word n / 4).
+constexpr uint32_t entry(const uint32_t (&t)[4], int n) { return (t[n >> 2] >> (8 * (n & 3))) & 0xffu; }
+constexpr uint32_t sgn(uint32_t b) { return (b & 0x80u) ? 0xffu : 0u; }
+
+constexpr Tabs solve(const uint32_t (&t)[4]) {
+  // fixed bytes with constant selectors: g(4) = 0, g(5..7) = ff; f(12) = 0, f(13..15) = ff
+  const uint32_t P4 = entry(t, 4), P5 = entry(t, 5) ^ 0xffu, P6 = entry(t, 6) ^ 0xffu, P7 = entry(t, 7) ^ 0xffu;
+  const uint32_t Q4 = entry(t, 12), Q5 = entry(t, 13) ^ 0xffu, Q6 = entry(t, 14) ^ 0xffu, Q7 = entry(t, 15) ^ 0xffu;
+  // g(n) = sign of Q[2n + 1] for n < 4, f(n) = sign of P[2(n - 8) + 1] for 8 <= n < 12
+  const uint32_t P3 = entry(t, 3) ^ sgn(Q7), P2 = entry(t, 2) ^ sgn(Q5);
+  const uint32_t Q3 = entry(t, 11) ^ sgn(P7), Q2 = entry(t, 10) ^ sgn(P5);
+  const uint32_t P1 = entry(t, 1) ^ sgn(Q3), Q1 = entry(t, 9) ^ sgn(P3);
+  const uint32_t P0 = entry(t, 0) ^ sgn(Q1), Q0 = entry(t, 8) ^ sgn(P1);
+  return Tabs{P0 | P1 << 8 | P2 << 16 | P3 << 24, P4 | P5 << 8 | P6 << 16 | P7 << 24,
+              Q0 | Q1 << 8 | Q2 << 16 | Q3 << 24, Q4 | Q5 << 8 | Q6 << 16 | Q7 << 24};
 }
+
+// v_perm_b32 on one selector byte, as the ISA defines it (pool bytes 0-3 = lo, 4-7 = hi).
+constexpr uint32_t perm_byte(uint32_t hi, uint32_t lo, uint32_t sel) {
+  const uint64_t pool = (uint64_t)hi << 32 | lo;
+  return sel >= 13 ? 0xffu : sel == 12 ? 0u
+       : sel >= 8 ? (((pool >> (8 * (2 * (sel - 8) + 1) + 7)) & 1u) ? 0xffu : 0u)
+                  : (uint32_t)((pool >> (8 * sel)) & 0xffu);
+}
+constexpr bool check(const uint32_t (&t)[4], Tabs x) {
+  for (uint32_t n = 0; n < 16; ++n)
+    if ((perm_byte(x.p1, x.p0, n) ^ perm_byte(x.q1, x.q0, n ^ 8u)) != entry(t, (int)n)) return false;
+  return true;
+}
+constexpr Tabs kKv = solve(kGmKv);
+static_assert(check(kGmKv, kKv), "IQ4 XOR lookup tables do not reproduce kvalues_iq4nl");
+}  // namespace gm_iq4_xor
+
+// Lookup of four nibbles in a 16-entry byte table through its solved pools.
+__device__ __forceinline__ uint32_t gm_lut16_xor(gm_iq4_xor::Tabs t, uint32_t nib) {
+  return __builtin_amdgcn_perm(t.p1, t.p0, nib) ^ __builtin_amdgcn_perm(t.q1, t.q0, nib ^ 0x08080808u);
+}
+
+__device__ __forceinline__ uint32_t gm_iq4nl_lut4(uint32_t nib) { return gm_lut16_xor(gm_iq4_xor::kKv, nib); }
 
 __device__ __forceinline__ float gm_sbyte(uint32_t v, int i) {
   return (float)(int)(int8_t)(uint8_t)(v >> (8 * i));

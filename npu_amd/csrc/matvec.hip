@@ -287,26 +287,64 @@ static int launch_matvec_l(const uint8_t* w, int M, int K, const float* x, int n
 }
 
 // One token (BASELINE configs 1 and 2, the reference's NpuQuantMatVec /
-// NpuIQ4MatVec call, npu/quant_mv.py:419-463): LR lanes per row, 64 / LR rows
-// per wave.  Every thread first loads its 8 values of x per 2048-wide pass,
-// then every lane issues the loads of all SPL sub-blocks of its row, so the
-// wait for x (vmcnt retires in issue order) never waits for weights; the
-// block converts x into the int8-limb row in LDS while the weights are in
-// flight, then multiplies on v_dot4_i32_i8 as the MoE decode kernels do.
+// NpuIQ4MatVec call, npu/quant_mv.py:419-463).  LR lanes per row, so a wave
+// covers G = 64 / LR rows per row group, and each wave takes RPW row groups:
+// a block of 4 waves computes 4 RPW G rows.  Every thread first loads its 8
+// values of x per 2048-wide pass, then every lane issues the loads of all
+// RPW x SPL sub-blocks it multiplies (sub-blocks lir + LR i of each of its
+// RPW rows), so the wait for x (vmcnt retires in issue order) never waits
+// for weights and every row's bytes are in flight at once.  While they
+// arrive the block converts x into the int8-limb row in LDS; then each lane
+// reads the limbs of a sub-block once and multiplies them with that
+// sub-block of all RPW rows on v_dot4_i32_i8 (the MoE decode kernels'
+// arithmetic).  RPW > 1 amortises the x load and its conversion over RPW
+// times the weight bytes (a batched launch of many matrices has thousands
+// of blocks, each of which used to convert x for 4 rows).
 constexpr int kMv1MaxK = 8192;
 
-template <int QT, int LR, int SPL>
+// The three limb planes and the scale of one activation sub-block (LDS).
+struct GmLimbSub {
+  uint32_t l0[8], l1[8], l2[8];
+  float scale;
+};
+
+__device__ __forceinline__ void gm_read_limb_sub(const uint8_t* __restrict__ s, GmLimbSub& a) {
+  const gm_u32x4* p = reinterpret_cast<const gm_u32x4*>(s);
+  const gm_u32x4 v[6] = {p[0], p[1], p[2], p[3], p[4], p[5]};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    a.l0[4 * h] = v[h].x; a.l0[4 * h + 1] = v[h].y; a.l0[4 * h + 2] = v[h].z; a.l0[4 * h + 3] = v[h].w;
+    a.l1[4 * h] = v[2 + h].x; a.l1[4 * h + 1] = v[2 + h].y; a.l1[4 * h + 2] = v[2 + h].z; a.l1[4 * h + 3] = v[2 + h].w;
+    a.l2[4 * h] = v[4 + h].x; a.l2[4 * h + 1] = v[4 + h].y; a.l2[4 * h + 2] = v[4 + h].z; a.l2[4 * h + 3] = v[4 + h].w;
+  }
+  a.scale = *reinterpret_cast<const float*>(s + 96);
+}
+
+// sum_k w_k a_k of 32 int8 weights against one limb sub-block, before scales.
+__device__ __forceinline__ float gm_dot_limb_sub(const uint32_t (&w)[8], const GmLimbSub& a) {
+  int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    s0 = __builtin_amdgcn_sdot4((int)w[c], (int)a.l0[c], s0, false);
+    s1 = __builtin_amdgcn_sdot4((int)w[c], (int)a.l1[c], s1, false);
+    s2 = __builtin_amdgcn_sdot4((int)w[c], (int)a.l2[c], s2, false);
+  }
+  return fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0));
+}
+
+template <int QT, int LR, int SPL, int RPW>
 __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int M, int K, int64_t rb,
                                               const float* __restrict__ x, float* __restrict__ y) {
   using namespace gm_moe;
   constexpr int NXP = kMv1MaxK / 2048;                           // passes of 8 values per thread
+  constexpr int G = 64 / LR;                                     // rows per row group of a wave
   constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
   extern __shared__ float smem[];                                  // the limb row, then the IQ3 tables
   const int nsub = K / GM_SUB, rbytes = gm_limb_row_bytes(K);
   uint8_t* xs = reinterpret_cast<uint8_t*>(smem);
   Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(xs + rbytes);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane % LR;
-  const int row = (blockIdx.x * 4 + wave) * (64 / LR) + lane / LR;
+  const int row0 = (blockIdx.x * 4 + wave) * (RPW * G) + lane / LR;  // row of group j: row0 + G j
   gm_f32x4 xa[NXP], xb[NXP];
 #pragma unroll
   for (int p = 0; p < NXP; ++p) {
@@ -317,8 +355,12 @@ __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int
   }
   uint32_t gw = 0;
   if constexpr (IQ3) gw = gm_iq3_tab_load();
-  RowFetch<QT, SPL> f;
-  fetch_subs<QT, LR, SPL, true>(f, w + (int64_t)(row < M ? row : M - 1) * rb, lir, nsub);
+  RowFetch<QT, SPL> f[RPW];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    const int row = row0 + G * j;
+    fetch_subs<QT, LR, SPL, true>(f[j], w + (int64_t)(row < M ? row : M - 1) * rb, lir, nsub);
+  }
   issue_fence();
 #pragma unroll
   for (int p = 0; p < NXP; ++p) {
@@ -327,32 +369,64 @@ __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int
   }
   if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
   __syncthreads();
-  const int tok[1] = {0};
-  float acc[1] = {0.f};
-  dot_subs_i8<QT, LR, SPL, 1>(f, lir, nsub, xs, rbytes, tok, 1, tab, acc);
-  const float v = row_sum<LR>(acc[0]);
-  if (row < M && lir == 0) y[row] = v;
+  float acc[RPW];
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) acc[j] = 0.f;
+#pragma unroll
+  for (int i = 0; i < SPL; ++i) {
+    const int sub = lir + LR * i;
+    if (sub < nsub) {
+      GmLimbSub a;
+      gm_read_limb_sub(xs + sub * GM_LSUB, a);
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) {
+        uint32_t wq[8];
+        const float ws = gm_decode_i8<QT>(f[j].r[i], sub, tab, wq);
+        acc[j] = fmaf(ws * a.scale, gm_dot_limb_sub(wq, a), acc[j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < RPW; ++j) {
+    const float v = row_sum<LR>(acc[j]);
+    const int row = row0 + G * j;
+    if (row < M && lir == 0) y[row] = v;
+  }
 }
 
-template <int QT, int LR, int SPL>
+template <int QT, int LR, int SPL, int RPW>
 static int launch_mv1q_t(const uint8_t* w, int M, int K, const float* x, float* y, hipStream_t s) {
-  const int rows_per_block = 4 * (64 / LR);
+  const int rows_per_block = 4 * RPW * (64 / LR);
   const size_t smem = (size_t)gm_moe::gm_limb_row_bytes(K) + sizeof(Iq3Tab);
-  if (int rc = gm_set_smem(k_mv1q<QT, LR, SPL>, smem)) return rc;
-  hipLaunchKernelGGL((k_mv1q<QT, LR, SPL>), dim3((unsigned)((M + rows_per_block - 1) / rows_per_block)), dim3(256),
-                     smem, s, w, M, K, gm_row_bytes(QT, K), x, y);
+  if (int rc = gm_set_smem(k_mv1q<QT, LR, SPL, RPW>, smem)) return rc;
+  hipLaunchKernelGGL((k_mv1q<QT, LR, SPL, RPW>), dim3((unsigned)((M + rows_per_block - 1) / rows_per_block)),
+                     dim3(256), smem, s, w, M, K, gm_row_bytes(QT, K), x, y);
   GM_TRY(hipGetLastError());
   return GM_OK;
+}
+
+// Row groups per wave: as many as keep at least kMv1Blocks blocks in the grid
+// (4 per CU), up to 8 sub-block loads in flight per lane.
+constexpr int kMv1Blocks = 1024;
+
+template <int QT, int LR, int SPL>
+static int launch_mv1q_r(const uint8_t* w, int M, int K, const float* x, float* y, hipStream_t s) {
+  const int64_t groups = (int64_t)(M + 64 / LR - 1) / (64 / LR);        // row groups over the matrix
+  auto fits = [&](int rpw) { return SPL * rpw <= 8 && groups >= (int64_t)4 * rpw * kMv1Blocks; };
+  if (fits(8)) return launch_mv1q_t<QT, LR, SPL, 8>(w, M, K, x, y, s);
+  if (fits(4)) return launch_mv1q_t<QT, LR, SPL, 4>(w, M, K, x, y, s);
+  if (fits(2)) return launch_mv1q_t<QT, LR, SPL, 2>(w, M, K, x, y, s);
+  return launch_mv1q_t<QT, LR, SPL, 1>(w, M, K, x, y, s);
 }
 
 template <int QT>
 static int launch_mv1q(const uint8_t* w, int M, int K, const float* x, float* y, hipStream_t s) {
   const int nsub = K / GM_SUB;                                   // 8 .. 256
-  if (nsub <= 16) return launch_mv1q_t<QT, 16, 1>(w, M, K, x, y, s);
-  if (nsub <= 32) return launch_mv1q_t<QT, 32, 1>(w, M, K, x, y, s);
-  if (nsub <= 64) return launch_mv1q_t<QT, 64, 1>(w, M, K, x, y, s);
-  if (nsub <= 128) return launch_mv1q_t<QT, 64, 2>(w, M, K, x, y, s);
-  return launch_mv1q_t<QT, 64, 4>(w, M, K, x, y, s);
+  if (nsub <= 16) return launch_mv1q_r<QT, 16, 1>(w, M, K, x, y, s);
+  if (nsub <= 32) return launch_mv1q_r<QT, 32, 1>(w, M, K, x, y, s);
+  if (nsub <= 64) return launch_mv1q_r<QT, 64, 1>(w, M, K, x, y, s);
+  if (nsub <= 128) return launch_mv1q_r<QT, 64, 2>(w, M, K, x, y, s);
+  return launch_mv1q_r<QT, 64, 4>(w, M, K, x, y, s);
 }
 
 template <int QT>

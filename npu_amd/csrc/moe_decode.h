@@ -29,9 +29,13 @@ struct GmDecArgs {
 // its copies, added in copy order.  Either the router kernel writes copy 0 and
 // zeros the others, or the previous layer's down kernel (block b) adds its
 // rows' fp32 partials into copy b % 8 with fp64 atomics, which spreads the
-// 256-way contention on one address over 8 addresses.  An fp64 sum of fp32
-// terms is exact, hence independent of the order the atomics land in, unless
-// the terms span more than 29 binades.
+// 256-way contention on one address over 8 addresses.  Each copy receives 32
+// fp32 terms; their fp64 sum is exact, hence independent of the order the
+// atomics land in, when the terms' exponents lie within 24 binades of each
+// other (24 significant bits + 24 binades + log2(32) = 5 bits of growth fit
+// fp64's 53).  Partials that cancel to tiny values can exceed that span; then
+// one fp64 rounding can differ with the atomics' order, a 2^-53-relative
+// difference.  So replays are bit-identical in practice, not by construction.
 // (GM_ACC_COPIES, gm_acc_ld and gm_acc_bytes are in kernels.h.)
 
 // The next layer's router, for the T = 1 down kernel of a chain: block b adds

@@ -511,12 +511,11 @@ __device__ __forceinline__ float pf_dscale(const PfRaw<QT>& r) {
 constexpr uint32_t kKvU[4] = {kGmKv[0] ^ 0x80808080u, kGmKv[1] ^ 0x80808080u, kGmKv[2] ^ 0x80808080u,
                               kGmKv[3] ^ 0x80808080u};
 
-__device__ __forceinline__ uint32_t lut_kvu(uint32_t nib) {
-  const uint32_t sel = nib & 0x07070707u;
-  const uint32_t lo = __builtin_amdgcn_perm(kKvU[1], kKvU[0], sel);
-  const uint32_t hi = __builtin_amdgcn_perm(kKvU[3], kKvU[2], sel);
-  return __builtin_amdgcn_perm(hi, lo, ((nib >> 1) & 0x04040404u) | 0x03020100u);
-}
+// Two-lookup XOR form of the table (see gm_lut16_xor), checked at compile time.
+constexpr gm_iq4_xor::Tabs kKvUx = gm_iq4_xor::solve(kKvU);
+static_assert(gm_iq4_xor::check(kKvU, kKvUx), "XOR lookup of kvalues + 128");
+
+__device__ __forceinline__ uint32_t lut_kvu(uint32_t nib) { return gm_lut16_xor(kKvUx, nib); }
 
 // Four unsigned bytes u -> two f16x2 holding (u - 128) * s, rounded once:
 // 0x6400 | u is the f16 1024 + u, and fma(1024 + u, s, c) with c = -1152 s

@@ -144,6 +144,7 @@ class GpuMoeBlock:
         s.router_t = L.ptr(self.router_t)
         self.struct = s
         self._ws: torch.Tensor | None = None
+        self._retired: list[torch.Tensor] = []
 
     def _check_shapes(self) -> None:
         D, FF, E = self.D, self.FF, self.E
@@ -177,11 +178,15 @@ class GpuMoeBlock:
     def workspace(self, T: int) -> torch.Tensor:
         """The block's one workspace, grown (never shrunk) to the largest T seen.  Offsets
         inside it are recomputed from T on every call, so every smaller T reuses it.  A
-        call with a larger T replaces the buffer: graphs captured before then hold the
-        old one and must be captured again."""
+        call with a larger T installs a larger buffer; the smaller ones stay referenced
+        (``_retired``) for the block's lifetime, so a graph captured before the growth
+        still replays into memory that nothing else has been handed (growth happens at
+        most a few times: each step at least doubles the size)."""
         n = ops.moe_workspace_bytes(self.struct, T)
         if self._ws is None or self._ws.numel() < n:
-            self._ws = None                      # release the old buffer before allocating
+            if self._ws is not None:
+                self._retired.append(self._ws)
+                n = max(n, 2 * self._ws.numel())
             self._ws = torch.zeros(n, dtype=torch.uint8, device=self.gate.device)
         return self._ws
 
@@ -243,6 +248,11 @@ class GpuMoeChain:
         self.blocks = list(blocks)
         self.D = blocks[0].D
         self._buf: torch.Tensor | None = None
+
+    def fused(self, T: int) -> bool:
+        """True when a T-token call runs on the accumulator-linked kernels (T = 1 and every
+        layer fits them), False when it runs one gm_moe_forward per layer."""
+        return ops.moe_chain_fused([b.struct for b in self.blocks], T)
 
     def __call__(self, x: torch.Tensor, *, residual: bool = True, out: torch.Tensor | None = None) -> torch.Tensor:
         if x.dim() != 2 or x.shape[1] != self.D:

@@ -169,3 +169,15 @@ def moe_chain_raw(layers, x: torch.Tensor, y: torch.Tensor, buf: torch.Tensor | 
                               flags, wsp, wsb, L.stream_ptr())
     L.check(rc, "gm_moe_chain")
 
+
+
+def moe_chain_fused(layers, T: int) -> bool:
+    """Whether gm_moe_chain runs ``layers`` at ``T`` tokens on the accumulator-linked T = 1
+    kernels (one router launch, then two launches per layer) rather than one
+    gm_moe_forward per layer."""
+    n = len(layers)
+    arr = (L.GmMoeLayer * n)(*layers)
+    rc = L.lib().gm_moe_chain_fused(arr, n, T)
+    if rc < 0:
+        L.check(rc, "gm_moe_chain_fused")
+    return rc == 1

@@ -15,7 +15,6 @@ from npu_amd.gguf_types import GGMLQuantizationType as QT
 from npu_amd.quant_mv_iq4 import BLK, RAW_B_BYTES, NpuIQ4MatVec
 
 B_BYTES = 136
-_KVALUES = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], dtype=np.int8)
 
 __all__ = ["BLK", "RAW_B_BYTES", "B_BYTES", "NpuIQ4PackedMatVec", "repack_iq4_xs_packed_weight",
            "repack_iq4_xs_packed_per_expert"]

@@ -253,23 +253,50 @@ def _expert_cache_limit_from_env(default: int) -> int | None:
     return None if limit < 0 else limit
 
 
-def enable_npu(model, ops: Sequence[str] = ("router",), *, expert_cache_limit: int | None = None) -> None:
-    """Attach device operators to every MoE layer of ``model`` (same op names as the reference).
+def _is_attn(core) -> bool:
+    """An attention core (the reference's ``AttnLayer``, qwen/forward.py:100-130): wq/wk/wv/wo."""
+    return core is not None and all(hasattr(core, n) for n in ("wq", "wk", "wv", "wo"))
 
-    Every expert-family op makes the layer run through the fused device block;
-    ``router`` / ``shexp`` / ``shexp_split`` additionally expose the stand-alone
-    operators under the reference's ``layer.npu`` keys.  The expert cache limit
-    is kept for compatibility: all experts are resident in HBM, so nothing is
-    evicted.  ``attn_*`` / ``ssm`` are outside this package's path and ignored.
+
+def _is_ssm(core) -> bool:
+    """A Gated DeltaNet core (the reference's ``SSMLayer``, :245-285): w_in/w_gate/w_out."""
+    return core is not None and all(hasattr(core, n) for n in ("w_in", "w_gate", "w_out"))
+
+
+def _pairs(model):
+    """(core, moe) per layer: ``model.layers`` holds the pairs (reference :775); a plain
+    sequence of MoE layers has no cores."""
+    if hasattr(model, "layers"):
+        for item in model.layers:
+            if isinstance(item, tuple):
+                yield item
+            else:
+                yield None, item
+    else:
+        for moe in model:
+            yield None, moe
+
+
+def enable_npu(model, ops: Sequence[str] = ("router",), *, expert_cache_limit: int | None = None) -> None:
+    """Attach device operators to every layer of ``model`` (reference :723-831, same op names
+    and ``npu`` keys).
+
+    For each ``(core, moe)`` pair of ``model.layers``: every expert-family op makes the MoE
+    layer run through the fused device block; ``router`` / ``shexp`` / ``shexp_split``
+    additionally expose the stand-alone operators under the reference's ``layer.npu`` keys.
+    The expert cache limit is kept for compatibility: all experts are resident in HBM, so
+    nothing is evicted.  On the cores: ``attn_o`` puts ``NpuMatVec(core.wo)`` under
+    ``core.npu["wo"]``, ``attn_qkv`` ``NpuConcatMatVec((wq, wk, wv))`` under ``"wqkv"``
+    (attention cores), and ``ssm`` ``NpuMatVec`` of ``w_in`` / ``w_gate`` / ``w_out`` under
+    the same names (Gated DeltaNet cores), as :813-831 do.
     """
     from npu_amd.mlp import NpuFusedMLP
-    from npu_amd.mv import NpuMatVec
+    from npu_amd.mv import NpuConcatMatVec, NpuMatVec
 
     unknown = set(ops) - VALID_OPS
     if unknown:
         raise ValueError(f"unknown NPU ops: {sorted(unknown)} (valid: {sorted(VALID_OPS)})")
-    layers = [m for _, m in model.layers] if hasattr(model, "layers") else list(model)
-    for moe in layers:
+    for core, moe in _pairs(model):
         if moe.npu is None:
             moe.npu = {}
         if "router" in ops:
@@ -291,6 +318,20 @@ def enable_npu(model, ops: Sequence[str] = ("router",), *, expert_cache_limit: i
             moe.npu["expert_cache_limit"] = (_expert_cache_limit_from_env(8) if expert_cache_limit is None
                                              else (None if expert_cache_limit < 0 else expert_cache_limit))
         moe.npu["moe_block"] = _build_block(moe)
+        if "attn_o" in ops and _is_attn(core):
+            if core.npu is None:
+                core.npu = {}
+            core.npu["wo"] = NpuMatVec(core.wo)
+        if "attn_qkv" in ops and _is_attn(core):
+            if core.npu is None:
+                core.npu = {}
+            core.npu["wqkv"] = NpuConcatMatVec((core.wq, core.wk, core.wv), profile_prefix="attn_qkv_mv")
+        if "ssm" in ops and _is_ssm(core):
+            if core.npu is None:
+                core.npu = {}
+            core.npu["w_in"] = NpuMatVec(core.w_in)
+            core.npu["w_gate"] = NpuMatVec(core.w_gate)
+            core.npu["w_out"] = NpuMatVec(core.w_out)
 
 
 def moe_forward(x: torch.Tensor, layer: MoELayer, cfg) -> torch.Tensor:

@@ -222,6 +222,40 @@ def device_config5_layers(n_layers: int, device, seed: int):
     return layers
 
 
+class _DeviceStack:
+    """Expert e of a device-resident [E, M, row_bytes] stack, copied to the host on access."""
+
+    def __init__(self, t: torch.Tensor):
+        self.t = t
+
+    def __getitem__(self, e: int) -> np.ndarray:
+        return self.t[e].cpu().numpy()
+
+
+def host_view(blk) -> HostMoeLayer:
+    """A ``HostMoeLayer`` over a ``GpuMoeBlock``'s weights that copies only what is read: the
+    router, shared expert and norm weight up front, one expert's rows on each ``gate[e]`` /
+    ``up[e]`` / ``down[e]`` (a 40-layer config-5 chain is 15.6 GB; a routed token reads 8
+    experts per layer).  IQ4_XS / IQ3_XXS routed and shared formats only."""
+    def host(t):
+        return None if t is None else t.cpu().numpy()
+
+    def small(t):
+        if t is None:
+            return None
+        a = t.cpu()
+        return a.numpy() if a.dtype == torch.float32 else a.view(torch.int16).numpy().view(np.uint16)
+
+    for q in (blk.q_gate, blk.q_down, blk.q_gate_sh, blk.q_down_sh):
+        if q not in (QT.IQ4_XS, QT.IQ3_XXS):
+            raise ValueError("host_view serves IQ4_XS / IQ3_XXS blocks")
+    return HostMoeLayer(D=blk.D, FF=blk.FF, E=blk.E, k=blk.k, q_gate=blk.q_gate, q_down=blk.q_down,
+                        gate=_DeviceStack(blk.gate), up=_DeviceStack(blk.up), down=_DeviceStack(blk.down),
+                        router=small(blk.router), gate_sh=host(blk.gate_sh), up_sh=host(blk.up_sh),
+                        down_sh=host(blk.down_sh), sh_gate_inp=small(blk.sh_gate_inp),
+                        router_bias=host(blk.router_bias), norm_w=host(blk.norm_w))
+
+
 # ------------------------------------------------------------------ files
 def write_gguf_model(path, layers, *, arch: str = "qwen3next", rms_eps: float = 1e-6) -> None:
     """A GGUF file holding the MoE tensors of `layers` (``HostMoeLayer``) under the model's

@@ -96,3 +96,20 @@ def test_workspace_sizing_and_layer_validation():
     bad = _layer(norm_w=4100)
     rc = lib.gm_moe_forward(ctypes.byref(bad), 1024, 2048, 1, 0, 4096, 1 << 30, None)
     assert rc == L.GM_EINVAL and "16-byte aligned" in L.last_error()
+
+
+def test_chain_path_query_without_gpu():
+    """gm_moe_chain_fused reports the accumulator-linked path only at T = 1 with every layer
+    after the first carrying router_t; a rejected layer gives its GM_E* code."""
+    lib = L.lib()
+    a, b = _layer(router_t=512), _layer(router_t=512)
+    arr = (L.GmMoeLayer * 2)(a, b)
+    assert lib.gm_moe_chain_fused(arr, 2, 1) == 1
+    assert lib.gm_moe_chain_fused(arr, 2, 8) == 0
+    arr = (L.GmMoeLayer * 2)(a, _layer())          # layer 1 without router_t: per-layer path
+    assert lib.gm_moe_chain_fused(arr, 2, 1) == 0
+    arr = (L.GmMoeLayer * 2)(a, _layer(router_t=512, E=128))   # layers must share E
+    assert lib.gm_moe_chain_fused(arr, 2, 1) == 0
+    arr = (L.GmMoeLayer * 2)(a, _layer(k=9))
+    assert lib.gm_moe_chain_fused(arr, 2, 1) == L.GM_EINVAL
+    assert lib.gm_moe_chain_fused(None, 2, 1) == L.GM_EINVAL

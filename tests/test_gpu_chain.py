@@ -119,6 +119,7 @@ def test_gm_moe_chain(gpu, variant_chain, T):
         x0 = x0 * 0.01           # without RMSNorm the block amplifies ~x^2: keeps layer 1's logits spread ~10
     ids_ref, y_ref = _oracle_chain(hosts, x0, hosts[0].k)
     ch = GpuMoeChain(blocks)
+    assert ch.fused(T) == (T == 1), f"{name}: the chain took the {'per-layer' if T == 1 else 'fused'} path"
     xd = x0.to(gpu)
     y_eager = ch(xd, residual=True)
     torch.cuda.synchronize()
@@ -149,3 +150,40 @@ def test_gm_moe_chain(gpu, variant_chain, T):
         assert torch.equal(out, y_eager), f"replay {rep} differs from the eager chain"
         blocks[0](torch.randn_like(xd), residual=True)
         torch.cuda.synchronize()
+
+
+def test_config5_headline_chain_40_layers(gpu):
+    """The bench's headline workload itself: bench.py's 40 config-5 layers (same seed, same
+    input) through one gm_moe_chain call (the accumulator-linked kernels, asserted), against
+    (a) the same 40 layers run one gm_moe_forward at a time: top-k ids equal at every layer,
+    output rel <= 1e-5 (the chain's logits are the same dot products added in another order);
+    (b) the oracle, layer by layer from the device weights (experts fetched as routed): ids
+    equal at every layer (every layer's input asserted near-tie free) and output rel <= 1e-3."""
+    import bench
+    print("headline chain case: 40 config-5 layers, T=1", flush=True)
+    layers = synth.device_config5_layers(bench.N_LAYERS, gpu, bench.SEED)
+    x0 = torch.from_numpy(synth.host_input(bench.SEED, 1, bench.D, rmsnorm=False))
+    ch = GpuMoeChain(layers)
+    assert ch.fused(1)
+    y_chain = ch(x0.to(gpu), residual=True)
+    torch.cuda.synchronize()
+    ids_chain = [blk.stages(1)["topk_ids"].cpu().long().clone() for blk in layers]
+    x = x0.to(gpu)
+    ids_pl = []
+    for blk in layers:
+        x = blk(x, residual=True)
+        ids_pl.append(blk.stages(1)["topk_ids"].cpu().long().clone())
+    torch.cuda.synchronize()
+    for li in range(len(layers)):
+        assert torch.equal(ids_chain[li], ids_pl[li]), f"layer {li}: chain and per-layer ids differ"
+    rel_pl = OM.rel_err(y_chain.cpu(), x.cpu())
+    assert rel_pl <= 1e-5, f"chain vs per-layer rel {rel_pl:.3e}"
+    hosts = [synth.host_view(blk) for blk in layers]
+    ids_ref, y_ref = _oracle_chain(hosts, x0, 8)
+    for li in range(len(layers)):
+        assert torch.equal(ids_chain[li], ids_ref[li]), f"layer {li}: ids differ from the oracle"
+    rel = OM.rel_err(y_chain.cpu(), y_ref)
+    print(f"headline chain: rel vs per-layer {rel_pl:.2e}, vs oracle {rel:.2e}", flush=True)
+    assert rel <= 1e-3, f"chain vs oracle rel {rel:.3e}"
+    del layers, hosts
+    torch.cuda.empty_cache()

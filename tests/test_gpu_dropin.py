@@ -164,3 +164,50 @@ def test_qwen_moe_forward_kquant_layers(gpu, tmp_path, T):
         bar = 1e-2 if (i == 0 and T > 8) else 1e-3
         assert OM.rel_err(y, ref) <= bar, (i, OM.rel_err(y, ref))
 
+
+
+def test_enable_npu_attention_and_ssm_cores(gpu):
+    """enable_npu over a model's (core, moe) pairs (qwen/forward.py:775, 813-831): an attention
+    core gets ``wo`` (attn_o) and ``wqkv`` (attn_qkv, split (8192, 512, 512)), a Gated
+    DeltaNet core ``w_in`` / ``w_gate`` / ``w_out`` (ssm), at the shapes of
+    qwen/test_npu_{attn_o,attn_qkv,ssm}.py; each output against float64 F.linear of the bf16
+    weight (the operators stage weights in bf16, as the reference does) at rel <= 1e-5.  Ops
+    that are not asked for leave their keys absent, and a core of the other kind is left alone."""
+    from types import SimpleNamespace
+
+    g = torch.Generator().manual_seed(11)
+
+    def w(*shape):
+        return torch.randn(*shape, generator=g) * 0.02
+
+    attn = SimpleNamespace(wq=w(8192, 2048), wk=w(512, 2048), wv=w(512, 2048), wo=w(2048, 4096), npu=None)
+    ssm = SimpleNamespace(w_in=w(8192, 2048), w_gate=w(4096, 2048), w_out=w(2048, 4096), npu=None)
+    hs = [synth.host_moe_layer(70 + i, D=2048, FF=256, E=16, k=4) for i in range(2)]
+    ts = qwen_moe.SyntheticTensorStore(hs)
+    model = SimpleNamespace(layers=[(ssm, qwen_moe.MoELayer.load(ts, 0)), (attn, qwen_moe.MoELayer.load(ts, 1))])
+    qwen_moe.enable_npu(model, ops=("router", "attn_o", "attn_qkv", "ssm"))
+    assert set(attn.npu) == {"wo", "wqkv"} and set(ssm.npu) == {"w_in", "w_gate", "w_out"}
+    assert all("moe_block" in moe.npu and "router" in moe.npu for _, moe in model.layers)
+
+    def ref(x, W):
+        return (x.double() @ W.to(torch.bfloat16).double().T).float()
+
+    x = torch.randn(2048, generator=g) * 0.05               # post-norm hidden state scale
+    xo = torch.randn(4096, generator=g) * 0.05
+    checks = [("attn_o", attn.npu["wo"](xo), ref(xo, attn.wo)),
+              ("attn_qkv", attn.npu["wqkv"](x), ref(x, torch.cat([attn.wq, attn.wk, attn.wv]))),
+              ("ssm_in", ssm.npu["w_in"](x), ref(x, ssm.w_in)),
+              ("ssm_gate", ssm.npu["w_gate"](x), ref(x, ssm.w_gate)),
+              ("ssm_out", ssm.npu["w_out"](xo), ref(xo, ssm.w_out))]
+    for name, y, yr in checks:
+        assert y.shape == yr.shape, name
+        assert OM.rel_err(y, yr) <= 1e-5, f"{name}: rel {OM.rel_err(y, yr):.3e}"
+    assert attn.npu["wqkv"].out_splits == (8192, 512, 512)
+    q, k, v = attn.npu["wqkv"](x).split((8192, 512, 512))
+    assert OM.rel_err(k, ref(x, attn.wk)) <= 1e-5 and OM.rel_err(v, ref(x, attn.wv)) <= 1e-5
+    # only what is asked for
+    attn2 = SimpleNamespace(wq=attn.wq, wk=attn.wk, wv=attn.wv, wo=attn.wo, npu=None)
+    ssm2 = SimpleNamespace(w_in=ssm.w_in, w_gate=ssm.w_gate, w_out=ssm.w_out, npu=None)
+    qwen_moe.enable_npu(SimpleNamespace(layers=[(attn2, qwen_moe.MoELayer.load(ts, 0)),
+                                                (ssm2, qwen_moe.MoELayer.load(ts, 1))]), ops=("attn_o",))
+    assert set(attn2.npu) == {"wo"} and ssm2.npu is None

@@ -71,6 +71,33 @@ def test_matvec(gpu, qtype, M, K, n_tok):
     assert float(((y.double() - ref64).abs() / ref64.abs().amax(dim=1, keepdim=True)).max()) <= 1e-5
 
 
+# Tall one-token matvecs (a batched launch over many matrices stacked by rows, as
+# bench.py's configs 1-2 legs run them): the kernel then gives each wave 2, 4 or 8 row
+# groups with all their sub-blocks in flight.  Against float64 on the exact device
+# dequant, and row slices recomputed as separate short calls (1 row group per wave)
+# must be bit-identical: each row's sum is formed in the same order either way.
+@pytest.mark.parametrize("qtype,M,K", [
+    (QT.IQ4_XS, 32768 + 37, 2048),     # 8 row groups per wave, ragged last block
+    (QT.IQ3_XXS, 131072 + 6, 512),     # 16 lanes per row, 8 row groups
+    (QT.IQ3_XXS, 16384 + 1, 2048),     # 4 row groups
+    (QT.IQ4_XS, 8192 + 3, 8192),       # 4 sub-blocks per lane, 2 row groups
+    (QT.IQ4_XS, 8192, 4096),           # 2 sub-blocks per lane, 2 row groups
+])
+def test_matvec_tall(gpu, qtype, M, K):
+    gen = torch.Generator(device=gpu)
+    gen.manual_seed(M + K)
+    W = synth.device_quant_matrix(gen, qtype, M, K, None, gpu)
+    x = torch.randn(K, generator=gen, device=gpu)
+    y = ops.matvec(qtype, W, M, K, x.view(1, K)).view(M)
+    Wd = ops.dequant(qtype, W.reshape(-1)).view(M, K).double()
+    ref = Wd @ x.double()
+    assert OM.rel_err(y, ref) <= 1e-5
+    assert float(((y.double() - ref).abs() / ref.abs().max()).max()) <= 1e-5
+    for r0, n in ((0, 512), (M - 300, 300), (M // 2 + 5, 96)):
+        ys = ops.matvec(qtype, W[r0:r0 + n].clone(), n, K, x.view(1, K)).view(n)   # clone: 16-byte aligned
+        assert torch.equal(ys, y[r0:r0 + n]), f"rows {r0}..{r0 + n} differ from the tall call"
+
+
 # The projection shapes of qwen/test_npu_ssm.py and test_npu_attn_o.py (8192 x 2048,
 # 4096 x 2048, 2048 x 4096), plus ragged M, K tails inside a 512-wide slot, and K
 # large enough for two passes over the row.

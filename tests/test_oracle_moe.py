@@ -68,3 +68,35 @@ def test_oracle_small_block_fixture():
         y = OM.block_forward(torch.from_numpy(x), OM.OracleLayer(h), stages=st).numpy()
         np.testing.assert_allclose(y, d[f"c{case}_y64"], rtol=0, atol=2e-6 * np.abs(d[f"c{case}_y64"]).max())
         assert np.array_equal(st["topk_ids"].numpy(), d[f"c{case}_ids"])
+
+
+def test_rms_norm_invariants():
+    """oracle.moe.rms_norm (qwen/forward.py:58-61) against what the formula fixes, with no
+    second copy of it: with weight 1 the output's mean square is 1 (to eps), so a sum in
+    place of a mean or a missing square root fails; scaling x by c leaves the output
+    unchanged (up to eps), so a missing normalisation fails; the weight multiplies element by
+    element (a weight of 2 doubles exactly, a one-hot weight keeps one column), so a weight
+    applied before the statistics or broadcast on the wrong axis fails; eps enters under the
+    root (x = 0 gives 0, a constant row c gives c / sqrt(c^2 + eps) in closed form); the
+    reduction runs over the last axis only."""
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(5, 2048, generator=g, dtype=torch.float32) * 3.0 + 0.5
+    eps = 1e-6
+    y = OM.rms_norm(x, None, eps)
+    ms = y.double().pow(2).mean(-1)
+    assert torch.allclose(ms, torch.ones_like(ms), rtol=0, atol=1e-5)
+    for c in (1e-3, 7.0, 1e4):
+        assert torch.allclose(OM.rms_norm(x * c, None, 0.0), OM.rms_norm(x, None, 0.0), rtol=1e-6, atol=1e-6)
+    assert torch.equal(OM.rms_norm(x, torch.full((2048,), 2.0), eps), 2.0 * y)
+    onehot = torch.zeros(2048)
+    onehot[17] = 1.0
+    z = OM.rms_norm(x, onehot, eps)
+    assert torch.equal(z[:, 17], y[:, 17]) and int((z != 0).sum()) == 5
+    assert torch.equal(OM.rms_norm(torch.zeros(3, 64), None, eps), torch.zeros(3, 64))
+    for c in (0.25, 3.0, -5.0):
+        row = torch.full((1, 256), c, dtype=torch.float32)
+        want = c / np.sqrt(np.float64(c) ** 2 + 1e-2)
+        assert abs(float(OM.rms_norm(row, None, 1e-2)[0, 0]) - want) < 1e-6 * abs(want)
+    # last axis only: each row normalised by its own statistics
+    rows = torch.stack([x[0], 100.0 * x[1]])
+    assert torch.allclose(OM.rms_norm(rows, None, eps)[1], y[1], rtol=1e-5, atol=1e-6)

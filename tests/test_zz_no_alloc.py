@@ -62,3 +62,47 @@ def test_noalloc_rejects_oversize(gpu):
     assert rc == L.GM_EWORKSPACE and "static scratch" in L.last_error()
     torch.cuda.synchronize()
     assert bool((y == 7.0).all()), "nothing may run on a rejected call"
+
+
+def test_noalloc_under_graph_capture(gpu):
+    """After a first eager call on the device (which resolves the static scratch's address,
+    and so must happen outside capture), gm_moe_forward_noalloc is captured in a hipGraph and
+    replayed three times with other work between the replays: every replay bit-identical to
+    gm_moe_forward, and neither torch's allocator nor the device's free memory moves across
+    the eager calls and replays that follow the capture."""
+    print("noalloc capture case T=1 and T=8", flush=True)
+    blk = GpuMoeBlock.from_host(synth.host_moe_layer(420, norm=True), device=gpu)
+    s = torch.cuda.Stream()
+    for T in (1, 8):
+        x = torch.from_numpy(synth.host_input(520 + T, T, blk.D, rmsnorm=False)).to(gpu)
+        want = blk(x, residual=True)
+        torch.cuda.synchronize()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            y = torch.empty_like(x)
+            L.check(L.lib().gm_moe_forward_noalloc(ctypes.byref(blk.struct), L.ptr(x), L.ptr(y), T,
+                                                   L.GM_MOE_RESIDUAL, s.cuda_stream), "gm_moe_forward_noalloc")
+        s.synchronize()
+        assert torch.equal(y, want)
+        y.zero_()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            L.check(L.lib().gm_moe_forward_noalloc(ctypes.byref(blk.struct), L.ptr(x), L.ptr(y), T,
+                                                   L.GM_MOE_RESIDUAL, s.cuda_stream), "gm_moe_forward_noalloc")
+        with torch.cuda.stream(s):
+            z = torch.empty_like(x)                 # the eager calls' output, allocated before measuring
+        torch.cuda.synchronize()
+        alloc0, free0 = torch.cuda.memory_allocated(), torch.cuda.mem_get_info()[0]
+        for rep in range(3):
+            y.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, want), f"T={T} replay {rep} differs from gm_moe_forward"
+            with torch.cuda.stream(s):              # eager no-alloc work on the same scratch in between
+                L.check(L.lib().gm_moe_forward_noalloc(ctypes.byref(blk.struct), L.ptr(want), L.ptr(z), T, 0,
+                                                       s.cuda_stream), "gm_moe_forward_noalloc")
+            s.synchronize()
+        torch.cuda.synchronize()
+        assert torch.cuda.memory_allocated() == alloc0
+        assert torch.cuda.mem_get_info()[0] == free0, "device free memory changed across no-alloc calls"
