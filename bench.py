@@ -276,6 +276,32 @@ def run_prefill(layers, T: int = 512, n_blocks: int = 8, reps: int = 5, samples:
             "mfma_util_vs_bf16_dense_peak": flops / (us * 1e-6) / 2.5e15, "finite": finite}
 
 
+def kquant_shared_layers(layers, seed: int = SEED + 6):
+    """The same blocks with the shared expert as the reference model's GGUF stores it: Q6_K
+    gate, Q8_0 up and Q6_K down (seeded random blocks, transcoded once on the device to I8
+    rows), beside the IQ routed experts (the same device tensors, not copied)."""
+    import numpy as np
+    import torch
+    from npu_amd import _lib as L
+    from npu_amd import ops, synth
+    from npu_amd.gguf_types import GGMLQuantizationType as QT
+    from npu_amd.moe import GpuMoeBlock
+    g = np.random.default_rng(seed)
+    dev = layers[0].gate.device
+    out = []
+    for b in layers:
+        def i8(q, M, K, per):
+            raw = synth.host_kquant_blocks(g, q, M * K // per)
+            return ops.transcode_i8(int(q), torch.from_numpy(raw.reshape(-1)).to(dev)).view(M, K // 32 * 48)
+        out.append(GpuMoeBlock(gate=b.gate, up=b.up, down=b.down, router=b.router, q_gate=b.q_gate,
+                               q_down=b.q_down, D=b.D, FF=b.FF, E=b.E, k=b.k,
+                               gate_sh=i8(QT.Q6_K, b.FF, b.D, 256), up_sh=i8(QT.Q8_0, b.FF, b.D, 32),
+                               down_sh=i8(QT.Q6_K, b.D, b.FF, 256), q_gate_sh=L.GM_QTYPE_I8,
+                               q_down_sh=L.GM_QTYPE_I8, sh_gate_inp=b.sh_gate_inp, norm_w=b.norm_w,
+                               norm_eps=b.norm_eps, device=dev))
+    return out
+
+
 DENSE_SHAPES = (("ssm_in", 8192, 2048), ("ssm_gate", 4096, 2048), ("ssm_out", 2048, 4096))
 
 
@@ -645,7 +671,9 @@ def main() -> int:
     if args.prefill_only:
         layers = build_layers(8, dev)
         torch.cuda.synchronize()
-        print(json.dumps({"prefill": run_prefill(layers)}))
+        out = {"prefill": run_prefill(layers)}
+        out["prefill_kquant_shared"] = run_prefill(kquant_shared_layers(layers))
+        print(json.dumps(out))
         return 0
     if args.dense_only:
         print(json.dumps({"dense_mv": run_dense_mv(dev, shapes=args.dense_shapes.split(","),
@@ -709,6 +737,10 @@ def main() -> int:
         log(f"B=8: {extra['batch8']}")
         extra["prefill"] = run_prefill(layers, samples=samples)
         log(f"prefill: {extra['prefill']}")
+        extra["prefill_kquant_shared"] = run_prefill(kquant_shared_layers(layers[:8]))
+        extra["prefill_kquant_shared"]["workload"] = ("config4 with the shared expert as the real GGUF holds it "
+                                                      "(Q6_K gate, Q8_0 up, Q6_K down as I8 rows), 8 layers")
+        log(f"prefill, K-quant shared expert: {extra['prefill_kquant_shared']}")
         extra["dense_mv"] = run_dense_mv(dev)
         log(f"dense bf16 matvec: {extra['dense_mv']}")
         extra["quant_mv"] = run_quant_mv(dev, samples=samples)

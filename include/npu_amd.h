@@ -184,10 +184,11 @@ int gm_moe_forward(const gm_moe_layer* L, const float* x, float* y, int T, int f
  * decode kernels, 1 <= T <= 8 (the reference's NPU expert path is T = 1:
  * qwen/forward.py:494-560 via _npu_routed_expert).  gm_moe_prefill: the
  * grouped f16/bf16-MFMA GEMMs for any T >= 1 (the reference runs prefill through
- * the CPU loop of qwen/forward.py:622-663); a layer with BF16 routed experts,
- * or with a shared expert in other formats than the routed ones,
- * runs its tokens as decode chunks of at most 8 instead.  Same workspace as
- * gm_moe_forward.
+ * the CPU loop of qwen/forward.py:622-663); a layer with BF16 or I8 routed
+ * experts runs its tokens as decode chunks of at most 8 instead.  A shared
+ * expert in other formats than the (IQ) routed ones, such as the real
+ * model's K-quant shared experts held as I8 rows, runs as an fp32 pass of
+ * its own beside the routed GEMMs.  Same workspace as gm_moe_forward.
  */
 int gm_moe_decode(const gm_moe_layer* L, const float* x, float* y, int T, int flags, void* ws,
                   size_t ws_bytes, void* stream);

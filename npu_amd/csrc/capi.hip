@@ -378,15 +378,14 @@ static int moe_forward_impl(const gm_moe_layer* L, const float* x, float* y, int
   const bool decode = path == kPathDecode || (path == kPathAuto && T <= GM_DECODE_MAX_T && T * L->k <= GM_GRP_MAXU);
   if (decode) return gm_dec_run(L, x, y, T, flags, w, lay, s, stage);
   if (stage != 0) return gm_fail_arg("gm_moe_forward_stage: stages are only defined for the decode path (T <= 8)");
-  const bool sh_mixed = L->gate_sh && (L->q_gate_sh != L->q_gate || L->q_down_sh != L->q_down);
-  if (!is_quant(L->q_gate) || !is_quant(L->q_down) || sh_mixed) {
-    // Routed experts held as bf16 or I8 rows (K-quant expert tensors),
-    // or a shared expert in other formats than the routed ones (a dense bf16
-    // shared expert beside IQ routed experts): the prefill GEMMs run the shared
-    // expert as a ninth unit of the routed formats only, so the tokens run as
-    // decode chunks of at most 8 (every token's MoE output is independent of
-    // the others).  Each chunk writes its logits / ids / weights / shared gate
-    // into its rows of the full-T arrays.
+  if (!is_quant(L->q_gate) || !is_quant(L->q_down)) {
+    // Routed experts held as bf16 or I8 rows (K-quant expert tensors): the
+    // prefill GEMMs decode IQ4_XS / IQ3_XXS only, so the tokens run as decode
+    // chunks of at most 8 (every token's MoE output is independent of the
+    // others).  Each chunk writes its logits / ids / weights / shared gate into
+    // its rows of the full-T arrays.  (A shared expert in other formats than IQ
+    // routed experts stays on the prefill path: gm_pf_run runs it as a pass of
+    // its own.)
     const int D = L->D, E = L->E, k = L->k;
     for (int t0 = 0; t0 < T; t0 += GM_DECODE_MAX_T) {
       const int tc = T - t0 < GM_DECODE_MAX_T ? T - t0 : GM_DECODE_MAX_T;

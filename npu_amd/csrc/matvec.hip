@@ -432,7 +432,8 @@ static int launch_mv1q(const uint8_t* w, int M, int K, const float* x, float* y,
 template <int QT>
 static int launch_matvec_q(const uint8_t* w, int M, int K, const float* x, int n_tok, float* y,
                            hipStream_t s) {
-  if (n_tok == 1 && K <= kMv1MaxK) return launch_mv1q<QT>(w, M, K, x, y, s);
+  if constexpr (QT != GM_QTYPE_I8)
+    if (n_tok == 1 && K <= kMv1MaxK) return launch_mv1q<QT>(w, M, K, x, y, s);
   const int nsub = K / GM_SUB;
   if (nsub >= 64) return launch_matvec_l<QT, 64>(w, M, K, x, n_tok, y, s);
   if (nsub >= 32) return launch_matvec_l<QT, 32>(w, M, K, x, n_tok, y, s);
@@ -450,6 +451,7 @@ int gm_launch_matvec(int qtype, const void* w, int M, int K, const float* x, int
     case GM_QTYPE_IQ4_XS: return launch_matvec_q<GM_QTYPE_IQ4_XS>(p, M, K, x, n_tok, y, s);
     case GM_QTYPE_IQ3_XXS: return launch_matvec_q<GM_QTYPE_IQ3_XXS>(p, M, K, x, n_tok, y, s);
     case GM_QTYPE_BF16: return gm_launch_mv_bf16(static_cast<const uint16_t*>(w), M, K, x, n_tok, y, s);
+    case GM_QTYPE_I8: return launch_matvec_q<GM_QTYPE_I8>(p, M, K, x, n_tok, y, s);   // prefill's shared expert
     default: return gm_fail_arg("gm_matvec: unsupported qtype %d", qtype);
   }
 }
@@ -534,6 +536,7 @@ int gm_launch_gateup(int qtype, const void* wg, const void* wu, int FF, int D, c
     case GM_QTYPE_IQ4_XS: return launch_gateup_q<GM_QTYPE_IQ4_XS>(g, u, FF, D, x, n_tok, h, s);
     case GM_QTYPE_IQ3_XXS: return launch_gateup_q<GM_QTYPE_IQ3_XXS>(g, u, FF, D, x, n_tok, h, s);
     case GM_QTYPE_BF16: return launch_gateup_q<GM_QTYPE_BF16>(g, u, FF, D, x, n_tok, h, s);
+    case GM_QTYPE_I8: return launch_gateup_q<GM_QTYPE_I8>(g, u, FF, D, x, n_tok, h, s);
     default: return gm_fail_arg("gm_swiglu_mlp: unsupported gate/up qtype %d", qtype);
   }
 }

@@ -78,7 +78,19 @@ struct PfWs {
   uint16_t* hh;       // [P + T][FF]  the same rows as scaled f16
   float* hsc;         // [P + T]      their scales
   float* yp;          // [P + T][D]   fp32 per-pair / shared outputs
+  float* xn;          // [T][D]  fp32 xn, for a shared expert in other formats than the routed ones
+  float* hsh;         // [T][FF] its fp32 SwiGLU rows
 };
+
+// A shared expert stored in other formats than the routed experts (the real
+// model's K-quant shared experts, held as I8 rows, beside IQ routed experts; or
+// a dense bf16 one) does not run as the GEMMs' ninth unit: its T tokens run as
+// one fp32 pass of the multi-token gate/up and down matvec kernels over xn,
+// which writes the rows yp[P + t] the combine reads.  The routed experts keep
+// the grouped GEMMs.
+inline bool pf_shared_apart(const gm_moe_layer* L) {
+  return L->gate_sh && (L->q_gate_sh != L->q_gate || L->q_down_sh != L->q_down);
+}
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -113,6 +125,10 @@ PfWs pf_layout(const gm_moe_layer* L, int T, uint8_t* base, size_t* total) {
   w.hh = reinterpret_cast<uint16_t*>(take((P + T) * (size_t)L->FF * 2));
   w.hsc = reinterpret_cast<float*>(take((P + T) * 4));
   w.yp = reinterpret_cast<float*>(take((P + T) * (size_t)L->D * 4));
+  if (pf_shared_apart(L)) {
+    w.xn = reinterpret_cast<float*>(take((size_t)T * L->D * 4));
+    w.hsh = reinterpret_cast<float*>(take((size_t)T * L->FF * 4));
+  }
   if (total) *total = o;
   return w;
 }
@@ -167,7 +183,7 @@ __device__ __forceinline__ void pf_put_planes(gm_f32x2 v, int sh, uint32_t& o0, 
 __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, int T, int D,
                                                  const float* __restrict__ norm_w, float eps,
                                                  uint16_t* __restrict__ xr, uint16_t* __restrict__ xh,
-                                                 float* __restrict__ xsc) {
+                                                 float* __restrict__ xsc, float* __restrict__ xn32) {
   __shared__ float red[4], redm[4];
   const int t = blockIdx.x;
   const gm_f32x2* x2 = reinterpret_cast<const gm_f32x2*>(x + (int64_t)t * D);
@@ -222,6 +238,7 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
       q1[c] = make_uint2(o1[0], o1[1]);
       q2[c] = make_uint2(o2[0], o2[1]);
       qh[c] = make_uint2(oh[0], oh[1]);
+      if (xn32) reinterpret_cast<gm_f32x4*>(xn32 + (int64_t)t * D)[c] = v[i];
     }
   } else {
     // two passes over the row: x^2 and max |x w| (rms > 0 scales the maximum
@@ -250,6 +267,7 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
       gm_f32x2 v = x2[i];
       if (norm_w) { const gm_f32x2 w = w2[i]; v.x = (v.x * rms) * w.x; v.y = (v.y * rms) * w.y; }
       pf_put_planes(v, sh, p0[i], p1[i], p2[i], ph[i]);
+      if (xn32) reinterpret_cast<gm_f32x2*>(xn32 + (int64_t)t * D)[i] = v;
     }
   }
   if (threadIdx.x == 0) xsc[t] = __builtin_ldexpf(1.0f, -sh);
@@ -1027,8 +1045,11 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
   float* wts = reinterpret_cast<float*>(ws + lay.wts);
   PfWs w = pf_layout(L, T, ws + lay.pre, nullptr);
   const bool has_sh = L->gate_sh != nullptr;
+  const bool sh_apart = pf_shared_apart(L);
+  const bool sh_gemm = has_sh && !sh_apart;          // the shared expert as the GEMMs' ninth unit
   const int nrows = E + (L->sh_gate_inp ? 1 : 0);
-  hipLaunchKernelGGL(k_pf_prep, dim3(T), dim3(256), 0, s, x, T, D, L->norm_w, L->norm_eps, w.xr, w.xh, w.xsc);
+  hipLaunchKernelGGL(k_pf_prep, dim3(T), dim3(256), 0, s, x, T, D, L->norm_w, L->norm_eps, w.xr, w.xh, w.xsc,
+                     sh_apart ? w.xn : nullptr);
   GM_TRY(hipGetLastError());
   const int ldp = router_ld(L);
   const int nsplit = router_split(D);
@@ -1066,8 +1087,13 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
   }
   GM_TRY(hipGetLastError());
   if (int rc = gm_launch_dispatch_seg(ids, T, k, E, w.counts, w.offsets, w.sorted, w.inv, w.segs, kSegTok,
-                                     has_sh ? T : 0, s))
+                                     sh_gemm ? T : 0, s))
     return rc;
+  if (sh_apart) {                                    // shared expert rows yp[P + t], fp32
+    if (int rc = gm_launch_gateup(L->q_gate_sh, L->gate_sh, L->up_sh, FF, D, w.xn, T, w.hsh, s)) return rc;
+    if (int rc = gm_launch_matvec(L->q_down_sh, L->down_sh, D, FF, w.hsh, T, w.yp + (size_t)T * k * D, s))
+      return rc;
+  }
   const int nseg = max_segments(T, k, E);
   {
     const int nrt = FF / 64;
@@ -1078,7 +1104,7 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
     GM_TRY(hipGetLastError());
   }
   {
-    const int rows = T * k + (has_sh ? T : 0);
+    const int rows = T * k + (sh_gemm ? T : 0);
     hipLaunchKernelGGL(k_pf_h16, dim3((rows + 3) / 4), dim3(256), 0, s, w.hb, rows, FF, w.hh, w.hsc);
     GM_TRY(hipGetLastError());
   }
@@ -1122,9 +1148,6 @@ size_t gm_prefill_scratch_bytes(const gm_moe_layer* L, int T) {
 
 int gm_pf_run(const gm_moe_layer* L, const float* x, float* y, int T, int flags, uint8_t* ws, const GmMoeWs& lay,
               hipStream_t s) {
-  if (L->gate_sh && (L->q_gate_sh != L->q_gate || L->q_down_sh != L->q_down))
-    return gm_fail_arg("gm_moe_forward: the prefill path needs the shared expert in the routed formats"),
-           GM_EUNSUPPORTED;
   if (L->D % kChunk || L->FF % kChunk || L->FF > 4 * kChunk)
     return gm_fail_arg("gm_moe_forward: prefill needs D and FF multiples of %d and FF <= %d", kChunk, 4 * kChunk);
   if (router_split(L->D) > kRouterSplit)

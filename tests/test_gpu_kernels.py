@@ -231,7 +231,9 @@ def test_dequant_kquants_exact(gpu, qtype):
 def test_tensor_store_kquant_shared_expert(gpu, tmp_path, T):
     """A layer whose shared expert is Q6_K / Q8_0 in the file (as in the real model): the
     drop-in transcodes the file's bytes to I8 rows (Q6_K gate beside Q8_0 up) and runs
-    them beside the IQ routed experts, also for T > 8 (decode chunks).  Bar: 1e-3."""
+    them beside the IQ routed experts, also for T > 8 (the routed experts on the prefill
+    GEMMs, the shared expert as an fp32 pass of its own).  Bar: 1e-3 (decode), 1e-2
+    (prefill)."""
     from npu_amd import gguf_file, qwen_moe
     from oracle import kquants as KQ
     rng = np.random.default_rng(7)
@@ -269,4 +271,4 @@ def test_tensor_store_kquant_shared_expert(gpu, tmp_path, T):
     sgate = torch.sigmoid(xs @ torch.full((D,), 0.01, dtype=torch.float64))
     ref = routed.reshape(T, D) + sgate[:, None] * (hsh @ ds.T)
     assert layer.npu["moe_block"].q_gate_sh == L.GM_QTYPE_I8
-    assert OM.rel_err(y.reshape(T, D).double(), ref) <= 1e-3
+    assert OM.rel_err(y.reshape(T, D).double(), ref) <= (1e-3 if T <= 8 else 1e-2)

@@ -156,3 +156,65 @@ def test_prefill_rejects_wide_ff(gpu):
     x = torch.from_numpy(synth.host_input(1, 12, h.D)).to(gpu)
     with pytest.raises(ValueError, match="FF"):
         blk(x, path="prefill")
+
+
+def _kquant_blocks(rng, qtype, n):
+    """Random blocks of a K-quant / Q8_0 type with finite fp16 d (and dmin)."""
+    from oracle import kquants as KQ
+    w, nb = KQ.BLOCK[qtype]
+    b = rng.integers(0, 256, (n, nb), dtype=np.uint8)
+    d = (rng.standard_normal(n) * 1e-2).astype(np.float16).view(np.uint8).reshape(n, 2)
+    if qtype == KQ.Q6_K:
+        b[:, 208:210] = d
+    else:
+        b[:, 0:2] = d
+        if qtype != KQ.Q8_0:
+            b[:, 2:4] = (np.abs(rng.standard_normal(n)) * 1e-2).astype(np.float16).view(np.uint8).reshape(n, 2)
+    return b
+
+
+@pytest.mark.parametrize("T,D,FF,E,k", [(12, 512, 256, 16, 4), (130, 1024, 512, 64, 8), (512, 2048, 512, 256, 8)])
+def test_prefill_kquant_shared_expert(gpu, T, D, FF, E, k):
+    """IQ routed experts beside a Q6_K / Q8_0 shared expert (as the real model's GGUF holds
+    it; transcoded once to I8 rows) at T > 8.  The routed experts stay on the prefill GEMMs
+    and the shared expert runs as an fp32 pass of its own: the output equals the same layer
+    without the shared expert, run on the prefill path, plus sigmoid(xn . g_sh) times the
+    fp64 shared expert, to 2e-5 of the output's maximum (the routed part is the same
+    computation bit for bit, so a run of the tokens as fp32 decode chunks, which rounds the
+    routed part differently at ~1e-4, fails this); and the oracle's routed part plus that
+    shared term within the prefill bar."""
+    import torch.nn.functional as F
+    from npu_amd import _lib as L, ops
+    from oracle import kquants as KQ
+    print(f"prefill kquant-shared case T={T} D={D} FF={FF} E={E} k={k}", flush=True)
+    rng = np.random.default_rng(T + D)
+    h = synth.host_moe_layer(90 + T, D=D, FF=FF, E=E, k=k, shared=False)
+    raw = {"gate": (_kquant_blocks(rng, KQ.Q6_K, FF * D // 256), KQ.Q6_K, (FF, D)),
+           "up": (_kquant_blocks(rng, KQ.Q8_0, FF * D // 32), KQ.Q8_0, (FF, D)),
+           "down": (_kquant_blocks(rng, KQ.Q6_K, D * FF // 256), KQ.Q6_K, (D, FF))}
+    i8 = {n: ops.transcode_i8(int(q), torch.from_numpy(b.reshape(-1)).to(gpu)).view(shp[0], shp[1] // 32 * 48)
+          for n, (b, q, shp) in raw.items()}
+    g_sh = torch.from_numpy((rng.standard_normal(D) * 0.02).astype(np.float32)).to(torch.bfloat16)  # bf16 router kept
+    common = dict(gate=h.gate, up=h.up, down=h.down, router=h.router, q_gate=h.q_gate, q_down=h.q_down,
+                  D=D, FF=FF, E=E, k=k, device=gpu)
+    blk = GpuMoeBlock(**common, gate_sh=i8["gate"], up_sh=i8["up"], down_sh=i8["down"], q_gate_sh=L.GM_QTYPE_I8,
+                      q_down_sh=L.GM_QTYPE_I8, sh_gate_inp=g_sh)
+    blk_r = GpuMoeBlock(**common)
+    x = torch.from_numpy(synth.host_input(31 + T, T, D))
+    y = blk(x.to(gpu)).cpu().double()
+    y_r = blk_r(x.to(gpu)).cpu().double()
+    assert torch.equal(blk(x.to(gpu)).cpu().double(), y), "repeat calls must be bit-identical"
+    xs = x.double()
+    gs, us, ds = (torch.from_numpy(KQ.dequant(b, q).reshape(shp)).double() for b, q, shp in raw.values())
+    sh = (F.silu(xs @ gs.T) * (xs @ us.T)) @ ds.T
+    sg = torch.sigmoid(xs @ g_sh.double())
+    shared = sg[:, None] * sh
+    err = float((y - y_r - shared).abs().max() / y.abs().max())
+    assert err <= 2e-5, f"shared pass beside the routed GEMMs: {err:.3e}"
+    ol = OM.OracleLayer(h)
+    margin = OM.topk_margin(OM.router_logits64(x, ol), k)
+    clear = margin > 1e-5
+    assert int(clear.sum()) >= T - 2
+    ref = OM.block_forward(x, ol).double() + shared
+    rel = float((y[clear] - ref[clear]).abs().max() / ref[clear].abs().max())
+    assert rel <= REL_TOL, rel
