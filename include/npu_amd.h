@@ -238,6 +238,77 @@ int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float
  */
 int gm_moe_chain_fused(const gm_moe_layer* layers, int n_layers, int T);
 
+/*
+ * The core layers beside the MoE block in every decoder layer, one decode
+ * token (qwen/forward.py:834-893 runs x = x + core(x) and then the MoE step).
+ * fp32 activations and state; the large projections are bf16 weights, as the
+ * reference's NPU operators stage them for these sites (qwen/forward.py:813-831).
+ */
+
+/* Gated attention layer (the reference's AttnLayer, qwen/forward.py:100-130). */
+typedef struct gm_attn_layer {
+  const void* wqkv;         /* bf16 [(2 n_head + 2 n_head_kv) head_dim][D]: attn_q (q and gate
+                               interleaved per head, [q_h | gate_h]), then attn_k, then attn_v */
+  const void* wo;           /* bf16 [D][n_head head_dim] (attn_output) */
+  const float* attn_norm;   /* [D] */
+  const float* q_norm;      /* [head_dim] */
+  const float* k_norm;      /* [head_dim] */
+  float eps;
+  int32_t D, n_head, n_head_kv, head_dim, rope_dim;
+} gm_attn_layer;
+
+/* Workspace bytes of gm_attn_decode for caches of max_pos positions (0 on bad arguments). */
+size_t gm_attn_workspace_bytes(const gm_attn_layer* L, int max_pos);
+
+/*
+ * y = attn(x) (+ x with GM_MOE_RESIDUAL) for one token at position pos:
+ * RMSNorm, the q / gate / k / v projection, per-head RMSNorm of q and k,
+ * partial RoPE with rows pos of rope_cos / rope_sin ([max_pos][rope_dim], the
+ * reference's build_partial_rope_cache tables), k and v written to row pos of
+ * k_cache / v_cache ([max_pos][n_head_kv][head_dim] fp32: one row per kv head,
+ * the reference repeats each kv head over its n_head / n_head_kv q heads), the
+ * softmax over positions 0 .. pos, the output times sigmoid(gate), and wo.
+ * head_dim in {64, 128, 256, 512}, rope_dim even and <= head_dim, D and
+ * n_head head_dim multiples of 32.  x and y must not alias.
+ * Replaces qwen/forward.py:attn_forward (133-239) at T = 1.
+ */
+int gm_attn_decode(const gm_attn_layer* L, const float* x, float* y, float* k_cache, float* v_cache, int pos,
+                   int max_pos, const float* rope_cos, const float* rope_sin, int flags, void* ws, size_t ws_bytes,
+                   void* stream);
+
+/* Gated DeltaNet layer (the reference's SSMLayer, qwen/forward.py:242-284). */
+typedef struct gm_ssm_layer {
+  const void* w_in;         /* bf16 [2 n_k_heads d_state + n_v_heads d_state][D] (attn_qkv) */
+  const void* w_gate;       /* bf16 [n_v_heads d_state][D] (attn_gate) */
+  const void* w_out;        /* bf16 [D][n_v_heads d_state] (ssm_out) */
+  const float* alpha;       /* [n_v_heads][D] (ssm_alpha) */
+  const float* beta;        /* [n_v_heads][D] (ssm_beta) */
+  const float* conv1d;      /* [conv channels][conv_k] (ssm_conv1d) */
+  const float* a;           /* [n_v_heads] (ssm_a) */
+  const float* dt_bias;     /* [n_v_heads] (ssm_dt.bias) */
+  const float* ssm_norm;    /* [d_state] */
+  const float* attn_norm;   /* [D] */
+  float eps;
+  int32_t D, n_k_heads, n_v_heads, d_state, conv_k;
+} gm_ssm_layer;
+
+/* Workspace bytes of gm_ssm_decode (0 on bad arguments). */
+size_t gm_ssm_workspace_bytes(const gm_ssm_layer* L);
+
+/*
+ * y = ssm(x) (+ x with GM_MOE_RESIDUAL) for one token, updating in place
+ * conv_state ([conv channels][conv_k - 1] fp32) and rec_state ([n_v_heads]
+ * [d_state][d_state] fp32, the reference's [H][K][V] layout).  d_state in {64,
+ * 128, 256}, n_v_heads a multiple of n_k_heads, conv_k in 1 .. 8.  x and y must
+ * not alias.  Replaces qwen/forward.py:ssm_forward (292-431) at T = 1.
+ */
+int gm_ssm_decode(const gm_ssm_layer* L, const float* x, float* y, float* conv_state, float* rec_state, int flags,
+                  void* ws, size_t ws_bytes, void* stream);
+
+/* y[r] = rmsnorm(x[r], w, eps) for n_rows rows of D (qwen/forward.py:58-61; the
+ * decoder's output norm, :887-888). */
+int gm_rms_norm(const float* x, const float* w, int D, int n_rows, float eps, float* y, void* stream);
+
 /* Size of the static scratch gm_moe_forward_noalloc works in: 16 MiB per GPU. */
 #define GM_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
 

@@ -57,6 +57,27 @@ class GmMoeLayer(ctypes.Structure):
     ]
 
 
+class GmAttnLayer(ctypes.Structure):
+    """Mirror of ``gm_attn_layer`` (include/npu_amd.h)."""
+
+    _fields_ = [
+        ("wqkv", _vp), ("wo", _vp), ("attn_norm", _vp), ("q_norm", _vp), ("k_norm", _vp),
+        ("eps", _f32),
+        ("D", _i32), ("n_head", _i32), ("n_head_kv", _i32), ("head_dim", _i32), ("rope_dim", _i32),
+    ]
+
+
+class GmSsmLayer(ctypes.Structure):
+    """Mirror of ``gm_ssm_layer`` (include/npu_amd.h)."""
+
+    _fields_ = [
+        ("w_in", _vp), ("w_gate", _vp), ("w_out", _vp), ("alpha", _vp), ("beta", _vp), ("conv1d", _vp),
+        ("a", _vp), ("dt_bias", _vp), ("ssm_norm", _vp), ("attn_norm", _vp),
+        ("eps", _f32),
+        ("D", _i32), ("n_k_heads", _i32), ("n_v_heads", _i32), ("d_state", _i32), ("conv_k", _i32),
+    ]
+
+
 # name -> (restype, argtypes); every symbol include/npu_amd.h declares.
 SIGNATURES = {
     "gm_last_error": (ctypes.c_char_p, []),
@@ -78,6 +99,12 @@ SIGNATURES = {
     "gm_moe_chain": (_i32, [ctypes.POINTER(GmMoeLayer), _i32, _vp, _vp, _vp, _i32, _i32,
                             ctypes.POINTER(_vp), ctypes.POINTER(_sz), _vp]),
     "gm_moe_chain_fused": (_i32, [ctypes.POINTER(GmMoeLayer), _i32, _i32]),
+    "gm_attn_workspace_bytes": (_sz, [ctypes.POINTER(GmAttnLayer), _i32]),
+    "gm_attn_decode": (_i32, [ctypes.POINTER(GmAttnLayer), _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _i32, _vp,
+                              _sz, _vp]),
+    "gm_ssm_workspace_bytes": (_sz, [ctypes.POINTER(GmSsmLayer)]),
+    "gm_ssm_decode": (_i32, [ctypes.POINTER(GmSsmLayer), _vp, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
+    "gm_rms_norm": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp]),
 }
 
 _LIB: ctypes.CDLL | None = None
@@ -94,7 +121,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(h, name)
             fn.restype = res
             fn.argtypes = args
-        if h.gm_abi_version() != 5:
+        if h.gm_abi_version() != 6:
             raise RuntimeError("libnpu_amd.so ABI version mismatch; rebuild it")
         _LIB = h
     return _LIB

@@ -25,7 +25,7 @@ LIB = HERE / "libnpu_amd.so"
 LIB_TL = HERE / "libnpu_amd_tl.so"
 LIB_ASAN = HERE / "libnpu_amd_asan.so"
 SOURCES = ["capi.hip", "matvec.hip", "router.hip", "moe_decode.hip", "moe_decode_gu.hip", "moe_decode_dn.hip",
-           "dispatch.hip", "prefill.hip", "mv_bf16.hip"]
+           "dispatch.hip", "prefill.hip", "mv_bf16.hip", "core_decode.hip"]
 ARCH = os.environ.get("NPU_AMD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

@@ -95,7 +95,7 @@ extern "C" {
 
 const char* gm_last_error(void) { return g_err; }
 
-int gm_abi_version(void) { return 5; }
+int gm_abi_version(void) { return 6; }
 
 int gm_dequant_f32(int qtype, const void* raw, int64_t n_superblocks, float* out, void* stream) {
   if (gm_kquant_block(qtype).bytes)
@@ -304,6 +304,102 @@ int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float
     in = out;
   }
   return GM_OK;
+}
+
+// ------------------------------------------------------------ core layers
+static int check_attn(const gm_attn_layer* L) {
+  if (!L) return gm_fail_arg("gm_attn_decode: layer is NULL");
+  if (!L->wqkv || !L->wo || !L->attn_norm || !L->q_norm || !L->k_norm)
+    return gm_fail_arg("gm_attn_decode: weights and norms must be non-NULL");
+  const int Dh = L->head_dim;
+  if (Dh != 64 && Dh != 128 && Dh != 256 && Dh != 512)
+    return gm_fail_arg("gm_attn_decode: head_dim=%d must be 64, 128, 256 or 512", Dh);
+  if (L->n_head <= 0 || L->n_head_kv <= 0 || L->n_head % L->n_head_kv)
+    return gm_fail_arg("gm_attn_decode: n_head=%d must be a positive multiple of n_head_kv=%d", L->n_head,
+                       L->n_head_kv);
+  if (L->rope_dim < 0 || L->rope_dim % 2 || L->rope_dim > Dh)
+    return gm_fail_arg("gm_attn_decode: rope_dim=%d must be even and <= head_dim", L->rope_dim);
+  if (L->D <= 0 || L->D % GM_SUB || L->D > 16384 || (L->n_head * Dh) > 16384)
+    return gm_fail_arg("gm_attn_decode: D=%d must be a multiple of 32 up to 16384", L->D);
+  if (!(L->eps >= 0.f)) return gm_fail_arg("gm_attn_decode: eps must be >= 0");
+  if (reinterpret_cast<uintptr_t>(L->wqkv) % 16 || reinterpret_cast<uintptr_t>(L->wo) % 16)
+    return gm_fail_arg("gm_attn_decode: wqkv and wo must be 16-byte aligned");
+  return GM_OK;
+}
+
+static int check_ssm(const gm_ssm_layer* L) {
+  if (!L) return gm_fail_arg("gm_ssm_decode: layer is NULL");
+  if (!L->w_in || !L->w_gate || !L->w_out || !L->alpha || !L->beta || !L->conv1d || !L->a || !L->dt_bias ||
+      !L->ssm_norm || !L->attn_norm)
+    return gm_fail_arg("gm_ssm_decode: weights must be non-NULL");
+  const int S = L->d_state;
+  if (S != 64 && S != 128 && S != 256) return gm_fail_arg("gm_ssm_decode: d_state=%d must be 64, 128 or 256", S);
+  if (L->n_k_heads <= 0 || L->n_v_heads <= 0 || L->n_v_heads % L->n_k_heads)
+    return gm_fail_arg("gm_ssm_decode: n_v_heads=%d must be a positive multiple of n_k_heads=%d", L->n_v_heads,
+                       L->n_k_heads);
+  if (L->conv_k < 1 || L->conv_k > 8) return gm_fail_arg("gm_ssm_decode: conv_k=%d must be in 1..8", L->conv_k);
+  if (L->D <= 0 || L->D % GM_SUB || L->D > 16384 || L->n_v_heads * S > 16384)
+    return gm_fail_arg("gm_ssm_decode: D=%d must be a multiple of 32 up to 16384", L->D);
+  if (!(L->eps >= 0.f)) return gm_fail_arg("gm_ssm_decode: eps must be >= 0");
+  const void* w[] = {L->w_in, L->w_gate, L->w_out};
+  for (const void* p : w)
+    if (reinterpret_cast<uintptr_t>(p) % 16) return gm_fail_arg("gm_ssm_decode: bf16 weights must be 16-byte aligned");
+  return GM_OK;
+}
+
+static int check_io(const char* fn, const float* x, const float* y) {
+  if (!x || !y) return gm_fail_arg("%s: NULL x or y", fn);
+  if (x == y) return gm_fail_arg("%s: x and y must not alias", fn);
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 16)
+    return gm_fail_arg("%s: x and y must be 16-byte aligned", fn);
+  return GM_OK;
+}
+
+size_t gm_attn_workspace_bytes(const gm_attn_layer* L, int max_pos) {
+  if (max_pos < 1 || check_attn(L) != GM_OK) return 0;
+  return gm_attn_ws_layout(L, max_pos).total;
+}
+
+int gm_attn_decode(const gm_attn_layer* L, const float* x, float* y, float* k_cache, float* v_cache, int pos,
+                   int max_pos, const float* rope_cos, const float* rope_sin, int flags, void* ws, size_t ws_bytes,
+                   void* stream) {
+  if (int rc = check_attn(L)) return rc;
+  if (int rc = check_io("gm_attn_decode", x, y)) return rc;
+  if (max_pos < 1 || pos < 0 || pos >= max_pos)
+    return gm_fail_arg("gm_attn_decode: pos=%d must be in [0, max_pos=%d)", pos, max_pos);
+  if (!k_cache || !v_cache || !ws || (L->rope_dim > 0 && (!rope_cos || !rope_sin)))
+    return gm_fail_arg("gm_attn_decode: NULL cache, rope table or workspace");
+  const size_t need = gm_attn_ws_layout(L, max_pos).total;
+  if (ws_bytes < need)
+    return gm_fail_arg("gm_attn_decode: workspace %zu bytes < %zu needed", ws_bytes, need), GM_EWORKSPACE;
+  if (reinterpret_cast<uintptr_t>(ws) % 256) return gm_fail_arg("gm_attn_decode: workspace must be 256-byte aligned");
+  return gm_attn_run(L, x, y, k_cache, v_cache, pos, max_pos, rope_cos, rope_sin, flags, static_cast<uint8_t*>(ws),
+                     as_stream(stream));
+}
+
+size_t gm_ssm_workspace_bytes(const gm_ssm_layer* L) {
+  if (check_ssm(L) != GM_OK) return 0;
+  return gm_ssm_ws_layout(L).total;
+}
+
+int gm_ssm_decode(const gm_ssm_layer* L, const float* x, float* y, float* conv_state, float* rec_state, int flags,
+                  void* ws, size_t ws_bytes, void* stream) {
+  if (int rc = check_ssm(L)) return rc;
+  if (int rc = check_io("gm_ssm_decode", x, y)) return rc;
+  if (!rec_state || !ws || (L->conv_k > 1 && !conv_state))
+    return gm_fail_arg("gm_ssm_decode: NULL state or workspace");
+  const size_t need = gm_ssm_ws_layout(L).total;
+  if (ws_bytes < need)
+    return gm_fail_arg("gm_ssm_decode: workspace %zu bytes < %zu needed", ws_bytes, need), GM_EWORKSPACE;
+  if (reinterpret_cast<uintptr_t>(ws) % 256) return gm_fail_arg("gm_ssm_decode: workspace must be 256-byte aligned");
+  return gm_ssm_run(L, x, y, conv_state, rec_state, flags, static_cast<uint8_t*>(ws), as_stream(stream));
+}
+
+int gm_rms_norm(const float* x, const float* w, int D, int n_rows, float eps, float* y, void* stream) {
+  if (D <= 0 || n_rows < 0 || !(eps >= 0.f)) return gm_fail_arg("gm_rms_norm: bad sizes or eps");
+  if (n_rows == 0) return GM_OK;
+  if (!x || !w || !y) return gm_fail_arg("gm_rms_norm: NULL pointer");
+  return gm_launch_rms_row(x, w, D, n_rows, eps, y, as_stream(stream));
 }
 
 }  // extern "C"

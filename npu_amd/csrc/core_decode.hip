@@ -1,0 +1,397 @@
+// One decode token through the Qwen3-Next core layers that sit beside the MoE
+// block in every decoder layer (qwen/forward.py:834-893): gated attention
+// (:133-239) and the Gated DeltaNet SSM (:292-431).  fp32 state and
+// activations; the large projections are bf16 weights (the reference's NPU
+// operators for these sites stage bf16, qwen/forward.py:813-831) on the bf16
+// matvec kernels of mv_bf16.hip, the small alpha / beta projections fp32.
+//
+// Attention, one token at position pos (gm_attn_decode):
+//   k_rms_row        h = rmsnorm(x, attn_norm)
+//   mv_bf16          qkv = Wqkv h  ([q_h | gate_h] per head, then k, then v)
+//   k_attn_prep      per head: RMSNorm of q / k over head_dim, partial RoPE at
+//                    pos; k and v written to the caches at row pos
+//   k_attn_part      per (q head, chunk of cached positions): online softmax
+//                    partials (max, sum, weighted v) of q . k / sqrt(Dh)
+//   k_attn_combine   per q head: the partials merged, times sigmoid(gate)
+//   mv_bf16 (+ x)    y = Wo out (+ x)
+// Gated DeltaNet, one token (gm_ssm_decode):
+//   k_rms_row        h = rmsnorm(x, attn_norm)
+//   mv_bf16 x2       mixed = W_in h, z = W_gate h
+//   k_ssm_ab         g = softplus(alpha h + dt_bias) a, beta = sigmoid(beta h)
+//   k_ssm_conv       depthwise causal conv (kernel conv_k) over [state, mixed],
+//                    SiLU, the state shifted; q and k heads L2-normalised, q
+//                    times 1/sqrt(Sk)
+//   k_ssm_rec        per (V head, 32 state columns): S = S exp(g),
+//                    d = (v - S^T k) beta, S += k d^T, o = S^T q; the state
+//                    [Hv][Sk][Sv] (the reference's layout) updated in place
+//   k_ssm_gnorm      rmsnorm(o_head, ssm_norm) * silu(z)
+//   mv_bf16 (+ x)    y = W_out o (+ x)
+// No kernel holds a scratch buffer of its own: intermediates live in the
+// caller's workspace (gm_attn_ws_layout / gm_ssm_ws_layout).
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+constexpr int kAttnChunk = 64;     // cached positions per attention partial
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = gm_wave_sum64(v);
+  const int wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  __syncthreads();                                            // red reused across calls
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int w = 0; w < nw; ++w) s += red[w];
+  return s;
+}
+
+// ------------------------------------------------------------ RMSNorm row
+// y = (x * rsqrt(mean(x^2) + eps)) * w (qwen/forward.py:58-61); one block per row.
+__global__ void __launch_bounds__(256) k_rms_row(const float* __restrict__ x, const float* __restrict__ w, int D,
+                                                 float eps, float* __restrict__ y) {
+  __shared__ float red[4];
+  x += (size_t)blockIdx.x * D;
+  y += (size_t)blockIdx.x * D;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < D; i += 256) ss = fmaf(x[i], x[i], ss);
+  const float r = 1.0f / sqrtf(block_sum(ss, red) / (float)D + eps);
+  for (int i = threadIdx.x; i < D; i += 256) y[i] = (x[i] * r) * w[i];
+}
+
+// ------------------------------------------------------------ attention
+// One block per head, blockDim = Dh (one value per thread).  Blocks 0..Hq-1:
+// q head b = qkv[2 Dh b ..] (its gate follows at + Dh), RMSNorm with q_norm,
+// RoPE -> qr[b]; blocks Hq..Hq+Hkv-1: k / v head j -> the caches' row pos.
+// RoPE (qwen/forward.py:81-97): lane i < rd/2 pairs with i + rd/2:
+// out_i = x_i cos_i - x_{i+h} sin_i, out_{i+h} = x_{i+h} cos_{i+h} + x_i sin_{i+h}.
+__global__ void k_attn_prep(const float* __restrict__ qkv, const float* __restrict__ q_norm,
+                            const float* __restrict__ k_norm, float eps, int Hq, int Hkv, int Dh, int rd,
+                            const float* __restrict__ cosr, const float* __restrict__ sinr,
+                            float* __restrict__ qr, float* __restrict__ kc, float* __restrict__ vc) {
+  extern __shared__ float sm[];                                 // [Dh] normalised row + [16] reduction
+  float* row = sm;
+  float* red = sm + Dh;
+  const int b = blockIdx.x, i = threadIdx.x;
+  const bool isq = b < Hq;
+  const float* src = isq ? qkv + (size_t)2 * Dh * b : qkv + (size_t)2 * Dh * Hq + (size_t)Dh * (b - Hq);
+  const float v = src[i];
+  const float r = 1.0f / sqrtf(block_sum(v * v, red) / (float)Dh + eps);
+  const float n = (v * r) * (isq ? q_norm[i] : k_norm[i]);
+  row[i] = n;
+  __syncthreads();
+  float o = n;
+  const int h = rd >> 1;
+  if (i < rd) {
+    const float other = i < h ? -row[i + h] : row[i - h];
+    o = n * cosr[i] + other * sinr[i];
+  }
+  if (isq) {
+    qr[(size_t)Dh * b + i] = o;
+  } else {
+    const int j = b - Hq;
+    kc[(size_t)Dh * j + i] = o;
+    vc[(size_t)Dh * j + i] = qkv[(size_t)2 * Dh * Hq + (size_t)Dh * Hkv + (size_t)Dh * j + i];
+  }
+}
+
+// Partial attention of q head hq over cached positions [c0, c0 + kAttnChunk)
+// (clipped to n = pos + 1): 4 waves, each lane holding DV = Dh / 64 dims; wave
+// w takes positions c0 + w, c0 + w + 4, ...  Per position the score
+// s = (q . k) / sqrt(Dh) (a wave sum), then the online softmax update
+// m' = max(m, s), l = l e^(m - m') + e^(s - m'), acc = acc e^(m - m') + e^(s - m') v.
+// The 4 waves' states are merged in LDS; part[hq][chunk] = {m, l, acc[Dh]}.
+template <int DV>
+__global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ qr, const float* __restrict__ kc,
+                                                   const float* __restrict__ vc, int Hq, int Hkv, int n,
+                                                   float scale, float* __restrict__ part, int ld) {
+  __shared__ float ms[4], ls[4];
+  __shared__ float accs[4][64 * DV];
+  const int hq = blockIdx.x, chunk = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int Dh = 64 * DV, hk = hq / (Hq / Hkv), c0 = chunk * kAttnChunk;
+  const int c1 = min(c0 + kAttnChunk, n);
+  float q[DV], acc[DV];
+#pragma unroll
+  for (int d = 0; d < DV; ++d) { q[d] = qr[(size_t)Dh * hq + lane + 64 * d]; acc[d] = 0.f; }
+  float m = -__builtin_inff(), l = 0.f;
+  for (int t = c0 + wave; t < c1; t += 4) {
+    const float* kt = kc + ((size_t)t * Hkv + hk) * Dh;
+    const float* vt = vc + ((size_t)t * Hkv + hk) * Dh;
+    float kv[DV], vv[DV];
+#pragma unroll
+    for (int d = 0; d < DV; ++d) { kv[d] = kt[lane + 64 * d]; vv[d] = vt[lane + 64 * d]; }
+    float s = 0.f;
+#pragma unroll
+    for (int d = 0; d < DV; ++d) s = fmaf(q[d], kv[d], s);
+    s = gm_wave_sum64(s) * scale;
+    const float mn = fmaxf(m, s);
+    const float a = expf(m - mn), p = expf(s - mn);
+    l = l * a + p;
+#pragma unroll
+    for (int d = 0; d < DV; ++d) acc[d] = fmaf(acc[d], a, p * vv[d]);
+    m = mn;
+  }
+  if (lane == 0) { ms[wave] = m; ls[wave] = l; }
+#pragma unroll
+  for (int d = 0; d < DV; ++d) accs[wave][lane + 64 * d] = acc[d];
+  __syncthreads();
+  if (wave == 0) {
+    const float M = fmaxf(fmaxf(ms[0], ms[1]), fmaxf(ms[2], ms[3]));
+    float f[4], L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) { f[w] = ms[w] == -__builtin_inff() ? 0.f : expf(ms[w] - M); L = fmaf(ls[w], f[w], L); }
+    float* out = part + ((size_t)hq * ld + chunk) * (Dh + 2);
+#pragma unroll
+    for (int d = 0; d < DV; ++d) {
+      float o = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) o = fmaf(accs[w][lane + 64 * d], f[w], o);
+      out[2 + lane + 64 * d] = o;
+    }
+    if (lane == 0) { out[0] = M; out[1] = L; }
+  }
+}
+
+// out[hq][i] = (sum_c acc_c[i] e^(m_c - M)) / (sum_c l_c e^(m_c - M)) * sigmoid(gate);
+// one block per q head, blockDim = Dh.
+__global__ void k_attn_combine(const float* __restrict__ part, int ld, int nch, const float* __restrict__ qkv,
+                               int Dh, float* __restrict__ out) {
+  const int hq = blockIdx.x, i = threadIdx.x;
+  const float* p = part + (size_t)hq * ld * (Dh + 2);
+  float M = -__builtin_inff();
+  for (int c = 0; c < nch; ++c) M = fmaxf(M, p[(size_t)c * (Dh + 2)]);
+  float L = 0.f, o = 0.f;
+  for (int c = 0; c < nch; ++c) {
+    const float* pc = p + (size_t)c * (Dh + 2);
+    const float f = expf(pc[0] - M);
+    L = fmaf(pc[1], f, L);
+    o = fmaf(pc[2 + i], f, o);
+  }
+  const float g = qkv[(size_t)2 * Dh * hq + Dh + i];
+  out[(size_t)Dh * hq + i] = (o / L) * (1.0f / (1.0f + expf(-g)));
+}
+
+// ------------------------------------------------------------ Gated DeltaNet
+// Rows 0..Hv-1: alpha, Hv..2Hv-1: beta (fp32 weights [Hv][D]); one wave per row.
+// g = softplus(alpha . h + dt_bias) * a (torch's softplus: x above 20 passes
+// through, else log1p(exp(x))), beta = sigmoid(beta . h).
+__global__ void __launch_bounds__(256) k_ssm_ab(const float* __restrict__ alpha, const float* __restrict__ beta,
+                                                const float* __restrict__ dt_bias, const float* __restrict__ a,
+                                                const float* __restrict__ h, int D, int Hv, float* __restrict__ gb) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (r >= 2 * Hv) return;
+  const float* w = r < Hv ? alpha + (size_t)r * D : beta + (size_t)(r - Hv) * D;
+  float s = 0.f;
+  for (int i = lane; i < D; i += 64) s = fmaf(w[i], h[i], s);
+  s = gm_wave_sum64(s);
+  if (lane == 0) {
+    if (r < Hv) {
+      const float u = s + dt_bias[r];
+      gb[r] = (u > 20.f ? u : log1pf(expf(u))) * a[r];
+    } else {
+      gb[r] = 1.0f / (1.0f + expf(-s));
+    }
+  }
+}
+
+// One block per group of Sk channels (blockDim = Sk): the depthwise causal
+// conv out_c = sum_j w[c][j] in_c[j] over in_c = [state_c[0 .. ck-2], mixed_c],
+// SiLU; the state shifted by one (mixed_c last).  Blocks 0..Hk-1 (q heads) and
+// Hk..2Hk-1 (k heads) are L2-normalised (x / sqrt(max(sum x^2, eps))), q then
+// times 1/sqrt(Sk).
+__global__ void k_ssm_conv(const float* __restrict__ mixed, const float* __restrict__ w, float* __restrict__ state,
+                           int ck, int Hk, int Sk, float eps, float* __restrict__ conv) {
+  __shared__ float red[16];
+  const int c = blockIdx.x * Sk + threadIdx.x, g = blockIdx.x;
+  float* st = state + (size_t)c * (ck - 1);
+  const float* wc = w + (size_t)c * ck;
+  const float xin = mixed[c];
+  float acc = 0.f;
+  for (int j = 0; j < ck - 1; ++j) acc = fmaf(wc[j], st[j], acc);
+  acc = fmaf(wc[ck - 1], xin, acc);
+  for (int j = 0; j + 1 < ck - 1; ++j) st[j] = st[j + 1];
+  if (ck > 1) st[ck - 2] = xin;
+  float v = acc / (1.0f + expf(-acc));
+  if (g < 2 * Hk) {                                              // block-uniform
+    const float ss = block_sum(v * v, red);
+    v = v / sqrtf(fmaxf(ss, eps));
+    if (g < Hk) v = v * (1.0f / sqrtf((float)Sk));
+  }
+  conv[c] = v;
+}
+
+// Delta rule for V head hv, state columns v0 .. v0 + 31 (blockDim = 32 x KG):
+// thread (kg, col) holds rows kg SPT .. + SPT - 1 of column col of
+// S[hv][k][v] (row-major [Sk][Sv], the reference's layout).  K / Q head
+// hv % Hk (the reference tiles the Hk heads over the Hv heads).
+template <int SPT>
+__global__ void __launch_bounds__(256) k_ssm_rec(float* __restrict__ S, const float* __restrict__ conv,
+                                                 const float* __restrict__ gb, int Hk, int Hv, int Sk, int Sv,
+                                                 float* __restrict__ o) {
+  __shared__ float red[8][33];
+  __shared__ float dsh[32];
+  const int hv = blockIdx.x, col = threadIdx.x & 31, kg = threadIdx.x >> 5, v = blockIdx.y * 32 + col;
+  const int hk = hv % Hk, Ck = Hk * Sk;
+  const float* q = conv + (size_t)hk * Sk;
+  const float* k = conv + (size_t)Ck + (size_t)hk * Sk;
+  const float vv = conv[(size_t)2 * Ck + (size_t)hv * Sv + v];
+  const float decay = expf(gb[hv]), bt = gb[Hv + hv];
+  float* Sc = S + (size_t)hv * Sk * Sv + v;
+  float s[SPT], kk[SPT], qq[SPT];
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+    const int r = kg * SPT + j;
+    s[j] = Sc[(size_t)r * Sv] * decay;
+    kk[j] = k[r];
+    qq[j] = q[r];
+  }
+  float p = 0.f;
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) p = fmaf(s[j], kk[j], p);
+  red[kg][col] = p;
+  __syncthreads();
+  if (kg == 0) {
+    float sk = 0.f;
+    for (int g = 0; g < 8; ++g) sk += red[g][col];
+    dsh[col] = (vv - sk) * bt;
+  }
+  __syncthreads();
+  const float d = dsh[col];
+  p = 0.f;
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+    s[j] = fmaf(kk[j], d, s[j]);
+    Sc[(size_t)(kg * SPT + j) * Sv] = s[j];
+    p = fmaf(s[j], qq[j], p);
+  }
+  __syncthreads();
+  red[kg][col] = p;
+  __syncthreads();
+  if (kg == 0) {
+    float ov = 0.f;
+    for (int g = 0; g < 8; ++g) ov += red[g][col];
+    o[(size_t)hv * Sv + v] = ov;
+  }
+}
+
+// rmsnorm(o_head, ssm_norm) * silu(z) per V head (blockDim = Sv).
+__global__ void k_ssm_gnorm(const float* __restrict__ o, const float* __restrict__ nw, const float* __restrict__ z,
+                            int Sv, float eps, float* __restrict__ out) {
+  __shared__ float red[16];
+  const size_t i = (size_t)blockIdx.x * Sv + threadIdx.x;
+  const float v = o[i];
+  const float r = 1.0f / sqrtf(block_sum(v * v, red) / (float)Sv + eps);
+  const float zi = z[i];
+  out[i] = ((v * r) * nw[threadIdx.x]) * (zi / (1.0f + expf(-zi)));
+}
+
+}  // namespace
+
+// ------------------------------------------------------------ host side
+GmAttnWs gm_attn_ws_layout(const gm_attn_layer* L, int max_pos) {
+  GmAttnWs w{};
+  size_t o = 0;
+  const size_t Dh = (size_t)L->head_dim, Hq = (size_t)L->n_head, Hkv = (size_t)L->n_head_kv;
+  const size_t nch = ((size_t)max_pos + kAttnChunk - 1) / kAttnChunk;
+  w.h = o; o = align256(o + (size_t)L->D * 4);
+  w.qkv = o; o = align256(o + (2 * Hq + 2 * Hkv) * Dh * 4);
+  w.qr = o; o = align256(o + Hq * Dh * 4);
+  w.part = o; o = align256(o + Hq * nch * (Dh + 2) * 4);
+  w.out = o; o = align256(o + Hq * Dh * 4);
+  w.nch = (int)nch;
+  w.total = o;
+  return w;
+}
+
+int gm_attn_run(const gm_attn_layer* L, const float* x, float* y, float* kc, float* vc, int pos, int max_pos,
+                const float* cosr, const float* sinr, int flags, uint8_t* ws, hipStream_t s) {
+  const GmAttnWs lay = gm_attn_ws_layout(L, max_pos);
+  const int D = L->D, Hq = L->n_head, Hkv = L->n_head_kv, Dh = L->head_dim, rd = L->rope_dim;
+  float* h = reinterpret_cast<float*>(ws + lay.h);
+  float* qkv = reinterpret_cast<float*>(ws + lay.qkv);
+  float* qr = reinterpret_cast<float*>(ws + lay.qr);
+  float* part = reinterpret_cast<float*>(ws + lay.part);
+  float* out = reinterpret_cast<float*>(ws + lay.out);
+  hipLaunchKernelGGL(k_rms_row, dim3(1), dim3(256), 0, s, x, L->attn_norm, D, L->eps, h);
+  GM_TRY(hipGetLastError());
+  const int Mqkv = (2 * Hq + 2 * Hkv) * Dh;
+  if (int rc = gm_launch_mv_bf16(static_cast<const uint16_t*>(L->wqkv), Mqkv, D, h, 1, qkv, s)) return rc;
+  hipLaunchKernelGGL(k_attn_prep, dim3(Hq + Hkv), dim3(Dh), (Dh + 16) * sizeof(float), s, qkv, L->q_norm,
+                     L->k_norm, L->eps, Hq, Hkv, Dh, rd, cosr + (size_t)pos * rd, sinr + (size_t)pos * rd, qr,
+                     kc + (size_t)pos * Hkv * Dh, vc + (size_t)pos * Hkv * Dh);
+  GM_TRY(hipGetLastError());
+  const int n = pos + 1, nch = (n + kAttnChunk - 1) / kAttnChunk;
+  const float scale = 1.0f / sqrtf((float)Dh);
+  const dim3 g(Hq, nch);
+  switch (Dh / 64) {
+    case 1: hipLaunchKernelGGL(k_attn_part<1>, g, dim3(256), 0, s, qr, kc, vc, Hq, Hkv, n, scale, part, lay.nch); break;
+    case 2: hipLaunchKernelGGL(k_attn_part<2>, g, dim3(256), 0, s, qr, kc, vc, Hq, Hkv, n, scale, part, lay.nch); break;
+    case 4: hipLaunchKernelGGL(k_attn_part<4>, g, dim3(256), 0, s, qr, kc, vc, Hq, Hkv, n, scale, part, lay.nch); break;
+    default: hipLaunchKernelGGL(k_attn_part<8>, g, dim3(256), 0, s, qr, kc, vc, Hq, Hkv, n, scale, part, lay.nch); break;
+  }
+  GM_TRY(hipGetLastError());
+  hipLaunchKernelGGL(k_attn_combine, dim3(Hq), dim3(Dh), 0, s, part, lay.nch, nch, qkv, Dh, out);
+  GM_TRY(hipGetLastError());
+  return gm_launch_mv_bf16_add(static_cast<const uint16_t*>(L->wo), D, Hq * Dh, out, y,
+                               (flags & GM_MOE_RESIDUAL) ? x : nullptr, s);
+}
+
+GmSsmWs gm_ssm_ws_layout(const gm_ssm_layer* L) {
+  GmSsmWs w{};
+  size_t o = 0;
+  const size_t Ck = (size_t)L->n_k_heads * L->d_state, di = (size_t)L->n_v_heads * L->d_state;
+  const size_t C = 2 * Ck + di;
+  w.h = o; o = align256(o + (size_t)L->D * 4);
+  w.mixed = o; o = align256(o + C * 4);
+  w.z = o; o = align256(o + di * 4);
+  w.gb = o; o = align256(o + 2 * (size_t)L->n_v_heads * 4);
+  w.conv = o; o = align256(o + C * 4);
+  w.o = o; o = align256(o + di * 4);
+  w.o2 = o; o = align256(o + di * 4);
+  w.total = o;
+  return w;
+}
+
+int gm_ssm_run(const gm_ssm_layer* L, const float* x, float* y, float* conv_state, float* rec_state, int flags,
+               uint8_t* ws, hipStream_t s) {
+  const GmSsmWs lay = gm_ssm_ws_layout(L);
+  const int D = L->D, Hk = L->n_k_heads, Hv = L->n_v_heads, Sk = L->d_state, Sv = L->d_state;
+  const int Ck = Hk * Sk, di = Hv * Sv, C = 2 * Ck + di;
+  float* h = reinterpret_cast<float*>(ws + lay.h);
+  float* mixed = reinterpret_cast<float*>(ws + lay.mixed);
+  float* z = reinterpret_cast<float*>(ws + lay.z);
+  float* gb = reinterpret_cast<float*>(ws + lay.gb);
+  float* conv = reinterpret_cast<float*>(ws + lay.conv);
+  float* o = reinterpret_cast<float*>(ws + lay.o);
+  float* o2 = reinterpret_cast<float*>(ws + lay.o2);
+  hipLaunchKernelGGL(k_rms_row, dim3(1), dim3(256), 0, s, x, L->attn_norm, D, L->eps, h);
+  GM_TRY(hipGetLastError());
+  if (int rc = gm_launch_mv_bf16(static_cast<const uint16_t*>(L->w_in), C, D, h, 1, mixed, s)) return rc;
+  if (int rc = gm_launch_mv_bf16(static_cast<const uint16_t*>(L->w_gate), di, D, h, 1, z, s)) return rc;
+  hipLaunchKernelGGL(k_ssm_ab, dim3((2 * Hv + 3) / 4), dim3(256), 0, s, L->alpha, L->beta, L->dt_bias, L->a, h, D,
+                     Hv, gb);
+  GM_TRY(hipGetLastError());
+  hipLaunchKernelGGL(k_ssm_conv, dim3(C / Sk), dim3(Sk), 0, s, mixed, L->conv1d, conv_state, L->conv_k, Hk, Sk,
+                     L->eps, conv);
+  GM_TRY(hipGetLastError());
+  const dim3 g(Hv, Sv / 32);
+  switch (Sk / 8) {
+    case 8: hipLaunchKernelGGL(k_ssm_rec<8>, g, dim3(256), 0, s, rec_state, conv, gb, Hk, Hv, Sk, Sv, o); break;
+    case 16: hipLaunchKernelGGL(k_ssm_rec<16>, g, dim3(256), 0, s, rec_state, conv, gb, Hk, Hv, Sk, Sv, o); break;
+    case 32: hipLaunchKernelGGL(k_ssm_rec<32>, g, dim3(256), 0, s, rec_state, conv, gb, Hk, Hv, Sk, Sv, o); break;
+    default: return gm_fail_arg("gm_ssm_decode: d_state=%d must be 64, 128 or 256", Sk);
+  }
+  GM_TRY(hipGetLastError());
+  hipLaunchKernelGGL(k_ssm_gnorm, dim3(Hv), dim3(Sv), 0, s, o, L->ssm_norm, z, Sv, L->eps, o2);
+  GM_TRY(hipGetLastError());
+  return gm_launch_mv_bf16_add(static_cast<const uint16_t*>(L->w_out), D, di, o2, y,
+                               (flags & GM_MOE_RESIDUAL) ? x : nullptr, s);
+}
+
+int gm_launch_rms_row(const float* x, const float* w, int D, int n_rows, float eps, float* y, hipStream_t s) {
+  hipLaunchKernelGGL(k_rms_row, dim3(n_rows), dim3(256), 0, s, x, w, D, eps, y);
+  GM_TRY(hipGetLastError());
+  return GM_OK;
+}

@@ -24,6 +24,25 @@ int gm_launch_matvec(int qtype, const void* w, int M, int K, const float* x, int
 int gm_launch_mv_bf16(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s);
 int gm_launch_gateup(int qtype, const void* wg, const void* wu, int FF, int D, const float* x, int n_tok,
                      float* h, hipStream_t s);
+// One token, y = add + W x (add may be NULL).
+int gm_launch_mv_bf16_add(const uint16_t* w, int M, int K, const float* x, float* y, const float* add,
+                          hipStream_t s);
+int gm_launch_rms_row(const float* x, const float* w, int D, int n_rows, float eps, float* y, hipStream_t s);
+
+// Core-layer decode workspaces (core_decode.hip), byte offsets, 256-byte aligned.
+struct GmAttnWs {
+  size_t h, qkv, qr, part, out, total;
+  int nch;         // attention partial slots per head (max_pos / chunk, rounded up)
+};
+GmAttnWs gm_attn_ws_layout(const gm_attn_layer* L, int max_pos);
+int gm_attn_run(const gm_attn_layer* L, const float* x, float* y, float* kc, float* vc, int pos, int max_pos,
+                const float* cosr, const float* sinr, int flags, uint8_t* ws, hipStream_t s);
+struct GmSsmWs {
+  size_t h, mixed, z, gb, conv, o, o2, total;
+};
+GmSsmWs gm_ssm_ws_layout(const gm_ssm_layer* L);
+int gm_ssm_run(const gm_ssm_layer* L, const float* x, float* y, float* conv_state, float* rec_state, int flags,
+               uint8_t* ws, hipStream_t s);
 
 // MoE workspace layout for T tokens (offsets in bytes, 256-byte aligned).
 struct GmMoeWs {

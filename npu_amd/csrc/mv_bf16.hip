@@ -31,7 +31,8 @@ constexpr int kSlotK = 512;                   // k values per slot (64 lanes x 8
 
 template <int NT, int R, int S>
 __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w, int M, int K,
-                                                 const float* __restrict__ x, int n_tok, float* __restrict__ y) {
+                                                 const float* __restrict__ x, int n_tok, float* __restrict__ y,
+                                                 const float* __restrict__ add) {
   extern __shared__ gm_f32x4 xs4[];                               // [NT][K / 4]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + wave) * R;
@@ -105,7 +106,10 @@ __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w,
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const float v = gm_wave_sum64(acc[r][t]);
-      if (lane == 0 && row0 + r < M && t < nt) y[(int64_t)(t0 + t) * M + row0 + r] = v;
+      if (lane == 0 && row0 + r < M && t < nt) {
+        const int64_t i = (int64_t)(t0 + t) * M + row0 + r;
+        y[i] = add ? add[i] + v : v;                             // y = add + W x (a residual), or W x
+      }
     }
   }
 }
@@ -236,24 +240,26 @@ int launch_mfma(const uint16_t* w, int M, int K, const float* x, int n_tok, floa
 }
 
 template <int NT, int R, int S>
-int launch_mv(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
+int launch_mv(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, const float* add,
+              hipStream_t s) {
   const size_t smem = (size_t)NT * K * sizeof(float);
   if (int rc = gm_set_smem(k_mv_bf16<NT, R, S>, smem)) return rc;
   const dim3 grid((unsigned)((M + 4 * R - 1) / (4 * R)), (unsigned)((n_tok + NT - 1) / NT));
-  hipLaunchKernelGGL((k_mv_bf16<NT, R, S>), grid, dim3(256), smem, s, w, M, K, x, n_tok, y);
+  hipLaunchKernelGGL((k_mv_bf16<NT, R, S>), grid, dim3(256), smem, s, w, M, K, x, n_tok, y, add);
   GM_TRY(hipGetLastError());
   return GM_OK;
 }
 
 // S = the row's slots (at most 16 per pass), one row per wave (the most
 // waves, each with its whole row in flight, was the fastest launch shape).
-int launch_mv1(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
+int launch_mv1(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, const float* add,
+               hipStream_t s) {
   const int slots = (K + kSlotK - 1) / kSlotK;
-  if (slots <= 1) return launch_mv<1, 1, 1>(w, M, K, x, n_tok, y, s);
-  if (slots <= 2) return launch_mv<1, 1, 2>(w, M, K, x, n_tok, y, s);
-  if (slots <= 4) return launch_mv<1, 1, 4>(w, M, K, x, n_tok, y, s);
-  if (slots <= 8) return launch_mv<1, 1, 8>(w, M, K, x, n_tok, y, s);
-  return launch_mv<1, 1, 16>(w, M, K, x, n_tok, y, s);
+  if (slots <= 1) return launch_mv<1, 1, 1>(w, M, K, x, n_tok, y, add, s);
+  if (slots <= 2) return launch_mv<1, 1, 2>(w, M, K, x, n_tok, y, add, s);
+  if (slots <= 4) return launch_mv<1, 1, 4>(w, M, K, x, n_tok, y, add, s);
+  if (slots <= 8) return launch_mv<1, 1, 8>(w, M, K, x, n_tok, y, add, s);
+  return launch_mv<1, 1, 16>(w, M, K, x, n_tok, y, add, s);
 }
 
 }  // namespace
@@ -262,6 +268,12 @@ int launch_mv1(const uint16_t* w, int M, int K, const float* x, int n_tok, float
 // caller).  One token: the streaming FMA kernel; more: the MFMA kernel, 16
 // tokens per column tile.
 int gm_launch_mv_bf16(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
-  if (n_tok == 1) return launch_mv1(w, M, K, x, n_tok, y, s);
+  if (n_tok == 1) return launch_mv1(w, M, K, x, n_tok, y, nullptr, s);
   return launch_mfma(w, M, K, x, n_tok, y, s);
+}
+
+// One token, y = add + W x (the residual of the core layers' output projections).
+int gm_launch_mv_bf16_add(const uint16_t* w, int M, int K, const float* x, float* y, const float* add,
+                          hipStream_t s) {
+  return launch_mv1(w, M, K, x, 1, y, add, s);
 }

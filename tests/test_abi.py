@@ -32,12 +32,14 @@ def test_library_exports_every_declared_symbol():
         assert name in L.SIGNATURES, f"{name} has no ctypes signature in npu_amd._lib"
 
 
-def test_struct_layout_matches_header():
-    fields = re.search(r"typedef struct gm_moe_layer \{(.*?)\} gm_moe_layer;", HEADER, re.S).group(1)
+@pytest.mark.parametrize("cname,mirror", [("gm_moe_layer", "GmMoeLayer"), ("gm_attn_layer", "GmAttnLayer"),
+                                          ("gm_ssm_layer", "GmSsmLayer")])
+def test_struct_layout_matches_header(cname, mirror):
+    fields = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), HEADER, re.S).group(1)
     fields = re.sub(r"/\*.*?\*/", "", fields, flags=re.S)
     names =re.findall(r"(\w+)(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?(?:\s*,\s*(\w+))?;", fields)
     flat = [n for grp in names for n in grp if n]
-    assert flat == [f for f, _ in L.GmMoeLayer._fields_]
+    assert flat == [f for f, _ in getattr(L, mirror)._fields_]
 
 
 def test_argument_errors_without_gpu():
@@ -113,3 +115,31 @@ def test_chain_path_query_without_gpu():
     arr = (L.GmMoeLayer * 2)(a, _layer(k=9))
     assert lib.gm_moe_chain_fused(arr, 2, 1) == L.GM_EINVAL
     assert lib.gm_moe_chain_fused(None, 2, 1) == L.GM_EINVAL
+
+
+def test_core_layer_argument_errors_without_gpu():
+    """gm_attn_decode / gm_ssm_decode reject bad shapes, positions and workspaces before
+    any launch."""
+    lib = L.lib()
+    a = L.GmAttnLayer(wqkv=256, wo=256, attn_norm=256, q_norm=256, k_norm=256, eps=1e-6, D=2048, n_head=16,
+                      n_head_kv=2, head_dim=256, rope_dim=64)
+    n = lib.gm_attn_workspace_bytes(ctypes.byref(a), 4096)
+    assert n > 0 and n % 256 == 0
+    assert lib.gm_attn_workspace_bytes(ctypes.byref(a), 8192) > n
+    bad = L.GmAttnLayer.from_buffer_copy(a)
+    bad.head_dim = 96
+    assert lib.gm_attn_workspace_bytes(ctypes.byref(bad), 4096) == 0 and "head_dim" in L.last_error()
+    rc = lib.gm_attn_decode(ctypes.byref(a), 1024, 2048, 4096, 4096, 4096, 4096, 256, 256, 0, 1 << 20, n, None)
+    assert rc == L.GM_EINVAL and "pos" in L.last_error()
+    rc = lib.gm_attn_decode(ctypes.byref(a), 1024, 2048, 4096, 4096, 3, 4096, 256, 256, 0, 1 << 20, n - 1, None)
+    assert rc == L.GM_EWORKSPACE
+    s = L.GmSsmLayer(w_in=256, w_gate=256, w_out=256, alpha=256, beta=256, conv1d=256, a=256, dt_bias=256,
+                     ssm_norm=256, attn_norm=256, eps=1e-6, D=2048, n_k_heads=16, n_v_heads=32, d_state=128,
+                     conv_k=4)
+    m = lib.gm_ssm_workspace_bytes(ctypes.byref(s))
+    assert m > 0 and m % 256 == 0
+    bad = L.GmSsmLayer.from_buffer_copy(s)
+    bad.n_v_heads = 24
+    assert lib.gm_ssm_workspace_bytes(ctypes.byref(bad), ) == 0 and "multiple" in L.last_error()
+    rc = lib.gm_ssm_decode(ctypes.byref(s), 1024, 1024, 4096, 4096, 0, 1 << 20, m, None)
+    assert rc == L.GM_EINVAL and "alias" in L.last_error()
