@@ -272,7 +272,13 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
 #pragma unroll
         for (int i = 0; i < 8; ++i) p = fmaf(yv[i], yv[i], p);
       }
-      unsafeAtomicAdd(nx.acc + (blockIdx.x & (GM_ACC_COPIES - 1)) * nx.ld + tid, (double)p);
+      // copy = this block's XCD: all adds into one copy meet in one L2, so a
+      // workgroup-scope atomic (performed in that L2, not at device scope) is
+      // enough; the kernel boundary writes the L2 back for the next launch
+      int xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      __hip_atomic_fetch_add(nx.acc + (xcc & (GM_ACC_COPIES - 1)) * nx.ld + tid, (double)p, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
   GM_TL_END(2);
