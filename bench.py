@@ -53,6 +53,8 @@ def parse() -> argparse.Namespace:
                     help="only the per-stage graphs the roofline is measured on (for rocprof)")
     ap.add_argument("--chain-only", action="store_true", help="only the B=1 chain (for rocprof)")
     ap.add_argument("--matvec-only", action="store_true", help="only BASELINE configs 1-2 (quantised matvec)")
+    ap.add_argument("--decode-step-only", action="store_true",
+                    help="only the full decoder step (attention, Gated DeltaNet, MoE, lm_head), one JSON line")
     ap.add_argument("--quant-shapes", default=None,
                     help="comma-separated subset of the configs 1-2 shapes for --matvec-only")
     ap.add_argument("--dense-shapes", default="ssm_in,ssm_gate,ssm_out", help="projections for --dense-only")
@@ -300,6 +302,96 @@ def kquant_shared_layers(layers, seed: int = SEED + 6):
                                q_down_sh=L.GM_QTYPE_I8, sh_gate_inp=b.sh_gate_inp, norm_w=b.norm_w,
                                norm_eps=b.norm_eps, device=dev))
     return out
+
+
+def run_decode_step(moe_layers, n_prefill: int = 64, steps: int = 20, seed: int = SEED + 50):
+    """The whole decoder for one token (qwen/forward.py:834-893 at T = 1) through
+    npu_amd.qwen_core.forward: the reference model's 40 layers (Gated DeltaNet in 30, gated
+    attention in every fourth, Qwen3.6-35B-A3B shapes: D 2048, 16 q / 2 kv heads of 256,
+    RoPE 64; 16 K / 32 V heads of 128 with a conv of 4), each followed by its MoE block
+    (the chain's config-5 blocks, RMSNorm weight 1), the output norm and a 248,320 x 2048
+    lm_head.  Seeded device weights: the core projections bf16 N(0, 0.02), embedding
+    N(0, 1).  `n_prefill` tokens are decoded first to fill the KV caches and the recurrent
+    states; then one decode step at position `n_prefill` is captured in a hipGraph and
+    replayed `steps` times (each replay rewrites cache row `n_prefill` and advances the
+    recurrent states), timed between HIP events on the replay stream.  Eager steps (one
+    C-ABI call per core layer and MoE block, host launch included) are timed beside it."""
+    import torch
+    from npu_amd import qwen_core as QN
+    dev = moe_layers[0].gate.device
+    n_layer = len(moe_layers)
+    cfg = QN.Config(n_layer=n_layer, is_attention=[(i + 1) % 4 == 0 for i in range(n_layer)])
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def w(*shape, std=0.02):
+        return (torch.randn(*shape, generator=g, device=dev) * std).to(torch.bfloat16).float()
+
+    def v(n, base=1.0, std=0.1):
+        return base + torch.randn(n, generator=g, device=dev) * std
+    D, Dh, Hq, Hkv = cfg.d_model, cfg.head_dim, cfg.n_head, cfg.n_head_kv
+    Hk, Hv, S = cfg.ssm_n_k_heads, cfg.ssm_n_v_heads, cfg.ssm_d_state
+    C = 2 * Hk * S + Hv * S
+    layers = []
+    for i in range(n_layer):
+        if cfg.is_attention[i]:
+            core = QN.AttnLayer(i=i, attn_norm=v(D), post_norm=torch.ones(D, device=dev), wq=w(2 * Hq * Dh, D),
+                                wk=w(Hkv * Dh, D), wv=w(Hkv * Dh, D), wo=w(D, Hq * Dh), q_norm=v(Dh), k_norm=v(Dh))
+            core.gpu = QN.GpuAttn(core, cfg)
+        else:
+            core = QN.SSMLayer(i=i, attn_norm=v(D), post_norm=torch.ones(D, device=dev), w_in=w(C, D),
+                               w_gate=w(Hv * S, D), conv1d=v(C * cfg.ssm_d_conv, 0.0, 0.5).view(C, -1),
+                               a=-torch.rand(Hv, generator=g, device=dev), alpha=w(Hv, D, std=0.05),
+                               beta=w(Hv, D, std=0.05), dt_bias=v(Hv, 0.0, 0.5), ssm_norm=v(S), w_out=w(D, Hv * S))
+            core.gpu = QN.GpuSsm(core, cfg)
+        for name in [f for f in ("wq", "wk", "wv", "wo", "w_in", "w_gate", "w_out") if hasattr(core, f)]:
+            setattr(core, name, None)                  # the bf16 device copies are what runs
+        layers.append((core, moe_layers[i]))
+    V = cfg.vocab_size
+    max_pos = n_prefill + 8
+    cos, sin = QN.build_partial_rope_cache(cfg.rope_dim, max_pos, cfg.rope_theta, device=dev)
+    model = QN.Model(cfg=cfg, token_embd=torch.randn(V, D, generator=g, device=dev), output_norm=v(D),
+                     lm_head=w(V, D), layers=layers, rope_cos=cos, rope_sin=sin)
+    kv, st = None, None
+    tok = 17
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for pos in range(n_prefill):                        # eager decode steps
+        logits, kv, st = QN.forward(model, [tok], start_pos=pos, kv_caches=kv, ssm_states=st)
+        tok = (tok * 31 + pos) % V
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / n_prefill
+    kv_len = [c.length if c is not None else None for c in kv]
+    tok_dev = torch.tensor([tok], dtype=torch.long, device=dev)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        logits, _, _ = QN.forward(model, tok_dev, start_pos=n_prefill, kv_caches=kv, ssm_states=st)
+    for c, n in zip(kv, kv_len):                        # the replays rewrite row n_prefill
+        if c is not None:
+            c.length = n
+    gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    core_bytes = sum((l[0].gpu.wqkv.numel() + l[0].gpu.wo.numel()) * 2 if isinstance(l[0], QN.AttnLayer) else
+                     (l[0].gpu.w_in.numel() + l[0].gpu.w_gate.numel() + l[0].gpu.w_out.numel()) * 2
+                     for l in layers)
+    moe_bytes = sum(b.weight_bytes_per_token() for b in moe_layers)
+    head = V * D * 2
+    total = core_bytes + moe_bytes + head
+    return {"workload": f"full decode step: {n_layer} layers ({sum(cfg.is_attention)} gated attention, "
+                        f"{n_layer - sum(cfg.is_attention)} Gated DeltaNet) + MoE blocks + lm_head {V} x {D}, "
+                        f"position {n_prefill}, hipGraph replay",
+            "ms_per_token": ms, "tokens_per_s": 1e3 / ms, "eager_ms_per_token": eager_ms,
+            "weight_bytes_per_token": total, "core_weight_bytes": core_bytes, "moe_weight_bytes": moe_bytes,
+            "lm_head_bytes": head, "effective_weight_GBps": total / (ms * 1e-3) / 1e9,
+            "hbm_frac": total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "finite": bool(torch.isfinite(logits).all())}
 
 
 DENSE_SHAPES = (("ssm_in", 8192, 2048), ("ssm_gate", 4096, 2048), ("ssm_out", 2048, 4096))
@@ -682,6 +774,11 @@ def main() -> int:
     if args.matvec_only:
         shapes = None if args.quant_shapes is None else args.quant_shapes.split(",")
         print(json.dumps({"quant_mv": run_quant_mv(dev, shapes=shapes)}))
+        return 0
+    if args.decode_step_only:
+        layers = build_layers(args.layers, dev)
+        torch.cuda.synchronize()
+        print(json.dumps({"decode_step": run_decode_step(layers)}))
         return 0
     if args.roofline_only:
         layers = build_layers(args.layers, dev)

@@ -334,7 +334,10 @@ def forward(model: Model, tokens, *, start_pos: int = 0, kv_caches=None, ssm_sta
         g["onorm"] = _f32_dev(model.output_norm)
         g["lm_head"] = _bf16_dev(model.lm_head)
         g["rope"] = _rope_on_device(model.rope_cos, model.rope_sin)
-    tok = torch.as_tensor(list(tokens), dtype=torch.long, device=device())
+    if isinstance(tokens, torch.Tensor):                 # already on the device: nothing to copy (capturable)
+        tok = tokens.to(device(), torch.long).reshape(-1)
+    else:
+        tok = torch.as_tensor(list(tokens), dtype=torch.long, device=device())
     T = tok.numel()
     x = g["embd"][tok].view(1, T, cfg.d_model).contiguous()
     cos, sin = g["rope"]
@@ -359,17 +362,22 @@ def forward(model: Model, tokens, *, start_pos: int = 0, kv_caches=None, ssm_sta
     return logits, kv_caches, ssm_states
 
 
-def _moe_residual(g: dict, i: int, x: torch.Tensor, core, moe: MoELayer, cfg: Config) -> torch.Tensor:
+def _moe_residual(g: dict, i: int, x: torch.Tensor, core, moe, cfg: Config) -> torch.Tensor:
     """x + moe_forward(rms_norm(x, core.post_norm)) in one gm_moe_forward call: a copy of
     the layer's block struct carrying post_norm as its RMSNorm weight, with the residual
-    flag (the block's own struct, which the drop-in moe_forward uses, is left as it is)."""
+    flag (the block's own struct, which the drop-in moe_forward uses, is left as it is).
+    ``moe`` is a ``MoELayer`` or an already resident ``GpuMoeBlock``."""
     from npu_amd import ops
+    from npu_amd.moe import GpuMoeBlock
     from npu_amd.qwen_moe import _build_block
-    if moe.npu is None:
-        moe.npu = {}
-    blk = moe.npu.get("moe_block")
-    if blk is None:
-        blk = moe.npu["moe_block"] = _build_block(moe)
+    if isinstance(moe, GpuMoeBlock):
+        blk = moe
+    else:
+        if moe.npu is None:
+            moe.npu = {}
+        blk = moe.npu.get("moe_block")
+        if blk is None:
+            blk = moe.npu["moe_block"] = _build_block(moe)
     key = ("moe", i)
     if key not in g:
         nw = _f32_dev(core.post_norm)
