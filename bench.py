@@ -53,6 +53,7 @@ def parse() -> argparse.Namespace:
                     help="only the per-stage graphs the roofline is measured on (for rocprof)")
     ap.add_argument("--chain-only", action="store_true", help="only the B=1 chain (for rocprof)")
     ap.add_argument("--matvec-only", action="store_true", help="only BASELINE configs 1-2 (quantised matvec)")
+    ap.add_argument("--eager", action="store_true", help="--matvec-only: eager launches instead of graph replays")
     ap.add_argument("--decode-step-only", action="store_true",
                     help="only the full decoder step (attention, Gated DeltaNet, MoE, lm_head), one JSON line")
     ap.add_argument("--quant-shapes", default=None,
@@ -467,7 +468,7 @@ QUANT_MV_SHAPES = (("config1_iq4xs_512x2048", 23, 512, 2048), ("config2_iq3xxs_2
 
 
 def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330, samples: dict | None = None,
-                 shapes=None):
+                 shapes=None, graph: bool = True):
     """BASELINE configs 1 and 2: one y = W x with W a raw IQ4_XS [512 x 2048] or IQ3_XXS
     [2048 x 512] / [512 x 2048] matrix (the reference's NpuIQ4MatVec / NpuQuantMatVec
     call, npu/quant_mv.py:419-463), fp32 x ~ N(0, 1), seeded device-generated
@@ -475,7 +476,9 @@ def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330, samp
     are resident; one hipGraph holds one gm_matvec per matrix (the back-to-back calls of
     the configs), replayed `reps` times: period per call.  Batched variant: `batch`
     consecutive matrices are one [batch M x K] raw matrix, so one launch computes their
-    products with the same x.  Algorithmic bytes per call: W + x + y."""
+    products with the same x.  Algorithmic bytes per call: W + x + y.  ``graph=False``
+    times the same launches eagerly (for counter collection, which serialises every
+    dispatch anyway)."""
     import torch
     from npu_amd import _lib as L
     from npu_amd import ops, synth
@@ -507,15 +510,18 @@ def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330, samp
         def period_us(fn, launches):
             fn()
             torch.cuda.synchronize()
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                fn()
-            g.replay()
-            torch.cuda.synchronize()
+            run = fn
+            if graph:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    fn()
+                g.replay()
+                torch.cuda.synchronize()
+                run = g.replay
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             for _ in range(reps):
-                g.replay()
+                run()
             e1.record()
             torch.cuda.synchronize()
             return e0.elapsed_time(e1) * 1e3 / (reps * launches)
@@ -773,7 +779,7 @@ def main() -> int:
         return 0
     if args.matvec_only:
         shapes = None if args.quant_shapes is None else args.quant_shapes.split(",")
-        print(json.dumps({"quant_mv": run_quant_mv(dev, shapes=shapes)}))
+        print(json.dumps({"quant_mv": run_quant_mv(dev, shapes=shapes, graph=not args.eager)}))
         return 0
     if args.decode_step_only:
         layers = build_layers(args.layers, dev)

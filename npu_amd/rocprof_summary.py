@@ -13,6 +13,10 @@ instruction counters of one ``--pmc`` pass (``SQ_WAVES``, ``SQ_INSTS_VALU``,
 ``SQ_INSTS_SALU``, ``SQ_INSTS_LDS``, ``SQ_INSTS_VMEM_RD``: device totals per dispatch),
 with the VALU issue time they imply (``<name>.md``).
 
+With ``--trace T.csv`` it tabulates durations per kernel and launch shape (grid size)
+from a kernel trace; ``--grid-pmc`` counter CSVs add, per shape, the copy-calibrated
+HBM bytes (FETCH_SIZE / WRITE_SIZE) and instruction counts per wave.
+
 With ``--prefill-pmc P.csv`` it instead summarises the prefill kernels: rocprof
 durations and, from the counters ``MfmaUtil``, ``MfmaFlopsF16`` and ``MfmaFlopsBF16``
 (one ``--pmc`` pass), each kernel's MFMA busy fraction and issued MFMA TFLOP/s
@@ -176,12 +180,54 @@ def trace_by_grid(a) -> None:
                 continue
             grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
             rows[(name, grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    lines = [f"# {a.name}: kernel durations by launch shape", "", a.commands, "",
-             "| kernel | grid (work-items) | dispatches | avg us | median us | min us | max us |",
-             "|---|---|---|---|---|---|---|"]
+    pmc: dict[tuple[str, int], dict[str, list[float]]] = defaultdict(lambda: defaultdict(list))
+    for path in a.grid_pmc:
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                name = short(r["Kernel_Name"])
+                if a.kernel and a.kernel not in name:
+                    continue
+                pmc[(name, int(r["Grid_Size"]))][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    s_fetch = s_write = 1.0
+    if a.calib_fetch and a.calib_write:
+        s_fetch = a.calib_bytes / (counter_means(a.calib_fetch)[a.calib_kernel] * 1024)
+        s_write = a.calib_bytes / (counter_means(a.calib_write)[a.calib_kernel] * 1024)
+    algo = {}
+    for kv in a.algo:
+        key, b = kv.rsplit("=", 1)
+        kern, grid = key.rsplit("@", 1)
+        algo[(kern, int(grid))] = int(b)
+    head = "| kernel | grid (work-items) | dispatches | avg us | median us | min us | max us |"
+    rule = "|---|---|---|---|---|---|---|"
+    if pmc:
+        head += (" HBM bytes/dispatch | algorithmic bytes | traffic/algorithmic | waves | VALU / wave | SALU / wave |"
+                 " LDS / wave | VMEM rd / wave |")
+        rule += "---|---|---|---|---|---|---|---|"
+    lines = [f"# {a.name}: kernel durations by launch shape", "", a.commands, ""]
+    if pmc and a.calib_fetch:
+        lines += [f"HBM bytes = FETCH_SIZE x 1024 x {s_fetch:.4f} + WRITE_SIZE x 1024 x {s_write:.4f} (the scales "
+                  f"make a {a.calib_bytes} B {a.calib_kernel} read as that many bytes each way); instruction "
+                  "counts are device totals per dispatch over SQ_WAVES.", ""]
+    lines += [head, rule]
+
+    def fmt(x, spec):
+        return "-" if x is None else format(x, spec)
     for (name, grid), d in sorted(rows.items()):
-        lines.append(f"| {name[:80]} | {grid} | {len(d)} | {statistics.fmean(d):.2f} | {statistics.median(d):.2f} | "
-                     f"{min(d):.2f} | {max(d):.2f} |")
+        line = (f"| {name[:80]} | {grid} | {len(d)} | {statistics.fmean(d):.2f} | {statistics.median(d):.2f} | "
+                f"{min(d):.2f} | {max(d):.2f} |")
+        if pmc:
+            c = {k: statistics.fmean(v) for k, v in pmc.get((name, grid), {}).items()}
+            hbm = None
+            if "FETCH_SIZE" in c:
+                hbm = c["FETCH_SIZE"] * 1024 * s_fetch + c.get("WRITE_SIZE", 0.0) * 1024 * s_write
+            alg = next((b for (k, g), b in algo.items() if g == grid and k in name), None)
+            ratio = hbm / alg if hbm is not None and alg else None
+            w = c.get("SQ_WAVES")
+            per = (lambda key: c[key] / w if w and key in c else None)
+            line += (f" {fmt(hbm, '.0f')} | {fmt(alg, 'd')} | {fmt(ratio, '.3f')} | {fmt(w, '.0f')} | "
+                     f"{fmt(per('SQ_INSTS_VALU'), '.0f')} | {fmt(per('SQ_INSTS_SALU'), '.0f')} | "
+                     f"{fmt(per('SQ_INSTS_LDS'), '.0f')} | {fmt(per('SQ_INSTS_VMEM_RD'), '.0f')} |")
+        lines.append(line)
     out = Path(a.out)
     out.mkdir(parents=True, exist_ok=True)
     (out / f"{a.name}.md").write_text("\n".join(lines) + "\n")
@@ -192,6 +238,9 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--trace", help="kernel-trace CSV: durations per kernel and grid size (trace mode)")
     ap.add_argument("--kernel", default="", help="trace mode: only kernels whose name contains this")
+    ap.add_argument("--grid-pmc", action="append", default=[],
+                    help="trace mode: counter CSV whose means per kernel and grid size become columns "
+                         "(FETCH_SIZE / WRITE_SIZE, SQ_WAVES / SQ_INSTS_*; repeatable)")
     ap.add_argument("--stats")
     ap.add_argument("--prefill-pmc", help="counter CSV of MfmaUtil/MfmaFlopsF16/MfmaFlopsBF16 (prefill mode)")
     ap.add_argument("--inst-pmc", help="counter CSV of SQ_WAVES/SQ_INSTS_* (instruction mode)")
@@ -208,7 +257,7 @@ def main() -> None:
     ap.add_argument("--commands", default="", help="text describing the commands (markdown)")
     ap.add_argument("--algo", action="append", default=[],
                     help="KERNEL=BYTES: algorithmic bytes per launch of a kernel family (replaces the "
-                         "T = 1 decode table; repeatable)")
+                         "T = 1 decode table; repeatable); in trace mode KERNEL@GRID=BYTES")
     ap.add_argument("--json", default="hbm_traffic.json", help="name of the JSON written to --out")
     a = ap.parse_args()
     if a.trace:
