@@ -137,26 +137,49 @@ struct RawIq3 {
 // 2 mod 4.  Fields are fetched with aligned dword loads (global memory or
 // LDS) and re-aligned with v_alignbyte_b32; every dword read contains at
 // least one byte of this superblock, so no load crosses into an unmapped page.
+// gm_load_iq3_words issues the loads only; gm_iq3_align re-aligns them.  A
+// kernel that issues many rows' loads before an issue fence keeps the words
+// raw until it decodes them, so no ALU work on loaded values (which would
+// wait for the loads) sits in front of the fence.
+struct RawIq3Words {
+  uint32_t d0, q0, q1, q2, w0, w1;
+  uint32_t rq;     // 2 when the superblock starts at 0 mod 4 (d in the low half), else 0
+};
+
 template <bool ST = false>
-__device__ __forceinline__ RawIq3 gm_load_iq3(const uint8_t* __restrict__ row, int sub) {
+__device__ __forceinline__ RawIq3Words gm_load_iq3_words(const uint8_t* __restrict__ row, int sub) {
   const int sb = sub >> 3, s = sub & 7;
   const uint8_t* base = row + sb * GM_IQ3XXS_BYTES;
   const int odd = (int)((reinterpret_cast<uintptr_t>(base) >> 1) & 1);   // base % 4 == 2 * odd
   const uint32_t* dp = reinterpret_cast<const uint32_t*>(base - 2 * odd);
-  RawIq3 r;
-  const uint32_t d0 = gm_ld<ST>(dp);
-  r.d = odd ? (d0 >> 16) : (d0 & 0xffffu);
+  RawIq3Words t;
+  t.d0 = gm_ld<ST>(dp);
   // qs at base + 2 + 8s: offset % 4 == 2 when sb is even, 0 when odd
   const int rq = odd ? 0 : 2;
+  t.rq = (uint32_t)rq;
   const uint32_t* qp = reinterpret_cast<const uint32_t*>(base + 2 + 8 * s - rq);
-  const uint32_t q0 = gm_ld<ST>(qp), q1 = gm_ld<ST>(qp + 1), q2 = gm_ld<ST>(qp + (rq ? 2 : 1));
-  r.q0 = __builtin_amdgcn_alignbyte(q1, q0, rq);
-  r.q1 = __builtin_amdgcn_alignbyte(q2, q1, rq);
+  t.q0 = gm_ld<ST>(qp);
+  t.q1 = gm_ld<ST>(qp + 1);
+  t.q2 = gm_ld<ST>(qp + (rq ? 2 : 1));
   // word at base + 66 + 4s: same parity rule
   const uint32_t* wp = reinterpret_cast<const uint32_t*>(base + 66 + 4 * s - rq);
-  const uint32_t w0 = gm_ld<ST>(wp), w1 = gm_ld<ST>(wp + (rq ? 1 : 0));
-  r.w = __builtin_amdgcn_alignbyte(w1, w0, rq);
+  t.w0 = gm_ld<ST>(wp);
+  t.w1 = gm_ld<ST>(wp + (rq ? 1 : 0));
+  return t;
+}
+
+__device__ __forceinline__ RawIq3 gm_iq3_align(const RawIq3Words& t) {
+  RawIq3 r;
+  r.d = t.rq ? (t.d0 & 0xffffu) : (t.d0 >> 16);
+  r.q0 = __builtin_amdgcn_alignbyte(t.q1, t.q0, t.rq);
+  r.q1 = __builtin_amdgcn_alignbyte(t.q2, t.q1, t.rq);
+  r.w = __builtin_amdgcn_alignbyte(t.w1, t.w0, t.rq);
   return r;
+}
+
+template <bool ST = false>
+__device__ __forceinline__ RawIq3 gm_load_iq3(const uint8_t* __restrict__ row, int sub) {
+  return gm_iq3_align(gm_load_iq3_words<ST>(row, sub));
 }
 
 // ksigns byte for a 7-bit index: the 7 explicit sign bits plus a parity bit

@@ -332,17 +332,34 @@ __device__ __forceinline__ float gm_dot_limb_sub(const uint32_t (&w)[8], const G
   return fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0));
 }
 
+// What k_mv1q keeps of a fetched sub-block until it decodes it: the raw
+// sub-block, or for IQ3_XXS its unaligned words (aligned at decode time).
+template <int QT> struct Mv1Raw { using T = typename RawSub<QT>::T; };
+template <> struct Mv1Raw<GM_QTYPE_IQ3_XXS> { using T = RawIq3Words; };
+
+template <int QT>
+__device__ __forceinline__ typename Mv1Raw<QT>::T mv1_load(const uint8_t* __restrict__ row, int sub) {
+  if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_load_iq3_words<true>(row, sub);
+  else return gm_load_sub<QT, true>(row, sub);
+}
+
+template <int QT>
+__device__ __forceinline__ typename RawSub<QT>::T mv1_raw(const typename Mv1Raw<QT>::T& t) {
+  if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_iq3_align(t);
+  else return t;
+}
+
 template <int QT, int LR, int SPL, int RPW>
 __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int M, int K, int64_t rb,
                                               const float* __restrict__ x, float* __restrict__ y) {
   using namespace gm_moe;
-  constexpr int NXP = kMv1MaxK / 2048;                           // passes of 8 values per thread
+  constexpr int NXP = SPL;                      // passes of 8 values per thread: K <= 2048 SPL (LR = 64 for SPL > 1)
   constexpr int G = 64 / LR;                                     // rows per row group of a wave
   constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
-  extern __shared__ float smem[];                                  // the limb row, then the IQ3 tables
+  extern __shared__ float smem[];              // the limb row, a spare sub-block, then the IQ3 tables
   const int nsub = K / GM_SUB, rbytes = gm_limb_row_bytes(K);
   uint8_t* xs = reinterpret_cast<uint8_t*>(smem);
-  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(xs + rbytes);
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(xs + rbytes + GM_LSUB);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane % LR;
   const int row0 = (blockIdx.x * 4 + wave) * (RPW * G) + lane / LR;  // row of group j: row0 + G j
   gm_f32x4 xa[NXP], xb[NXP];
@@ -355,35 +372,48 @@ __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int
   }
   uint32_t gw = 0;
   if constexpr (IQ3) gw = gm_iq3_tab_load();
-  RowFetch<QT, SPL> f[RPW];
+  issue_fence();                                                 // x and the table ahead of the weights
+  typename Mv1Raw<QT>::T f[RPW][SPL];
 #pragma unroll
   for (int j = 0; j < RPW; ++j) {
     const int row = row0 + G * j;
-    fetch_subs<QT, LR, SPL, true>(f[j], w + (int64_t)(row < M ? row : M - 1) * rb, lir, nsub);
+    const uint8_t* wr = w + (int64_t)(row < M ? row : M - 1) * rb;
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) {
+      const int sub = lir + LR * i;
+      f[j][i] = mv1_load<QT>(wr, sub < nsub ? sub : nsub - 1);
+    }
   }
   issue_fence();
+  // Unconditional stores (threads past K write the spare sub-block): a store
+  // under `if (k0 < K)` let the compiler sink the x loads into the branch,
+  // behind every weight load, and wait for all of them before the limbs.
 #pragma unroll
   for (int p = 0; p < NXP; ++p) {
     const int k0 = 2048 * p + 8 * (int)threadIdx.x;
-    if (k0 < K) gm_put_limbs8(xa[p], xb[p], k0 >> 2, xs);      // uniform per quad (K % 32 == 0)
+    const int c = k0 < K ? k0 >> 2 : (nsub << 3) + ((k0 >> 2) & 7);
+    gm_put_limbs8(xa[p], xb[p], c, xs);                          // uniform per quad (K % 32 == 0)
   }
   if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
   __syncthreads();
   float acc[RPW];
 #pragma unroll
   for (int j = 0; j < RPW; ++j) acc[j] = 0.f;
+  // Branch-free over the sub-blocks (a sub-block past K repeats the last one
+  // with a zero factor): under `if (sub < nsub)` the compiler sank the weight
+  // loads into the branch, behind the block barrier.
 #pragma unroll
   for (int i = 0; i < SPL; ++i) {
-    const int sub = lir + LR * i;
-    if (sub < nsub) {
-      GmLimbSub a;
-      gm_read_limb_sub(xs + sub * GM_LSUB, a);
+    const int sub = lir + LR * i, subc = sub < nsub ? sub : nsub - 1;
+    GmLimbSub a;
+    gm_read_limb_sub(xs + subc * GM_LSUB, a);
+    const float live = sub < nsub ? a.scale : 0.f;
 #pragma unroll
-      for (int j = 0; j < RPW; ++j) {
-        uint32_t wq[8];
-        const float ws = gm_decode_i8<QT>(f[j].r[i], sub, tab, wq);
-        acc[j] = fmaf(ws * a.scale, gm_dot_limb_sub(wq, a), acc[j]);
-      }
+    for (int j = 0; j < RPW; ++j) {
+      uint32_t wq[8];
+      const float ws = gm_decode_i8<QT>(mv1_raw<QT>(f[j][i]), subc, tab, wq);
+      acc[j] = fmaf(ws * live, gm_dot_limb_sub(wq, a), acc[j]);
+      issue_fence();                              // row by row, so each waits only for its own loads
     }
   }
 #pragma unroll
@@ -397,7 +427,7 @@ __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int
 template <int QT, int LR, int SPL, int RPW>
 static int launch_mv1q_t(const uint8_t* w, int M, int K, const float* x, float* y, hipStream_t s) {
   const int rows_per_block = 4 * RPW * (64 / LR);
-  const size_t smem = (size_t)gm_moe::gm_limb_row_bytes(K) + sizeof(Iq3Tab);
+  const size_t smem = (size_t)gm_moe::gm_limb_row_bytes(K) + gm_moe::GM_LSUB + sizeof(Iq3Tab);
   if (int rc = gm_set_smem(k_mv1q<QT, LR, SPL, RPW>, smem)) return rc;
   hipLaunchKernelGGL((k_mv1q<QT, LR, SPL, RPW>), dim3((unsigned)((M + rows_per_block - 1) / rows_per_block)),
                      dim3(256), smem, s, w, M, K, gm_row_bytes(QT, K), x, y);
@@ -407,12 +437,22 @@ static int launch_mv1q_t(const uint8_t* w, int M, int K, const float* x, float* 
 
 // Row groups per wave: as many as keep at least kMv1Blocks blocks in the grid
 // (4 per CU), up to 8 sub-block loads in flight per lane.
-constexpr int kMv1Blocks = 1024;
+#ifndef GM_MV1_BLOCKS
+#define GM_MV1_BLOCKS 1024
+#endif
+#ifndef GM_MV1_IQ3_RPW
+#define GM_MV1_IQ3_RPW 4
+#endif
+constexpr int kMv1Blocks = GM_MV1_BLOCKS;
 
 template <int QT, int LR, int SPL>
 static int launch_mv1q_r(const uint8_t* w, int M, int K, const float* x, float* y, hipStream_t s) {
   const int64_t groups = (int64_t)(M + 64 / LR - 1) / (64 / LR);        // row groups over the matrix
-  auto fits = [&](int rpw) { return SPL * rpw <= 8 && groups >= (int64_t)4 * rpw * kMv1Blocks; };
+  // IQ3_XXS rows take 6 narrow loads per sub-block against IQ4_XS's 2: at most 4 row groups per wave
+  const int max_rpw = QT == GM_QTYPE_IQ3_XXS ? GM_MV1_IQ3_RPW : 8;
+  auto fits = [&](int rpw) {
+    return SPL * rpw <= 8 && rpw <= max_rpw && groups >= (int64_t)4 * rpw * kMv1Blocks;
+  };
   if (fits(8)) return launch_mv1q_t<QT, LR, SPL, 8>(w, M, K, x, y, s);
   if (fits(4)) return launch_mv1q_t<QT, LR, SPL, 4>(w, M, K, x, y, s);
   if (fits(2)) return launch_mv1q_t<QT, LR, SPL, 2>(w, M, K, x, y, s);
