@@ -297,9 +297,13 @@ static int launch_matvec_l(const uint8_t* w, int M, int K, const float* x, int n
 // arrive the block converts x into the int8-limb row in LDS; then each lane
 // reads the limbs of a sub-block once and multiplies them with that
 // sub-block of all RPW rows on v_dot4_i32_i8 (the MoE decode kernels'
-// arithmetic).  RPW > 1 amortises the x load and its conversion over RPW
-// times the weight bytes (a batched launch of many matrices has thousands
-// of blocks, each of which used to convert x for 4 rows).
+// arithmetic), row by row, so that each row waits only for its own loads.
+// RPW > 1 amortises the x load and its conversion over RPW times the weight
+// bytes (a batched launch of many matrices has thousands of blocks, each of
+// which used to convert x for 4 rows).  Issue order, waits and the absence
+// of branches around the loads' uses were checked in the kernel's gfx950
+// assembly: x's loads first, then every weight load, one wait for x before
+// the limbs and one per row after the barrier.
 constexpr int kMv1MaxK = 8192;
 
 // The three limb planes and the scale of one activation sub-block (LDS).
@@ -356,12 +360,26 @@ __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int
   constexpr int NXP = SPL;                      // passes of 8 values per thread: K <= 2048 SPL (LR = 64 for SPL > 1)
   constexpr int G = 64 / LR;                                     // rows per row group of a wave
   constexpr bool IQ3 = QT == GM_QTYPE_IQ3_XXS;
-  extern __shared__ float smem[];              // the limb row, a spare sub-block, then the IQ3 tables
-  const int nsub = K / GM_SUB, rbytes = gm_limb_row_bytes(K);
+  extern __shared__ float smem[];              // the limb row of NXP 2048-wide passes, then the IQ3 tables
+  const int nsub = K / GM_SUB;
   uint8_t* xs = reinterpret_cast<uint8_t*>(smem);
-  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(xs + rbytes + GM_LSUB);
+  Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(xs + gm_limb_row_bytes(2048 * NXP));
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane % LR;
   const int row0 = (blockIdx.x * 4 + wave) * (RPW * G) + lane / LR;  // row of group j: row0 + G j
+  typename Mv1Raw<QT>::T f[RPW][SPL];
+  auto fetch_rows = [&]() {
+#pragma unroll
+    for (int j = 0; j < RPW; ++j) {
+      const int row = row0 + G * j;
+      const uint8_t* wr = w + (int64_t)(row < M ? row : M - 1) * rb;
+#pragma unroll
+      for (int i = 0; i < SPL; ++i) {
+        const int sub = lir + LR * i;
+        f[j][i] = mv1_load<QT>(wr, sub < nsub ? sub : nsub - 1);
+      }
+    }
+    issue_fence();
+  };
   gm_f32x4 xa[NXP], xb[NXP];
 #pragma unroll
   for (int p = 0; p < NXP; ++p) {
@@ -373,27 +391,14 @@ __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int
   uint32_t gw = 0;
   if constexpr (IQ3) gw = gm_iq3_tab_load();
   issue_fence();                                                 // x and the table ahead of the weights
-  typename Mv1Raw<QT>::T f[RPW][SPL];
+  fetch_rows();
+  // Unconditional stores (threads past K fill the row's unused tail, one
+  // slot each): a store under `if (k0 < K)` let the compiler sink the x loads
+  // into the branch, behind every weight load, and wait for all of them
+  // before the limbs.
 #pragma unroll
-  for (int j = 0; j < RPW; ++j) {
-    const int row = row0 + G * j;
-    const uint8_t* wr = w + (int64_t)(row < M ? row : M - 1) * rb;
-#pragma unroll
-    for (int i = 0; i < SPL; ++i) {
-      const int sub = lir + LR * i;
-      f[j][i] = mv1_load<QT>(wr, sub < nsub ? sub : nsub - 1);
-    }
-  }
-  issue_fence();
-  // Unconditional stores (threads past K write the spare sub-block): a store
-  // under `if (k0 < K)` let the compiler sink the x loads into the branch,
-  // behind every weight load, and wait for all of them before the limbs.
-#pragma unroll
-  for (int p = 0; p < NXP; ++p) {
-    const int k0 = 2048 * p + 8 * (int)threadIdx.x;
-    const int c = k0 < K ? k0 >> 2 : (nsub << 3) + ((k0 >> 2) & 7);
-    gm_put_limbs8(xa[p], xb[p], c, xs);                          // uniform per quad (K % 32 == 0)
-  }
+  for (int p = 0; p < NXP; ++p)
+    gm_put_limbs8(xa[p], xb[p], (2048 * p + 8 * (int)threadIdx.x) >> 2, xs);   // uniform per quad
   if constexpr (IQ3) gm_iq3_tab_store(gw, tab);
   __syncthreads();
   float acc[RPW];
@@ -427,7 +432,7 @@ __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int
 template <int QT, int LR, int SPL, int RPW>
 static int launch_mv1q_t(const uint8_t* w, int M, int K, const float* x, float* y, hipStream_t s) {
   const int rows_per_block = 4 * RPW * (64 / LR);
-  const size_t smem = (size_t)gm_moe::gm_limb_row_bytes(K) + gm_moe::GM_LSUB + sizeof(Iq3Tab);
+  const size_t smem = (size_t)gm_moe::gm_limb_row_bytes(2048 * SPL) + sizeof(Iq3Tab);   // NXP = SPL passes
   if (int rc = gm_set_smem(k_mv1q<QT, LR, SPL, RPW>, smem)) return rc;
   hipLaunchKernelGGL((k_mv1q<QT, LR, SPL, RPW>), dim3((unsigned)((M + rows_per_block - 1) / rows_per_block)),
                      dim3(256), smem, s, w, M, K, gm_row_bytes(QT, K), x, y);
@@ -448,7 +453,8 @@ constexpr int kMv1Blocks = GM_MV1_BLOCKS;
 template <int QT, int LR, int SPL>
 static int launch_mv1q_r(const uint8_t* w, int M, int K, const float* x, float* y, hipStream_t s) {
   const int64_t groups = (int64_t)(M + 64 / LR - 1) / (64 / LR);        // row groups over the matrix
-  // IQ3_XXS rows take 6 narrow loads per sub-block against IQ4_XS's 2: at most 4 row groups per wave
+  // IQ3_XXS (6 narrow loads per sub-block against IQ4_XS's 2): 4 row groups
+  // per wave measured 13.4 us for 64 config-2 matrices against 15.7 at 8
   const int max_rpw = QT == GM_QTYPE_IQ3_XXS ? GM_MV1_IQ3_RPW : 8;
   auto fits = [&](int rpw) {
     return SPL * rpw <= 8 && rpw <= max_rpw && groups >= (int64_t)4 * rpw * kMv1Blocks;
