@@ -336,23 +336,6 @@ __device__ __forceinline__ float gm_dot_limb_sub(const uint32_t (&w)[8], const G
   return fmaf((float)s2, 65536.f, fmaf((float)s1, 256.f, (float)s0));
 }
 
-// What k_mv1q keeps of a fetched sub-block until it decodes it: the raw
-// sub-block, or for IQ3_XXS its unaligned words (aligned at decode time).
-template <int QT> struct Mv1Raw { using T = typename RawSub<QT>::T; };
-template <> struct Mv1Raw<GM_QTYPE_IQ3_XXS> { using T = RawIq3Words; };
-
-template <int QT>
-__device__ __forceinline__ typename Mv1Raw<QT>::T mv1_load(const uint8_t* __restrict__ row, int sub) {
-  if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_load_iq3_words<true>(row, sub);
-  else return gm_load_sub<QT, true>(row, sub);
-}
-
-template <int QT>
-__device__ __forceinline__ typename RawSub<QT>::T mv1_raw(const typename Mv1Raw<QT>::T& t) {
-  if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_iq3_align(t);
-  else return t;
-}
-
 template <int QT, int LR, int SPL, int RPW>
 __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int M, int K, int64_t rb,
                                               const float* __restrict__ x, float* __restrict__ y) {
@@ -366,7 +349,7 @@ __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int
   Iq3Tab* tab = reinterpret_cast<Iq3Tab*>(xs + gm_limb_row_bytes(2048 * NXP));
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane % LR;
   const int row0 = (blockIdx.x * 4 + wave) * (RPW * G) + lane / LR;  // row of group j: row0 + G j
-  typename Mv1Raw<QT>::T f[RPW][SPL];
+  typename FetchRaw<QT>::T f[RPW][SPL];
   auto fetch_rows = [&]() {
 #pragma unroll
     for (int j = 0; j < RPW; ++j) {
@@ -375,7 +358,7 @@ __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int
 #pragma unroll
       for (int i = 0; i < SPL; ++i) {
         const int sub = lir + LR * i;
-        f[j][i] = mv1_load<QT>(wr, sub < nsub ? sub : nsub - 1);
+        f[j][i] = gm_fetch_sub<QT, true>(wr, sub < nsub ? sub : nsub - 1);
       }
     }
     issue_fence();
@@ -416,7 +399,7 @@ __global__ void __launch_bounds__(256) k_mv1q(const uint8_t* __restrict__ w, int
 #pragma unroll
     for (int j = 0; j < RPW; ++j) {
       uint32_t wq[8];
-      const float ws = gm_decode_i8<QT>(mv1_raw<QT>(f[j][i]), subc, tab, wq);
+      const float ws = gm_decode_i8<QT>(gm_fetched<QT>(f[j][i]), subc, tab, wq);
       acc[j] = fmaf(ws * live, gm_dot_limb_sub(wq, a), acc[j]);
       issue_fence();                              // row by row, so each waits only for its own loads
     }

@@ -585,9 +585,27 @@ __device__ __forceinline__ float gm_i8_dot_limbs(const RawI8& r, const uint8_t* 
 // past the row are clamped to its last sub-block (a harmless duplicate load
 // whose result is skipped), so the loads are unconditional and straight-line
 // and the compiler can count them instead of draining the queue before each.
+// What a fetch keeps until the decode: the raw sub-block, or for IQ3_XXS its
+// unaligned words (gm_iq3_align at decode time), so that no ALU work on
+// loaded values, which would wait for the loads, is issued with the loads.
+template <int QT> struct FetchRaw { using T = typename RawSub<QT>::T; };
+template <> struct FetchRaw<GM_QTYPE_IQ3_XXS> { using T = RawIq3Words; };
+
+template <int QT, bool ST = false>
+__device__ __forceinline__ typename FetchRaw<QT>::T gm_fetch_sub(const uint8_t* __restrict__ row, int sub) {
+  if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_load_iq3_words<ST>(row, sub);
+  else return gm_load_sub<QT, ST>(row, sub);
+}
+
+template <int QT>
+__device__ __forceinline__ typename RawSub<QT>::T gm_fetched(const typename FetchRaw<QT>::T& t) {
+  if constexpr (QT == GM_QTYPE_IQ3_XXS) return gm_iq3_align(t);
+  else return t;
+}
+
 template <int QT, int SPL>
 struct RowFetch {
-  typename RawSub<QT>::T r[SPL];
+  typename FetchRaw<QT>::T r[SPL];
 };
 
 template <int QT, int LR, int SPL, bool ST = false>
@@ -595,7 +613,7 @@ __device__ __forceinline__ void fetch_subs(RowFetch<QT, SPL>& f, const uint8_t* 
 #pragma unroll
   for (int i = 0; i < SPL; ++i) {
     const int sub = lir + LR * i;
-    f.r[i] = gm_load_sub<QT, ST>(row, sub < nsub ? sub : nsub - 1);
+    f.r[i] = gm_fetch_sub<QT, ST>(row, sub < nsub ? sub : nsub - 1);
   }
 }
 
@@ -621,7 +639,7 @@ __device__ __forceinline__ void dot_subs(const RowFetch<QT, SPL>& f, int lir, in
     const int sub = lir + LR * i;
     if (sub < nsub) {
       float wv[32];
-      const float sc = gm_decode_sub_t<QT>(f.r[i], sub, tab, wv);
+      const float sc = gm_decode_sub_t<QT>(gm_fetched<QT>(f.r[i]), sub, tab, wv);
 #pragma unroll
       for (int m = 0; m < NT; ++m)
         if (m < nt) acc[m] = fmaf(sc, gm_dot32_il(wv, act + idx[m] * K, sub, nsub), acc[m]);
@@ -847,7 +865,7 @@ __device__ __forceinline__ void dot_subs_i8(const RowFetch<QT, SPL>& f, int lir,
         }
       } else {
         uint32_t w[8];
-        const float ws = gm_decode_i8<QT, ARITH>(f.r[i], sub, tab, w);
+        const float ws = gm_decode_i8<QT, ARITH>(gm_fetched<QT>(f.r[i]), sub, tab, w);
 #pragma unroll
         for (int m = 0; m < NT; ++m) {
           if (m < nt) {

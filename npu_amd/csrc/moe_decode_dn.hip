@@ -287,9 +287,10 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
 // 64 rows of one down matrix for nm <= 8 member rows of hsrc (global rows
 // src[m] of h, where h_sh follows h), written to yp rows dst[m].
 // Rows [row0, row0 + 64 NTILE) of one down matrix for nm member rows of h
-// (h rows src[m] -> yp rows dst[m]): every tile's raw rows are fetched first
-// (wave w, pass q of tile t -> row row0 + 64t + 16w + 4q + (lane >> 4), 16 lanes
-// per row), the members are staged in LDS meanwhile, then the tiles are decoded.
+// (h rows src[m] -> yp rows dst[m]): the members' h rows are loaded, then
+// every tile's raw rows (wave w, pass q of tile t -> row row0 + 64t + 16w + 4q
+// + (lane >> 4), 16 lanes per row); the members are staged in LDS as limb rows
+// while the weights are in flight, then the tiles are decoded as they land.
 template <int QTW, int FC, int NTILE>
 __device__ __forceinline__ void down_rows(const uint8_t* __restrict__ wbase, int D, int FF, int row0, int nm,
                                           const int (&src)[8], const int (&dst)[8], const float* __restrict__ h,
@@ -298,14 +299,8 @@ __device__ __forceinline__ void down_rows(const uint8_t* __restrict__ wbase, int
   constexpr int HPT = 4 * FC;     // float4 per thread: 8 * FF <= 8 * 512 * FC floats over 256 threads
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lir = lane & 15, nsub = FF >> 5;
   const int64_t rb = gm_row_bytes(QTW, FF);
-  RowFetch<QTW, FC> f[NTILE][4];
-#pragma unroll
-  for (int t = 0; t < NTILE; ++t)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = row0 + 64 * t + wave * 16 + q * 4 + (lane >> 4);
-      fetch_subs<QTW, 16, FC, true>(f[t][q], wbase + (int64_t)(row < D ? row : 0) * rb, lir, nsub);
-    }
+  // the member rows first: vmcnt retires in issue order, so the wait for
+  // them before the limb staging does not wait for the weights
   const int nqr = FF >> 2, nq = nm * nqr;
   const gm_f32x4* h4 = reinterpret_cast<const gm_f32x4*>(h);
   gm_f32x4 hr[HPT];
@@ -318,6 +313,15 @@ __device__ __forceinline__ void down_rows(const uint8_t* __restrict__ wbase, int
     for (int mm = 1; mm < 8; ++mm) s = m == mm ? src[mm] : s;
     hr[i] = h4[(int64_t)s * nqr + (c < nq ? c - m * nqr : 0)];
   }
+  issue_fence();
+  RowFetch<QTW, FC> f[NTILE][4];
+#pragma unroll
+  for (int t = 0; t < NTILE; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int row = row0 + 64 * t + wave * 16 + q * 4 + (lane >> 4);
+      fetch_subs<QTW, 16, FC, true>(f[t][q], wbase + (int64_t)(row < D ? row : 0) * rb, lir, nsub);
+    }
   issue_fence();
   if constexpr (QTW == GM_QTYPE_IQ3_XXS) gm_iq3_tab_store(gw, tab);
   const int rbytes = gm_limb_row_bytes(FF);
