@@ -41,7 +41,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--layers", type=int, default=N_LAYERS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=8, help="blocks in the bounded CPU sample")
-    ap.add_argument("--no-extra", action="store_true", help="skip the batch-8 chain")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the extra legs (B = 8, prefill, dense and quantised matvecs, full decode step)")
     ap.add_argument("--calib-copy", action="store_true", help="only run a plain 256 MiB copy (counter calibration)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the config-4 prefill measurement (8 layers), one JSON line")
@@ -848,6 +849,8 @@ def main() -> int:
         log(f"dense bf16 matvec: {extra['dense_mv']}")
         extra["quant_mv"] = run_quant_mv(dev, samples=samples)
         log(f"quant matvec (configs 1-2): {extra['quant_mv']}")
+        extra["decode_step"] = run_decode_step(layers)
+        log(f"full decode step: {extra['decode_step']}")
 
     cpu = None
     if not args.no_cpu_baseline:
