@@ -490,9 +490,10 @@ __device__ __forceinline__ PfRaw<QT> pf_load(const uint8_t* __restrict__ sb, int
 // superblock factor pf_dscale applied to the fp32 accumulator instead:
 //   IQ4_XS: d * (ls - 32)            -> integer ls - 32 in [-32, 31], factor d
 //   IQ3_XXS: d * (0.5 + s4) * 0.5    -> integer 2 s4 + 1 in [1, 31], factor d / 4
-// so every f16 weight is an exact integer (|kv (ls - 32)| <= 4064 rounds at
-// most once, |(2 s4 + 1) g| <= 1922 is exact) and f16's small exponent range
-// never meets a tiny d.
+// so every f16 weight is an integer product, exact up to 2048 in magnitude:
+// |(2 s4 + 1) g| <= 1922 is always exact, |kv (ls - 32)| <= 4064 is rounded
+// once to f16's 11 significant bits when odd and above 2048; f16's small
+// exponent range never meets a tiny d.
 template <int QT>
 __device__ __forceinline__ gm_f32x2 pf_scales(const PfRaw<QT>& r, int q) {
   if constexpr (QT == GM_QTYPE_IQ4_XS) {
