@@ -84,10 +84,12 @@ struct PfWs {
 
 // A shared expert stored in other formats than the routed experts (the real
 // model's K-quant shared experts, held as I8 rows, beside IQ routed experts; or
-// a dense bf16 one) does not run as the GEMMs' ninth unit: its T tokens run as
-// one fp32 pass of the multi-token gate/up and down matvec kernels over xn,
-// which writes the rows yp[P + t] the combine reads.  The routed experts keep
-// the grouped GEMMs.
+// a dense bf16 one) does not run as the GEMMs' ninth unit.  In I8 rows it runs
+// as two dense f16 MFMA GEMMs of its own (k_pfs_gateup_i8 into the shared
+// SwiGLU rows hb[P + t], k_pf_h16, k_pfs_down_i8 into yp[P + t]); in bf16 its T
+// tokens run as one fp32 pass of the multi-token gate/up and down matvec
+// kernels over xn.  Either way it writes the rows yp[P + t] the combine reads,
+// and the routed experts keep the grouped GEMMs.
 inline bool pf_shared_apart(const gm_moe_layer* L) {
   return L->gate_sh && (L->q_gate_sh != L->q_gate || L->q_down_sh != L->q_down);
 }
@@ -1034,6 +1036,136 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ x,
   }
 }
 
+// ------------------------------------------------- shared expert in I8 rows
+// A shared expert held as I8 rows (the reference model's K-quant shared
+// experts, transcoded) beside IQ routed experts runs as two dense GEMMs of its
+// own over all T tokens, on the routed experts' f16 MFMA: A = the I8 weights
+// decoded to f16 (s q + off, rounded once), B = the tokens' f16 rows (xh for
+// gate/up, the scaled SwiGLU rows hh for down).  Wave tile: 16 weight rows x
+// 16 tokens over the whole K, one I8 sub-block (32 k) per MFMA step: lane l
+// holds row l % 16 and k-octet o = l / 16 of A (8 quants, 8 bytes, and the
+// sub-block's {s0, s1, off}), token l % 16 and the same octet of B (16 bytes).
+// Sub-blocks are loaded kShStep at a time into two register sets used in turn
+// (no register copy at the loop latch), so one set's loads are in flight
+// while the other is multiplied.
+constexpr int kShStep = 4;
+
+typedef uint32_t gm_u32x3 __attribute__((ext_vector_type(3)));
+
+struct I8Oct {
+  uint2 q;       // quants 8o .. 8o + 7 of the sub-block
+  gm_u32x3 m;    // s0 (quants 0-15), s1 (16-31), off
+};
+
+__device__ __forceinline__ I8Oct i8_oct_load(const uint8_t* __restrict__ row, int sub, int o) {
+  const uint8_t* sb = row + sub * 48;
+  return I8Oct{*reinterpret_cast<const uint2*>(sb + 8 * o), *reinterpret_cast<const gm_u32x3*>(sb + 32)};
+}
+
+// The octet's 8 weights s q + off as f16 (each rounded once from fp32, where
+// s q + off is the transcoded row's exact weight).
+__device__ __forceinline__ gm_f16x8 i8_oct_f16(const I8Oct& r, int o) {
+  const float sc = __uint_as_float(o < 2 ? r.m.x : r.m.y), off = __uint_as_float(r.m.z);
+  gm_f16x8 a;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    a[b] = (_Float16)fmaf(sc, gm_sbyte(r.q.x, b), off);
+    a[4 + b] = (_Float16)fmaf(sc, gm_sbyte(r.q.y, b), off);
+  }
+  return a;
+}
+
+// One pipeline stage: kShStep sub-blocks of NW weight rows and of the token row.
+template <int NW>
+struct ShStage {
+  I8Oct w[NW][kShStep];
+  gm_u32x4 b[kShStep];
+};
+
+template <int NW>
+__device__ __forceinline__ void sh_stage_load(ShStage<NW>& st, const uint8_t* const (&wrow)[NW],
+                                              const uint16_t* __restrict__ brow, int s0, int o) {
+#pragma unroll
+  for (int i = 0; i < kShStep; ++i) {
+#pragma unroll
+    for (int n = 0; n < NW; ++n) st.w[n][i] = i8_oct_load(wrow[n], s0 + i, o);
+    st.b[i] = *reinterpret_cast<const gm_u32x4*>(brow + 32 * (s0 + i));
+  }
+  issue_fence();
+}
+
+template <int NW>
+__device__ __forceinline__ void sh_stage_mfma(const ShStage<NW>& st, int o, gm_f32x4 (&acc)[NW]) {
+#pragma unroll
+  for (int i = 0; i < kShStep; ++i) {
+    const gm_f16x8 B = __builtin_bit_cast(gm_f16x8, st.b[i]);
+#pragma unroll
+    for (int n = 0; n < NW; ++n)
+      acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8_oct_f16(st.w[n][i], o), B, acc[n], 0, 0, 0);
+  }
+  issue_fence();
+}
+
+// acc[n] = W_n[rows r0 .. r0 + 15] . brow over K (nsub sub-blocks, a multiple of
+// 2 kShStep) for the lane's token.
+template <int NW>
+__device__ __forceinline__ void sh_gemm_tile(const uint8_t* const (&wrow)[NW], const uint16_t* __restrict__ brow,
+                                             int nsub, int o, gm_f32x4 (&acc)[NW]) {
+#pragma unroll
+  for (int n = 0; n < NW; ++n) acc[n] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+  ShStage<NW> sa, sb;
+  sh_stage_load<NW>(sa, wrow, brow, 0, o);
+  for (int s0 = 0; s0 < nsub; s0 += 2 * kShStep) {
+    sh_stage_load<NW>(sb, wrow, brow, s0 + kShStep, o);
+    sh_stage_mfma<NW>(sa, o, acc);
+    const int s2 = s0 + 2 * kShStep < nsub ? s0 + 2 * kShStep : s0;     // the last round reloads, unused
+    sh_stage_load<NW>(sa, wrow, brow, s2, o);
+    sh_stage_mfma<NW>(sb, o, acc);
+  }
+}
+
+// h[P + t] = silu(g) u for the shared expert, t < T: block (row tile of 16
+// FF rows, group of 4 waves x 16 tokens); bf16 rows as k_pf_gateup writes them.
+__global__ void __launch_bounds__(256) k_pfs_gateup_i8(const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu,
+                                                       int FF, int D, const uint16_t* __restrict__ xh,
+                                                       const float* __restrict__ xsc, int T,
+                                                       uint16_t* __restrict__ hsh) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, o = lane >> 4;
+  const int r0 = blockIdx.x * 16, t0 = (blockIdx.y * 4 + wave) * 16;
+  if (t0 >= T) return;                                         // uniform per wave; no barrier below
+  const int64_t rb = (int64_t)(D / 32) * 48;
+  const int t = t0 + l16, tc = t < T ? t : T - 1;
+  const uint8_t* const wrow[2] = {wg + (r0 + l16) * rb, wu + (r0 + l16) * rb};
+  gm_f32x4 acc[2];
+  sh_gemm_tile<2>(wrow, xh + (int64_t)tc * D + 8 * o, D / 32, o, acc);
+  if (t < T) {                                                 // C: rows r0 + 4 o + i, token column l16
+    const float ds = xsc[t];
+    const gm_f32x4 g = acc[0] * ds, u = acc[1] * ds;
+    const gm_f32x2 h01 = {gm_silu(g[0]) * u[0], gm_silu(g[1]) * u[1]};
+    const gm_f32x2 h23 = {gm_silu(g[2]) * u[2], gm_silu(g[3]) * u[3]};
+    *reinterpret_cast<uint2*>(hsh + (int64_t)t * FF + r0 + 4 * o) =
+        make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(h01, gm_bf16x2)),
+                   __builtin_bit_cast(uint32_t, __builtin_convertvector(h23, gm_bf16x2)));
+  }
+}
+
+// y[t] = W_down h[t] for the shared expert from its scaled f16 rows (hh, scales
+// hsc, as k_pf_h16 writes them): block (row tile of 16 D rows, 4 waves x 16
+// tokens), fp32 rows y[t] that k_pf_combine adds last.
+__global__ void __launch_bounds__(256) k_pfs_down_i8(const uint8_t* __restrict__ wd, int D, int FF,
+                                                     const uint16_t* __restrict__ hh, const float* __restrict__ hsc,
+                                                     int T, float* __restrict__ y) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, o = lane >> 4;
+  const int r0 = blockIdx.x * 16, t0 = (blockIdx.y * 4 + wave) * 16;
+  if (t0 >= T) return;
+  const int64_t rb = (int64_t)(FF / 32) * 48;
+  const int t = t0 + l16, tc = t < T ? t : T - 1;
+  const uint8_t* const wrow[1] = {wd + (r0 + l16) * rb};
+  gm_f32x4 acc[1];
+  sh_gemm_tile<1>(wrow, hh + (int64_t)tc * FF + 8 * o, FF / 32, o, acc);
+  if (t < T) *reinterpret_cast<gm_f32x4*>(y + (int64_t)t * D + r0 + 4 * o) = acc[0] * hsc[t];
+}
+
 constexpr size_t kGemmSmem = 2 * (size_t)kTileG + 256 * 4 + 128 * 16 + 2 * kSegTok * 4;
 
 template <int QTG, int QTD>
@@ -1048,9 +1180,14 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
   const bool has_sh = L->gate_sh != nullptr;
   const bool sh_apart = pf_shared_apart(L);
   const bool sh_gemm = has_sh && !sh_apart;          // the shared expert as the GEMMs' ninth unit
+  // a shared expert in I8 rows: its own f16 MFMA GEMMs; other formats (bf16): the fp32 pass
+  const bool sh_i8 = sh_apart && L->q_gate_sh == GM_QTYPE_I8 && L->q_up_sh == GM_QTYPE_I8 &&
+                     L->q_down_sh == GM_QTYPE_I8;
+  const bool sh_f32 = sh_apart && !sh_i8;
+  const size_t P = (size_t)T * k;
   const int nrows = E + (L->sh_gate_inp ? 1 : 0);
   hipLaunchKernelGGL(k_pf_prep, dim3(T), dim3(256), 0, s, x, T, D, L->norm_w, L->norm_eps, w.xr, w.xh, w.xsc,
-                     sh_apart ? w.xn : nullptr);
+                     sh_f32 ? w.xn : nullptr);
   GM_TRY(hipGetLastError());
   const int ldp = router_ld(L);
   const int nsplit = router_split(D);
@@ -1090,10 +1227,9 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
   if (int rc = gm_launch_dispatch_seg(ids, T, k, E, w.counts, w.offsets, w.sorted, w.inv, w.segs, kSegTok,
                                      sh_gemm ? T : 0, s))
     return rc;
-  if (sh_apart) {                                    // shared expert rows yp[P + t], fp32
+  if (sh_f32) {                                      // shared expert rows yp[P + t], fp32
     if (int rc = gm_launch_gateup(L->q_gate_sh, L->gate_sh, L->up_sh, FF, D, w.xn, T, w.hsh, s)) return rc;
-    if (int rc = gm_launch_matvec(L->q_down_sh, L->down_sh, D, FF, w.hsh, T, w.yp + (size_t)T * k * D, s))
-      return rc;
+    if (int rc = gm_launch_matvec(L->q_down_sh, L->down_sh, D, FF, w.hsh, T, w.yp + P * D, s)) return rc;
   }
   const int nseg = max_segments(T, k, E);
   {
@@ -1104,8 +1240,14 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
                        w.xsc, w.hb, T, nrt);
     GM_TRY(hipGetLastError());
   }
+  if (sh_i8) {                                       // shared SwiGLU rows hb[P + t] (D % 256 == 0)
+    hipLaunchKernelGGL(k_pfs_gateup_i8, dim3(FF / 16, (T + 63) / 64), dim3(256), 0, s,
+                       static_cast<const uint8_t*>(L->gate_sh), static_cast<const uint8_t*>(L->up_sh), FF, D, w.xh,
+                       w.xsc, T, w.hb + P * FF);
+    GM_TRY(hipGetLastError());
+  }
   {
-    const int rows = T * k + (sh_gemm ? T : 0);
+    const int rows = T * k + (sh_gemm || sh_i8 ? T : 0);
     hipLaunchKernelGGL(k_pf_h16, dim3((rows + 3) / 4), dim3(256), 0, s, w.hb, rows, FF, w.hh, w.hsc);
     GM_TRY(hipGetLastError());
   }
@@ -1131,6 +1273,11 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
                            T, n_blk, kGroupsPerBlock);
         break;
     }
+    GM_TRY(hipGetLastError());
+  }
+  if (sh_i8) {                                       // shared expert rows yp[P + t] (FF % 256 == 0)
+    hipLaunchKernelGGL(k_pfs_down_i8, dim3(D / 16, (T + 63) / 64), dim3(256), 0, s,
+                       static_cast<const uint8_t*>(L->down_sh), D, FF, w.hh + P * FF, w.hsc + P, T, w.yp + P * D);
     GM_TRY(hipGetLastError());
   }
   hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(256), 0, s, x, w.yp, w.inv, wts, shg, T, k, D, has_sh ? 1 : 0,

@@ -177,12 +177,14 @@ def _kquant_blocks(rng, qtype, n):
 def test_prefill_kquant_shared_expert(gpu, T, D, FF, E, k):
     """IQ routed experts beside a Q6_K / Q8_0 shared expert (as the real model's GGUF holds
     it; transcoded once to I8 rows) at T > 8.  The routed experts stay on the prefill GEMMs
-    and the shared expert runs as an fp32 pass of its own: the output equals the same layer
-    without the shared expert, run on the prefill path, plus sigmoid(xn . g_sh) times the
-    fp64 shared expert, to 2e-5 of the output's maximum (the routed part is the same
-    computation bit for bit, so a run of the tokens as fp32 decode chunks, which rounds the
-    routed part differently at ~1e-4, fails this); and the oracle's routed part plus that
-    shared term within the prefill bar."""
+    and the shared expert runs as two f16 MFMA GEMMs of its own:
+    (a) with an all-zero I8 shared expert the output equals the same layer without one, bit
+    for bit (the routed part is the same computation, so a run of the tokens as decode
+    chunks, which rounds the routed part differently, fails this);
+    (b) with the K-quant shared expert, the output minus that layer's output equals
+    sigmoid(xn . g_sh) times the fp64 shared expert within 5e-3 of the shared term's maximum
+    (f16 weights and activations, bf16 SwiGLU rows, as the routed prefill experts);
+    (c) the oracle's routed part plus that shared term matches within the prefill bar."""
     import torch.nn.functional as F
     from npu_amd import _lib as L, ops
     from oracle import kquants as KQ
@@ -200,17 +202,21 @@ def test_prefill_kquant_shared_expert(gpu, T, D, FF, E, k):
     blk = GpuMoeBlock(**common, gate_sh=i8["gate"], up_sh=i8["up"], down_sh=i8["down"], q_gate_sh=L.GM_QTYPE_I8,
                       q_down_sh=L.GM_QTYPE_I8, sh_gate_inp=g_sh)
     blk_r = GpuMoeBlock(**common)
+    zero = {n: torch.zeros_like(t) for n, t in i8.items()}
+    blk_0 = GpuMoeBlock(**common, gate_sh=zero["gate"], up_sh=zero["up"], down_sh=zero["down"],
+                        q_gate_sh=L.GM_QTYPE_I8, q_down_sh=L.GM_QTYPE_I8, sh_gate_inp=g_sh)
     x = torch.from_numpy(synth.host_input(31 + T, T, D))
     y = blk(x.to(gpu)).cpu().double()
     y_r = blk_r(x.to(gpu)).cpu().double()
+    assert torch.equal(blk_0(x.to(gpu)).cpu().double(), y_r), "zero shared expert: routed part must be unchanged"
     assert torch.equal(blk(x.to(gpu)).cpu().double(), y), "repeat calls must be bit-identical"
     xs = x.double()
     gs, us, ds = (torch.from_numpy(KQ.dequant(b, q).reshape(shp)).double() for b, q, shp in raw.values())
     sh = (F.silu(xs @ gs.T) * (xs @ us.T)) @ ds.T
     sg = torch.sigmoid(xs @ g_sh.double())
     shared = sg[:, None] * sh
-    err = float((y - y_r - shared).abs().max() / y.abs().max())
-    assert err <= 2e-5, f"shared pass beside the routed GEMMs: {err:.3e}"
+    err = float((y - y_r - shared).abs().max() / shared.abs().max())
+    assert err <= 5e-3, f"shared GEMMs beside the routed GEMMs: {err:.3e}"
     ol = OM.OracleLayer(h)
     margin = OM.topk_margin(OM.router_logits64(x, ol), k)
     clear = margin > 1e-5
