@@ -1042,13 +1042,15 @@ __global__ void __launch_bounds__(256) k_pf_combine(const float* __restrict__ x,
 // own over all T tokens, on the routed experts' f16 MFMA: A = the I8 weights
 // decoded to f16 (s q + off, rounded once), B = the tokens' f16 rows (xh for
 // gate/up, the scaled SwiGLU rows hh for down).  Wave tile: 16 weight rows x
-// 16 tokens over the whole K, one I8 sub-block (32 k) per MFMA step: lane l
-// holds row l % 16 and k-octet o = l / 16 of A (8 quants, 8 bytes, and the
-// sub-block's {s0, s1, off}), token l % 16 and the same octet of B (16 bytes).
+// 16 kShTiles tokens over a K part, one I8 sub-block (32 k) per step, one
+// decoded A operand for kShTiles MFMAs: lane l holds row l % 16 and k-octet
+// o = l / 16 of A (8 quants, 8 bytes, and the sub-block's {s0, s1, off}),
+// token l % 16 of each token tile and the same octet of B (16 bytes).
 // Sub-blocks are loaded kShStep at a time into two register sets used in turn
 // (no register copy at the loop latch), so one set's loads are in flight
 // while the other is multiplied.
-constexpr int kShStep = 4;
+constexpr int kShStep = 2;
+constexpr int kShTiles = 4;           // 16-token tiles per wave: one decoded A operand, 4 MFMAs
 
 typedef uint32_t gm_u32x3 __attribute__((ext_vector_type(3)));
 
@@ -1075,95 +1077,156 @@ __device__ __forceinline__ gm_f16x8 i8_oct_f16(const I8Oct& r, int o) {
   return a;
 }
 
-// One pipeline stage: kShStep sub-blocks of NW weight rows and of the token row.
+// One pipeline stage: kShStep sub-blocks of NW weight rows and of the
+// kShTiles token rows.
 template <int NW>
 struct ShStage {
   I8Oct w[NW][kShStep];
-  gm_u32x4 b[kShStep];
+  gm_u32x4 b[kShStep][kShTiles];
 };
 
 template <int NW>
 __device__ __forceinline__ void sh_stage_load(ShStage<NW>& st, const uint8_t* const (&wrow)[NW],
-                                              const uint16_t* __restrict__ brow, int s0, int o) {
+                                              const uint16_t* const (&brow)[kShTiles], int s0, int o) {
 #pragma unroll
   for (int i = 0; i < kShStep; ++i) {
 #pragma unroll
     for (int n = 0; n < NW; ++n) st.w[n][i] = i8_oct_load(wrow[n], s0 + i, o);
-    st.b[i] = *reinterpret_cast<const gm_u32x4*>(brow + 32 * (s0 + i));
+#pragma unroll
+    for (int j = 0; j < kShTiles; ++j) st.b[i][j] = *reinterpret_cast<const gm_u32x4*>(brow[j] + 32 * (s0 + i));
   }
   issue_fence();
 }
 
 template <int NW>
-__device__ __forceinline__ void sh_stage_mfma(const ShStage<NW>& st, int o, gm_f32x4 (&acc)[NW]) {
+__device__ __forceinline__ void sh_stage_mfma(const ShStage<NW>& st, int o, gm_f32x4 (&acc)[NW][kShTiles]) {
 #pragma unroll
   for (int i = 0; i < kShStep; ++i) {
-    const gm_f16x8 B = __builtin_bit_cast(gm_f16x8, st.b[i]);
 #pragma unroll
-    for (int n = 0; n < NW; ++n)
-      acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8_oct_f16(st.w[n][i], o), B, acc[n], 0, 0, 0);
+    for (int n = 0; n < NW; ++n) {
+      const gm_f16x8 A = i8_oct_f16(st.w[n][i], o);
+#pragma unroll
+      for (int j = 0; j < kShTiles; ++j)
+        acc[n][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(gm_f16x8, st.b[i][j]), acc[n][j],
+                                                           0, 0, 0);
+    }
   }
   issue_fence();
 }
 
-// acc[n] = W_n[rows r0 .. r0 + 15] . brow over K (nsub sub-blocks, a multiple of
-// 2 kShStep) for the lane's token.
+// acc[n][j] = W_n[rows r0 .. r0 + 15] . brow[j] over sub-blocks [sb, sb + ns) (ns
+// a multiple of 2 kShStep) for the lane's token of tile j.
 template <int NW>
-__device__ __forceinline__ void sh_gemm_tile(const uint8_t* const (&wrow)[NW], const uint16_t* __restrict__ brow,
-                                             int nsub, int o, gm_f32x4 (&acc)[NW]) {
+__device__ __forceinline__ void sh_gemm_tile(const uint8_t* const (&wrow)[NW], const uint16_t* const (&brow)[kShTiles],
+                                             int sb, int ns, int o, gm_f32x4 (&acc)[NW][kShTiles]) {
 #pragma unroll
-  for (int n = 0; n < NW; ++n) acc[n] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
-  ShStage<NW> sa, sb;
-  sh_stage_load<NW>(sa, wrow, brow, 0, o);
-  for (int s0 = 0; s0 < nsub; s0 += 2 * kShStep) {
-    sh_stage_load<NW>(sb, wrow, brow, s0 + kShStep, o);
+  for (int n = 0; n < NW; ++n)
+#pragma unroll
+    for (int j = 0; j < kShTiles; ++j) acc[n][j] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+  ShStage<NW> sa, sb2;
+  const int se = sb + ns;
+  sh_stage_load<NW>(sa, wrow, brow, sb, o);
+  for (int s0 = sb; s0 < se; s0 += 2 * kShStep) {
+    sh_stage_load<NW>(sb2, wrow, brow, s0 + kShStep, o);
     sh_stage_mfma<NW>(sa, o, acc);
-    const int s2 = s0 + 2 * kShStep < nsub ? s0 + 2 * kShStep : s0;     // the last round reloads, unused
+    const int s2 = s0 + 2 * kShStep < se ? s0 + 2 * kShStep : s0;      // the last round reloads, unused
     sh_stage_load<NW>(sa, wrow, brow, s2, o);
-    sh_stage_mfma<NW>(sb, o, acc);
+    sh_stage_mfma<NW>(sb2, o, acc);
   }
 }
 
-// h[P + t] = silu(g) u for the shared expert, t < T: block (row tile of 16
-// FF rows, group of 4 waves x 16 tokens); bf16 rows as k_pf_gateup writes them.
+// K parts: the block's 4 waves split K into nkw parts (4, 2 or 1) of whole
+// pipeline rounds and cover 4 / nkw token groups; the parts are added in LDS
+// in part order by the group's part-0 wave.
+inline int sh_kparts(int nsub) {
+  return nsub % (8 * kShStep) == 0 ? 4 : nsub % (4 * kShStep) == 0 ? 2 : 1;
+}
+
+// Sums the block's K parts of acc (LDS red: 4 waves x NW x kShTiles x 256
+// floats) into the part-0 wave of each token group; true on those waves.
+template <int NW>
+__device__ __forceinline__ bool sh_reduce(gm_f32x4 (&acc)[NW][kShTiles], int nkw, float* __restrict__ red) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, part = wave % nkw;
+  gm_f32x4* r4 = reinterpret_cast<gm_f32x4*>(red);
+  if (nkw > 1 && part != 0) {
+#pragma unroll
+    for (int n = 0; n < NW; ++n)
+#pragma unroll
+      for (int j = 0; j < kShTiles; ++j) r4[((wave * NW + n) * kShTiles + j) * 64 + lane] = acc[n][j];
+  }
+  __syncthreads();
+  if (part != 0) return false;
+  for (int p = 1; p < nkw; ++p)
+#pragma unroll
+    for (int n = 0; n < NW; ++n)
+#pragma unroll
+      for (int j = 0; j < kShTiles; ++j) acc[n][j] += r4[(((wave + p) * NW + n) * kShTiles + j) * 64 + lane];
+  return true;
+}
+
+// h[P + t] = silu(g) u for the shared expert, t < T: block (row tile of 16 FF
+// rows, 4 / nkw token groups of 16 kShTiles tokens, nkw K parts each); bf16
+// rows as k_pf_gateup writes them.
 __global__ void __launch_bounds__(256) k_pfs_gateup_i8(const uint8_t* __restrict__ wg, const uint8_t* __restrict__ wu,
                                                        int FF, int D, const uint16_t* __restrict__ xh,
-                                                       const float* __restrict__ xsc, int T,
+                                                       const float* __restrict__ xsc, int T, int nkw,
                                                        uint16_t* __restrict__ hsh) {
+  __shared__ float red[4 * 2 * kShTiles * 256];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, o = lane >> 4;
-  const int r0 = blockIdx.x * 16, t0 = (blockIdx.y * 4 + wave) * 16;
-  if (t0 >= T) return;                                         // uniform per wave; no barrier below
+  const int gpb = 4 / nkw, part = wave % nkw, ns = D / 32 / nkw;
+  const int r0 = blockIdx.x * 16, t0 = (blockIdx.y * gpb + wave / nkw) * 16 * kShTiles;
   const int64_t rb = (int64_t)(D / 32) * 48;
-  const int t = t0 + l16, tc = t < T ? t : T - 1;
   const uint8_t* const wrow[2] = {wg + (r0 + l16) * rb, wu + (r0 + l16) * rb};
-  gm_f32x4 acc[2];
-  sh_gemm_tile<2>(wrow, xh + (int64_t)tc * D + 8 * o, D / 32, o, acc);
-  if (t < T) {                                                 // C: rows r0 + 4 o + i, token column l16
-    const float ds = xsc[t];
-    const gm_f32x4 g = acc[0] * ds, u = acc[1] * ds;
-    const gm_f32x2 h01 = {gm_silu(g[0]) * u[0], gm_silu(g[1]) * u[1]};
-    const gm_f32x2 h23 = {gm_silu(g[2]) * u[2], gm_silu(g[3]) * u[3]};
-    *reinterpret_cast<uint2*>(hsh + (int64_t)t * FF + r0 + 4 * o) =
-        make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(h01, gm_bf16x2)),
-                   __builtin_bit_cast(uint32_t, __builtin_convertvector(h23, gm_bf16x2)));
+  const uint16_t* brow[kShTiles];
+#pragma unroll
+  for (int j = 0; j < kShTiles; ++j) {                         // tokens past T read a valid row, unstored
+    const int t = t0 + 16 * j + l16;
+    brow[j] = xh + (int64_t)(t < T ? t : T - 1) * D + 8 * o;
+  }
+  gm_f32x4 acc[2][kShTiles];
+  sh_gemm_tile<2>(wrow, brow, part * ns, ns, o, acc);
+  if (!sh_reduce<2>(acc, nkw, red)) return;
+#pragma unroll
+  for (int j = 0; j < kShTiles; ++j) {                         // C: rows r0 + 4 o + i, token column l16
+    const int t = t0 + 16 * j + l16;
+    if (t < T) {
+      const float ds = xsc[t];
+      const gm_f32x4 g = acc[0][j] * ds, u = acc[1][j] * ds;
+      const gm_f32x2 h01 = {gm_silu(g[0]) * u[0], gm_silu(g[1]) * u[1]};
+      const gm_f32x2 h23 = {gm_silu(g[2]) * u[2], gm_silu(g[3]) * u[3]};
+      *reinterpret_cast<uint2*>(hsh + (int64_t)t * FF + r0 + 4 * o) =
+          make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(h01, gm_bf16x2)),
+                     __builtin_bit_cast(uint32_t, __builtin_convertvector(h23, gm_bf16x2)));
+    }
   }
 }
 
 // y[t] = W_down h[t] for the shared expert from its scaled f16 rows (hh, scales
-// hsc, as k_pf_h16 writes them): block (row tile of 16 D rows, 4 waves x 16
-// tokens), fp32 rows y[t] that k_pf_combine adds last.
+// hsc, as k_pf_h16 writes them): block (row tile of 16 D rows, 4 / nkw token
+// groups, nkw K parts), fp32 rows y[t] that k_pf_combine adds last.
 __global__ void __launch_bounds__(256) k_pfs_down_i8(const uint8_t* __restrict__ wd, int D, int FF,
                                                      const uint16_t* __restrict__ hh, const float* __restrict__ hsc,
-                                                     int T, float* __restrict__ y) {
+                                                     int T, int nkw, float* __restrict__ y) {
+  __shared__ float red[4 * kShTiles * 256];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, o = lane >> 4;
-  const int r0 = blockIdx.x * 16, t0 = (blockIdx.y * 4 + wave) * 16;
-  if (t0 >= T) return;
+  const int gpb = 4 / nkw, part = wave % nkw, ns = FF / 32 / nkw;
+  const int r0 = blockIdx.x * 16, t0 = (blockIdx.y * gpb + wave / nkw) * 16 * kShTiles;
   const int64_t rb = (int64_t)(FF / 32) * 48;
-  const int t = t0 + l16, tc = t < T ? t : T - 1;
   const uint8_t* const wrow[1] = {wd + (r0 + l16) * rb};
-  gm_f32x4 acc[1];
-  sh_gemm_tile<1>(wrow, hh + (int64_t)tc * FF + 8 * o, FF / 32, o, acc);
-  if (t < T) *reinterpret_cast<gm_f32x4*>(y + (int64_t)t * D + r0 + 4 * o) = acc[0] * hsc[t];
+  const uint16_t* brow[kShTiles];
+#pragma unroll
+  for (int j = 0; j < kShTiles; ++j) {
+    const int t = t0 + 16 * j + l16;
+    brow[j] = hh + (int64_t)(t < T ? t : T - 1) * FF + 8 * o;
+  }
+  gm_f32x4 acc[1][kShTiles];
+  sh_gemm_tile<1>(wrow, brow, part * ns, ns, o, acc);
+  if (!sh_reduce<1>(acc, nkw, red)) return;
+#pragma unroll
+  for (int j = 0; j < kShTiles; ++j) {
+    const int t = t0 + 16 * j + l16;
+    if (t < T) *reinterpret_cast<gm_f32x4*>(y + (int64_t)t * D + r0 + 4 * o) = acc[0][j] * hsc[t];
+  }
 }
 
 constexpr size_t kGemmSmem = 2 * (size_t)kTileG + 256 * 4 + 128 * 16 + 2 * kSegTok * 4;
@@ -1241,9 +1304,10 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
     GM_TRY(hipGetLastError());
   }
   if (sh_i8) {                                       // shared SwiGLU rows hb[P + t] (D % 256 == 0)
-    hipLaunchKernelGGL(k_pfs_gateup_i8, dim3(FF / 16, (T + 63) / 64), dim3(256), 0, s,
+    const int nkw = sh_kparts(D / 32), tok = 16 * kShTiles * (4 / nkw);    // tokens per block
+    hipLaunchKernelGGL(k_pfs_gateup_i8, dim3(FF / 16, (T + tok - 1) / tok), dim3(256), 0, s,
                        static_cast<const uint8_t*>(L->gate_sh), static_cast<const uint8_t*>(L->up_sh), FF, D, w.xh,
-                       w.xsc, T, w.hb + P * FF);
+                       w.xsc, T, nkw, w.hb + P * FF);
     GM_TRY(hipGetLastError());
   }
   {
@@ -1276,8 +1340,10 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
     GM_TRY(hipGetLastError());
   }
   if (sh_i8) {                                       // shared expert rows yp[P + t] (FF % 256 == 0)
-    hipLaunchKernelGGL(k_pfs_down_i8, dim3(D / 16, (T + 63) / 64), dim3(256), 0, s,
-                       static_cast<const uint8_t*>(L->down_sh), D, FF, w.hh + P * FF, w.hsc + P, T, w.yp + P * D);
+    const int nkw = sh_kparts(FF / 32), tok = 16 * kShTiles * (4 / nkw);
+    hipLaunchKernelGGL(k_pfs_down_i8, dim3(D / 16, (T + tok - 1) / tok), dim3(256), 0, s,
+                       static_cast<const uint8_t*>(L->down_sh), D, FF, w.hh + P * FF, w.hsc + P, T, nkw,
+                       w.yp + P * D);
     GM_TRY(hipGetLastError());
   }
   hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(256), 0, s, x, w.yp, w.inv, wts, shg, T, k, D, has_sh ? 1 : 0,
