@@ -250,7 +250,7 @@ typedef struct gm_attn_layer {
   const void* wqkv;         /* bf16 [(2 n_head + 2 n_head_kv) head_dim][D]: attn_q (q and gate
                                interleaved per head, [q_h | gate_h]), then attn_k, then attn_v */
   const void* wo;           /* bf16 [D][n_head head_dim] (attn_output) */
-  const float* attn_norm;   /* [D] */
+  const float* attn_norm;   /* [D], 16-byte aligned */
   const float* q_norm;      /* [head_dim] */
   const float* k_norm;      /* [head_dim] */
   float eps;
@@ -287,7 +287,7 @@ typedef struct gm_ssm_layer {
   const float* a;           /* [n_v_heads] (ssm_a) */
   const float* dt_bias;     /* [n_v_heads] (ssm_dt.bias) */
   const float* ssm_norm;    /* [d_state] */
-  const float* attn_norm;   /* [D] */
+  const float* attn_norm;   /* [D], 16-byte aligned */
   float eps;
   int32_t D, n_k_heads, n_v_heads, d_state, conv_k;
 } gm_ssm_layer;

@@ -6,8 +6,8 @@
 // matvec kernels of mv_bf16.hip, the small alpha / beta projections fp32.
 //
 // Attention, one token at position pos (gm_attn_decode):
-//   k_rms_row        h = rmsnorm(x, attn_norm)
-//   mv_bf16          qkv = Wqkv h  ([q_h | gate_h] per head, then k, then v)
+//   mv_bf16 (+norm)  qkv = Wqkv rmsnorm(x, attn_norm) ([q_h | gate_h] per head,
+//                    then k, then v); the norm is formed while x is staged
 //   k_attn_prep      per head: RMSNorm of q / k over head_dim, partial RoPE at
 //                    pos; k and v written to the caches at row pos
 //   k_attn_part      per (q head, chunk of cached positions): online softmax
@@ -15,12 +15,13 @@
 //   k_attn_combine   per q head: the partials merged, times sigmoid(gate)
 //   mv_bf16 (+ x)    y = Wo out (+ x)
 // Gated DeltaNet, one token (gm_ssm_decode):
-//   k_rms_row        h = rmsnorm(x, attn_norm)
-//   mv_bf16 x2       mixed = W_in h, z = W_gate h
-//   k_ssm_ab         g = softplus(alpha h + dt_bias) a, beta = sigmoid(beta h)
-//   k_ssm_conv       depthwise causal conv (kernel conv_k) over [state, mixed],
-//                    SiLU, the state shifted; q and k heads L2-normalised, q
-//                    times 1/sqrt(Sk)
+//   mv_bf16 (+norm)  mixed = W_in h and z = W_gate h in one launch, h =
+//                    rmsnorm(x, attn_norm) formed while x is staged
+//   k_ssm_conv_ab    the depthwise causal conv (kernel conv_k) over [state,
+//                    mixed], SiLU, the state shifted, q and k heads
+//                    L2-normalised, q times 1/sqrt(Sk); beside it (other
+//                    blocks of the launch) g = softplus(alpha h + dt_bias) a
+//                    and beta = sigmoid(beta h)
 //   k_ssm_rec        per (V head, 32 state columns): S = S exp(g),
 //                    d = (v - S^T k) beta, S += k d^T, o = S^T q; the state
 //                    [Hv][Sk][Sv] (the reference's layout) updated in place
@@ -174,52 +175,61 @@ __global__ void k_attn_combine(const float* __restrict__ part, int ld, int nch, 
 }
 
 // ------------------------------------------------------------ Gated DeltaNet
-// Rows 0..Hv-1: alpha, Hv..2Hv-1: beta (fp32 weights [Hv][D]); one wave per row.
-// g = softplus(alpha . h + dt_bias) * a (torch's softplus: x above 20 passes
-// through, else log1p(exp(x))), beta = sigmoid(beta . h).
-__global__ void __launch_bounds__(256) k_ssm_ab(const float* __restrict__ alpha, const float* __restrict__ beta,
-                                                const float* __restrict__ dt_bias, const float* __restrict__ a,
-                                                const float* __restrict__ h, int D, int Hv, float* __restrict__ gb) {
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (r >= 2 * Hv) return;
-  const float* w = r < Hv ? alpha + (size_t)r * D : beta + (size_t)(r - Hv) * D;
-  float s = 0.f;
-  for (int i = lane; i < D; i += 64) s = fmaf(w[i], h[i], s);
-  s = gm_wave_sum64(s);
-  if (lane == 0) {
-    if (r < Hv) {
-      const float u = s + dt_bias[r];
-      gb[r] = (u > 20.f ? u : log1pf(expf(u))) * a[r];
-    } else {
-      gb[r] = 1.0f / (1.0f + expf(-s));
-    }
-  }
-}
-
-// One block per group of Sk channels (blockDim = Sk): the depthwise causal
-// conv out_c = sum_j w[c][j] in_c[j] over in_c = [state_c[0 .. ck-2], mixed_c],
-// SiLU; the state shifted by one (mixed_c last).  Blocks 0..Hk-1 (q heads) and
+// One launch, two kinds of block (blockDim = Sk; block-uniform roles):
+// blocks [0, C / Sk), one per group of Sk channels: the depthwise causal conv
+// out_c = sum_j w[c][j] in_c[j] over in_c = [state_c[0 .. ck-2], mixed_c],
+// SiLU; the state shifted by one (mixed_c last).  Groups 0..Hk-1 (q heads) and
 // Hk..2Hk-1 (k heads) are L2-normalised (x / sqrt(max(sum x^2, eps))), q then
 // times 1/sqrt(Sk).
-__global__ void k_ssm_conv(const float* __restrict__ mixed, const float* __restrict__ w, float* __restrict__ state,
-                           int ck, int Hk, int Sk, float eps, float* __restrict__ conv) {
+// Blocks [C / Sk, ...): one wave per alpha / beta row (rows 0..Hv-1 alpha,
+// Hv..2Hv-1 beta, fp32 weights [Hv][D]) on h = (x * rsqrt(mean(x^2) + eps)) *
+// attn_norm, which each wave forms from x itself: g = softplus(alpha . h +
+// dt_bias) * a (torch's softplus: x above 20 passes through, else
+// log1p(exp(x))), beta = sigmoid(beta . h).
+__global__ void k_ssm_conv_ab(const float* __restrict__ mixed, const float* __restrict__ w, float* __restrict__ state,
+                              int ck, int Hk, int Sk, float eps, float* __restrict__ conv, int nconv,
+                              const float* __restrict__ alpha, const float* __restrict__ beta,
+                              const float* __restrict__ dt_bias, const float* __restrict__ a,
+                              const float* __restrict__ x, const float* __restrict__ norm_w, int D, int Hv,
+                              float* __restrict__ gb) {
   __shared__ float red[16];
-  const int c = blockIdx.x * Sk + threadIdx.x, g = blockIdx.x;
-  float* st = state + (size_t)c * (ck - 1);
-  const float* wc = w + (size_t)c * ck;
-  const float xin = mixed[c];
-  float acc = 0.f;
-  for (int j = 0; j < ck - 1; ++j) acc = fmaf(wc[j], st[j], acc);
-  acc = fmaf(wc[ck - 1], xin, acc);
-  for (int j = 0; j + 1 < ck - 1; ++j) st[j] = st[j + 1];
-  if (ck > 1) st[ck - 2] = xin;
-  float v = acc / (1.0f + expf(-acc));
-  if (g < 2 * Hk) {                                              // block-uniform
-    const float ss = block_sum(v * v, red);
-    v = v / sqrtf(fmaxf(ss, eps));
-    if (g < Hk) v = v * (1.0f / sqrtf((float)Sk));
+  if ((int)blockIdx.x < nconv) {
+    const int c = blockIdx.x * Sk + threadIdx.x, g = blockIdx.x;
+    float* st = state + (size_t)c * (ck - 1);
+    const float* wc = w + (size_t)c * ck;
+    const float xin = mixed[c];
+    float acc = 0.f;
+    for (int j = 0; j < ck - 1; ++j) acc = fmaf(wc[j], st[j], acc);
+    acc = fmaf(wc[ck - 1], xin, acc);
+    for (int j = 0; j + 1 < ck - 1; ++j) st[j] = st[j + 1];
+    if (ck > 1) st[ck - 2] = xin;
+    float v = acc / (1.0f + expf(-acc));
+    if (g < 2 * Hk) {                                            // block-uniform
+      const float ss = block_sum(v * v, red);
+      v = v / sqrtf(fmaxf(ss, eps));
+      if (g < Hk) v = v * (1.0f / sqrtf((float)Sk));
+    }
+    conv[c] = v;
+    return;
   }
-  conv[c] = v;
+  const int lane = threadIdx.x & 63;
+  const int r = ((int)blockIdx.x - nconv) * ((int)blockDim.x >> 6) + (int)(threadIdx.x >> 6);
+  if (r >= 2 * Hv) return;
+  float ss = 0.f;
+  for (int i = lane; i < D; i += 64) ss = fmaf(x[i], x[i], ss);
+  const float rs = 1.0f / sqrtf(gm_wave_sum64(ss) / (float)D + eps);
+  const float* wr = r < Hv ? alpha + (size_t)r * D : beta + (size_t)(r - Hv) * D;
+  float sd = 0.f;
+  for (int i = lane; i < D; i += 64) sd = fmaf(wr[i], (x[i] * rs) * norm_w[i], sd);
+  sd = gm_wave_sum64(sd);
+  if (lane == 0) {
+    if (r < Hv) {
+      const float u = sd + dt_bias[r];
+      gb[r] = (u > 20.f ? u : log1pf(expf(u))) * a[r];
+    } else {
+      gb[r] = 1.0f / (1.0f + expf(-sd));
+    }
+  }
 }
 
 // Delta rule for V head hv, state columns v0 .. v0 + 31 (blockDim = 32 x KG):
@@ -309,15 +319,14 @@ int gm_attn_run(const gm_attn_layer* L, const float* x, float* y, float* kc, flo
                 const float* cosr, const float* sinr, int flags, uint8_t* ws, hipStream_t s) {
   const GmAttnWs lay = gm_attn_ws_layout(L, max_pos);
   const int D = L->D, Hq = L->n_head, Hkv = L->n_head_kv, Dh = L->head_dim, rd = L->rope_dim;
-  float* h = reinterpret_cast<float*>(ws + lay.h);
   float* qkv = reinterpret_cast<float*>(ws + lay.qkv);
   float* qr = reinterpret_cast<float*>(ws + lay.qr);
   float* part = reinterpret_cast<float*>(ws + lay.part);
   float* out = reinterpret_cast<float*>(ws + lay.out);
-  hipLaunchKernelGGL(k_rms_row, dim3(1), dim3(256), 0, s, x, L->attn_norm, D, L->eps, h);
-  GM_TRY(hipGetLastError());
   const int Mqkv = (2 * Hq + 2 * Hkv) * Dh;
-  if (int rc = gm_launch_mv_bf16(static_cast<const uint16_t*>(L->wqkv), Mqkv, D, h, 1, qkv, s)) return rc;
+  if (int rc = gm_launch_mv_bf16_norm2(static_cast<const uint16_t*>(L->wqkv), Mqkv, nullptr, 0, D, x, L->attn_norm,
+                                       L->eps, qkv, nullptr, s))
+    return rc;
   hipLaunchKernelGGL(k_attn_prep, dim3(Hq + Hkv), dim3(Dh), (Dh + 16) * sizeof(float), s, qkv, L->q_norm,
                      L->k_norm, L->eps, Hq, Hkv, Dh, rd, cosr + (size_t)pos * rd, sinr + (size_t)pos * rd, qr,
                      kc + (size_t)pos * Hkv * Dh, vc + (size_t)pos * Hkv * Dh);
@@ -359,22 +368,19 @@ int gm_ssm_run(const gm_ssm_layer* L, const float* x, float* y, float* conv_stat
   const GmSsmWs lay = gm_ssm_ws_layout(L);
   const int D = L->D, Hk = L->n_k_heads, Hv = L->n_v_heads, Sk = L->d_state, Sv = L->d_state;
   const int Ck = Hk * Sk, di = Hv * Sv, C = 2 * Ck + di;
-  float* h = reinterpret_cast<float*>(ws + lay.h);
   float* mixed = reinterpret_cast<float*>(ws + lay.mixed);
   float* z = reinterpret_cast<float*>(ws + lay.z);
   float* gb = reinterpret_cast<float*>(ws + lay.gb);
   float* conv = reinterpret_cast<float*>(ws + lay.conv);
   float* o = reinterpret_cast<float*>(ws + lay.o);
   float* o2 = reinterpret_cast<float*>(ws + lay.o2);
-  hipLaunchKernelGGL(k_rms_row, dim3(1), dim3(256), 0, s, x, L->attn_norm, D, L->eps, h);
-  GM_TRY(hipGetLastError());
-  if (int rc = gm_launch_mv_bf16(static_cast<const uint16_t*>(L->w_in), C, D, h, 1, mixed, s)) return rc;
-  if (int rc = gm_launch_mv_bf16(static_cast<const uint16_t*>(L->w_gate), di, D, h, 1, z, s)) return rc;
-  hipLaunchKernelGGL(k_ssm_ab, dim3((2 * Hv + 3) / 4), dim3(256), 0, s, L->alpha, L->beta, L->dt_bias, L->a, h, D,
-                     Hv, gb);
-  GM_TRY(hipGetLastError());
-  hipLaunchKernelGGL(k_ssm_conv, dim3(C / Sk), dim3(Sk), 0, s, mixed, L->conv1d, conv_state, L->conv_k, Hk, Sk,
-                     L->eps, conv);
+  if (int rc = gm_launch_mv_bf16_norm2(static_cast<const uint16_t*>(L->w_in), C,
+                                       static_cast<const uint16_t*>(L->w_gate), di, D, x, L->attn_norm, L->eps, mixed,
+                                       z, s))
+    return rc;
+  const int nconv = C / Sk, nab = (2 * Hv + Sk / 64 - 1) / (Sk / 64);
+  hipLaunchKernelGGL(k_ssm_conv_ab, dim3(nconv + nab), dim3(Sk), 0, s, mixed, L->conv1d, conv_state, L->conv_k, Hk,
+                     Sk, L->eps, conv, nconv, L->alpha, L->beta, L->dt_bias, L->a, x, L->attn_norm, D, Hv, gb);
   GM_TRY(hipGetLastError());
   const dim3 g(Hv, Sv / 32);
   switch (Sk / 8) {

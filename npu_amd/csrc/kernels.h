@@ -27,6 +27,10 @@ int gm_launch_gateup(int qtype, const void* wg, const void* wu, int FF, int D, c
 // One token, y = add + W x (add may be NULL).
 int gm_launch_mv_bf16_add(const uint16_t* w, int M, int K, const float* x, float* y, const float* add,
                           hipStream_t s);
+// One token: h = RMSNorm(x) (norm_w, eps; none when norm_w is null), y = W h and,
+// when w2 is given, y2 = W2 h with W2's M2 rows in the same launch.
+int gm_launch_mv_bf16_norm2(const uint16_t* w, int M, const uint16_t* w2, int M2, int K, const float* x,
+                            const float* norm_w, float eps, float* y, float* y2, hipStream_t s);
 int gm_launch_rms_row(const float* x, const float* w, int D, int n_rows, float eps, float* y, hipStream_t s);
 
 // Core-layer decode workspaces (core_decode.hip), byte offsets, 256-byte aligned.

@@ -29,23 +29,36 @@ namespace {
 
 constexpr int kSlotK = 512;                   // k values per slot (64 lanes x 8)
 
+// One-token extras of k_mv_bf16: a second matrix w2 [M2 x K] whose rows follow
+// w's in the launch (its products go to y2), and an RMSNorm weight: with
+// norm_w, x is staged as (x * rsqrt(mean(x^2) + eps)) * norm_w.
+struct MvEx {
+  const uint16_t* w2;
+  int M2;
+  float* y2;
+  const float* norm_w;
+  float eps;
+};
+
 template <int NT, int R, int S>
 __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w, int M, int K,
                                                  const float* __restrict__ x, int n_tok, float* __restrict__ y,
-                                                 const float* __restrict__ add) {
+                                                 const float* __restrict__ add, MvEx ex) {
   extern __shared__ gm_f32x4 xs4[];                               // [NT][K / 4]
+  __shared__ float red[4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + wave) * R;
   const int t0 = blockIdx.y * NT;
   const int nt = min(NT, n_tok - t0);
   const int npass = (K + S * kSlotK - 1) / (S * kSlotK);
   const float* xs = reinterpret_cast<const float*>(xs4);
+  const int Mt = M + ex.M2;
 
   const gm_u32x4* rp[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int row = min(row0 + r, M - 1);                        // rows past M: loaded, never stored
-    rp[r] = reinterpret_cast<const gm_u32x4*>(w + (int64_t)row * K);
+    const int row = min(row0 + r, Mt - 1);                       // rows past Mt: loaded, never stored
+    rp[r] = reinterpret_cast<const gm_u32x4*>(row < M ? w + (int64_t)row * K : ex.w2 + (int64_t)(row - M) * K);
   }
 
   float acc[R][NT];
@@ -70,10 +83,21 @@ __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w,
     }
     if (p == 0) {
       const int kq = K >> 2;
+      float ss = 0.f;
       for (int i = threadIdx.x; i < NT * kq; i += 256) {
         const int t = i / kq;
-        xs4[i] = t < nt ? reinterpret_cast<const gm_f32x4*>(x + (int64_t)(t0 + t) * K)[i - t * kq]
-                        : gm_f32x4{0.f, 0.f, 0.f, 0.f};
+        const gm_f32x4 v = t < nt ? reinterpret_cast<const gm_f32x4*>(x + (int64_t)(t0 + t) * K)[i - t * kq]
+                                  : gm_f32x4{0.f, 0.f, 0.f, 0.f};
+        xs4[i] = v;
+        ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+      }
+      if (ex.norm_w) {                                           // one token (the launcher checks)
+        ss = gm_wave_sum64(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        const float rs = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + ex.eps);
+        const gm_f32x4* nw4 = reinterpret_cast<const gm_f32x4*>(ex.norm_w);
+        for (int i = threadIdx.x; i < kq; i += 256) xs4[i] = (xs4[i] * rs) * nw4[i];
       }
       __syncthreads();
     }
@@ -109,6 +133,8 @@ __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w,
       if (lane == 0 && row0 + r < M && t < nt) {
         const int64_t i = (int64_t)(t0 + t) * M + row0 + r;
         y[i] = add ? add[i] + v : v;                             // y = add + W x (a residual), or W x
+      } else if (lane == 0 && row0 + r >= M && row0 + r < Mt && t < nt) {
+        ex.y2[(int64_t)(t0 + t) * ex.M2 + row0 + r - M] = v;
       }
     }
   }
@@ -241,11 +267,11 @@ int launch_mfma(const uint16_t* w, int M, int K, const float* x, int n_tok, floa
 
 template <int NT, int R, int S>
 int launch_mv(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, const float* add,
-              hipStream_t s) {
+              const MvEx& ex, hipStream_t s) {
   const size_t smem = (size_t)NT * K * sizeof(float);
   if (int rc = gm_set_smem(k_mv_bf16<NT, R, S>, smem)) return rc;
-  const dim3 grid((unsigned)((M + 4 * R - 1) / (4 * R)), (unsigned)((n_tok + NT - 1) / NT));
-  hipLaunchKernelGGL((k_mv_bf16<NT, R, S>), grid, dim3(256), smem, s, w, M, K, x, n_tok, y, add);
+  const dim3 grid((unsigned)((M + ex.M2 + 4 * R - 1) / (4 * R)), (unsigned)((n_tok + NT - 1) / NT));
+  hipLaunchKernelGGL((k_mv_bf16<NT, R, S>), grid, dim3(256), smem, s, w, M, K, x, n_tok, y, add, ex);
   GM_TRY(hipGetLastError());
   return GM_OK;
 }
@@ -253,13 +279,13 @@ int launch_mv(const uint16_t* w, int M, int K, const float* x, int n_tok, float*
 // S = the row's slots (at most 16 per pass), one row per wave (the most
 // waves, each with its whole row in flight, was the fastest launch shape).
 int launch_mv1(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, const float* add,
-               hipStream_t s) {
+               hipStream_t s, const MvEx& ex = MvEx{nullptr, 0, nullptr, nullptr, 0.f}) {
   const int slots = (K + kSlotK - 1) / kSlotK;
-  if (slots <= 1) return launch_mv<1, 1, 1>(w, M, K, x, n_tok, y, add, s);
-  if (slots <= 2) return launch_mv<1, 1, 2>(w, M, K, x, n_tok, y, add, s);
-  if (slots <= 4) return launch_mv<1, 1, 4>(w, M, K, x, n_tok, y, add, s);
-  if (slots <= 8) return launch_mv<1, 1, 8>(w, M, K, x, n_tok, y, add, s);
-  return launch_mv<1, 1, 16>(w, M, K, x, n_tok, y, add, s);
+  if (slots <= 1) return launch_mv<1, 1, 1>(w, M, K, x, n_tok, y, add, ex, s);
+  if (slots <= 2) return launch_mv<1, 1, 2>(w, M, K, x, n_tok, y, add, ex, s);
+  if (slots <= 4) return launch_mv<1, 1, 4>(w, M, K, x, n_tok, y, add, ex, s);
+  if (slots <= 8) return launch_mv<1, 1, 8>(w, M, K, x, n_tok, y, add, ex, s);
+  return launch_mv<1, 1, 16>(w, M, K, x, n_tok, y, add, ex, s);
 }
 
 }  // namespace
@@ -276,4 +302,12 @@ int gm_launch_mv_bf16(const uint16_t* w, int M, int K, const float* x, int n_tok
 int gm_launch_mv_bf16_add(const uint16_t* w, int M, int K, const float* x, float* y, const float* add,
                           hipStream_t s) {
   return launch_mv1(w, M, K, x, 1, y, add, s);
+}
+
+// One token, the core layers' input projections in one launch: h = RMSNorm(x)
+// (norm_w, eps; skipped when norm_w is null), y = W h and, when w2 is given,
+// y2 = W2 h (its M2 rows follow W's in the launch).
+int gm_launch_mv_bf16_norm2(const uint16_t* w, int M, const uint16_t* w2, int M2, int K, const float* x,
+                            const float* norm_w, float eps, float* y, float* y2, hipStream_t s) {
+  return launch_mv1(w, M, K, x, 1, y, nullptr, s, MvEx{w2, w2 ? M2 : 0, y2, norm_w, eps});
 }

@@ -143,3 +143,10 @@ def test_core_layer_argument_errors_without_gpu():
     assert lib.gm_ssm_workspace_bytes(ctypes.byref(bad), ) == 0 and "multiple" in L.last_error()
     rc = lib.gm_ssm_decode(ctypes.byref(s), 1024, 1024, 4096, 4096, 0, 1 << 20, m, None)
     assert rc == L.GM_EINVAL and "alias" in L.last_error()
+    # the input projections form the RMSNorm from attn_norm with 16-byte loads
+    bad = L.GmAttnLayer.from_buffer_copy(a)
+    bad.attn_norm = 260
+    assert lib.gm_attn_workspace_bytes(ctypes.byref(bad), 4096) == 0 and "attn_norm" in L.last_error()
+    bad = L.GmSsmLayer.from_buffer_copy(s)
+    bad.attn_norm = 260
+    assert lib.gm_ssm_workspace_bytes(ctypes.byref(bad)) == 0 and "attn_norm" in L.last_error()
