@@ -40,18 +40,26 @@ struct MvEx {
   float eps;
 };
 
-template <int NT, int R, int S>
+// One token.  Per pass of S slots: the pass's x values are loaded into
+// registers first (their loads retire before the weights', vmcnt being in
+// issue order), then every weight load of the pass, all unconditional (lanes
+// and slots past K reload the last granule and are zeroed by a select, so no
+// branch separates a load from its use); x goes to LDS while the weights are
+// in flight (normalised first with ex.norm_w), and each slot is multiplied as
+// it lands.
+template <int R, int S>
 __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w, int M, int K,
-                                                 const float* __restrict__ x, int n_tok, float* __restrict__ y,
+                                                 const float* __restrict__ x, float* __restrict__ y,
                                                  const float* __restrict__ add, MvEx ex) {
-  extern __shared__ gm_f32x4 xs4[];                               // [NT][K / 4]
+  extern __shared__ gm_f32x4 xs4[];                               // [XQ x 256]: one pass of x
   __shared__ float red[4];
+  constexpr int XQ = (S * kSlotK / 4 + 255) / 256;                // x float4 per thread and pass
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * 4 + wave) * R;
-  const int t0 = blockIdx.y * NT;
-  const int nt = min(NT, n_tok - t0);
   const int npass = (K + S * kSlotK - 1) / (S * kSlotK);
+  const int kq = K >> 2, ng = K >> 3;
   const float* xs = reinterpret_cast<const float*>(xs4);
+  const gm_f32x4* x4 = reinterpret_cast<const gm_f32x4*>(x);
   const int Mt = M + ex.M2;
 
   const gm_u32x4* rp[R];
@@ -61,81 +69,79 @@ __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w,
     rp[r] = reinterpret_cast<const gm_u32x4*>(row < M ? w + (int64_t)row * K : ex.w2 + (int64_t)(row - M) * K);
   }
 
-  float acc[R][NT];
+  float acc[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int t = 0; t < NT; ++t) acc[r][t] = 0.f;
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
 
   for (int p = 0; p < npass; ++p) {
+    const int q0 = p * (S * kSlotK / 4);                          // first float4 of the pass
+    // x and the norm weights (x again without a norm: a harmless duplicate)
+    const gm_f32x4* n4 = ex.norm_w ? reinterpret_cast<const gm_f32x4*>(ex.norm_w) : x4;
+    gm_f32x4 xr[XQ], nr[XQ];
+#pragma unroll
+    for (int q = 0; q < XQ; ++q) {
+      const int i = q0 + (int)threadIdx.x + 256 * q, ic = i < kq ? i : kq - 1;   // past K: zeroed below
+      xr[q] = x4[ic];
+      nr[q] = n4[ic];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     gm_u32x4 wv[R][S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const int gb = (p * S + s) * 64;                           // first 16-byte granule of the slot
-      if (8 * gb < K) {                                          // wave-uniform
-        const int g = min(gb + lane, (K >> 3) - 1);              // lanes past K reload the last granule
+      const int g = min((p * S + s) * 64 + lane, ng - 1);
 #pragma unroll
-        for (int r = 0; r < R; ++r) wv[r][s] = gm_ld<true>(rp[r] + g);
-      } else {
-#pragma unroll
-        for (int r = 0; r < R; ++r) wv[r][s] = gm_u32x4{0u, 0u, 0u, 0u};
-      }
+      for (int r = 0; r < R; ++r) wv[r][s] = gm_ld<true>(rp[r] + g);
     }
-    if (p == 0) {
-      const int kq = K >> 2;
+    __builtin_amdgcn_sched_barrier(0);
+    if (p > 0) __syncthreads();                                   // the previous pass's x reads are done
+#pragma unroll
+    for (int q = 0; q < XQ; ++q)
+      if (q0 + (int)threadIdx.x + 256 * q >= kq) xr[q] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+    if (ex.norm_w) {                                              // one pass (the launcher checks)
       float ss = 0.f;
-      for (int i = threadIdx.x; i < NT * kq; i += 256) {
-        const int t = i / kq;
-        const gm_f32x4 v = t < nt ? reinterpret_cast<const gm_f32x4*>(x + (int64_t)(t0 + t) * K)[i - t * kq]
-                                  : gm_f32x4{0.f, 0.f, 0.f, 0.f};
-        xs4[i] = v;
-        ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
-      }
-      if (ex.norm_w) {                                           // one token (the launcher checks)
-        ss = gm_wave_sum64(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        const float rs = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + ex.eps);
-        const gm_f32x4* nw4 = reinterpret_cast<const gm_f32x4*>(ex.norm_w);
-        for (int i = threadIdx.x; i < kq; i += 256) xs4[i] = (xs4[i] * rs) * nw4[i];
-      }
+#pragma unroll
+      for (int q = 0; q < XQ; ++q)
+        ss = fmaf(xr[q].x, xr[q].x, fmaf(xr[q].y, xr[q].y, fmaf(xr[q].z, xr[q].z, fmaf(xr[q].w, xr[q].w, ss))));
+      ss = gm_wave_sum64(ss);
+      if (lane == 0) red[wave] = ss;
       __syncthreads();
+      const float rs = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + ex.eps);
+#pragma unroll
+      for (int q = 0; q < XQ; ++q) xr[q] = (xr[q] * rs) * nr[q];
     }
+#pragma unroll
+    for (int q = 0; q < XQ; ++q) xs4[threadIdx.x + 256 * q] = xr[q];   // unconditional: XQ x 256 slots
+    __syncthreads();
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const int k0 = 8 * ((p * S + s) * 64 + lane);
-      if (k0 >= K) continue;
+      const bool live = k0 < K;
+      const int kl = 8 * (s * 64 + lane);                         // offset in the pass's x
+      const gm_f32x4 xa = *reinterpret_cast<const gm_f32x4*>(xs + kl);
+      const gm_f32x4 xb = *reinterpret_cast<const gm_f32x4*>(xs + kl + 4);
+      const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const gm_f32x4 xa = *reinterpret_cast<const gm_f32x4*>(xs + t * K + k0);
-        const gm_f32x4 xb = *reinterpret_cast<const gm_f32x4*>(xs + t * K + k0 + 4);
-        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+      for (int r = 0; r < R; ++r) {
+        const uint32_t u[4] = {live ? wv[r][s].x : 0u, live ? wv[r][s].y : 0u, live ? wv[r][s].z : 0u,
+                               live ? wv[r][s].w : 0u};
+        float a = acc[r];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const uint32_t u[4] = {wv[r][s].x, wv[r][s].y, wv[r][s].z, wv[r][s].w};
-          float a = acc[r][t];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            a = fmaf(__uint_as_float(u[j] << 16), xv[2 * j], a);
-            a = fmaf(__uint_as_float(u[j] & 0xffff0000u), xv[2 * j + 1], a);
-          }
-          acc[r][t] = a;
+        for (int j = 0; j < 4; ++j) {
+          a = fmaf(__uint_as_float(u[j] << 16), xv[2 * j], a);
+          a = fmaf(__uint_as_float(u[j] & 0xffff0000u), xv[2 * j + 1], a);
         }
+        acc[r] = a;
       }
     }
   }
 
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const float v = gm_wave_sum64(acc[r][t]);
-      if (lane == 0 && row0 + r < M && t < nt) {
-        const int64_t i = (int64_t)(t0 + t) * M + row0 + r;
-        y[i] = add ? add[i] + v : v;                             // y = add + W x (a residual), or W x
-      } else if (lane == 0 && row0 + r >= M && row0 + r < Mt && t < nt) {
-        ex.y2[(int64_t)(t0 + t) * ex.M2 + row0 + r - M] = v;
-      }
+    const float v = gm_wave_sum64(acc[r]);
+    if (lane == 0 && row0 + r < M) {
+      y[row0 + r] = add ? add[row0 + r] + v : v;                  // y = add + W x (a residual), or W x
+    } else if (lane == 0 && row0 + r >= M && row0 + r < Mt) {
+      ex.y2[row0 + r - M] = v;
     }
   }
 }
@@ -265,27 +271,29 @@ int launch_mfma(const uint16_t* w, int M, int K, const float* x, int n_tok, floa
 #undef GM_MV_W
 }
 
-template <int NT, int R, int S>
-int launch_mv(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, const float* add,
-              const MvEx& ex, hipStream_t s) {
-  const size_t smem = (size_t)NT * K * sizeof(float);
-  if (int rc = gm_set_smem(k_mv_bf16<NT, R, S>, smem)) return rc;
-  const dim3 grid((unsigned)((M + ex.M2 + 4 * R - 1) / (4 * R)), (unsigned)((n_tok + NT - 1) / NT));
-  hipLaunchKernelGGL((k_mv_bf16<NT, R, S>), grid, dim3(256), smem, s, w, M, K, x, n_tok, y, add, ex);
+template <int R, int S>
+int launch_mv(const uint16_t* w, int M, int K, const float* x, float* y, const float* add, const MvEx& ex,
+              hipStream_t s) {
+  const size_t smem = (size_t)((S * kSlotK / 4 + 255) / 256) * 256 * sizeof(gm_f32x4);   // XQ x 256 float4
+  if (int rc = gm_set_smem(k_mv_bf16<R, S>, smem)) return rc;
+  const dim3 grid((unsigned)((M + ex.M2 + 4 * R - 1) / (4 * R)));
+  hipLaunchKernelGGL((k_mv_bf16<R, S>), grid, dim3(256), smem, s, w, M, K, x, y, add, ex);
   GM_TRY(hipGetLastError());
   return GM_OK;
 }
 
 // S = the row's slots (at most 16 per pass), one row per wave (the most
 // waves, each with its whole row in flight, was the fastest launch shape).
-int launch_mv1(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, const float* add,
-               hipStream_t s, const MvEx& ex = MvEx{nullptr, 0, nullptr, nullptr, 0.f}) {
+// The RMSNorm of ex.norm_w needs the whole row in one pass (K <= 8192).
+int launch_mv1(const uint16_t* w, int M, int K, const float* x, float* y, const float* add, hipStream_t s,
+               const MvEx& ex = MvEx{nullptr, 0, nullptr, nullptr, 0.f}) {
   const int slots = (K + kSlotK - 1) / kSlotK;
-  if (slots <= 1) return launch_mv<1, 1, 1>(w, M, K, x, n_tok, y, add, ex, s);
-  if (slots <= 2) return launch_mv<1, 1, 2>(w, M, K, x, n_tok, y, add, ex, s);
-  if (slots <= 4) return launch_mv<1, 1, 4>(w, M, K, x, n_tok, y, add, ex, s);
-  if (slots <= 8) return launch_mv<1, 1, 8>(w, M, K, x, n_tok, y, add, ex, s);
-  return launch_mv<1, 1, 16>(w, M, K, x, n_tok, y, add, ex, s);
+  if (ex.norm_w && slots > 16) return gm_fail_arg("mv_bf16: a fused RMSNorm needs K <= %d", 16 * kSlotK);
+  if (slots <= 1) return launch_mv<1, 1>(w, M, K, x, y, add, ex, s);
+  if (slots <= 2) return launch_mv<1, 2>(w, M, K, x, y, add, ex, s);
+  if (slots <= 4) return launch_mv<1, 4>(w, M, K, x, y, add, ex, s);
+  if (slots <= 8) return launch_mv<1, 8>(w, M, K, x, y, add, ex, s);
+  return launch_mv<1, 16>(w, M, K, x, y, add, ex, s);
 }
 
 }  // namespace
@@ -294,14 +302,14 @@ int launch_mv1(const uint16_t* w, int M, int K, const float* x, int n_tok, float
 // caller).  One token: the streaming FMA kernel; more: the MFMA kernel, 16
 // tokens per column tile.
 int gm_launch_mv_bf16(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s) {
-  if (n_tok == 1) return launch_mv1(w, M, K, x, n_tok, y, nullptr, s);
+  if (n_tok == 1) return launch_mv1(w, M, K, x, y, nullptr, s);
   return launch_mfma(w, M, K, x, n_tok, y, s);
 }
 
 // One token, y = add + W x (the residual of the core layers' output projections).
 int gm_launch_mv_bf16_add(const uint16_t* w, int M, int K, const float* x, float* y, const float* add,
                           hipStream_t s) {
-  return launch_mv1(w, M, K, x, 1, y, add, s);
+  return launch_mv1(w, M, K, x, y, add, s);
 }
 
 // One token, the core layers' input projections in one launch: h = RMSNorm(x)
@@ -309,5 +317,5 @@ int gm_launch_mv_bf16_add(const uint16_t* w, int M, int K, const float* x, float
 // y2 = W2 h (its M2 rows follow W's in the launch).
 int gm_launch_mv_bf16_norm2(const uint16_t* w, int M, const uint16_t* w2, int M2, int K, const float* x,
                             const float* norm_w, float eps, float* y, float* y2, hipStream_t s) {
-  return launch_mv1(w, M, K, x, 1, y, nullptr, s, MvEx{w2, w2 ? M2 : 0, y2, norm_w, eps});
+  return launch_mv1(w, M, K, x, y, nullptr, s, MvEx{w2, w2 ? M2 : 0, y2, norm_w, eps});
 }
