@@ -281,8 +281,8 @@ typedef struct gm_ssm_layer {
   const void* w_in;         /* bf16 [2 n_k_heads d_state + n_v_heads d_state][D] (attn_qkv) */
   const void* w_gate;       /* bf16 [n_v_heads d_state][D] (attn_gate) */
   const void* w_out;        /* bf16 [D][n_v_heads d_state] (ssm_out) */
-  const float* alpha;       /* [n_v_heads][D] (ssm_alpha) */
-  const float* beta;        /* [n_v_heads][D] (ssm_beta) */
+  const float* alpha;       /* [n_v_heads][D] (ssm_alpha), 16-byte aligned */
+  const float* beta;        /* [n_v_heads][D] (ssm_beta), 16-byte aligned */
   const float* conv1d;      /* [conv channels][conv_k] (ssm_conv1d) */
   const float* a;           /* [n_v_heads] (ssm_a) */
   const float* dt_bias;     /* [n_v_heads] (ssm_dt.bias) */

@@ -342,10 +342,10 @@ static int check_ssm(const gm_ssm_layer* L) {
   if (L->D <= 0 || L->D % GM_SUB || L->D > 16384 || L->n_v_heads * S > 16384)
     return gm_fail_arg("gm_ssm_decode: D=%d must be a multiple of 32 up to 16384", L->D);
   if (!(L->eps >= 0.f)) return gm_fail_arg("gm_ssm_decode: eps must be >= 0");
-  const void* w[] = {L->w_in, L->w_gate, L->w_out, L->attn_norm};
+  const void* w[] = {L->w_in, L->w_gate, L->w_out, L->attn_norm, L->alpha, L->beta};
   for (const void* p : w)
     if (reinterpret_cast<uintptr_t>(p) % 16)
-      return gm_fail_arg("gm_ssm_decode: bf16 weights and attn_norm must be 16-byte aligned");
+      return gm_fail_arg("gm_ssm_decode: bf16 weights, alpha, beta and attn_norm must be 16-byte aligned");
   return GM_OK;
 }
 

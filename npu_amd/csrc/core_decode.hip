@@ -37,6 +37,7 @@ namespace {
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 constexpr int kAttnChunk = 64;     // cached positions per attention partial
+constexpr int kAttnNB = 8;         // positions per wave and load round (4 waves: 32 per round)
 
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = gm_wave_sum64(v);
@@ -117,22 +118,33 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ qr,
 #pragma unroll
   for (int d = 0; d < DV; ++d) { q[d] = qr[(size_t)Dh * hq + lane + 64 * d]; acc[d] = 0.f; }
   float m = -__builtin_inff(), l = 0.f;
-  for (int t = c0 + wave; t < c1; t += 4) {
-    const float* kt = kc + ((size_t)t * Hkv + hk) * Dh;
-    const float* vt = vc + ((size_t)t * Hkv + hk) * Dh;
-    float kv[DV], vv[DV];
+  // kAttnNB positions per round, every k / v load of the round issued before
+  // the first use; positions past c1 reload the last one and leave the state
+  // unchanged (selects, so no branch separates a load from its use)
+  for (int t0 = c0 + wave; t0 < c1; t0 += 4 * kAttnNB) {
+    float kv[kAttnNB][DV], vv[kAttnNB][DV];
 #pragma unroll
-    for (int d = 0; d < DV; ++d) { kv[d] = kt[lane + 64 * d]; vv[d] = vt[lane + 64 * d]; }
-    float s = 0.f;
+    for (int j = 0; j < kAttnNB; ++j) {
+      const int t = t0 + 4 * j, tc = t < c1 ? t : c1 - 1;
+      const float* kt = kc + ((size_t)tc * Hkv + hk) * Dh;
+      const float* vt = vc + ((size_t)tc * Hkv + hk) * Dh;
 #pragma unroll
-    for (int d = 0; d < DV; ++d) s = fmaf(q[d], kv[d], s);
-    s = gm_wave_sum64(s) * scale;
-    const float mn = fmaxf(m, s);
-    const float a = expf(m - mn), p = expf(s - mn);
-    l = l * a + p;
+      for (int d = 0; d < DV; ++d) { kv[j][d] = kt[lane + 64 * d]; vv[j][d] = vt[lane + 64 * d]; }
+    }
 #pragma unroll
-    for (int d = 0; d < DV; ++d) acc[d] = fmaf(acc[d], a, p * vv[d]);
-    m = mn;
+    for (int j = 0; j < kAttnNB; ++j) {
+      const bool live = t0 + 4 * j < c1;                         // wave-uniform
+      float s = 0.f;
+#pragma unroll
+      for (int d = 0; d < DV; ++d) s = fmaf(q[d], kv[j][d], s);
+      s = gm_wave_sum64(s) * scale;
+      const float mn = fmaxf(m, s);
+      const float a = expf(m - mn), p = expf(s - mn);
+      l = live ? l * a + p : l;
+#pragma unroll
+      for (int d = 0; d < DV; ++d) acc[d] = live ? fmaf(acc[d], a, p * vv[j][d]) : acc[d];
+      m = live ? mn : m;
+    }
   }
   if (lane == 0) { ms[wave] = m; ls[wave] = l; }
 #pragma unroll
@@ -186,7 +198,7 @@ __global__ void k_attn_combine(const float* __restrict__ part, int ld, int nch, 
 // attn_norm, which each wave forms from x itself: g = softplus(alpha . h +
 // dt_bias) * a (torch's softplus: x above 20 passes through, else
 // log1p(exp(x))), beta = sigmoid(beta . h).
-__global__ void k_ssm_conv_ab(const float* __restrict__ mixed, const float* __restrict__ w, float* __restrict__ state,
+__global__ void __launch_bounds__(256) k_ssm_conv_ab(const float* __restrict__ mixed, const float* __restrict__ w, float* __restrict__ state,
                               int ck, int Hk, int Sk, float eps, float* __restrict__ conv, int nconv,
                               const float* __restrict__ alpha, const float* __restrict__ beta,
                               const float* __restrict__ dt_bias, const float* __restrict__ a,
@@ -215,13 +227,37 @@ __global__ void k_ssm_conv_ab(const float* __restrict__ mixed, const float* __re
   const int lane = threadIdx.x & 63;
   const int r = ((int)blockIdx.x - nconv) * ((int)blockDim.x >> 6) + (int)(threadIdx.x >> 6);
   if (r >= 2 * Hv) return;
-  float ss = 0.f;
-  for (int i = lane; i < D; i += 64) ss = fmaf(x[i], x[i], ss);
+  // alpha . h = rs (alpha . (x * norm_w)): one pass over x, the row and the norm
+  // weight in float4s, every load of a round (8 per lane and array) issued
+  // before the first use (D % 32 == 0; lanes past D reload the last float4
+  // and add nothing)
+  const gm_f32x4* x4 = reinterpret_cast<const gm_f32x4*>(x);
+  const gm_f32x4* n4 = reinterpret_cast<const gm_f32x4*>(norm_w);
+  const gm_f32x4* w4 = reinterpret_cast<const gm_f32x4*>(r < Hv ? alpha + (size_t)r * D : beta + (size_t)(r - Hv) * D);
+  const int d4 = D >> 2;
+  float ss = 0.f, sd = 0.f;
+  for (int i0 = 0; i0 < d4; i0 += 64 * 8) {
+    gm_f32x4 xv[8], wv[8], nv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + lane + 64 * u, ic = i < d4 ? i : d4 - 1;
+      xv[u] = x4[ic];
+      wv[u] = w4[ic];
+      nv[u] = n4[ic];
+    }
+    __builtin_amdgcn_sched_barrier(0);                           // all 24 loads before the first use
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const bool live = i0 + lane + 64 * u < d4;
+      const gm_f32x4 xn = xv[u] * nv[u];
+      const float q = fmaf(xv[u].x, xv[u].x, fmaf(xv[u].y, xv[u].y, fmaf(xv[u].z, xv[u].z, xv[u].w * xv[u].w)));
+      const float t = fmaf(wv[u].x, xn.x, fmaf(wv[u].y, xn.y, fmaf(wv[u].z, xn.z, wv[u].w * xn.w)));
+      ss += live ? q : 0.f;
+      sd += live ? t : 0.f;
+    }
+  }
   const float rs = 1.0f / sqrtf(gm_wave_sum64(ss) / (float)D + eps);
-  const float* wr = r < Hv ? alpha + (size_t)r * D : beta + (size_t)(r - Hv) * D;
-  float sd = 0.f;
-  for (int i = lane; i < D; i += 64) sd = fmaf(wr[i], (x[i] * rs) * norm_w[i], sd);
-  sd = gm_wave_sum64(sd);
+  sd = rs * gm_wave_sum64(sd);
   if (lane == 0) {
     if (r < Hv) {
       const float u = sd + dt_bias[r];
