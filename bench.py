@@ -397,6 +397,8 @@ def run_decode_step(moe_layers, n_prefill: int = 64, steps: int = 20, seed: int 
 
 
 DENSE_SHAPES = (("ssm_in", 8192, 2048), ("ssm_gate", 4096, 2048), ("ssm_out", 2048, 4096))
+# on request only (--dense-shapes lm_head): the output projection, 1 GB, 2 distinct copies
+DENSE_EXTRA = (("lm_head", 248_320, 2048),)
 
 
 def run_dense_mv(dev, n_layers: int = 30, reps: int = 20, shapes=None, tokens=(1, 8)):
@@ -413,12 +415,14 @@ def run_dense_mv(dev, n_layers: int = 30, reps: int = 20, shapes=None, tokens=(1
     from npu_amd.gguf_types import GGMLQuantizationType as QT
     gen = torch.Generator(device=dev)
     gen.manual_seed(SEED + 30)
-    todo = [sh for sh in DENSE_SHAPES if shapes is None or sh[0] in shapes]
-    Ws = {name: [(torch.randn(M, K, generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(n_layers)]
+    todo = [sh for sh in DENSE_SHAPES + DENSE_EXTRA if (shapes is None and sh in DENSE_SHAPES)
+            or (shapes is not None and sh[0] in shapes)]
+    nl = {name: (2 if M * K * 2 > (1 << 29) else n_layers) for name, M, K in todo}     # >= 2 GB per shape
+    Ws = {name: [(torch.randn(M, K, generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(nl[name])]
           for name, M, K in todo}
     lib = L.lib()
 
-    def period_us(fn):
+    def period_us(fn, launches):
         fn()
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
@@ -432,7 +436,7 @@ def run_dense_mv(dev, n_layers: int = 30, reps: int = 20, shapes=None, tokens=(1
             g.replay()
         e1.record()
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (reps * n_layers)
+        return e0.elapsed_time(e1) * 1e3 / (reps * launches)
 
     out = {"workload": f"SSM projections (qwen/test_npu_ssm.py shapes), bf16 weights, {n_layers} distinct layers",
            "shapes": {}}
@@ -452,10 +456,10 @@ def run_dense_mv(dev, n_layers: int = 30, reps: int = 20, shapes=None, tokens=(1
                 for W in Ws[name]:
                     torch.nn.functional.linear(xb, W)
 
-            us = period_us(ours)
+            us = period_us(ours, nl[name])
             ref = x.double() @ Ws[name][-1].double().T
             rel = float((y.double() - ref).abs().max() / ref.abs().max())
-            tus = period_us(torch_linear)
+            tus = period_us(torch_linear, nl[name])
             gbps = (wbytes + T * (K + M) * 4) / (us * 1e-6) / 1e9
             out["shapes"][f"{name}_T{T}"] = {
                 "M": M, "K": K, "T": T, "us_per_launch": us, "weight_GBps": wbytes / (us * 1e-6) / 1e9,
