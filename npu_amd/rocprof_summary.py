@@ -13,6 +13,9 @@ instruction counters of one ``--pmc`` pass (``SQ_WAVES``, ``SQ_INSTS_VALU``,
 ``SQ_INSTS_SALU``, ``SQ_INSTS_LDS``, ``SQ_INSTS_VMEM_RD``: device totals per dispatch),
 with the VALU issue time they imply (``<name>.md``).
 
+With ``--durations`` it tabulates the kernel-stats CSV alone (optionally per unit of
+work, ``--per``).
+
 With ``--trace T.csv`` it tabulates durations per kernel and launch shape (grid size)
 from a kernel trace; ``--grid-pmc`` counter CSVs add, per shape, the copy-calibrated
 HBM bytes (FETCH_SIZE / WRITE_SIZE) and instruction counts per wave.
@@ -116,7 +119,7 @@ def prefill_summary(a) -> None:
     pmc = counter_table(a.prefill_pmc)
     kernels = {}
     for name, st in stats.items():
-        if not (family(name).startswith("k_pf_") or family(name) == "k_dispatch"):
+        if not (family(name).startswith(("k_pf_", "k_pfs_")) or family(name) == "k_dispatch"):
             continue
         c = pmc.get(name, {})
         flops = c.get("MfmaFlopsF16", 0.0) + c.get("MfmaFlopsBF16", 0.0)
@@ -163,6 +166,30 @@ def inst_summary(a) -> None:
         lines.append(f"| {name[:60]} | {st['calls']} | {st['avg_us']:.2f} | {w:.0f} | "
                      f"{c.get('SQ_INSTS_VALU', 0) / w:.0f} | {c.get('SQ_INSTS_SALU', 0) / w:.0f} | "
                      f"{c.get('SQ_INSTS_LDS', 0) / w:.0f} | {c.get('SQ_INSTS_VMEM_RD', 0) / w:.0f} | {valu_us:.2f} |")
+    out = Path(a.out)
+    out.mkdir(parents=True, exist_ok=True)
+    (out / f"{a.name}.md").write_text("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def durations(a) -> None:
+    """Durations per kernel from a ``--kernel-trace --stats`` kernel-stats CSV (kernels whose
+    name contains ``--kernel`` only), with each kernel's total per unit of work when
+    ``--per N`` gives the units the run timed (e.g. decode steps)."""
+    stats = kernel_stats(a.stats)
+    rows = [(n, st) for n, st in stats.items() if not a.kernel or a.kernel in n]
+    rows.sort(key=lambda kv: -kv[1]["calls"] * kv[1]["avg_us"])
+    head = "| kernel | calls | avg us | min us | max us |" + (" us per unit |" if a.per else "")
+    lines = [f"# {a.name}: kernel durations", "", a.commands, "", head,
+             "|---|---|---|---|---|" + ("---|" if a.per else "")]
+    total = 0.0
+    for n, st in rows:
+        per = st["calls"] * st["avg_us"] / a.per if a.per else None
+        total += per or 0.0
+        lines.append(f"| {n[:70]} | {st['calls']} | {st['avg_us']:.2f} | {st['min_us']:.2f} | {st['max_us']:.2f} |"
+                     + (f" {per:.1f} |" if per is not None else ""))
+    if a.per:
+        lines += ["", f"Sum over the listed kernels: {total:.1f} us per unit ({a.per} units)."]
     out = Path(a.out)
     out.mkdir(parents=True, exist_ok=True)
     (out / f"{a.name}.md").write_text("\n".join(lines) + "\n")
@@ -259,12 +286,18 @@ def main() -> None:
                     help="KERNEL=BYTES: algorithmic bytes per launch of a kernel family (replaces the "
                          "T = 1 decode table; repeatable); in trace mode KERNEL@GRID=BYTES")
     ap.add_argument("--json", default="hbm_traffic.json", help="name of the JSON written to --out")
+    ap.add_argument("--durations", action="store_true",
+                    help="durations mode: the kernel-stats table of --stats (filter --kernel, units --per)")
+    ap.add_argument("--per", type=float, default=0.0, help="durations mode: units of work the run timed")
     a = ap.parse_args()
     if a.trace:
         trace_by_grid(a)
         return
     if not a.stats:
         ap.error("--stats is required outside trace mode")
+    if a.durations:
+        durations(a)
+        return
     if a.prefill_pmc:
         prefill_summary(a)
         return
