@@ -221,7 +221,14 @@ int gm_moe_forward_stage(const gm_moe_layer* L, const float* x, float* y, int T,
  * (fp64 accumulators in the next layer's workspace), so the chain runs one
  * router launch and then two launches per layer; results equal gm_moe_forward
  * layer by layer to fp32 rounding (the logits are the same dot products added
- * in another order).  Otherwise each layer runs as gm_moe_forward.  After the
+ * in another order).  At 2 <= T <= 8 (decode path), when D is a multiple of
+ * 256 up to 4096, layers 1 .. n-1 carry router_t and consecutive layers'
+ * workspaces do not overlap, each layer's combine kernel also forms the next
+ * layer's router partials over 256-column slices, sums of x^2 and activation
+ * limb rows in the next layer's workspace, so the chain runs one router
+ * launch and then four launches per layer (routing, gate/up, down, combine),
+ * again equal to gm_moe_forward layer by layer to fp32 rounding.  Otherwise
+ * each layer runs as gm_moe_forward.  After the
  * call each workspace holds its layer's intermediates
  * (gm_moe_workspace_offsets) when the layers' workspaces are distinct.
  */
@@ -231,8 +238,10 @@ int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float
 /*
  * Which path gm_moe_chain takes for these layers and T, without running it:
  * 1 = the accumulator-linked T = 1 kernels (one router launch, then two
- * launches per layer), 0 = one gm_moe_forward per layer, negative = a
- * rejected layer (GM_E*).  No counterpart in the reference (its decoder loop
+ * launches per layer), 2 = the combine-linked 2 <= T <= 8 kernels (one router
+ * launch, then four launches per layer, when the layers' workspaces are
+ * distinct), 0 = one gm_moe_forward per layer, negative = a rejected layer
+ * (GM_E*).  No counterpart in the reference (its decoder loop
  * runs one block at a time); for callers and tests that must know the fast
  * path is the one that runs.
  */

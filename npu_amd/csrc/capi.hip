@@ -236,14 +236,39 @@ static bool chain_layer_fused(const gm_moe_layer* layers, int l, int T) {
          (l == 0 || L->router_t != nullptr);
 }
 
+// Whether layers l and l + 1 of a T-token chain (2 <= T <= 8, decode path)
+// can be linked through layer l's combine kernel, which then writes layer
+// l + 1's router inputs (partials over 256-column slices, sums of x^2, limb
+// rows) into layer l + 1's workspace: both take the decode path, D splits
+// into at most 16 slices, layer l + 1 has router_t and its workspace holds the
+// inputs.  gm_moe_chain also needs the two workspaces not to overlap (the
+// combine reads layer l's partial rows while it writes layer l + 1's inputs).
+static bool chain_pair_linkable(const gm_moe_layer* layers, int l, int T) {
+  const gm_moe_layer* A = layers + l;
+  const gm_moe_layer* B = layers + l + 1;
+  auto decode = [&](const gm_moe_layer* L) {
+    return T >= 2 && T <= GM_DECODE_MAX_T && T * L->k <= GM_GRP_MAXU && L->D % 256 == 0 && L->FF % 256 == 0 &&
+           L->D <= 4096 && L->FF <= 2048 && L->k <= 8;
+  };
+  if (!decode(A) || !decode(B) || A->D % GM_DEC_LINK_KR || gm_dec_link_nz(A->D) > GM_DEC_MAX_NZ) return false;
+  return B->router_t != nullptr && B->D == A->D && gm_dec_part_fits(B, T, gm_dec_link_nz(B->D));
+}
+
+static bool ws_disjoint(const void* a, size_t na, const void* b, size_t nb) {
+  const uint8_t* pa = static_cast<const uint8_t*>(a);
+  const uint8_t* pb = static_cast<const uint8_t*>(b);
+  return pa + na <= pb || pb + nb <= pa;
+}
+
 int gm_moe_chain_fused(const gm_moe_layer* layers, int n_layers, int T) {
   if (!layers || n_layers < 1 || T < 0) return gm_fail_arg("gm_moe_chain_fused: bad arguments");
-  bool fused = true;
+  bool fused = true, linked = n_layers > 1;
   for (int l = 0; l < n_layers; ++l) {
     if (int rc = check_layer(layers + l)) return rc;
     fused = fused && chain_layer_fused(layers, l, T);
+    if (l + 1 < n_layers) linked = linked && chain_pair_linkable(layers, l, T);
   }
-  return fused ? 1 : 0;
+  return fused ? 1 : linked ? 2 : 0;
 }
 
 int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float* y, float* buf, int T, int flags,
@@ -273,13 +298,35 @@ int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float
   if (T == 0) return GM_OK;
   hipStream_t s = as_stream(stream);
   const float* in = x;
+  bool linked_in = false;                                   // layer l's router inputs come from layer l - 1
   for (int l = 0; l < n_layers; ++l) {
     const gm_moe_layer* L = layers + l;
     float* out = (n_layers - 1 - l) % 2 == 0 ? y : buf;
     uint8_t* w = static_cast<uint8_t*>(ws[l]);
     const GmMoeWs lay = gm_moe_ws_layout(L, T);
-    if (!fused) {
+    const bool linked_out = !fused && l + 1 < n_layers && chain_pair_linkable(layers, l, T) &&
+                            ws_disjoint(ws[l], ws_bytes[l], ws[l + 1], ws_bytes[l + 1]);
+    if (!fused && (linked_in || linked_out)) {
+      GmNextB8 nx8{};
+      GmChainStep cs{nullptr, nullptr, nullptr, !linked_in, nullptr};
+      if (linked_out) {
+        const gm_moe_layer* N = layers + l + 1;
+        float* rms;
+        if (!gm_dec_part_ptrs(N, T, gm_dec_link_nz(N->D), static_cast<uint8_t*>(ws[l + 1]), gm_moe_ws_layout(N, T),
+                              &nx8.part, &nx8.ssq, &rms, &nx8.xl))
+          return gm_fail_arg("gm_moe_chain: internal workspace layout error (linked)");
+        nx8.w = N->router_t;
+        nx8.nw = N->norm_w;
+        nx8.E = N->E;
+        nx8.ldp = gm_dec_part_ld(N);
+        nx8.f32 = N->q_router == GM_QTYPE_F32 ? 1 : 0;
+        cs.next8 = &nx8;
+      }
+      if (int rc = gm_dec_run(L, in, out, T, flags, w, lay, s, 0, &cs)) return rc;
+      linked_in = linked_out;
+    } else if (!fused) {
       if (int rc = moe_forward_impl(L, in, out, T, flags, w, ws_bytes[l], 0, kPathAuto, stream)) return rc;
+      linked_in = false;
     } else {
       auto acc_of = [&](int j) {
         const GmMoeWs lj = gm_moe_ws_layout(layers + j, T);
@@ -287,7 +334,7 @@ int gm_moe_chain(const gm_moe_layer* layers, int n_layers, const float* x, float
                (size_t)(j % 2) * gm_acc_bytes(layers[j].E) / sizeof(double);
       };
       GmNextRouter nx{};
-      GmChainStep cs{acc_of(l), nullptr, nullptr, l == 0};
+      GmChainStep cs{acc_of(l), nullptr, nullptr, l == 0, nullptr};
       if (l + 1 < n_layers) {
         const gm_moe_layer* N = layers + l + 1;
         nx.w = N->router_t;

@@ -79,16 +79,20 @@ __host__ __device__ inline int gm_acc_pos(int e, int E) {
 }
 inline size_t gm_acc_bytes(int E) { return (size_t)GM_ACC_COPIES * gm_acc_ld(E) * sizeof(double); }
 
-// One layer of gm_moe_chain's T = 1 accumulator path: the router accumulators
-// the gate/up kernel reads (acc), those it clears for the next layer (acc_zero,
-// or NULL), the next layer for the down kernel (or NULL), and whether the
-// router kernel runs first (the chain's first layer).
+// One layer of a linked gm_moe_chain.  T = 1 (accumulator path): the router
+// accumulators the gate/up kernel reads (acc), those it clears for the next
+// layer (acc_zero, or NULL) and the next layer for the down kernel (next, or
+// NULL).  T > 1: the next layer's router inputs for the combine kernel (next8,
+// or NULL).  Either way, whether the router kernel runs first (the chain's
+// first layer; the others find their router inputs in their workspace).
 struct GmNextRouter;
+struct GmNextB8;
 struct GmChainStep {
   double* acc;
   double* acc_zero;
   const GmNextRouter* next;
   bool router;
+  const GmNextB8* next8;
 };
 bool gm_dec_chain_ok(const gm_moe_layer* P);
 

@@ -13,8 +13,10 @@ struct GmDecArgs {
   float* h;         // [T * k][FF], directly followed by hsh
   float* hsh;       // [T][FF]
   float* yp;        // [T * k + T][D] per-pair / shared partial outputs (general path)
-  float* part;      // [gm_dec_nz(D)][T][gm_dec_part_ld] router partials (general path, inside yp)
-  float* ssq;       // [gm_dec_nz(D)][T] partial sums of x^2 (general path, inside yp)
+  float* part;      // [nz][T][gm_dec_part_ld] router partials (general path, inside yp)
+  float* ssq;       // [nz][T] partial sums of x^2 (general path, inside yp)
+  int nz;           // router partial ranges: gm_dec_nz(D), or gm_dec_link_nz(D) when the previous
+                    // layer's combine kernel wrote them
   float* rms;       // [T] RMSNorm factors (general path, inside yp)
   uint8_t* xl;      // [T + 1] limb rows of x w_norm (general path, inside yp)
   uint64_t* tl;     // per-block timestamps (profiling build)
@@ -49,6 +51,19 @@ struct GmNextRouter {
   int E, ld, f32;
 };
 
+// The next layer's router inputs, for the T > 1 combine kernel of a chain
+// (k_dec_combine_nx): the router partials of 256-column slices, the slices'
+// sums of x^2 and the limb rows, written into the next layer's workspace where
+// its routing and gate/up kernels read them (gm_dec_part_ptrs).
+struct GmNextB8 {
+  const void* w;     // gm_moe_layer.router_t of the next layer: [D/8][E+1][8], bf16 bits or fp32 (f32 != 0)
+  const float* nw;   // [D] RMSNorm weight, or NULL
+  float* part;       // [D / 256][T][ldp]
+  float* ssq;        // [D / 256][T]
+  uint8_t* xl;       // [T + 1] limb rows (row T: spare)
+  int E, ldp, f32;
+};
+
 // gm_dec_chain_ok (kernels.h): the T = 1 layers that run on the accumulator
 // kernels (router, k_dec_gateup1w, k_dec_down1), which a chain links by the
 // down kernel feeding the next layer's accumulators.
@@ -62,6 +77,19 @@ inline int gm_dec_kr(int D) { return D % 512 == 0 ? 512 : 256; }
 inline int gm_dec_nz(int D) { return D / gm_dec_kr(D); }
 constexpr int GM_DEC_MAX_NZ = 16;
 
+// Partials of a T > 1 chain's combine kernel: 256-column slices.
+constexpr int GM_DEC_LINK_KR = 256;
+inline int gm_dec_link_nz(int D) { return D / GM_DEC_LINK_KR; }
+
+// Where the T > 1 router inputs sit in a layer's workspace (inside yp, which
+// the down stage overwrites only after the gate/up stage has read them): nz
+// partial ranges of [T][ldp], then GM_DEC_MAX_NZ x T sums of x^2, T RMSNorm
+// factors (16 words), T + 1 limb rows.  Returns false when they do not fit.
+bool gm_dec_part_ptrs(const gm_moe_layer* P, int T, int nz, uint8_t* ws, const GmMoeWs& lay, float** part,
+                      float** ssq, float** rms, uint8_t** xl);
+// Whether those inputs fit a T-token workspace of P with nz ranges.
+bool gm_dec_part_fits(const gm_moe_layer* P, int T, int nz);
+
 // Weight-row chunk sizes: D and FF in units of 1024 and 512 elements.
 inline int gm_dec_dc(int D) { return D <= 1024 ? 1 : D <= 2048 ? 2 : 4; }
 inline int gm_dec_fc(int FF) { return FF <= 512 ? 1 : FF <= 1024 ? 2 : 4; }
@@ -71,5 +99,6 @@ inline int gm_dec_fc(int FF) { return FF <= 512 ? 1 : FF <= 1024 ? 2 : 4; }
 // grouped gate/up kernel.
 int gm_dec_gateup(const gm_moe_layer* P, const float* x, int T, bool fast1, const GmDecArgs& a, hipStream_t s);
 // Stage 3: down projections and the weighted combine (+ shared expert, + x).
+// With next8 (T > 1 chains) the combine also writes the next layer's router inputs.
 int gm_dec_down(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
-                hipStream_t s, const GmNextRouter* next = nullptr);
+                hipStream_t s, const GmNextRouter* next = nullptr, const GmNextB8* next8 = nullptr);

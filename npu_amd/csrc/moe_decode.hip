@@ -273,12 +273,12 @@ int gm_dec_run(const gm_moe_layer* P, const float* x, float* y, int T, int flags
   a.yp = reinterpret_cast<float*>(ws + lay.yp);
   a.tl = reinterpret_cast<uint64_t*>(ws + lay.tl);
   // general path: router partials, x^2 partials, RMSNorm factors and the limb
-  // rows of x w_norm live in yp, which stage 3 overwrites only after stage 2
-  a.part = a.yp;
-  a.ssq = a.part + (size_t)gm_dec_nz(P->D) * T * gm_dec_part_ld(P);
-  a.rms = a.ssq + GM_DEC_MAX_NZ * T;
-  a.xl = reinterpret_cast<uint8_t*>(a.rms + 16);
-  if (a.xl + (size_t)(T + 1) * gm_limb_row_bytes(P->D) > reinterpret_cast<uint8_t*>(a.yp + (size_t)(T * P->k + T) * P->D))
+  // rows of x w_norm live in yp, which stage 3 overwrites only after stage 2;
+  // in a T > 1 chain the previous layer's combine kernel wrote them (256-column
+  // ranges) unless this is the chain's first layer
+  const bool linked_in = cs != nullptr && T > 1 && !cs->router;
+  a.nz = linked_in ? gm_dec_link_nz(P->D) : gm_dec_nz(P->D);
+  if (!gm_dec_part_ptrs(P, T, a.nz, ws, lay, &a.part, &a.ssq, &a.rms, &a.xl))
     return gm_fail_arg("gm_moe_forward: internal workspace layout error (yp)");
   if (a.hsh != a.h + (size_t)T * P->k * P->FF) return gm_fail_arg("gm_moe_forward: internal workspace layout error");
   // The T = 1 down kernel stages (k + 1) rows of FF activations per block and
@@ -291,8 +291,13 @@ int gm_dec_run(const gm_moe_layer* P, const float* x, float* y, int T, int flags
   a.acc = nullptr;
   a.acc_zero = nullptr;
   const GmNextRouter* next = nullptr;
+  const GmNextB8* next8 = nullptr;
   bool run_router = stage == 0 || stage == 1;
-  if (cs != nullptr) {
+  if (cs != nullptr && T > 1) {
+    if (stage != 0 || (a.nz > GM_DEC_MAX_NZ)) return gm_fail_arg("gm_moe_chain: internal error (linked step)");
+    next8 = cs->next8;
+    run_router = cs->router;
+  } else if (cs != nullptr) {
     if (!(fast1 && gm_dec_chain_ok(P)) || stage != 0) return gm_fail_arg("gm_moe_chain: internal error (chain step)");
     a.acc = cs->acc;
     a.acc_zero = cs->acc_zero;
@@ -306,6 +311,21 @@ int gm_dec_run(const gm_moe_layer* P, const float* x, float* y, int T, int flags
   if (stage == 0 || stage == 2)
     if (int rc = gm_dec_gateup(P, x, T, fast1, a, s)) return rc;
   if (stage == 0 || stage == 3)
-    if (int rc = gm_dec_down(P, x, y, T, flags, fast1, a, s, next)) return rc;
+    if (int rc = gm_dec_down(P, x, y, T, flags, fast1, a, s, next, next8)) return rc;
   return GM_OK;
+}
+
+bool gm_dec_part_fits(const gm_moe_layer* P, int T, int nz) {
+  const size_t words = (size_t)nz * T * gm_dec_part_ld(P) + (size_t)GM_DEC_MAX_NZ * T + 16;
+  return words * sizeof(float) + (size_t)(T + 1) * gm_limb_row_bytes(P->D) <= (size_t)(T * P->k + T) * P->D * sizeof(float);
+}
+
+bool gm_dec_part_ptrs(const gm_moe_layer* P, int T, int nz, uint8_t* ws, const GmMoeWs& lay, float** part,
+                      float** ssq, float** rms, uint8_t** xl) {
+  float* yp = reinterpret_cast<float*>(ws + lay.yp);
+  *part = yp;
+  *ssq = *part + (size_t)nz * T * gm_dec_part_ld(P);
+  *rms = *ssq + GM_DEC_MAX_NZ * T;
+  *xl = reinterpret_cast<uint8_t*>(*rms + 16);
+  return gm_dec_part_fits(P, T, nz);
 }

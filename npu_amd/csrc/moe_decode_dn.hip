@@ -446,9 +446,153 @@ __global__ void __launch_bounds__(256) k_dec_combine(const float* __restrict__ x
   GM_TL_END(3);
 }
 
+// T > 1 chain: the combine of k_dec_combine over the 256-column slice c =
+// blockIdx.x for every token, plus the next layer's router inputs over that
+// slice for its router rows 16 blockIdx.y .. +15 (row E: the shared gate
+// vector), so that the next layer starts with its routing kernel:
+//   part[c][t][r] = sum_{d in slice} (y[t][d] w_norm[d]) Wn[r][d]
+// and, from the blocks with blockIdx.y == 0, y itself, ssq[c][t] =
+// sum_{d in slice} y[t][d]^2 and the limb rows of y w_norm over the slice (the
+// outputs k_dec_router_ks has for its K ranges).  Combine: thread 64 t + q
+// holds columns 4q .. 4q+3 of token t; the slots are added in ascending
+// expert id, in the order and with the roundings of k_dec_combine (the lanes
+// rank their token's slots, every slot value goes to LDS, and each lane reads
+// them back in rank order).  Router: the block's rows come from router_t (8
+// columns of E + 1 rows per 16-byte group, so the block's 16 rows of a group
+// are one contiguous 256-byte run), loaded behind the combine's loads and
+// staged in LDS; thread 64 t + 16 h + r then forms row r's dot product for
+// token t over the quarter h of the slice in four interleaved partial sums,
+// and the quarters are added across lanes (h = 0 + 1, 2 + 3, then both).
+constexpr int kNxRows = 16;                                      // router rows per block
+
+template <bool RF32>
+__global__ void __launch_bounds__(512) k_dec_combine_nx(const float* __restrict__ x, int T, int k, int D, int flags,
+                                                        const int32_t* __restrict__ g_ids,
+                                                        const float* __restrict__ g_wts,
+                                                        const float* __restrict__ shg, int has_sh,
+                                                        const float* __restrict__ yp, float* __restrict__ y,
+                                                        GmNextB8 nx GM_TL_PARAM) {
+  GM_TL_BEGIN();
+  constexpr int NG = GM_DEC_LINK_KR / 8;                         // 8-column groups of the slice
+  constexpr int CW = RF32 ? 2 : 1;                               // 16-byte chunks per group row
+  constexpr int NRC = (NG * kNxRows * CW + 511) / 512;           // router chunks per thread
+  __shared__ gm_f32x4 vbuf[8][8][64];                            // [token][slot][column quad]
+  __shared__ gm_f32x4 ys[8][64];                                 // y w_norm of the slice
+  __shared__ gm_u32x4 rsl[NRC * 512];                            // router rows [group][row][chunk]
+  __shared__ int pslot[8][8];
+  __shared__ float pw[8][8];
+  const int tid = threadIdx.x, t = tid >> 6, q = tid & 63;
+  const int tc = t < T ? t : T - 1;
+  const int c = blockIdx.x, d = GM_DEC_LINK_KR * c + 4 * q;
+  int id[8];
+  float w[8];
+  gm_f32x4 v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int jj = j < k ? j : k - 1;
+    id[j] = g_ids[tc * k + jj];
+    w[j] = g_wts[tc * k + jj];
+    v[j] = *reinterpret_cast<const gm_f32x4*>(yp + (int64_t)(tc * k + jj) * D + d);
+  }
+  const gm_f32x4 zero4 = {0.f, 0.f, 0.f, 0.f}, one4 = {1.f, 1.f, 1.f, 1.f};
+  const gm_f32x4 vs = has_sh ? *reinterpret_cast<const gm_f32x4*>(yp + (int64_t)(T * k + tc) * D + d) : zero4;
+  const gm_f32x4 xr = (flags & GM_MOE_RESIDUAL) ? *reinterpret_cast<const gm_f32x4*>(x + (int64_t)tc * D + d) : zero4;
+  const gm_f32x4 nw4 = nx.nw ? *reinterpret_cast<const gm_f32x4*>(nx.nw + d) : one4;
+  const float gs = has_sh ? shg[tc] : 0.f;
+  // the block's router rows (rows past E: row E again, never stored)
+  const int es = RF32 ? 4 : 2;
+  const int64_t gstride = (int64_t)(nx.E + 1) * 8 * es;           // bytes per 8-column group
+  const uint8_t* rbase = static_cast<const uint8_t*>(nx.w) + (int64_t)(NG * c) * gstride;
+  gm_u32x4 rc[NRC];
+#pragma unroll
+  for (int i = 0; i < NRC; ++i) {
+    const int ch0 = tid + 512 * i, ch = ch0 < NG * kNxRows * CW ? ch0 : 0;
+    const int g = ch / (kNxRows * CW), rr = (ch / CW) % kNxRows, h = ch % CW;
+    const int R = kNxRows * (int)blockIdx.y + rr;
+    rc[i] = gm_ld<true>(reinterpret_cast<const gm_u32x4*>(rbase + g * gstride + (int64_t)(R <= nx.E ? R : nx.E) * 8 * es) + h);
+  }
+  issue_fence();
+  // rank of slot q % 8 among the token's slots (ascending id; slots past k after
+  // every real one, in slot order)
+  int key[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) key[j] = j < k ? id[j] : 0x7ffffff0 + j;
+  const int j0 = q & 7;
+  int mk = key[0];
+  float mw = w[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) {
+    mk = j0 == j ? key[j] : mk;
+    mw = j0 == j ? w[j] : mw;
+  }
+  int rank = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rank += key[j] < mk ? 1 : 0;
+  if (q < 8) {
+    pslot[t][rank] = j0;
+    pw[t][rank] = mw;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) vbuf[t][j][q] = v[j];
+  __syncthreads();
+  GM_TL_MARK1(vbuf[t][0][q].x);
+  gm_f32x4 acc = zero4;
+  for (int i = 0; i < k; ++i) {
+    const float wi = pw[t][i];
+    const gm_f32x4 vi = vbuf[t][pslot[t][i]][q];
+    acc.x = fmaf(wi, vi.x, acc.x);
+    acc.y = fmaf(wi, vi.y, acc.y);
+    acc.z = fmaf(wi, vi.z, acc.z);
+    acc.w = fmaf(wi, vi.w, acc.w);
+  }
+  if (has_sh) {
+    acc.x = fmaf(gs, vs.x, acc.x);
+    acc.y = fmaf(gs, vs.y, acc.y);
+    acc.z = fmaf(gs, vs.z, acc.z);
+    acc.w = fmaf(gs, vs.w, acc.w);
+  }
+  if (flags & GM_MOE_RESIDUAL) acc = xr + acc;
+  const gm_f32x4 yn = {acc.x * nw4.x, acc.y * nw4.y, acc.z * nw4.z, acc.w * nw4.w};
+  ys[t][q] = yn;
+  if (blockIdx.y == 0) {                                         // uniform per block
+    if (t < T) *reinterpret_cast<gm_f32x4*>(y + (int64_t)t * D + d) = acc;
+    const float s2 = gm_wave_sum64(fmaf(acc.x, acc.x, fmaf(acc.y, acc.y, fmaf(acc.z, acc.z, acc.w * acc.w))));
+    if (q == 0 && t < T) nx.ssq[c * T + t] = s2;
+    // the 8 lanes of a sub-block are lanes 8j .. 8j+7; tokens past T: spare row T
+    gm_put_limbs4(yn, d >> 2, nx.xl + (int64_t)(t < T ? t : T) * gm_limb_row_bytes(D));
+  }
+#pragma unroll
+  for (int i = 0; i < NRC; ++i)
+    if (tid + 512 * i < NG * kNxRows * CW) rsl[tid + 512 * i] = rc[i];
+  __syncthreads();
+  GM_TL_MARK2(ys[0][q].x);
+  const int r = q & 15, hq = q >> 4;                             // row, quarter of the slice
+  float da[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int gi = 0; gi < NG / 4; ++gi) {
+    const int g = (NG / 4) * hq + gi;
+    RouterChunk<RF32> wc;
+#pragma unroll
+    for (int h = 0; h < CW; ++h) wc[h] = rsl[(g * kNxRows + r) * CW + h];
+    float wv[8];
+    router_unpack8<RF32>(wc, wv);
+    const gm_f32x4 a0 = ys[t][2 * g], b0 = ys[t][2 * g + 1];
+    const float xv[8] = {a0.x, a0.y, a0.z, a0.w, b0.x, b0.y, b0.z, b0.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) da[gi & 3] = fmaf(xv[i], wv[i], da[gi & 3]);
+  }
+  float dsum = (da[0] + da[1]) + (da[2] + da[3]);
+  dsum += __shfl_xor(dsum, 16, 64);
+  dsum += __shfl_xor(dsum, 32, 64);
+  GM_TL_MARK3(dsum);
+  const int R = kNxRows * (int)blockIdx.y + r;
+  if (hq == 0 && R <= nx.E && t < T) nx.part[((int64_t)c * T + t) * nx.ldp + R] = dsum;
+  GM_TL_END(3);
+}
+
 template <int QTD, int QTS, int FC>
 int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
-              hipStream_t s, const GmNextRouter* next) {
+              hipStream_t s, const GmNextRouter* next, const GmNextB8* next8) {
   const int D = P->D, FF = P->FF, k = P->k;
   if (fast1) {
     if constexpr (FC <= (QTD == GM_QTYPE_BF16 || QTD == GM_QTYPE_I8 ? 1 : 2)) {   // bf16 / I8 rows: 8 / 6 KB per slice
@@ -477,31 +621,41 @@ int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags,
   hipLaunchKernelGGL((k_dec_down8<QTD, QTS, FC>), dim3(n_sh + max_u * n_tg), dim3(256), smem, s, *P, T, a.grp, a.h,
                      a.yp, n_sh, n_tg GM_TL_ARG(a.tl));
   GM_TRY(hipGetLastError());
-  hipLaunchKernelGGL(k_dec_combine, dim3((D + 255) / 256, T), dim3(256), 0, s, x, T, k, D, flags, a.ids, a.wts,
-                     a.shg, P->down_sh ? 1 : 0, a.yp, y GM_TL_ARG(a.tl));
+  if (next8 != nullptr) {
+    const dim3 grid((unsigned)(D / GM_DEC_LINK_KR), (unsigned)((next8->E + kNxRows) / kNxRows));
+    if (next8->f32)
+      hipLaunchKernelGGL(k_dec_combine_nx<true>, grid, dim3(512), 0, s, x, T, k, D, flags, a.ids, a.wts, a.shg,
+                         P->down_sh ? 1 : 0, a.yp, y, *next8 GM_TL_ARG(a.tl));
+    else
+      hipLaunchKernelGGL(k_dec_combine_nx<false>, grid, dim3(512), 0, s, x, T, k, D, flags, a.ids, a.wts, a.shg,
+                         P->down_sh ? 1 : 0, a.yp, y, *next8 GM_TL_ARG(a.tl));
+  } else {
+    hipLaunchKernelGGL(k_dec_combine, dim3((D + 255) / 256, T), dim3(256), 0, s, x, T, k, D, flags, a.ids, a.wts,
+                       a.shg, P->down_sh ? 1 : 0, a.yp, y GM_TL_ARG(a.tl));
+  }
   GM_TRY(hipGetLastError());
   return GM_OK;
 }
 
 template <int QTD, int QTS>
 int launch_dn_f(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
-                hipStream_t s, const GmNextRouter* next) {
+                hipStream_t s, const GmNextRouter* next, const GmNextB8* next8) {
   switch (gm_dec_fc(P->FF)) {
-    case 1: return launch_dn<QTD, QTS, 1>(P, x, y, T, flags, fast1, a, s, next);
-    case 2: return launch_dn<QTD, QTS, 2>(P, x, y, T, flags, fast1, a, s, next);
-    default: return launch_dn<QTD, QTS, 4>(P, x, y, T, flags, fast1, a, s, next);
+    case 1: return launch_dn<QTD, QTS, 1>(P, x, y, T, flags, fast1, a, s, next, next8);
+    case 2: return launch_dn<QTD, QTS, 2>(P, x, y, T, flags, fast1, a, s, next, next8);
+    default: return launch_dn<QTD, QTS, 4>(P, x, y, T, flags, fast1, a, s, next, next8);
   }
 }
 
 template <int QTD>
 int launch_dn_s(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
-                hipStream_t s, const GmNextRouter* next) {
-  if (!P->down_sh) return launch_dn_f<QTD, QTD>(P, x, y, T, flags, fast1, a, s, next);
+                hipStream_t s, const GmNextRouter* next, const GmNextB8* next8) {
+  if (!P->down_sh) return launch_dn_f<QTD, QTD>(P, x, y, T, flags, fast1, a, s, next, next8);
   switch (P->q_down_sh) {
-    case GM_QTYPE_IQ4_XS: return launch_dn_f<QTD, GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s, next);
-    case GM_QTYPE_IQ3_XXS: return launch_dn_f<QTD, GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s, next);
-    case GM_QTYPE_BF16: return launch_dn_f<QTD, GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s, next);
-    case GM_QTYPE_I8: return launch_dn_f<QTD, GM_QTYPE_I8>(P, x, y, T, flags, fast1, a, s, next);
+    case GM_QTYPE_IQ4_XS: return launch_dn_f<QTD, GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s, next, next8);
+    case GM_QTYPE_IQ3_XXS: return launch_dn_f<QTD, GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s, next, next8);
+    case GM_QTYPE_BF16: return launch_dn_f<QTD, GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s, next, next8);
+    case GM_QTYPE_I8: return launch_dn_f<QTD, GM_QTYPE_I8>(P, x, y, T, flags, fast1, a, s, next, next8);
     default: return gm_fail_arg("gm_moe_forward: shared down format %d unsupported", P->q_down_sh);
   }
 }
@@ -509,13 +663,15 @@ int launch_dn_s(const gm_moe_layer* P, const float* x, float* y, int T, int flag
 }  // namespace
 
 int gm_dec_down(const gm_moe_layer* P, const float* x, float* y, int T, int flags, bool fast1, const GmDecArgs& a,
-                hipStream_t s, const GmNextRouter* next) {
+                hipStream_t s, const GmNextRouter* next, const GmNextB8* next8) {
   if (next != nullptr && !(fast1 && T == 1)) return gm_fail_arg("gm_moe_chain: internal error (next router off T = 1)");
+  if (next8 != nullptr && (fast1 || P->D % GM_DEC_LINK_KR || gm_dec_link_nz(P->D) > GM_DEC_MAX_NZ))
+    return gm_fail_arg("gm_moe_chain: internal error (linked combine)");
   switch (P->q_down) {
-    case GM_QTYPE_IQ4_XS: return launch_dn_s<GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s, next);
-    case GM_QTYPE_IQ3_XXS: return launch_dn_s<GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s, next);
-    case GM_QTYPE_BF16: return launch_dn_s<GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s, next);
-    case GM_QTYPE_I8: return launch_dn_s<GM_QTYPE_I8>(P, x, y, T, flags, fast1, a, s, next);
+    case GM_QTYPE_IQ4_XS: return launch_dn_s<GM_QTYPE_IQ4_XS>(P, x, y, T, flags, fast1, a, s, next, next8);
+    case GM_QTYPE_IQ3_XXS: return launch_dn_s<GM_QTYPE_IQ3_XXS>(P, x, y, T, flags, fast1, a, s, next, next8);
+    case GM_QTYPE_BF16: return launch_dn_s<GM_QTYPE_BF16>(P, x, y, T, flags, fast1, a, s, next, next8);
+    case GM_QTYPE_I8: return launch_dn_s<GM_QTYPE_I8>(P, x, y, T, flags, fast1, a, s, next, next8);
     default: return gm_fail_arg("gm_moe_forward: routed down format %d unsupported", P->q_down);
   }
 }

@@ -549,7 +549,7 @@ int launch_gu(const gm_moe_layer* P, const float* x, int T, bool fast1, const Gm
     GM_TRY(hipGetLastError());
     return GM_OK;
   }
-  const int nz = gm_dec_nz(P->D);                                  // <= GM_DEC_MAX_NZ for D <= 4096
+  const int nz = a.nz;                                             // <= GM_DEC_MAX_NZ (checked below)
   if (nz > GM_DEC_MAX_NZ) return gm_fail_arg("gm_moe_forward: D=%d needs more than %d router ranges", P->D, GM_DEC_MAX_NZ);
   auto route = nz <= 8 ? (P->E <= 256 ? k_dec_route<4, 8> : k_dec_route<8, 8>)
                        : (P->E <= 256 ? k_dec_route<4, 16> : k_dec_route<8, 16>);

@@ -250,9 +250,15 @@ class GpuMoeChain:
         self._buf: torch.Tensor | None = None
 
     def fused(self, T: int) -> bool:
-        """True when a T-token call runs on the accumulator-linked kernels (T = 1 and every
-        layer fits them), False when it runs one gm_moe_forward per layer."""
+        """True when a T-token call links consecutive layers: at T = 1 the accumulator-linked
+        kernels, at 2 <= T <= 8 each layer's combine kernel forming the next layer's router
+        inputs (the blocks' workspaces are distinct); False when it runs one gm_moe_forward
+        per layer."""
         return ops.moe_chain_fused([b.struct for b in self.blocks], T)
+
+    def mode(self, T: int) -> int:
+        """gm_moe_chain_fused's answer: 1 (T = 1 linked), 2 (T > 1 linked) or 0."""
+        return ops.moe_chain_mode([b.struct for b in self.blocks], T)
 
     def __call__(self, x: torch.Tensor, *, residual: bool = True, out: torch.Tensor | None = None) -> torch.Tensor:
         if x.dim() != 2 or x.shape[1] != self.D:

@@ -171,13 +171,20 @@ def moe_chain_raw(layers, x: torch.Tensor, y: torch.Tensor, buf: torch.Tensor | 
 
 
 
-def moe_chain_fused(layers, T: int) -> bool:
-    """Whether gm_moe_chain runs ``layers`` at ``T`` tokens on the accumulator-linked T = 1
-    kernels (one router launch, then two launches per layer) rather than one
-    gm_moe_forward per layer."""
+def moe_chain_mode(layers, T: int) -> int:
+    """gm_moe_chain's path for ``layers`` at ``T`` tokens: 1 = the accumulator-linked T = 1
+    kernels (one router launch, then two launches per layer), 2 = the combine-linked T > 1
+    kernels (one router launch, then four launches per layer; needs distinct workspaces per
+    layer), 0 = one gm_moe_forward per layer."""
     n = len(layers)
     arr = (L.GmMoeLayer * n)(*layers)
     rc = L.lib().gm_moe_chain_fused(arr, n, T)
     if rc < 0:
         L.check(rc, "gm_moe_chain_fused")
-    return rc == 1
+    return int(rc)
+
+
+def moe_chain_fused(layers, T: int) -> bool:
+    """Whether gm_moe_chain links consecutive layers at ``T`` tokens (mode 1 or 2 above)
+    rather than running one gm_moe_forward per layer."""
+    return moe_chain_mode(layers, T) > 0

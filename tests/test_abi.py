@@ -101,15 +101,25 @@ def test_workspace_sizing_and_layer_validation():
 
 
 def test_chain_path_query_without_gpu():
-    """gm_moe_chain_fused reports the accumulator-linked path only at T = 1 with every layer
-    after the first carrying router_t; a rejected layer gives its GM_E* code."""
+    """gm_moe_chain_fused reports the accumulator-linked path (1) only at T = 1 and the
+    combine-linked path (2) only at 2 <= T <= 8, decode shapes with D a multiple of 256 up to
+    4096, both with every layer after the first carrying router_t; a rejected layer gives
+    its GM_E* code."""
     lib = L.lib()
     a, b = _layer(router_t=512), _layer(router_t=512)
     arr = (L.GmMoeLayer * 2)(a, b)
     assert lib.gm_moe_chain_fused(arr, 2, 1) == 1
-    assert lib.gm_moe_chain_fused(arr, 2, 8) == 0
+    assert lib.gm_moe_chain_fused(arr, 2, 2) == 2
+    assert lib.gm_moe_chain_fused(arr, 2, 8) == 2
+    assert lib.gm_moe_chain_fused(arr, 2, 9) == 0          # past the decode path
+    assert lib.gm_moe_chain_fused((L.GmMoeLayer * 1)(a), 1, 8) == 0
+    arr = (L.GmMoeLayer * 2)(_layer(router_t=512, D=4096), _layer(router_t=512, D=4096))
+    assert lib.gm_moe_chain_fused(arr, 2, 8) == 2          # 16 slices of 256 columns
+    arr = (L.GmMoeLayer * 2)(_layer(router_t=512, D=2048), _layer(router_t=512, D=4096))
+    assert lib.gm_moe_chain_fused(arr, 2, 8) == 0          # layers must share D
     arr = (L.GmMoeLayer * 2)(a, _layer())          # layer 1 without router_t: per-layer path
     assert lib.gm_moe_chain_fused(arr, 2, 1) == 0
+    assert lib.gm_moe_chain_fused(arr, 2, 8) == 0
     arr = (L.GmMoeLayer * 2)(a, _layer(router_t=512, E=128))   # layers must share E
     assert lib.gm_moe_chain_fused(arr, 2, 1) == 0
     arr = (L.GmMoeLayer * 2)(a, _layer(k=9))

@@ -119,7 +119,7 @@ def test_gm_moe_chain(gpu, variant_chain, T):
         x0 = x0 * 0.01           # without RMSNorm the block amplifies ~x^2: keeps layer 1's logits spread ~10
     ids_ref, y_ref = _oracle_chain(hosts, x0, hosts[0].k)
     ch = GpuMoeChain(blocks)
-    assert ch.fused(T) == (T == 1), f"{name}: the chain took the {'per-layer' if T == 1 else 'fused'} path"
+    assert ch.mode(T) == (1 if T == 1 else 2), f"{name}: the chain took path {ch.mode(T)}"
     xd = x0.to(gpu)
     y_eager = ch(xd, residual=True)
     torch.cuda.synchronize()
@@ -187,3 +187,28 @@ def test_config5_headline_chain_40_layers(gpu):
     assert rel <= 1e-3, f"chain vs oracle rel {rel:.3e}"
     del layers, hosts
     torch.cuda.empty_cache()
+
+
+def test_gm_moe_chain_shared_workspace_t8(gpu, chain):
+    """gm_moe_chain allows one workspace for every layer.  At T = 8 the layers then cannot
+    be linked (a combine kernel would write the next layer's router inputs over the partial
+    rows it reads), so each layer runs as gm_moe_forward: the output equals the per-layer
+    calls bit for bit, and the linked chain (distinct workspaces) to fp32 rounding."""
+    from npu_amd import ops
+    hosts, blocks = chain
+    T, n = 8, len(blocks)
+    print(f"gm_moe_chain case shared workspace T={T} layers={n}", flush=True)
+    xd = torch.from_numpy(synth.host_input(610, T, hosts[0].D, rmsnorm=False)).to(gpu)
+    ws = torch.zeros(ops.moe_workspace_bytes(blocks[0].struct, T), dtype=torch.uint8, device=gpu)
+    y, buf = torch.empty_like(xd), torch.empty_like(xd)
+    ops.moe_chain_raw([b.struct for b in blocks], xd, y, buf, [ws] * n, residual=True)
+    bufs = [xd.clone(), torch.empty_like(xd)]
+    for i, blk in enumerate(blocks):
+        blk(bufs[i % 2], residual=True, out=bufs[(i + 1) % 2])
+    ch = GpuMoeChain(blocks)
+    assert ch.mode(T) == 2
+    y_linked = ch(xd, residual=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y, bufs[n % 2]), "shared-workspace chain differs from the per-layer calls"
+    rel = OM.rel_err(y_linked.cpu(), y.cpu())
+    assert rel <= 1e-5, f"linked chain vs per-layer rel {rel:.3e}"

@@ -57,6 +57,9 @@ def _ref_matvec(w_raw, qtype, M, K, x):
     (QT.IQ4_XS, 70, 1024),     # one-token kernel: every lanes-per-row / sub-blocks-per-lane branch
     (QT.IQ3_XXS, 9, 8192),
     (QT.IQ4_XS, 3, 12288),     # one token past the one-token kernel's K limit
+    (QT.IQ3_XXS, 21, 1536),    # one-token kernel: lanes 48..63 of each row past the last sub-block
+    (QT.IQ4_XS, 50, 3072),     # one-token kernel: second sub-block per lane live on half the lanes
+    (QT.IQ4_XS, 26, 768),      # 32 lanes per row, 8 of them past the last sub-block
 ])
 @pytest.mark.parametrize("n_tok", [1, 3, 8, 13])
 def test_matvec(gpu, qtype, M, K, n_tok):
