@@ -55,6 +55,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--chain-only", action="store_true", help="only the B=1 chain (for rocprof)")
     ap.add_argument("--matvec-only", action="store_true", help="only BASELINE configs 1-2 (quantised matvec)")
     ap.add_argument("--eager", action="store_true", help="--matvec-only: eager launches instead of graph replays")
+    ap.add_argument("--matvec-batched-only", action="store_true",
+                    help="--matvec-only: only the batched launches (for counter passes)")
+    ap.add_argument("--reps", type=int, default=10, help="--matvec-only: timed repetitions")
     ap.add_argument("--decode-step-only", action="store_true",
                     help="only the full decoder step (attention, Gated DeltaNet, MoE, lm_head), one JSON line")
     ap.add_argument("--quant-shapes", default=None,
@@ -473,7 +476,7 @@ QUANT_MV_SHAPES = (("config1_iq4xs_512x2048", 23, 512, 2048), ("config2_iq3xxs_2
 
 
 def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330, samples: dict | None = None,
-                 shapes=None, graph: bool = True):
+                 shapes=None, graph: bool = True, per_call_leg: bool = True):
     """BASELINE configs 1 and 2: one y = W x with W a raw IQ4_XS [512 x 2048] or IQ3_XXS
     [2048 x 512] / [512 x 2048] matrix (the reference's NpuIQ4MatVec / NpuQuantMatVec
     call, npu/quant_mv.py:419-463), fp32 x ~ N(0, 1), seeded device-generated
@@ -483,7 +486,8 @@ def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330, samp
     consecutive matrices are one [batch M x K] raw matrix, so one launch computes their
     products with the same x.  Algorithmic bytes per call: W + x + y.  ``graph=False``
     times the same launches eagerly (for counter collection, which serialises every
-    dispatch anyway)."""
+    dispatch anyway); ``per_call_leg=False`` skips the per-call launches (a few batched
+    launches are all a counter pass needs)."""
     import torch
     from npu_amd import _lib as L
     from npu_amd import ops, synth
@@ -531,13 +535,14 @@ def run_quant_mv(dev, reps: int = 10, batch: int = 64, total_mb: int = 330, samp
             torch.cuda.synchronize()
             return e0.elapsed_time(e1) * 1e3 / (reps * launches)
 
-        us = period_us(per_call, n)
+        us = period_us(per_call, n) if per_call_leg else float("nan")
         ub = period_us(batched, n // batch)
         # the last matrix against its device dequant (gm_dequant_f32, exact) in float64
         Wd = ops.dequant(qt, W[n - 1].reshape(-1)).view(M, K).double()
         ref = Wd @ x.double()
-        rel = float((y[n - 1].double() - ref).abs().max() / ref.abs().max())
-        same = bool(torch.equal(yb.view(n, M), y))
+        y_last = y[n - 1] if per_call_leg else yb.view(n, M)[n - 1]
+        rel = float((y_last.double() - ref).abs().max() / ref.abs().max())
+        same = bool(torch.equal(yb.view(n, M), y)) if per_call_leg else None
         if samples is not None:                     # the CPU baseline's leg: the last matrix and x
             samples.setdefault("quant_mv", {})[name] = (qt, M, K, W[n - 1].cpu().numpy(), x.cpu().numpy())
         algo = M * rb + K * 4 + M * 4
@@ -784,7 +789,8 @@ def main() -> int:
         return 0
     if args.matvec_only:
         shapes = None if args.quant_shapes is None else args.quant_shapes.split(",")
-        print(json.dumps({"quant_mv": run_quant_mv(dev, shapes=shapes, graph=not args.eager)}))
+        print(json.dumps({"quant_mv": run_quant_mv(dev, reps=args.reps, shapes=shapes, graph=not args.eager,
+                                                   per_call_leg=not args.matvec_batched_only)}))
         return 0
     if args.decode_step_only:
         layers = build_layers(args.layers, dev)
