@@ -314,6 +314,40 @@ size_t gm_ssm_workspace_bytes(const gm_ssm_layer* L);
 int gm_ssm_decode(const gm_ssm_layer* L, const float* x, float* y, float* conv_state, float* rec_state, int flags,
                   void* ws, size_t ws_bytes, void* stream);
 
+/*
+ * A core layer linked to the MoE block that follows it in the decoder layer
+ * (qwen/forward.py:880-884 runs x = x + moe_forward(rms_norm(x, post_norm)) on
+ * the core layer's output): as gm_attn_decode / gm_ssm_decode, and the layer's
+ * output projection also forms that block's router inputs from its output y
+ * (the raw router dot products of y * moe->norm_w and the sum of y^2, added into
+ * the block's T = 1 router accumulators in moe_ws), so gm_moe_forward_acc then
+ * runs the block on y without a router launch.  moe must fit the T = 1
+ * accumulator kernels (gm_moe_chain_fused(moe, 1, 1) == 1), have the core
+ * layer's D and carry a 16-byte aligned router_t; moe_ws is the block's
+ * workspace (>= gm_moe_workspace_bytes(moe, 1) bytes, 256-byte aligned).  The
+ * call clears the accumulators itself (its first launch), so the pair is
+ * self-contained; the logits equal gm_moe_forward's to fp32 rounding (the same
+ * dot products added in another order).  No counterpart in the reference (its
+ * decoder loop calls the router per MoE block); for decoder loops that run a
+ * core layer and its MoE block back to back.
+ */
+int gm_attn_decode_moe(const gm_attn_layer* L, const float* x, float* y, float* k_cache, float* v_cache, int pos,
+                       int max_pos, const float* rope_cos, const float* rope_sin, int flags, void* ws,
+                       size_t ws_bytes, const gm_moe_layer* moe, void* moe_ws, size_t moe_ws_bytes, void* stream);
+int gm_ssm_decode_moe(const gm_ssm_layer* L, const float* x, float* y, float* conv_state, float* rec_state, int flags,
+                      void* ws, size_t ws_bytes, const gm_moe_layer* moe, void* moe_ws, size_t moe_ws_bytes,
+                      void* stream);
+
+/*
+ * One token through a MoE block whose router inputs the preceding
+ * gm_attn_decode_moe / gm_ssm_decode_moe call formed in ws (same block, same
+ * workspace, x = that call's y): gm_moe_forward at T = 1 without the router
+ * launch (gate/up and down).  flags as gm_moe_forward.  No counterpart in the
+ * reference; see gm_attn_decode_moe.
+ */
+int gm_moe_forward_acc(const gm_moe_layer* L, const float* x, float* y, int flags, void* ws, size_t ws_bytes,
+                       void* stream);
+
 /* y[r] = rmsnorm(x[r], w, eps) for n_rows rows of D (qwen/forward.py:58-61; the
  * decoder's output norm, :887-888). */
 int gm_rms_norm(const float* x, const float* w, int D, int n_rows, float eps, float* y, void* stream);

@@ -102,8 +102,13 @@ SIGNATURES = {
     "gm_attn_workspace_bytes": (_sz, [ctypes.POINTER(GmAttnLayer), _i32]),
     "gm_attn_decode": (_i32, [ctypes.POINTER(GmAttnLayer), _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _i32, _vp,
                               _sz, _vp]),
+    "gm_attn_decode_moe": (_i32, [ctypes.POINTER(GmAttnLayer), _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _i32,
+                                  _vp, _sz, ctypes.POINTER(GmMoeLayer), _vp, _sz, _vp]),
     "gm_ssm_workspace_bytes": (_sz, [ctypes.POINTER(GmSsmLayer)]),
     "gm_ssm_decode": (_i32, [ctypes.POINTER(GmSsmLayer), _vp, _vp, _vp, _vp, _i32, _vp, _sz, _vp]),
+    "gm_ssm_decode_moe": (_i32, [ctypes.POINTER(GmSsmLayer), _vp, _vp, _vp, _vp, _i32, _vp, _sz,
+                                 ctypes.POINTER(GmMoeLayer), _vp, _sz, _vp]),
+    "gm_moe_forward_acc": (_i32, [ctypes.POINTER(GmMoeLayer), _vp, _vp, _i32, _vp, _sz, _vp]),
     "gm_rms_norm": (_i32, [_vp, _vp, _i32, _i32, _f32, _vp, _vp]),
 }
 

@@ -444,6 +444,82 @@ int gm_ssm_decode(const gm_ssm_layer* L, const float* x, float* y, float* conv_s
   return gm_ssm_run(L, x, y, conv_state, rec_state, flags, static_cast<uint8_t*>(ws), as_stream(stream));
 }
 
+// The MoE block that follows a core layer, for the linked entry points: it must
+// run on the T = 1 accumulator kernels (gm_moe_chain_fused(&moe, 1, 1) == 1),
+// share the core layer's D and carry router_t; its workspace holds the
+// accumulators the core layer's launches clear and fill.
+static int moe_link(const char* fn, const gm_moe_layer* M, int D, void* ws, size_t ws_bytes, GmNextRouter* nx) {
+  if (int rc = check_layer(M)) return rc;
+  if (!chain_layer_fused(M, 0, 1) || M->D != D || !M->router_t)
+    return gm_fail_arg("%s: the MoE block must fit the T = 1 accumulator kernels, have D=%d and carry router_t", fn,
+                       D);
+  if (reinterpret_cast<uintptr_t>(M->router_t) % 16) return gm_fail_arg("%s: router_t must be 16-byte aligned", fn);
+  if (!ws || reinterpret_cast<uintptr_t>(ws) % 256) return gm_fail_arg("%s: MoE workspace NULL or not 256-byte aligned", fn);
+  const GmMoeWs lay = gm_moe_ws_layout(M, 1);
+  if (ws_bytes < lay.total)
+    return gm_fail_arg("%s: MoE workspace %zu bytes < %zu needed", fn, ws_bytes, lay.total), GM_EWORKSPACE;
+  nx->w = M->router_t;
+  nx->nw = M->norm_w;
+  nx->acc = reinterpret_cast<double*>(static_cast<uint8_t*>(ws) + lay.acc);
+  nx->E = M->E;
+  nx->ld = gm_acc_ld(M->E);
+  nx->f32 = M->q_router == GM_QTYPE_F32 ? 1 : 0;
+  return GM_OK;
+}
+
+int gm_attn_decode_moe(const gm_attn_layer* L, const float* x, float* y, float* k_cache, float* v_cache, int pos,
+                       int max_pos, const float* rope_cos, const float* rope_sin, int flags, void* ws,
+                       size_t ws_bytes, const gm_moe_layer* moe, void* moe_ws, size_t moe_ws_bytes, void* stream) {
+  if (int rc = check_attn(L)) return rc;
+  if (int rc = check_io("gm_attn_decode_moe", x, y)) return rc;
+  if (max_pos < 1 || pos < 0 || pos >= max_pos)
+    return gm_fail_arg("gm_attn_decode_moe: pos=%d must be in [0, max_pos=%d)", pos, max_pos);
+  if (!k_cache || !v_cache || !ws || (L->rope_dim > 0 && (!rope_cos || !rope_sin)))
+    return gm_fail_arg("gm_attn_decode_moe: NULL cache, rope table or workspace");
+  const size_t need = gm_attn_ws_layout(L, max_pos).total;
+  if (ws_bytes < need)
+    return gm_fail_arg("gm_attn_decode_moe: workspace %zu bytes < %zu needed", ws_bytes, need), GM_EWORKSPACE;
+  if (reinterpret_cast<uintptr_t>(ws) % 256) return gm_fail_arg("gm_attn_decode_moe: workspace must be 256-byte aligned");
+  GmNextRouter nx{};
+  if (int rc = moe_link("gm_attn_decode_moe", moe, L->D, moe_ws, moe_ws_bytes, &nx)) return rc;
+  return gm_attn_run(L, x, y, k_cache, v_cache, pos, max_pos, rope_cos, rope_sin, flags, static_cast<uint8_t*>(ws),
+                     as_stream(stream), &nx);
+}
+
+int gm_ssm_decode_moe(const gm_ssm_layer* L, const float* x, float* y, float* conv_state, float* rec_state, int flags,
+                      void* ws, size_t ws_bytes, const gm_moe_layer* moe, void* moe_ws, size_t moe_ws_bytes,
+                      void* stream) {
+  if (int rc = check_ssm(L)) return rc;
+  if (int rc = check_io("gm_ssm_decode_moe", x, y)) return rc;
+  if (!rec_state || !ws || (L->conv_k > 1 && !conv_state))
+    return gm_fail_arg("gm_ssm_decode_moe: NULL state or workspace");
+  const size_t need = gm_ssm_ws_layout(L).total;
+  if (ws_bytes < need)
+    return gm_fail_arg("gm_ssm_decode_moe: workspace %zu bytes < %zu needed", ws_bytes, need), GM_EWORKSPACE;
+  if (reinterpret_cast<uintptr_t>(ws) % 256) return gm_fail_arg("gm_ssm_decode_moe: workspace must be 256-byte aligned");
+  GmNextRouter nx{};
+  if (int rc = moe_link("gm_ssm_decode_moe", moe, L->D, moe_ws, moe_ws_bytes, &nx)) return rc;
+  return gm_ssm_run(L, x, y, conv_state, rec_state, flags, static_cast<uint8_t*>(ws), as_stream(stream), &nx);
+}
+
+int gm_moe_forward_acc(const gm_moe_layer* L, const float* x, float* y, int flags, void* ws, size_t ws_bytes,
+                       void* stream) {
+  if (int rc = check_layer(L)) return rc;
+  if (!chain_layer_fused(L, 0, 1) || !L->router_t)
+    return gm_fail_arg("gm_moe_forward_acc: the block must fit the T = 1 accumulator kernels and carry router_t");
+  if (!x || !y || !ws) return gm_fail_arg("gm_moe_forward_acc: NULL pointer");
+  if (x == y) return gm_fail_arg("gm_moe_forward_acc: x and y must not alias");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 16)
+    return gm_fail_arg("gm_moe_forward_acc: x and y must be 16-byte aligned");
+  const GmMoeWs lay = gm_moe_ws_layout(L, 1);
+  if (ws_bytes < lay.total)
+    return gm_fail_arg("gm_moe_forward_acc: workspace %zu bytes < %zu needed", ws_bytes, lay.total), GM_EWORKSPACE;
+  if (reinterpret_cast<uintptr_t>(ws) % 256) return gm_fail_arg("gm_moe_forward_acc: workspace must be 256-byte aligned");
+  uint8_t* w = static_cast<uint8_t*>(ws);
+  GmChainStep cs{reinterpret_cast<double*>(w + lay.acc), nullptr, nullptr, false, nullptr};
+  return gm_dec_run(L, x, y, 1, flags, w, lay, as_stream(stream), 0, &cs);
+}
+
 int gm_rms_norm(const float* x, const float* w, int D, int n_rows, float eps, float* y, void* stream) {
   if (D <= 0 || n_rows < 0 || !(eps >= 0.f)) return gm_fail_arg("gm_rms_norm: bad sizes or eps");
   if (n_rows == 0) return GM_OK;

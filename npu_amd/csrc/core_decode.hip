@@ -27,10 +27,16 @@
 //                    [Hv][Sk][Sv] (the reference's layout) updated in place
 //   k_ssm_gnorm      rmsnorm(o_head, ssm_norm) * silu(z)
 //   mv_bf16 (+ x)    y = W_out o (+ x)
+// Linked to the following MoE block (gm_attn_decode_moe / gm_ssm_decode_moe):
+// the first launch also clears that block's T = 1 router accumulators, and the
+// output projection adds the router dot products and the sum of squares of its
+// rows of y into them (as a chain's down kernel does for the next layer), so
+// the MoE block runs without its router launch.
 // No kernel holds a scratch buffer of its own: intermediates live in the
 // caller's workspace (gm_attn_ws_layout / gm_ssm_ws_layout).
 #include "common.h"
 #include "kernels.h"
+#include "moe_decode.h"
 
 namespace {
 
@@ -352,7 +358,7 @@ GmAttnWs gm_attn_ws_layout(const gm_attn_layer* L, int max_pos) {
 }
 
 int gm_attn_run(const gm_attn_layer* L, const float* x, float* y, float* kc, float* vc, int pos, int max_pos,
-                const float* cosr, const float* sinr, int flags, uint8_t* ws, hipStream_t s) {
+                const float* cosr, const float* sinr, int flags, uint8_t* ws, hipStream_t s, const GmNextRouter* moe) {
   const GmAttnWs lay = gm_attn_ws_layout(L, max_pos);
   const int D = L->D, Hq = L->n_head, Hkv = L->n_head_kv, Dh = L->head_dim, rd = L->rope_dim;
   float* qkv = reinterpret_cast<float*>(ws + lay.qkv);
@@ -361,7 +367,8 @@ int gm_attn_run(const gm_attn_layer* L, const float* x, float* y, float* kc, flo
   float* out = reinterpret_cast<float*>(ws + lay.out);
   const int Mqkv = (2 * Hq + 2 * Hkv) * Dh;
   if (int rc = gm_launch_mv_bf16_norm2(static_cast<const uint16_t*>(L->wqkv), Mqkv, nullptr, 0, D, x, L->attn_norm,
-                                       L->eps, qkv, nullptr, s))
+                                       L->eps, qkv, nullptr, s, moe ? moe->acc : nullptr,
+                                       moe ? GM_ACC_COPIES * moe->ld : 0))
     return rc;
   hipLaunchKernelGGL(k_attn_prep, dim3(Hq + Hkv), dim3(Dh), (Dh + 16) * sizeof(float), s, qkv, L->q_norm,
                      L->k_norm, L->eps, Hq, Hkv, Dh, rd, cosr + (size_t)pos * rd, sinr + (size_t)pos * rd, qr,
@@ -380,7 +387,7 @@ int gm_attn_run(const gm_attn_layer* L, const float* x, float* y, float* kc, flo
   hipLaunchKernelGGL(k_attn_combine, dim3(Hq), dim3(Dh), 0, s, part, lay.nch, nch, qkv, Dh, out);
   GM_TRY(hipGetLastError());
   return gm_launch_mv_bf16_add(static_cast<const uint16_t*>(L->wo), D, Hq * Dh, out, y,
-                               (flags & GM_MOE_RESIDUAL) ? x : nullptr, s);
+                               (flags & GM_MOE_RESIDUAL) ? x : nullptr, s, moe);
 }
 
 GmSsmWs gm_ssm_ws_layout(const gm_ssm_layer* L) {
@@ -400,7 +407,7 @@ GmSsmWs gm_ssm_ws_layout(const gm_ssm_layer* L) {
 }
 
 int gm_ssm_run(const gm_ssm_layer* L, const float* x, float* y, float* conv_state, float* rec_state, int flags,
-               uint8_t* ws, hipStream_t s) {
+               uint8_t* ws, hipStream_t s, const GmNextRouter* moe) {
   const GmSsmWs lay = gm_ssm_ws_layout(L);
   const int D = L->D, Hk = L->n_k_heads, Hv = L->n_v_heads, Sk = L->d_state, Sv = L->d_state;
   const int Ck = Hk * Sk, di = Hv * Sv, C = 2 * Ck + di;
@@ -412,7 +419,7 @@ int gm_ssm_run(const gm_ssm_layer* L, const float* x, float* y, float* conv_stat
   float* o2 = reinterpret_cast<float*>(ws + lay.o2);
   if (int rc = gm_launch_mv_bf16_norm2(static_cast<const uint16_t*>(L->w_in), C,
                                        static_cast<const uint16_t*>(L->w_gate), di, D, x, L->attn_norm, L->eps, mixed,
-                                       z, s))
+                                       z, s, moe ? moe->acc : nullptr, moe ? GM_ACC_COPIES * moe->ld : 0))
     return rc;
   const int nconv = C / Sk, nab = (2 * Hv + Sk / 64 - 1) / (Sk / 64);
   hipLaunchKernelGGL(k_ssm_conv_ab, dim3(nconv + nab), dim3(Sk), 0, s, mixed, L->conv1d, conv_state, L->conv_k, Hk,
@@ -429,7 +436,7 @@ int gm_ssm_run(const gm_ssm_layer* L, const float* x, float* y, float* conv_stat
   hipLaunchKernelGGL(k_ssm_gnorm, dim3(Hv), dim3(Sv), 0, s, o, L->ssm_norm, z, Sv, L->eps, o2);
   GM_TRY(hipGetLastError());
   return gm_launch_mv_bf16_add(static_cast<const uint16_t*>(L->w_out), D, di, o2, y,
-                               (flags & GM_MOE_RESIDUAL) ? x : nullptr, s);
+                               (flags & GM_MOE_RESIDUAL) ? x : nullptr, s, moe);
 }
 
 int gm_launch_rms_row(const float* x, const float* w, int D, int n_rows, float eps, float* y, hipStream_t s) {

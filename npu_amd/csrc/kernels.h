@@ -24,13 +24,17 @@ int gm_launch_matvec(int qtype, const void* w, int M, int K, const float* x, int
 int gm_launch_mv_bf16(const uint16_t* w, int M, int K, const float* x, int n_tok, float* y, hipStream_t s);
 int gm_launch_gateup(int qtype, const void* wg, const void* wu, int FF, int D, const float* x, int n_tok,
                      float* h, hipStream_t s);
-// One token, y = add + W x (add may be NULL).
+// One token, y = add + W x (add may be NULL); with nx (a MoE block's router,
+// moe_decode.h) y also feeds that block's T = 1 router accumulators.
+struct GmNextRouter;
 int gm_launch_mv_bf16_add(const uint16_t* w, int M, int K, const float* x, float* y, const float* add,
-                          hipStream_t s);
+                          hipStream_t s, const GmNextRouter* nx = nullptr);
 // One token: h = RMSNorm(x) (norm_w, eps; none when norm_w is null), y = W h and,
-// when w2 is given, y2 = W2 h with W2's M2 rows in the same launch.
+// when w2 is given, y2 = W2 h with W2's M2 rows in the same launch; zacc: zn
+// doubles the launch clears (NULL: none).
 int gm_launch_mv_bf16_norm2(const uint16_t* w, int M, const uint16_t* w2, int M2, int K, const float* x,
-                            const float* norm_w, float eps, float* y, float* y2, hipStream_t s);
+                            const float* norm_w, float eps, float* y, float* y2, hipStream_t s,
+                            double* zacc = nullptr, int zn = 0);
 int gm_launch_rms_row(const float* x, const float* w, int D, int n_rows, float eps, float* y, hipStream_t s);
 
 // Core-layer decode workspaces (core_decode.hip), byte offsets, 256-byte aligned.
@@ -39,14 +43,18 @@ struct GmAttnWs {
   int nch;         // attention partial slots per head (max_pos / chunk, rounded up)
 };
 GmAttnWs gm_attn_ws_layout(const gm_attn_layer* L, int max_pos);
+// With moe (the following MoE block's router, its T = 1 accumulators): the
+// layer's first launch clears the accumulators and its output projection adds
+// the router inputs of its output into them.
 int gm_attn_run(const gm_attn_layer* L, const float* x, float* y, float* kc, float* vc, int pos, int max_pos,
-                const float* cosr, const float* sinr, int flags, uint8_t* ws, hipStream_t s);
+                const float* cosr, const float* sinr, int flags, uint8_t* ws, hipStream_t s,
+                const GmNextRouter* moe = nullptr);
 struct GmSsmWs {
   size_t h, mixed, z, gb, conv, o, o2, total;
 };
 GmSsmWs gm_ssm_ws_layout(const gm_ssm_layer* L);
 int gm_ssm_run(const gm_ssm_layer* L, const float* x, float* y, float* conv_state, float* rec_state, int flags,
-               uint8_t* ws, hipStream_t s);
+               uint8_t* ws, hipStream_t s, const GmNextRouter* moe = nullptr);
 
 // MoE workspace layout for T tokens (offsets in bytes, 256-byte aligned).
 struct GmMoeWs {

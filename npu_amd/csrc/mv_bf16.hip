@@ -24,6 +24,7 @@
 // loads at a time, and their tiles are summed in LDS in wave order.
 #include "common.h"
 #include "kernels.h"
+#include "moe_decode.h"
 
 namespace {
 
@@ -31,14 +32,91 @@ constexpr int kSlotK = 512;                   // k values per slot (64 lanes x 8
 
 // One-token extras of k_mv_bf16: a second matrix w2 [M2 x K] whose rows follow
 // w's in the launch (its products go to y2), and an RMSNorm weight: with
-// norm_w, x is staged as (x * rsqrt(mean(x^2) + eps)) * norm_w.
+// norm_w, x is staged as (x * rsqrt(mean(x^2) + eps)) * norm_w.  zacc: zn
+// doubles the last block clears (a MoE block's router accumulators, which a
+// later launch of the same core layer adds into).
 struct MvEx {
   const uint16_t* w2;
   int M2;
   float* y2;
   const float* norm_w;
   float eps;
+  double* zacc;
+  int zn;
 };
+
+// Accumulator positions per thread of the next-router epilogue (512 threads;
+// E <= 512: 8 x 64 + 2 positions).
+constexpr int kNxSlots = 2;
+
+// The router epilogue's loads: thread t takes accumulator positions t + NT j
+// (gm_acc_pos order, so a wave's atomics fall on consecutive words) and loads
+// the 8 router values of its word at columns r0 .. r0+7 (one 8-column group of
+// router_t: 16 bytes of bf16 or 32 of fp32; positions without a router row load
+// row 0), and every thread the 8 norm weights (ones without a norm weight).
+template <int NT>
+__device__ __forceinline__ void nx_load(const GmNextRouter& nx, int r0, gm_u32x4 (&wv)[kNxSlots][2],
+                                        gm_f32x4 (&nw)[2]) {
+  const int mvn = gm_acc_mv(nx.E), es = nx.f32 ? 4 : 2;
+#pragma unroll
+  for (int j = 0; j < kNxSlots; ++j) {
+    const int pos = threadIdx.x + NT * j;
+    const int e = pos < 64 * mvn ? 64 * (pos % mvn) + pos / mvn : nx.E + (pos - 64 * mvn);
+    const int er = e <= nx.E ? e : 0;
+    const gm_u32x4* q = reinterpret_cast<const gm_u32x4*>(static_cast<const uint8_t*>(nx.w) +
+                                                          ((int64_t)(r0 >> 3) * (nx.E + 1) + er) * 8 * es);
+    wv[j][0] = gm_ld<true>(q);
+    wv[j][1] = gm_ld<true>(q + (nx.f32 ? 1 : 0));
+  }
+  const gm_f32x4 one = {1.f, 1.f, 1.f, 1.f};
+  nw[0] = nx.nw ? *reinterpret_cast<const gm_f32x4*>(nx.nw + r0) : one;
+  nw[1] = nx.nw ? *reinterpret_cast<const gm_f32x4*>(nx.nw + r0 + 4) : one;
+}
+
+template <int NT>
+__device__ __forceinline__ void nx_add(const GmNextRouter& nx, const float* s_y, const gm_u32x4 (&wv)[kNxSlots][2],
+                                       const gm_f32x4 (&nw)[2]) {
+  const int mvn = gm_acc_mv(nx.E);
+  float yv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) yv[i] = s_y[i];
+  const float nv[8] = {nw[0].x, nw[0].y, nw[0].z, nw[0].w, nw[1].x, nw[1].y, nw[1].z, nw[1].w};
+  int xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  double* copy = nx.acc + (xcc & (GM_ACC_COPIES - 1)) * nx.ld;
+#pragma unroll
+  for (int j = 0; j < kNxSlots; ++j) {
+    const int pos = threadIdx.x + NT * j;
+    const int e = pos < 64 * mvn ? 64 * (pos % mvn) + pos / mvn : nx.E + (pos - 64 * mvn);
+    const bool live = pos < 64 * mvn ? e < nx.E : e <= nx.E + 1;
+    if (!live) continue;
+    float wf[8];
+    if (nx.f32) {
+      const uint32_t u[8] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w,
+                             wv[j][1].x, wv[j][1].y, wv[j][1].z, wv[j][1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) wf[i] = __uint_as_float(u[i]);
+    } else {
+      const uint32_t u[4] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wf[2 * i] = __uint_as_float(u[i] << 16);
+        wf[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+      }
+    }
+    float p = 0.f;
+    if (e <= nx.E) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p = fmaf(wf[i], yv[i] * nv[i], p);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p = fmaf(yv[i], yv[i], p);
+    }
+    // all adds into one copy come from one XCD and meet in its L2: workgroup scope
+    // is enough, and the kernel boundary writes the L2 back for the MoE launch
+    __hip_atomic_fetch_add(copy + pos, (double)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+}
 
 // One token.  Per pass of S slots: the pass's x values are loaded into
 // registers first (their loads retire before the weights', vmcnt being in
@@ -47,21 +125,34 @@ struct MvEx {
 // branch separates a load from its use); x goes to LDS while the weights are
 // in flight (normalised first with ex.norm_w), and each slot is multiplied as
 // it lands.
-template <int R, int S>
-__global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w, int M, int K,
-                                                 const float* __restrict__ x, float* __restrict__ y,
-                                                 const float* __restrict__ add, MvEx ex) {
-  extern __shared__ gm_f32x4 xs4[];                               // [XQ x 256]: one pass of x
-  __shared__ float red[4];
-  constexpr int XQ = (S * kSlotK / 4 + 255) / 256;                // x float4 per thread and pass
+//
+// NW waves per block.  NXT (8 waves, one row each): the block's 8 outputs y
+// (rows r0 .. r0+7) also feed a MoE block's router (nx, its T = 1 accumulators,
+// as the chain's down kernel feeds the next layer's): every accumulator
+// position gets sum_i Wn[e][r0 + i] (y[r0 + i] w_norm[r0 + i]) (router row e,
+// row E the shared gate vector, from router_t) or, at word E + 1,
+// sum_i y[r0 + i]^2, added with fp64 atomics into the copy of the block's XCD.
+// The router values and norm weights are loaded behind the matrix rows.
+template <int R, int S, int NW, bool NXT>
+__global__ void __launch_bounds__(64 * NW) k_mv_bf16(const uint16_t* __restrict__ w, int M, int K,
+                                                     const float* __restrict__ x, float* __restrict__ y,
+                                                     const float* __restrict__ add, MvEx ex, GmNextRouter nx) {
+  static_assert(!NXT || (R == 1 && NW == 8), "the router epilogue takes 8 waves of one row");
+  constexpr int NT = 64 * NW;
+  extern __shared__ gm_f32x4 xs4[];                               // [XQ x NT]: one pass of x
+  __shared__ float red[NW];
+  __shared__ float s_y[NW];
+  constexpr int XQ = (S * kSlotK / 4 + NT - 1) / NT;              // x float4 per thread and pass
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int row0 = (blockIdx.x * 4 + wave) * R;
+  const int row0 = (blockIdx.x * NW + wave) * R;
   const int npass = (K + S * kSlotK - 1) / (S * kSlotK);
   const int kq = K >> 2, ng = K >> 3;
   const float* xs = reinterpret_cast<const float*>(xs4);
   const gm_f32x4* x4 = reinterpret_cast<const gm_f32x4*>(x);
   const int Mt = M + ex.M2;
 
+  gm_u32x4 nxw[kNxSlots][2];                                      // router values of the epilogue (NXT)
+  gm_f32x4 nxn[2];
   const gm_u32x4* rp[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -72,6 +163,8 @@ __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w,
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  if (ex.zacc != nullptr && blockIdx.x == gridDim.x - 1)          // uniform per block
+    for (int i = threadIdx.x; i < ex.zn; i += NT) ex.zacc[i] = 0.0;
 
   for (int p = 0; p < npass; ++p) {
     const int q0 = p * (S * kSlotK / 4);                          // first float4 of the pass
@@ -80,7 +173,7 @@ __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w,
     gm_f32x4 xr[XQ], nr[XQ];
 #pragma unroll
     for (int q = 0; q < XQ; ++q) {
-      const int i = q0 + (int)threadIdx.x + 256 * q, ic = i < kq ? i : kq - 1;   // past K: zeroed below
+      const int i = q0 + (int)threadIdx.x + NT * q, ic = i < kq ? i : kq - 1;    // past K: zeroed below
       xr[q] = x4[ic];
       nr[q] = n4[ic];
     }
@@ -93,10 +186,14 @@ __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w,
       for (int r = 0; r < R; ++r) wv[r][s] = gm_ld<true>(rp[r] + g);
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NXT) {
+      if (p == 0) nx_load<NT>(nx, blockIdx.x * 8, nxw, nxn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if (p > 0) __syncthreads();                                   // the previous pass's x reads are done
 #pragma unroll
     for (int q = 0; q < XQ; ++q)
-      if (q0 + (int)threadIdx.x + 256 * q >= kq) xr[q] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
+      if (q0 + (int)threadIdx.x + NT * q >= kq) xr[q] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
     if (ex.norm_w) {                                              // one pass (the launcher checks)
       float ss = 0.f;
 #pragma unroll
@@ -105,12 +202,15 @@ __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w,
       ss = gm_wave_sum64(ss);
       if (lane == 0) red[wave] = ss;
       __syncthreads();
-      const float rs = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + ex.eps);
+      float rsum = 0.f;
+#pragma unroll
+      for (int i = 0; i < NW; ++i) rsum += red[i];
+      const float rs = 1.0f / sqrtf(rsum / (float)K + ex.eps);
 #pragma unroll
       for (int q = 0; q < XQ; ++q) xr[q] = (xr[q] * rs) * nr[q];
     }
 #pragma unroll
-    for (int q = 0; q < XQ; ++q) xs4[threadIdx.x + 256 * q] = xr[q];   // unconditional: XQ x 256 slots
+    for (int q = 0; q < XQ; ++q) xs4[threadIdx.x + NT * q] = xr[q];    // unconditional: XQ x NT slots
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -139,10 +239,18 @@ __global__ void __launch_bounds__(256) k_mv_bf16(const uint16_t* __restrict__ w,
   for (int r = 0; r < R; ++r) {
     const float v = gm_wave_sum64(acc[r]);
     if (lane == 0 && row0 + r < M) {
-      y[row0 + r] = add ? add[row0 + r] + v : v;                  // y = add + W x (a residual), or W x
+      const float yv = add ? add[row0 + r] + v : v;               // y = add + W x (a residual), or W x
+      y[row0 + r] = yv;
+      if constexpr (NXT) s_y[wave] = yv;
     } else if (lane == 0 && row0 + r >= M && row0 + r < Mt) {
       ex.y2[row0 + r - M] = v;
     }
+    if constexpr (NXT)
+      if (lane == 0 && row0 + r >= M) s_y[wave] = 0.f;
+  }
+  if constexpr (NXT) {
+    __syncthreads();
+    nx_add<NT>(nx, s_y, nxw, nxn);
   }
 }
 
@@ -271,29 +379,47 @@ int launch_mfma(const uint16_t* w, int M, int K, const float* x, int n_tok, floa
 #undef GM_MV_W
 }
 
-template <int R, int S>
+template <int R, int S, int NW, bool NXT>
 int launch_mv(const uint16_t* w, int M, int K, const float* x, float* y, const float* add, const MvEx& ex,
-              hipStream_t s) {
-  const size_t smem = (size_t)((S * kSlotK / 4 + 255) / 256) * 256 * sizeof(gm_f32x4);   // XQ x 256 float4
-  if (int rc = gm_set_smem(k_mv_bf16<R, S>, smem)) return rc;
-  const dim3 grid((unsigned)((M + ex.M2 + 4 * R - 1) / (4 * R)));
-  hipLaunchKernelGGL((k_mv_bf16<R, S>), grid, dim3(256), smem, s, w, M, K, x, y, add, ex);
+              const GmNextRouter& nx, hipStream_t s) {
+  constexpr int NT = 64 * NW;
+  const size_t smem = (size_t)((S * kSlotK / 4 + NT - 1) / NT) * NT * sizeof(gm_f32x4);   // XQ x NT float4
+  if (int rc = gm_set_smem(k_mv_bf16<R, S, NW, NXT>, smem)) return rc;
+  const dim3 grid((unsigned)((M + ex.M2 + NW * R - 1) / (NW * R)));
+  hipLaunchKernelGGL((k_mv_bf16<R, S, NW, NXT>), grid, dim3(NT), smem, s, w, M, K, x, y, add, ex, nx);
   GM_TRY(hipGetLastError());
   return GM_OK;
 }
 
+// 4 waves per block, or 8 with the router epilogue (one 8-column router group per block).
+template <bool NXT>
+int launch_mv1_t(const uint16_t* w, int M, int K, const float* x, float* y, const float* add, const MvEx& ex,
+                 const GmNextRouter& nx, hipStream_t s) {
+  constexpr int NW = NXT ? 8 : 4;
+  const int slots = (K + kSlotK - 1) / kSlotK;
+  if (slots <= 1) return launch_mv<1, 1, NW, NXT>(w, M, K, x, y, add, ex, nx, s);
+  if (slots <= 2) return launch_mv<1, 2, NW, NXT>(w, M, K, x, y, add, ex, nx, s);
+  if (slots <= 4) return launch_mv<1, 4, NW, NXT>(w, M, K, x, y, add, ex, nx, s);
+  if (slots <= 8) return launch_mv<1, 8, NW, NXT>(w, M, K, x, y, add, ex, nx, s);
+  return launch_mv<1, 16, NW, NXT>(w, M, K, x, y, add, ex, nx, s);
+}
+
 // S = the row's slots (at most 16 per pass), one row per wave (the most
 // waves, each with its whole row in flight, was the fastest launch shape).
-// The RMSNorm of ex.norm_w needs the whole row in one pass (K <= 8192).
+// The RMSNorm of ex.norm_w needs the whole row in one pass (K <= 8192).  With
+// nx, the launch also adds the MoE router inputs of its rows (M % 8 == 0, M
+// the router's D, E <= 512).
 int launch_mv1(const uint16_t* w, int M, int K, const float* x, float* y, const float* add, hipStream_t s,
-               const MvEx& ex = MvEx{nullptr, 0, nullptr, nullptr, 0.f}) {
+               const MvEx& ex = MvEx{nullptr, 0, nullptr, nullptr, 0.f, nullptr, 0},
+               const GmNextRouter* nx = nullptr) {
   const int slots = (K + kSlotK - 1) / kSlotK;
   if (ex.norm_w && slots > 16) return gm_fail_arg("mv_bf16: a fused RMSNorm needs K <= %d", 16 * kSlotK);
-  if (slots <= 1) return launch_mv<1, 1>(w, M, K, x, y, add, ex, s);
-  if (slots <= 2) return launch_mv<1, 2>(w, M, K, x, y, add, ex, s);
-  if (slots <= 4) return launch_mv<1, 4>(w, M, K, x, y, add, ex, s);
-  if (slots <= 8) return launch_mv<1, 8>(w, M, K, x, y, add, ex, s);
-  return launch_mv<1, 16>(w, M, K, x, y, add, ex, s);
+  if (nx != nullptr) {
+    if (M % 8 || ex.M2 || nx->E > 512 || 64 * gm_acc_mv(nx->E) + 2 > 512 * kNxSlots)
+      return gm_fail_arg("mv_bf16: router epilogue needs M %% 8 == 0, one matrix and E <= 512");
+    return launch_mv1_t<true>(w, M, K, x, y, add, ex, *nx, s);
+  }
+  return launch_mv1_t<false>(w, M, K, x, y, add, ex, GmNextRouter{}, s);
 }
 
 }  // namespace
@@ -306,16 +432,18 @@ int gm_launch_mv_bf16(const uint16_t* w, int M, int K, const float* x, int n_tok
   return launch_mfma(w, M, K, x, n_tok, y, s);
 }
 
-// One token, y = add + W x (the residual of the core layers' output projections).
+// One token, y = add + W x (the residual of the core layers' output projections);
+// with nx, y also feeds the MoE router accumulators nx->acc (cleared beforehand).
 int gm_launch_mv_bf16_add(const uint16_t* w, int M, int K, const float* x, float* y, const float* add,
-                          hipStream_t s) {
-  return launch_mv1(w, M, K, x, y, add, s);
+                          hipStream_t s, const GmNextRouter* nx) {
+  return launch_mv1(w, M, K, x, y, add, s, MvEx{nullptr, 0, nullptr, nullptr, 0.f, nullptr, 0}, nx);
 }
 
 // One token, the core layers' input projections in one launch: h = RMSNorm(x)
 // (norm_w, eps; skipped when norm_w is null), y = W h and, when w2 is given,
-// y2 = W2 h (its M2 rows follow W's in the launch).
+// y2 = W2 h (its M2 rows follow W's in the launch); zacc: zn doubles to clear.
 int gm_launch_mv_bf16_norm2(const uint16_t* w, int M, const uint16_t* w2, int M2, int K, const float* x,
-                            const float* norm_w, float eps, float* y, float* y2, hipStream_t s) {
-  return launch_mv1(w, M, K, x, y, nullptr, s, MvEx{w2, w2 ? M2 : 0, y2, norm_w, eps});
+                            const float* norm_w, float eps, float* y, float* y2, hipStream_t s, double* zacc,
+                            int zn) {
+  return launch_mv1(w, M, K, x, y, nullptr, s, MvEx{w2, w2 ? M2 : 0, y2, norm_w, eps, zacc, zn});
 }

@@ -140,12 +140,23 @@ class GpuAttn:
         return ws
 
     def step(self, x: torch.Tensor, cache: "KVCache", pos: int, cos: torch.Tensor, sin: torch.Tensor,
-             residual: bool, out: torch.Tensor) -> None:
+             residual: bool, out: torch.Tensor, moe_link=None) -> None:
+        """One token; with ``moe_link = (moe struct, moe workspace)`` the layer also forms
+        the following MoE block's router inputs (gm_attn_decode_moe)."""
         ws = self.workspace(cache.max_pos)
-        rc = L.lib().gm_attn_decode(ctypes.byref(self.struct), L.ptr(x), L.ptr(out), L.ptr(cache.k), L.ptr(cache.v),
-                                    pos, cache.max_pos, L.ptr(cos), L.ptr(sin),
-                                    L.GM_MOE_RESIDUAL if residual else 0, L.ptr(ws), ws.numel(), L.stream_ptr())
-        L.check(rc, "gm_attn_decode")
+        flags = L.GM_MOE_RESIDUAL if residual else 0
+        if moe_link is None:
+            rc = L.lib().gm_attn_decode(ctypes.byref(self.struct), L.ptr(x), L.ptr(out), L.ptr(cache.k),
+                                        L.ptr(cache.v), pos, cache.max_pos, L.ptr(cos), L.ptr(sin), flags,
+                                        L.ptr(ws), ws.numel(), L.stream_ptr())
+            L.check(rc, "gm_attn_decode")
+            return
+        st, mws = moe_link
+        rc = L.lib().gm_attn_decode_moe(ctypes.byref(self.struct), L.ptr(x), L.ptr(out), L.ptr(cache.k),
+                                        L.ptr(cache.v), pos, cache.max_pos, L.ptr(cos), L.ptr(sin), flags,
+                                        L.ptr(ws), ws.numel(), ctypes.byref(st), L.ptr(mws), mws.numel(),
+                                        L.stream_ptr())
+        L.check(rc, "gm_attn_decode_moe")
 
 
 class KVCache:
@@ -171,12 +182,15 @@ def _rope_on_device(cos: torch.Tensor, sin: torch.Tensor):
 
 
 def attn_forward(x: torch.Tensor, layer: AttnLayer, cfg: Config, cos: torch.Tensor, sin: torch.Tensor,
-                 kv_cache: KVCache | None, start_pos: int, *, residual: bool = False):
+                 kv_cache: KVCache | None, start_pos: int, *, residual: bool = False, moe_link=None):
     """x [1, T, D] -> (out [1, T, D], kv_cache) (reference :133-239).  ``residual`` returns
-    x + out (the decoder's ``x = x + y``) in the same pass."""
+    x + out (the decoder's ``x = x + y``) in the same pass; ``moe_link`` (T = 1) also forms
+    the following MoE block's router inputs (see ``forward``)."""
     B, T, D = x.shape
     if B != 1:
         raise ValueError("attn_forward: batch 1 (the reference's decoder runs one sequence)")
+    if moe_link is not None and T != 1:
+        raise ValueError("attn_forward: a MoE link is for one token")
     if layer.gpu is None:
         layer.gpu = GpuAttn(layer, cfg)
     if kv_cache is None:
@@ -191,7 +205,7 @@ def attn_forward(x: torch.Tensor, layer: AttnLayer, cfg: Config, cos: torch.Tens
     y = torch.empty_like(xd)
     with profile("attn.decode"):
         for t in range(T):
-            layer.gpu.step(xd[t], kv_cache, start_pos + t, cd, sd, residual, y[t])
+            layer.gpu.step(xd[t], kv_cache, start_pos + t, cd, sd, residual, y[t], moe_link)
             kv_cache.length += 1
     y = y.view(1, T, D)
     return (y.cpu() if on_host else y), kv_cache
@@ -259,22 +273,34 @@ class GpuSsm:
         S = torch.zeros(1, c.ssm_n_v_heads, c.ssm_d_state, c.ssm_d_state, device=self.w_out.device)
         return conv, S
 
-    def step(self, x: torch.Tensor, state, residual: bool, out: torch.Tensor) -> None:
+    def step(self, x: torch.Tensor, state, residual: bool, out: torch.Tensor, moe_link=None) -> None:
+        """One token; with ``moe_link = (moe struct, moe workspace)`` the layer also forms
+        the following MoE block's router inputs (gm_ssm_decode_moe)."""
         conv, S = state
-        rc = L.lib().gm_ssm_decode(ctypes.byref(self.struct), L.ptr(x), L.ptr(out), L.ptr(conv), L.ptr(S),
-                                   L.GM_MOE_RESIDUAL if residual else 0, L.ptr(self.ws), self.ws.numel(),
-                                   L.stream_ptr())
-        L.check(rc, "gm_ssm_decode")
+        flags = L.GM_MOE_RESIDUAL if residual else 0
+        if moe_link is None:
+            rc = L.lib().gm_ssm_decode(ctypes.byref(self.struct), L.ptr(x), L.ptr(out), L.ptr(conv), L.ptr(S),
+                                       flags, L.ptr(self.ws), self.ws.numel(), L.stream_ptr())
+            L.check(rc, "gm_ssm_decode")
+            return
+        st, mws = moe_link
+        rc = L.lib().gm_ssm_decode_moe(ctypes.byref(self.struct), L.ptr(x), L.ptr(out), L.ptr(conv), L.ptr(S),
+                                       flags, L.ptr(self.ws), self.ws.numel(), ctypes.byref(st), L.ptr(mws),
+                                       mws.numel(), L.stream_ptr())
+        L.check(rc, "gm_ssm_decode_moe")
 
 
-def ssm_forward(x: torch.Tensor, layer: SSMLayer, cfg: Config, ssm_state, *, residual: bool = False):
+def ssm_forward(x: torch.Tensor, layer: SSMLayer, cfg: Config, ssm_state, *, residual: bool = False,
+                moe_link=None):
     """x [1, T, D] -> (out [1, T, D], (conv_state [1, C, k-1], S [1, Hv, Sk, Sv])) (reference
     :292-431).  A state given as the reference's tuple of (possibly host) tensors is
     copied to the device once; the returned tuple is device tensors, updated in place by
-    later calls."""
+    later calls.  ``moe_link`` (T = 1) also forms the following MoE block's router inputs."""
     B, T, D = x.shape
     if B != 1:
         raise ValueError("ssm_forward: batch 1 (the reference's decoder runs one sequence)")
+    if moe_link is not None and T != 1:
+        raise ValueError("ssm_forward: a MoE link is for one token")
     if layer.gpu is None:
         layer.gpu = GpuSsm(layer, cfg)
     if ssm_state is None:
@@ -286,7 +312,7 @@ def ssm_forward(x: torch.Tensor, layer: SSMLayer, cfg: Config, ssm_state, *, res
     y = torch.empty_like(xd)
     with profile("ssm.decode"):
         for t in range(T):
-            layer.gpu.step(xd[t], state, residual, y[t])
+            layer.gpu.step(xd[t], state, residual, y[t], moe_link)
     y = y.view(1, T, D)
     return (y.cpu() if on_host else y), state
 
@@ -319,11 +345,14 @@ class Model:
 
 
 def forward(model: Model, tokens, *, start_pos: int = 0, kv_caches=None, ssm_states=None,
-            n_layer: int | None = None, skip_moe: bool = False):
+            n_layer: int | None = None, skip_moe: bool = False, link_moe: bool = True):
     """tokens -> (logits [T, vocab], kv_caches, ssm_states) for one sequence (reference
     :834-893): embedding, per layer ``x = x + core(x)`` then
     ``x = x + moe_forward(rms_norm(x, post_norm))``, the output norm and lm_head, all on
-    the GPU (logits stay there)."""
+    the GPU (logits stay there).  At T = 1 (``link_moe``) each core layer whose MoE block
+    fits the T = 1 accumulator kernels also forms that block's router inputs
+    (gm_attn_decode_moe / gm_ssm_decode_moe), and the block runs without its router launch
+    (gm_moe_forward_acc); the logits equal the unlinked ones to fp32 rounding."""
     cfg = model.cfg
     n = n_layer if n_layer is not None else cfg.n_layer
     kv_caches = list(kv_caches) if kv_caches is not None else [None] * cfg.n_layer
@@ -343,15 +372,17 @@ def forward(model: Model, tokens, *, start_pos: int = 0, kv_caches=None, ssm_sta
     cos, sin = g["rope"]
     for i in range(n):
         core, moe = model.layers[i]
+        link = _moe_link(g, i, core, moe, cfg) if (link_moe and not skip_moe and T == 1) else None
         if cfg.is_attention[i]:
             with profile("forward.attn"):
-                x, kv_caches[i] = attn_forward(x, core, cfg, cos, sin, kv_caches[i], start_pos, residual=True)
+                x, kv_caches[i] = attn_forward(x, core, cfg, cos, sin, kv_caches[i], start_pos, residual=True,
+                                               moe_link=link)
         else:
             with profile("forward.ssm"):
-                x, ssm_states[i] = ssm_forward(x, core, cfg, ssm_states[i], residual=True)
+                x, ssm_states[i] = ssm_forward(x, core, cfg, ssm_states[i], residual=True, moe_link=link)
         if not skip_moe:
             with profile("forward.moe"):
-                x = _moe_residual(g, i, x, core, moe, cfg)
+                x = _moe_residual(g, i, x, core, moe, cfg, linked=link is not None)
     with profile("forward.out_norm"):
         xn = _rms_norm_dev(x, model.output_norm, cfg.rms_eps, w_dev=g["onorm"])
     with profile("forward.lm_head"):
@@ -362,12 +393,11 @@ def forward(model: Model, tokens, *, start_pos: int = 0, kv_caches=None, ssm_sta
     return logits, kv_caches, ssm_states
 
 
-def _moe_residual(g: dict, i: int, x: torch.Tensor, core, moe, cfg: Config) -> torch.Tensor:
-    """x + moe_forward(rms_norm(x, core.post_norm)) in one gm_moe_forward call: a copy of
-    the layer's block struct carrying post_norm as its RMSNorm weight, with the residual
-    flag (the block's own struct, which the drop-in moe_forward uses, is left as it is).
-    ``moe`` is a ``MoELayer`` or an already resident ``GpuMoeBlock``."""
-    from npu_amd import ops
+def _moe_struct(g: dict, i: int, core, moe, cfg: Config):
+    """(struct, block) of layer i's MoE step: a copy of the block's struct carrying
+    post_norm as its RMSNorm weight (the block's own struct, which the drop-in moe_forward
+    uses, is left as it is).  ``moe`` is a ``MoELayer`` or an already resident
+    ``GpuMoeBlock``."""
     from npu_amd.moe import GpuMoeBlock
     from npu_amd.qwen_moe import _build_block
     if isinstance(moe, GpuMoeBlock):
@@ -383,12 +413,33 @@ def _moe_residual(g: dict, i: int, x: torch.Tensor, core, moe, cfg: Config) -> t
         nw = _f32_dev(core.post_norm)
         st = L.GmMoeLayer.from_buffer_copy(blk.struct)
         st.norm_w, st.norm_eps = L.ptr(nw), float(cfg.rms_eps)
-        g[key] = (st, nw)
-    st = g[key][0]
+        g[key] = (st, nw, L.lib().gm_moe_chain_fused(ctypes.byref(st), 1, 1) == 1 and bool(st.router_t))
+    return g[key][0], blk
+
+
+def _moe_link(g: dict, i: int, core, moe, cfg: Config):
+    """(struct, workspace) for a core layer to form layer i's MoE router inputs, or None
+    when the block does not fit the T = 1 accumulator kernels."""
+    st, blk = _moe_struct(g, i, core, moe, cfg)
+    return (st, blk.workspace(1)) if g[("moe", i)][2] else None
+
+
+def _moe_residual(g: dict, i: int, x: torch.Tensor, core, moe, cfg: Config, linked: bool = False) -> torch.Tensor:
+    """x + moe_forward(rms_norm(x, core.post_norm)) in one gm_moe_forward call (with the
+    residual flag), or, ``linked``, one gm_moe_forward_acc call on the router inputs the
+    core layer formed."""
+    from npu_amd import ops
+    st, blk = _moe_struct(g, i, core, moe, cfg)
     T, D = x.shape[1], x.shape[2]
     xf = x.reshape(T, D).contiguous()
     y = torch.empty_like(xf)
-    ops.moe_forward_raw(st, xf, y, blk.workspace(T), residual=True)
+    if linked:
+        ws = blk.workspace(1)
+        rc = L.lib().gm_moe_forward_acc(ctypes.byref(st), L.ptr(xf), L.ptr(y), L.GM_MOE_RESIDUAL, L.ptr(ws),
+                                        ws.numel(), L.stream_ptr())
+        L.check(rc, "gm_moe_forward_acc")
+    else:
+        ops.moe_forward_raw(st, xf, y, blk.workspace(T), residual=True)
     return y.view(1, T, D)
 
 

@@ -160,3 +160,36 @@ def test_core_layer_argument_errors_without_gpu():
     bad = L.GmSsmLayer.from_buffer_copy(s)
     bad.attn_norm = 260
     assert lib.gm_ssm_workspace_bytes(ctypes.byref(bad)) == 0 and "attn_norm" in L.last_error()
+
+
+def test_linked_core_moe_argument_errors_without_gpu():
+    """gm_attn_decode_moe / gm_ssm_decode_moe / gm_moe_forward_acc reject a MoE block that
+    does not fit the T = 1 accumulator kernels, lacks router_t, has another D, or comes
+    with a short workspace, before any launch."""
+    lib = L.lib()
+    s = L.GmSsmLayer(w_in=256, w_gate=256, w_out=256, alpha=256, beta=256, conv1d=256, a=256, dt_bias=256,
+                     ssm_norm=256, attn_norm=256, eps=1e-6, D=2048, n_k_heads=16, n_v_heads=32, d_state=128,
+                     conv_k=4)
+    m = lib.gm_ssm_workspace_bytes(ctypes.byref(s))
+    good = _layer(router_t=512)
+    n1 = lib.gm_moe_workspace_bytes(ctypes.byref(good), 1)
+    assert n1 > 0
+
+    def ssm(moe, ws_bytes=n1, moe_ws=1 << 22):
+        return lib.gm_ssm_decode_moe(ctypes.byref(s), 1024, 1 << 20, 4096, 1 << 21, 0, 1 << 23, m,
+                                     ctypes.byref(moe), moe_ws, ws_bytes, None)
+    assert ssm(_layer()) == L.GM_EINVAL and "router_t" in L.last_error()
+    assert ssm(_layer(router_t=512, D=1024)) == L.GM_EINVAL and "D=2048" in L.last_error()
+    assert ssm(_layer(router_t=512, k=4, FF=256)) == L.GM_EINVAL and "accumulator" in L.last_error()
+    assert ssm(good, ws_bytes=n1 - 256) == L.GM_EWORKSPACE
+    assert ssm(good, moe_ws=1024 + 16) == L.GM_EINVAL and "256-byte" in L.last_error()
+    a = L.GmAttnLayer(wqkv=256, wo=256, attn_norm=256, q_norm=256, k_norm=256, eps=1e-6, D=2048, n_head=16,
+                      n_head_kv=2, head_dim=256, rope_dim=64)
+    na = lib.gm_attn_workspace_bytes(ctypes.byref(a), 64)
+    rc = lib.gm_attn_decode_moe(ctypes.byref(a), 1024, 1 << 20, 4096, 4096, 0, 64, 256, 256, 0, 1 << 23, na,
+                                ctypes.byref(_layer()), 1 << 22, n1, None)
+    assert rc == L.GM_EINVAL and "router_t" in L.last_error()
+    rc = lib.gm_moe_forward_acc(ctypes.byref(_layer(router_t=512, k=4, FF=256)), 1024, 1 << 20, 0, 1 << 22, n1, None)
+    assert rc == L.GM_EINVAL and "accumulator" in L.last_error()
+    rc = lib.gm_moe_forward_acc(ctypes.byref(good), 1024, 1 << 20, 0, 1 << 22, n1 - 256, None)
+    assert rc == L.GM_EWORKSPACE

@@ -153,3 +153,61 @@ def test_decoder_forward_prefill_and_decode(gpu):
         ln, kv, st = QN.forward(model, [tok], start_pos=pos, kv_caches=kv, ssm_states=st)
         assert _rel(ln, lo) <= 2e-3, f"decode step {step}: logits rel {_rel(ln, lo):.2e}"
         pos += 1
+
+
+def test_decoder_linked_moe_router(gpu):
+    """Decode steps with every core layer linked to its MoE block (gm_attn_decode_moe /
+    gm_ssm_decode_moe form the block's router inputs, gm_moe_forward_acc runs it without the
+    router launch) against the same steps unlinked (gm_attn_decode / gm_ssm_decode, then
+    gm_moe_forward): top-k ids equal at every layer and step, logits rel <= 1e-5 (the same
+    router dot products added in another order), and both against the oracle decoder at
+    2e-3.  4 layers (three Gated DeltaNet, one attention), D = 512, MoE E = 64, k = 8,
+    FF = 512 (a block that fits the T = 1 accumulator kernels); a 3-token prompt, then 3
+    steps."""
+    print("decoder case: linked MoE router, 4 layers, prompt 3, 3 steps", flush=True)
+    ocfg, ncfg = _cfgs(True)
+    n_layer = 4
+    ncfg.n_layer, ncfg.is_attention = n_layer, [(i + 1) % 4 == 0 for i in range(n_layer)]
+    ncfg.n_expert, ncfg.n_expert_used, ncfg.d_expert_ff = 64, 8, 512
+    hs = [synth.host_moe_layer(700 + i, D=512, FF=512, E=64, k=8) for i in range(n_layer)]
+    ts = qwen_moe.SyntheticTensorStore(hs)
+    g = torch.Generator().manual_seed(11)
+    V = 1000
+    emb = torch.randn(V, 512, generator=g)
+    onorm = 1 + 0.1 * torch.randn(512, generator=g)
+    lm_head = _bf(torch.randn(V, 512, generator=g) * 0.05)
+    cores_o, cores_n = [], []
+    for i in range(n_layer):
+        if ncfg.is_attention[i]:
+            W = _attn_weights(ocfg, 40 + i)
+            cores_o.append(QC.AttnW(**W))
+            cores_n.append(QN.AttnLayer(i=i, **W))
+        else:
+            W = _ssm_weights(ocfg, 40 + i)
+            cores_o.append(QC.SSMW(**W))
+            cores_n.append(QN.SSMLayer(i=i, **W))
+    cos, sin = QC.build_partial_rope_cache(ocfg.rope_dim, 64, ocfg.rope_theta)
+    moes = [qwen_moe.MoELayer.load(ts, i) for i in range(n_layer)]
+    model = QN.Model(cfg=ncfg, token_embd=emb, output_norm=onorm, lm_head=lm_head,
+                     layers=[(cores_n[i], moes[i]) for i in range(n_layer)], rope_cos=cos, rope_sin=sin)
+    olayers = [(cores_o[i], OM.OracleLayer(hs[i])) for i in range(n_layer)]
+
+    def ids():
+        return [m.npu["moe_block"].stages(1)["topk_ids"].cpu().clone() for m in moes]
+    prompt = [5, 77, 901]
+    lo, oc = QC.decoder_forward(prompt, emb, olayers, onorm, lm_head, ocfg, cos, sin)
+    _, kv_u, st_u = QN.forward(model, prompt, link_moe=False)
+    _, kv_l, st_l = QN.forward(model, prompt, link_moe=True)      # T = 3: never linked
+    assert all(model.gpu[("moe", i)][2] for i in range(n_layer)), "a MoE block does not fit the linked path"
+    pos = len(prompt)
+    for step, tok in enumerate([int(lo[-1].argmax()), 3, 512]):
+        lo, oc = QC.decoder_forward([tok], emb, olayers, onorm, lm_head, ocfg, cos, sin, oc, pos)
+        lu, kv_u, st_u = QN.forward(model, [tok], start_pos=pos, kv_caches=kv_u, ssm_states=st_u, link_moe=False)
+        ids_u = ids()
+        ll, kv_l, st_l = QN.forward(model, [tok], start_pos=pos, kv_caches=kv_l, ssm_states=st_l, link_moe=True)
+        ids_l = ids()
+        for li in range(n_layer):
+            assert torch.equal(ids_l[li], ids_u[li]), f"step {step} layer {li}: linked ids differ"
+        assert _rel(ll, lu) <= 1e-5, f"step {step}: linked vs unlinked logits rel {_rel(ll, lu):.2e}"
+        assert _rel(ll, lo) <= 2e-3, f"step {step}: linked logits vs oracle rel {_rel(ll, lo):.2e}"
+        pos += 1
