@@ -155,21 +155,24 @@ def test_decoder_forward_prefill_and_decode(gpu):
         pos += 1
 
 
-def test_decoder_linked_moe_router(gpu):
+@pytest.mark.parametrize("router_f32,E,bias", [(False, 64, False), (True, 512, True)])
+def test_decoder_linked_moe_router(gpu, router_f32, E, bias):
     """Decode steps with every core layer linked to its MoE block (gm_attn_decode_moe /
     gm_ssm_decode_moe form the block's router inputs, gm_moe_forward_acc runs it without the
     router launch) against the same steps unlinked (gm_attn_decode / gm_ssm_decode, then
     gm_moe_forward): top-k ids equal at every layer and step, logits rel <= 1e-5 (the same
     router dot products added in another order), and both against the oracle decoder at
-    2e-3.  4 layers (three Gated DeltaNet, one attention), D = 512, MoE E = 64, k = 8,
-    FF = 512 (a block that fits the T = 1 accumulator kernels); a 3-token prompt, then 3
-    steps."""
-    print("decoder case: linked MoE router, 4 layers, prompt 3, 3 steps", flush=True)
+    2e-3.  4 layers (three Gated DeltaNet, one attention), D = 512, MoE k = 8, FF = 512 (a
+    block that fits the T = 1 accumulator kernels) with a bf16 router and E = 64, or an fp32
+    router with a bias and E = 512 (two accumulator positions per thread); a 3-token prompt,
+    then 3 steps."""
+    print(f"decoder case: linked MoE router, router_f32={router_f32} E={E} bias={bias}", flush=True)
     ocfg, ncfg = _cfgs(True)
     n_layer = 4
     ncfg.n_layer, ncfg.is_attention = n_layer, [(i + 1) % 4 == 0 for i in range(n_layer)]
-    ncfg.n_expert, ncfg.n_expert_used, ncfg.d_expert_ff = 64, 8, 512
-    hs = [synth.host_moe_layer(700 + i, D=512, FF=512, E=64, k=8) for i in range(n_layer)]
+    ncfg.n_expert, ncfg.n_expert_used, ncfg.d_expert_ff = E, 8, 512
+    hs = [synth.host_moe_layer(700 + i, D=512, FF=512, E=E, k=8, router_f32=router_f32, bias=bias)
+          for i in range(n_layer)]
     ts = qwen_moe.SyntheticTensorStore(hs)
     g = torch.Generator().manual_seed(11)
     V = 1000
