@@ -109,7 +109,7 @@ def variant_chain(request, gpu):
     return request.param, hosts, [GpuMoeBlock.from_host(h, device=gpu) for h in hosts]
 
 
-@pytest.mark.parametrize("T", [1, 8])
+@pytest.mark.parametrize("T", [1, 3, 8])
 def test_gm_moe_chain(gpu, variant_chain, T):
     name, hosts, blocks = variant_chain
     n = len(hosts)
