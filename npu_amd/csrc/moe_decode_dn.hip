@@ -286,11 +286,18 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
 
 // 64 rows of one down matrix for nm <= 8 member rows of hsrc (global rows
 // src[m] of h, where h_sh follows h), written to yp rows dst[m].
-// Rows [row0, row0 + 64 NTILE) of one down matrix for nm member rows of h
+// Rows [row0, row0 + kDnRows NTILE) of one down matrix for nm member rows of h
 // (h rows src[m] -> yp rows dst[m]): the members' h rows are loaded, then
-// every tile's raw rows (wave w, pass q of tile t -> row row0 + 64t + 16w + 4q
-// + (lane >> 4), 16 lanes per row); the members are staged in LDS as limb rows
-// while the weights are in flight, then the tiles are decoded as they land.
+// every tile's raw rows (wave w, pass q < kDnPasses of tile t -> row row0 +
+// kDnRows t + 4 kDnPasses w + 4q + (lane >> 4), 16 lanes per row); the members
+// are staged in LDS as limb rows while the weights are in flight, then the
+// tiles are decoded as they land.
+// Four passes (64-row tiles, 78 VGPRs, 6 waves per SIMD): 2.04 ms per B = 8 step,
+// against 2.15 ms with two and 2.51 ms with one (more blocks, each staging the
+// members' limb rows again).
+constexpr int kDnPasses = 4;
+constexpr int kDnRows = 16 * kDnPasses;                      // rows per tile (4 waves)
+
 template <int QTW, int FC, int NTILE>
 __device__ __forceinline__ void down_rows(const uint8_t* __restrict__ wbase, int D, int FF, int row0, int nm,
                                           const int (&src)[8], const int (&dst)[8], const float* __restrict__ h,
@@ -314,12 +321,12 @@ __device__ __forceinline__ void down_rows(const uint8_t* __restrict__ wbase, int
     hr[i] = h4[(int64_t)s * nqr + (c < nq ? c - m * nqr : 0)];
   }
   issue_fence();
-  RowFetch<QTW, FC> f[NTILE][4];
+  RowFetch<QTW, FC> f[NTILE][kDnPasses];
 #pragma unroll
   for (int t = 0; t < NTILE; ++t)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int row = row0 + 64 * t + wave * 16 + q * 4 + (lane >> 4);
+    for (int q = 0; q < kDnPasses; ++q) {
+      const int row = row0 + kDnRows * t + wave * 4 * kDnPasses + q * 4 + (lane >> 4);
       fetch_subs<QTW, 16, FC, true>(f[t][q], wbase + (int64_t)(row < D ? row : 0) * rb, lir, nsub);
     }
   issue_fence();
@@ -338,13 +345,13 @@ __device__ __forceinline__ void down_rows(const uint8_t* __restrict__ wbase, int
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kDnPasses; ++q) {
       opaque(f[t][q]);
       float part[8];
 #pragma unroll
       for (int m = 0; m < 8; ++m) part[m] = 0.f;
       dot_subs_i8<QTW, 16, FC, 8>(f[t][q], lir, nsub, hs, rbytes, idx, nm, tab, part);
-      const int row = row0 + 64 * t + wave * 16 + q * 4 + (lane >> 4);
+      const int row = row0 + kDnRows * t + wave * 4 * kDnPasses + q * 4 + (lane >> 4);
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         if (m < nm) {
@@ -357,9 +364,9 @@ __device__ __forceinline__ void down_rows(const uint8_t* __restrict__ wbase, int
   }
 }
 
-// Blocks [0, n_sh): the shared expert (all T tokens), dn_tiles(FC) 64-row
+// Blocks [0, n_sh): the shared expert (all T tokens), dn_tiles(FC) kDnRows-row
 // tiles each; blocks [n_sh, ...): unit (b - n_sh) / n_tg of the unique routed
-// experts.  Tiles per block: 4 / FC, so the raw rows of a block stay 64 VGPRs.
+// experts.
 constexpr int dn_tiles(int fc) { return 1; }
 
 template <int QTD, int QTS, int FC>
@@ -376,7 +383,7 @@ __global__ void __launch_bounds__(256) k_dec_down8(gm_moe_layer P, int T, const 
   const int tg = shared ? (int)blockIdx.x : (int)blockIdx.x - n_sh - u * n_tg;
   if (u > nu || (!shared && u == nu)) return;   // uniform per block
   constexpr int NT = dn_tiles(FC);
-  const int row0 = tg * 64 * NT;
+  const int row0 = tg * kDnRows * NT;
   uint32_t gw = 0;
   if constexpr (QTD == GM_QTYPE_IQ3_XXS || QTS == GM_QTYPE_IQ3_XXS) gw = gm_iq3_tab_load();
   int src[8], dst[8];
@@ -612,7 +619,7 @@ int launch_dn(const gm_moe_layer* P, const float* x, float* y, int T, int flags,
       return GM_OK;
     }
   }
-  const int n_tg = (D + 64 * dn_tiles(FC) - 1) / (64 * dn_tiles(FC));
+  const int n_tg = (D + kDnRows * dn_tiles(FC) - 1) / (kDnRows * dn_tiles(FC));
   const int n_sh = P->down_sh ? n_tg : 0;
   const int max_u = T * k < P->E ? T * k : P->E;
   const size_t smem = 8 * (size_t)gm_limb_row_bytes(FF) + GM_LSUB +

@@ -10,7 +10,7 @@
 // stage 3.
 //
 // T > 1: k_dec_route (one block) runs the per-token top-k and groups the
-// (token, slot) pairs by expert; k_dec_gateup8 then runs (unit, 16-row chunk)
+// (token, slot) pairs by expert; k_dec_gateup8 then runs (unit, 8-row chunk)
 // blocks, a unit being a unique routed expert over its member tokens only or
 // the shared expert over all T tokens, reading the limb rows of x that stage 1
 // wrote and the RMSNorm factors of the routing kernel.
@@ -476,8 +476,11 @@ __device__ __forceinline__ void gateup_rows(const uint8_t* __restrict__ gbase, c
 // ones); blocks [n_sh, ...): unit (b - n_sh) / n_rg of the unique routed
 // experts (members from the grouping table); 8 kGuPasses rows per block.  The
 // launcher sets n_sh = 0 when the shared expert is in another format, and
-// launches its blocks separately with that format.
-constexpr int kGuPasses = 2;
+// launches its blocks separately with that format.  One pass (8 rows) per
+// block: 84 VGPRs, 5 waves per SIMD, and twice the blocks of two passes, whose
+// last ones (the launch's tail, where few blocks still run) end sooner:
+// 2.07 -> 2.03 ms per B = 8 step.
+constexpr int kGuPasses = 1;
 
 template <int QT, int DC>
 __global__ void __launch_bounds__(256) k_dec_gateup8(gm_moe_layer P, const uint8_t* __restrict__ xl,
