@@ -1,11 +1,16 @@
 // MoE block, prefill path (T > 8 tokens): grouped dequant-GEMMs on MFMA.
 //
-//   1. k_pf_prep:     xn = rmsnorm(x) (or x) -> three bf16 planes whose sum is
-//                     xn to ~2^-27 (router operand) and an f16 copy (gate/up operand)
-//   2. k_pf_router:   logits = xn W^T (+ bias) and the shared scalar gate on
-//                     v_mfma_f32_16x16x32_bf16, one MFMA per plane: every
-//                     product of a bf16 weight and a bf16 plane is exact in fp32
-//   3. k_pf_topk sums the router partials, then dispatch (dispatch.hip):
+//   1. k_pf_prep_router, two roles in one launch:
+//      prep blocks:   xn = rmsnorm(x) (or x) -> an f16 copy (gate/up operand),
+//                     and each token's RMSNorm factor
+//      router blocks: partial router dot products of x w_norm over K ranges and
+//                     the shared scalar gate's on v_mfma_f32_16x16x32_bf16, x w_norm
+//                     split in registers into three bf16 planes whose sum is it
+//                     to ~2^-27, one MFMA per plane: every product of a bf16
+//                     weight and a bf16 plane is exact in fp32; the RMSNorm
+//                     factor multiplies the summed partials in step 3
+//   3. k_pf_topk sums the router partials (times the RMSNorm factor, + bias),
+//      then dispatch (dispatch.hip):
 //      histogram -> exclusive scan -> stable scatter of (token, slot) pairs by
 //      expert, the inverse permutation, and every expert's token list (and the
 //      shared expert's, which takes all T tokens) cut into segments of <= kSegTok
@@ -70,7 +75,7 @@ struct PfWs {
   int32_t* sorted;    // [P]
   int32_t* inv;       // [P]   position of pair p in sorted order
   int32_t* segs;      // [1 + 4 * max_seg]  n_seg, then (expert, start, n, unused)
-  uint16_t* xr;       // [3][T][D]  bf16 planes of xn (router operand)
+  float* rmsv;        // [T]        RMSNorm factor per token (1 without a norm), for k_pf_topk
   uint16_t* xh;       // [T][D]     f16 xn 2^s (gate/up operand)
   float* xsc;         // [T]        2^-s per token
   float* part;        // [kRouterSplit][T][ldp]  partial router dot products
@@ -119,7 +124,7 @@ PfWs pf_layout(const gm_moe_layer* L, int T, uint8_t* base, size_t* total) {
   w.sorted = reinterpret_cast<int32_t*>(take(P * 4));
   w.inv = reinterpret_cast<int32_t*>(take(P * 4));
   w.segs = reinterpret_cast<int32_t*>(take((1 + 4 * (size_t)max_segments(T, L->k, L->E)) * 4));
-  w.xr = reinterpret_cast<uint16_t*>(take(3 * (size_t)T * L->D * 2));
+  w.rmsv = reinterpret_cast<float*>(take((size_t)T * 4));
   w.xh = reinterpret_cast<uint16_t*>(take((size_t)T * L->D * 2));
   w.xsc = reinterpret_cast<float*>(take((size_t)T * 4));
   w.part = reinterpret_cast<float*>(take((size_t)kRouterSplit * T * router_ld(L) * 4));
@@ -147,13 +152,12 @@ __device__ __forceinline__ void xcd_tile(int b, int nrt, int& seg, int& rt) {
 }
 
 // ---------------------------------------------------------------- prep x
-// xn = (x * rms) * w (qwen/forward.py:58-61) or x; planes p0 = bf16(xn),
-// p1 = bf16(xn - p0), p2 = bf16(xn - p0 - p1) (each difference exact in fp32);
-// xh = f16(xn 2^s) with the per-token power of two that puts max |xn| in
-// [2^14, 2^15) (no f16 overflow whatever the input scale, and f16's 11 bits
-// for every value down to 2^-10 of the token's maximum; rows below 2^-100 are
-// scaled as if their maximum were 2^-100), and xsc[t] = 2^-s, which the
-// gate/up kernel multiplies into its sums.  One block per token.
+// xn = (x * rms) * w (qwen/forward.py:58-61) or x; xh = f16(xn 2^s) with the
+// per-token power of two that puts max |xn| in [2^14, 2^15) (no f16 overflow
+// whatever the input scale, and f16's 11 bits for every value down to 2^-10 of
+// the token's maximum; rows below 2^-100 are scaled as if their maximum were
+// 2^-100), xsc[t] = 2^-s, which the gate/up kernel multiplies into its sums,
+// and rmsv[t] = rms (1 without a norm).  One block per token.
 __device__ __forceinline__ float pf_block_max(float m, float* red4) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
@@ -168,26 +172,16 @@ __device__ __forceinline__ int pf_f16_shift(float m) {
   return 15 - E;
 }
 
-__device__ __forceinline__ void pf_put_planes(gm_f32x2 v, int sh, uint32_t& o0, uint32_t& o1, uint32_t& o2,
-                                              uint32_t& oh) {
-  const gm_bf16x2 b0 = __builtin_convertvector(v, gm_bf16x2);
-  const gm_f32x2 r0 = v - __builtin_convertvector(b0, gm_f32x2);
-  const gm_bf16x2 b1 = __builtin_convertvector(r0, gm_bf16x2);
-  const gm_f32x2 r1 = r0 - __builtin_convertvector(b1, gm_f32x2);
-  const gm_bf16x2 b2 = __builtin_convertvector(r1, gm_bf16x2);
-  o0 = __builtin_bit_cast(uint32_t, b0);
-  o1 = __builtin_bit_cast(uint32_t, b1);
-  o2 = __builtin_bit_cast(uint32_t, b2);
+__device__ __forceinline__ uint32_t pf_f16x2(gm_f32x2 v, int sh) {
   const gm_f32x2 vs = {__builtin_ldexpf(v.x, sh), __builtin_ldexpf(v.y, sh)};
-  oh = __builtin_bit_cast(uint32_t, __builtin_convertvector(vs, gm_f16x2));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(vs, gm_f16x2));
 }
 
-__global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, int T, int D,
-                                                 const float* __restrict__ norm_w, float eps,
-                                                 uint16_t* __restrict__ xr, uint16_t* __restrict__ xh,
-                                                 float* __restrict__ xsc, float* __restrict__ xn32) {
-  __shared__ float red[4], redm[4];
-  const int t = blockIdx.x;
+__device__ __forceinline__ void pf_prep_token(int t, const float* __restrict__ x, int D,
+                                              const float* __restrict__ norm_w, float eps,
+                                              uint16_t* __restrict__ xh, float* __restrict__ xsc,
+                                              float* __restrict__ xn32, float* __restrict__ rmsv, float* red,
+                                              float* redm) {
   const gm_f32x2* x2 = reinterpret_cast<const gm_f32x2*>(x + (int64_t)t * D);
   const int n2 = D >> 1;
   int sh;
@@ -225,21 +219,13 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
         m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
     }
     sh = pf_f16_shift(pf_block_max(m, redm));
-    uint2* q0 = reinterpret_cast<uint2*>(xr) + (int64_t)t * n4;
-    uint2* q1 = q0 + (int64_t)T * n4;
-    uint2* q2 = q1 + (int64_t)T * n4;
+    if (threadIdx.x == 0) rmsv[t] = rms;
     uint2* qh = reinterpret_cast<uint2*>(xh) + (int64_t)t * n4;
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int c = (int)threadIdx.x + 256 * i;
       if (c >= n4) break;
-      uint32_t o0[2], o1[2], o2[2], oh[2];
-      pf_put_planes(gm_f32x2{v[i].x, v[i].y}, sh, o0[0], o1[0], o2[0], oh[0]);
-      pf_put_planes(gm_f32x2{v[i].z, v[i].w}, sh, o0[1], o1[1], o2[1], oh[1]);
-      q0[c] = make_uint2(o0[0], o0[1]);
-      q1[c] = make_uint2(o1[0], o1[1]);
-      q2[c] = make_uint2(o2[0], o2[1]);
-      qh[c] = make_uint2(oh[0], oh[1]);
+      qh[c] = make_uint2(pf_f16x2(gm_f32x2{v[i].x, v[i].y}, sh), pf_f16x2(gm_f32x2{v[i].z, v[i].w}, sh));
       if (xn32) reinterpret_cast<gm_f32x4*>(xn32 + (int64_t)t * D)[c] = v[i];
     }
   } else {
@@ -261,14 +247,12 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
       rms = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)D + eps);
     }
     sh = pf_f16_shift(pf_block_max(m, redm) * rms);
-    uint32_t* p0 = reinterpret_cast<uint32_t*>(xr) + (int64_t)t * n2;
-    uint32_t* p1 = p0 + (int64_t)T * n2;
-    uint32_t* p2 = p1 + (int64_t)T * n2;
+    if (threadIdx.x == 0) rmsv[t] = rms;
     uint32_t* ph = reinterpret_cast<uint32_t*>(xh) + (int64_t)t * n2;
     for (int i = threadIdx.x; i < n2; i += 256) {
       gm_f32x2 v = x2[i];
       if (norm_w) { const gm_f32x2 w = w2[i]; v.x = (v.x * rms) * w.x; v.y = (v.y * rms) * w.y; }
-      pf_put_planes(v, sh, p0[i], p1[i], p2[i], ph[i]);
+      ph[i] = pf_f16x2(v, sh);
       if (xn32) reinterpret_cast<gm_f32x2*>(xn32 + (int64_t)t * D)[i] = v;
     }
   }
@@ -276,12 +260,15 @@ __global__ void __launch_bounds__(256) k_pf_prep(const float* __restrict__ x, in
 }
 
 // ---------------------------------------------------------------- router
-// Partial router dot products part[z][t][r] = xn[t] . W[r] over the z-th K range
-// of kr = 128 NK values (rows r < E of W and row E = the shared gate vector,
-// qwen/forward.py:599-600, 608).  Block: 64 rows x 16 tokens x one K range;
-// wave w takes the w-th quarter of the range for all four 16-row tiles, and
-// issues every operand load of its NK k-steps before its first MFMA (one
-// memory round trip).  The four waves' tiles are added in LDS in wave order.
+// Partial router dot products part[z][t][r] = (x[t] w_norm) . W[r] over the z-th
+// K range of kr = 128 NK values (rows r < E of W and row E = the shared gate
+// vector, qwen/forward.py:599-600, 608; the token's RMSNorm factor is applied to
+// the summed partials by k_pf_topk, so no block needs a whole row of x).  Block:
+// 64 rows x 16 tokens x one K range; wave w takes the w-th quarter of the range
+// for all four 16-row tiles, and issues every operand load of its NK k-steps (x,
+// the norm weights and the router rows) before its first MFMA (one memory round
+// trip); x w_norm is formed in fp32 and split into three bf16 planes in
+// registers.  The four waves' tiles are added in LDS in wave order.
 // MFMA operand layout (16x16x32): lane l holds row / column l % 16 at
 // k = 8 (l / 16) .. +7.
 
@@ -326,20 +313,21 @@ __device__ __forceinline__ void router_step(const gm_u32x4 (&a)[4][RF32 ? 2 : 1]
 }
 
 template <int NK, bool RF32>
-__global__ void __launch_bounds__(256) k_pf_router(const void* __restrict__ w, const void* __restrict__ wsh,
-                                                   const uint16_t* __restrict__ xr, int T, int D, int E, int ldp,
-                                                   float* __restrict__ part) {
-  __shared__ gm_f32x4 red[3][4][64];
+__device__ __forceinline__ void pf_router_block(int rb, int tb, int z, const void* __restrict__ w,
+                                                const void* __restrict__ wsh, const float* __restrict__ x,
+                                                const float* __restrict__ norm_w, int T, int D, int E, int ldp,
+                                                float* __restrict__ part, gm_f32x4 (*red)[4][64]) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, q = lane >> 4;
   const int nrows = E + (wsh ? 1 : 0);
-  const int r0 = blockIdx.x * 64;
-  const int tok = blockIdx.y * 16 + l16;
+  const int r0 = rb * 64;
+  const int tok = tb * 16 + l16;
   const int tokc = tok < T ? tok : T - 1;
-  const int k0 = (blockIdx.z * 4 + wave) * (32 * NK);
-  const int64_t plane = (int64_t)T * D / 8;                     // in 16-byte units
-  const gm_u32x4* brow = reinterpret_cast<const gm_u32x4*>(xr + (int64_t)tokc * D + k0 + 8 * q);
+  const int k0 = (z * 4 + wave) * (32 * NK);
+  const gm_f32x4* xrow = reinterpret_cast<const gm_f32x4*>(x + (int64_t)tokc * D + k0 + 8 * q);
+  const gm_f32x4* nrow = reinterpret_cast<const gm_f32x4*>((norm_w ? norm_w : x) + k0 + 8 * q);
   constexpr int RW = RF32 ? 2 : 1;                              // 16-byte loads per 8 weights
-  gm_u32x4 a[NK][4][RW], b[NK][3];
+  gm_u32x4 a[NK][4][RW];
+  gm_f32x4 xv[NK][2], nv[NK][2];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) {
     const int row = r0 + rt * 16 + l16;
@@ -353,12 +341,27 @@ __global__ void __launch_bounds__(256) k_pf_router(const void* __restrict__ w, c
 #pragma unroll
   for (int ks = 0; ks < NK; ++ks)
 #pragma unroll
-    for (int p = 0; p < 3; ++p) b[ks][p] = brow[p * plane + 4 * ks];
+    for (int h = 0; h < 2; ++h) {
+      xv[ks][h] = xrow[8 * ks + h];
+      nv[ks][h] = nrow[8 * ks + h];                             // x again without a norm: not used
+    }
   gm_f32x4 acc[4];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) acc[rt] = gm_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < NK; ++ks) router_step<RF32>(a[ks], b[ks], acc);
+  for (int ks = 0; ks < NK; ++ks) {
+    gm_u32x4 xw[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const gm_f32x4 v = norm_w ? xv[ks][h] * nv[ks][h] : xv[ks][h];
+      xw[h] = __builtin_bit_cast(gm_u32x4, v);
+    }
+    gm_bf16x8 pl[3];
+    split3_bf16(xw, pl);
+    const gm_u32x4 b[3] = {__builtin_bit_cast(gm_u32x4, pl[0]), __builtin_bit_cast(gm_u32x4, pl[1]),
+                           __builtin_bit_cast(gm_u32x4, pl[2])};
+    router_step<RF32>(a[ks], b, acc);
+  }
   if (wave > 0) {
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) red[wave - 1][rt][lane] = acc[rt];
@@ -369,7 +372,7 @@ __global__ void __launch_bounds__(256) k_pf_router(const void* __restrict__ w, c
   for (int v = 0; v < 3; ++v)
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) acc[rt] += red[v][rt][lane];
-  float* out = part + ((int64_t)blockIdx.z * T + tok) * ldp;
+  float* out = part + ((int64_t)z * T + tok) * ldp;
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt) {
     const int row = r0 + rt * 16 + 4 * q;
@@ -381,19 +384,42 @@ __global__ void __launch_bounds__(256) k_pf_router(const void* __restrict__ w, c
   }
 }
 
-// One wave per token: logits = sum of the nsplit <= NZ partials (fixed order)
-// + bias, the shared gate sigmoid, and the top-k (ties -> lower id) with
+// Blocks [0, n_rt): the router blocks (row block, token tile, K range) = (b %
+// nrb, b / nrb % ntb, b / (nrb ntb)); blocks [n_rt, n_rt + T): the prep of
+// token b - n_rt.  The two roles share nothing: the launch replaces a prep
+// launch followed by a router launch.
+template <int NK, bool RF32>
+__global__ void __launch_bounds__(256) k_pf_prep_router(const void* __restrict__ w, const void* __restrict__ wsh,
+                                                        const float* __restrict__ x, const float* __restrict__ norm_w,
+                                                        float eps, int T, int D, int E, int ldp,
+                                                        float* __restrict__ part, int nrb, int ntb, int n_rt,
+                                                        uint16_t* __restrict__ xh, float* __restrict__ xsc,
+                                                        float* __restrict__ xn32, float* __restrict__ rmsv) {
+  __shared__ gm_f32x4 red[3][4][64];
+  __shared__ float pred[4], predm[4];
+  const int b = blockIdx.x;
+  if (b >= n_rt) {                                              // uniform per block
+    pf_prep_token(b - n_rt, x, D, norm_w, eps, xh, xsc, xn32, rmsv, pred, predm);
+    return;
+  }
+  pf_router_block<NK, RF32>(b % nrb, (b / nrb) % ntb, b / (nrb * ntb), w, wsh, x, norm_w, T, D, E, ldp, part, red);
+}
+
+// One wave per token: logits = the token's RMSNorm factor x the sum of the
+// nsplit <= NZ partials (fixed order) + bias, the shared gate sigmoid, and the top-k (ties -> lower id) with
 // renormalised softmax weights (qwen/forward.py:609-611).  Every partial is
 // loaded (clamped index) before any is summed.
 template <int MAXV, int NZ>
 __global__ void __launch_bounds__(256) k_pf_topk(const float* __restrict__ part, int ldp, int nsplit, int T, int E, int k,
                                                  int has_gate, const float* __restrict__ bias,
+                                                 const float* __restrict__ rmsv,
                                                  float* __restrict__ logits, float* __restrict__ shg,
                                                  int32_t* __restrict__ ids, float* __restrict__ wts) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (t >= T) return;
   const int64_t zs = (int64_t)T * ldp;
   const float* pt = part + (int64_t)t * ldp;
+  const float rms = rmsv[t];
   float v[MAXV], pv[MAXV][NZ], pg[NZ];
   int ix[MAXV];
 #pragma unroll
@@ -413,14 +439,14 @@ __global__ void __launch_bounds__(256) k_pf_topk(const float* __restrict__ part,
     float acc = 0.f;
 #pragma unroll
     for (int z = 0; z < NZ; ++z) acc += z < nsplit ? pv[i][z] : 0.f;
-    v[i] = acc + (bias ? bias[r] : 0.f);
+    v[i] = rms * acc + (bias ? bias[r] : 0.f);
     if (ix[i] < E) logits[(int64_t)t * E + ix[i]] = v[i];
   }
   if (lane == 0) {                                          // no gate row: the shared expert is ungated
     float g = 0.f;
 #pragma unroll
     for (int z = 0; z < NZ; ++z) g += z < nsplit ? pg[z] : 0.f;
-    shg[t] = has_gate ? gm_sigmoid(g) : 1.f;
+    shg[t] = has_gate ? gm_sigmoid(rms * g) : 1.f;
   }
   int id;
   float wt;
@@ -1249,22 +1275,21 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
   const bool sh_f32 = sh_apart && !sh_i8;
   const size_t P = (size_t)T * k;
   const int nrows = E + (L->sh_gate_inp ? 1 : 0);
-  hipLaunchKernelGGL(k_pf_prep, dim3(T), dim3(256), 0, s, x, T, D, L->norm_w, L->norm_eps, w.xr, w.xh, w.xsc,
-                     sh_f32 ? w.xn : nullptr);
-  GM_TRY(hipGetLastError());
   const int ldp = router_ld(L);
   const int nsplit = router_split(D);
   {
-    const dim3 g((nrows + 63) / 64, (T + 15) / 16, nsplit);
+    const int nrb = (nrows + 63) / 64, ntb = (T + 15) / 16, n_rt = nrb * ntb * nsplit;
+    const dim3 g((unsigned)(n_rt + T));
     const bool f32 = L->q_router == GM_QTYPE_F32;
-    if (router_krange(D) == 512 && f32)
-      hipLaunchKernelGGL((k_pf_router<4, true>), g, dim3(256), 0, s, L->router, L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
-    else if (router_krange(D) == 512)
-      hipLaunchKernelGGL((k_pf_router<4, false>), g, dim3(256), 0, s, L->router, L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
-    else if (f32)
-      hipLaunchKernelGGL((k_pf_router<2, true>), g, dim3(256), 0, s, L->router, L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
-    else
-      hipLaunchKernelGGL((k_pf_router<2, false>), g, dim3(256), 0, s, L->router, L->sh_gate_inp, w.xr, T, D, E, ldp, w.part);
+    float* xn32 = sh_f32 ? w.xn : nullptr;
+#define GM_PR(NK, F32)                                                                                       \
+  hipLaunchKernelGGL((k_pf_prep_router<NK, F32>), g, dim3(256), 0, s, L->router, L->sh_gate_inp, x, L->norm_w, \
+                     L->norm_eps, T, D, E, ldp, w.part, nrb, ntb, n_rt, w.xh, w.xsc, xn32, w.rmsv)
+    if (router_krange(D) == 512 && f32) GM_PR(4, true);
+    else if (router_krange(D) == 512) GM_PR(4, false);
+    else if (f32) GM_PR(2, true);
+    else GM_PR(2, false);
+#undef GM_PR
   }
   GM_TRY(hipGetLastError());
   {
@@ -1272,19 +1297,19 @@ int prefill_t(const gm_moe_layer* L, const float* x, float* y, int T, int flags,
     const dim3 g((T + 3) / 4);
     if (E <= 256 && nsplit <= 4)
       hipLaunchKernelGGL((k_pf_topk<4, 4>), g, dim3(256), 0, s, w.part, ldp, nsplit, T, E, k, hg, L->router_bias,
-                         logits, shg, ids, wts);
+                         w.rmsv, logits, shg, ids, wts);
     else if (E <= 256 && nsplit <= 8)
       hipLaunchKernelGGL((k_pf_topk<4, 8>), g, dim3(256), 0, s, w.part, ldp, nsplit, T, E, k, hg, L->router_bias,
-                         logits, shg, ids, wts);
+                         w.rmsv, logits, shg, ids, wts);
     else if (E <= 256)
       hipLaunchKernelGGL((k_pf_topk<4, 16>), g, dim3(256), 0, s, w.part, ldp, nsplit, T, E, k, hg, L->router_bias,
-                         logits, shg, ids, wts);
+                         w.rmsv, logits, shg, ids, wts);
     else if (nsplit <= 8)
       hipLaunchKernelGGL((k_pf_topk<8, 8>), g, dim3(256), 0, s, w.part, ldp, nsplit, T, E, k, hg, L->router_bias,
-                         logits, shg, ids, wts);
+                         w.rmsv, logits, shg, ids, wts);
     else
       hipLaunchKernelGGL((k_pf_topk<8, 16>), g, dim3(256), 0, s, w.part, ldp, nsplit, T, E, k, hg, L->router_bias,
-                         logits, shg, ids, wts);
+                         w.rmsv, logits, shg, ids, wts);
   }
   GM_TRY(hipGetLastError());
   if (int rc = gm_launch_dispatch_seg(ids, T, k, E, w.counts, w.offsets, w.sorted, w.inv, w.segs, kSegTok,
