@@ -26,6 +26,8 @@
 //                    d = (v - S^T k) beta, S += k d^T, o = S^T q; the state
 //                    [Hv][Sk][Sv] (the reference's layout) updated in place
 //   k_ssm_gnorm      rmsnorm(o_head, ssm_norm) * silu(z)
+//   (k_ssm_rec_gn    both in one launch, one block per V head, for d_state
+//                    64 and 128)
 //   mv_bf16 (+ x)    y = W_out o (+ x)
 // Linked to the following MoE block (gm_attn_decode_moe / gm_ssm_decode_moe):
 // the first launch also clears that block's T = 1 router accumulators, and the
@@ -328,6 +330,74 @@ __global__ void __launch_bounds__(256) k_ssm_rec(float* __restrict__ S, const fl
   }
 }
 
+// The delta rule of k_ssm_rec and the gated norm of k_ssm_gnorm for a whole V
+// head in one block (Sk == Sv == SV, blockDim = 1024 = SV columns x KG row
+// groups of SPT state rows): the head's SV outputs o end up in the first SV
+// threads, which form rmsnorm(o, ssm_norm) * silu(z) directly.
+template <int SV>
+__global__ void __launch_bounds__(1024) k_ssm_rec_gn(float* __restrict__ S, const float* __restrict__ conv,
+                                                     const float* __restrict__ gb, int Hk, int Hv,
+                                                     const float* __restrict__ nw, const float* __restrict__ z,
+                                                     float eps, float* __restrict__ out) {
+  constexpr int KG = 1024 / SV, SPT = SV / KG;
+  __shared__ float red[KG][SV + 1];
+  __shared__ float dsh[SV];
+  __shared__ float wred[SV / 64];
+  const int hv = blockIdx.x, col = threadIdx.x % SV, kg = threadIdx.x / SV;
+  const int hk = hv % Hk, Ck = Hk * SV;
+  const float* q = conv + (size_t)hk * SV;
+  const float* k = conv + (size_t)Ck + (size_t)hk * SV;
+  const float vv = conv[(size_t)2 * Ck + (size_t)hv * SV + col];
+  const float decay = expf(gb[hv]), bt = gb[Hv + hv];
+  const size_t oi = (size_t)hv * SV + col;
+  const float zi = kg == 0 ? z[oi] : 0.f, nwc = kg == 0 ? nw[col] : 0.f;
+  float* Sc = S + (size_t)hv * SV * SV + col;
+  float s[SPT], kk[SPT], qq[SPT];
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+    const int r = kg * SPT + j;
+    s[j] = Sc[(size_t)r * SV] * decay;
+    kk[j] = k[r];
+    qq[j] = q[r];
+  }
+  float p = 0.f;
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) p = fmaf(s[j], kk[j], p);
+  red[kg][col] = p;
+  __syncthreads();
+  if (kg == 0) {
+    float sk = 0.f;
+    for (int g = 0; g < KG; ++g) sk += red[g][col];
+    dsh[col] = (vv - sk) * bt;
+  }
+  __syncthreads();
+  const float d = dsh[col];
+  p = 0.f;
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+    s[j] = fmaf(kk[j], d, s[j]);
+    Sc[(size_t)(kg * SPT + j) * SV] = s[j];
+    p = fmaf(s[j], qq[j], p);
+  }
+  __syncthreads();
+  red[kg][col] = p;
+  __syncthreads();
+  float ov = 0.f;
+  if (kg == 0)
+    for (int g = 0; g < KG; ++g) ov += red[g][col];
+  // the first SV threads (SV / 64 whole waves) hold the head's outputs
+  const float sq = gm_wave_sum64(kg == 0 ? ov * ov : 0.f);
+  if ((threadIdx.x & 63) == 0 && (int)threadIdx.x < SV) wred[threadIdx.x >> 6] = sq;
+  __syncthreads();
+  if (kg == 0) {
+    float ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < SV / 64; ++w) ss += wred[w];
+    const float r = 1.0f / sqrtf(ss / (float)SV + eps);
+    out[oi] = ((ov * r) * nwc) * (zi / (1.0f + expf(-zi)));
+  }
+}
+
 // rmsnorm(o_head, ssm_norm) * silu(z) per V head (blockDim = Sv).
 __global__ void k_ssm_gnorm(const float* __restrict__ o, const float* __restrict__ nw, const float* __restrict__ z,
                             int Sv, float eps, float* __restrict__ out) {
@@ -425,6 +495,17 @@ int gm_ssm_run(const gm_ssm_layer* L, const float* x, float* y, float* conv_stat
   hipLaunchKernelGGL(k_ssm_conv_ab, dim3(nconv + nab), dim3(Sk), 0, s, mixed, L->conv1d, conv_state, L->conv_k, Hk,
                      Sk, L->eps, conv, nconv, L->alpha, L->beta, L->dt_bias, L->a, x, L->attn_norm, D, Hv, gb);
   GM_TRY(hipGetLastError());
+  if (Sk == Sv && (Sv == 64 || Sv == 128)) {         // delta rule and gated norm in one launch
+    if (Sv == 128)
+      hipLaunchKernelGGL(k_ssm_rec_gn<128>, dim3(Hv), dim3(1024), 0, s, rec_state, conv, gb, Hk, Hv, L->ssm_norm, z,
+                         L->eps, o2);
+    else
+      hipLaunchKernelGGL(k_ssm_rec_gn<64>, dim3(Hv), dim3(1024), 0, s, rec_state, conv, gb, Hk, Hv, L->ssm_norm, z,
+                         L->eps, o2);
+    GM_TRY(hipGetLastError());
+    return gm_launch_mv_bf16_add(static_cast<const uint16_t*>(L->w_out), D, di, o2, y,
+                                 (flags & GM_MOE_RESIDUAL) ? x : nullptr, s, moe);
+  }
   const dim3 g(Hv, Sv / 32);
   switch (Sk / 8) {
     case 8: hipLaunchKernelGGL(k_ssm_rec<8>, g, dim3(256), 0, s, rec_state, conv, gb, Hk, Hv, Sk, Sv, o); break;
