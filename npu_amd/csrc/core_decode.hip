@@ -11,7 +11,9 @@
 //   k_attn_prep      per head: RMSNorm of q / k over head_dim, partial RoPE at
 //                    pos; k and v written to the caches at row pos
 //   k_attn_part      per (q head, chunk of cached positions): online softmax
-//                    partials (max, sum, weighted v) of q . k / sqrt(Dh)
+//                    partials (max, sum, weighted v) of q . k / sqrt(Dh); for
+//                    rope_dim <= 64 (a power of two) it also does k_attn_prep's
+//                    work and k_attn_prep is not launched
 //   k_attn_combine   per q head: the partials merged, times sigmoid(gate)
 //   mv_bf16 (+ x)    y = Wo out (+ x)
 // Gated DeltaNet, one token (gm_ssm_decode):
@@ -113,18 +115,74 @@ __global__ void k_attn_prep(const float* __restrict__ qkv, const float* __restri
 // s = (q . k) / sqrt(Dh) (a wave sum), then the online softmax update
 // m' = max(m, s), l = l e^(m - m') + e^(s - m'), acc = acc e^(m - m') + e^(s - m') v.
 // The 4 waves' states are merged in LDS; part[hq][chunk] = {m, l, acc[Dh]}.
+//
+// With ROPE the launch also does k_attn_prep's work (rope_dim rd <= 64, rd / 2
+// a power of two): every wave forms its head's q from qkv itself, the blocks
+// of the last chunk form the new k and v row at pos = n - 1 and use it for
+// that position instead of the cache, and the first q head of each kv group
+// writes it to the caches.
+struct AttnRope {
+  const float* qkv;
+  const float* q_norm;
+  const float* k_norm;
+  float eps;
+  int rd;
+  const float* cosr;   // at pos
+  const float* sinr;
+};
+
+// One head row of qkv (DV values per lane), RMSNorm'd with nw over 64 DV
+// values, then the partial RoPE on dims i < rd (partner i ^ (rd / 2), in the
+// same wave); as k_attn_prep forms it.
 template <int DV>
-__global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ qr, const float* __restrict__ kc,
-                                                   const float* __restrict__ vc, int Hq, int Hkv, int n,
-                                                   float scale, float* __restrict__ part, int ld) {
+__device__ __forceinline__ void rope_head(const float* __restrict__ src, const float* __restrict__ nw,
+                                          const AttnRope& rp, float (&out)[DV]) {
+  const int lane = threadIdx.x & 63;
+  float v[DV];
+#pragma unroll
+  for (int d = 0; d < DV; ++d) v[d] = src[lane + 64 * d];
+  float ss = 0.f;
+#pragma unroll
+  for (int d = 0; d < DV; ++d) ss = fmaf(v[d], v[d], ss);
+  const float r = 1.0f / sqrtf(gm_wave_sum64(ss) / (float)(64 * DV) + rp.eps);
+#pragma unroll
+  for (int d = 0; d < DV; ++d) out[d] = (v[d] * r) * nw[lane + 64 * d];
+  const int h = rp.rd >> 1;
+  const float other = __shfl_xor(out[0], h, 64);
+  if (lane < rp.rd) out[0] = out[0] * rp.cosr[lane] + (lane < h ? -other : other) * rp.sinr[lane];
+}
+
+template <int DV, bool ROPE>
+__global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ qr, float* __restrict__ kc,
+                                                   float* __restrict__ vc, int Hq, int Hkv, int n,
+                                                   float scale, float* __restrict__ part, int ld, AttnRope rp) {
   __shared__ float ms[4], ls[4];
   __shared__ float accs[4][64 * DV];
   const int hq = blockIdx.x, chunk = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int Dh = 64 * DV, hk = hq / (Hq / Hkv), c0 = chunk * kAttnChunk;
   const int c1 = min(c0 + kAttnChunk, n);
-  float q[DV], acc[DV];
+  float q[DV], acc[DV], kp[DV], vp[DV];
 #pragma unroll
-  for (int d = 0; d < DV; ++d) { q[d] = qr[(size_t)Dh * hq + lane + 64 * d]; acc[d] = 0.f; }
+  for (int d = 0; d < DV; ++d) { acc[d] = 0.f; kp[d] = 0.f; vp[d] = 0.f; }
+  const bool last = c1 == n;                                     // this chunk holds pos = n - 1
+  if constexpr (ROPE) {
+    rope_head<DV>(rp.qkv + (size_t)2 * Dh * hq, rp.q_norm, rp, q);
+    if (last) {
+      const float* kv0 = rp.qkv + (size_t)2 * Dh * Hq;
+      rope_head<DV>(kv0 + (size_t)Dh * hk, rp.k_norm, rp, kp);
+#pragma unroll
+      for (int d = 0; d < DV; ++d) vp[d] = kv0[(size_t)Dh * Hkv + (size_t)Dh * hk + lane + 64 * d];
+      if (hq % (Hq / Hkv) == 0 && wave == 0) {
+        float* kr = kc + ((size_t)(n - 1) * Hkv + hk) * Dh;
+        float* vr = vc + ((size_t)(n - 1) * Hkv + hk) * Dh;
+#pragma unroll
+        for (int d = 0; d < DV; ++d) { kr[lane + 64 * d] = kp[d]; vr[lane + 64 * d] = vp[d]; }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int d = 0; d < DV; ++d) q[d] = qr[(size_t)Dh * hq + lane + 64 * d];
+  }
   float m = -__builtin_inff(), l = 0.f;
   // kAttnNB positions per round, every k / v load of the round issued before
   // the first use; positions past c1 reload the last one and leave the state
@@ -142,6 +200,10 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ qr,
 #pragma unroll
     for (int j = 0; j < kAttnNB; ++j) {
       const bool live = t0 + 4 * j < c1;                         // wave-uniform
+      if (ROPE && t0 + 4 * j == n - 1) {                        // the new row, formed above
+#pragma unroll
+        for (int d = 0; d < DV; ++d) { kv[j][d] = kp[d]; vv[j][d] = vp[d]; }
+      }
       float s = 0.f;
 #pragma unroll
       for (int d = 0; d < DV; ++d) s = fmaf(q[d], kv[j][d], s);
@@ -440,19 +502,34 @@ int gm_attn_run(const gm_attn_layer* L, const float* x, float* y, float* kc, flo
                                        L->eps, qkv, nullptr, s, moe ? moe->acc : nullptr,
                                        moe ? GM_ACC_COPIES * moe->ld : 0))
     return rc;
-  hipLaunchKernelGGL(k_attn_prep, dim3(Hq + Hkv), dim3(Dh), (Dh + 16) * sizeof(float), s, qkv, L->q_norm,
-                     L->k_norm, L->eps, Hq, Hkv, Dh, rd, cosr + (size_t)pos * rd, sinr + (size_t)pos * rd, qr,
-                     kc + (size_t)pos * Hkv * Dh, vc + (size_t)pos * Hkv * Dh);
-  GM_TRY(hipGetLastError());
   const int n = pos + 1, nch = (n + kAttnChunk - 1) / kAttnChunk;
   const float scale = 1.0f / sqrtf((float)Dh);
   const dim3 g(Hq, nch);
-  switch (Dh / 64) {
-    case 1: hipLaunchKernelGGL(k_attn_part<1>, g, dim3(256), 0, s, qr, kc, vc, Hq, Hkv, n, scale, part, lay.nch); break;
-    case 2: hipLaunchKernelGGL(k_attn_part<2>, g, dim3(256), 0, s, qr, kc, vc, Hq, Hkv, n, scale, part, lay.nch); break;
-    case 4: hipLaunchKernelGGL(k_attn_part<4>, g, dim3(256), 0, s, qr, kc, vc, Hq, Hkv, n, scale, part, lay.nch); break;
-    default: hipLaunchKernelGGL(k_attn_part<8>, g, dim3(256), 0, s, qr, kc, vc, Hq, Hkv, n, scale, part, lay.nch); break;
+  float* kpos = kc + (size_t)pos * Hkv * Dh;
+  float* vpos = vc + (size_t)pos * Hkv * Dh;
+  const float* cp = cosr + (size_t)pos * rd;
+  const float* sp = sinr + (size_t)pos * rd;
+  // q / k norm and RoPE inside the partial launch when the rotated pairs sit in one wave
+  const bool fused = rd >= 2 && rd <= 64 && ((rd >> 1) & ((rd >> 1) - 1)) == 0;
+  const AttnRope rp{qkv, L->q_norm, L->k_norm, L->eps, rd, cp, sp};
+  if (!fused) {
+    hipLaunchKernelGGL(k_attn_prep, dim3(Hq + Hkv), dim3(Dh), (Dh + 16) * sizeof(float), s, qkv, L->q_norm,
+                       L->k_norm, L->eps, Hq, Hkv, Dh, rd, cp, sp, qr, kpos, vpos);
+    GM_TRY(hipGetLastError());
   }
+#define GM_AP(DV)                                                                                              \
+  if (fused) hipLaunchKernelGGL((k_attn_part<DV, true>), g, dim3(256), 0, s, qr, kc, vc, Hq, Hkv, n, scale, part, \
+                                lay.nch, rp);                                                                  \
+  else hipLaunchKernelGGL((k_attn_part<DV, false>), g, dim3(256), 0, s, qr, kc, vc, Hq, Hkv, n, scale, part,    \
+                          lay.nch, rp);                                                                        \
+  break;
+  switch (Dh / 64) {
+    case 1: GM_AP(1)
+    case 2: GM_AP(2)
+    case 4: GM_AP(4)
+    default: GM_AP(8)
+  }
+#undef GM_AP
   GM_TRY(hipGetLastError());
   hipLaunchKernelGGL(k_attn_combine, dim3(Hq), dim3(Dh), 0, s, part, lay.nch, nch, qkv, Dh, out);
   GM_TRY(hipGetLastError());
