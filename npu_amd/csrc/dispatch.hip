@@ -34,6 +34,7 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ i
   __syncthreads();
   const int chunk = (P + kWaves - 1) / kWaves;
   const int p0 = wave * chunk, p1 = min(P, p0 + chunk);
+  int e0[kBatch];                            // the first batch's ids, kept for the scatter
   for (int b = p0; b < p1; b += 64 * kBatch) {
     int eb[kBatch];                          // every load of the batch before the first use
 #pragma unroll
@@ -42,8 +43,10 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ i
       eb[j] = p < p1 ? ids[p] : -1;
     }
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j)
+    for (int j = 0; j < kBatch; ++j) {
+      if (b == p0) e0[j] = eb[j];
       if (eb[j] >= 0 && eb[j] < E) atomicAdd(&cnt[wave * E + eb[j]], 1);
+    }
   }
   __syncthreads();
   // per-expert totals (thread e) and their exclusive scan across the block
@@ -86,7 +89,7 @@ __global__ void __launch_bounds__(1024) k_dispatch(const int32_t* __restrict__ i
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       const int p = b0 + 64 * j + lane;
-      eb[j] = p < p1 ? ids[p] : -1;
+      eb[j] = b0 == p0 ? e0[j] : p < p1 ? ids[p] : -1;
     }
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
