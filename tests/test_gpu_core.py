@@ -111,6 +111,35 @@ def test_ssm_decode_steps(gpu, small):
     assert _rel(yn - x1.to(gpu), yo) <= 1e-4 and _rel(nst2[1], ost2[1]) <= 1e-4
 
 
+def test_core_layers_general_paths(gpu):
+    """The shapes the launch merges leave on their own kernels: a rope_dim above 64 whose half
+    is no power of two (k_attn_prep before the partials) and d_state 256 (the recurrence in
+    32-column blocks, then the gated norm), step by step against the oracle."""
+    print("core general-path case: rope_dim 96, d_state 256", flush=True)
+    kw = dict(d_model=512, n_head=4, n_head_kv=2, head_dim=128, rope_dim=96, rope_theta=1e6,
+              ssm_d_inner=1024, ssm_d_state=256, ssm_n_k_heads=2, ssm_n_v_heads=4)
+    ocfg, ncfg = QC.CoreCfg(**kw), QN.Config(**kw)
+    W = _attn_weights(ocfg, 11)
+    OL, NL = QC.AttnW(**W), QN.AttnLayer(i=0, **W)
+    steps = 66                                            # past one 64-position chunk
+    cos, sin = QC.build_partial_rope_cache(ocfg.rope_dim, 80, ocfg.rope_theta)
+    xs = torch.randn(1, steps, ocfg.d_model, generator=torch.Generator().manual_seed(12))
+    ocache, ncache = None, None
+    for t in range(steps):
+        yo, ocache = QC.attn_forward(xs[:, t:t + 1], OL, ocfg, cos, sin, ocache, t)
+        yn, ncache = QN.attn_forward(xs[:, t:t + 1].to(gpu), NL, ncfg, cos, sin, ncache, t)
+        assert _rel(yn, yo) <= 1e-4, f"attention step {t}: rel {_rel(yn, yo):.2e}"
+    W = _ssm_weights(ocfg, 13)
+    OS, NS = QC.SSMW(**W), QN.SSMLayer(i=0, **W)
+    xs = torch.randn(1, 6, ocfg.d_model, generator=torch.Generator().manual_seed(14))
+    ost, nst = None, None
+    for t in range(6):
+        yo, ost = QC.ssm_forward(xs[:, t:t + 1], OS, ocfg, ost)
+        yn, nst = QN.ssm_forward(xs[:, t:t + 1].to(gpu), NS, ncfg, nst)
+        assert _rel(yn, yo) <= 1e-4, f"ssm step {t}: rel {_rel(yn, yo):.2e}"
+        assert _rel(nst[1], ost[1]) <= 1e-4, f"ssm step {t}: recurrent state rel {_rel(nst[1], ost[1]):.2e}"
+
+
 def test_decoder_forward_prefill_and_decode(gpu):
     """A 4-layer model (three Gated DeltaNet layers and one attention layer, the reference
     model's pattern; D = 512, MoE E = 16, k = 4, FF = 256; vocab 1000): a 5-token prompt,
