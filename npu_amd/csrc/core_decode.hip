@@ -68,8 +68,10 @@ __global__ void __launch_bounds__(256) k_rms_row(const float* __restrict__ x, co
   x += (size_t)blockIdx.x * D;
   y += (size_t)blockIdx.x * D;
   float ss = 0.f;
+#pragma unroll 8
   for (int i = threadIdx.x; i < D; i += 256) ss = fmaf(x[i], x[i], ss);
   const float r = 1.0f / sqrtf(block_sum(ss, red) / (float)D + eps);
+#pragma unroll 8
   for (int i = threadIdx.x; i < D; i += 256) y[i] = (x[i] * r) * w[i];
 }
 
@@ -284,12 +286,25 @@ __global__ void __launch_bounds__(256) k_ssm_conv_ab(const float* __restrict__ m
     const int c = blockIdx.x * Sk + threadIdx.x, g = blockIdx.x;
     float* st = state + (size_t)c * (ck - 1);
     const float* wc = w + (size_t)c * ck;
+    // the channel's weights and state in registers, every load issued before the
+    // first use (ck <= 8; indices past the kernel reload the last entry)
+    constexpr int KMAX = 8;
     const float xin = mixed[c];
-    float acc = 0.f;
-    for (int j = 0; j < ck - 1; ++j) acc = fmaf(wc[j], st[j], acc);
-    acc = fmaf(wc[ck - 1], xin, acc);
-    for (int j = 0; j + 1 < ck - 1; ++j) st[j] = st[j + 1];
-    if (ck > 1) st[ck - 2] = xin;
+    float wv[KMAX], sv[KMAX - 1];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) wv[j] = wc[j < ck ? j : ck - 1];
+#pragma unroll
+    for (int j = 0; j < KMAX - 1; ++j) sv[j] = ck > 1 ? st[j < ck - 1 ? j : ck - 2] : 0.f;
+    float acc = 0.f, wl = wv[0];
+#pragma unroll
+    for (int j = 0; j < KMAX - 1; ++j)
+      if (j < ck - 1) acc = fmaf(wv[j], sv[j], acc);
+#pragma unroll
+    for (int j = 1; j < KMAX; ++j) wl = j == ck - 1 ? wv[j] : wl;
+    acc = fmaf(wl, xin, acc);
+#pragma unroll
+    for (int j = 0; j < KMAX - 1; ++j)
+      if (j < ck - 1) st[j] = j + 1 < ck - 1 ? sv[j + 1] : xin;
     float v = acc / (1.0f + expf(-acc));
     if (g < 2 * Hk) {                                            // block-uniform
       const float ss = block_sum(v * v, red);
