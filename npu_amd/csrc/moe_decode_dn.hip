@@ -294,7 +294,7 @@ __global__ void __launch_bounds__(576) k_dec_down1(gm_moe_layer P, const float* 
 // tiles are decoded as they land.
 // Four passes (64-row tiles, 78 VGPRs, 6 waves per SIMD): 2.04 ms per B = 8 step,
 // against 2.15 ms with two and 2.51 ms with one (more blocks, each staging the
-// members' limb rows again).
+// members' limb rows again), and 2.16 ms with eight (136 VGPRs, 3 waves per SIMD).
 constexpr int kDnPasses = 4;
 constexpr int kDnRows = 16 * kDnPasses;                      // rows per tile (4 waves)
 
