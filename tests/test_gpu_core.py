@@ -111,6 +111,24 @@ def test_ssm_decode_steps(gpu, small):
     assert _rel(yn - x1.to(gpu), yo) <= 1e-4 and _rel(nst2[1], ost2[1]) <= 1e-4
 
 
+def test_attention_long_context(gpu):
+    """600 decode steps (10 chunks of the split softmax: the combine's unrolled 8-chunk body and
+    its remainder) against the oracle, checked every 50 steps and at the end."""
+    ocfg, ncfg = _cfgs(True)
+    print("attention long-context case: 600 steps", flush=True)
+    W = _attn_weights(ocfg, 21)
+    OL, NL = QC.AttnW(**W), QN.AttnLayer(i=0, **W)
+    steps = 600
+    cos, sin = QC.build_partial_rope_cache(ocfg.rope_dim, steps + 8, ocfg.rope_theta)
+    xs = torch.randn(1, steps, ocfg.d_model, generator=torch.Generator().manual_seed(22))
+    ocache, ncache = None, None
+    for t in range(steps):
+        yo, ocache = QC.attn_forward(xs[:, t:t + 1], OL, ocfg, cos, sin, ocache, t)
+        yn, ncache = QN.attn_forward(xs[:, t:t + 1].to(gpu), NL, ncfg, cos, sin, ncache, t)
+        if t % 50 == 49 or t == steps - 1:
+            assert _rel(yn, yo) <= 1e-4, f"step {t}: rel {_rel(yn, yo):.2e}"
+
+
 def test_core_layers_general_paths(gpu):
     """The shapes the launch merges leave on their own kernels: a rope_dim above 64 whose half
     is no power of two (k_attn_prep before the partials) and d_state 256 (the recurrence in
